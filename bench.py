@@ -1,0 +1,205 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X Moonlight hot path (one GPU).
+
+Metric: q8/q4 dequant-GEMV GB/s (% of HBM peak); Moonlight q8
+decode tok/s.  A "step" is one dequant-GEMV launch over one batch of synthetic
+input.  The headline workload is BASELINE config 1: the q4 [11264 x 2048]
+Moonlight dense-FFN projection, W ~ N(0, 0.02) rounded to bf16 and packed
+with the container's per-row-scale int4 scheme, x ~ N(0, 1), batch 1.
+
+`value` = algorithmic bytes per launch / average launch time (HIP events on the
+library stream around K back-to-back launches replayed from one hipGraph),
+rotating over enough weight copies (> 370 MB) that the 256 MB last-level cache
+cannot serve them.  The other configs are reported under "extra".
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+"""
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+METRIC = "q8/q4 dequant-GEMV GB/s (% HBM peak); Moonlight q8 decode tok/s, 1 GPU"
+
+
+def gemv_bytes(fmt, out_width, in_width, rows):
+    """Algorithmic HBM bytes of one GEMV launch: weights + scales + x + y."""
+    wbytes = out_width * (in_width * 4 if fmt == 0 else in_width if fmt == 1
+                          else (in_width + 1) // 2)
+    scale = 0 if fmt == 0 else out_width * 4
+    return wbytes + scale + rows * in_width * 4 + rows * out_width * 4
+
+
+class GemvCase:
+    """Synthetic resident inputs for one GEMV shape, replicated in HBM."""
+
+    def __init__(self, native, fmt, out_width, in_width, rows, seed, min_bytes=400e6):
+        self.native = native
+        self.fmt, self.O, self.I, self.rows = fmt, out_width, in_width, rows
+        wf = native.DeviceBuffer(out_width * in_width * 4)
+        native.fill_normal(wf, out_width * in_width, seed, 0.0, 0.02, bf16=True)
+        self.wbytes = out_width * (in_width if fmt == 1 else (in_width + 1) // 2
+                                   if fmt == 2 else in_width * 4)
+        first_w = native.DeviceBuffer(self.wbytes)
+        first_s = native.DeviceBuffer(out_width * 4) if fmt else None
+        if fmt == 0:
+            native.load().mlk_memcpy_d2d(first_w.ptr, wf.ptr, self.wbytes)
+        else:
+            native.quantize(8 if fmt == 1 else 4, wf, out_width, in_width, first_w, first_s)
+        wf.close()
+        # >= 16 distinct copies and > min_bytes in total, so the last-level
+        # cache (256 MB) cannot hold the rotation
+        copies = max(16 if self.wbytes < 64e6 else 2, math.ceil(min_bytes / self.wbytes))
+        self.w = [first_w]
+        self.s = [first_s] if fmt else []
+        for _ in range(copies - 1):
+            w = native.DeviceBuffer(self.wbytes)
+            native.load().mlk_memcpy_d2d(w.ptr, first_w.ptr, self.wbytes)
+            self.w.append(w)
+            if fmt:
+                s = native.DeviceBuffer(out_width * 4)
+                native.load().mlk_memcpy_d2d(s.ptr, first_s.ptr, out_width * 4)
+                self.s.append(s)
+        self.x = native.DeviceBuffer(rows * in_width * 4)
+        native.fill_normal(self.x, rows * in_width, seed + 1, 0.0, 1.0)
+        self.y = native.DeviceBuffer(rows * out_width * 4)
+        native.synchronize()
+        self.bytes = gemv_bytes(fmt, out_width, in_width, rows)
+
+    def time(self, warmup, iters, use_graph=True):
+        us = self.native.time_gemv(self.fmt, self.w, self.s, self.x, self.y, self.O, self.I,
+                                   self.rows, warmup, iters, use_graph)
+        return us, self.bytes / (us * 1e-6) / 1e9
+
+    def host_inputs(self):
+        import numpy as np
+        q = self.w[0].download(np.uint8 if self.fmt else np.float32)
+        s = self.s[0].download(np.float32) if self.fmt else None
+        x = self.x.download(np.float32).reshape(self.rows, self.I)
+        return q, s, x
+
+    def close(self):
+        for b in self.w + self.s + [self.x, self.y]:
+            b.close()
+
+
+def cpu_baseline(case, budget_s=10.0):
+    """The oracle's GEMV (restatement of the reference arithmetic) timed on the
+    host cores on the same inputs, with the same parity check."""
+    import numpy as np
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import oracle_lib
+    from conftest import rel_l2
+    q, s, x = case.host_inputs()
+    threads = len(os.sched_getaffinity(0))
+    case.native.gemv(case.fmt, case.w[0], case.s[0] if case.fmt else None, case.x, case.y,
+                     case.O, case.I, case.rows)
+    got = case.y.download(np.float32).reshape(case.rows, case.O)
+    expect = oracle_lib.matmul(case.fmt, q, s, x, case.O, case.I, threads=threads)
+    err = rel_l2(got, expect)
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        oracle_lib.matmul(case.fmt, q, s, x, case.O, case.I, threads=threads)
+        reps += 1
+        elapsed = time.perf_counter() - t0
+        if elapsed >= budget_s or reps >= 20000:
+            break
+    per = elapsed / reps
+    return {"value": round(case.bytes / per / 1e9, 3), "unit": "GB/s", "cores": threads,
+            "kind": "port",
+            "sample": f"{reps} oracle GEMVs of the same workload, {elapsed:.1f} s "
+                      f"(OpenMP over output rows, gcc -O3 -march=x86-64-v3)",
+            "ms_per_step": round(per * 1e3, 4), "parity_rel_l2": err}
+
+
+def main():
+    parser = argparse.ArgumentParser()
+    parser.add_argument("--gpus", type=int, default=1)
+    parser.add_argument("--steps", type=int, default=200)
+    parser.add_argument("--warmup", type=int, default=10)
+    parser.add_argument("--no-cpu", action="store_true")
+    parser.add_argument("--cpu-budget", type=float, default=10.0)
+    args = parser.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU only: the hot path is single-device "
+              "(multi-GPU sharding is a design note in DESIGN.md, not a measured path)",
+              file=sys.stderr)
+        sys.exit(2)
+
+    from floyd_amd import native
+    device = native.init()
+    print(f"[bench] device {device}", file=sys.stderr, flush=True)
+
+    # headline: BASELINE config 1, q4 [11264 x 2048], batch 1
+    head = GemvCase(native, 2, 11264, 2048, 1, seed=101)
+    head_us, head_gbs = head.time(args.warmup, args.steps, use_graph=True)
+    head_us_stream, head_gbs_stream = head.time(args.warmup, args.steps, use_graph=False)
+    print(f"[bench] q4 11264x2048 B=1: {head_us:.2f} us {head_gbs:.0f} GB/s (graph), "
+          f"{head_us_stream:.2f} us (stream launches)", file=sys.stderr, flush=True)
+
+    extra = {}
+    for index, (name, (fmt, o, i, rows)) in enumerate({
+            "cfg0_q8_11264x2048_b1": (1, 11264, 2048, 1),
+            "cfg0_q8_11264x2048_b4": (1, 11264, 2048, 4),
+            "cfg1_q4_2048x11264_b1": (2, 2048, 11264, 1),
+            "q8_2048x11264_b1": (1, 2048, 11264, 1),
+            "f32_lmhead_163840x2048_b1": (0, 163840, 2048, 1)}.items()):
+        case = GemvCase(native, fmt, o, i, rows, seed=1000 + index)
+        us, gbs = case.time(args.warmup, max(50, args.steps // 2))
+        extra[name] = {"us": round(us, 3), "GB/s": round(gbs, 1),
+                       "frac": round(gbs / HBM_PEAK_GBS, 4), "bytes": case.bytes}
+        print(f"[bench] {name}: {us:.2f} us {gbs:.0f} GB/s", file=sys.stderr, flush=True)
+        case.close()
+
+    # copy yardstick: 256 MiB per launch, two buffer pairs
+    nbytes = 256 << 20
+    src = [native.DeviceBuffer(nbytes) for _ in range(2)]
+    dst = [native.DeviceBuffer(nbytes) for _ in range(2)]
+    copy_us = native.time_copy(src, dst, nbytes, 3, 20)
+    extra["copy_256MiB"] = {"us": round(copy_us, 2),
+                            "GB/s": round(2 * nbytes / (copy_us * 1e-6) / 1e9, 1)}
+    for b in src + dst:
+        b.close()
+
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline(head, args.cpu_budget)
+        print(f"[bench] cpu baseline {cpu['value']} GB/s on {cpu['cores']} threads, "
+              f"parity rel-L2 {cpu['parity_rel_l2']:.2e}", file=sys.stderr, flush=True)
+
+    line = {
+        "metric": METRIC,
+        "value": round(head_gbs, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(head_us / 1e3, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "q4 weights (u8 nibbles) x f32 activations, f32 accumulate",
+        "data": "synthetic: W~N(0,0.02) bf16 -> per-row int4; x~N(0,1)",
+        "config": {"workload": "BASELINE config 1: q4 dequant-GEMV [11264 x 2048] "
+                               "(Moonlight dense-FFN projection), batch 1",
+                   "weight_copies": len(head.w), "timing": "hipGraph of K launches"},
+        "roofline": {"bound": "hbm", "achieved": round(head_gbs, 2), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(head_gbs / HBM_PEAK_GBS, 4),
+                     "traffic": None, "algorithmic_bytes": head.bytes,
+                     "kernel": "mlh::gemv_kernel<2,1,1,64>"},
+        "cpu_baseline": cpu,
+        "extra": extra,
+    }
+    line["extra"]["headline_stream_launch_us"] = round(head_us_stream, 3)
+    head.close()
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,95 @@
+// mlh_device.h -- device building blocks shared by the Moonlight HIP kernels
+// (gfx950 / CDNA4, wave64).  Header-only; included by the .hip sources.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mlh {
+
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kWave = 64;
+
+// 16-byte global load.  Weights are streamed exactly once per launch, so the
+// load is marked non-temporal to keep L2 / MALL for the activations.
+__device__ __forceinline__ u32x4 load_stream16(const void *p) {
+    return __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p));
+}
+
+__device__ __forceinline__ f32x4 load_f4(const float *p) {
+    return *reinterpret_cast<const f32x4 *>(p);
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, kWave);
+    return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
+    return v;
+}
+
+// Sum over groups of G lanes (G a power of two <= 64).
+template <int G>
+__device__ __forceinline__ float group_sum(float v) {
+#pragma unroll
+    for (int o = G / 2; o >= 1; o >>= 1) v += __shfl_xor(v, o, kWave);
+    return v;
+}
+
+// Transposed butterfly: NV partial sums per lane, reduced over groups of G
+// lanes.  After the call v[0] of a lane holds the group total of value index
+// butterfly_index<NV, G>(lane); every lane of the group ends up holding one
+// total (NV <= G), lanes whose low bits are zero are the designated writers.
+template <int NV, int G>
+__device__ __forceinline__ void butterfly_reduce(float (&v)[NV], int lane) {
+    static_assert(NV <= G, "more values than lanes in the group");
+    int n = NV;
+    int o = G / 2;
+#pragma unroll
+    for (int step = 0; (1 << step) < NV; ++step) {
+        const bool upper = (lane & o) != 0;
+        const int half = n / 2;
+#pragma unroll
+        for (int i = 0; i < NV / 2; ++i) {
+            if (i < half) {
+                float send = upper ? v[i] : v[i + half];
+                float keep = upper ? v[i + half] : v[i];
+                v[i] = keep + __shfl_xor(send, o, kWave);
+            }
+        }
+        n = half;
+        o >>= 1;
+    }
+    for (; o >= 1; o >>= 1) v[0] += __shfl_xor(v[0], o, kWave);
+}
+
+// Value index a lane holds after butterfly_reduce<NV, G>.
+template <int NV, int G>
+__device__ __forceinline__ int butterfly_index(int lane) {
+    int idx = 0, n = NV, o = G / 2;
+    while (n > 1) {
+        n >>= 1;
+        if (lane & o) idx += n;
+        o >>= 1;
+    }
+    return idx;
+}
+
+// Lanes that write: the bits below the last transposed offset are zero.
+template <int NV, int G>
+__device__ __forceinline__ bool butterfly_writer(int lane) {
+    int steps = 0;
+    while ((1 << steps) < NV) ++steps;
+    int low = G >> steps;  // lanes in the final plain-reduction subgroup
+    return (lane & (low - 1)) == 0;
+}
+
+__device__ __forceinline__ float silu(float g) { return g / (1.0f + expf(-g)); }
+
+}  // namespace mlh
