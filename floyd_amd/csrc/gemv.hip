@@ -1,238 +1,12 @@
-// gemv.hip -- bandwidth-bound dequant GEMV for decode (gfx950, wave64).
-//
-// Semantics follow moonlight_matmul_f32 / _q8_reduction / _q4
-// (moonlight_kernels.metal:43-130): y[b,o] = (sum_i x[b,i] * q[o,i]) * s[o]
-// with fp32 accumulation; q8 is int8 row-major [O, I], q4 packs column 2j in
-// the low nibble and 2j+1 in the high nibble of byte j, stored as q+8
-// (tools/convert_moonlight.py:46-66).
-//
-// Design (one wavefront = R weight rows x B token rows):
-//  * each lane owns the same 16-byte column chunks of every row it visits, so
-//    its slice of x is loaded once into registers and reused for R rows;
-//  * weights stream with 16-byte non-temporal loads, R*KT of them issued back
-//    to back per lane before any arithmetic (bytes in flight hide HBM latency);
-//  * int8 / nibbles become floats with v_cvt_f32_ubyteN on byte-biased values
-//    (q+128 resp. nibble) and the bias is removed once per row:
-//      sum x*q = sum x*(q+128) - 128*sum x
-//  * the R*B partial sums are reduced across the lane group with a transposed
-//    butterfly (R*B values cost ~R*B + log2(G) shuffles instead of R*B*log2(G)).
-// Optional fused prologue (RMSNorm of x) and epilogues (residual add; SwiGLU
-// of a gate/up matrix pair) remove separate elementwise launches.
-#include "mlh_device.h"
-#include "mlh_host.h"
+// gemv.hip -- launch planning for the dequant GEMV (kernel core in gemv_impl.h)
+// and the generic fallback kernel for shapes the vector core does not take.
+#include <cstdio>
+#include <cstdlib>
+
+#include "gemv_impl.h"
+#include "moe.h"
 
 namespace mlh {
-
-template <int FMT> struct FmtTraits;
-template <> struct FmtTraits<kF32> { static constexpr int kElemsPerChunk = 4; };
-template <> struct FmtTraits<kQ8> { static constexpr int kElemsPerChunk = 16; };
-template <> struct FmtTraits<kQ4> { static constexpr int kElemsPerChunk = 32; };
-
-// Dot product of one 16-byte weight chunk with EPC x values, accumulated on
-// the byte-biased integer values (bias removed later through sum x).
-template <int FMT>
-__device__ __forceinline__ float chunk_dot(u32x4 w, const float *x, float acc) {
-    if constexpr (FMT == kF32) {
-        acc = fmaf(__uint_as_float(w.x), x[0], acc);
-        acc = fmaf(__uint_as_float(w.y), x[1], acc);
-        acc = fmaf(__uint_as_float(w.z), x[2], acc);
-        acc = fmaf(__uint_as_float(w.w), x[3], acc);
-    } else if constexpr (FMT == kQ8) {
-        unsigned int d[4] = {w.x ^ 0x80808080u, w.y ^ 0x80808080u,
-                             w.z ^ 0x80808080u, w.w ^ 0x80808080u};
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            acc = fmaf((float)(d[j] & 0xFFu), x[4 * j + 0], acc);
-            acc = fmaf((float)((d[j] >> 8) & 0xFFu), x[4 * j + 1], acc);
-            acc = fmaf((float)((d[j] >> 16) & 0xFFu), x[4 * j + 2], acc);
-            acc = fmaf((float)(d[j] >> 24), x[4 * j + 3], acc);
-        }
-    } else {
-        unsigned int d[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            unsigned int lo = d[j] & 0x0F0F0F0Fu;
-            unsigned int hi = (d[j] >> 4) & 0x0F0F0F0Fu;
-            const float *xs = x + 8 * j;
-            acc = fmaf((float)(lo & 0xFFu), xs[0], acc);
-            acc = fmaf((float)(hi & 0xFFu), xs[1], acc);
-            acc = fmaf((float)((lo >> 8) & 0xFFu), xs[2], acc);
-            acc = fmaf((float)((hi >> 8) & 0xFFu), xs[3], acc);
-            acc = fmaf((float)((lo >> 16) & 0xFFu), xs[4], acc);
-            acc = fmaf((float)((hi >> 16) & 0xFFu), xs[5], acc);
-            acc = fmaf((float)(lo >> 24), xs[6], acc);
-            acc = fmaf((float)(hi >> 24), xs[7], acc);
-        }
-    }
-    return acc;
-}
-
-template <int FMT> __device__ __forceinline__ float bias_of() {
-    return FMT == kQ8 ? 128.0f : (FMT == kQ4 ? 8.0f : 0.0f);
-}
-
-// Rows per wave pass for a (KT chunks per lane, B token rows) shape: keep
-// about 16 weight loads in flight per lane and at most 16 partial sums.
-template <int KT, int B, int LPR>
-struct RowsPerGroup {
-    static constexpr int kLoads = 16 / KT > 1 ? 16 / KT : 2;
-    static constexpr int kSums = 16 / B > 1 ? 16 / B : 2;
-    static constexpr int kMin = kLoads < kSums ? kLoads : kSums;
-    static constexpr int value = kMin * B <= LPR ? kMin : (LPR / B > 1 ? LPR / B : 2);
-};
-
-template <int FMT, int B, int KT, int LPR>
-__global__ __launch_bounds__(256) void gemv_kernel(GemvParams p) {
-    constexpr int EPC = FmtTraits<FMT>::kElemsPerChunk;
-    constexpr int R = RowsPerGroup<KT, B, LPR>::value;
-    constexpr int GPW = kWave / LPR;  // row groups per wave
-    constexpr int NV = R * B;
-    static_assert(NV <= LPR, "partial sums exceed group width");
-
-    const int lane = threadIdx.x & (kWave - 1);
-    const int wave = (blockIdx.x * blockDim.x + threadIdx.x) / kWave;
-    const int group = lane / LPR;
-    const int li = lane & (LPR - 1);
-
-    const int row_bytes = FMT == kF32 ? p.I * 4 : (FMT == kQ8 ? p.I : p.I / 2);
-    const int nc = row_bytes / 16;  // chunks per row
-    const bool dual = p.epilogue == kEpiSiluDual;
-    // Logical row r of this group -> matrix row.  Dual mode: first half gate,
-    // second half up, same output index.
-    const int rows_per_group_out = dual ? R / 2 : R;
-    const int out0 = (wave * GPW + group) * rows_per_group_out;
-    if (out0 >= p.O) return;
-
-    float acc[NV];
-#pragma unroll
-    for (int v = 0; v < NV; ++v) acc[v] = 0.0f;
-    float sumx[B];
-#pragma unroll
-    for (int b = 0; b < B; ++b) sumx[b] = 0.0f;
-
-    // RMSNorm prologue scale per token row (whole row must be one k-tile).
-    float inv_rms[B];
-#pragma unroll
-    for (int b = 0; b < B; ++b) inv_rms[b] = 1.0f;
-    if (p.norm_w) {
-        float ss[B];
-#pragma unroll
-        for (int b = 0; b < B; ++b) ss[b] = 0.0f;
-#pragma unroll
-        for (int k = 0; k < KT; ++k) {
-            const int c = li + LPR * k;
-            if (c < nc) {
-#pragma unroll
-                for (int b = 0; b < B; ++b) {
-                    if (b < p.rows) {
-                        const float *xs = p.x + (long)b * p.x_stride + c * EPC;
-#pragma unroll
-                        for (int e = 0; e < EPC; e += 4) {
-                            f32x4 v = load_f4(xs + e);
-                            ss[b] += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
-                        }
-                    }
-                }
-            }
-        }
-#pragma unroll
-        for (int b = 0; b < B; ++b) {
-            float t = group_sum<LPR>(ss[b]);
-            inv_rms[b] = 1.0f / sqrtf(t / (float)p.I + p.eps);
-        }
-    }
-
-    for (int kt0 = 0; kt0 < nc; kt0 += KT * LPR) {
-        // weights first: R * KT independent 16-byte loads per lane
-        u32x4 wv[R][KT];
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-            const uint8_t *base;
-            int row;
-            if (dual) {
-                row = out0 + (r < R / 2 ? r : r - R / 2);
-                base = r < R / 2 ? p.w : p.w2;
-            } else {
-                row = out0 + r;
-                base = p.w;
-            }
-#pragma unroll
-            for (int k = 0; k < KT; ++k) {
-                const int c = kt0 + li + LPR * k;
-                if (row < p.O && c < nc)
-                    wv[r][k] = load_stream16(base + (long)row * row_bytes + c * 16);
-                else
-                    wv[r][k] = u32x4{0u, 0u, 0u, 0u};
-            }
-        }
-        // activations for the same chunks
-        float xr[B][KT][EPC];
-#pragma unroll
-        for (int k = 0; k < KT; ++k) {
-            const int c = kt0 + li + LPR * k;
-#pragma unroll
-            for (int b = 0; b < B; ++b) {
-                const bool ok = c < nc && b < p.rows;
-                const float *xs = p.x + (long)b * p.x_stride + c * EPC;
-                const float *ns = p.norm_w + c * EPC;
-#pragma unroll
-                for (int e = 0; e < EPC; e += 4) {
-                    f32x4 v = ok ? load_f4(xs + e) : f32x4{0.f, 0.f, 0.f, 0.f};
-                    if (p.norm_w && ok) {
-                        f32x4 n = load_f4(ns + e);
-                        v.x = v.x * inv_rms[b] * n.x;
-                        v.y = v.y * inv_rms[b] * n.y;
-                        v.z = v.z * inv_rms[b] * n.z;
-                        v.w = v.w * inv_rms[b] * n.w;
-                    }
-                    xr[b][k][e + 0] = v.x;
-                    xr[b][k][e + 1] = v.y;
-                    xr[b][k][e + 2] = v.z;
-                    xr[b][k][e + 3] = v.w;
-                    sumx[b] += (v.x + v.y) + (v.z + v.w);
-                }
-            }
-        }
-#pragma unroll
-        for (int r = 0; r < R; ++r)
-#pragma unroll
-            for (int k = 0; k < KT; ++k)
-#pragma unroll
-                for (int b = 0; b < B; ++b)
-                    acc[r * B + b] = chunk_dot<FMT>(wv[r][k], xr[b][k], acc[r * B + b]);
-    }
-
-    // remove the byte bias: sum x*(q+bias) - bias*sum x
-    if constexpr (FMT != kF32) {
-#pragma unroll
-        for (int r = 0; r < R; ++r)
-#pragma unroll
-            for (int b = 0; b < B; ++b) acc[r * B + b] -= bias_of<FMT>() * sumx[b];
-    }
-
-    butterfly_reduce<NV, LPR>(acc, lane);
-    const int vi = butterfly_index<NV, LPR>(lane);
-    const int r = vi / B, b = vi % B;
-    float value = acc[0];
-    if (dual) {
-        // the up-projection partner of value index vi is vi + NV/2, held by
-        // the lane across the first butterfly offset
-        float partner = __shfl_xor(value, LPR / 2, kWave);
-        const int row = out0 + r;
-        if (butterfly_writer<NV, LPR>(lane) && r < R / 2 && row < p.O && b < p.rows) {
-            float g = FMT == kF32 ? value : value * p.s[row];
-            float u = FMT == kF32 ? partner : partner * p.s2[row];
-            p.y[(long)b * p.y_stride + row] = silu(g) * u;
-        }
-        return;
-    }
-    const int row = out0 + r;
-    if (butterfly_writer<NV, LPR>(lane) && row < p.O && b < p.rows) {
-        float out = FMT == kF32 ? value : value * p.s[row];
-        if (p.epilogue == kEpiResidual) out = p.resid[(long)b * p.resid_stride + row] + out;
-        p.y[(long)b * p.y_stride + row] = out;
-    }
-}
 
 // Generic fallback for shapes the vector kernel does not take (row bytes not
 // a multiple of 16, unaligned pointers, odd q4 widths): one wave per output,
@@ -282,53 +56,113 @@ __global__ __launch_bounds__(64) void gemv_generic_kernel(GemvParams p, int fmt)
 }
 
 // ---------------------------------------------------------------------------
-// host dispatch
+// planning
 // ---------------------------------------------------------------------------
 
-template <int FMT, int B, int KT, int LPR>
-static void launch_one(const GemvParams &p, hipStream_t stream) {
-    constexpr int R = RowsPerGroup<KT, B, LPR>::value;
-    constexpr int GPW = kWave / LPR;
-    const int out_per_group = p.epilogue == kEpiSiluDual ? R / 2 : R;
-    const long groups = (p.O + out_per_group - 1) / out_per_group;
-    const long waves = (groups + GPW - 1) / GPW;
-    const long blocks = (waves + 3) / 4;
-    hipLaunchKernelGGL((gemv_kernel<FMT, B, KT, LPR>), dim3((unsigned)blocks), dim3(256),
-                       0, stream, p);
-}
+// Waves the planner tries to keep in flight: with ~8 waves per CU the HBM
+// latency (~1-2 us under load) is hidden without relying on deep per-wave
+// queues.  MLH_GEMV_PLAN="kt,r,ks" (read once) overrides the choice for
+// tuning sweeps.
+static constexpr long kTargetWaves = 2048;
 
-template <int FMT, int B>
-static bool dispatch_shape(const GemvParams &p, int nc, hipStream_t stream) {
-    // Rows of at most 64 chunks: one chunk per lane, lane groups sized to the
-    // row.  Longer rows: KT chunks per lane and k-tile; a row that fits one
-    // k-tile stays resident in registers (required by the RMSNorm prologue).
-    // KT is capped per format by the register cost of the x slice (q4 chunks
-    // carry 32 x values, q8 16, f32 4).
-    if (nc <= 8) { launch_one<FMT, B, 1, 8>(p, stream); return true; }
-    if (nc <= 16) { launch_one<FMT, B, 1, 16>(p, stream); return true; }
-    if (nc <= 32) { launch_one<FMT, B, 1, 32>(p, stream); return true; }
-    if (nc <= 64) { launch_one<FMT, B, 1, 64>(p, stream); return true; }
-    if (p.norm_w && nc > (FMT == kF32 ? 512 : FMT == kQ8 ? 128 : 64)) return false;
-    if constexpr (FMT == kQ4) {
-        launch_one<FMT, B, 1, 64>(p, stream);
-    } else if constexpr (FMT == kQ8) {
-        launch_one<FMT, B, 2, 64>(p, stream);
-    } else {
-        if (nc <= 128) launch_one<FMT, B, 2, 64>(p, stream);
-        else if (nc <= 256) launch_one<FMT, B, 4, 64>(p, stream);
-        else if (nc <= 512) launch_one<FMT, B, 8, 64>(p, stream);
-        else launch_one<FMT, B, 4, 64>(p, stream);
+static bool plan_override(GemvPlan *plan) {
+    static int parsed = 0, kt = 0, r = 0, ks = 0;
+    if (!parsed) {
+        const char *env = getenv("MLH_GEMV_PLAN");
+        if (!env || sscanf(env, "%d,%d,%d", &kt, &r, &ks) != 3) kt = 0;
+        parsed = 1;
     }
+    if (!kt) return false;
+    plan->kt = kt;
+    plan->r = r;
+    plan->ks = ks;
     return true;
 }
 
-template <int FMT>
-static bool dispatch_fmt(const GemvParams &p, int nc, hipStream_t stream) {
-    switch (p.rows <= 1 ? 1 : p.rows <= 2 ? 2 : 4) {
-    case 1: return dispatch_shape<FMT, 1>(p, nc, stream);
-    case 2: return dispatch_shape<FMT, 2>(p, nc, stream);
-    default: return dispatch_shape<FMT, 4>(p, nc, stream);
+// Plans measured best on MI355X for the Moonlight decode shapes (batch 1):
+// sweeps over kt x r x ks of back-to-back launches, 400+ MB weight rotation.
+struct PlanEntry {
+    int fmt, O, I, dual, kt, r, ks;
+};
+static const PlanEntry kMeasuredPlans[] = {
+    {kQ4, 11264, 2048, 0, 1, 4, 1}, {kQ8, 11264, 2048, 0, 1, 4, 1},
+    {kQ4, 2048, 11264, 0, 1, 8, 4}, {kQ8, 2048, 11264, 0, 1, 4, 4},
+    {kQ8, 3072, 2048, 0, 1, 2, 4},  {kQ8, 2048, 2048, 0, 1, 2, 4},
+    {kQ8, 2048, 1408, 0, 1, 2, 4},  {kQ8, 2048, 2816, 0, 1, 2, 4},
+    {kQ8, 576, 2048, 0, 1, 1, 4},   {kF32, 64, 2048, 0, 2, 1, 4},
+    {kQ4, 2048, 1408, 0, 1, 2, 1},
+};
+
+GemvPlan plan_gemv(int fmt, int O, int I, int rows, bool dual) {
+    GemvPlan plan;
+    plan.b = rows <= 1 ? 1 : rows <= 2 ? 2 : 4;
+    const int nc = row_bytes_of(fmt, I) / 16;
+    if (nc <= 32) {
+        // rows per lane group fixed by dispatch_gemv_b for narrow rows
+        plan.lpr = nc <= 8 ? 8 : nc <= 16 ? 16 : 32;
+        plan.kt = 1;
+        plan.ks = 1;
+        if (plan.lpr == 8) plan.r = 8 / plan.b > 1 ? 8 / plan.b : 2;
+        else plan.r = plan.lpr / plan.b < 8 ? plan.lpr / plan.b : 8;
+        return plan;
     }
+    plan.lpr = 64;
+    if (plan_override(&plan)) {
+        if (plan.r * plan.b > 16) plan.r = 16 / plan.b;
+        if (dual && plan.r < 2) plan.r = 2;
+        return plan;
+    }
+    if (plan.b == 1) {
+        for (const PlanEntry &e : kMeasuredPlans) {
+            if (e.fmt == fmt && e.O == O && e.I == I && e.dual == (int)dual) {
+                plan.kt = e.kt;
+                plan.r = e.r;
+                plan.ks = e.ks;
+                return plan;
+            }
+        }
+    }
+    // Fallback heuristic from the same sweeps: one chunk per lane for the
+    // quantized formats (more waves beat deeper per-wave queues), k split over
+    // the workgroup's 4 waves when the matrix is short and rows span several
+    // k-tiles, and rows per wave sized to keep ~2048+ waves in flight.
+    plan.kt = fmt == kF32 ? (nc > 64 ? 2 : 1) : 1;
+    const int tiles = (nc + 64 * plan.kt - 1) / (64 * plan.kt);
+    const long out_rows_total = (long)O * (dual ? 2 : 1);
+    plan.ks = (tiles >= 4 || (tiles >= 2 && out_rows_total <= 4096)) ? 4 : 1;
+    const int rmin = dual ? 2 : 1;
+    int chosen = 0;
+    for (int r = 8; r >= rmin; r >>= 1) {
+        if (r * plan.b > 16 || r * plan.kt > 16) continue;
+        const long out_rows = dual ? r / 2 : r;
+        const long waves = (O + out_rows - 1) / out_rows * (plan.ks == 4 ? 4 : 1);
+        chosen = r;
+        if (waves >= kTargetWaves) break;
+    }
+    plan.r = chosen ? chosen : rmin;
+    return plan;
+}
+
+// Grouped expert launches: same core, but the work is spread over `tasks`
+// matrices, so fewer rows per wave are needed to fill the machine.
+GemvPlan plan_expert_gemv(int fmt, int O, int I, int rows, bool dual, int tasks) {
+    GemvPlan plan = plan_gemv(fmt, O, I, rows, dual);
+    if (plan.lpr < 64 || tasks <= 1) return plan;
+    const int rmin = dual ? 2 : 1;
+    for (int r = plan.r; r <= 8; r <<= 1) {
+        if (r * plan.b > 16 || r * plan.kt > 16) break;
+        const long out_rows = dual ? r / 2 : r;
+        const long waves = (O + out_rows - 1) / out_rows * (plan.ks == 4 ? 4 : 1) * tasks;
+        plan.r = r;
+        if (waves <= 4 * kTargetWaves) break;
+    }
+    if (plan.r < rmin) plan.r = rmin;
+    return plan;
+}
+
+int gemv_rows_per_block(const GemvPlan &plan, bool dual) {
+    const int out = dual ? plan.r / 2 : plan.r;
+    return out * (64 / plan.lpr) * (plan.ks == 1 ? 4 : 1);
 }
 
 static bool aligned16(const void *ptr) { return ((uintptr_t)ptr & 15u) == 0; }
@@ -340,12 +174,11 @@ int gemv(const GemvParams &p_in, hipStream_t stream) {
     if (p_in.epilogue == kEpiSiluDual && (!p_in.w2 || (p_in.fmt != kF32 && !p_in.s2)))
         return kErrArgs;
     if (p_in.epilogue == kEpiResidual && !p_in.resid) return kErrArgs;
-    const long row_bytes = p_in.fmt == kF32 ? (long)p_in.I * 4
-                         : p_in.fmt == kQ8 ? p_in.I : (p_in.I + 1) / 2;
+    const long row_bytes = row_bytes_of(p_in.fmt, p_in.I);
     const bool vector_ok =
-        row_bytes % 16 == 0 && (p_in.fmt != kQ4 || p_in.I % 2 == 0) &&
-        aligned16(p_in.w) && (!p_in.w2 || aligned16(p_in.w2)) && aligned16(p_in.x) &&
-        p_in.x_stride % 4 == 0 && (!p_in.norm_w || aligned16(p_in.norm_w));
+        row_bytes % 16 == 0 && (p_in.fmt != kQ4 || p_in.I % 2 == 0) && aligned16(p_in.w) &&
+        (!p_in.w2 || aligned16(p_in.w2)) && aligned16(p_in.x) && p_in.x_stride % 4 == 0 &&
+        (!p_in.norm_w || aligned16(p_in.norm_w));
     // token rows beyond 4 are processed in slices of 4 (register budget)
     for (int r0 = 0; r0 < p_in.rows; r0 += kMaxGemvRows) {
         GemvParams p = p_in;
@@ -355,14 +188,15 @@ int gemv(const GemvParams &p_in, hipStream_t stream) {
         if (p.resid) p.resid = p_in.resid + (long)r0 * p_in.resid_stride;
         bool done = false;
         if (vector_ok) {
-            const int nc = (int)(row_bytes / 16);
-            if (p.fmt == kF32) done = dispatch_fmt<kF32>(p, nc, stream);
-            else if (p.fmt == kQ8) done = dispatch_fmt<kQ8>(p, nc, stream);
-            else done = dispatch_fmt<kQ4>(p, nc, stream);
+            const GemvPlan plan = plan_gemv(p.fmt, p.O, p.I, p.rows,
+                                            p.epilogue == kEpiSiluDual);
+            GemvLaunch L;
+            L.plain = p;
+            done = dispatch_gemv(p.fmt, L, 0, plan, dim3(1), stream);
         }
         if (!done) {
-            hipLaunchKernelGGL(gemv_generic_kernel, dim3(p.O, p.rows), dim3(64), 0, stream,
-                               p, p.fmt);
+            hipLaunchKernelGGL(gemv_generic_kernel, dim3(p.O, p.rows), dim3(64), 0, stream, p,
+                               p.fmt);
         }
     }
     return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;

@@ -46,7 +46,10 @@ DeviceContext *context() {
         return nullptr;
     }
     g_context.device = 0;
-    g_context.name = prop.name;
+    // Marketing names can be empty inside containers; the architecture is
+    // always appended so callers can tell the device class.
+    g_context.name = std::string(prop.name[0] ? prop.name : "AMD Instinct GPU") + " [" +
+                     arch.substr(0, arch.find(':')) + "]";
     g_context.arch = arch;
     g_context.cu_count = prop.multiProcessorCount;
     g_context.ready = true;
@@ -254,6 +257,43 @@ int mlk_time_copy(void *const *src, void *const *dst, int n_buffers, size_t byte
     (void)hipEventDestroy(start);
     (void)hipEventDestroy(stop);
     if (status) return finish(status, "mlk_time_copy");
+    if (sync) return sync;
+    *avg_us = (double)ms * 1000.0 / iters;
+    return kOk;
+}
+
+int mlk_time_read(void *const *src, int n_buffers, size_t bytes, int blocks, unsigned *scratch,
+                  int warmup, int iters, double *avg_us) {
+    hipStream_t st = lib_stream();
+    if (!st) return kErrDevice;
+    if (!src || n_buffers <= 0 || iters <= 0 || !avg_us || !scratch)
+        return finish(kErrArgs, "mlk_time_read");
+    for (int i = 0; i < warmup; ++i)
+        if (int e = read16(src[i % n_buffers], bytes, blocks, scratch, st))
+            return finish(e, "mlk_time_read");
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+    if (int e = check_hip(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal), "capture"))
+        return e;
+    for (int i = 0; i < iters; ++i) read16(src[i % n_buffers], bytes, blocks, scratch, st);
+    if (int e = check_hip(hipStreamEndCapture(st, &graph), "end capture")) return e;
+    if (int e = check_hip(hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0), "instantiate"))
+        return e;
+    (void)hipGraphLaunch(exec, st);
+    hipEvent_t start, stop;
+    (void)hipEventCreate(&start);
+    (void)hipEventCreate(&stop);
+    (void)hipEventRecord(start, st);
+    int status = check_hip(hipGraphLaunch(exec, st), "graph launch");
+    (void)hipEventRecord(stop, st);
+    int sync = check_hip(hipEventSynchronize(stop), "event sync");
+    float ms = 0.0f;
+    (void)hipEventElapsedTime(&ms, start, stop);
+    (void)hipEventDestroy(start);
+    (void)hipEventDestroy(stop);
+    (void)hipGraphExecDestroy(exec);
+    (void)hipGraphDestroy(graph);
+    if (status) return status;
     if (sync) return sync;
     *avg_us = (double)ms * 1000.0 / iters;
     return kOk;

@@ -1,0 +1,47 @@
+// mla.h -- compressed-MLA attention launches (internal; see mla.hip).
+#pragma once
+
+#include "mlh_host.h"
+
+namespace mlh {
+
+constexpr int kMlaMaxHeads = 16;        // Moonlight: 16 heads
+constexpr int kMlaKeysPerSplit = 64;    // keys per workgroup in mla_attend
+constexpr int kMlaMaxLatent = 512;      // kv_lora_rank limit (moonlight_metal.m:1041)
+constexpr int kMlaMaxSplitsInLds = 1024;
+
+// A weight matrix in one of the container formats (f32 / int8 / packed int4)
+// with its per-row scales.
+struct MatrixRef {
+    int fmt = kQ8;
+    const uint8_t *w = nullptr;
+    const float *s = nullptr;
+};
+
+// One attention call for `rows` token rows starting at `position`, for one
+// layer: caches point at that layer's [context][latent] / [context][rope].
+struct MlaParams {
+    int rows = 0, position = 0, heads = 0;
+    int nope = 0, rope = 0, vdim = 0, latent = 0;
+    float eps = 1e-5f, scale = 1.0f;
+    const float *query = nullptr;       // [rows, heads, nope + rope] (q_proj output)
+    const float *compressed = nullptr;  // [rows, latent + rope] (kv_a output)
+    const float *kv_norm = nullptr;     // [latent] kv_a_layernorm weight
+    const float *inv_freq = nullptr;    // [rope / 2] theta^(-2p/rope), host-computed
+    MatrixRef kv_b;                     // [heads * (nope + vdim), latent]
+    float *latent_cache = nullptr;      // this layer: [context, latent]
+    float *rope_cache = nullptr;        // this layer: [context, rope]
+    float *query_rope = nullptr;        // scratch [rows, heads, rope]
+    float *query_absorbed = nullptr;    // scratch [rows, heads, latent]
+    int max_splits = 0;                 // split capacity of the partial buffers
+    float *part_max = nullptr;          // [rows, max_splits, kMlaMaxHeads]
+    float *part_sum = nullptr;          // [rows, max_splits, kMlaMaxHeads]
+    float *part_lc = nullptr;           // [rows, max_splits, kMlaMaxHeads, latent]
+    float *context = nullptr;           // out [rows, heads, vdim]
+};
+
+// Cache append + query RoPE + absorb, split-K attention, merge + value
+// projection (three launches).  o_proj is a plain GEMV on `context`.
+int mla_attention_core(const MlaParams &p, hipStream_t stream);
+
+}  // namespace mlh

@@ -37,6 +37,11 @@ struct GemvParams {
 
 int gemv(const GemvParams &p, hipStream_t stream);
 
+struct GemvPlan;
+// Launch geometry the planner picks for a GEMV shape (exposed for the grouped
+// expert launches, which share the GEMV core).
+GemvPlan plan_gemv(int fmt, int O, int I, int rows, bool dual);
+
 // Packs f32 rows like tools/convert_moonlight.py:46-66 (bits 8 or 4).
 int quantize_rows(int bits, const float *w, int rows, int cols, uint8_t *q, float *s,
                   hipStream_t stream);
@@ -47,5 +52,7 @@ int fill_normal(float *out, int64_t n, uint64_t seed, float mean, float std, int
 
 // dst = src with 16-byte non-temporal loads/stores (bandwidth yardstick).
 int copy16(const void *src, void *dst, size_t bytes, hipStream_t stream);
+// Reads `bytes` of src with `blocks` workgroups (out: blocks*4 words).
+int read16(const void *src, size_t bytes, int blocks, unsigned *out, hipStream_t stream);
 
 }  // namespace mlh

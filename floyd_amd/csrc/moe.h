@@ -1,0 +1,68 @@
+// moe.h -- MoE routing / expert launches (internal; see moe.hip).
+#pragma once
+
+#include "gemv_impl.h"
+
+namespace mlh {
+
+// Sigmoid top-k + route tables for `rows` token rows (one workgroup).
+struct RouteParams {
+    const float *logits = nullptr;  // [rows, experts] router logits
+    const float *bias = nullptr;    // [experts] e_score_correction_bias (selection only)
+    int rows = 0, experts = 0, top_k = 0, normalize = 1;
+    float routed_scale = 1.0f;
+    int *ids = nullptr;        // [rows, top_k] selection order
+    float *weights = nullptr;  // [rows, top_k] finalised weights
+    int *trace = nullptr;      // optional copy of ids (per-layer route trace)
+    int *n_unique = nullptr;   // [1]
+    int *unique = nullptr;     // [experts] active experts, first-appearance order
+    int *counts = nullptr;     // [experts] entries per expert
+    int *offsets = nullptr;    // [experts] start of each expert's compact list
+    int *list_rows = nullptr;  // [rows*top_k] token row per list entry
+    int *list_slots = nullptr; // [rows*top_k] slot per list entry
+    int *list_pos = nullptr;   // [rows*top_k] list entry of (row, slot), -1 if invalid
+    int *error = nullptr;      // [1] set to 1 when an id is out of range
+};
+int route_topk(const RouteParams &p, hipStream_t stream);
+
+struct CombineParams {
+    int rows = 0, hidden = 0, top_k = 0;
+    const float *weights = nullptr;     // [rows, top_k]
+    const int *list_pos = nullptr;      // [rows, top_k]
+    const float *expert_out = nullptr;  // [list, hidden]
+    const float *shared_out = nullptr;  // [rows, hidden]
+    const float *resid = nullptr;       // optional [rows, hidden]
+    float *routed_copy = nullptr;       // optional [rows, hidden]
+    float *out = nullptr;               // [rows, hidden]
+};
+int moe_combine(const CombineParams &p, hipStream_t stream);
+
+struct ExpertFfnParams {
+    int rows = 0, experts = 0, top_k = 0, hidden = 0, inter = 0, shared_width = 0;
+    int expert_fmt = kQ8, shared_fmt = kQ8, has_shared = 1;
+    const ExpertWeights *expert_table = nullptr;  // device [experts]
+    const uint8_t *shared_gate = nullptr, *shared_up = nullptr, *shared_down = nullptr;
+    const float *shared_gate_s = nullptr, *shared_up_s = nullptr, *shared_down_s = nullptr;
+    const int *n_unique = nullptr, *unique = nullptr, *counts = nullptr, *offsets = nullptr;
+    const int *list_rows = nullptr;
+    const float *x = nullptr;       // residual stream [rows, hidden] (normalised on the fly)
+    const float *norm_w = nullptr;  // post-attention RMSNorm weight
+    float eps = 1e-5f;
+    float *expert_hidden = nullptr;  // [rows*top_k, inter]
+    float *expert_out = nullptr;     // [rows*top_k, hidden]
+    float *shared_hidden = nullptr;  // [rows, shared_width]
+    float *shared_out = nullptr;     // [rows, hidden]
+};
+int expert_ffn(const ExpertFfnParams &f, hipStream_t stream);
+
+int rmsnorm_rows(const float *x, const float *w, float *y, int rows, int width, float eps,
+                 long in_stride, long out_stride, hipStream_t stream);
+int embed_rows(const float *table, const int *ids, float *out, int rows, int width, int vocab,
+               hipStream_t stream);
+int add_vectors(const float *a, const float *b, float *out, long n, hipStream_t stream);
+
+// Planning helpers shared with gemv.hip.
+GemvPlan plan_expert_gemv(int fmt, int O, int I, int rows, bool dual, int tasks);
+int gemv_rows_per_block(const GemvPlan &plan, bool dual);
+
+}  // namespace mlh

@@ -1,0 +1,349 @@
+// moe.hip -- device routing, route tables, grouped expert FFN launches and the
+// deterministic combine of the Moonlight MoE layer.
+//
+// References (c4pt0r/floyd):
+//   routing   moonlight_route_sigmoid_topk (moonlight_kernels.metal:469-512) =
+//             moe_route_select + moe_route_finalize (moe_route.h:47-99)
+//   tables    prepare_route_tables (moonlight_metal.m:525-559), which the
+//             reference runs on the HOST after a blocking wait; here they are
+//             built on the device so a layer needs no host round trip
+//   experts   encode_moe_residual_buffer (moonlight_metal.m:561-676)
+//   combine   moonlight_scatter_expert + moonlight_add_f32
+//             (moonlight_kernels.metal:543-569)
+#include "mlh_device.h"
+#include "moe.h"
+
+#include <climits>
+
+namespace mlh {
+
+// Sigmoid as moe_route.h:12-14 computes it with glibc: 1 / (1 + expf(-x)).
+// exp is evaluated in double and rounded once, which is the correctly rounded
+// expf (glibc's expf is correctly rounded except in cases below its 0.502 ulp
+// bound), so the scores -- and therefore the selected expert ids -- match the
+// host twin bit for bit.
+__device__ __forceinline__ float sigmoid_exact(float logit) {
+    const float e = (float)exp(-(double)logit);
+    return 1.0f / (1.0f + e);
+}
+
+constexpr int kMaxExperts = 256;
+constexpr int kMaxTopK = 16;
+
+// One workgroup: top-k for every token row, then the route tables.
+__global__ __launch_bounds__(256) void route_kernel(RouteParams p) {
+    __shared__ int first_pos[kMaxExperts];
+    __shared__ int counts[kMaxExperts];
+    __shared__ int offsets[kMaxExperts];
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int E = p.experts, K = p.top_k, M = p.rows;
+    const int n_pos = M * K;
+
+    // ---- top-k selection: one wave per token row, experts spread over lanes
+    for (int r = wave; r < M; r += 4) {
+        float score[kMaxExperts / 64];
+        float sel[kMaxExperts / 64];
+#pragma unroll
+        for (int j = 0; j < kMaxExperts / 64; ++j) {
+            const int e = lane + 64 * j;
+            if (e < E) {
+                score[j] = sigmoid_exact(p.logits[(long)r * E + e]);
+                sel[j] = score[j] + p.bias[e];
+            } else {
+                score[j] = 0.0f;
+                sel[j] = -INFINITY;
+            }
+        }
+        unsigned taken = 0;  // bit j: lane's expert lane + 64 j already chosen
+        float wsum = 0.0f;
+        float wk[kMaxTopK];
+        int ids[kMaxTopK];
+        for (int k = 0; k < K; ++k) {
+            // lane-local scan in increasing expert order, strict '>' keeps the
+            // lower index on ties (moe_route.h:59-71)
+            float best_v = -INFINITY;
+            int best_e = INT_MAX;
+#pragma unroll
+            for (int j = 0; j < kMaxExperts / 64; ++j) {
+                const int e = lane + 64 * j;
+                if (e < E && !(taken & (1u << j)) && sel[j] > best_v) {
+                    best_v = sel[j];
+                    best_e = e;
+                }
+            }
+            // wave arg-max: larger value wins, equal values keep the lower id
+#pragma unroll
+            for (int o = 32; o >= 1; o >>= 1) {
+                const float ov = __shfl_xor(best_v, o, 64);
+                const int oe = __shfl_xor(best_e, o, 64);
+                if (ov > best_v || (ov == best_v && oe < best_e)) {
+                    best_v = ov;
+                    best_e = oe;
+                }
+            }
+            if (best_e == INT_MAX) best_e = -1;  // only NaN scores remain
+            const int owner = best_e < 0 ? 0 : (best_e & 63), slot_j = best_e < 0 ? -1 : best_e >> 6;
+            float chosen = 0.0f;
+#pragma unroll
+            for (int j = 0; j < kMaxExperts / 64; ++j)
+                if (lane == owner && j == slot_j) {
+                    taken |= 1u << j;
+                    chosen = score[j];
+                }
+            chosen = __shfl(chosen, owner, 64);
+            ids[k] = best_e;
+            wk[k] = chosen;
+        }
+        if (p.normalize) {
+            for (int k = 0; k < K; ++k) wsum += wk[k];
+            wsum += 1e-20f;
+        } else {
+            wsum = 1.0f;
+        }
+        if (lane < K) {
+            int id = ids[0];
+            float w = wk[0];
+            for (int k = 1; k < K; ++k)
+                if (lane == k) {
+                    id = ids[k];
+                    w = wk[k];
+                }
+            p.ids[(long)r * K + lane] = id;
+            p.weights[(long)r * K + lane] = w / wsum * p.routed_scale;
+            if (p.trace) p.trace[(long)r * K + lane] = id;
+        }
+    }
+    for (int e = tid; e < E; e += blockDim.x) {
+        first_pos[e] = INT_MAX;
+        counts[e] = 0;
+    }
+    __syncthreads();
+    __threadfence_block();
+
+    // ---- tables: first appearance and count per expert (order-independent
+    // atomics on LDS), then ranks in first-appearance order
+    for (int q = tid; q < n_pos; q += blockDim.x) {
+        const int e = p.ids[q];
+        if (e < 0 || e >= E) {
+            p.list_pos[q] = -1;
+            *p.error = 1;  // prepare_route_tables rejects such ids (moonlight_metal.m:545)
+            continue;
+        }
+        atomicMin(&first_pos[e], q);
+        atomicAdd(&counts[e], 1);
+    }
+    __syncthreads();
+    if (tid < E && counts[tid] > 0) {
+        int rank = 0, off = 0;
+        const int mine = first_pos[tid];
+        for (int e = 0; e < E; ++e) {
+            if (counts[e] > 0 && first_pos[e] < mine) {
+                ++rank;
+                off += counts[e];
+            }
+        }
+        p.unique[rank] = tid;
+        offsets[tid] = off;
+        p.offsets[tid] = off;
+    }
+    if (tid < E) p.counts[tid] = counts[tid];
+    if (tid == 0) {
+        int n = 0;
+        for (int e = 0; e < E; ++e) n += counts[e] > 0;
+        *p.n_unique = n;
+    }
+    __syncthreads();
+
+    // ---- compact lists: entries of expert e in (row, slot) order
+    for (int e = wave; e < E; e += 4) {
+        if (counts[e] == 0) continue;
+        int running = 0;
+        const int base = offsets[e];
+        for (int q0 = 0; q0 < n_pos; q0 += 64) {
+            const int q = q0 + lane;
+            const bool match = q < n_pos && p.ids[q] == e;
+            const unsigned long long mask = __ballot(match);
+            if (match) {
+                const int j = running + __popcll(mask & ((1ull << lane) - 1ull));
+                p.list_rows[base + j] = q / K;
+                p.list_slots[base + j] = q % K;
+                p.list_pos[q] = base + j;
+            }
+            running += __popcll(mask);
+        }
+    }
+}
+
+int route_topk(const RouteParams &p, hipStream_t stream) {
+    if (!p.logits || !p.bias || !p.ids || !p.weights || p.rows <= 0 || p.experts <= 0 ||
+        p.experts > kMaxExperts || p.top_k <= 0 || p.top_k > kMaxTopK ||
+        p.top_k > p.experts || !p.n_unique || !p.unique || !p.counts || !p.offsets ||
+        !p.list_rows || !p.list_slots || !p.list_pos || !p.error)
+        return kErrArgs;
+    hipLaunchKernelGGL(route_kernel, dim3(1), dim3(256), 0, stream, p);
+    return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
+}
+
+// out[r] = resid[r] + (sum_k w[r,k] * y[pos[r,k]] + shared[r]); routed sum in
+// slot order (tests/test_moonlight_metal_moe.c:118-135), deterministic.
+__global__ __launch_bounds__(256) void combine_kernel(CombineParams p) {
+    const int r = blockIdx.x;
+    const int K = p.top_k;
+    for (int d = threadIdx.x; d < p.hidden; d += blockDim.x) {
+        float routed = 0.0f;
+        for (int k = 0; k < K; ++k) {
+            const int q = r * K + k;
+            const int pos = p.list_pos[q];
+            if (pos >= 0) routed += p.weights[q] * p.expert_out[(long)pos * p.hidden + d];
+        }
+        const float shared = p.shared_out[(long)r * p.hidden + d];
+        if (p.routed_copy) p.routed_copy[(long)r * p.hidden + d] = routed;
+        float out = routed + shared;
+        if (p.resid) out = p.resid[(long)r * p.hidden + d] + out;
+        p.out[(long)r * p.hidden + d] = out;
+    }
+}
+
+int moe_combine(const CombineParams &p, hipStream_t stream) {
+    if (!p.weights || !p.list_pos || !p.expert_out || !p.shared_out || !p.out || p.rows <= 0)
+        return kErrArgs;
+    hipLaunchKernelGGL(combine_kernel, dim3(p.rows), dim3(256), 0, stream, p);
+    return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
+}
+
+// Both grouped expert launches (gate/up + SwiGLU, then down).  The routed
+// experts use one format (ebits) and the shared expert possibly another
+// (dbits); one launch covers both when the formats agree.
+int expert_ffn(const ExpertFfnParams &f, hipStream_t stream) {
+    const int max_tasks = f.rows * f.top_k < f.experts ? f.rows * f.top_k : f.experts;
+    const int max_rows = f.rows;  // token rows any task can hold
+    for (int stage = 0; stage < 2; ++stage) {
+        GemvLaunch L;
+        ExpertGemvParams &e = L.expert;
+        e.stage = stage;
+        e.experts = f.expert_table;
+        e.n_unique = f.n_unique;
+        e.unique = f.unique;
+        e.counts = f.counts;
+        e.offsets = f.offsets;
+        e.rows = f.list_rows;
+        e.shared_rows = f.rows;
+        e.hidden = f.hidden;
+        e.inter = f.inter;
+        e.shared_width = f.shared_width;
+        e.norm_w = f.norm_w;
+        e.eps = f.eps;
+        if (stage == 0) {
+            e.x = f.x;
+            e.y = f.expert_hidden;
+            e.sh_w = f.shared_gate;
+            e.sh_s = f.shared_gate_s;
+            e.sh_w2 = f.shared_up;
+            e.sh_s2 = f.shared_up_s;
+            e.sh_y = f.shared_hidden;
+        } else {
+            e.x = f.expert_hidden;
+            e.y = f.expert_out;
+            e.sh_w = f.shared_down;
+            e.sh_s = f.shared_down_s;
+            e.sh_x = f.shared_hidden;
+            e.sh_y = f.shared_out;
+        }
+        const bool dual = stage == 0;
+        const int routed_O = stage == 0 ? f.inter : f.hidden;
+        const int routed_I = stage == 0 ? f.hidden : f.inter;
+        const int shared_O = stage == 0 ? f.shared_width : f.hidden;
+        const int shared_I = stage == 0 ? f.hidden : f.shared_width;
+        const bool fused = f.expert_fmt == f.shared_fmt && f.has_shared;
+        // routed (+ shared when the formats agree)
+        {
+            GemvPlan plan = plan_expert_gemv(f.expert_fmt, routed_O, routed_I, max_rows, dual,
+                                             max_tasks + (fused ? 2 : 0));
+            GemvLaunch Lr = L;
+            Lr.expert.routed_tasks = max_tasks;
+            Lr.expert.shared_task = fused ? 1 : 0;
+            int per_block = gemv_rows_per_block(plan, dual);
+            int blocks_x = (routed_O + per_block - 1) / per_block;
+            if (fused) {
+                const int sb = (shared_O + per_block - 1) / per_block;
+                if (sb > blocks_x) blocks_x = sb;
+            }
+            dim3 grid(blocks_x, max_tasks + (fused ? 1 : 0));
+            if (!dispatch_gemv(f.expert_fmt, Lr, 1, plan, grid, stream)) return kErrArgs;
+            (void)shared_I;
+        }
+        if (f.has_shared && !fused) {
+            GemvPlan plan = plan_expert_gemv(f.shared_fmt, shared_O, shared_I, max_rows, dual, 1);
+            GemvLaunch Ls = L;
+            Ls.expert.routed_tasks = 0;
+            Ls.expert.shared_task = 1;
+            const int per_block = gemv_rows_per_block(plan, dual);
+            dim3 grid((shared_O + per_block - 1) / per_block, 1);
+            if (!dispatch_gemv(f.shared_fmt, Ls, 1, plan, grid, stream)) return kErrArgs;
+        }
+    }
+    return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
+}
+
+// y[r] = x[r] * rsqrt(mean(x[r]^2) + eps) * w (moonlight_kernels.metal:23-41).
+__global__ __launch_bounds__(256) void rmsnorm_kernel(const float *x, const float *w, float *y,
+                                                      int width, float eps, long in_stride,
+                                                      long out_stride) {
+    __shared__ float part[4];
+    const float *src = x + (long)blockIdx.x * in_stride;
+    float *dst = y + (long)blockIdx.x * out_stride;
+    float ss = 0.0f;
+    for (int i = threadIdx.x; i < width; i += blockDim.x) ss += src[i] * src[i];
+    ss = wave_sum(ss);
+    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = ss;
+    __syncthreads();
+    const float total = (part[0] + part[1]) + (part[2] + part[3]);
+    const float inv = 1.0f / sqrtf(total / (float)width + eps);
+    for (int i = threadIdx.x; i < width; i += blockDim.x) dst[i] = src[i] * inv * w[i];
+}
+
+int rmsnorm_rows(const float *x, const float *w, float *y, int rows, int width, float eps,
+                 long in_stride, long out_stride, hipStream_t stream) {
+    if (!x || !w || !y || rows <= 0 || width <= 0) return kErrArgs;
+    hipLaunchKernelGGL(rmsnorm_kernel, dim3(rows), dim3(256), 0, stream, x, w, y, width, eps,
+                       in_stride, out_stride);
+    return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
+}
+
+// out[r, :] = table[ids[r], :] (moonlight_kernels.metal:10-21).
+__global__ __launch_bounds__(256) void embed_kernel(const float *table, const int *ids, float *out,
+                                                    int width, int vocab) {
+    const int r = blockIdx.x;
+    int id = ids[r];
+    id = id < 0 ? 0 : (id >= vocab ? vocab - 1 : id);  // host validated; clamp defensively
+    const float *src = table + (long)id * width;
+    for (int i = threadIdx.x; i < width; i += blockDim.x) out[(long)r * width + i] = src[i];
+}
+
+int embed_rows(const float *table, const int *ids, float *out, int rows, int width, int vocab,
+               hipStream_t stream) {
+    if (!table || !ids || !out || rows <= 0 || width <= 0) return kErrArgs;
+    hipLaunchKernelGGL(embed_kernel, dim3(rows), dim3(256), 0, stream, table, ids, out, width,
+                       vocab);
+    return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
+}
+
+// out = a + b elementwise (moonlight_kernels.metal:563-569).
+__global__ __launch_bounds__(256) void add_kernel(const float *a, const float *b, float *out,
+                                                  long n) {
+    for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (long)gridDim.x * blockDim.x)
+        out[i] = a[i] + b[i];
+}
+
+int add_vectors(const float *a, const float *b, float *out, long n, hipStream_t stream) {
+    if (!a || !b || !out || n <= 0) return kErrArgs;
+    long blocks = (n + 255) / 256;
+    if (blocks > 4096) blocks = 4096;
+    hipLaunchKernelGGL(add_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, a, b, out, n);
+    return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
+}
+
+}  // namespace mlh

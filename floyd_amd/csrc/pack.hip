@@ -107,6 +107,27 @@ __global__ __launch_bounds__(256) void copy16_kernel(const u32x4 *src, u32x4 *ds
         __builtin_nontemporal_store(load_stream16(src + i), dst + i);
 }
 
+// Read-only streaming yardstick: every workgroup folds its share of `src`
+// into one word.  Measures what pure HBM reads of a given size cost,
+// launch ramp and tail included (the ceiling for a GEMV of that size).
+__global__ __launch_bounds__(256) void read16_kernel(const u32x4 *src, long n, unsigned *out) {
+    unsigned acc = 0;
+    for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (long)gridDim.x * blockDim.x) {
+        u32x4 v = load_stream16(src + i);
+        acc ^= v.x ^ v.y ^ v.z ^ v.w;
+    }
+    acc = __reduce_xor_sync(~0ull, acc);
+    if ((threadIdx.x & 63) == 0) out[blockIdx.x * 4 + threadIdx.x / 64] = acc;
+}
+
+int read16(const void *src, size_t bytes, int blocks, unsigned *out, hipStream_t stream) {
+    if (!src || !out || bytes % 16 || blocks <= 0 || ((uintptr_t)src & 15)) return kErrArgs;
+    hipLaunchKernelGGL(read16_kernel, dim3((unsigned)blocks), dim3(256), 0, stream,
+                       static_cast<const u32x4 *>(src), (long)(bytes / 16), out);
+    return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
+}
+
 int copy16(const void *src, void *dst, size_t bytes, hipStream_t stream) {
     if (!src || !dst || bytes % 16 || ((uintptr_t)src | (uintptr_t)dst) & 15) return kErrArgs;
     const long n = (long)(bytes / 16);

@@ -1,0 +1,1325 @@
+// runtime.cpp -- the Moonlight session API (include/moonlight_hip.h and
+// include/moonlight_hip_ext.h) over the HIP kernels.
+//
+// Replaces floyd's moonlight_metal.m.  The per-layer graph and residual order
+// are the reference's (encode_attention_block / encode_dense_residual_buffer /
+// encode_moe_residual_buffer, moonlight_metal.m:442-706):
+//     h = x + o_proj(MLA(RMSNorm(x)))
+//     x' = h + FFN(RMSNorm(h)),  FFN = dense SwiGLU or routed + shared experts
+// but a forward is ONE submission: routing and its tables stay on the device,
+// so the 1 + (layers - first_dense) host waits of run_tokens_fast
+// (moonlight_metal.m:1892-1986) become a single wait for the logits.
+#include "container.h"
+#include "device_context.h"
+#include "mla.h"
+#include "moe.h"
+#include "../../include/moonlight_hip.h"
+#include "../../include/moonlight_hip_ext.h"
+
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <ctime>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+using namespace mlh;
+
+namespace {
+
+int set_error(char *error, size_t error_size, const char *format, ...) {
+    if (error && error_size) {
+        va_list args;
+        va_start(args, format);
+        vsnprintf(error, error_size, format, args);
+        va_end(args);
+    }
+    return 0;
+}
+
+double monotonic_seconds() {
+    timespec ts;
+    clock_gettime(CLOCK_MONOTONIC, &ts);
+    return ts.tv_sec + ts.tv_nsec * 1e-9;
+}
+
+size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+struct DeviceTensor {
+    std::string name;
+    int dtype = 0;
+    int64_t numel = 0, nbytes = 0;
+    uint8_t *dev = nullptr;
+};
+
+struct Matrix {
+    int fmt = kQ8;
+    const uint8_t *w = nullptr;
+    const float *s = nullptr;
+};
+
+struct LayerPlan {
+    std::string error;  // first problem found while resolving, empty if usable
+    Matrix q, kv_a, kv_b, o;
+    const float *input_norm = nullptr, *post_norm = nullptr, *kv_norm = nullptr;
+    bool dense = false;
+    Matrix gate, up, down;
+    Matrix router;
+    const float *bias = nullptr;
+    Matrix sh_gate, sh_up, sh_down;
+    int expert_fmt = kQ8;
+    ExpertWeights *expert_table = nullptr;  // device [experts] (inside the model's table)
+};
+
+}  // namespace
+
+struct MoonlightModel {
+    ModelConfig cfg;
+    std::vector<DeviceTensor> tensors;
+    std::unordered_map<std::string, int> index;
+    uint8_t *arena = nullptr;
+    size_t arena_bytes = 0;
+    uint64_t resident_bytes = 0;
+    std::vector<LayerPlan> layers;
+    ExpertWeights *expert_tables = nullptr;  // device [layers][experts]
+    float *inv_freq = nullptr;               // device [rope / 2]
+    const float *embed = nullptr;
+    const float *final_norm = nullptr;
+    Matrix lm_head;
+    std::string head_error;
+    std::string device_name;
+};
+
+struct MoonlightSession {
+    MoonlightModel *model = nullptr;
+    MoonlightOptions options{};
+    MoonlightStats stats{};
+    int max_splits = 0;
+    std::vector<void *> allocations;
+    // device buffers
+    float *h = nullptr, *tmp = nullptr, *query = nullptr, *compressed = nullptr;
+    float *query_rope = nullptr, *query_absorbed = nullptr, *context = nullptr;
+    float *part_max = nullptr, *part_sum = nullptr, *part_lc = nullptr;
+    float *latent_kv = nullptr, *rope_kv = nullptr, *logits = nullptr;
+    float *router_logits = nullptr, *route_weights = nullptr;
+    int *route_ids = nullptr, *n_unique = nullptr, *unique = nullptr, *counts = nullptr;
+    int *offsets = nullptr, *list_rows = nullptr, *list_slots = nullptr, *list_pos = nullptr;
+    int *route_error = nullptr, *route_trace = nullptr, *ids = nullptr;
+    float *expert_hidden = nullptr, *expert_out = nullptr;
+    float *shared_hidden = nullptr, *shared_out = nullptr, *dense_hidden = nullptr;
+    float *moe_routed = nullptr;  // routed part of moonlight_test_moe
+    // pinned host mirrors
+    int *host_ids = nullptr;
+    int *host_flag = nullptr;
+    std::vector<int> kv_lengths;
+    int last_forward_rows = 0;
+    int position = 0;
+    hipEvent_t ev_start = nullptr, ev_stop = nullptr;
+    double last_device_ms = 0.0;
+};
+
+namespace {
+
+// ---------------------------------------------------------------------------
+// model: tensors and layer plans
+// ---------------------------------------------------------------------------
+
+const DeviceTensor *find_tensor(const MoonlightModel *m, const std::string &name) {
+    auto it = m->index.find(name);
+    return it == m->index.end() ? nullptr : &m->tensors[it->second];
+}
+
+// resolve_matrix (moonlight_metal.m:129-162): f32 of in*out elements, or U8
+// with a `.qs` f32 scale of `out` elements and out*in (q8) or out*ceil(in/2)
+// (q4) bytes.
+bool resolve(const MoonlightModel *m, const std::string &name, int in_width, int out_width,
+             Matrix *mat) {
+    const DeviceTensor *t = find_tensor(m, name);
+    if (!t) return false;
+    mat->w = t->dev;
+    mat->s = nullptr;
+    if (t->dtype == kDtypeF32) {
+        if (t->numel != (int64_t)in_width * out_width) return false;
+        mat->fmt = kF32;
+        return true;
+    }
+    if (t->dtype != kDtypeU8) return false;
+    const DeviceTensor *st = find_tensor(m, name + ".qs");
+    if (!st || st->dtype != kDtypeF32 || st->numel != out_width) return false;
+    mat->s = reinterpret_cast<const float *>(st->dev);
+    if (t->nbytes == (int64_t)out_width * in_width) {
+        mat->fmt = kQ8;
+        return true;
+    }
+    if (t->nbytes == (int64_t)out_width * ((in_width + 1) / 2)) {
+        mat->fmt = kQ4;
+        return true;
+    }
+    return false;
+}
+
+const float *vector_f32(const MoonlightModel *m, const std::string &name, int64_t numel) {
+    const DeviceTensor *t = find_tensor(m, name);
+    if (!t || t->dtype != kDtypeF32 || t->numel != numel) return nullptr;
+    return reinterpret_cast<const float *>(t->dev);
+}
+
+std::string layer_name(int layer, const char *suffix) {
+    char buf[256];
+    snprintf(buf, sizeof(buf), "model.layers.%d.%s", layer, suffix);
+    return buf;
+}
+
+// Resolves every tensor a forward needs, once, at model open (the reference
+// resolves them per encode, moonlight_metal.m:307-329).  A missing or
+// mis-sized tensor is recorded and reported when a forward reaches it.
+bool build_plans(MoonlightModel *m, std::string *error) {
+    const ModelConfig &c = m->cfg;
+    m->layers.assign(c.layer_count, LayerPlan());
+    std::vector<ExpertWeights> host_tables((size_t)c.layer_count * c.expert_count);
+    const int qw = c.head_count * (c.qk_nope_dim + c.qk_rope_dim);
+    const int cw = c.kv_lora_rank + c.qk_rope_dim;
+    const int sw = c.moe_intermediate_size * c.shared_expert_count;
+    for (int l = 0; l < c.layer_count; ++l) {
+        LayerPlan &p = m->layers[l];
+        auto need = [&](bool ok, const std::string &what) {
+            if (!ok && p.error.empty()) p.error = "missing or mis-sized tensor " + what;
+        };
+        std::string n;
+        n = layer_name(l, "self_attn.q_proj.weight");
+        need(resolve(m, n, c.hidden_size, qw, &p.q), n);
+        n = layer_name(l, "self_attn.kv_a_proj_with_mqa.weight");
+        need(resolve(m, n, c.hidden_size, cw, &p.kv_a), n);
+        n = layer_name(l, "self_attn.kv_b_proj.weight");
+        need(resolve(m, n, c.kv_lora_rank, c.head_count * (c.qk_nope_dim + c.value_dim), &p.kv_b),
+             n);
+        n = layer_name(l, "self_attn.o_proj.weight");
+        need(resolve(m, n, c.head_count * c.value_dim, c.hidden_size, &p.o), n);
+        n = layer_name(l, "self_attn.kv_a_layernorm.weight");
+        need((p.kv_norm = vector_f32(m, n, c.kv_lora_rank)) != nullptr, n);
+        n = layer_name(l, "input_layernorm.weight");
+        need((p.input_norm = vector_f32(m, n, c.hidden_size)) != nullptr, n);
+        n = layer_name(l, "post_attention_layernorm.weight");
+        need((p.post_norm = vector_f32(m, n, c.hidden_size)) != nullptr, n);
+        p.dense = l < c.first_dense_layer_count;
+        if (p.dense) {
+            n = layer_name(l, "mlp.gate_proj.weight");
+            need(resolve(m, n, c.hidden_size, c.dense_intermediate_size, &p.gate), n);
+            n = layer_name(l, "mlp.up_proj.weight");
+            need(resolve(m, n, c.hidden_size, c.dense_intermediate_size, &p.up), n);
+            n = layer_name(l, "mlp.down_proj.weight");
+            need(resolve(m, n, c.dense_intermediate_size, c.hidden_size, &p.down), n);
+            if (p.error.empty() && (p.gate.fmt != p.up.fmt))
+                p.error = "gate and up projections of layer " + std::to_string(l) +
+                          " use different formats";
+            continue;
+        }
+        n = layer_name(l, "mlp.gate.weight");
+        need(resolve(m, n, c.hidden_size, c.expert_count, &p.router), n);
+        n = layer_name(l, "mlp.gate.e_score_correction_bias");
+        need((p.bias = vector_f32(m, n, c.expert_count)) != nullptr, n);
+        n = layer_name(l, "mlp.shared_experts.gate_proj.weight");
+        need(resolve(m, n, c.hidden_size, sw, &p.sh_gate), n);
+        n = layer_name(l, "mlp.shared_experts.up_proj.weight");
+        need(resolve(m, n, c.hidden_size, sw, &p.sh_up), n);
+        n = layer_name(l, "mlp.shared_experts.down_proj.weight");
+        need(resolve(m, n, sw, c.hidden_size, &p.sh_down), n);
+        if (p.error.empty() && (p.sh_gate.fmt != p.sh_up.fmt || p.sh_gate.fmt != p.sh_down.fmt))
+            p.error = "shared expert projections of layer " + std::to_string(l) +
+                      " use different formats";
+        for (int e = 0; e < c.expert_count; ++e) {
+            Matrix g, u, d;
+            char buf[256];
+            snprintf(buf, sizeof(buf), "model.layers.%d.mlp.experts.%d.", l, e);
+            const std::string base = buf;
+            const bool ok = resolve(m, base + "gate_proj.weight", c.hidden_size,
+                                    c.moe_intermediate_size, &g) &&
+                            resolve(m, base + "up_proj.weight", c.hidden_size,
+                                    c.moe_intermediate_size, &u) &&
+                            resolve(m, base + "down_proj.weight", c.moe_intermediate_size,
+                                    c.hidden_size, &d);
+            need(ok, base + "{gate,up,down}_proj.weight");
+            if (!ok) continue;
+            if (e == 0) p.expert_fmt = g.fmt;
+            if (p.error.empty() && (g.fmt != p.expert_fmt || u.fmt != g.fmt || d.fmt != g.fmt ||
+                                    g.fmt == kF32))
+                p.error = "routed experts of layer " + std::to_string(l) +
+                          " must all use one quantized format";
+            ExpertWeights &w = host_tables[(size_t)l * c.expert_count + e];
+            w.gate = g.w;
+            w.up = u.w;
+            w.down = d.w;
+            w.gate_s = g.s;
+            w.up_s = u.s;
+            w.down_s = d.s;
+        }
+    }
+    if (!resolve(m, "lm_head.weight", c.hidden_size, c.vocab_size, &m->lm_head))
+        m->head_error = "missing or mis-sized tensor lm_head.weight";
+    m->embed = vector_f32(m, "model.embed_tokens.weight", (int64_t)c.vocab_size * c.hidden_size);
+    m->final_norm = vector_f32(m, "model.norm.weight", c.hidden_size);
+    if (!m->embed && m->head_error.empty()) m->head_error = "missing tensor model.embed_tokens.weight";
+    if (!m->final_norm && m->head_error.empty()) m->head_error = "missing tensor model.norm.weight";
+
+    // device tables: expert pointers per layer, RoPE inverse frequencies
+    // theta^(-2p/rope) computed with the host libm powf exactly as the
+    // reference's CPU check does (tests/test_moonlight_metal_mla.c:92-108)
+    const size_t table_bytes = host_tables.size() * sizeof(ExpertWeights);
+    std::vector<float> inv(c.qk_rope_dim / 2 > 0 ? c.qk_rope_dim / 2 : 1);
+    for (int p = 0; p < c.qk_rope_dim / 2; ++p)
+        inv[p] = powf(c.rope_theta, -2.0f * (float)p / (float)c.qk_rope_dim);
+    if (hipMalloc((void **)&m->expert_tables, table_bytes ? table_bytes : 1) != hipSuccess ||
+        hipMalloc((void **)&m->inv_freq, inv.size() * sizeof(float)) != hipSuccess) {
+        *error = "cannot allocate model tables";
+        return false;
+    }
+    if ((table_bytes && hipMemcpy(m->expert_tables, host_tables.data(), table_bytes,
+                                  hipMemcpyHostToDevice) != hipSuccess) ||
+        hipMemcpy(m->inv_freq, inv.data(), inv.size() * sizeof(float), hipMemcpyHostToDevice) !=
+            hipSuccess) {
+        *error = "cannot upload model tables";
+        return false;
+    }
+    for (int l = 0; l < c.layer_count; ++l)
+        m->layers[l].expert_table = m->expert_tables + (size_t)l * c.expert_count;
+    return true;
+}
+
+void free_model(MoonlightModel *m) {
+    if (!m) return;
+    if (m->arena) (void)hipFree(m->arena);
+    if (m->expert_tables) (void)hipFree(m->expert_tables);
+    if (m->inv_freq) (void)hipFree(m->inv_freq);
+    delete m;
+}
+
+bool place_tensors(MoonlightModel *m, std::string *error) {
+    size_t total = 0;
+    for (auto &t : m->tensors) total += align256((size_t)(t.nbytes > 0 ? t.nbytes : 1));
+    size_t free_b = 0, total_b = 0;
+    if (hipMemGetInfo(&free_b, &total_b) == hipSuccess && total > free_b * 9 / 10) {
+        char buf[256];
+        snprintf(buf, sizeof(buf), "model requires %.2f GiB, above the free HBM budget %.2f GiB",
+                 total / 1073741824.0, free_b * 0.9 / 1073741824.0);
+        *error = buf;
+        return false;
+    }
+    if (hipMalloc((void **)&m->arena, total ? total : 256) != hipSuccess) {
+        *error = "HBM allocation of the model failed";
+        return false;
+    }
+    m->arena_bytes = total;
+    size_t off = 0;
+    for (size_t i = 0; i < m->tensors.size(); ++i) {
+        DeviceTensor &t = m->tensors[i];
+        t.dev = m->arena + off;
+        off += align256((size_t)(t.nbytes > 0 ? t.nbytes : 1));
+        m->resident_bytes += (uint64_t)t.nbytes;
+        if (!m->index.count(t.name)) m->index[t.name] = (int)i;
+    }
+    return true;
+}
+
+// Container upload: pread into two pinned staging buffers alternately while
+// the previous one is copied to HBM.
+bool upload_container(MoonlightModel *m, const Container &ct, std::string *error) {
+    constexpr size_t kStage = 64u << 20;
+    DeviceContext *ctx = context();
+    void *stage[2] = {nullptr, nullptr};
+    hipEvent_t done[2] = {nullptr, nullptr};
+    bool ok = hipHostMalloc(&stage[0], kStage, hipHostMallocDefault) == hipSuccess &&
+              hipHostMalloc(&stage[1], kStage, hipHostMallocDefault) == hipSuccess &&
+              hipEventCreateWithFlags(&done[0], hipEventDisableTiming) == hipSuccess &&
+              hipEventCreateWithFlags(&done[1], hipEventDisableTiming) == hipSuccess;
+    int which = 0;
+    bool pending[2] = {false, false};
+    for (size_t i = 0; ok && i < m->tensors.size(); ++i) {
+        const TensorEntry &te = ct.tensors()[i];
+        const DeviceTensor &t = m->tensors[i];
+        int64_t done_bytes = 0;
+        while (ok && done_bytes < te.nbytes) {
+            const size_t n = (size_t)std::min<int64_t>((int64_t)kStage, te.nbytes - done_bytes);
+            if (pending[which]) {
+                ok = hipEventSynchronize(done[which]) == hipSuccess;
+                pending[which] = false;
+            }
+            if (ok) ok = ct.read_slice(i, done_bytes, n, stage[which]);
+            if (ok)
+                ok = hipMemcpyAsync(t.dev + done_bytes, stage[which], n, hipMemcpyHostToDevice,
+                                    ctx->stream) == hipSuccess &&
+                     hipEventRecord(done[which], ctx->stream) == hipSuccess;
+            pending[which] = ok;
+            which ^= 1;
+            done_bytes += (int64_t)n;
+        }
+        if (!ok) *error = "cannot upload tensor " + te.name;
+    }
+    if (ok) ok = hipStreamSynchronize(ctx->stream) == hipSuccess;
+    for (int i = 0; i < 2; ++i) {
+        if (done[i]) (void)hipEventDestroy(done[i]);
+        if (stage[i]) (void)hipHostFree(stage[i]);
+    }
+    if (!ok && error->empty()) *error = "model upload failed";
+    return ok;
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+// model API
+// ---------------------------------------------------------------------------
+
+extern "C" int moonlight_model_open(MoonlightModel **out, const char *path, char *error,
+                                    size_t error_size) {
+    if (!out) return set_error(error, error_size, "model output is required");
+    *out = nullptr;
+    if (!path || !path[0]) return set_error(error, error_size, "model path is required");
+    DeviceContext *ctx = context();
+    if (!ctx) return set_error(error, error_size, "HIP device is unavailable: %s", last_error());
+    Container ct;
+    std::string why;
+    if (!ct.open(path, &why)) return set_error(error, error_size, "%s", why.c_str());
+    MoonlightModel *m = new MoonlightModel();
+    m->cfg = ct.config();
+    m->device_name = ctx->name;
+    for (const TensorEntry &te : ct.tensors()) {
+        DeviceTensor t;
+        t.name = te.name;
+        t.dtype = te.dtype;
+        t.numel = te.numel;
+        t.nbytes = te.nbytes;
+        m->tensors.push_back(t);
+    }
+    if (!place_tensors(m, &why) || !upload_container(m, ct, &why) || !build_plans(m, &why)) {
+        free_model(m);
+        return set_error(error, error_size, "%s", why.c_str());
+    }
+    *out = m;
+    return 1;
+}
+
+extern "C" void moonlight_model_close(MoonlightModel *model) { free_model(model); }
+
+extern "C" const char *moonlight_device_name(const MoonlightModel *model) {
+    return model ? model->device_name.c_str() : "(none)";
+}
+
+extern "C" MoonlightModelInfo moonlight_model_info(const MoonlightModel *model) {
+    MoonlightModelInfo r;
+    memset(&r, 0, sizeof(r));
+    if (!model) return r;
+    const ModelConfig &c = model->cfg;
+    r.hidden_size = c.hidden_size;
+    r.layer_count = c.layer_count;
+    r.vocab_size = c.vocab_size;
+    r.head_count = c.head_count;
+    r.kv_lora_rank = c.kv_lora_rank;
+    r.qk_nope_dim = c.qk_nope_dim;
+    r.qk_rope_dim = c.qk_rope_dim;
+    r.value_dim = c.value_dim;
+    r.expert_count = c.expert_count;
+    r.experts_per_token = c.experts_per_token;
+    r.moe_intermediate_size = c.moe_intermediate_size;
+    r.shared_expert_count = c.shared_expert_count;
+    r.first_dense_layer_count = c.first_dense_layer_count;
+    r.rms_norm_epsilon = c.rms_norm_epsilon;
+    r.rope_theta = c.rope_theta;
+    r.routed_scale = c.routed_scale;
+    r.resident_bytes = model->resident_bytes;
+    return r;
+}
+
+extern "C" MoonlightSyntheticConfig moonlight_synthetic_moonlight_config(void) {
+    MoonlightSyntheticConfig c;
+    memset(&c, 0, sizeof(c));
+    c.hidden_size = 2048;
+    c.layer_count = 27;
+    c.head_count = 16;
+    c.expert_count = 64;
+    c.experts_per_token = 6;
+    c.dense_intermediate_size = 11264;
+    c.moe_intermediate_size = 1408;
+    c.first_dense_layer_count = 1;
+    c.kv_lora_rank = 512;
+    c.qk_nope_dim = 128;
+    c.qk_rope_dim = 64;
+    c.value_dim = 128;
+    c.shared_expert_count = 2;
+    c.normalize_topk = 1;
+    c.vocab_size = 163840;
+    c.rms_norm_epsilon = 1e-5f;
+    c.rope_theta = 50000.0f;
+    c.routed_scale = 2.446f;
+    c.expert_bits = 8;
+    c.dense_bits = 8;
+    c.weight_std = 0.02f;
+    c.seed = 1;
+    return c;
+}
+
+namespace {
+
+// One synthetic tensor: a packed matrix, an f32 matrix, a norm (ones) or the
+// selection bias.
+struct SynthSpec {
+    std::string name;
+    enum Kind { kPacked, kF32Matrix, kOnes, kBias } kind;
+    int rows = 0, cols = 0, bits = 8;
+};
+
+void add_matrix(std::vector<SynthSpec> &v, const std::string &name, int rows, int cols, int bits) {
+    v.push_back({name, SynthSpec::kPacked, rows, cols, bits});
+}
+
+}  // namespace
+
+extern "C" int moonlight_model_create_synthetic(MoonlightModel **out,
+                                                const MoonlightSyntheticConfig *sc, char *error,
+                                                size_t error_size) {
+    if (!out || !sc) return set_error(error, error_size, "model output and config are required");
+    *out = nullptr;
+    DeviceContext *ctx = context();
+    if (!ctx) return set_error(error, error_size, "HIP device is unavailable: %s", last_error());
+    if (sc->hidden_size <= 0 || sc->layer_count <= 0 || sc->head_count <= 0 ||
+        sc->expert_count <= 0 || sc->experts_per_token <= 0 || sc->kv_lora_rank <= 0 ||
+        sc->qk_rope_dim <= 0 || sc->vocab_size <= 0 ||
+        (sc->expert_bits != 8 && sc->expert_bits != 4) ||
+        (sc->dense_bits != 8 && sc->dense_bits != 4))
+        return set_error(error, error_size, "unsupported synthetic Moonlight config");
+    MoonlightModel *m = new MoonlightModel();
+    ModelConfig &c = m->cfg;
+    c.hidden_size = sc->hidden_size;
+    c.layer_count = sc->layer_count;
+    c.head_count = sc->head_count;
+    c.expert_count = sc->expert_count;
+    c.experts_per_token = sc->experts_per_token;
+    c.dense_intermediate_size = sc->dense_intermediate_size;
+    c.moe_intermediate_size = sc->moe_intermediate_size;
+    c.first_dense_layer_count = sc->first_dense_layer_count;
+    c.kv_lora_rank = sc->kv_lora_rank;
+    c.qk_nope_dim = sc->qk_nope_dim;
+    c.qk_rope_dim = sc->qk_rope_dim;
+    c.value_dim = sc->value_dim;
+    c.shared_expert_count = sc->shared_expert_count;
+    c.normalize_topk = sc->normalize_topk;
+    c.vocab_size = sc->vocab_size;
+    c.rms_norm_epsilon = sc->rms_norm_epsilon;
+    c.rope_theta = sc->rope_theta;
+    c.routed_scale = sc->routed_scale;
+    m->device_name = ctx->name;
+
+    std::vector<SynthSpec> specs;
+    const int H = c.hidden_size, eb = sc->expert_bits, db = sc->dense_bits;
+    specs.push_back({"model.embed_tokens.weight", SynthSpec::kF32Matrix, c.vocab_size, H, 0});
+    specs.push_back({"model.norm.weight", SynthSpec::kOnes, 1, H, 0});
+    specs.push_back({"lm_head.weight", SynthSpec::kF32Matrix, c.vocab_size, H, 0});
+    for (int l = 0; l < c.layer_count; ++l) {
+        specs.push_back({layer_name(l, "input_layernorm.weight"), SynthSpec::kOnes, 1, H, 0});
+        specs.push_back({layer_name(l, "post_attention_layernorm.weight"), SynthSpec::kOnes, 1, H, 0});
+        add_matrix(specs, layer_name(l, "self_attn.q_proj.weight"),
+                   c.head_count * (c.qk_nope_dim + c.qk_rope_dim), H, db);
+        add_matrix(specs, layer_name(l, "self_attn.kv_a_proj_with_mqa.weight"),
+                   c.kv_lora_rank + c.qk_rope_dim, H, db);
+        specs.push_back({layer_name(l, "self_attn.kv_a_layernorm.weight"), SynthSpec::kOnes, 1,
+                         c.kv_lora_rank, 0});
+        add_matrix(specs, layer_name(l, "self_attn.kv_b_proj.weight"),
+                   c.head_count * (c.qk_nope_dim + c.value_dim), c.kv_lora_rank, db);
+        add_matrix(specs, layer_name(l, "self_attn.o_proj.weight"), H, c.head_count * c.value_dim,
+                   db);
+        if (l < c.first_dense_layer_count) {
+            add_matrix(specs, layer_name(l, "mlp.gate_proj.weight"), c.dense_intermediate_size, H, db);
+            add_matrix(specs, layer_name(l, "mlp.up_proj.weight"), c.dense_intermediate_size, H, db);
+            add_matrix(specs, layer_name(l, "mlp.down_proj.weight"), H, c.dense_intermediate_size, db);
+            continue;
+        }
+        specs.push_back({layer_name(l, "mlp.gate.weight"), SynthSpec::kF32Matrix, c.expert_count, H, 0});
+        specs.push_back({layer_name(l, "mlp.gate.e_score_correction_bias"), SynthSpec::kBias, 1,
+                         c.expert_count, 0});
+        const int sw = c.moe_intermediate_size * c.shared_expert_count;
+        add_matrix(specs, layer_name(l, "mlp.shared_experts.gate_proj.weight"), sw, H, db);
+        add_matrix(specs, layer_name(l, "mlp.shared_experts.up_proj.weight"), sw, H, db);
+        add_matrix(specs, layer_name(l, "mlp.shared_experts.down_proj.weight"), H, sw, db);
+        for (int e = 0; e < c.expert_count; ++e) {
+            char buf[256];
+            snprintf(buf, sizeof(buf), "model.layers.%d.mlp.experts.%d.", l, e);
+            add_matrix(specs, std::string(buf) + "down_proj.weight", H, c.moe_intermediate_size, eb);
+            add_matrix(specs, std::string(buf) + "gate_proj.weight", c.moe_intermediate_size, H, eb);
+            add_matrix(specs, std::string(buf) + "up_proj.weight", c.moe_intermediate_size, H, eb);
+        }
+    }
+    // tensor table in container order: a packed matrix is followed by its scale
+    size_t scratch_elems = 1;
+    for (const SynthSpec &s : specs) {
+        DeviceTensor t;
+        t.name = s.name;
+        if (s.kind == SynthSpec::kPacked) {
+            t.dtype = kDtypeU8;
+            t.nbytes = (int64_t)s.rows * (s.bits == 8 ? s.cols : (s.cols + 1) / 2);
+            t.numel = t.nbytes;
+            m->tensors.push_back(t);
+            DeviceTensor qs;
+            qs.name = s.name + ".qs";
+            qs.dtype = kDtypeF32;
+            qs.numel = s.rows;
+            qs.nbytes = (int64_t)s.rows * 4;
+            m->tensors.push_back(qs);
+            scratch_elems = std::max(scratch_elems, (size_t)s.rows * s.cols);
+        } else {
+            t.dtype = kDtypeF32;
+            t.numel = (int64_t)s.rows * s.cols;
+            t.nbytes = t.numel * 4;
+            m->tensors.push_back(t);
+        }
+    }
+    std::string why;
+    if (!place_tensors(m, &why)) {
+        free_model(m);
+        return set_error(error, error_size, "%s", why.c_str());
+    }
+    float *scratch = nullptr;
+    std::vector<float> host_small;
+    bool ok = hipMalloc((void **)&scratch, scratch_elems * sizeof(float)) == hipSuccess;
+    uint64_t stream_id = 0;
+    for (const SynthSpec &s : specs) {
+        if (!ok) break;
+        const DeviceTensor &t = m->tensors[m->index[s.name]];
+        const uint64_t seed = sc->seed * 0x9E3779B97F4A7C15ULL + 1000003ULL * (++stream_id);
+        if (s.kind == SynthSpec::kPacked) {
+            const DeviceTensor &qs = m->tensors[m->index[s.name + ".qs"]];
+            ok = fill_normal(scratch, (int64_t)s.rows * s.cols, seed, 0.0f, sc->weight_std, 1,
+                             ctx->stream) == kOk &&
+                 quantize_rows(s.bits, scratch, s.rows, s.cols, t.dev,
+                               reinterpret_cast<float *>(qs.dev), ctx->stream) == kOk;
+        } else if (s.kind == SynthSpec::kF32Matrix) {
+            ok = fill_normal(reinterpret_cast<float *>(t.dev), t.numel, seed, 0.0f, sc->weight_std,
+                             1, ctx->stream) == kOk;
+        } else {
+            host_small.assign((size_t)t.numel, 1.0f);
+            if (s.kind == SynthSpec::kBias)
+                for (int64_t i = 0; i < t.numel; ++i)
+                    host_small[i] = t.numel > 1 ? -0.1f + 0.2f * (float)i / (float)(t.numel - 1)
+                                                : 0.0f;
+            ok = hipMemcpyAsync(t.dev, host_small.data(), t.nbytes, hipMemcpyHostToDevice,
+                                ctx->stream) == hipSuccess &&
+                 hipStreamSynchronize(ctx->stream) == hipSuccess;
+        }
+    }
+    if (ok) ok = hipStreamSynchronize(ctx->stream) == hipSuccess;
+    if (scratch) (void)hipFree(scratch);
+    if (!ok || !build_plans(m, &why)) {
+        free_model(m);
+        return set_error(error, error_size, "synthetic model generation failed: %s",
+                         why.empty() ? "device error" : why.c_str());
+    }
+    *out = m;
+    return 1;
+}
+
+extern "C" int moonlight_container_probe(const char *path, int *ints16, float *floats3,
+                                         char *error, size_t error_size) {
+    if (!path || !ints16 || !floats3) {
+        set_error(error, error_size, "path and outputs are required");
+        return -1;
+    }
+    Container ct;
+    std::string why;
+    if (!ct.open(path, &why)) {
+        set_error(error, error_size, "%s", why.c_str());
+        return -1;
+    }
+    const ModelConfig &c = ct.config();
+    const int v[16] = {c.hidden_size, c.layer_count, c.head_count, c.expert_count,
+                       c.experts_per_token, c.dense_intermediate_size, c.moe_intermediate_size,
+                       c.first_dense_layer_count, c.q_lora_rank, c.kv_lora_rank, c.qk_nope_dim,
+                       c.qk_rope_dim, c.value_dim, c.shared_expert_count, c.normalize_topk,
+                       c.vocab_size};
+    memcpy(ints16, v, sizeof(v));
+    floats3[0] = c.rms_norm_epsilon;
+    floats3[1] = c.rope_theta;
+    floats3[2] = c.routed_scale;
+    return (int)ct.tensors().size();
+}
+
+extern "C" int moonlight_container_tensor(const char *path, const char *name, int *dtype,
+                                          int64_t *numel, int64_t *nbytes) {
+    if (!path || !name) return 0;
+    Container ct;
+    std::string why;
+    if (!ct.open(path, &why)) return 0;
+    const int i = ct.find(name);
+    if (i < 0) return 0;
+    const TensorEntry &t = ct.tensors()[i];
+    if (dtype) *dtype = t.dtype;
+    if (numel) *numel = t.numel;
+    if (nbytes) *nbytes = t.nbytes;
+    return 1;
+}
+
+extern "C" size_t moonlight_model_read_tensor(const MoonlightModel *model, const char *name,
+                                              void *dst, size_t capacity) {
+    if (!model || !name || !dst) return 0;
+    const DeviceTensor *t = find_tensor(model, name);
+    if (!t || (size_t)t->nbytes > capacity) return 0;
+    DeviceContext *ctx = context();
+    if (!ctx || hipMemcpyAsync(dst, t->dev, (size_t)t->nbytes, hipMemcpyDeviceToHost,
+                               ctx->stream) != hipSuccess ||
+        hipStreamSynchronize(ctx->stream) != hipSuccess)
+        return 0;
+    return (size_t)t->nbytes;
+}
+
+extern "C" int moonlight_model_tensor_info(const MoonlightModel *model, const char *name,
+                                           int *dtype, int64_t *numel, int64_t *nbytes) {
+    if (!model || !name) return 0;
+    const DeviceTensor *t = find_tensor(model, name);
+    if (!t) return 0;
+    if (dtype) *dtype = t->dtype;
+    if (numel) *numel = t->numel;
+    if (nbytes) *nbytes = t->nbytes;
+    return 1;
+}
+
+// ---------------------------------------------------------------------------
+// session
+// ---------------------------------------------------------------------------
+
+namespace {
+
+bool mul_ok(size_t a, size_t b, size_t *r) {
+    if (b && a > SIZE_MAX / b) return false;
+    *r = a * b;
+    return true;
+}
+
+template <typename T>
+bool session_alloc(MoonlightSession *s, T **ptr, size_t elems, char *error, size_t error_size) {
+    size_t bytes;
+    if (!mul_ok(elems ? elems : 1, sizeof(T), &bytes)) {
+        set_error(error, error_size, "Moonlight session size overflow");
+        return false;
+    }
+    void *p = nullptr;
+    if (hipMalloc(&p, bytes) != hipSuccess) {
+        set_error(error, error_size, "HBM allocation failed: %zu bytes", bytes);
+        return false;
+    }
+    s->allocations.push_back(p);
+    s->stats.buffer_allocations++;
+    s->stats.resident_bytes += bytes;
+    *ptr = static_cast<T *>(p);
+    return true;
+}
+
+void free_session(MoonlightSession *s) {
+    if (!s) return;
+    for (void *p : s->allocations) (void)hipFree(p);
+    if (s->host_ids) (void)hipHostFree(s->host_ids);
+    if (s->host_flag) (void)hipHostFree(s->host_flag);
+    if (s->ev_start) (void)hipEventDestroy(s->ev_start);
+    if (s->ev_stop) (void)hipEventDestroy(s->ev_stop);
+    delete s;
+}
+
+hipStream_t stream_of(const MoonlightSession *) { return context()->stream; }
+
+// Synchronises the stream (one "command buffer" in the reference's sense).
+bool finish(MoonlightSession *s) {
+    s->stats.command_buffers++;
+    return hipStreamSynchronize(stream_of(s)) == hipSuccess;
+}
+
+bool to_device(MoonlightSession *s, void *dst, const void *src, size_t bytes) {
+    return hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, stream_of(s)) == hipSuccess;
+}
+
+bool to_host(MoonlightSession *s, void *dst, const void *src, size_t bytes) {
+    return hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, stream_of(s)) == hipSuccess;
+}
+
+int gemv_rows(MoonlightSession *s, const Matrix &m, const float *x, int rows, int in_w,
+              int out_w, float *y, const float *norm_w = nullptr, const float *resid = nullptr) {
+    GemvParams p;
+    p.fmt = m.fmt;
+    p.w = m.w;
+    p.s = m.s;
+    p.O = out_w;
+    p.I = in_w;
+    p.rows = rows;
+    p.x = x;
+    p.x_stride = in_w;
+    p.norm_w = norm_w;
+    p.eps = s->model->cfg.rms_norm_epsilon;
+    p.y = y;
+    p.y_stride = out_w;
+    p.resid = resid;
+    p.resid_stride = out_w;
+    p.epilogue = resid ? kEpiResidual : kEpiPlain;
+    return gemv(p, stream_of(s));
+}
+
+int swiglu_rows(MoonlightSession *s, const Matrix &g, const Matrix &u, const float *x, int rows,
+                int in_w, int width, float *h, const float *norm_w) {
+    GemvParams p;
+    p.fmt = g.fmt;
+    p.w = g.w;
+    p.s = g.s;
+    p.w2 = u.w;
+    p.s2 = u.s;
+    p.O = width;
+    p.I = in_w;
+    p.rows = rows;
+    p.x = x;
+    p.x_stride = in_w;
+    p.norm_w = norm_w;
+    p.eps = s->model->cfg.rms_norm_epsilon;
+    p.y = h;
+    p.y_stride = width;
+    p.epilogue = kEpiSiluDual;
+    return gemv(p, stream_of(s));
+}
+
+// Attention of `layer` for `rows` rows of (already normalised) x at
+// `position`; writes o_proj(ctx) (+ resid) into out.
+int attention(MoonlightSession *s, int layer, const float *x, int rows, int position,
+              float *out, const float *norm_w, const float *resid) {
+    const ModelConfig &c = s->model->cfg;
+    const LayerPlan &lp = s->model->layers[layer];
+    const int qw = c.head_count * (c.qk_nope_dim + c.qk_rope_dim);
+    const int cw = c.kv_lora_rank + c.qk_rope_dim;
+    if (gemv_rows(s, lp.q, x, rows, c.hidden_size, qw, s->query, norm_w)) return kErrLaunch;
+    if (gemv_rows(s, lp.kv_a, x, rows, c.hidden_size, cw, s->compressed, norm_w))
+        return kErrLaunch;
+    MlaParams p;
+    p.rows = rows;
+    p.position = position;
+    p.heads = c.head_count;
+    p.nope = c.qk_nope_dim;
+    p.rope = c.qk_rope_dim;
+    p.vdim = c.value_dim;
+    p.latent = c.kv_lora_rank;
+    p.eps = c.rms_norm_epsilon;
+    p.scale = 1.0f / sqrtf((float)(c.qk_nope_dim + c.qk_rope_dim));
+    p.query = s->query;
+    p.compressed = s->compressed;
+    p.kv_norm = lp.kv_norm;
+    p.inv_freq = s->model->inv_freq;
+    p.kv_b.fmt = lp.kv_b.fmt;
+    p.kv_b.w = lp.kv_b.w;
+    p.kv_b.s = lp.kv_b.s;
+    p.latent_cache = s->latent_kv + (size_t)layer * s->options.context_size * c.kv_lora_rank;
+    p.rope_cache = s->rope_kv + (size_t)layer * s->options.context_size * c.qk_rope_dim;
+    p.query_rope = s->query_rope;
+    p.query_absorbed = s->query_absorbed;
+    p.max_splits = s->max_splits;
+    p.part_max = s->part_max;
+    p.part_sum = s->part_sum;
+    p.part_lc = s->part_lc;
+    p.context = s->context;
+    if (int e = mla_attention_core(p, stream_of(s))) return e;
+    return gemv_rows(s, lp.o, s->context, rows, c.head_count * c.value_dim, c.hidden_size, out,
+                     nullptr, resid);
+}
+
+int route(MoonlightSession *s, int layer, const float *x, int rows, const float *norm_w,
+          int *trace) {
+    const ModelConfig &c = s->model->cfg;
+    const LayerPlan &lp = s->model->layers[layer];
+    if (gemv_rows(s, lp.router, x, rows, c.hidden_size, c.expert_count, s->router_logits, norm_w))
+        return kErrLaunch;
+    RouteParams r;
+    r.logits = s->router_logits;
+    r.bias = lp.bias;
+    r.rows = rows;
+    r.experts = c.expert_count;
+    r.top_k = c.experts_per_token;
+    r.normalize = c.normalize_topk;
+    r.routed_scale = c.routed_scale;
+    r.ids = s->route_ids;
+    r.weights = s->route_weights;
+    r.trace = trace;
+    r.n_unique = s->n_unique;
+    r.unique = s->unique;
+    r.counts = s->counts;
+    r.offsets = s->offsets;
+    r.list_rows = s->list_rows;
+    r.list_slots = s->list_slots;
+    r.list_pos = s->list_pos;
+    r.error = s->route_error;
+    return route_topk(r, stream_of(s));
+}
+
+int experts(MoonlightSession *s, int layer, const float *x, int rows, const float *norm_w,
+            const float *resid, float *out, float *routed_copy) {
+    const ModelConfig &c = s->model->cfg;
+    const LayerPlan &lp = s->model->layers[layer];
+    ExpertFfnParams f;
+    f.rows = rows;
+    f.experts = c.expert_count;
+    f.top_k = c.experts_per_token;
+    f.hidden = c.hidden_size;
+    f.inter = c.moe_intermediate_size;
+    f.shared_width = c.moe_intermediate_size * c.shared_expert_count;
+    f.expert_fmt = lp.expert_fmt;
+    f.shared_fmt = lp.sh_gate.fmt;
+    f.has_shared = 1;
+    f.expert_table = lp.expert_table;
+    f.shared_gate = lp.sh_gate.w;
+    f.shared_up = lp.sh_up.w;
+    f.shared_down = lp.sh_down.w;
+    f.shared_gate_s = lp.sh_gate.s;
+    f.shared_up_s = lp.sh_up.s;
+    f.shared_down_s = lp.sh_down.s;
+    f.n_unique = s->n_unique;
+    f.unique = s->unique;
+    f.counts = s->counts;
+    f.offsets = s->offsets;
+    f.list_rows = s->list_rows;
+    f.x = x;
+    f.norm_w = norm_w;
+    f.eps = c.rms_norm_epsilon;
+    f.expert_hidden = s->expert_hidden;
+    f.expert_out = s->expert_out;
+    f.shared_hidden = s->shared_hidden;
+    f.shared_out = s->shared_out;
+    if (int e = expert_ffn(f, stream_of(s))) return e;
+    CombineParams cb;
+    cb.rows = rows;
+    cb.hidden = c.hidden_size;
+    cb.top_k = c.experts_per_token;
+    cb.weights = s->route_weights;
+    cb.list_pos = s->list_pos;
+    cb.expert_out = s->expert_out;
+    cb.shared_out = s->shared_out;
+    cb.resid = resid;
+    cb.routed_copy = routed_copy;
+    cb.out = out;
+    return moe_combine(cb, stream_of(s));
+}
+
+// run_tokens_fast (moonlight_metal.m:1892-1986) as one device submission.
+int forward(MoonlightSession *s, const int *ids, int count, int start, float *last_logits,
+            float *layer_outputs, char *error, size_t error_size) {
+    MoonlightModel *m = s->model;
+    const ModelConfig &c = m->cfg;
+    if (!m->head_error.empty())
+        return set_error(error, error_size, "Moonlight fast final projection failed: %s",
+                         m->head_error.c_str());
+    for (int i = 0; i < count; ++i)
+        if (ids[i] < 0 || ids[i] >= c.vocab_size)
+            return set_error(error, error_size, "Moonlight fast embedding failed");
+    for (int l = 0; l < c.layer_count; ++l) {
+        if (!m->layers[l].error.empty())
+            return set_error(error, error_size, "Moonlight fast %s failed at layer %d: %s",
+                             l < c.first_dense_layer_count ? "dense block" : "MoE", l,
+                             m->layers[l].error.c_str());
+        if (s->kv_lengths[l] != start)
+            return set_error(error, error_size,
+                             "Moonlight fast sparse attention failed at layer %d", l);
+    }
+    hipStream_t st = stream_of(s);
+    memcpy(s->host_ids, ids, (size_t)count * sizeof(int));
+    const size_t H = (size_t)c.hidden_size;
+    bool ok = hipEventRecord(s->ev_start, st) == hipSuccess &&
+              to_device(s, s->ids, s->host_ids, (size_t)count * sizeof(int)) &&
+              hipMemsetAsync(s->route_error, 0, sizeof(int), st) == hipSuccess &&
+              embed_rows(m->embed, s->ids, s->h, count, c.hidden_size, c.vocab_size, st) == kOk;
+    for (int l = 0; ok && l < c.layer_count; ++l) {
+        const LayerPlan &lp = m->layers[l];
+        ok = attention(s, l, s->h, count, start, s->h, lp.input_norm, s->h) == kOk;
+        if (ok && lp.dense) {
+            ok = swiglu_rows(s, lp.gate, lp.up, s->h, count, c.hidden_size,
+                             c.dense_intermediate_size, s->dense_hidden, lp.post_norm) == kOk &&
+                 gemv_rows(s, lp.down, s->dense_hidden, count, c.dense_intermediate_size,
+                           c.hidden_size, s->h, nullptr, s->h) == kOk;
+        } else if (ok) {
+            int *trace = s->route_trace + (size_t)l * s->options.max_batch * c.experts_per_token;
+            ok = route(s, l, s->h, count, lp.post_norm, trace) == kOk &&
+                 experts(s, l, s->h, count, lp.post_norm, s->h, s->h, nullptr) == kOk;
+        }
+        if (ok && layer_outputs)
+            ok = to_host(s, layer_outputs + (size_t)l * count * H, s->h, (size_t)count * H * 4);
+        if (ok) s->kv_lengths[l] = start + count;
+    }
+    if (ok)
+        ok = gemv_rows(s, m->lm_head, s->h + (size_t)(count - 1) * H, 1, c.hidden_size,
+                       c.vocab_size, s->logits, m->final_norm) == kOk &&
+             hipEventRecord(s->ev_stop, st) == hipSuccess &&
+             to_host(s, last_logits, s->logits, (size_t)c.vocab_size * sizeof(float)) &&
+             to_host(s, s->host_flag, s->route_error, sizeof(int));
+    if (!finish(s) || !ok) {
+        // the device state of a partial forward is unusable: invalidate the caches
+        for (int l = 0; l < c.layer_count; ++l)
+            if (s->kv_lengths[l] > start) s->kv_lengths[l] = start;
+        return set_error(error, error_size, "Moonlight forward failed on the device: %s",
+                         hipGetErrorString(hipGetLastError()));
+    }
+    if (*s->host_flag) return set_error(error, error_size, "Moonlight fast route table failed");
+    float ms = 0.0f;
+    if (hipEventElapsedTime(&ms, s->ev_start, s->ev_stop) == hipSuccess) s->last_device_ms = ms;
+    s->position = start + count;
+    s->last_forward_rows = count;
+    return 1;
+}
+
+}  // namespace
+
+extern "C" int moonlight_session_create(MoonlightSession **out, MoonlightModel *model,
+                                        const MoonlightOptions *options, char *error,
+                                        size_t error_size) {
+    if (!out || !model || !options)
+        return set_error(error, error_size, "model and session options are required");
+    *out = nullptr;
+    if (options->context_size <= 0 || options->max_batch <= 0 ||
+        options->max_batch > options->context_size)
+        return set_error(error, error_size, "invalid context or batch size");
+    const ModelConfig &c = model->cfg;
+    if (c.kv_lora_rank > 512 || c.qk_rope_dim > 256 || (c.qk_rope_dim & 1) ||
+        c.expert_count > 256 || c.experts_per_token > c.expert_count ||
+        // limits of the HIP kernels (mla.h, moe.hip)
+        c.head_count > kMlaMaxHeads || c.kv_lora_rank % 64 || c.qk_rope_dim > 64 ||
+        c.qk_nope_dim > 256 || c.qk_nope_dim <= 0 || c.value_dim <= 0 || c.experts_per_token > 16)
+        return set_error(error, error_size, "unsupported Moonlight MLA dimensions");
+    if (c.q_lora_rank)
+        return set_error(error, error_size, "unsupported Moonlight MLA dimensions");
+    MoonlightSession *s = new MoonlightSession();
+    s->model = model;
+    s->options = *options;
+    s->stats.resident_bytes = model->resident_bytes;
+    const size_t mb = (size_t)options->max_batch, ctx = (size_t)options->context_size;
+    const size_t H = (size_t)c.hidden_size, L = (size_t)c.layer_count, E = (size_t)c.expert_count;
+    const size_t K = (size_t)c.experts_per_token;
+    const size_t heads = (size_t)c.head_count;
+    s->max_splits = (int)((ctx + kMlaKeysPerSplit - 1) / kMlaKeysPerSplit);
+    const size_t splits = (size_t)s->max_splits;
+    const size_t sw = (size_t)c.moe_intermediate_size * c.shared_expert_count;
+    size_t lat_elems, rope_elems, lc_elems, logit_elems;
+    if (!mul_ok(L * ctx, (size_t)c.kv_lora_rank, &lat_elems) ||
+        !mul_ok(L * ctx, (size_t)c.qk_rope_dim, &rope_elems) ||
+        !mul_ok(mb * splits * kMlaMaxHeads, (size_t)c.kv_lora_rank, &lc_elems) ||
+        !mul_ok(mb, (size_t)c.vocab_size, &logit_elems)) {
+        delete s;
+        return set_error(error, error_size, "Moonlight session size overflow");
+    }
+    const bool ok =
+        session_alloc(s, &s->h, mb * H, error, error_size) &&
+        session_alloc(s, &s->tmp, mb * H, error, error_size) &&
+        session_alloc(s, &s->latent_kv, lat_elems, error, error_size) &&
+        session_alloc(s, &s->rope_kv, rope_elems, error, error_size) &&
+        session_alloc(s, &s->ids, mb, error, error_size) &&
+        session_alloc(s, &s->logits, logit_elems, error, error_size) &&
+        session_alloc(s, &s->query, mb * heads * (c.qk_nope_dim + c.qk_rope_dim), error,
+                      error_size) &&
+        session_alloc(s, &s->compressed, mb * (c.kv_lora_rank + c.qk_rope_dim), error,
+                      error_size) &&
+        session_alloc(s, &s->context, mb * heads * c.value_dim, error, error_size) &&
+        session_alloc(s, &s->query_rope, mb * heads * c.qk_rope_dim, error, error_size) &&
+        session_alloc(s, &s->query_absorbed, mb * heads * c.kv_lora_rank, error, error_size) &&
+        session_alloc(s, &s->part_max, mb * splits * kMlaMaxHeads, error, error_size) &&
+        session_alloc(s, &s->part_sum, mb * splits * kMlaMaxHeads, error, error_size) &&
+        session_alloc(s, &s->part_lc, lc_elems, error, error_size) &&
+        session_alloc(s, &s->router_logits, mb * E, error, error_size) &&
+        session_alloc(s, &s->route_ids, mb * K, error, error_size) &&
+        session_alloc(s, &s->route_weights, mb * K, error, error_size) &&
+        session_alloc(s, &s->n_unique, 1, error, error_size) &&
+        session_alloc(s, &s->unique, E, error, error_size) &&
+        session_alloc(s, &s->counts, E, error, error_size) &&
+        session_alloc(s, &s->offsets, E, error, error_size) &&
+        session_alloc(s, &s->list_rows, mb * K, error, error_size) &&
+        session_alloc(s, &s->list_slots, mb * K, error, error_size) &&
+        session_alloc(s, &s->list_pos, mb * K, error, error_size) &&
+        session_alloc(s, &s->route_error, 1, error, error_size) &&
+        session_alloc(s, &s->route_trace, L * mb * K, error, error_size) &&
+        session_alloc(s, &s->expert_hidden, mb * K * (size_t)c.moe_intermediate_size, error,
+                      error_size) &&
+        session_alloc(s, &s->expert_out, mb * K * H, error, error_size) &&
+        session_alloc(s, &s->shared_hidden, mb * (sw ? sw : 1), error, error_size) &&
+        session_alloc(s, &s->shared_out, mb * H, error, error_size) &&
+        session_alloc(s, &s->moe_routed, mb * H, error, error_size) &&
+        session_alloc(s, &s->dense_hidden,
+                      mb * (size_t)(c.dense_intermediate_size > 0 ? c.dense_intermediate_size : 1),
+                      error, error_size) &&
+        hipHostMalloc((void **)&s->host_ids, mb * sizeof(int), hipHostMallocDefault) ==
+            hipSuccess &&
+        hipHostMalloc((void **)&s->host_flag, sizeof(int), hipHostMallocDefault) == hipSuccess &&
+        hipEventCreate(&s->ev_start) == hipSuccess && hipEventCreate(&s->ev_stop) == hipSuccess;
+    if (!ok) {
+        free_session(s);
+        if (error && error_size && !error[0]) set_error(error, error_size, "session allocation failed");
+        return 0;
+    }
+    s->kv_lengths.assign(c.layer_count, 0);
+    *out = s;
+    return 1;
+}
+
+extern "C" void moonlight_session_destroy(MoonlightSession *session) { free_session(session); }
+
+extern "C" void moonlight_session_reset(MoonlightSession *s) {
+    if (!s) return;
+    s->position = 0;
+    s->last_forward_rows = 0;
+    std::fill(s->kv_lengths.begin(), s->kv_lengths.end(), 0);
+    s->stats.command_buffers = 0;
+    s->stats.prefill_tokens = 0;
+    s->stats.decode_tokens = 0;
+    s->stats.cpu_fallbacks = 0;
+    s->stats.prefill_ms = 0;
+    s->stats.decode_ms = 0;
+}
+
+extern "C" int moonlight_session_position(const MoonlightSession *s) {
+    return s ? s->position : 0;
+}
+
+extern "C" MoonlightStats moonlight_session_stats(const MoonlightSession *s) {
+    MoonlightStats r;
+    memset(&r, 0, sizeof(r));
+    return s ? s->stats : r;
+}
+
+extern "C" int moonlight_session_prefill(MoonlightSession *s, const int *ids, int count,
+                                         float *last_logits, char *error, size_t error_size) {
+    if (!s || !ids || !last_logits || count <= 0 || count > s->options.max_batch ||
+        count > s->options.context_size)
+        return set_error(error, error_size, "invalid Moonlight prefill request");
+    if (s->position != 0)
+        return set_error(error, error_size, "Moonlight prefill requires an empty session");
+    const double t0 = monotonic_seconds();
+    if (!forward(s, ids, count, 0, last_logits, nullptr, error, error_size)) return 0;
+    s->stats.prefill_tokens += (uint64_t)count;
+    s->stats.prefill_ms += (monotonic_seconds() - t0) * 1000.0;
+    return 1;
+}
+
+extern "C" int moonlight_session_append(MoonlightSession *s, const int *ids, int count,
+                                        float *last_logits, char *error, size_t error_size) {
+    if (!s || !ids || !last_logits || count <= 0 || count > s->options.max_batch ||
+        s->position <= 0 || s->position + count > s->options.context_size)
+        return set_error(error, error_size, "invalid Moonlight append request");
+    const double t0 = monotonic_seconds();
+    if (!forward(s, ids, count, s->position, last_logits, nullptr, error, error_size)) return 0;
+    s->stats.prefill_tokens += (uint64_t)count;
+    s->stats.prefill_ms += (monotonic_seconds() - t0) * 1000.0;
+    return 1;
+}
+
+extern "C" int moonlight_session_decode(MoonlightSession *s, int token, float *logits,
+                                        char *error, size_t error_size) {
+    if (!s || !logits || s->position < 0 || s->position >= s->options.context_size)
+        return set_error(error, error_size, "invalid Moonlight decode request");
+    const double t0 = monotonic_seconds();
+    if (!forward(s, &token, 1, s->position, logits, nullptr, error, error_size)) return 0;
+    s->stats.decode_tokens++;
+    s->stats.decode_ms += (monotonic_seconds() - t0) * 1000.0;
+    return 1;
+}
+
+extern "C" int moonlight_test_prefill_layers(MoonlightSession *s, const int *ids, int count,
+                                             float *layer_outputs, float *last_logits,
+                                             char *error, size_t error_size) {
+    if (!s || !ids || !layer_outputs || !last_logits || count <= 0 ||
+        count > s->options.max_batch || s->position != 0)
+        return set_error(error, error_size, "invalid Moonlight layer trace request");
+    const double t0 = monotonic_seconds();
+    if (!forward(s, ids, count, 0, last_logits, layer_outputs, error, error_size)) return 0;
+    s->stats.prefill_tokens += (uint64_t)count;
+    s->stats.prefill_ms += (monotonic_seconds() - t0) * 1000.0;
+    return 1;
+}
+
+// ---------------------------------------------------------------------------
+// test hooks (moonlight_metal.m:1188-1812, 2055-2070)
+// ---------------------------------------------------------------------------
+
+extern "C" int moonlight_test_embed(MoonlightSession *s, const int *ids, int count, float *output) {
+    if (!s || !ids || !output || count <= 0 || count > s->options.max_batch) return 0;
+    const ModelConfig &c = s->model->cfg;
+    if (!s->model->embed) return 0;
+    for (int i = 0; i < count; ++i)
+        if (ids[i] < 0 || ids[i] >= c.vocab_size) return 0;
+    memcpy(s->host_ids, ids, (size_t)count * sizeof(int));
+    const size_t bytes = (size_t)count * c.hidden_size * sizeof(float);
+    bool ok = to_device(s, s->ids, s->host_ids, (size_t)count * sizeof(int)) &&
+              embed_rows(s->model->embed, s->ids, s->h, count, c.hidden_size, c.vocab_size,
+                         stream_of(s)) == kOk &&
+              to_host(s, output, s->h, bytes);
+    return finish(s) && ok;
+}
+
+extern "C" int moonlight_test_rmsnorm(MoonlightSession *s, const float *input,
+                                      const char *weight_name, int rows, int width,
+                                      float *output) {
+    if (!s || !input || !weight_name || !output || rows <= 0 || width <= 0 ||
+        rows > s->options.max_batch)
+        return 0;
+    const float *w = vector_f32(s->model, weight_name, width);
+    if (!w) return 0;
+    const size_t bytes = (size_t)rows * width * sizeof(float);
+    if (bytes > (size_t)s->options.max_batch * s->model->cfg.hidden_size * sizeof(float))
+        return 0;
+    bool ok = to_device(s, s->tmp, input, bytes) &&
+              rmsnorm_rows(s->tmp, w, s->h, rows, width, s->model->cfg.rms_norm_epsilon, width,
+                           width, stream_of(s)) == kOk &&
+              to_host(s, output, s->h, bytes);
+    return finish(s) && ok;
+}
+
+extern "C" int moonlight_test_matmul(MoonlightSession *s, const char *weight_name,
+                                     const float *input, int rows, int input_width,
+                                     int output_width, float *output) {
+    if (!s || !weight_name || !input || !output || rows <= 0 || input_width <= 0 ||
+        output_width <= 0 || rows > s->options.max_batch)
+        return 0;
+    Matrix m;
+    if (!resolve(s->model, weight_name, input_width, output_width, &m)) return 0;
+    const ModelConfig &c = s->model->cfg;
+    const size_t in_bytes = (size_t)rows * input_width * sizeof(float);
+    const size_t out_bytes = (size_t)rows * output_width * sizeof(float);
+    if (in_bytes > (size_t)s->options.max_batch * c.hidden_size * sizeof(float) ||
+        out_bytes > (size_t)s->options.max_batch * c.vocab_size * sizeof(float))
+        return 0;
+    bool ok = to_device(s, s->tmp, input, in_bytes) &&
+              gemv_rows(s, m, s->tmp, rows, input_width, output_width, s->logits) == kOk &&
+              to_host(s, output, s->logits, out_bytes);
+    return finish(s) && ok;
+}
+
+extern "C" int moonlight_test_attention(MoonlightSession *s, int layer, const float *input,
+                                        int rows, int position, float *output) {
+    if (!s || !input || !output || rows <= 0 || position < 0 || rows > s->options.max_batch)
+        return 0;
+    const ModelConfig &c = s->model->cfg;
+    if (layer < 0 || layer >= c.layer_count || position != s->kv_lengths[layer] ||
+        position + rows > s->options.context_size || c.q_lora_rank)
+        return 0;
+    if (!s->model->layers[layer].error.empty()) return 0;
+    const size_t bytes = (size_t)rows * c.hidden_size * sizeof(float);
+    bool ok = to_device(s, s->tmp, input, bytes) &&
+              attention(s, layer, s->tmp, rows, position, s->h, nullptr, nullptr) == kOk &&
+              to_host(s, output, s->h, bytes);
+    if (!finish(s) || !ok) return 0;
+    s->kv_lengths[layer] = position + rows;
+    if (s->position < position + rows) s->position = position + rows;
+    return 1;
+}
+
+extern "C" int moonlight_test_kv_length(const MoonlightSession *s, int layer) {
+    if (!s || layer < 0 || layer >= s->model->cfg.layer_count) return 0;
+    return s->kv_lengths[layer];
+}
+
+extern "C" int moonlight_test_copy_kv(const MoonlightSession *s, int layer, float *latent,
+                                      float *rope, int capacity) {
+    if (!s || !latent || !rope || capacity < 0) return 0;
+    const ModelConfig &c = s->model->cfg;
+    if (layer < 0 || layer >= c.layer_count || capacity < s->kv_lengths[layer]) return 0;
+    const size_t n = (size_t)s->kv_lengths[layer];
+    const size_t ctx = (size_t)s->options.context_size;
+    hipStream_t st = context()->stream;
+    bool ok = hipMemcpyAsync(latent, s->latent_kv + (size_t)layer * ctx * c.kv_lora_rank,
+                             n * c.kv_lora_rank * sizeof(float), hipMemcpyDeviceToHost,
+                             st) == hipSuccess &&
+              hipMemcpyAsync(rope, s->rope_kv + (size_t)layer * ctx * c.qk_rope_dim,
+                             n * c.qk_rope_dim * sizeof(float), hipMemcpyDeviceToHost,
+                             st) == hipSuccess &&
+              hipStreamSynchronize(st) == hipSuccess;
+    return ok ? 1 : 0;
+}
+
+extern "C" int moonlight_test_moe(MoonlightSession *s, int layer, const float *input, int rows,
+                                  int *route_ids, float *route_weights, float *router_scores,
+                                  float *routed_output, float *shared_output, float *output) {
+    if (!s || !input || !output || rows <= 0 || rows > s->options.max_batch) return 0;
+    const ModelConfig &c = s->model->cfg;
+    if (layer < c.first_dense_layer_count || layer >= c.layer_count || c.expert_count <= 0 ||
+        c.experts_per_token <= 0 || c.shared_expert_count <= 0)
+        return 0;
+    if (!s->model->layers[layer].error.empty()) return 0;
+    const size_t hidden_bytes = (size_t)rows * c.hidden_size * sizeof(float);
+    const size_t route_bytes = (size_t)rows * c.experts_per_token * sizeof(float);
+    const size_t score_bytes = (size_t)rows * c.expert_count * sizeof(float);
+    hipStream_t st = stream_of(s);
+    // submission 1: router + top-k (+ device route tables)
+    bool ok = to_device(s, s->tmp, input, hidden_bytes) &&
+              hipMemsetAsync(s->route_error, 0, sizeof(int), st) == hipSuccess &&
+              route(s, layer, s->tmp, rows, nullptr, nullptr) == kOk &&
+              to_host(s, s->host_flag, s->route_error, sizeof(int));
+    if (!finish(s) || !ok || *s->host_flag) return 0;
+    // submission 2: experts, shared expert, routed + shared (no residual)
+    ok = experts(s, layer, s->tmp, rows, nullptr, nullptr, s->h, s->moe_routed) == kOk;
+    const float *routed_dev = s->moe_routed;
+    if (ok && route_ids) ok = to_host(s, route_ids, s->route_ids, route_bytes);
+    if (ok && route_weights) ok = to_host(s, route_weights, s->route_weights, route_bytes);
+    if (ok && router_scores) ok = to_host(s, router_scores, s->router_logits, score_bytes);
+    if (ok && routed_output) ok = to_host(s, routed_output, routed_dev, hidden_bytes);
+    if (ok && shared_output) ok = to_host(s, shared_output, s->shared_out, hidden_bytes);
+    if (ok) ok = to_host(s, output, s->h, hidden_bytes);
+    return finish(s) && ok;
+}
+
+extern "C" int moonlight_test_dense_mlp(MoonlightSession *s, int layer, const float *input,
+                                        int rows, float *output) {
+    if (!s || !input || !output || rows <= 0 || rows > s->options.max_batch) return 0;
+    const ModelConfig &c = s->model->cfg;
+    if (layer < 0 || layer >= c.layer_count || !s->model->layers[layer].dense ||
+        !s->model->layers[layer].error.empty())
+        return 0;
+    const LayerPlan &lp = s->model->layers[layer];
+    const size_t bytes = (size_t)rows * c.hidden_size * sizeof(float);
+    bool ok = to_device(s, s->tmp, input, bytes) &&
+              swiglu_rows(s, lp.gate, lp.up, s->tmp, rows, c.hidden_size,
+                          c.dense_intermediate_size, s->dense_hidden, nullptr) == kOk &&
+              gemv_rows(s, lp.down, s->dense_hidden, rows, c.dense_intermediate_size,
+                        c.hidden_size, s->h) == kOk &&
+              to_host(s, output, s->h, bytes);
+    return finish(s) && ok;
+}
+
+extern "C" int moonlight_test_copy_routes(const MoonlightSession *s, int layer, int *route_ids,
+                                          int capacity) {
+    if (!s || !route_ids || capacity < s->last_forward_rows) return 0;
+    const ModelConfig &c = s->model->cfg;
+    if (layer < c.first_dense_layer_count || layer >= c.layer_count) return 0;
+    hipStream_t st = context()->stream;
+    const size_t n = (size_t)s->last_forward_rows * c.experts_per_token;
+    const int *src = s->route_trace + (size_t)layer * s->options.max_batch * c.experts_per_token;
+    return hipMemcpyAsync(route_ids, src, n * sizeof(int), hipMemcpyDeviceToHost, st) ==
+                   hipSuccess &&
+                   hipStreamSynchronize(st) == hipSuccess
+               ? 1
+               : 0;
+}
+
+// ---------------------------------------------------------------------------
+// extensions
+// ---------------------------------------------------------------------------
+
+extern "C" int moonlight_session_fill_kv(MoonlightSession *s, int layer, int length,
+                                         uint64_t seed) {
+    if (!s || length < 0 || length > s->options.context_size) return 0;
+    const ModelConfig &c = s->model->cfg;
+    if (layer >= c.layer_count) return 0;
+    const size_t ctx = (size_t)s->options.context_size;
+    hipStream_t st = stream_of(s);
+    const int first = layer < 0 ? 0 : layer, last = layer < 0 ? c.layer_count : layer + 1;
+    for (int l = first; l < last; ++l) {
+        const uint64_t sd = seed + (uint64_t)l * 2;
+        if (length > 0 &&
+            (fill_normal(s->latent_kv + (size_t)l * ctx * c.kv_lora_rank,
+                         (int64_t)length * c.kv_lora_rank, sd, 0.0f, 1.0f, 0, st) != kOk ||
+             fill_normal(s->rope_kv + (size_t)l * ctx * c.qk_rope_dim,
+                         (int64_t)length * c.qk_rope_dim, sd + 1, 0.0f, 1.0f, 0, st) != kOk))
+            return 0;
+        s->kv_lengths[l] = length;
+    }
+    if (layer < 0) s->position = length;
+    return hipStreamSynchronize(st) == hipSuccess ? 1 : 0;
+}
+
+extern "C" int moonlight_session_device_time(MoonlightSession *s, double *ms) {
+    if (!s || !ms) return 0;
+    *ms = s->last_device_ms;
+    return 1;
+}

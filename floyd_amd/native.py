@@ -44,6 +44,8 @@ SIGNATURES = {
                                  _c.c_int, _c.POINTER(_c.c_double)]),
     "mlk_time_copy": (_c.c_int, [_c.POINTER(_vp), _c.POINTER(_vp), _c.c_int, _c.c_size_t,
                                  _c.c_int, _c.c_int, _c.POINTER(_c.c_double)]),
+    "mlk_time_read": (_c.c_int, [_c.POINTER(_vp), _c.c_int, _c.c_size_t, _c.c_int, _vp,
+                                 _c.c_int, _c.c_int, _c.POINTER(_c.c_double)]),
     "mlk_quantize": (_c.c_int, [_c.c_int, _vp, _c.c_int, _c.c_int, _vp, _vp]),
     "mlk_fill_normal": (_c.c_int, [_vp, _c.c_int64, _c.c_uint64, _c.c_float, _c.c_float,
                                    _c.c_int]),
@@ -184,6 +186,15 @@ def time_copy(src_list, dst_list, nbytes, warmup, iters):
     out = _c.c_double()
     check(load().mlk_time_copy(sa, da, n, nbytes, warmup, iters, _c.byref(out)),
           "mlk_time_copy")
+    return out.value
+
+
+def time_read(src_list, nbytes, blocks, scratch, warmup, iters):
+    n = len(src_list)
+    sa = (_vp * n)(*[_ptr(b) for b in src_list])
+    out = _c.c_double()
+    check(load().mlk_time_read(sa, n, nbytes, blocks, _ptr(scratch), warmup, iters,
+                               _c.byref(out)), "mlk_time_read")
     return out.value
 
 

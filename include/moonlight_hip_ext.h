@@ -1,0 +1,80 @@
+/*
+ * moonlight_hip_ext.h -- additions to the Moonlight session API that have no
+ * counterpart in floyd's moonlight_metal.h.  They exist for callers that
+ * build models in HBM without a container on disk (benchmarks, synthetic
+ * parity runs) and for inspecting device state.
+ */
+#ifndef MOONLIGHT_HIP_EXT_H
+#define MOONLIGHT_HIP_EXT_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include "moonlight_hip.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Shape and packing of a synthetic Moonlight container generated directly in
+ * HBM: every tensor a converted container holds (tools/convert_moonlight.py),
+ * same names, dtypes and byte counts.  Matrices are drawn ~N(0, weight_std),
+ * rounded to bf16 and packed per row at `expert_bits` (routed experts) or
+ * `dense_bits` (attention, dense and shared FFNs), 8 or 4; embed, lm_head and
+ * the router stay f32; norm weights are 1; e_score_correction_bias is
+ * linspace(-0.1, 0.1, experts). */
+typedef struct {
+    int hidden_size, layer_count, head_count, expert_count, experts_per_token;
+    int dense_intermediate_size, moe_intermediate_size, first_dense_layer_count;
+    int kv_lora_rank, qk_nope_dim, qk_rope_dim, value_dim;
+    int shared_expert_count, normalize_topk, vocab_size;
+    float rms_norm_epsilon, rope_theta, routed_scale;
+    int expert_bits, dense_bits;
+    float weight_std;
+    uint64_t seed;
+} MoonlightSyntheticConfig;
+
+/* Parses config.json and every safetensors header of a container directory
+ * without touching the GPU (moonlight_model.c:41-190 semantics): fills
+ * ints16 / floats3 in the field order of floyd's MoonlightConfig
+ * (moonlight_model.h:17-37) and returns the tensor count, or -1 with a
+ * message in `error`. */
+int moonlight_container_probe(const char *path, int *ints16, float *floats3,
+                              char *error, size_t error_size);
+/* dtype code, element and byte count of one tensor of a container directory
+ * (no GPU); 1 when found, 0 otherwise. */
+int moonlight_container_tensor(const char *path, const char *name, int *dtype,
+                               int64_t *numel, int64_t *nbytes);
+
+/* Moonlight-16B-A3B dimensions (27 layers, hidden 2048, 16 heads, MLA 512+64,
+ * 64 experts top-6 + 2 shared, vocab 163840), q8 packing, seed 1. */
+MoonlightSyntheticConfig moonlight_synthetic_moonlight_config(void);
+
+int moonlight_model_create_synthetic(MoonlightModel **out,
+                                     const MoonlightSyntheticConfig *config,
+                                     char *error, size_t error_size);
+
+/* Copies tensor `name` of the model (its raw bytes as stored in HBM) into
+ * host memory; returns the byte count, 0 if absent or capacity too small. */
+size_t moonlight_model_read_tensor(const MoonlightModel *model,
+                                   const char *name, void *dst,
+                                   size_t capacity);
+/* dtype code (0 bf16, 1 f16, 2 f32, 3 u8) and sizes of a tensor; 0 if absent. */
+int moonlight_model_tensor_info(const MoonlightModel *model, const char *name,
+                                int *dtype, int64_t *numel, int64_t *nbytes);
+
+/* Overwrites the latent / rope cache of `layer` with `length` rows drawn
+ * ~N(0, 1) from `seed` on the device, and sets that layer's kv length; when
+ * `layer` < 0 every layer is filled (seed + layer) and the session position
+ * becomes `length`.  Used to measure decode at a given context. */
+int moonlight_session_fill_kv(MoonlightSession *session, int layer,
+                              int length, uint64_t seed);
+
+/* Device time (milliseconds, HIP events around the launches) of the last
+ * prefill / append / decode of the session. */
+int moonlight_session_device_time(MoonlightSession *session, double *ms);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -69,6 +69,12 @@ int mlk_time_gemv(int fmt, const void *const *w_copies,
 int mlk_time_copy(void *const *src, void *const *dst, int n_buffers,
                   size_t bytes, int warmup, int iters, double *avg_us);
 
+/* Same for a read-only stream of `bytes` split over `blocks` workgroups
+ * (scratch: blocks * 4 words of device memory): the ceiling a GEMV reading
+ * that many bytes can reach, launch ramp and tail included. */
+int mlk_time_read(void *const *src, int n_buffers, size_t bytes, int blocks,
+                  unsigned *scratch, int warmup, int iters, double *avg_us);
+
 /* ---- packing / synthetic weights ---------------------------------------- */
 int mlk_quantize(int bits, const float *w, int rows, int cols, uint8_t *q,
                  float *s);

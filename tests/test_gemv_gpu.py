@@ -56,7 +56,9 @@ def test_gemv_matches_oracle(device, fmt, out_width, in_width, rows):
 
 @pytest.mark.parametrize("fmt,out_width,in_width,rows", [
     (1, 3072, 2048, 1), (2, 3648, 2048, 2), (0, 64, 2048, 3), (1, 192, 256, 4),
-    (0, 163840 // 16, 2048, 1)])
+    (0, 163840 // 16, 2048, 1),
+    # narrow rows with a partially filled last wave (lane groups past O)
+    (1, 80, 256, 2), (2, 80, 256, 1), (1, 40, 128, 3), (2, 72, 256, 2), (1, 20, 64, 1)])
 def test_gemv_rmsnorm_prologue(device, fmt, out_width, in_width, rows):
     print(f"[gpu] gemv+norm fmt={fmt} O={out_width} I={in_width} rows={rows}", flush=True)
     q, s = make_weights(fmt, out_width, in_width, seed=5 + out_width)
@@ -140,8 +142,7 @@ def test_fm_backend_reference_kernel_gate(device):
     max relative error vs f64 <= 1e-3 for cache=0 (twice) and cache=1 (twice)."""
     lib = native.load()
     assert lib.fm_init() == 1
-    assert b"MI355" in lib.fm_device_name() or b"gfx950" in lib.fm_device_name() or \
-        lib.fm_device_name()
+    assert b"gfx950" in lib.fm_device_name()
     rng = np.random.default_rng(42)
     O_, I_, S_ = 128, 257, 4
     w8 = rng.integers(-127, 128, O_ * I_).astype(np.int8)
