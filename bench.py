@@ -89,6 +89,71 @@ class GemvCase:
             b.close()
 
 
+def moe_layer_bytes(unique, rows):
+    """Algorithmic bytes of one q8 MoE decode layer:
+    U routed experts x (gate + up + down + scales) + fused shared expert +
+    f32 router and bias + the token rows in and out."""
+    expert = 3 * 1408 * 2048 + 2 * 1408 * 4 + 2048 * 4
+    shared = 3 * 2816 * 2048 + 2 * 2816 * 4 + 2048 * 4
+    router = 64 * 2048 * 4 + 64 * 4
+    return unique * expert + shared + router + rows * 2048 * 4 * 2
+
+
+# Algorithmic bytes of one full q8 decode step (BASELINE.md section 3).
+DECODE_STEP_BYTES = {4096: 3856274688, 16384: 4620686592}
+
+
+def moonlight_extras(native, extra, decode_tokens):
+    """BASELINE configs 2 and 4 on a synthetic Moonlight-16B-A3B q8 model built
+    in HBM: one MoE layer at T = 1, 8, 64 and a full decode step at ctx 4096
+    and 16384."""
+    from floyd_amd import session as S
+    t0 = time.perf_counter()
+    model = S.Model.synthetic()
+    extra["moonlight_model_build_s"] = round(time.perf_counter() - t0, 2)
+    print(f"[bench] synthetic Moonlight q8 model in {extra['moonlight_model_build_s']} s",
+          file=sys.stderr, flush=True)
+    sess = S.Session(model, 128, 64)
+    for rows in (1, 8, 64):
+        us, uniq = sess.time_moe(1, rows, seed=rows, warmup=5, iters=50)
+        nbytes = moe_layer_bytes(uniq, rows)
+        gbs = nbytes / (us * 1e-6) / 1e9
+        extra[f"cfg2_moe_decode_q8_T{rows}"] = {
+            "us": round(us, 2), "unique_experts": uniq, "bytes": nbytes,
+            "GB/s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)}
+        print(f"[bench] MoE layer T={rows}: {us:.1f} us, U={uniq}, {gbs:.0f} GB/s",
+              file=sys.stderr, flush=True)
+    sess.close()
+    for ctx in (4096, 16384):
+        sess = S.Session(model, ctx + decode_tokens + 8, 1)
+        sess.fill_kv(ctx, seed=ctx)
+        token = 1
+        for _ in range(3):
+            logits = sess.decode(token)
+            token = int(logits.argmax())
+        dev, wall = [], []
+        for _ in range(decode_tokens):
+            t1 = time.perf_counter()
+            logits = sess.decode(token)
+            wall.append(time.perf_counter() - t1)
+            dev.append(sess.device_time_ms())
+            token = int(logits.argmax())
+        dev_ms = sorted(dev)[len(dev) // 2]
+        wall_ms = sorted(wall)[len(wall) // 2] * 1e3
+        nbytes = DECODE_STEP_BYTES[ctx]
+        extra[f"cfg4_decode_q8_ctx{ctx}"] = {
+            "tok_per_s": round(1e3 / wall_ms, 2), "ms_per_token_wall": round(wall_ms, 3),
+            "ms_per_token_device": round(dev_ms, 3), "bytes": nbytes,
+            "GB/s_device": round(nbytes / (dev_ms * 1e-3) / 1e9, 1),
+            "frac_device": round(nbytes / (dev_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "tokens": decode_tokens}
+        print(f"[bench] decode ctx {ctx}: {wall_ms:.3f} ms/token wall "
+              f"({1e3 / wall_ms:.1f} tok/s), device {dev_ms:.3f} ms",
+              file=sys.stderr, flush=True)
+        sess.close()
+    model.close()
+
+
 def cpu_baseline(case, budget_s=10.0):
     """The oracle's GEMV (restatement of the reference arithmetic) timed on the
     host cores on the same inputs, with the same parity check."""
@@ -125,6 +190,9 @@ def main():
     parser.add_argument("--warmup", type=int, default=10)
     parser.add_argument("--no-cpu", action="store_true")
     parser.add_argument("--cpu-budget", type=float, default=10.0)
+    parser.add_argument("--no-moonlight", action="store_true",
+                        help="skip the synthetic Moonlight MoE / decode measurements")
+    parser.add_argument("--decode-tokens", type=int, default=20)
     args = parser.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: the hot path is single-device "
@@ -166,6 +234,9 @@ def main():
                             "GB/s": round(2 * nbytes / (copy_us * 1e-6) / 1e9, 1)}
     for b in src + dst:
         b.close()
+
+    if not args.no_moonlight:
+        moonlight_extras(native, extra, args.decode_tokens)
 
     cpu = None
     if not args.no_cpu:

@@ -1318,6 +1318,38 @@ extern "C" int moonlight_session_fill_kv(MoonlightSession *s, int layer, int len
     return hipStreamSynchronize(st) == hipSuccess ? 1 : 0;
 }
 
+extern "C" int moonlight_session_time_moe(MoonlightSession *s, int layer, int rows, uint64_t seed,
+                                          int warmup, int iters, double *avg_us,
+                                          int *unique_experts) {
+    if (!s || !avg_us || rows <= 0 || rows > s->options.max_batch || iters <= 0 || warmup < 0)
+        return 0;
+    const ModelConfig &c = s->model->cfg;
+    if (layer < c.first_dense_layer_count || layer >= c.layer_count ||
+        !s->model->layers[layer].error.empty())
+        return 0;
+    const LayerPlan &lp = s->model->layers[layer];
+    hipStream_t st = stream_of(s);
+    if (fill_normal(s->tmp, (int64_t)rows * c.hidden_size, seed, 0.0f, 1.0f, 0, st) != kOk)
+        return 0;
+    auto pass = [&]() {
+        return route(s, layer, s->tmp, rows, lp.post_norm, nullptr) == kOk &&
+               experts(s, layer, s->tmp, rows, lp.post_norm, s->tmp, s->h, nullptr) == kOk;
+    };
+    bool ok = hipMemsetAsync(s->route_error, 0, sizeof(int), st) == hipSuccess;
+    for (int i = 0; ok && i < warmup; ++i) ok = pass();
+    ok = ok && hipEventRecord(s->ev_start, st) == hipSuccess;
+    for (int i = 0; ok && i < iters; ++i) ok = pass();
+    ok = ok && hipEventRecord(s->ev_stop, st) == hipSuccess &&
+         to_host(s, s->host_flag, s->route_error, sizeof(int)) &&
+         to_host(s, s->host_ids, s->n_unique, sizeof(int));
+    if (!finish(s) || !ok || *s->host_flag) return 0;
+    float ms = 0.0f;
+    if (hipEventElapsedTime(&ms, s->ev_start, s->ev_stop) != hipSuccess) return 0;
+    *avg_us = (double)ms * 1000.0 / iters;
+    if (unique_experts) *unique_experts = s->host_ids[0];
+    return 1;
+}
+
 extern "C" int moonlight_session_device_time(MoonlightSession *s, double *ms) {
     if (!s || !ms) return 0;
     *ms = s->last_device_ms;

@@ -85,6 +85,9 @@ SIGNATURES = {
     "moonlight_model_tensor_info": (C.c_int, [_vp, _cp, _vp, _vp, _vp]),
     "moonlight_session_fill_kv": (C.c_int, [_vp, C.c_int, C.c_int, C.c_uint64]),
     "moonlight_session_device_time": (C.c_int, [_vp, C.POINTER(C.c_double)]),
+    "moonlight_session_time_moe": (C.c_int, [_vp, C.c_int, C.c_int, C.c_uint64, C.c_int,
+                                             C.c_int, C.POINTER(C.c_double),
+                                             C.POINTER(C.c_int)]),
 }
 
 _bound = False
@@ -252,6 +255,13 @@ class Session:
     def fill_kv(self, length, seed, layer=-1):
         if not lib().moonlight_session_fill_kv(self.handle, layer, length, seed):
             raise SessionError("fill_kv failed")
+
+    def time_moe(self, layer, rows, seed=7, warmup=5, iters=50):
+        us, uniq = C.c_double(), C.c_int()
+        if not lib().moonlight_session_time_moe(self.handle, layer, rows, seed, warmup, iters,
+                                                C.byref(us), C.byref(uniq)):
+            raise SessionError("time_moe failed")
+        return us.value, uniq.value
 
     # ---- test hooks (0 = failure, no message) ----
     def test_embed(self, ids):

@@ -70,6 +70,16 @@ int moonlight_model_tensor_info(const MoonlightModel *model, const char *name,
 int moonlight_session_fill_kv(MoonlightSession *session, int layer,
                               int length, uint64_t seed);
 
+/* Times `iters` back-to-back device passes of one MoE layer exactly as a
+ * forward runs it (router GEMV with the fused post-attention RMSNorm, top-k
+ * and route tables, grouped gate/up + down expert launches, shared expert,
+ * combine into the residual) on `rows` token rows drawn ~N(0, 1) from `seed`
+ * and resident in HBM.  avg_us: HIP-event time per pass; unique_experts: the
+ * number of distinct routed experts of the pass (for the byte count). */
+int moonlight_session_time_moe(MoonlightSession *session, int layer, int rows,
+                               uint64_t seed, int warmup, int iters,
+                               double *avg_us, int *unique_experts);
+
 /* Device time (milliseconds, HIP events around the launches) of the last
  * prefill / append / decode of the session. */
 int moonlight_session_device_time(MoonlightSession *session, double *ms);
