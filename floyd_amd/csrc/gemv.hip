@@ -129,7 +129,9 @@ GemvPlan plan_gemv(int fmt, int O, int I, int rows, bool dual) {
     plan.kt = fmt == kF32 ? (nc > 64 ? 2 : 1) : 1;
     const int tiles = (nc + 64 * plan.kt - 1) / (64 * plan.kt);
     const long out_rows_total = (long)O * (dual ? 2 : 1);
-    plan.ks = (tiles >= 4 || (tiles >= 2 && out_rows_total <= 4096)) ? 4 : 1;
+    // k split only pays when every wave of the workgroup gets a k-tile, or for
+    // short plain matrices (few rows: more waves); not for the gate/up pairs
+    plan.ks = (tiles >= 4 || (tiles >= 2 && out_rows_total <= 4096 && !dual)) ? 4 : 1;
     const int rmin = dual ? 2 : 1;
     int chosen = 0;
     for (int r = 8; r >= rmin; r >>= 1) {

@@ -6,7 +6,7 @@
 namespace mlh {
 
 constexpr int kMlaMaxHeads = 16;        // Moonlight: 16 heads
-constexpr int kMlaKeysPerSplit = 64;    // keys per workgroup in mla_attend
+constexpr int kMlaKeysPerSplit = 32;    // keys per workgroup in mla_attend
 constexpr int kMlaMaxLatent = 512;      // kv_lora_rank limit (moonlight_metal.m:1041)
 constexpr int kMlaMaxSplitsInLds = 1024;
 
@@ -24,8 +24,10 @@ struct MlaParams {
     int rows = 0, position = 0, heads = 0;
     int nope = 0, rope = 0, vdim = 0, latent = 0;
     float eps = 1e-5f, scale = 1.0f;
-    const float *query = nullptr;       // [rows, heads, nope + rope] (q_proj output)
-    const float *compressed = nullptr;  // [rows, latent + rope] (kv_a output)
+    const float *query = nullptr;       // [rows][heads * (nope + rope)] (q_proj output)
+    long query_stride = 0;              // floats between token rows of query
+    const float *compressed = nullptr;  // [rows][latent + rope] (kv_a output)
+    long compressed_stride = 0;         // floats between token rows of compressed
     const float *kv_norm = nullptr;     // [latent] kv_a_layernorm weight
     const float *inv_freq = nullptr;    // [rope / 2] theta^(-2p/rope), host-computed
     MatrixRef kv_b;                     // [heads * (nope + vdim), latent]
@@ -37,11 +39,12 @@ struct MlaParams {
     float *part_max = nullptr;          // [rows, max_splits, kMlaMaxHeads]
     float *part_sum = nullptr;          // [rows, max_splits, kMlaMaxHeads]
     float *part_lc = nullptr;           // [rows, max_splits, kMlaMaxHeads, latent]
+    float *latent_context = nullptr;    // scratch [rows, heads, latent] merged lc
     float *context = nullptr;           // out [rows, heads, vdim]
 };
 
-// Cache append + query RoPE + absorb, split-K attention, merge + value
-// projection (three launches).  o_proj is a plain GEMV on `context`.
+// Cache append + query RoPE + absorb, split-K attention, merge, value
+// projection (four launches).  o_proj is a plain GEMV on `context`.
 int mla_attention_core(const MlaParams &p, hipStream_t stream);
 
 }  // namespace mlh

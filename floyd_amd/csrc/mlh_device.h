@@ -46,27 +46,36 @@ __device__ __forceinline__ float group_sum(float v) {
 // lanes.  After the call v[0] of a lane holds the group total of value index
 // butterfly_index<NV, G>(lane); every lane of the group ends up holding one
 // total (NV <= G), lanes whose low bits are zero are the designated writers.
+// Step s exchanges half of the live values across lane offset G >> (s + 1);
+// the recursion keeps every array index a compile-time constant (a runtime
+// index would turn each access into a compare/select chain over the array).
+template <int NV, int G, int STEP>
+struct ButterflyStep {
+    static __device__ __forceinline__ void run(float (&v)[NV], int lane) {
+        constexpr int N = NV >> STEP;
+        if constexpr (N > 1) {
+            constexpr int HALF = N / 2;
+            constexpr int O = G >> (STEP + 1);
+            const bool upper = (lane & O) != 0;
+#pragma unroll
+            for (int i = 0; i < HALF; ++i) {
+                const float send = upper ? v[i] : v[i + HALF];
+                const float keep = upper ? v[i + HALF] : v[i];
+                v[i] = keep + __shfl_xor(send, O, kWave);
+            }
+            ButterflyStep<NV, G, STEP + 1>::run(v, lane);
+        } else {
+#pragma unroll
+            for (int o = G >> (STEP + 1); o >= 1; o >>= 1) v[0] += __shfl_xor(v[0], o, kWave);
+        }
+    }
+};
+
 template <int NV, int G>
 __device__ __forceinline__ void butterfly_reduce(float (&v)[NV], int lane) {
     static_assert(NV <= G, "more values than lanes in the group");
-    int n = NV;
-    int o = G / 2;
-#pragma unroll
-    for (int step = 0; (1 << step) < NV; ++step) {
-        const bool upper = (lane & o) != 0;
-        const int half = n / 2;
-#pragma unroll
-        for (int i = 0; i < NV / 2; ++i) {
-            if (i < half) {
-                float send = upper ? v[i] : v[i + half];
-                float keep = upper ? v[i + half] : v[i];
-                v[i] = keep + __shfl_xor(send, o, kWave);
-            }
-        }
-        n = half;
-        o >>= 1;
-    }
-    for (; o >= 1; o >>= 1) v[0] += __shfl_xor(v[0], o, kWave);
+    static_assert((NV & (NV - 1)) == 0, "NV must be a power of two");
+    ButterflyStep<NV, G, 0>::run(v, lane);
 }
 
 // Value index a lane holds after butterfly_reduce<NV, G>.

@@ -57,8 +57,10 @@ int expert_ffn(const ExpertFfnParams &f, hipStream_t stream);
 
 int rmsnorm_rows(const float *x, const float *w, float *y, int rows, int width, float eps,
                  long in_stride, long out_stride, hipStream_t stream);
+// Embedding gather; also zeroes *clear_flag (the route error flag of the
+// forward) when it is non-null.
 int embed_rows(const float *table, const int *ids, float *out, int rows, int width, int vocab,
-               hipStream_t stream);
+               int *clear_flag, hipStream_t stream);
 int add_vectors(const float *a, const float *b, float *out, long n, hipStream_t stream);
 
 // Planning helpers shared with gemv.hip.

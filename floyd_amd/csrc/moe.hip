@@ -29,17 +29,25 @@ __device__ __forceinline__ float sigmoid_exact(float logit) {
 
 constexpr int kMaxExperts = 256;
 constexpr int kMaxTopK = 16;
+constexpr int kRouteLdsIds = 4096;
+constexpr int kRouteMaxPositions = 16384;  // rows * top_k per routing call
 
 // One workgroup: top-k for every token row, then the route tables.
 __global__ __launch_bounds__(256) void route_kernel(RouteParams p) {
     __shared__ int first_pos[kMaxExperts];
     __shared__ int counts[kMaxExperts];
     __shared__ int offsets[kMaxExperts];
+    __shared__ int lds_ids[kRouteLdsIds];  // selected ids when rows*top_k fits
+    __shared__ unsigned long long first_mask[kRouteMaxPositions / 64];
+    __shared__ int word_prefix[kRouteMaxPositions / 64];
+    __shared__ int rank_of[kMaxExperts], count_by_rank[kMaxExperts], offset_by_rank[kMaxExperts];
+    __shared__ int unique_total;
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
     const int E = p.experts, K = p.top_k, M = p.rows;
     const int n_pos = M * K;
+    const bool ids_in_lds = n_pos <= kRouteLdsIds;
 
     // ---- top-k selection: one wave per token row, experts spread over lanes
     for (int r = wave; r < M; r += 4) {
@@ -111,6 +119,7 @@ __global__ __launch_bounds__(256) void route_kernel(RouteParams p) {
                     w = wk[k];
                 }
             p.ids[(long)r * K + lane] = id;
+            if (ids_in_lds) lds_ids[r * K + lane] = id;
             p.weights[(long)r * K + lane] = w / wsum * p.routed_scale;
             if (p.trace) p.trace[(long)r * K + lane] = id;
         }
@@ -120,12 +129,11 @@ __global__ __launch_bounds__(256) void route_kernel(RouteParams p) {
         counts[e] = 0;
     }
     __syncthreads();
-    __threadfence_block();
 
     // ---- tables: first appearance and count per expert (order-independent
     // atomics on LDS), then ranks in first-appearance order
     for (int q = tid; q < n_pos; q += blockDim.x) {
-        const int e = p.ids[q];
+        const int e = ids_in_lds ? lds_ids[q] : p.ids[q];
         if (e < 0 || e >= E) {
             p.list_pos[q] = -1;
             *p.error = 1;  // prepare_route_tables rejects such ids (moonlight_metal.m:545)
@@ -135,24 +143,73 @@ __global__ __launch_bounds__(256) void route_kernel(RouteParams p) {
         atomicAdd(&counts[e], 1);
     }
     __syncthreads();
-    if (tid < E && counts[tid] > 0) {
-        int rank = 0, off = 0;
-        const int mine = first_pos[tid];
-        for (int e = 0; e < E; ++e) {
-            if (counts[e] > 0 && first_pos[e] < mine) {
-                ++rank;
-                off += counts[e];
-            }
+    // first-appearance ranks without serial scans: a bit per list position
+    // that is the first occurrence of its expert; the rank of expert e is the
+    // number of such bits before first_pos[e]
+    const int nwords = (n_pos + 63) / 64;
+    for (int w = wave; w < nwords; w += 4) {
+        const int q = w * 64 + lane;
+        bool first = false;
+        if (q < n_pos) {
+            const int e = ids_in_lds ? lds_ids[q] : p.ids[q];
+            first = e >= 0 && e < E && first_pos[e] == q;
         }
-        p.unique[rank] = tid;
-        offsets[tid] = off;
-        p.offsets[tid] = off;
+        const unsigned long long m = __ballot(first);
+        if (lane == 0) first_mask[w] = m;
     }
-    if (tid < E) p.counts[tid] = counts[tid];
+    __syncthreads();
     if (tid == 0) {
-        int n = 0;
-        for (int e = 0; e < E; ++e) n += counts[e] > 0;
-        *p.n_unique = n;
+        int acc = 0;
+        for (int w = 0; w < nwords; ++w) {
+            word_prefix[w] = acc;
+            acc += __popcll(first_mask[w]);
+        }
+        unique_total = acc;
+        *p.n_unique = acc;
+    }
+    __syncthreads();
+    for (int e = tid; e < E; e += blockDim.x) {
+        rank_of[e] = -1;
+        if (counts[e] > 0) {
+            const int q = first_pos[e];
+            const int rank = word_prefix[q / 64] +
+                             __popcll(first_mask[q / 64] & ((1ull << (q % 64)) - 1ull));
+            rank_of[e] = rank;
+            count_by_rank[rank] = counts[e];
+            p.unique[rank] = e;
+        }
+        p.counts[e] = counts[e];
+    }
+    __syncthreads();
+    if (wave == 0) {  // exclusive scan of the counts in rank order (<= 256 ranks)
+        int c4[4], local = 0;
+        const int n_unique = unique_total;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int rk = lane * 4 + i;
+            c4[i] = rk < n_unique ? count_by_rank[rk] : 0;
+            local += c4[i];
+        }
+        int incl = local;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const int v = __shfl_up(incl, o, 64);
+            if (lane >= o) incl += v;
+        }
+        int run = incl - local;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int rk = lane * 4 + i;
+            if (rk < n_unique) offset_by_rank[rk] = run;
+            run += c4[i];
+        }
+    }
+    __syncthreads();
+    for (int e = tid; e < E; e += blockDim.x) {
+        if (rank_of[e] >= 0) {
+            offsets[e] = offset_by_rank[rank_of[e]];
+            p.offsets[e] = offsets[e];
+        }
     }
     __syncthreads();
 
@@ -163,7 +220,7 @@ __global__ __launch_bounds__(256) void route_kernel(RouteParams p) {
         const int base = offsets[e];
         for (int q0 = 0; q0 < n_pos; q0 += 64) {
             const int q = q0 + lane;
-            const bool match = q < n_pos && p.ids[q] == e;
+            const bool match = q < n_pos && (ids_in_lds ? lds_ids[q] : p.ids[q]) == e;
             const unsigned long long mask = __ballot(match);
             if (match) {
                 const int j = running + __popcll(mask & ((1ull << lane) - 1ull));
@@ -180,7 +237,8 @@ int route_topk(const RouteParams &p, hipStream_t stream) {
     if (!p.logits || !p.bias || !p.ids || !p.weights || p.rows <= 0 || p.experts <= 0 ||
         p.experts > kMaxExperts || p.top_k <= 0 || p.top_k > kMaxTopK ||
         p.top_k > p.experts || !p.n_unique || !p.unique || !p.counts || !p.offsets ||
-        !p.list_rows || !p.list_slots || !p.list_pos || !p.error)
+        !p.list_rows || !p.list_slots || !p.list_pos || !p.error ||
+        p.rows * p.top_k > kRouteMaxPositions)
         return kErrArgs;
     hipLaunchKernelGGL(route_kernel, dim3(1), dim3(256), 0, stream, p);
     return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
@@ -191,7 +249,8 @@ int route_topk(const RouteParams &p, hipStream_t stream) {
 __global__ __launch_bounds__(256) void combine_kernel(CombineParams p) {
     const int r = blockIdx.x;
     const int K = p.top_k;
-    for (int d = threadIdx.x; d < p.hidden; d += blockDim.x) {
+    for (int d = blockIdx.y * blockDim.x + threadIdx.x; d < p.hidden;
+         d += gridDim.y * blockDim.x) {
         float routed = 0.0f;
         for (int k = 0; k < K; ++k) {
             const int q = r * K + k;
@@ -209,7 +268,10 @@ __global__ __launch_bounds__(256) void combine_kernel(CombineParams p) {
 int moe_combine(const CombineParams &p, hipStream_t stream) {
     if (!p.weights || !p.list_pos || !p.expert_out || !p.shared_out || !p.out || p.rows <= 0)
         return kErrArgs;
-    hipLaunchKernelGGL(combine_kernel, dim3(p.rows), dim3(256), 0, stream, p);
+    // one workgroup per 256 hidden dims of a row: the per-row dependent load
+    // chain (list position -> expert output) is latency bound
+    hipLaunchKernelGGL(combine_kernel, dim3(p.rows, (p.hidden + 255) / 256), dim3(256), 0, stream,
+                       p);
     return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
 }
 
@@ -314,8 +376,9 @@ int rmsnorm_rows(const float *x, const float *w, float *y, int rows, int width, 
 
 // out[r, :] = table[ids[r], :] (moonlight_kernels.metal:10-21).
 __global__ __launch_bounds__(256) void embed_kernel(const float *table, const int *ids, float *out,
-                                                    int width, int vocab) {
+                                                    int width, int vocab, int *clear_flag) {
     const int r = blockIdx.x;
+    if (clear_flag && r == 0 && threadIdx.x == 0) *clear_flag = 0;
     int id = ids[r];
     id = id < 0 ? 0 : (id >= vocab ? vocab - 1 : id);  // host validated; clamp defensively
     const float *src = table + (long)id * width;
@@ -323,10 +386,10 @@ __global__ __launch_bounds__(256) void embed_kernel(const float *table, const in
 }
 
 int embed_rows(const float *table, const int *ids, float *out, int rows, int width, int vocab,
-               hipStream_t stream) {
+               int *clear_flag, hipStream_t stream) {
     if (!table || !ids || !out || rows <= 0 || width <= 0) return kErrArgs;
     hipLaunchKernelGGL(embed_kernel, dim3(rows), dim3(256), 0, stream, table, ids, out, width,
-                       vocab);
+                       vocab, clear_flag);
     return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
 }
 

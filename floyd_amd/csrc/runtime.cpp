@@ -63,6 +63,9 @@ struct Matrix {
 struct LayerPlan {
     std::string error;  // first problem found while resolving, empty if usable
     Matrix q, kv_a, kv_b, o;
+    // q_proj rows followed by kv_a rows in one matrix (same format): one GEMV
+    // launch produces [q | compressed] per token row; fmt -1 when not fused
+    Matrix qkv_a;
     const float *input_norm = nullptr, *post_norm = nullptr, *kv_norm = nullptr;
     bool dense = false;
     Matrix gate, up, down;
@@ -90,6 +93,7 @@ struct MoonlightModel {
     Matrix lm_head;
     std::string head_error;
     std::string device_name;
+    std::vector<void *> extra;  // device buffers owned by the model (fused matrices)
 };
 
 struct MoonlightSession {
@@ -101,7 +105,7 @@ struct MoonlightSession {
     // device buffers
     float *h = nullptr, *tmp = nullptr, *query = nullptr, *compressed = nullptr;
     float *query_rope = nullptr, *query_absorbed = nullptr, *context = nullptr;
-    float *part_max = nullptr, *part_sum = nullptr, *part_lc = nullptr;
+    float *part_max = nullptr, *part_sum = nullptr, *part_lc = nullptr, *latent_ctx = nullptr;
     float *latent_kv = nullptr, *rope_kv = nullptr, *logits = nullptr;
     float *router_logits = nullptr, *route_weights = nullptr;
     int *route_ids = nullptr, *n_unique = nullptr, *unique = nullptr, *counts = nullptr;
@@ -284,6 +288,32 @@ bool build_plans(MoonlightModel *m, std::string *error) {
     }
     for (int l = 0; l < c.layer_count; ++l)
         m->layers[l].expert_table = m->expert_tables + (size_t)l * c.expert_count;
+    // [q_proj ; kv_a] row concatenation per layer: each row keeps its packed
+    // bytes and its scale, only the placement changes
+    for (int l = 0; l < c.layer_count; ++l) {
+        LayerPlan &p = m->layers[l];
+        p.qkv_a.fmt = -1;
+        if (!p.error.empty() || p.q.fmt != p.kv_a.fmt) continue;
+        const size_t rb = (size_t)(p.q.fmt == kF32 ? c.hidden_size * 4
+                                   : p.q.fmt == kQ8 ? c.hidden_size : (c.hidden_size + 1) / 2);
+        const size_t wbytes = (size_t)(qw + cw) * rb;
+        const size_t sbytes = p.q.fmt == kF32 ? 0 : (size_t)(qw + cw) * sizeof(float);
+        uint8_t *buf = nullptr;
+        if (hipMalloc((void **)&buf, align256(wbytes) + sbytes) != hipSuccess) continue;
+        m->extra.push_back(buf);
+        bool ok = hipMemcpy(buf, p.q.w, (size_t)qw * rb, hipMemcpyDeviceToDevice) == hipSuccess &&
+                  hipMemcpy(buf + (size_t)qw * rb, p.kv_a.w, (size_t)cw * rb,
+                            hipMemcpyDeviceToDevice) == hipSuccess;
+        float *sc = reinterpret_cast<float *>(buf + align256(wbytes));
+        if (ok && sbytes)
+            ok = hipMemcpy(sc, p.q.s, (size_t)qw * 4, hipMemcpyDeviceToDevice) == hipSuccess &&
+                 hipMemcpy(sc + qw, p.kv_a.s, (size_t)cw * 4, hipMemcpyDeviceToDevice) ==
+                     hipSuccess;
+        if (!ok) continue;
+        p.qkv_a.fmt = p.q.fmt;
+        p.qkv_a.w = buf;
+        p.qkv_a.s = sbytes ? sc : nullptr;
+    }
     return true;
 }
 
@@ -292,6 +322,7 @@ void free_model(MoonlightModel *m) {
     if (m->arena) (void)hipFree(m->arena);
     if (m->expert_tables) (void)hipFree(m->expert_tables);
     if (m->inv_freq) (void)hipFree(m->inv_freq);
+    for (void *p : m->extra) (void)hipFree(p);
     delete m;
 }
 
@@ -788,10 +819,24 @@ int attention(MoonlightSession *s, int layer, const float *x, int rows, int posi
     const LayerPlan &lp = s->model->layers[layer];
     const int qw = c.head_count * (c.qk_nope_dim + c.qk_rope_dim);
     const int cw = c.kv_lora_rank + c.qk_rope_dim;
-    if (gemv_rows(s, lp.q, x, rows, c.hidden_size, qw, s->query, norm_w)) return kErrLaunch;
-    if (gemv_rows(s, lp.kv_a, x, rows, c.hidden_size, cw, s->compressed, norm_w))
-        return kErrLaunch;
     MlaParams p;
+    if (lp.qkv_a.fmt >= 0) {
+        // one launch: [q | compressed] rows of width qw + cw
+        if (gemv_rows(s, lp.qkv_a, x, rows, c.hidden_size, qw + cw, s->query, norm_w))
+            return kErrLaunch;
+        p.query = s->query;
+        p.query_stride = qw + cw;
+        p.compressed = s->query + qw;
+        p.compressed_stride = qw + cw;
+    } else {
+        if (gemv_rows(s, lp.q, x, rows, c.hidden_size, qw, s->query, norm_w)) return kErrLaunch;
+        if (gemv_rows(s, lp.kv_a, x, rows, c.hidden_size, cw, s->compressed, norm_w))
+            return kErrLaunch;
+        p.query = s->query;
+        p.query_stride = qw;
+        p.compressed = s->compressed;
+        p.compressed_stride = cw;
+    }
     p.rows = rows;
     p.position = position;
     p.heads = c.head_count;
@@ -801,8 +846,6 @@ int attention(MoonlightSession *s, int layer, const float *x, int rows, int posi
     p.latent = c.kv_lora_rank;
     p.eps = c.rms_norm_epsilon;
     p.scale = 1.0f / sqrtf((float)(c.qk_nope_dim + c.qk_rope_dim));
-    p.query = s->query;
-    p.compressed = s->compressed;
     p.kv_norm = lp.kv_norm;
     p.inv_freq = s->model->inv_freq;
     p.kv_b.fmt = lp.kv_b.fmt;
@@ -816,6 +859,7 @@ int attention(MoonlightSession *s, int layer, const float *x, int rows, int posi
     p.part_max = s->part_max;
     p.part_sum = s->part_sum;
     p.part_lc = s->part_lc;
+    p.latent_context = s->latent_ctx;
     p.context = s->context;
     if (int e = mla_attention_core(p, stream_of(s))) return e;
     return gemv_rows(s, lp.o, s->context, rows, c.head_count * c.value_dim, c.hidden_size, out,
@@ -923,8 +967,8 @@ int forward(MoonlightSession *s, const int *ids, int count, int start, float *la
     const size_t H = (size_t)c.hidden_size;
     bool ok = hipEventRecord(s->ev_start, st) == hipSuccess &&
               to_device(s, s->ids, s->host_ids, (size_t)count * sizeof(int)) &&
-              hipMemsetAsync(s->route_error, 0, sizeof(int), st) == hipSuccess &&
-              embed_rows(m->embed, s->ids, s->h, count, c.hidden_size, c.vocab_size, st) == kOk;
+              embed_rows(m->embed, s->ids, s->h, count, c.hidden_size, c.vocab_size,
+                         s->route_error, st) == kOk;
     for (int l = 0; ok && l < c.layer_count; ++l) {
         const LayerPlan &lp = m->layers[l];
         ok = attention(s, l, s->h, count, start, s->h, lp.input_norm, s->h) == kOk;
@@ -1009,8 +1053,10 @@ extern "C" int moonlight_session_create(MoonlightSession **out, MoonlightModel *
         session_alloc(s, &s->rope_kv, rope_elems, error, error_size) &&
         session_alloc(s, &s->ids, mb, error, error_size) &&
         session_alloc(s, &s->logits, logit_elems, error, error_size) &&
-        session_alloc(s, &s->query, mb * heads * (c.qk_nope_dim + c.qk_rope_dim), error,
-                      error_size) &&
+        session_alloc(s, &s->query,
+                      mb * (heads * (c.qk_nope_dim + c.qk_rope_dim) + c.kv_lora_rank +
+                            c.qk_rope_dim),
+                      error, error_size) &&
         session_alloc(s, &s->compressed, mb * (c.kv_lora_rank + c.qk_rope_dim), error,
                       error_size) &&
         session_alloc(s, &s->context, mb * heads * c.value_dim, error, error_size) &&
@@ -1019,6 +1065,7 @@ extern "C" int moonlight_session_create(MoonlightSession **out, MoonlightModel *
         session_alloc(s, &s->part_max, mb * splits * kMlaMaxHeads, error, error_size) &&
         session_alloc(s, &s->part_sum, mb * splits * kMlaMaxHeads, error, error_size) &&
         session_alloc(s, &s->part_lc, lc_elems, error, error_size) &&
+        session_alloc(s, &s->latent_ctx, mb * heads * c.kv_lora_rank, error, error_size) &&
         session_alloc(s, &s->router_logits, mb * E, error, error_size) &&
         session_alloc(s, &s->route_ids, mb * K, error, error_size) &&
         session_alloc(s, &s->route_weights, mb * K, error, error_size) &&
@@ -1143,7 +1190,7 @@ extern "C" int moonlight_test_embed(MoonlightSession *s, const int *ids, int cou
     const size_t bytes = (size_t)count * c.hidden_size * sizeof(float);
     bool ok = to_device(s, s->ids, s->host_ids, (size_t)count * sizeof(int)) &&
               embed_rows(s->model->embed, s->ids, s->h, count, c.hidden_size, c.vocab_size,
-                         stream_of(s)) == kOk &&
+                         nullptr, stream_of(s)) == kOk &&
               to_host(s, output, s->h, bytes);
     return finish(s) && ok;
 }
