@@ -154,6 +154,22 @@ def moonlight_extras(native, extra, decode_tokens):
     model.close()
 
 
+def measured_traffic(kernel):
+    """HBM bytes per launch of the headline kernel from the committed
+    rocprofv3 FETCH_SIZE / WRITE_SIZE passes (profiles/headline_traffic.json,
+    each counter scaled by what it reads for a copy of known size), or None
+    when that record is for another kernel instantiation."""
+    path = os.path.join(ROOT, "profiles", "headline_traffic.json")
+    try:
+        with open(path) as f:
+            rec = json.load(f)
+    except (OSError, ValueError):
+        return None
+    if rec.get("kernel") != kernel:
+        return None
+    return rec.get("bytes_per_launch")
+
+
 def cpu_baseline(case, budget_s=10.0):
     """The oracle's GEMV (restatement of the reference arithmetic) timed on the
     host cores on the same inputs, with the same parity check."""
@@ -193,6 +209,8 @@ def main():
     parser.add_argument("--no-moonlight", action="store_true",
                         help="skip the synthetic Moonlight MoE / decode measurements")
     parser.add_argument("--decode-tokens", type=int, default=20)
+    parser.add_argument("--only-headline", action="store_true",
+                        help="headline GEMV and the copy yardstick only (profiler runs)")
     args = parser.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: the hot path is single-device "
@@ -212,12 +230,13 @@ def main():
           f"{head_us_stream:.2f} us (stream launches)", file=sys.stderr, flush=True)
 
     extra = {}
-    for index, (name, (fmt, o, i, rows)) in enumerate({
+    extra_cases = {} if args.only_headline else {
             "cfg0_q8_11264x2048_b1": (1, 11264, 2048, 1),
             "cfg0_q8_11264x2048_b4": (1, 11264, 2048, 4),
             "cfg1_q4_2048x11264_b1": (2, 2048, 11264, 1),
             "q8_2048x11264_b1": (1, 2048, 11264, 1),
-            "f32_lmhead_163840x2048_b1": (0, 163840, 2048, 1)}.items()):
+            "f32_lmhead_163840x2048_b1": (0, 163840, 2048, 1)}
+    for index, (name, (fmt, o, i, rows)) in enumerate(extra_cases.items()):
         case = GemvCase(native, fmt, o, i, rows, seed=1000 + index)
         us, gbs = case.time(args.warmup, max(50, args.steps // 2))
         extra[name] = {"us": round(us, 3), "GB/s": round(gbs, 1),
@@ -235,7 +254,7 @@ def main():
     for b in src + dst:
         b.close()
 
-    if not args.no_moonlight:
+    if not args.no_moonlight and not args.only_headline:
         moonlight_extras(native, extra, args.decode_tokens)
 
     cpu = None
@@ -244,6 +263,7 @@ def main():
         print(f"[bench] cpu baseline {cpu['value']} GB/s on {cpu['cores']} threads, "
               f"parity rel-L2 {cpu['parity_rel_l2']:.2e}", file=sys.stderr, flush=True)
 
+    head_kernel = native.gemv_kernel_name(2, 11264, 2048, 1)
     line = {
         "metric": METRIC,
         "value": round(head_gbs, 2),
@@ -262,8 +282,8 @@ def main():
                    "weight_copies": len(head.w), "timing": "hipGraph of K launches"},
         "roofline": {"bound": "hbm", "achieved": round(head_gbs, 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(head_gbs / HBM_PEAK_GBS, 4),
-                     "traffic": None, "algorithmic_bytes": head.bytes,
-                     "kernel": "mlh::gemv_kernel<2,1,1,64>"},
+                     "traffic": measured_traffic(head_kernel), "algorithmic_bytes": head.bytes,
+                     "kernel": head_kernel},
         "cpu_baseline": cpu,
         "extra": extra,
     }

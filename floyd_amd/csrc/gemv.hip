@@ -3,6 +3,8 @@
 #include <cstdio>
 #include <cstdlib>
 
+#include <string>
+
 #include "gemv_impl.h"
 #include "moe.h"
 
@@ -165,6 +167,15 @@ GemvPlan plan_expert_gemv(int fmt, int O, int I, int rows, bool dual, int tasks)
 int gemv_rows_per_block(const GemvPlan &plan, bool dual) {
     const int out = dual ? plan.r / 2 : plan.r;
     return out * (64 / plan.lpr) * (plan.ks == 1 ? 4 : 1);
+}
+
+// Template name of the kernel gemv() launches for this shape (vector path).
+std::string gemv_kernel_name(int fmt, int O, int I, int rows, bool dual) {
+    const GemvPlan pl = plan_gemv(fmt, O, I, rows < kMaxGemvRows ? rows : kMaxGemvRows, dual);
+    char buf[96];
+    snprintf(buf, sizeof(buf), "mlh::gemv_kernel<0, %d, %d, %d, %d, %d, %d>", fmt, pl.b, pl.kt,
+             pl.lpr, pl.r, pl.ks);
+    return buf;
 }
 
 static bool aligned16(const void *ptr) { return ((uintptr_t)ptr & 15u) == 0; }

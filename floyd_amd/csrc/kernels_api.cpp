@@ -151,6 +151,16 @@ int mlk_gemv(int fmt, const void *w, const float *s, const float *x, float *y, i
     return finish(gemv(p, st), "mlk_gemv");
 }
 
+int mlk_gemv_kernel_name(int fmt, int out_width, int in_width, int rows, int swiglu, char *name,
+                         size_t name_size) {
+    if (!name || name_size == 0 || fmt < kF32 || fmt > kQ4 || out_width <= 0 || in_width <= 0 ||
+        rows <= 0)
+        return finish(kErrArgs, "mlk_gemv_kernel_name");
+    const std::string n = gemv_kernel_name(fmt, out_width, in_width, rows, swiglu != 0);
+    snprintf(name, name_size, "%s", n.c_str());
+    return kOk;
+}
+
 int mlk_gemv_swiglu(int fmt, const void *w_gate, const float *s_gate, const void *w_up,
                     const float *s_up, const float *x, float *h, int out_width, int in_width,
                     int rows, const float *norm_w, float eps) {

@@ -5,6 +5,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <string>
+
 namespace mlh {
 
 enum Fmt { kF32 = 0, kQ8 = 1, kQ4 = 2 };
@@ -41,6 +43,7 @@ struct GemvPlan;
 // Launch geometry the planner picks for a GEMV shape (exposed for the grouped
 // expert launches, which share the GEMV core).
 GemvPlan plan_gemv(int fmt, int O, int I, int rows, bool dual);
+std::string gemv_kernel_name(int fmt, int O, int I, int rows, bool dual);
 
 // Packs f32 rows like tools/convert_moonlight.py:46-66 (bits 8 or 4).
 int quantize_rows(int bits, const float *w, int rows, int cols, uint8_t *q, float *s,

@@ -39,6 +39,8 @@ SIGNATURES = {
                             _vp, _c.c_float, _vp]),
     "mlk_gemv_swiglu": (_c.c_int, [_c.c_int, _vp, _vp, _vp, _vp, _vp, _vp, _c.c_int,
                                    _c.c_int, _c.c_int, _vp, _c.c_float]),
+    "mlk_gemv_kernel_name": (_c.c_int, [_c.c_int, _c.c_int, _c.c_int, _c.c_int, _c.c_int,
+                                        _c.c_char_p, _c.c_size_t]),
     "mlk_time_gemv": (_c.c_int, [_c.c_int, _c.POINTER(_vp), _c.POINTER(_vp), _c.c_int, _vp,
                                  _vp, _c.c_int, _c.c_int, _c.c_int, _c.c_int, _c.c_int,
                                  _c.c_int, _c.POINTER(_c.c_double)]),
@@ -166,6 +168,13 @@ def gemv_swiglu(fmt, wg, sg, wu, su, x, h, out_width, in_width, rows, norm_w=Non
     check(load().mlk_gemv_swiglu(fmt, _ptr(wg), _ptr(sg), _ptr(wu), _ptr(su), _ptr(x),
                                  _ptr(h), out_width, in_width, rows, _ptr(norm_w), eps),
           "mlk_gemv_swiglu")
+
+
+def gemv_kernel_name(fmt, out_width, in_width, rows, swiglu=False):
+    buf = _c.create_string_buffer(128)
+    check(load().mlk_gemv_kernel_name(fmt, out_width, in_width, rows, int(swiglu), buf, 128),
+          "mlk_gemv_kernel_name")
+    return buf.value.decode()
 
 
 def time_gemv(fmt, w_list, s_list, x, y, out_width, in_width, rows, warmup, iters,

@@ -54,6 +54,11 @@ int mlk_gemv_swiglu(int fmt, const void *w_gate, const float *s_gate,
                     const void *w_up, const float *s_up, const float *x,
                     float *h, int out_width, int in_width, int rows,
                     const float *norm_w, float eps);
+/* Name of the kernel instantiation mlk_gemv (swiglu = 0) or mlk_gemv_swiglu
+ * (swiglu = 1) launches for this shape, as profilers print it; written into
+ * name[name_size]. */
+int mlk_gemv_kernel_name(int fmt, int out_width, int in_width, int rows,
+                         int swiglu, char *name, size_t name_size);
 /* Average device time per launch (microseconds) of `iters` back-to-back
  * mlk_gemv launches that rotate over n_copies weight copies (defeats the
  * 256 MB last-level cache), measured with HIP events on the library stream.

@@ -17,3 +17,20 @@ gcc $CFLAGS -I"$REF" -o "$OUT/libref_moe.so" "$HERE/ref_wrap_moe.c" -lm
 gcc $CFLAGS -I"$REF" -o "$OUT/libref_model.so" "$HERE/ref_wrap_model.c" \
     "$REF/moonlight_model.c" -lm
 echo "build_ref: built $OUT/libref_moe.so $OUT/libref_model.so"
+
+# The reference's own boundary tests, compiled unchanged from their sources
+# and linked against libfloyd_amd.so in place of moonlight_metal.m /
+# backend_metal.m: proof that the C ABI is a drop-in.  test_backend_metal
+# needs no fixtures and runs on the GPU (tests/test_reference_link_gpu.py);
+# the Moonlight tests need model/oracle fixture directories that do not exist
+# here, so they are only linked.
+LIB="$HERE/../floyd_amd/lib"
+if [ -f "$LIB/libfloyd_amd.so" ]; then
+    LINK="-L$LIB -lfloyd_amd -Wl,-rpath,\$ORIGIN/../../floyd_amd/lib -lm"
+    gcc -O2 -w -I"$REF" -o "$OUT/test_backend_metal" "$REF/tests/test_backend_metal.c" $LINK
+    for t in runtime primitives mla moe; do
+        gcc -O2 -w -fopenmp -I"$REF" -o "$OUT/test_moonlight_metal_$t" \
+            "$REF/tests/test_moonlight_metal_$t.c" "$REF/moonlight_model.c" $LINK
+    done
+    echo "build_ref: linked the reference's backend and Moonlight tests against libfloyd_amd.so"
+fi

@@ -50,3 +50,23 @@ def test_library_loads_and_binds_without_gpu():
     for name in native.SIGNATURES:
         assert hasattr(lib, name)
     assert set(native.SIGNATURES) <= declared_functions()
+
+
+REF_TESTS = ["test_backend_metal"] + [f"test_moonlight_metal_{t}"
+                                      for t in ("runtime", "primitives", "mla", "moe")]
+
+
+@pytest.mark.parametrize("name", REF_TESTS)
+def test_reference_tests_link_against_library(exported, name):
+    """The reference's own boundary tests (compiled unchanged by
+    oracle/build_ref.sh) take every moonlight_* / fm_* symbol they use from
+    libfloyd_amd.so."""
+    path = os.path.join(ROOT, "oracle", "_ref", name)
+    if not os.path.exists(path):
+        pytest.skip("oracle/_ref not built (needs the reference tree)")
+    out = subprocess.run(["nm", "-D", "--undefined-only", path], capture_output=True,
+                         text=True, check=True).stdout
+    used = {line.split()[-1] for line in out.splitlines()}
+    boundary = {s for s in used if s.startswith(("moonlight_", "fm_"))}
+    assert boundary, "no boundary symbols used"
+    assert boundary <= exported, sorted(boundary - exported)
