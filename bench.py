@@ -3,7 +3,7 @@
 
 Metric: q8/q4 dequant-GEMV GB/s (% of HBM peak); Moonlight q8
 decode tok/s.  A "step" is one dequant-GEMV launch over one batch of synthetic
-input.  The headline workload is BASELINE config 1: the q4 [11264 x 2048]
+input.  The headline workload is benchmark config 1: the q4 [11264 x 2048]
 Moonlight dense-FFN projection, W ~ N(0, 0.02) rounded to bf16 and packed
 with the container's per-row-scale int4 scheme, x ~ N(0, 1), batch 1.
 
@@ -90,7 +90,7 @@ class GemvCase:
 
 
 def moe_layer_bytes(unique, rows):
-    """Algorithmic bytes of one q8 MoE decode layer (BASELINE.md section 3):
+    """Algorithmic bytes of one q8 MoE decode layer:
     U routed experts x (gate + up + down + scales) + fused shared expert +
     f32 router and bias + the token rows in and out."""
     expert = 3 * 1408 * 2048 + 2 * 1408 * 4 + 2048 * 4
@@ -99,12 +99,48 @@ def moe_layer_bytes(unique, rows):
     return unique * expert + shared + router + rows * 2048 * 4 * 2
 
 
-# Algorithmic bytes of one full q8 decode step.
+# Algorithmic bytes of one full q8 decode step: attention 13.8 MB x 27 layers,
+# dense FFN 69.3 MB, MoE 69.9 MB x 26, f32 lm_head 1.342 GB, KV cache reads.
 DECODE_STEP_BYTES = {4096: 3856274688, 16384: 4620686592}
 
 
+def prefill_moe_ops(ids, rows, experts=64):
+    """(algorithmic FLOP, int8 MFMA ops executed) of one MoE prefill layer with
+    the given routes: routed 2*(3*1408*2048) FLOP per (token, expert), shared
+    2*(3*2816*2048) per token, router 2*64*2048 per token; the MFMA path runs
+    128-row tiles with two int8 limbs."""
+    import numpy as np
+    counts = np.bincount(np.asarray(ids).ravel(), minlength=experts)
+    flop = counts.sum() * 2 * 3 * 1408 * 2048 + rows * (2 * 3 * 2816 * 2048 + 2 * 64 * 2048)
+    padded = sum(-(-int(c) // 128) * 128 for c in counts if c)
+    shared_pad = -(-rows // 128) * 128
+    ops = 2 * 2 * (padded * 3 * 1408 * 2048 + shared_pad * 3 * 2816 * 2048)
+    return int(flop), int(ops)
+
+
+def prefill_moe(model, bits, extra, rows=2048):
+    """Config 3: one MoE layer over 2048 tokens whose experts follow Zipf(1.1)
+    (fixed per token), on the int8-MFMA grouped GEMM."""
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import oracle_lib
+    from floyd_amd import session as S
+    ids = oracle_lib.zipf_routes(rows, 64, 6, seed=2048)
+    sess = S.Session(model, rows, rows)
+    sess.fix_routes(ids)
+    us, uniq = sess.time_moe(1, rows, seed=3, warmup=3, iters=20)
+    sess.close()
+    flop, ops = prefill_moe_ops(ids, rows)
+    tflops = flop / (us * 1e-6) / 1e12
+    extra[f"cfg3_moe_prefill_q{bits}_T{rows}"] = {
+        "us": round(us, 1), "unique_experts": uniq, "algorithmic_flop": flop,
+        "TFLOP/s": round(tflops, 1), "frac_of_fp16_dense_peak": round(tflops / 2500.0, 4),
+        "int8_mfma_ops": ops, "int8_mfma_util": round(ops / (us * 1e-6) / 5.0e15, 4)}
+    print(f"[bench] MoE prefill q{bits} T={rows}: {us:.1f} us, {tflops:.1f} TFLOP/s "
+          f"(int8 MFMA busy {ops / (us * 1e-6) / 5.0e15:.2%})", file=sys.stderr, flush=True)
+
+
 def moonlight_extras(native, extra, decode_tokens):
-    """BASELINE configs 2 and 4 on a synthetic Moonlight-16B-A3B q8 model built
+    """Benchmark configs 2 and 4 on a synthetic Moonlight-16B-A3B q8 model built
     in HBM: one MoE layer at T = 1, 8, 64 and a full decode step at ctx 4096
     and 16384."""
     from floyd_amd import session as S
@@ -124,6 +160,7 @@ def moonlight_extras(native, extra, decode_tokens):
         print(f"[bench] MoE layer T={rows}: {us:.1f} us, U={uniq}, {gbs:.0f} GB/s",
               file=sys.stderr, flush=True)
     sess.close()
+    prefill_moe(model, 8, extra)
     for ctx in (4096, 16384):
         sess = S.Session(model, ctx + decode_tokens + 8, 1)
         sess.fill_kv(ctx, seed=ctx)
@@ -151,6 +188,9 @@ def moonlight_extras(native, extra, decode_tokens):
               f"({1e3 / wall_ms:.1f} tok/s), device {dev_ms:.3f} ms",
               file=sys.stderr, flush=True)
         sess.close()
+    model.close()
+    model = S.Model.synthetic(expert_bits=4, dense_bits=4)
+    prefill_moe(model, 4, extra)
     model.close()
 
 
@@ -214,7 +254,7 @@ def main():
     args = parser.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: the hot path is single-device "
-              "(multi-GPU sharding is a design note in DESIGN.md, not a measured path)",
+              "(multi-GPU sharding is a design note, not a measured path)",
               file=sys.stderr)
         sys.exit(2)
 
@@ -222,7 +262,7 @@ def main():
     device = native.init()
     print(f"[bench] device {device}", file=sys.stderr, flush=True)
 
-    # headline: BASELINE config 1, q4 [11264 x 2048], batch 1
+    # headline: benchmark config 1, q4 [11264 x 2048], batch 1
     head = GemvCase(native, 2, 11264, 2048, 1, seed=101)
     head_us, head_gbs = head.time(args.warmup, args.steps, use_graph=True)
     head_us_stream, head_gbs_stream = head.time(args.warmup, args.steps, use_graph=False)
@@ -277,7 +317,7 @@ def main():
         "vs_baseline": None,
         "dtype": "q4 weights (u8 nibbles) x f32 activations, f32 accumulate",
         "data": "synthetic: W~N(0,0.02) bf16 -> per-row int4; x~N(0,1)",
-        "config": {"workload": "BASELINE config 1: q4 dequant-GEMV [11264 x 2048] "
+        "config": {"workload": "config 1: q4 dequant-GEMV [11264 x 2048] "
                                "(Moonlight dense-FFN projection), batch 1",
                    "weight_copies": len(head.w), "timing": "hipGraph of K launches"},
         "roofline": {"bound": "hbm", "achieved": round(head_gbs, 2), "peak": HBM_PEAK_GBS,

@@ -192,25 +192,20 @@ int gemv(const GemvParams &p_in, hipStream_t stream) {
         row_bytes % 16 == 0 && (p_in.fmt != kQ4 || p_in.I % 2 == 0) && aligned16(p_in.w) &&
         (!p_in.w2 || aligned16(p_in.w2)) && aligned16(p_in.x) && p_in.x_stride % 4 == 0 &&
         (!p_in.norm_w || aligned16(p_in.norm_w));
-    // token rows beyond 4 are processed in slices of 4 (register budget)
-    for (int r0 = 0; r0 < p_in.rows; r0 += kMaxGemvRows) {
-        GemvParams p = p_in;
-        p.rows = p_in.rows - r0 < kMaxGemvRows ? p_in.rows - r0 : kMaxGemvRows;
-        p.x = p_in.x + (long)r0 * p_in.x_stride;
-        p.y = p_in.y + (long)r0 * p_in.y_stride;
-        if (p.resid) p.resid = p_in.resid + (long)r0 * p_in.resid_stride;
-        bool done = false;
-        if (vector_ok) {
-            const GemvPlan plan = plan_gemv(p.fmt, p.O, p.I, p.rows,
-                                            p.epilogue == kEpiSiluDual);
-            GemvLaunch L;
-            L.plain = p;
-            done = dispatch_gemv(p.fmt, L, 0, plan, dim3(1), stream);
-        }
-        if (!done) {
-            hipLaunchKernelGGL(gemv_generic_kernel, dim3(p.O, p.rows), dim3(64), 0, stream, p,
-                               p.fmt);
-        }
+    // token rows beyond 4 run as slices of 4 (register budget) along grid.y
+    // of one launch
+    bool done = false;
+    if (vector_ok) {
+        const int plan_rows = p_in.rows < kMaxGemvRows ? p_in.rows : kMaxGemvRows;
+        const GemvPlan plan = plan_gemv(p_in.fmt, p_in.O, p_in.I, plan_rows,
+                                        p_in.epilogue == kEpiSiluDual);
+        GemvLaunch L;
+        L.plain = p_in;
+        done = dispatch_gemv(p_in.fmt, L, 0, plan, dim3(1), stream);
+    }
+    if (!done) {
+        hipLaunchKernelGGL(gemv_generic_kernel, dim3(p_in.O, p_in.rows), dim3(64), 0, stream,
+                           p_in, p_in.fmt);
     }
     return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
 }

@@ -315,12 +315,15 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvLaunch L) {
         job.s2 = p.s2;
         job.O = p.O;
         job.I = p.I;
-        job.rows = p.rows;
+        // blockIdx.y selects a slice of B token rows
+        const int row0 = blockIdx.y * B;
+        job.rows = p.rows - row0 < B ? p.rows - row0 : B;
 #pragma unroll
         for (int b = 0; b < B; ++b) {
-            job.x[b] = p.x + (long)b * p.x_stride;
-            job.y[b] = p.y + (long)b * p.y_stride;
-            job.resid[b] = p.resid ? p.resid + (long)b * p.resid_stride : nullptr;
+            const long r = row0 + (b < job.rows ? b : 0);
+            job.x[b] = p.x + r * p.x_stride;
+            job.y[b] = p.y + r * p.y_stride;
+            job.resid[b] = p.resid ? p.resid + r * p.resid_stride : nullptr;
         }
         job.norm_w = p.norm_w;
         job.eps = p.eps;
@@ -390,7 +393,8 @@ template <int MODE, int FMT, int B, int KT, int LPR, int R, int KS>
 static void launch_gemv(const GemvLaunch &L, dim3 grid, hipStream_t stream) {
     if constexpr (MODE == 0) {
         const int per_block = rows_per_block<LPR, R, KS>(L.plain.epilogue == kEpiSiluDual);
-        grid = dim3((unsigned)((L.plain.O + per_block - 1) / per_block));
+        grid = dim3((unsigned)((L.plain.O + per_block - 1) / per_block),
+                    (unsigned)((L.plain.rows + B - 1) / B));
     }
     hipLaunchKernelGGL((gemv_kernel<MODE, FMT, B, KT, LPR, R, KS>), grid, dim3(256), 0, stream, L);
 }

@@ -22,6 +22,9 @@ struct RouteParams {
     int *list_slots = nullptr; // [rows*top_k] slot per list entry
     int *list_pos = nullptr;   // [rows*top_k] list entry of (row, slot), -1 if invalid
     int *error = nullptr;      // [1] set to 1 when an id is out of range
+    // optional [rows, top_k] expert ids given by the caller: weights come from
+    // their scores (moe_route_fixed, moe_route.h:76-87) instead of a top-k
+    const int *fixed_ids = nullptr;
 };
 int route_topk(const RouteParams &p, hipStream_t stream);
 

@@ -17,11 +17,11 @@
 
 namespace mlh {
 
-// Sigmoid as moe_route.h:12-14 computes it with glibc: 1 / (1 + expf(-x)).
-// exp is evaluated in double and rounded once, which is the correctly rounded
-// expf (glibc's expf is correctly rounded except in cases below its 0.502 ulp
-// bound), so the scores -- and therefore the selected expert ids -- match the
-// host twin bit for bit.
+// Router score 1 / (1 + e^-x) (moe_route.h:12-14) with e^-x correctly
+// rounded to f32: exp is evaluated in double and rounded once.  Host glibc
+// expf, which the reference's CPU twin calls, misrounds ~0.06 % of inputs by
+// one ulp; a selection can only change where two selection scores tie within
+// that ulp.
 __device__ __forceinline__ float sigmoid_exact(float logit) {
     const float e = (float)exp(-(double)logit);
     return 1.0f / (1.0f + e);
@@ -32,42 +32,41 @@ constexpr int kMaxTopK = 16;
 constexpr int kRouteLdsIds = 4096;
 constexpr int kRouteMaxPositions = 16384;  // rows * top_k per routing call
 
-// One workgroup: top-k for every token row, then the route tables.
-__global__ __launch_bounds__(256) void route_kernel(RouteParams p) {
-    __shared__ int first_pos[kMaxExperts];
-    __shared__ int counts[kMaxExperts];
-    __shared__ int offsets[kMaxExperts];
-    __shared__ int lds_ids[kRouteLdsIds];  // selected ids when rows*top_k fits
-    __shared__ unsigned long long first_mask[kRouteMaxPositions / 64];
-    __shared__ int word_prefix[kRouteMaxPositions / 64];
-    __shared__ int rank_of[kMaxExperts], count_by_rank[kMaxExperts], offset_by_rank[kMaxExperts];
-    __shared__ int unique_total;
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int wave = tid >> 6;
-    const int E = p.experts, K = p.top_k, M = p.rows;
-    const int n_pos = M * K;
-    const bool ids_in_lds = n_pos <= kRouteLdsIds;
-
-    // ---- top-k selection: one wave per token row, experts spread over lanes
-    for (int r = wave; r < M; r += 4) {
-        float score[kMaxExperts / 64];
-        float sel[kMaxExperts / 64];
+// Routing of one token row by one wave: sigmoid scores, top-k selection (or
+// the given expert ids, moe_route_fixed, moe_route.h:76-87), finalised
+// weights (moe_route_finalize, moe_route.h:89-99).  Writes ids / weights /
+// trace, and the ids into lds_ids when it is non-null.
+__device__ void route_row(const RouteParams &p, int r, int lane, int *lds_ids) {
+    const int E = p.experts, K = p.top_k;
+    float score[kMaxExperts / 64];
+    float sel[kMaxExperts / 64];
 #pragma unroll
-        for (int j = 0; j < kMaxExperts / 64; ++j) {
-            const int e = lane + 64 * j;
-            if (e < E) {
-                score[j] = sigmoid_exact(p.logits[(long)r * E + e]);
-                sel[j] = score[j] + p.bias[e];
-            } else {
-                score[j] = 0.0f;
-                sel[j] = -INFINITY;
-            }
+    for (int j = 0; j < kMaxExperts / 64; ++j) {
+        const int e = lane + 64 * j;
+        if (e < E) {
+            score[j] = sigmoid_exact(p.logits[(long)r * E + e]);
+            sel[j] = score[j] + p.bias[e];
+        } else {
+            score[j] = 0.0f;
+            sel[j] = -INFINITY;
         }
+    }
+    float wk[kMaxTopK];
+    int ids[kMaxTopK];
+    if (p.fixed_ids) {
+        for (int k = 0; k < K; ++k) {
+            const int e = p.fixed_ids[(long)r * K + k];
+            const bool valid = e >= 0 && e < E;
+            const int owner = valid ? (e & 63) : 0, slot_j = valid ? e >> 6 : -1;
+            float chosen = 0.0f;
+#pragma unroll
+            for (int j = 0; j < kMaxExperts / 64; ++j)
+                if (lane == owner && j == slot_j) chosen = score[j];
+            ids[k] = valid ? e : -1;
+            wk[k] = __shfl(chosen, owner, 64);
+        }
+    } else {
         unsigned taken = 0;  // bit j: lane's expert lane + 64 j already chosen
-        float wsum = 0.0f;
-        float wk[kMaxTopK];
-        int ids[kMaxTopK];
         for (int k = 0; k < K; ++k) {
             // lane-local scan in increasing expert order, strict '>' keeps the
             // lower index on ties (moe_route.h:59-71)
@@ -100,30 +99,50 @@ __global__ __launch_bounds__(256) void route_kernel(RouteParams p) {
                     taken |= 1u << j;
                     chosen = score[j];
                 }
-            chosen = __shfl(chosen, owner, 64);
             ids[k] = best_e;
-            wk[k] = chosen;
-        }
-        if (p.normalize) {
-            for (int k = 0; k < K; ++k) wsum += wk[k];
-            wsum += 1e-20f;
-        } else {
-            wsum = 1.0f;
-        }
-        if (lane < K) {
-            int id = ids[0];
-            float w = wk[0];
-            for (int k = 1; k < K; ++k)
-                if (lane == k) {
-                    id = ids[k];
-                    w = wk[k];
-                }
-            p.ids[(long)r * K + lane] = id;
-            if (ids_in_lds) lds_ids[r * K + lane] = id;
-            p.weights[(long)r * K + lane] = w / wsum * p.routed_scale;
-            if (p.trace) p.trace[(long)r * K + lane] = id;
+            wk[k] = __shfl(chosen, owner, 64);
         }
     }
+    float wsum = 1.0f;
+    if (p.normalize) {
+        wsum = 0.0f;
+        for (int k = 0; k < K; ++k) wsum += wk[k];
+        wsum += 1e-20f;
+    }
+    if (lane < K) {
+        int id = ids[0];
+        float w = wk[0];
+        for (int k = 1; k < K; ++k)
+            if (lane == k) {
+                id = ids[k];
+                w = wk[k];
+            }
+        p.ids[(long)r * K + lane] = id;
+        if (lds_ids) lds_ids[r * K + lane] = id;
+        p.weights[(long)r * K + lane] = w / wsum * p.routed_scale;
+        if (p.trace) p.trace[(long)r * K + lane] = id;
+    }
+}
+
+// One workgroup: routing of every token row, then the route tables (small
+// batches: decode and short appends).
+__global__ __launch_bounds__(256) void route_kernel(RouteParams p) {
+    __shared__ int first_pos[kMaxExperts];
+    __shared__ int counts[kMaxExperts];
+    __shared__ int offsets[kMaxExperts];
+    __shared__ int lds_ids[kRouteLdsIds];  // selected ids when rows*top_k fits
+    __shared__ unsigned long long first_mask[kRouteMaxPositions / 64];
+    __shared__ int word_prefix[kRouteMaxPositions / 64];
+    __shared__ int rank_of[kMaxExperts], count_by_rank[kMaxExperts], offset_by_rank[kMaxExperts];
+    __shared__ int unique_total;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int E = p.experts, K = p.top_k, M = p.rows;
+    const int n_pos = M * K;
+    const bool ids_in_lds = n_pos <= kRouteLdsIds;
+
+    for (int r = wave; r < M; r += 4) route_row(p, r, lane, ids_in_lds ? lds_ids : nullptr);
     for (int e = tid; e < E; e += blockDim.x) {
         first_pos[e] = INT_MAX;
         counts[e] = 0;
@@ -233,6 +252,145 @@ __global__ __launch_bounds__(256) void route_kernel(RouteParams p) {
     }
 }
 
+// Large batches (prefill): one wave per token row over many workgroups ...
+__global__ __launch_bounds__(256) void route_select_kernel(RouteParams p) {
+    const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (r < p.rows) route_row(p, r, threadIdx.x & 63, nullptr);
+}
+
+// ... then the tables in one workgroup of 16 waves.  List order within an
+// expert is (row, slot) order: each wave owns a contiguous block of rows,
+// counts its entries per expert, and after a scan over the waves walks its
+// rows in order with private per-expert cursors (the experts of one row are
+// distinct, so the lanes of a row never share a cursor).
+constexpr int kTableWaves = 16;
+__global__ __launch_bounds__(1024) void route_tables_kernel(RouteParams p) {
+    __shared__ int first_pos[kMaxExperts];
+    __shared__ int counts[kMaxExperts];
+    __shared__ int offsets[kMaxExperts];
+    __shared__ unsigned long long first_mask[kRouteMaxPositions / 64];
+    __shared__ int word_prefix[kRouteMaxPositions / 64];
+    __shared__ int rank_of[kMaxExperts], count_by_rank[kMaxExperts], offset_by_rank[kMaxExperts];
+    __shared__ int cursor[kTableWaves][kMaxExperts];
+    __shared__ int unique_total;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int E = p.experts, K = p.top_k, M = p.rows;
+    const int n_pos = M * K;
+    for (int e = tid; e < E; e += blockDim.x) {
+        first_pos[e] = INT_MAX;
+        counts[e] = 0;
+    }
+    for (int i = tid; i < kTableWaves * kMaxExperts; i += blockDim.x) (&cursor[0][0])[i] = 0;
+    __syncthreads();
+    const int rows_per_wave = (M + kTableWaves - 1) / kTableWaves;
+    const int r_begin = wave * rows_per_wave;
+    const int r_end = min(M, r_begin + rows_per_wave);
+    for (int q = tid; q < n_pos; q += blockDim.x) {
+        const int e = p.ids[q];
+        if (e < 0 || e >= E) {
+            p.list_pos[q] = -1;
+            *p.error = 1;  // prepare_route_tables rejects such ids (moonlight_metal.m:545)
+            continue;
+        }
+        atomicMin(&first_pos[e], q);
+        atomicAdd(&counts[e], 1);
+    }
+    for (int q = r_begin * K + lane; q < r_end * K; q += 64) {
+        const int e = p.ids[q];
+        if (e >= 0 && e < E) atomicAdd(&cursor[wave][e], 1);
+    }
+    __syncthreads();
+    const int nwords = (n_pos + 63) / 64;
+    for (int w = wave; w < nwords; w += kTableWaves) {
+        const int q = w * 64 + lane;
+        bool first = false;
+        if (q < n_pos) {
+            const int e = p.ids[q];
+            first = e >= 0 && e < E && first_pos[e] == q;
+        }
+        const unsigned long long m = __ballot(first);
+        if (lane == 0) first_mask[w] = m;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        int acc = 0;
+        for (int w = 0; w < nwords; ++w) {
+            word_prefix[w] = acc;
+            acc += __popcll(first_mask[w]);
+        }
+        unique_total = acc;
+        *p.n_unique = acc;
+    }
+    __syncthreads();
+    for (int e = tid; e < E; e += blockDim.x) {
+        rank_of[e] = -1;
+        if (counts[e] > 0) {
+            const int q = first_pos[e];
+            const int rank = word_prefix[q / 64] +
+                             __popcll(first_mask[q / 64] & ((1ull << (q % 64)) - 1ull));
+            rank_of[e] = rank;
+            count_by_rank[rank] = counts[e];
+            p.unique[rank] = e;
+        }
+        p.counts[e] = counts[e];
+    }
+    __syncthreads();
+    if (wave == 0) {  // exclusive scan of the counts in rank order (<= 256 ranks)
+        int c4[4], local = 0;
+        const int n_unique = unique_total;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int rk = lane * 4 + i;
+            c4[i] = rk < n_unique ? count_by_rank[rk] : 0;
+            local += c4[i];
+        }
+        int incl = local;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const int v = __shfl_up(incl, o, 64);
+            if (lane >= o) incl += v;
+        }
+        int run = incl - local;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int rk = lane * 4 + i;
+            if (rk < n_unique) offset_by_rank[rk] = run;
+            run += c4[i];
+        }
+    }
+    __syncthreads();
+    for (int e = tid; e < E; e += blockDim.x) {
+        if (rank_of[e] >= 0) {
+            offsets[e] = offset_by_rank[rank_of[e]];
+            p.offsets[e] = offsets[e];
+            int run = offsets[e];  // per-wave starting cursors, waves in row order
+            for (int w = 0; w < kTableWaves; ++w) {
+                const int c = cursor[w][e];
+                cursor[w][e] = run;
+                run += c;
+            }
+        }
+    }
+    __syncthreads();
+    for (int r = r_begin; r < r_end; ++r) {
+        if (lane < K) {
+            const int q = r * K + lane;
+            const int e = p.ids[q];
+            if (e >= 0 && e < E) {
+                const int j = cursor[wave][e];
+                cursor[wave][e] = j + 1;
+                p.list_rows[j] = r;
+                p.list_slots[j] = lane;
+                p.list_pos[q] = j;
+            }
+        }
+    }
+}
+
+constexpr int kRouteFusedMaxPositions = 1024;
+
 int route_topk(const RouteParams &p, hipStream_t stream) {
     if (!p.logits || !p.bias || !p.ids || !p.weights || p.rows <= 0 || p.experts <= 0 ||
         p.experts > kMaxExperts || p.top_k <= 0 || p.top_k > kMaxTopK ||
@@ -240,7 +398,12 @@ int route_topk(const RouteParams &p, hipStream_t stream) {
         !p.list_rows || !p.list_slots || !p.list_pos || !p.error ||
         p.rows * p.top_k > kRouteMaxPositions)
         return kErrArgs;
-    hipLaunchKernelGGL(route_kernel, dim3(1), dim3(256), 0, stream, p);
+    if (p.rows * p.top_k <= kRouteFusedMaxPositions) {
+        hipLaunchKernelGGL(route_kernel, dim3(1), dim3(256), 0, stream, p);
+    } else {
+        hipLaunchKernelGGL(route_select_kernel, dim3((p.rows + 3) / 4), dim3(256), 0, stream, p);
+        hipLaunchKernelGGL(route_tables_kernel, dim3(1), dim3(1024), 0, stream, p);
+    }
     return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
 }
 

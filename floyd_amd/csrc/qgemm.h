@@ -1,0 +1,97 @@
+// qgemm.h -- grouped int8-MFMA GEMM for prefill (many token rows per matrix).
+//
+// Y[m][n] = s_w[n] * sum_k W[n][k] * x[m][k] for the token rows m of a task,
+// with W in the container's q8 (int8) or q4 (nibble) packing, used as exact
+// int8 operands of v_mfma_i32_32x32x32_i8.  Activations are quantised per
+// token row into two int8 limbs, x ~= s_x * (256 * hi + lo) with
+// |256 * hi + lo| <= 2^14 (15 significant bits against the row's max), and
+// both limbs are multiplied by the same weight fragment; the int32 sums are
+// combined in fp32 in the epilogue.  The per-element rounding of x is at most
+// amax / 2^15, so outputs stay within ~1e-4 relative of the fp32 matmul of
+// moonlight_kernels.metal:62-130 while every product and sum is exact.
+//
+// A launch covers a table of independent tasks (one per active routed expert
+// plus the shared expert, or one dense matrix).  Tiles are 128 token rows x
+// 128 weight rows (SwiGLU pairs: 64 gate + 64 matching up rows, 64 outputs);
+// the tile order groups 4 row tiles of a task so that consecutive workgroups on
+// one XCD share weight tiles in that XCD's L2.
+#pragma once
+
+#include "gemv_impl.h"
+
+namespace mlh {
+
+constexpr int kQgBM = 128;  // token rows per tile
+constexpr int kQgBW = 128;  // weight rows per tile
+constexpr int kQgBK = 64;   // k per pipeline stage
+constexpr int kQgGroup = 4; // row tiles per locality group
+constexpr int kQgMaxTasks = 272;
+
+// One independent product: rows x n_out outputs, reduction length k.
+struct GemmTask {
+    const uint8_t *w = nullptr, *w2 = nullptr;  // [n_out][k] packed (w2: up rows, SwiGLU)
+    const float *s = nullptr, *s2 = nullptr;    // per weight row scales
+    int rows = 0, n_out = 0, k = 0;
+    const int8_t *a_hi = nullptr, *a_lo = nullptr;  // quantised activations, row stride a_stride
+    const float *a_scale = nullptr;
+    long a_stride = 0;
+    const int *a_rows = nullptr;  // optional: activation row of token row m
+    float *y = nullptr;           // output row m at y + m * y_stride
+    long y_stride = 0;
+    const float *resid = nullptr;  // optional residual (y = resid + product)
+    long resid_stride = 0;
+};
+
+struct QGemmLaunch {
+    const GemmTask *tasks = nullptr;  // device table (MoE); nullptr: `single`
+    const int *tile_start = nullptr;  // device [tasks + 1] tile prefix sums
+    const int *n_routed = nullptr;    // device: routed task count (shared task follows)
+    int range = 0;                    // 0 all tasks, 1 routed only, 2 shared only
+    GemmTask single;
+};
+
+// Per-row activation quantisation (optionally RMSNorm'ed first,
+// moonlight_kernels.metal:23-41): rows of `x` (stride x_stride floats) ->
+// hi/lo limbs (row stride `width` bytes) and scales.  rows_dev, when non-null,
+// holds the row count on the device (capped by rows).
+int quantize_activations(const float *x, long x_stride, int rows, int width, const float *norm_w,
+                         float eps, int8_t *hi, int8_t *lo, float *scale, hipStream_t stream);
+
+// One dense task, e.g. a prefill projection.  Epilogue: plain or residual
+// (task.resid) or SwiGLU pair (dual, task.w2 = up).
+int qgemm_single(int fmt, bool dual, const GemmTask &task, hipStream_t stream);
+
+// MoE prefill: builds the per-expert task tables from the device route tables
+// and runs both expert stages for all active experts plus the shared expert.
+struct MoeGemmParams {
+    int rows = 0, experts = 0, top_k = 0, hidden = 0, inter = 0, shared_width = 0;
+    int expert_fmt = kQ8, shared_fmt = kQ8, has_shared = 1;
+    const ExpertWeights *expert_table = nullptr;
+    const uint8_t *shared_gate = nullptr, *shared_up = nullptr, *shared_down = nullptr;
+    const float *shared_gate_s = nullptr, *shared_up_s = nullptr, *shared_down_s = nullptr;
+    const int *n_unique = nullptr, *unique = nullptr, *counts = nullptr, *offsets = nullptr;
+    const int *list_rows = nullptr;
+    const float *x = nullptr;  // residual stream [rows, hidden]
+    const float *norm_w = nullptr;
+    float eps = 1e-5f;
+    // scratch
+    int8_t *xq_hi = nullptr, *xq_lo = nullptr;  // [rows, hidden]
+    float *xq_scale = nullptr;                   // [rows]
+    int8_t *hq_hi = nullptr, *hq_lo = nullptr;  // [rows*top_k, inter]
+    float *hq_scale = nullptr;                   // [rows*top_k]
+    int8_t *sq_hi = nullptr, *sq_lo = nullptr;  // [rows, shared_width]
+    float *sq_scale = nullptr;                   // [rows]
+    GemmTask *tasks = nullptr;                   // [2][kQgMaxTasks]
+    int *tile_start = nullptr;                   // [2][kQgMaxTasks + 1]
+    // outputs (same layouts as the GEMV expert path)
+    float *expert_hidden = nullptr;  // [rows*top_k, inter]
+    float *expert_out = nullptr;     // [rows*top_k, hidden]
+    float *shared_hidden = nullptr;  // [rows, shared_width]
+    float *shared_out = nullptr;     // [rows, hidden]
+};
+int moe_gemm(const MoeGemmParams &p, hipStream_t stream);
+
+// Shapes the MFMA path takes (k a multiple of kQgBK, 16-byte aligned rows).
+bool qgemm_shape_ok(int fmt, int k);
+
+}  // namespace mlh

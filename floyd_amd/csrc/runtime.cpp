@@ -13,6 +13,7 @@
 #include "device_context.h"
 #include "mla.h"
 #include "moe.h"
+#include "qgemm.h"
 #include "../../include/moonlight_hip.h"
 #include "../../include/moonlight_hip_ext.h"
 
@@ -114,6 +115,17 @@ struct MoonlightSession {
     float *expert_hidden = nullptr, *expert_out = nullptr;
     float *shared_hidden = nullptr, *shared_out = nullptr, *dense_hidden = nullptr;
     float *moe_routed = nullptr;  // routed part of moonlight_test_moe
+    // MFMA path for batches of >= kGemmMinRows token rows (prefill)
+    int8_t *aq_hi = nullptr, *aq_lo = nullptr;  // quantised activations [max_batch][aq_width]
+    float *aq_scale = nullptr;
+    int aq_width = 0;
+    int8_t *hq_hi = nullptr, *hq_lo = nullptr;  // quantised expert hidden [max_batch*K][inter]
+    float *hq_scale = nullptr;
+    GemmTask *gemm_tasks = nullptr;
+    int *gemm_tile_start = nullptr;
+    // caller-given expert ids for the MoE test / timing hooks
+    int *fixed_ids = nullptr;
+    int fixed_rows = 0;
     // pinned host mirrors
     int *host_ids = nullptr;
     int *host_flag = nullptr;
@@ -769,8 +781,45 @@ bool to_host(MoonlightSession *s, void *dst, const void *src, size_t bytes) {
     return hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, stream_of(s)) == hipSuccess;
 }
 
+// Batches of at least this many token rows take the int8-MFMA GEMM (weights
+// read once per 128 rows) instead of the GEMV (once per 4 rows).
+constexpr int kGemmMinRows = 16;
+
+bool use_gemm(const MoonlightSession *s, int fmt, int rows, int in_w) {
+    return rows >= kGemmMinRows && s->aq_hi && in_w <= s->aq_width && qgemm_shape_ok(fmt, in_w);
+}
+
+int gemm_rows(MoonlightSession *s, const Matrix &m, const Matrix *up, const float *x, int rows,
+              int in_w, int out_w, float *y, const float *norm_w, const float *resid) {
+    hipStream_t st = stream_of(s);
+    if (int e = quantize_activations(x, in_w, rows, in_w, norm_w, s->model->cfg.rms_norm_epsilon,
+                                     s->aq_hi, s->aq_lo, s->aq_scale, st))
+        return e;
+    GemmTask t;
+    t.w = m.w;
+    t.s = m.s;
+    if (up) {
+        t.w2 = up->w;
+        t.s2 = up->s;
+    }
+    t.rows = rows;
+    t.n_out = out_w;
+    t.k = in_w;
+    t.a_hi = s->aq_hi;
+    t.a_lo = s->aq_lo;
+    t.a_scale = s->aq_scale;
+    t.a_stride = in_w;
+    t.y = y;
+    t.y_stride = out_w;
+    t.resid = resid;
+    t.resid_stride = out_w;
+    return qgemm_single(m.fmt, up != nullptr, t, st);
+}
+
 int gemv_rows(MoonlightSession *s, const Matrix &m, const float *x, int rows, int in_w,
               int out_w, float *y, const float *norm_w = nullptr, const float *resid = nullptr) {
+    if (use_gemm(s, m.fmt, rows, in_w))
+        return gemm_rows(s, m, nullptr, x, rows, in_w, out_w, y, norm_w, resid);
     GemvParams p;
     p.fmt = m.fmt;
     p.w = m.w;
@@ -792,6 +841,8 @@ int gemv_rows(MoonlightSession *s, const Matrix &m, const float *x, int rows, in
 
 int swiglu_rows(MoonlightSession *s, const Matrix &g, const Matrix &u, const float *x, int rows,
                 int in_w, int width, float *h, const float *norm_w) {
+    if (g.fmt == u.fmt && use_gemm(s, g.fmt, rows, in_w))
+        return gemm_rows(s, g, &u, x, rows, in_w, width, h, norm_w, nullptr);
     GemvParams p;
     p.fmt = g.fmt;
     p.w = g.w;
@@ -891,6 +942,7 @@ int route(MoonlightSession *s, int layer, const float *x, int rows, const float 
     r.list_slots = s->list_slots;
     r.list_pos = s->list_pos;
     r.error = s->route_error;
+    r.fixed_ids = s->fixed_rows >= rows ? s->fixed_ids : nullptr;
     return route_topk(r, stream_of(s));
 }
 
@@ -927,7 +979,56 @@ int experts(MoonlightSession *s, int layer, const float *x, int rows, const floa
     f.expert_out = s->expert_out;
     f.shared_hidden = s->shared_hidden;
     f.shared_out = s->shared_out;
-    if (int e = expert_ffn(f, stream_of(s))) return e;
+    const bool gemm = rows >= kGemmMinRows && s->hq_hi &&
+                      qgemm_shape_ok(f.expert_fmt, f.hidden) &&
+                      qgemm_shape_ok(f.expert_fmt, f.inter) &&
+                      qgemm_shape_ok(f.shared_fmt, f.hidden) &&
+                      qgemm_shape_ok(f.shared_fmt, f.shared_width) &&
+                      f.hidden <= s->aq_width && f.shared_width <= s->aq_width;
+    if (gemm) {
+        MoeGemmParams g;
+        g.rows = f.rows;
+        g.experts = f.experts;
+        g.top_k = f.top_k;
+        g.hidden = f.hidden;
+        g.inter = f.inter;
+        g.shared_width = f.shared_width;
+        g.expert_fmt = f.expert_fmt;
+        g.shared_fmt = f.shared_fmt;
+        g.has_shared = 1;
+        g.expert_table = f.expert_table;
+        g.shared_gate = f.shared_gate;
+        g.shared_up = f.shared_up;
+        g.shared_down = f.shared_down;
+        g.shared_gate_s = f.shared_gate_s;
+        g.shared_up_s = f.shared_up_s;
+        g.shared_down_s = f.shared_down_s;
+        g.n_unique = f.n_unique;
+        g.unique = f.unique;
+        g.counts = f.counts;
+        g.offsets = f.offsets;
+        g.list_rows = f.list_rows;
+        g.x = f.x;
+        g.norm_w = f.norm_w;
+        g.eps = f.eps;
+        // the token-row quantisation is consumed by stage 0 before the shared
+        // hidden is quantised into the same buffer
+        g.xq_hi = g.sq_hi = s->aq_hi;
+        g.xq_lo = g.sq_lo = s->aq_lo;
+        g.xq_scale = g.sq_scale = s->aq_scale;
+        g.hq_hi = s->hq_hi;
+        g.hq_lo = s->hq_lo;
+        g.hq_scale = s->hq_scale;
+        g.tasks = s->gemm_tasks;
+        g.tile_start = s->gemm_tile_start;
+        g.expert_hidden = f.expert_hidden;
+        g.expert_out = f.expert_out;
+        g.shared_hidden = f.shared_hidden;
+        g.shared_out = f.shared_out;
+        if (int e = moe_gemm(g, stream_of(s))) return e;
+    } else if (int e = expert_ffn(f, stream_of(s))) {
+        return e;
+    }
     CombineParams cb;
     cb.rows = rows;
     cb.hidden = c.hidden_size;
@@ -1087,11 +1188,33 @@ extern "C" int moonlight_session_create(MoonlightSession **out, MoonlightModel *
         session_alloc(s, &s->dense_hidden,
                       mb * (size_t)(c.dense_intermediate_size > 0 ? c.dense_intermediate_size : 1),
                       error, error_size) &&
+        session_alloc(s, &s->fixed_ids, mb * K, error, error_size) &&
         hipHostMalloc((void **)&s->host_ids, mb * sizeof(int), hipHostMallocDefault) ==
             hipSuccess &&
         hipHostMalloc((void **)&s->host_flag, sizeof(int), hipHostMallocDefault) == hipSuccess &&
         hipEventCreate(&s->ev_start) == hipSuccess && hipEventCreate(&s->ev_stop) == hipSuccess;
-    if (!ok) {
+    bool gemm_ok = ok;
+    if (ok && options->max_batch >= kGemmMinRows) {
+        // MFMA prefill scratch: quantised activations of the widest matmul
+        // input, quantised expert hidden rows, per-stage task tables
+        const int widths[] = {c.hidden_size, c.head_count * c.value_dim,
+                              c.dense_intermediate_size, (int)sw};
+        int aw = 0;
+        for (int w : widths) aw = w > aw ? w : aw;
+        s->aq_width = aw;
+        gemm_ok = session_alloc(s, &s->aq_hi, mb * (size_t)aw, error, error_size) &&
+                  session_alloc(s, &s->aq_lo, mb * (size_t)aw, error, error_size) &&
+                  session_alloc(s, &s->aq_scale, mb, error, error_size) &&
+                  session_alloc(s, &s->hq_hi, mb * K * (size_t)c.moe_intermediate_size, error,
+                                error_size) &&
+                  session_alloc(s, &s->hq_lo, mb * K * (size_t)c.moe_intermediate_size, error,
+                                error_size) &&
+                  session_alloc(s, &s->hq_scale, mb * K, error, error_size) &&
+                  session_alloc(s, &s->gemm_tasks, 2 * (size_t)kQgMaxTasks, error, error_size) &&
+                  session_alloc(s, &s->gemm_tile_start, 2 * (size_t)(kQgMaxTasks + 1), error,
+                                error_size);
+    }
+    if (!ok || !gemm_ok) {
         free_session(s);
         if (error && error_size && !error[0]) set_error(error, error_size, "session allocation failed");
         return 0;
@@ -1394,6 +1517,25 @@ extern "C" int moonlight_session_time_moe(MoonlightSession *s, int layer, int ro
     if (hipEventElapsedTime(&ms, s->ev_start, s->ev_stop) != hipSuccess) return 0;
     *avg_us = (double)ms * 1000.0 / iters;
     if (unique_experts) *unique_experts = s->host_ids[0];
+    return 1;
+}
+
+extern "C" int moonlight_session_fix_routes(MoonlightSession *s, const int *expert_ids,
+                                            int rows) {
+    if (!s) return 0;
+    const ModelConfig &c = s->model->cfg;
+    if (!expert_ids || rows <= 0) {
+        s->fixed_rows = 0;
+        return 1;
+    }
+    if (rows > s->options.max_batch) return 0;
+    const size_t n = (size_t)rows * c.experts_per_token;
+    for (size_t i = 0; i < n; ++i)
+        if (expert_ids[i] < 0 || expert_ids[i] >= c.expert_count) return 0;
+    if (hipMemcpy(s->fixed_ids, expert_ids, n * sizeof(int), hipMemcpyHostToDevice) !=
+        hipSuccess)
+        return 0;
+    s->fixed_rows = rows;
     return 1;
 }
 

@@ -85,6 +85,7 @@ SIGNATURES = {
     "moonlight_model_tensor_info": (C.c_int, [_vp, _cp, _vp, _vp, _vp]),
     "moonlight_session_fill_kv": (C.c_int, [_vp, C.c_int, C.c_int, C.c_uint64]),
     "moonlight_session_device_time": (C.c_int, [_vp, C.POINTER(C.c_double)]),
+    "moonlight_session_fix_routes": (C.c_int, [_vp, _vp, C.c_int]),
     "moonlight_session_time_moe": (C.c_int, [_vp, C.c_int, C.c_int, C.c_uint64, C.c_int,
                                              C.c_int, C.POINTER(C.c_double),
                                              C.POINTER(C.c_int)]),
@@ -255,6 +256,16 @@ class Session:
     def fill_kv(self, length, seed, layer=-1):
         if not lib().moonlight_session_fill_kv(self.handle, layer, length, seed):
             raise SessionError("fill_kv failed")
+
+    def fix_routes(self, ids):
+        """Expert ids [rows, top_k] used by test_moe / time_moe (None: top-k)."""
+        if ids is None:
+            ok = lib().moonlight_session_fix_routes(self.handle, None, 0)
+        else:
+            ids, p = _arr(ids, np.int32)
+            ok = lib().moonlight_session_fix_routes(self.handle, p, ids.shape[0])
+        if not ok:
+            raise SessionError("fix_routes failed")
 
     def time_moe(self, layer, rows, seed=7, warmup=5, iters=50):
         us, uniq = C.c_double(), C.c_int()

@@ -80,6 +80,15 @@ int moonlight_session_time_moe(MoonlightSession *session, int layer, int rows,
                                uint64_t seed, int warmup, int iters,
                                double *avg_us, int *unique_experts);
 
+/* Fixes the routed experts of the next moonlight_test_moe /
+ * moonlight_session_time_moe calls: token row r uses expert_ids[r * top_k ..]
+ * (moe_route_fixed semantics, moe_route.h:76-87: weights are the router's
+ * sigmoid scores of those ids, then finalised), for batches of at most `rows`
+ * rows.  expert_ids == NULL restores top-k routing.  Forward passes always
+ * route by top-k.  Returns 0 for ids out of range or rows > max_batch. */
+int moonlight_session_fix_routes(MoonlightSession *session,
+                                 const int *expert_ids, int rows);
+
 /* Device time (milliseconds, HIP events around the launches) of the last
  * prefill / append / decode of the session. */
 int moonlight_session_device_time(MoonlightSession *session, double *ms);

@@ -209,6 +209,15 @@ float orc_silu_mul(float gate, float up) {
 /* * routed_scale.                                                           */
 /* ------------------------------------------------------------------------ */
 
+/* Router score 1 / (1 + e^-x) with e^-x correctly rounded to f32 (exp in
+ * double, rounded once).  moe_route.h:12-14 calls glibc expf, which is not
+ * correctly rounded for about 0.06 % of inputs (measured over [-12, 12]):
+ * there the two scores differ by one ulp.  Selection ids are unaffected unless
+ * two selection scores tie within that ulp; weights may differ by a few ulp. */
+static float route_sigmoid(float x) {
+    return 1.0f / (1.0f + (float)exp(-(double)x));
+}
+
 void orc_route_sigmoid_topk(const float *logits, const float *bias, int rows,
                             int experts, int top_k, int normalize,
                             float routed_scale, int *ids, float *weights) {
@@ -217,7 +226,7 @@ void orc_route_sigmoid_topk(const float *logits, const float *bias, int rows,
         const float *lg = logits + (int64_t)r * experts;
         int *id = ids + (int64_t)r * top_k;
         float *wt = weights + (int64_t)r * top_k;
-        for (int e = 0; e < experts; ++e) scores[e] = 1.0f / (1.0f + expf(-lg[e]));
+        for (int e = 0; e < experts; ++e) scores[e] = route_sigmoid(lg[e]);
         for (int k = 0; k < top_k; ++k) {
             int best = -1;
             float best_value = -INFINITY;
@@ -598,12 +607,55 @@ int orc_dense_mlp(OrcModel *m, int layer, const float *x, int rows, float *out) 
     return ffn(m, prefix, x, rows, m->cfg.dense_intermediate_size, out);
 }
 
+/* moe_route_fixed + moe_route_finalize (moe_route.h:76-99) with sigmoid
+ * scores: the weights of the given ids are their unbiased scores, then
+ * /(sum + 1e-20) when normalising, then * routed_scale. */
+int orc_route_fixed(const float *logits, int rows, int experts, int top_k,
+                    int normalize, float routed_scale, const int *ids,
+                    float *weights) {
+    for (int r = 0; r < rows; ++r) {
+        const float *lg = logits + (int64_t)r * experts;
+        const int *id = ids + (int64_t)r * top_k;
+        float *wt = weights + (int64_t)r * top_k;
+        for (int k = 0; k < top_k; ++k) {
+            if (id[k] < 0 || id[k] >= experts) return 0;
+            wt[k] = route_sigmoid(lg[id[k]]);
+        }
+        float denom = 1.0f;
+        if (normalize) {
+            float sum = 0.0f;
+            for (int k = 0; k < top_k; ++k) sum += wt[k];
+            denom = sum + 1e-20f;
+        }
+        for (int k = 0; k < top_k; ++k) wt[k] = wt[k] / denom * routed_scale;
+    }
+    return 1;
+}
+
+static int moe_layer(OrcModel *m, int layer, const float *x, int rows,
+                     const int *fixed_ids, int *route_ids, float *route_weights,
+                     float *router_logits, float *routed, float *shared, float *out);
+
 /* moonlight_test_moe (moonlight_metal.m:1520-1733); routed sum in slot order
  * per row as quantized_moe_reference (tests/test_moonlight_metal_moe.c:83-149),
  * then routed + shared. */
 int orc_moe_layer(OrcModel *m, int layer, const float *x, int rows,
                   int *route_ids, float *route_weights, float *router_logits,
                   float *routed, float *shared, float *out) {
+    return moe_layer(m, layer, x, rows, NULL, route_ids, route_weights,
+                     router_logits, routed, shared, out);
+}
+
+/* The same layer with caller-given expert ids (orc_route_fixed). */
+int orc_moe_layer_fixed(OrcModel *m, int layer, const float *x, int rows,
+                        const int *fixed_ids, float *route_weights, float *out) {
+    return moe_layer(m, layer, x, rows, fixed_ids, NULL, route_weights, NULL,
+                     NULL, NULL, out);
+}
+
+static int moe_layer(OrcModel *m, int layer, const float *x, int rows,
+                     const int *fixed_ids, int *route_ids, float *route_weights,
+                     float *router_logits, float *routed, float *shared, float *out) {
     const OrcConfig *c = &m->cfg;
     char name[512];
     OrcMatrix router;
@@ -622,8 +674,13 @@ int orc_moe_layer(OrcModel *m, int layer, const float *x, int rows,
     float *y = malloc((size_t)H * sizeof(float));
     int ok = 1;
     mm(&router, x, logits, rows, H, E);
-    orc_route_sigmoid_topk(logits, bias, rows, E, K, c->normalize_topk,
-                           c->routed_scale, ids, wts);
+    if (fixed_ids) {
+        memcpy(ids, fixed_ids, (size_t)rows * K * sizeof(int));
+        ok = orc_route_fixed(logits, rows, E, K, c->normalize_topk, c->routed_scale, ids, wts);
+    } else {
+        orc_route_sigmoid_topk(logits, bias, rows, E, K, c->normalize_topk,
+                               c->routed_scale, ids, wts);
+    }
     memset(rt, 0, (size_t)rows * H * sizeof(float));
     for (int r = 0; r < rows && ok; ++r) {
         for (int k = 0; k < K && ok; ++k) {

@@ -17,14 +17,20 @@
  *       closed-form special cases (zero rows, amax element, odd width, ties).
  *   orc_matmul_*   : f64 brute force (tests/test_backend_metal.c:9-33 method),
  *                    closed forms (unit-vector input, constant input).
- *   orc_route_*    : moe_route.h compiled from the reference (oracle/_ref) and
- *                    the closed-form cases of tests/test_moe_route.c:16-112.
+ *   orc_route_*    : moe_route.h compiled from the reference (oracle/_ref):
+ *                    ids bit-exact, weights within 4 ulp (the reference twin's
+ *                    glibc expf is not correctly rounded for ~0.06 % of inputs,
+ *                    the oracle's score is); the closed-form cases of
+ *                    tests/test_moe_route.c:16-112; the score itself against
+ *                    numpy's f64 exp rounded to f32.
  *   orc_route_tables : brute force on tiny inputs (first-appearance order).
  *   orc_rmsnorm / orc_rope / orc_cache_append : closed forms (unit weight,
  *                    position 0 identity, rotation norm preservation).
  *   orc_mla_attention : explicit decompression K=W_UK lat, V=W_UV lat and
  *                    textbook softmax in f64 (algebraic identity), single-key
  *                    and shift-invariance cases.
+ *   orc_route_fixed : moe_route_fixed + moe_route_finalize compiled from the
+ *                    reference (oracle/_ref), weights within 4 ulp as above.
  *   orc_moe_layer / orc_dense_mlp : moe_exec.h compiled from the reference
  *                    (f32 SwiGLU MoE) on dequantised weights.
  *   orc_forward    : composition of the above; split prefill+append equals full
@@ -120,6 +126,11 @@ int orc_named_matmul(const OrcModel *model, const char *name, const float *x,
 int orc_attention(OrcModel *model, int layer, const float *x, int rows,
                   int position, float *out);
 /* moonlight_test_moe (moonlight_metal.m:1520-1733) semantics. */
+int orc_route_fixed(const float *logits, int rows, int experts, int top_k,
+                    int normalize, float routed_scale, const int *ids,
+                    float *weights);
+int orc_moe_layer_fixed(OrcModel *model, int layer, const float *x, int rows,
+                        const int *fixed_ids, float *route_weights, float *out);
 int orc_moe_layer(OrcModel *model, int layer, const float *x, int rows,
                   int *route_ids, float *route_weights, float *router_logits,
                   float *routed, float *shared, float *out);

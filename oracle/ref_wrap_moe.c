@@ -29,6 +29,15 @@ void ref_route_finalize(float *weights, int count, int normalize, float scale) {
     moe_route_finalize(weights, count, normalize, scale);
 }
 
+static int forward_flat(int hidden, int intermediate, int experts, int top_k,
+                        int normalize, float route_scale, float swiglu_limit,
+                        const float *router, const float *bias,
+                        const float *gate, const float *up, const float *down,
+                        int n_shared, const float *shared_gate,
+                        const float *shared_up, const float *shared_down,
+                        const float *input, int tokens, const int64_t *fixed,
+                        float *output);
+
 /* moe_f32_forward over flat arrays: gate/up [E][I][H], down [E][H][I];
  * shared experts likewise with n_shared entries of width I. */
 int ref_moe_forward_flat(int hidden, int intermediate, int experts, int top_k,
@@ -38,6 +47,33 @@ int ref_moe_forward_flat(int hidden, int intermediate, int experts, int top_k,
                          int n_shared, const float *shared_gate,
                          const float *shared_up, const float *shared_down,
                          const float *input, int tokens, float *output) {
+    return forward_flat(hidden, intermediate, experts, top_k, normalize, route_scale,
+                        swiglu_limit, router, bias, gate, up, down, n_shared, shared_gate,
+                        shared_up, shared_down, input, tokens, NULL, output);
+}
+
+/* The same with fixed experts per token row (moe_f32_forward's fixed_experts
+ * path: token t uses fixed[t * top_k ...]). */
+int ref_moe_forward_fixed_flat(int hidden, int intermediate, int experts, int top_k,
+                               int normalize, float route_scale, const float *router,
+                               const float *gate, const float *up, const float *down,
+                               int n_shared, const float *shared_gate,
+                               const float *shared_up, const float *shared_down,
+                               const float *input, int tokens, const int64_t *fixed,
+                               float *output) {
+    return forward_flat(hidden, intermediate, experts, top_k, normalize, route_scale, 0.0f,
+                        router, NULL, gate, up, down, n_shared, shared_gate, shared_up,
+                        shared_down, input, tokens, fixed, output);
+}
+
+static int forward_flat(int hidden, int intermediate, int experts, int top_k,
+                        int normalize, float route_scale, float swiglu_limit,
+                        const float *router, const float *bias,
+                        const float *gate, const float *up, const float *down,
+                        int n_shared, const float *shared_gate,
+                        const float *shared_up, const float *shared_down,
+                        const float *input, int tokens, const int64_t *fixed,
+                        float *output) {
     size_t mat = (size_t)intermediate * hidden;
     MoeExpertF32 *routed = calloc((size_t)experts, sizeof(*routed));
     MoeExpertF32 *shared = calloc((size_t)(n_shared > 0 ? n_shared : 1), sizeof(*shared));
@@ -65,7 +101,15 @@ int ref_moe_forward_flat(int hidden, int intermediate, int experts, int top_k,
     model.experts = routed;
     model.shared_experts = n_shared > 0 ? shared : NULL;
     model.n_shared_experts = n_shared;
-    int ok = moe_f32_forward(&model, input, NULL, tokens, output);
+    int *token_ids = NULL;
+    if (fixed) {
+        token_ids = malloc((size_t)tokens * sizeof(int));
+        for (int t = 0; t < tokens; ++t) token_ids[t] = t;
+        model.fixed_experts = fixed;
+        model.vocab_size = tokens;
+    }
+    int ok = moe_f32_forward(&model, input, token_ids, tokens, output);
+    free(token_ids);
     free(routed);
     free(shared);
     return ok;

@@ -103,6 +103,10 @@ def lib():
                                     ctypes.c_int, _f32p]
         L.orc_moe_layer.argtypes = [ctypes.c_void_p, ctypes.c_int, _f32p, ctypes.c_int,
                                     _i32p, _f32p, _f32p, _f32p, _f32p, _f32p]
+        L.orc_route_fixed.argtypes = [_f32p, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                      ctypes.c_int, ctypes.c_float, _i32p, _f32p]
+        L.orc_moe_layer_fixed.argtypes = [ctypes.c_void_p, ctypes.c_int, _f32p, ctypes.c_int,
+                                          _i32p, _f32p, _f32p]
         L.orc_dense_mlp.argtypes = [ctypes.c_void_p, ctypes.c_int, _f32p, ctypes.c_int,
                                     _f32p]
         L.orc_forward.argtypes = [ctypes.c_void_p, _i32p, ctypes.c_int, ctypes.c_int,
@@ -193,3 +197,18 @@ class Model:
 
     def __del__(self):
         self.close()
+
+
+def zipf_routes(rows, experts, top_k, seed, s=1.1):
+    """Expert ids [rows, top_k]: per row top_k distinct experts drawn without
+    replacement with p_e proportional to (rank_e + 1)^-s over a seeded
+    permutation of the expert ids (the skewed prefill routing of the MoE
+    prefill benchmark)."""
+    rng = np.random.default_rng(seed)
+    perm = rng.permutation(experts)
+    p = np.empty(experts)
+    p[perm] = (np.arange(experts) + 1.0) ** -s
+    p /= p.sum()
+    return np.stack([rng.choice(experts, top_k, replace=False, p=p)
+                     for _ in range(rows)]).astype(np.int32)
+

@@ -28,7 +28,7 @@ def make_weights(fmt, out_width, in_width, seed):
 
 
 SHAPES = [
-    # (fmt, out, in, rows): BASELINE configs 0-1 and the Moonlight decode shapes
+    # (fmt, out, in, rows): benchmark configs 0-1 and the Moonlight decode shapes
     (1, 11264, 2048, 1), (1, 11264, 2048, 4), (2, 11264, 2048, 1), (2, 2048, 11264, 1),
     (1, 2048, 11264, 1), (1, 3072, 2048, 1), (1, 576, 2048, 2), (1, 2048, 1408, 1),
     (1, 2048, 2816, 3), (2, 1408, 2048, 1), (2, 2048, 1408, 1), (1, 128, 512, 1),

@@ -1,4 +1,4 @@
-"""Parity at the real Moonlight-16B-A3B shapes (BASELINE configs 2 and 4) on a
+"""Parity at the real Moonlight-16B-A3B shapes (benchmark configs 2 and 4) on a
 synthetic q8 model generated in HBM (moonlight_model_create_synthetic): the
 oracle reads the very same packed weights back from the device.
 
@@ -77,8 +77,12 @@ def test_moe_decode(moon, rows):
     assert rel_l2(got["logits"], e_logits) < 1e-5
     same = np.array([set(a) == set(b) for a, b in zip(got["ids"], e_ids)])
     assert same.all(), np.nonzero(~same)
+    # fp32 GEMV below 16 rows; from 16 rows the int8-limb MFMA GEMM (~2e-4)
+    tol = 1e-4 if rows < 16 else 1e-3
     for k in ("routed", "shared", "out"):
-        assert rel_l2(got[k], e[k]) < 1e-4, k
+        err = rel_l2(got[k], e[k])
+        print(f"[gpu] rows={rows} {k} rel-L2 {err:.2e}", flush=True)
+        assert err < tol, k
     sess.close()
     orc.close()
 

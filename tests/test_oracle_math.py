@@ -118,6 +118,23 @@ def test_route_kats_of_reference_tests():
 REF_MOE = os.path.join(O.REF_DIR, "libref_moe.so")
 
 
+def ulp_diff(a, b):
+    a = np.asarray(a, np.float32).view(np.int32).astype(np.int64)
+    b = np.asarray(b, np.float32).view(np.int32).astype(np.int64)
+    return int(np.max(np.abs(a - b))) if a.size else 0
+
+
+def test_route_score_is_correctly_rounded_sigmoid():
+    """K = 1, no normalisation, scale 1: the weight is the score itself,
+    1 / (1 + e^-x) with e^-x rounded once to f32 (numpy's f64 exp)."""
+    rng = np.random.default_rng(13)
+    x = rng.normal(0, 4.0, (4000, 1)).astype(np.float32)
+    ids, w = O.route(x, np.zeros(1, np.float32), 1, normalize=0, scale=1.0)
+    e = np.exp(-x.astype(np.float64)).astype(np.float32)
+    expect = np.float32(1.0) / (np.float32(1.0) + e)
+    assert (ids == 0).all() and np.array_equal(w.view(np.uint32), expect.view(np.uint32))
+
+
 @pytest.mark.skipif(not os.path.exists(REF_MOE), reason="oracle/_ref not built")
 def test_route_bit_exact_with_reference_moe_route_h():
     ref = ctypes.CDLL(REF_MOE)
@@ -140,7 +157,9 @@ def test_route_bit_exact_with_reference_moe_route_h():
                                            ctypes.c_int, ctypes.c_float]
         ref.ref_route_finalize(O.fptr(wt), n, 1, ctypes.c_float(2.446))
         assert np.array_equal(ids[r], ind), r
-        assert np.array_equal(w[r].view(np.uint32), wt.view(np.uint32)), r
+        # glibc expf (the reference twin) is not correctly rounded for ~0.06 %
+        # of inputs; the oracle's score is: weights agree to a few ulp
+        assert ulp_diff(w[r], wt) <= 4, r
 
 
 def test_route_tables_first_appearance_order():
@@ -167,3 +186,36 @@ def test_route_tables_bruteforce_random():
             pos = [(p // top_k, p % top_k) for p in range(flat.size) if flat[p] == e]
             assert counts[e] == len(pos)
             assert [(er[e * rows + j], es[e * rows + j]) for j in range(len(pos))] == pos
+
+
+@pytest.mark.skipif(not os.path.exists(REF_MOE), reason="oracle/_ref not built")
+def test_route_fixed_bit_exact_with_reference():
+    ref = ctypes.CDLL(REF_MOE)
+    ref.ref_route_finalize.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_int,
+                                       ctypes.c_int, ctypes.c_float]
+    rng = np.random.default_rng(12)
+    experts, top_k, rows = 64, 6, 300
+    logits = rng.normal(0, 2.0, (rows, experts)).astype(np.float32)
+    ids = O.zipf_routes(rows, experts, top_k, seed=5)
+    w = np.empty((rows, top_k), np.float32)
+    assert O.lib().orc_route_fixed(O.fptr(logits), rows, experts, top_k, 1, 2.446, O.iptr(ids),
+                                   O.fptr(w))
+    for r in range(rows):
+        wt = np.zeros(top_k, np.float32)
+        sc = np.zeros(experts, np.float32)
+        n = ref.ref_route_fixed(O.fptr(logits[r].copy()), experts, O.iptr(ids[r].copy()), top_k,
+                                1, O.fptr(wt), O.fptr(sc))
+        assert n == top_k
+        ref.ref_route_finalize(O.fptr(wt), n, 1, ctypes.c_float(2.446))
+        assert ulp_diff(w[r], wt) <= 4, r
+    bad = ids.copy()
+    bad[3, 2] = experts
+    assert not O.lib().orc_route_fixed(O.fptr(logits), rows, experts, top_k, 1, 2.446,
+                                       O.iptr(bad), O.fptr(w))
+
+
+def test_zipf_routes_are_distinct_and_skewed():
+    ids = O.zipf_routes(2048, 64, 6, seed=3)
+    assert all(len(set(r)) == 6 for r in ids)
+    counts = np.bincount(ids.ravel(), minlength=64)
+    assert counts.sum() == 2048 * 6 and counts.max() > 10 * counts.min()

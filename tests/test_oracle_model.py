@@ -208,6 +208,44 @@ def test_moe_layer_equals_reference_moe_exec(tiny):
     m.close()
 
 
+@pytest.mark.skipif(not os.path.exists(REF_MOE), reason="oracle/_ref not built")
+def test_moe_layer_fixed_equals_reference_moe_exec(tiny):
+    cfg, layer, rows = TINY, 3, 9
+    H, E, I, K = 256, 64, 64, 6
+    m = oracle_model(cfg, tiny, 4)
+    x = O.fill_normal(rows * H, 61).reshape(rows, H)
+    ids = O.zipf_routes(rows, E, K, seed=8)
+    out = np.empty_like(x)
+    w = np.empty((rows, K), np.float32)
+    assert O.lib().orc_moe_layer_fixed(m.handle, layer, O.fptr(x), rows, O.iptr(ids), O.fptr(w),
+                                       O.fptr(out))
+    p = f"model.layers.{layer}.mlp."
+
+    def f32(name, r, c):
+        return np.ascontiguousarray(dequant(tiny, name, r, c), np.float32)
+
+    gate = np.stack([f32(p + f"experts.{e}.gate_proj.weight", I, H) for e in range(E)])
+    up = np.stack([f32(p + f"experts.{e}.up_proj.weight", I, H) for e in range(E)])
+    down = np.stack([f32(p + f"experts.{e}.down_proj.weight", H, I) for e in range(E)])
+    sg = f32(p + "shared_experts.gate_proj.weight", 2 * I, H).reshape(2, I, H)
+    su = f32(p + "shared_experts.up_proj.weight", 2 * I, H).reshape(2, I, H)
+    sd_full = f32(p + "shared_experts.down_proj.weight", H, 2 * I)
+    sd = np.ascontiguousarray(np.stack([sd_full[:, :I], sd_full[:, I:]]))
+    router = np.ascontiguousarray(tiny[p + "gate.weight"])
+    fixed = np.ascontiguousarray(ids.astype(np.int64))
+    ref = ctypes.CDLL(REF_MOE)
+    fp = ctypes.POINTER(ctypes.c_float)
+    ref.ref_moe_forward_fixed_flat.argtypes = [ctypes.c_int] * 5 + [ctypes.c_float] + \
+        [fp] * 4 + [ctypes.c_int] + [fp] * 4 + [ctypes.c_int, ctypes.c_void_p, fp]
+    expect = np.empty_like(x)
+    assert ref.ref_moe_forward_fixed_flat(H, I, E, K, 1, 2.446, O.fptr(router), O.fptr(gate),
+                                          O.fptr(up), O.fptr(down), 2, O.fptr(sg), O.fptr(su),
+                                          O.fptr(sd), O.fptr(x), rows, fixed.ctypes.data,
+                                          O.fptr(expect))
+    assert rel_l2(out, expect) < 1e-5
+    m.close()
+
+
 def test_forward_split_prefill_equals_full(tiny):
     ids = np.array([5, 77, 300, 12, 511, 0], np.int32)
     L, H, V = TINY["layer_count"], 256, 512

@@ -1,0 +1,140 @@
+"""GPU parity of the prefill path: batches of >= 16 token rows run every q8/q4
+matmul on the int8-limb MFMA GEMM (floyd_amd/csrc/qgemm.hip) and route
+through the multi-workgroup routing kernels when rows * top_k > 1024.
+
+  test_tiny_moe_gemm         one MoE layer at 40 and 200 rows, top-k routing,
+                             three format mixes (tests/test_moonlight_metal_moe.c
+                             semantics)
+  test_tiny_prefill_gemm     a 40-token prefill through every GEMM path (q/kv_a,
+                             o_proj, dense SwiGLU + down, experts) vs orc_forward
+  test_moonlight_moe_fixed   the Moonlight MoE layer (config 3 shape) with Zipf
+                             routes fixed per token (moe_route_fixed), q8 and q4,
+                             T = 512 and the full T = 2048
+
+Tolerance: rel-L2 <= 1e-3 against the fp32 oracle;
+the limb quantisation keeps the measured error near 1e-4.
+"""
+import numpy as np
+import pytest
+
+import container_util as CU
+import oracle_lib as O
+from conftest import rel_l2
+from floyd_amd import session as S
+from test_moonlight_scale_gpu import MOON, moe_layer_names, oracle_with
+
+pytestmark = pytest.mark.gpu
+
+FORMATS = [(8, 8), (4, 4), (4, 8)]
+
+
+@pytest.fixture(scope="module", params=FORMATS, ids=lambda p: f"e{p[0]}d{p[1]}")
+def tiny(request, tmp_path_factory, device):
+    ebits, dbits = request.param
+    cfg = dict(CU.TINY)
+    tensors = CU.build_tensors(cfg, ebits=ebits, dbits=dbits, seed=777 + ebits * 10 + dbits)
+    path = CU.write_container(str(tmp_path_factory.mktemp(f"pf_e{ebits}d{dbits}")), cfg, tensors)
+    model = S.Model.open(path)
+    yield cfg, tensors, model
+    model.close()
+
+
+@pytest.mark.parametrize("rows", [40, 200])
+def test_tiny_moe_gemm(tiny, rows):
+    cfg, tensors, model = tiny
+    print(f"[gpu] tiny MoE GEMM rows={rows}", flush=True)
+    x = O.fill_normal(rows * 256, 90 + rows).reshape(rows, 256)
+    sess = S.Session(model, 256, 256)
+    got = sess.test_moe(2, x)
+    assert got is not None
+    bias = tensors["model.layers.2.mlp.gate.e_score_correction_bias"]
+    ids, w = O.route(got["logits"], bias, 6, 1, 2.446)
+    assert np.array_equal(got["ids"], ids)
+    assert np.array_equal(got["weights"].view(np.uint32), w.view(np.uint32))
+    orc = CU.oracle_model(cfg, tensors, 8)
+    e = {k: np.empty_like(x) for k in ("routed", "shared", "out")}
+    e_ids = np.empty((rows, 6), np.int32)
+    e_w = np.empty((rows, 6), np.float32)
+    e_logits = np.empty((rows, 64), np.float32)
+    assert O.lib().orc_moe_layer(orc.handle, 2, O.fptr(x), rows, O.iptr(e_ids), O.fptr(e_w),
+                                 O.fptr(e_logits), O.fptr(e["routed"]), O.fptr(e["shared"]),
+                                 O.fptr(e["out"]))
+    assert np.array_equal(got["ids"], e_ids)
+    errs = {k: rel_l2(got[k], e[k]) for k in e}
+    print(f"[gpu] rel-L2 {errs}", flush=True)
+    for k, v in errs.items():
+        assert v < 1e-3, k
+    sess.close()
+    orc.close()
+
+
+def test_tiny_prefill_gemm(tiny):
+    cfg, tensors, model = tiny
+    ids = np.random.default_rng(21).integers(0, cfg["vocab_size"], 40).astype(np.int32)
+    print("[gpu] tiny 40-token prefill on the GEMM path", flush=True)
+    orc = CU.oracle_model(cfg, tensors, 64)
+    L = cfg["layer_count"]
+    e_layers = np.empty((L, 40, 256), np.float32)
+    e_trace = np.full((L, 40, 6), -1, np.int32)
+    e_logits = np.empty(cfg["vocab_size"], np.float32)
+    assert O.lib().orc_forward(orc.handle, O.iptr(ids), 40, 0, O.fptr(e_layers),
+                               O.iptr(e_trace), O.fptr(e_logits))
+    sess = S.Session(model, 64, 64)
+    layers, logits = sess.prefill_layers(ids)
+    for l in range(L):
+        err = rel_l2(layers[l], e_layers[l])
+        print(f"[gpu] layer {l} rel-L2 {err:.2e}", flush=True)
+        assert err < 1e-3, l
+    for l in range(cfg["first_dense_layer_count"], L):
+        routes = sess.test_copy_routes(l, 40)
+        same = [set(routes[r]) == set(e_trace[l, r]) for r in range(40)]
+        assert all(same), (l, same.index(False))
+    assert rel_l2(logits, e_logits) < 1e-3
+    assert int(np.argmax(logits)) == int(np.argmax(e_logits))
+    # decode after a GEMM prefill continues from the same caches
+    greedy = int(np.argmax(e_logits))
+    dec = sess.decode(greedy)
+    e_dec = np.empty_like(e_logits)
+    assert O.lib().orc_forward(orc.handle, O.iptr(np.array([greedy], np.int32)), 1, 40, None,
+                               None, O.fptr(e_dec))
+    assert rel_l2(dec, e_dec) < 1e-3
+    sess.close()
+    orc.close()
+
+
+@pytest.fixture(scope="module", params=[8, 4], ids=["q8", "q4"])
+def moon(request, device):
+    bits = request.param
+    print(f"[gpu] building the synthetic Moonlight model, experts and dense at {bits} bits",
+          flush=True)
+    model = S.Model.synthetic(expert_bits=bits, dense_bits=bits)
+    O.lib().orc_set_threads(16)
+    yield model
+    model.close()
+
+
+@pytest.mark.parametrize("rows", [512, 2048])
+def test_moonlight_moe_fixed(moon, rows):
+    print(f"[gpu] Moonlight MoE layer, Zipf routes, T={rows}", flush=True)
+    ids = O.zipf_routes(rows, 64, 6, seed=1100 + rows)
+    x = O.fill_normal(rows * 2048, 300 + rows).reshape(rows, 2048)
+    sess = S.Session(moon, rows, rows)
+    sess.fix_routes(ids)
+    got = sess.test_moe(1, x)
+    assert got is not None
+    assert np.array_equal(got["ids"], ids)
+    w = np.empty((rows, 6), np.float32)
+    assert O.lib().orc_route_fixed(O.fptr(got["logits"]), rows, 64, 6, 1, 2.446, O.iptr(ids),
+                                   O.fptr(w))
+    assert np.array_equal(got["weights"].view(np.uint32), w.view(np.uint32))
+    orc = oracle_with(moon, moe_layer_names(1), 8)
+    expect = np.empty_like(x)
+    e_w = np.empty((rows, 6), np.float32)
+    assert O.lib().orc_moe_layer_fixed(orc.handle, 1, O.fptr(x), rows, O.iptr(ids),
+                                       O.fptr(e_w), O.fptr(expect))
+    err = rel_l2(got["out"], expect)
+    print(f"[gpu] T={rows} out rel-L2 {err:.2e}", flush=True)
+    assert err < 1e-3
+    sess.fix_routes(None)
+    sess.close()
+    orc.close()
