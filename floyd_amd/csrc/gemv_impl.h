@@ -142,9 +142,19 @@ __device__ __forceinline__ void gemv_block(const GemvJob<B> job) {
         for (int b = 0; b < B; ++b) {
             float ss = 0.0f;
             if (b < job.rows) {
-                for (int i = lane * 4; i < job.I; i += kWave * 4) {
-                    f32x4 v = load_f4(job.x[b] + i);
-                    ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+                // loads in batches of 8 issued before their use: a load-use
+                // chain per iteration would serialise the L2 latency
+                for (int i0 = lane * 4; i0 < job.I; i0 += kWave * 4 * 8) {
+                    f32x4 v[8];
+#pragma unroll
+                    for (int u = 0; u < 8; ++u) {
+                        const int i = i0 + kWave * 4 * u;
+                        v[u] = i < job.I ? load_f4(job.x[b] + i) : f32x4{0.f, 0.f, 0.f, 0.f};
+                    }
+#pragma unroll
+                    for (int u = 0; u < 8; ++u)
+                        ss += v[u].x * v[u].x + v[u].y * v[u].y + v[u].z * v[u].z +
+                              v[u].w * v[u].w;
                 }
             }
             ss = wave_sum(ss);

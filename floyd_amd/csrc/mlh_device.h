@@ -18,6 +18,24 @@ __device__ __forceinline__ u32x4 load_stream16(const void *p) {
     return __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p));
 }
 
+// 16-byte load through the global address space.  Pointers that reach a
+// kernel through a table in memory are generic; a generic (flat) load also
+// counts against the LDS wait counter, so a wait for LDS reads would wait for
+// every outstanding flat load as well.
+__device__ __forceinline__ u32x4 load_global16(const void *p) {
+    return *(const __attribute__((address_space(1))) u32x4 *)(p);
+}
+
+__device__ __forceinline__ float load_global_f32(const float *p) {
+    return *(const __attribute__((address_space(1))) float *)(p);
+}
+
+// 4-byte store through the global address space (a flat store would also
+// count against the LDS wait counter, see load_global16).
+__device__ __forceinline__ void store_global(float *p, float v) {
+    *(__attribute__((address_space(1))) float *)(p) = v;
+}
+
 __device__ __forceinline__ f32x4 load_f4(const float *p) {
     return *reinterpret_cast<const f32x4 *>(p);
 }

@@ -28,6 +28,11 @@ struct RouteParams {
 };
 int route_topk(const RouteParams &p, hipStream_t stream);
 
+// f32 router logits of many token rows, x RMSNorm'ed with norm_w when it is
+// non-null: logits [rows, experts].
+int router_logits(const float *x, const float *norm_w, float eps, const float *w, int rows,
+                  int experts, int width, float *logits, hipStream_t stream);
+
 struct CombineParams {
     int rows = 0, hidden = 0, top_k = 0;
     const float *weights = nullptr;     // [rows, top_k]

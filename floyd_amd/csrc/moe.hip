@@ -259,82 +259,121 @@ __global__ __launch_bounds__(256) void route_select_kernel(RouteParams p) {
 }
 
 // ... then the tables in one workgroup of 16 waves.  List order within an
-// expert is (row, slot) order: each wave owns a contiguous block of rows,
-// counts its entries per expert, and after a scan over the waves walks its
-// rows in order with private per-expert cursors (the experts of one row are
-// distinct, so the lanes of a row never share a cursor).
+// expert is (row, slot) order, and the experts of one row are distinct (top-k
+// selection; fixed routes are checked on the host), so the list entry of
+// (row r, expert e) is offsets[e] + the number of earlier rows that route to
+// e.  Rows are taken in chunks of 64 (one per lane): a ballot per (chunk,
+// expert) gives the rows of the chunk that use e.  From these masks come the
+// counts (popcounts), the first appearance (first set bit, then the slot in
+// that row), the first-appearance ranks (experts that appear earlier) and,
+// after a scan over the chunks, the list entries -- no atomics and no serial
+// pass over the positions.
 constexpr int kTableWaves = 16;
+constexpr int kTableMasks = 2048;  // (row chunks) x experts held in LDS
 __global__ __launch_bounds__(1024) void route_tables_kernel(RouteParams p) {
     __shared__ int first_pos[kMaxExperts];
     __shared__ int counts[kMaxExperts];
     __shared__ int offsets[kMaxExperts];
-    __shared__ unsigned long long first_mask[kRouteMaxPositions / 64];
-    __shared__ int word_prefix[kRouteMaxPositions / 64];
     __shared__ int rank_of[kMaxExperts], count_by_rank[kMaxExperts], offset_by_rank[kMaxExperts];
-    __shared__ int cursor[kTableWaves][kMaxExperts];
+    __shared__ unsigned long long row_mask[kTableMasks];  // [chunk][expert of the group]
+    __shared__ int before[kTableMasks];                   // [chunk][expert of the group]
+    __shared__ unsigned char ids8[kRouteMaxPositions];
+    __shared__ unsigned long long bad_mask[kRouteMaxPositions / 64];
     __shared__ int unique_total;
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
     const int E = p.experts, K = p.top_k, M = p.rows;
     const int n_pos = M * K;
-    for (int e = tid; e < E; e += blockDim.x) {
-        first_pos[e] = INT_MAX;
-        counts[e] = 0;
-    }
-    for (int i = tid; i < kTableWaves * kMaxExperts; i += blockDim.x) (&cursor[0][0])[i] = 0;
-    __syncthreads();
-    const int rows_per_wave = (M + kTableWaves - 1) / kTableWaves;
-    const int r_begin = wave * rows_per_wave;
-    const int r_end = min(M, r_begin + rows_per_wave);
-    for (int q = tid; q < n_pos; q += blockDim.x) {
-        const int e = p.ids[q];
-        if (e < 0 || e >= E) {
-            p.list_pos[q] = -1;
-            *p.error = 1;  // prepare_route_tables rejects such ids (moonlight_metal.m:545)
-            continue;
-        }
-        atomicMin(&first_pos[e], q);
-        atomicAdd(&counts[e], 1);
-    }
-    for (int q = r_begin * K + lane; q < r_end * K; q += 64) {
-        const int e = p.ids[q];
-        if (e >= 0 && e < E) atomicAdd(&cursor[wave][e], 1);
-    }
-    __syncthreads();
+    const int nchunks = (M + 63) / 64;
     const int nwords = (n_pos + 63) / 64;
-    for (int w = wave; w < nwords; w += kTableWaves) {
-        const int q = w * 64 + lane;
-        bool first = false;
-        if (q < n_pos) {
-            const int e = p.ids[q];
-            first = e >= 0 && e < E && first_pos[e] == q;
+    // ids in batches of 16 words per wave (loads issued before their use)
+    for (int w0 = wave; w0 < nwords; w0 += kTableWaves * 16) {
+        int ev[16];
+#pragma unroll
+        for (int b = 0; b < 16; ++b) {
+            const int q = (w0 + kTableWaves * b) * 64 + lane;
+            ev[b] = q < n_pos ? p.ids[q] : 0;
         }
-        const unsigned long long m = __ballot(first);
-        if (lane == 0) first_mask[w] = m;
+#pragma unroll
+        for (int b = 0; b < 16; ++b) {
+            const int w = w0 + kTableWaves * b;
+            if (w >= nwords) break;
+            const int q = w * 64 + lane;
+            bool bad = false;
+            if (q < n_pos) {
+                bad = ev[b] < 0 || ev[b] >= E;
+                ids8[q] = (unsigned char)(bad ? 0 : ev[b]);
+                if (bad) p.list_pos[q] = -1;
+            }
+            const unsigned long long m = __ballot(bad);
+            if (lane == 0) {
+                bad_mask[w] = m;
+                if (m) *p.error = 1;  // prepare_route_tables rejects such ids (moonlight_metal.m:545)
+            }
+        }
     }
     __syncthreads();
-    if (tid == 0) {
-        int acc = 0;
-        for (int w = 0; w < nwords; ++w) {
-            word_prefix[w] = acc;
-            acc += __popcll(first_mask[w]);
+    auto id_at = [&](int q) -> int {
+        return ((bad_mask[q >> 6] >> (q & 63)) & 1ull) ? -1 : (int)ids8[q];
+    };
+    // masks of the experts e0 .. e0 + ne - 1 for every row chunk
+    auto build_masks = [&](int e0, int ne) {
+        for (int c = wave; c < nchunks; c += kTableWaves) {
+            const int r = c * 64 + lane;
+            int ids[kMaxTopK];
+#pragma unroll
+            for (int k = 0; k < kMaxTopK; ++k) ids[k] = (k < K && r < M) ? id_at(r * K + k) : -1;
+            for (int ei = 0; ei < ne; ++ei) {
+                bool has = false;
+#pragma unroll
+                for (int k = 0; k < kMaxTopK; ++k) has |= ids[k] == e0 + ei;
+                const unsigned long long m = __ballot(has);
+                if (lane == 0) row_mask[c * ne + ei] = m;
+            }
         }
-        unique_total = acc;
-        *p.n_unique = acc;
+    };
+    const int group = max(1, kTableMasks / nchunks);
+    const bool one_group = group >= E;
+    // ---- counts and first appearance (position index row * K + slot)
+    for (int e0 = 0; e0 < E; e0 += group) {
+        const int ne = min(group, E - e0);
+        __syncthreads();
+        build_masks(e0, ne);
+        __syncthreads();
+        for (int ei = tid; ei < ne; ei += blockDim.x) {
+            int cnt = 0, first = INT_MAX;
+            for (int c = 0; c < nchunks; ++c) {
+                const unsigned long long m = row_mask[c * ne + ei];
+                if (m && first == INT_MAX) {
+                    const int r = c * 64 + __ffsll((long long)m) - 1;
+                    for (int k = 0; k < K; ++k)
+                        if (id_at(r * K + k) == e0 + ei) first = r * K + k;
+                }
+                cnt += __popcll(m);
+            }
+            counts[e0 + ei] = cnt;
+            first_pos[e0 + ei] = first;
+        }
     }
     __syncthreads();
+    // ---- ranks in first-appearance order
     for (int e = tid; e < E; e += blockDim.x) {
         rank_of[e] = -1;
         if (counts[e] > 0) {
-            const int q = first_pos[e];
-            const int rank = word_prefix[q / 64] +
-                             __popcll(first_mask[q / 64] & ((1ull << (q % 64)) - 1ull));
+            int rank = 0;
+            for (int o = 0; o < E; ++o) rank += counts[o] > 0 && first_pos[o] < first_pos[e];
             rank_of[e] = rank;
             count_by_rank[rank] = counts[e];
             p.unique[rank] = e;
         }
         p.counts[e] = counts[e];
+    }
+    if (tid == 0) {
+        int n = 0;
+        for (int e = 0; e < E; ++e) n += counts[e] > 0;
+        unique_total = n;
+        *p.n_unique = n;
     }
     __syncthreads();
     if (wave == 0) {  // exclusive scan of the counts in rank order (<= 256 ranks)
@@ -365,28 +404,145 @@ __global__ __launch_bounds__(1024) void route_tables_kernel(RouteParams p) {
         if (rank_of[e] >= 0) {
             offsets[e] = offset_by_rank[rank_of[e]];
             p.offsets[e] = offsets[e];
-            int run = offsets[e];  // per-wave starting cursors, waves in row order
-            for (int w = 0; w < kTableWaves; ++w) {
-                const int c = cursor[w][e];
-                cursor[w][e] = run;
-                run += c;
-            }
         }
     }
-    __syncthreads();
-    for (int r = r_begin; r < r_end; ++r) {
-        if (lane < K) {
-            const int q = r * K + lane;
-            const int e = p.ids[q];
-            if (e >= 0 && e < E) {
-                const int j = cursor[wave][e];
-                cursor[wave][e] = j + 1;
+    // ---- list entries
+    for (int e0 = 0; e0 < E; e0 += group) {
+        const int ne = min(group, E - e0);
+        if (!one_group) {
+            __syncthreads();
+            build_masks(e0, ne);
+        }
+        __syncthreads();
+        for (int ei = tid; ei < ne; ei += blockDim.x) {
+            int run = offsets[e0 + ei];  // list entries before each chunk
+            for (int c = 0; c < nchunks; ++c) {
+                before[c * ne + ei] = run;
+                run += __popcll(row_mask[c * ne + ei]);
+            }
+        }
+        __syncthreads();
+        for (int c = wave; c < nchunks; c += kTableWaves) {
+            const int r = c * 64 + lane;
+            if (r >= M) continue;
+            const unsigned long long below = (1ull << lane) - 1ull;
+            for (int k = 0; k < K; ++k) {
+                const int q = r * K + k;
+                const int e = id_at(q);
+                if (e < e0 || e >= e0 + ne) continue;
+                const int slot = c * ne + (e - e0);
+                const int j = before[slot] + __popcll(row_mask[slot] & below);
                 p.list_rows[j] = r;
-                p.list_slots[j] = lane;
+                p.list_slots[j] = k;
                 p.list_pos[q] = j;
             }
         }
     }
+}
+
+// Router logits for many token rows (prefill): logits[r][e] = RMSNorm(x[r]) .
+// W[e] with an f32 router [experts][width] (moonlight_kernels.metal:43-60, the
+// post-attention norm of :23-41 applied to x), on fp32 MFMA
+// (v_mfma_f32_32x32x2_f32: fp32 products and sums, like the VALU matmul, in
+// another order).  A workgroup owns 32 rows x 32 experts; its 8 waves split k
+// and their partial tiles are summed in wave order through LDS, so the result
+// is deterministic.  Lane l feeds row / expert l % 32 and, per group of 4
+// MFMAs, the 4 consecutive k values (l / 32) * 4 .. + 3 of an 8-wide k step.
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+constexpr int kRouterTile = 32;
+constexpr int kRouterWaves = 8;
+__global__ __launch_bounds__(512) void router_logits_kernel(const float *x, const float *norm_w,
+                                                            float eps, const float *w, int rows,
+                                                            int experts, int width,
+                                                            float *logits) {
+    __shared__ float inv_rms[kRouterTile];
+    __shared__ float part[kRouterWaves][kRouterTile * kRouterTile];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int r0 = blockIdx.x * kRouterTile, e0 = blockIdx.y * kRouterTile;
+    // sums of squares: the loads of a row are issued in batches of 8 before
+    // they are used (a load-use chain per iteration would serialise latency)
+    for (int rr = wave; rr < kRouterTile; rr += kRouterWaves) {
+        const int r = r0 + rr;
+        float ss = 0.0f;
+        if (norm_w && r < rows) {
+            for (int i0 = lane * 4; i0 < width; i0 += 256 * 8) {
+                f32x4 v[8];
+#pragma unroll
+                for (int b = 0; b < 8; ++b) {
+                    const int i = i0 + 256 * b;
+                    v[b] = i < width ? load_f4(x + (long)r * width + i) : f32x4{0.f, 0.f, 0.f, 0.f};
+                }
+#pragma unroll
+                for (int b = 0; b < 8; ++b)
+                    ss += v[b].x * v[b].x + v[b].y * v[b].y + v[b].z * v[b].z + v[b].w * v[b].w;
+            }
+        }
+        ss = wave_sum(ss);
+        if (lane == 0) inv_rms[rr] = norm_w ? 1.0f / sqrtf(ss / (float)width + eps) : 1.0f;
+    }
+    __syncthreads();
+    const int col = lane & 31, h = lane >> 5;
+    const int row = min(r0 + col, rows - 1);  // rows past the end are never stored
+    const int ex = min(e0 + col, experts - 1);
+    const float rs = inv_rms[col];
+    const int kper = ((width + 8 * kRouterWaves - 1) / (8 * kRouterWaves)) * 8;
+    const int kbeg = wave * kper, kend = min(width, kbeg + kper);
+    const float *xr = x + (long)row * width;
+    const float *wr = w + (long)ex * width;
+    f32x16 acc;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) acc[i] = 0.0f;
+    // batches of 8 k steps: all loads of a batch are issued before its MFMAs
+    constexpr int kBatch = 8;
+    for (int kb = kbeg + h * 4; kb < kend; kb += 8 * kBatch) {
+        f32x4 xv[kBatch], wv[kBatch], nv[kBatch];
+#pragma unroll
+        for (int b = 0; b < kBatch; ++b) {
+            const int k = kb + 8 * b;
+            const bool ok = k < kend;
+            xv[b] = ok ? load_f4(xr + k) : f32x4{0.f, 0.f, 0.f, 0.f};
+            wv[b] = ok ? load_f4(wr + k) : f32x4{0.f, 0.f, 0.f, 0.f};
+            nv[b] = (ok && norm_w) ? load_f4(norm_w + k) : f32x4{1.f, 1.f, 1.f, 1.f};
+        }
+#pragma unroll
+        for (int b = 0; b < kBatch; ++b) {
+            f32x4 x4 = xv[b];
+            if (norm_w) {
+                x4.x = x4.x * rs * nv[b].x;
+                x4.y = x4.y * rs * nv[b].y;
+                x4.z = x4.z * rs * nv[b].z;
+                x4.w = x4.w * rs * nv[b].w;
+            }
+            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(x4.x, wv[b].x, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(x4.y, wv[b].y, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(x4.z, wv[b].z, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(x4.w, wv[b].w, acc, 0, 0, 0);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const int r = (i >> 2) * 8 + h * 4 + (i & 3);
+        part[wave][r * kRouterTile + col] = acc[i];
+    }
+    __syncthreads();
+    for (int o = tid; o < kRouterTile * kRouterTile; o += blockDim.x) {
+        float v = 0.0f;
+#pragma unroll
+        for (int wv = 0; wv < kRouterWaves; ++wv) v += part[wv][o];
+        const int r = r0 + o / kRouterTile, e = e0 + o % kRouterTile;
+        if (r < rows && e < experts) logits[(long)r * experts + e] = v;
+    }
+}
+
+int router_logits(const float *x, const float *norm_w, float eps, const float *w, int rows,
+                  int experts, int width, float *logits, hipStream_t stream) {
+    if (!x || !w || !logits || rows <= 0 || experts <= 0 || width <= 0 || width % 8) return kErrArgs;
+    hipLaunchKernelGGL(router_logits_kernel,
+                       dim3((rows + kRouterTile - 1) / kRouterTile,
+                            (experts + kRouterTile - 1) / kRouterTile),
+                       dim3(64 * kRouterWaves), 0, stream, x, norm_w, eps, w, rows, experts,
+                       width, logits);
+    return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
 }
 
 constexpr int kRouteFusedMaxPositions = 1024;

@@ -12,9 +12,9 @@
 //
 // A launch covers a table of independent tasks (one per active routed expert
 // plus the shared expert, or one dense matrix).  Tiles are 128 token rows x
-// 128 weight rows (SwiGLU pairs: 64 gate + 64 matching up rows, 64 outputs);
-// the tile order groups 4 row tiles of a task so that consecutive workgroups on
-// one XCD share weight tiles in that XCD's L2.
+// 256 weight rows (SwiGLU pairs: 128 gate + 128 matching up rows, 128
+// outputs); the tile order groups 4 row tiles of a task so that consecutive
+// workgroups on one XCD share weight tiles in that XCD's L2.
 #pragma once
 
 #include "gemv_impl.h"
@@ -22,7 +22,7 @@
 namespace mlh {
 
 constexpr int kQgBM = 128;  // token rows per tile
-constexpr int kQgBW = 128;  // weight rows per tile
+constexpr int kQgBW = 256;  // weight rows per tile
 constexpr int kQgBK = 64;   // k per pipeline stage
 constexpr int kQgGroup = 4; // row tiles per locality group
 constexpr int kQgMaxTasks = 272;
@@ -52,8 +52,7 @@ struct QGemmLaunch {
 
 // Per-row activation quantisation (optionally RMSNorm'ed first,
 // moonlight_kernels.metal:23-41): rows of `x` (stride x_stride floats) ->
-// hi/lo limbs (row stride `width` bytes) and scales.  rows_dev, when non-null,
-// holds the row count on the device (capped by rows).
+// hi/lo limbs (row stride `width` bytes) and scales.
 int quantize_activations(const float *x, long x_stride, int rows, int width, const float *norm_w,
                          float eps, int8_t *hi, int8_t *lo, float *scale, hipStream_t stream);
 

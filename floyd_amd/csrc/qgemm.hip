@@ -11,12 +11,13 @@
 // C[(r / 4) * 8 + (l / 32) * 4 + r % 4][l % 32].
 #include "qgemm.h"
 
+#include <type_traits>
+
 namespace mlh {
 
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 typedef int i32x16 __attribute__((ext_vector_type(16)));
 
-constexpr int kLdsRow = kQgBK + 16;  // padded LDS row in bytes (conflict-free b128 reads)
 constexpr int kQuantMax = 16384;     // |256 * hi + lo| bound
 
 bool qgemm_shape_ok(int fmt, int k) {
@@ -35,6 +36,11 @@ __device__ __forceinline__ void quant_pair(float v, float inv, int &h, int &l) {
     l = qi - h * 256;
 }
 
+// Rows of up to kQuantRegChunks * 256 values stay in registers (one read of
+// the row); wider rows (the 11264-wide dense down input) are read per pass.
+constexpr int kQuantRegChunks = 16;
+
+template <bool REG>
 __global__ __launch_bounds__(256) void quantize_act_kernel(const float *x, long x_stride, int rows,
                                                            int width, const float *norm_w,
                                                            float eps, int8_t *hi, int8_t *lo,
@@ -43,47 +49,62 @@ __global__ __launch_bounds__(256) void quantize_act_kernel(const float *x, long 
     const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (row >= rows) return;
     const float *xr = x + (long)row * x_stride;
+    const int nchunks = (width / 4 + kWave - 1) / kWave;  // float4 chunks per lane (upper)
+    f32x4 v[REG ? kQuantRegChunks : 1];
+    if constexpr (REG) {
+#pragma unroll
+        for (int c = 0; c < kQuantRegChunks; ++c) {
+            const int i = (c * kWave + lane) * 4;
+            v[c] = (c < nchunks && i < width) ? load_f4(xr + i) : f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+    }
+    auto value = [&](int c) -> f32x4 {
+        if constexpr (REG) return v[c];
+        const int i = (c * kWave + lane) * 4;
+        return i < width ? load_f4(xr + i) : f32x4{0.f, 0.f, 0.f, 0.f};
+    };
+    const int nc = REG ? kQuantRegChunks : nchunks;
     float inv_rms = 1.0f;
     if (norm_w) {
         float ss = 0.0f;
-        for (int i = lane * 4; i < width; i += kWave * 4) {
-            const f32x4 v = load_f4(xr + i);
-            ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+        for (int c = 0; c < nc; ++c) {
+            const f32x4 t = value(c);
+            ss += t.x * t.x + t.y * t.y + t.z * t.z + t.w * t.w;
         }
         ss = wave_sum(ss);
         inv_rms = 1.0f / sqrtf(ss / (float)width + eps);
     }
-    float amax = 0.0f;
-    for (int i = lane * 4; i < width; i += kWave * 4) {
-        f32x4 v = load_f4(xr + i);
-        if (norm_w) {
+    auto normed = [&](int c) -> f32x4 {
+        f32x4 t = value(c);
+        const int i = (c * kWave + lane) * 4;
+        if (norm_w && i < width) {
             const f32x4 n = load_f4(norm_w + i);
-            v.x = v.x * inv_rms * n.x;
-            v.y = v.y * inv_rms * n.y;
-            v.z = v.z * inv_rms * n.z;
-            v.w = v.w * inv_rms * n.w;
+            t.x = t.x * inv_rms * n.x;
+            t.y = t.y * inv_rms * n.y;
+            t.z = t.z * inv_rms * n.z;
+            t.w = t.w * inv_rms * n.w;
         }
-        amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+        return t;
+    };
+    float amax = 0.0f;
+    for (int c = 0; c < nc; ++c) {
+        const f32x4 t = normed(c);
+        amax = fmaxf(amax, fmaxf(fmaxf(fabsf(t.x), fabsf(t.y)), fmaxf(fabsf(t.z), fabsf(t.w))));
     }
     amax = wave_max(amax);
     const float inv = amax > 0.0f ? (float)kQuantMax / amax : 0.0f;
     if (lane == 0) scale[row] = amax / (float)kQuantMax;
     int8_t *hr = hi + (long)row * width;
     int8_t *lr = lo + (long)row * width;
-    for (int i = lane * 4; i < width; i += kWave * 4) {
-        f32x4 v = load_f4(xr + i);
-        if (norm_w) {
-            const f32x4 n = load_f4(norm_w + i);
-            v.x = v.x * inv_rms * n.x;
-            v.y = v.y * inv_rms * n.y;
-            v.z = v.z * inv_rms * n.z;
-            v.w = v.w * inv_rms * n.w;
-        }
+    for (int c = 0; c < nc; ++c) {
+        const int i = (c * kWave + lane) * 4;
+        if (i >= width) continue;
+        const f32x4 t = normed(c);
         int h0, h1, h2, h3, l0, l1, l2, l3;
-        quant_pair(v.x, inv, h0, l0);
-        quant_pair(v.y, inv, h1, l1);
-        quant_pair(v.z, inv, h2, l2);
-        quant_pair(v.w, inv, h3, l3);
+        quant_pair(t.x, inv, h0, l0);
+        quant_pair(t.y, inv, h1, l1);
+        quant_pair(t.z, inv, h2, l2);
+        quant_pair(t.w, inv, h3, l3);
         const unsigned hp = (h0 & 0xFF) | ((h1 & 0xFF) << 8) | ((h2 & 0xFF) << 16) |
                             ((unsigned)(h3 & 0xFF) << 24);
         const unsigned lp = (l0 & 0xFF) | ((l1 & 0xFF) << 8) | ((l2 & 0xFF) << 16) |
@@ -97,8 +118,12 @@ int quantize_activations(const float *x, long x_stride, int rows, int width, con
                          float eps, int8_t *hi, int8_t *lo, float *scale, hipStream_t stream) {
     if (!x || !hi || !lo || !scale || rows <= 0 || width <= 0 || width % 4 || x_stride % 4)
         return kErrArgs;
-    hipLaunchKernelGGL(quantize_act_kernel, dim3((rows + 3) / 4), dim3(256), 0, stream, x,
-                       x_stride, rows, width, norm_w, eps, hi, lo, scale);
+    if (width <= kQuantRegChunks * kWave * 4)
+        hipLaunchKernelGGL(quantize_act_kernel<true>, dim3((rows + 3) / 4), dim3(256), 0, stream,
+                           x, x_stride, rows, width, norm_w, eps, hi, lo, scale);
+    else
+        hipLaunchKernelGGL(quantize_act_kernel<false>, dim3((rows + 3) / 4), dim3(256), 0, stream,
+                           x, x_stride, rows, width, norm_w, eps, hi, lo, scale);
     return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
 }
 
@@ -130,18 +155,62 @@ __device__ __forceinline__ int find_task(const int *tile_start, int n, int tile)
 }
 
 template <bool DUAL>
-__device__ __forceinline__ int tiles_of(int rows, int n_out) {
+__host__ __device__ __forceinline__ int tiles_of(int rows, int n_out) {
     constexpr int outw = DUAL ? kQgBW / 2 : kQgBW;
     return ((rows + kQgBM - 1) / kQgBM) * ((n_out + outw - 1) / outw);
 }
 
-template <int FMT, bool DUAL>
-__global__ __launch_bounds__(256, 2) void qgemm_kernel(QGemmLaunch L) {
-    __shared__ __attribute__((aligned(16))) int8_t lds_a[2][2][kQgBM * kLdsRow];
-    __shared__ __attribute__((aligned(16))) int8_t lds_b[2][kQgBW * kLdsRow];
-    __shared__ float lds_scale[kQgBM];
-    __shared__ int lds_arow[kQgBM];
+// LDS tiles hold one k slice per stage as rows of RB bytes (RB / 16 chunks of
+// 16 bytes): q8 slices are 128 wide and go straight from global memory into
+// LDS (global_load_lds_dwordx4, full 128-byte lines per row); q4 slices are
+// 64 wide and are unpacked in registers on the way.  Chunk c of row r lives
+// at chunk c ^ g(r):
+//   RB = 64:  g(r) = ((r >> 1) ^ (r >> 3)) & 3
+//   RB = 128: g(r) = (r ^ (r >> 3)) & 7
+// so that the MFMA fragment reads (32 consecutive rows, one chunk) and the
+// tile writes hit distinct banks whether the LDS serves 8 or 16 lanes of a
+// 128-bit access per cycle.
+template <int FMT> struct QgCfg;
+template <> struct QgCfg<kQ8> {
+    static constexpr int kRB = 128, kStages = 2;
+};
+template <> struct QgCfg<kQ4> {
+    static constexpr int kRB = 64, kStages = 2;
+};
 
+template <int RB>
+__device__ __forceinline__ int lds_off(int row, int chunk) {
+    if constexpr (RB == 64) return row * 64 + ((chunk ^ (((row >> 1) ^ (row >> 3)) & 3)) << 4);
+    else return row * 128 + ((chunk ^ ((row ^ (row >> 3)) & 7)) << 4);
+}
+
+template <int FMT> constexpr int qg_lds_a() { return 2 * kQgBM * QgCfg<FMT>::kRB; }
+template <int FMT> constexpr int qg_lds_stage() {
+    return (2 * kQgBM + kQgBW) * QgCfg<FMT>::kRB;
+}
+template <int FMT> constexpr int qg_lds_bytes() {
+    return QgCfg<FMT>::kStages * qg_lds_stage<FMT>() + kQgBM * 8;  // + scales and row map
+}
+
+// s_waitcnt on the vector-memory counter only (gfx9 encoding: vmcnt in bits
+// 3:0 and 15:14, expcnt 6:4 and lgkmcnt 11:8 left at their no-wait maxima).
+template <int N> __device__ __forceinline__ void wait_vmcnt() {
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// Workgroup: 4 waves in a 2 (rows) x 2 (weight rows) arrangement over a 128 x
+// 256 tile; a wave owns 64 token rows x 128 weight rows = 2 x 4 blocks of
+// 32 x 32 per limb (256 int32 accumulators, kept in AGPRs).
+template <int FMT, bool DUAL>
+__global__ __launch_bounds__(256, 1) void qgemm_kernel(QGemmLaunch L) {
+    extern __shared__ __attribute__((aligned(16))) int8_t qg_lds[];
+    constexpr int kRB = QgCfg<FMT>::kRB;
+    constexpr int kStages = QgCfg<FMT>::kStages;
+    constexpr int kStage = qg_lds_stage<FMT>();
+    constexpr int kLdsA = qg_lds_a<FMT>();
+    constexpr bool kDma = FMT == kQ8;
+    float *lds_scale = reinterpret_cast<float *>(qg_lds + kStages * kStage);
+    int *lds_arow = reinterpret_cast<int *>(qg_lds + kStages * kStage + kQgBM * 4);
     // ---- tile -> (task, row tile, column tile), XCD-contiguous order
     GemmTask tk;
     int local;
@@ -199,159 +268,295 @@ __global__ __launch_bounds__(256, 2) void qgemm_kernel(QGemmLaunch L) {
     }
     __syncthreads();
 
-    // ---- per-thread global sources (fixed over k)
-    // A: 4 chunks of 16 bytes: limb = c >> 9, row = (c >> 2) & 127, chunk = c & 3
-    const int8_t *a_src[4];
-    int a_dst[4];
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-        const int c = tid + 256 * q;
-        const int limb = c >> 9, r = (c >> 2) & (kQgBM - 1), kc = c & 3;
-        const int arow = lds_arow[r];
-        a_src[q] = arow < 0 ? nullptr
-                            : (limb ? tk.a_lo : tk.a_hi) + (long)arow * tk.a_stride + kc * 16;
-        a_dst[q] = limb * (kQgBM * kLdsRow) + r * kLdsRow + kc * 16;
-    }
-    // B: LDS row j holds weight row `out` of w (SwiGLU: rows 32..63 of each
-    // 64-row half come from the up matrix w2, matching gate rows 0..31)
-    constexpr int kBChunks = FMT == kQ8 ? 2 : 1;
-    const uint8_t *b_src[kBChunks];
-    int b_dst[kBChunks];
+    // ---- per-thread global sources (fixed over k).  Rows past the task's end
+    // read row m0 (A) or weight row 0 (B): their outputs are never stored.
     const long w_row_bytes = FMT == kQ8 ? tk.k : tk.k / 2;
     const uint8_t *const w_gate = tk.w;
     const uint8_t *const w_up = tk.w2;
+    // weight row held by LDS B row j: SwiGLU tiles put gate rows in blocks
+    // f = 0, 1 and the matching up rows in blocks f = 2, 3 of each wave half
+    auto b_row_src = [&](int j) -> const uint8_t * {
+        const int f = (j >> 5) & 3;
+        const int out = DUAL ? n0 + (j >> 7) * 64 + (f & 1) * 32 + (j & 31) : n0 + j;
+        const uint8_t *base = (DUAL && f >= 2) ? w_up : w_gate;
+        return base + (long)(out < tk.n_out ? out : 0) * w_row_bytes;
+    };
+    auto a_row_src = [&](int limb, int r) -> const int8_t * {
+        const int arow = lds_arow[r] >= 0 ? lds_arow[r] : lds_arow[0];
+        return (limb ? tk.a_lo : tk.a_hi) + (long)arow * tk.a_stride;
+    };
+
+    // DMA path (q8, 128-byte rows): wave w issues the 1 KB blocks
+    // blk = w + 4 q, q = 0..7, of A (blocks 0..15: rows (blk % 16) * 8 .. + 8 of
+    // limb blk / 16) and of B (rows blk * 8 .. + 8); lane l fills LDS row
+    // (block row 0 + l / 8), physical chunk l % 8, so it loads the logical
+    // chunk (l % 8) ^ g(row).  Only four distinct A rows per lane exist (both
+    // limbs share them); the B rows follow from q at compile time.
+    const int lr = lane >> 3, lc = lane & 7;
+    unsigned a_off[4] = {0u, 0u, 0u, 0u};  // byte offsets of this lane's A rows
+    // register path (q4, 64-byte rows): 4 A chunks and 2 packed B chunks
+    const int8_t *a_src[4];
+    int a_dst[4];
+    const uint8_t *b_src[2];
+    int b_dst[2];
+    u32x4 ra[4], rb[2];
+    if constexpr (kDma) {
 #pragma unroll
-    for (int q = 0; q < kBChunks; ++q) {
-        const int j = FMT == kQ8 ? (tid + 256 * q) >> 2 : tid >> 1;
-        const int out = DUAL ? n0 + (j >> 6) * 32 + (j & 31) : n0 + j;
-        const bool up = DUAL && ((j >> 5) & 1);
-        const uint8_t *base = up ? w_up : w_gate;
-        const int col = FMT == kQ8 ? ((tid + 256 * q) & 3) * 16 : (tid & 1) * 16;
-        b_src[q] = out < tk.n_out ? base + (long)out * w_row_bytes + col : nullptr;
-        b_dst[q] = j * kLdsRow + (FMT == kQ8 ? col : col * 2);
+        for (int q = 0; q < 4; ++q) {
+            const int r = (wave + 4 * q) * 8 + lr;
+            const int arow = lds_arow[r] >= 0 ? lds_arow[r] : lds_arow[0];
+            a_off[q] = (unsigned)(arow * tk.a_stride);
+        }
+    } else {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int c = tid + 256 * q;
+            const int limb = c >> 9, r = (c >> 2) & (kQgBM - 1), kc = c & 3;
+            a_src[q] = a_row_src(limb, r) + kc * 16;
+            a_dst[q] = limb * (kQgBM * kRB) + lds_off<kRB>(r, kc);
+        }
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+            const int c = tid + 256 * q;
+            const int j = c >> 1, part = c & 1;  // 32 packed columns per part
+            b_src[q] = b_row_src(j) + part * 16;
+            b_dst[q] = (j << 1) | part;
+        }
     }
 
-    u32x4 ra[4], rb[kBChunks];
-    auto fetch = [&](int k0) {
+    // one k slice of 128 (or, when k % 128 == 64, a last slice of 64: lanes
+    // whose chunk is 4..7 then re-read chunk - 4, in bounds, unused)
+    auto issue_dma = [&](int k0, int buf, bool half_slice) {
+        __attribute__((address_space(3))) int8_t *stage =
+            (__attribute__((address_space(3))) int8_t *)(qg_lds + buf * kStage);
 #pragma unroll
-        for (int q = 0; q < 4; ++q)
-            ra[q] = a_src[q] ? *reinterpret_cast<const u32x4 *>(a_src[q] + k0)
-                             : u32x4{0u, 0u, 0u, 0u};
-#pragma unroll
-        for (int q = 0; q < kBChunks; ++q) {
-            const long off = FMT == kQ8 ? k0 : k0 / 2;
-            rb[q] = b_src[q] ? *reinterpret_cast<const u32x4 *>(b_src[q] + off)
-                             : u32x4{0u, 0u, 0u, 0u};
+        for (int q = 0; q < 8; ++q) {
+            const int blk = wave + 4 * q;
+            const int r = (blk & 15) * 8 + lr;  // A row of this lane
+            int ca = lc ^ ((r ^ (r >> 3)) & 7);
+            if (half_slice && ca >= 4) ca -= 4;
+            // uniform base + 32-bit lane offset: one VGPR per address
+            const int8_t *abase = q >= 4 ? tk.a_lo : tk.a_hi;
+            const unsigned aoff = a_off[q & 3] + (unsigned)(k0 + ca * 16);
+            __builtin_amdgcn_global_load_lds(
+                (const __attribute__((address_space(1))) void *)(abase + aoff),
+                stage + (q >> 2) * (kQgBM * kRB) + (blk & 15) * 1024, 16, 0, 0);
+            const int j = blk * 8 + lr;  // B row of this lane
+            const int f = (j >> 5) & 3;
+            const int out = DUAL ? n0 + (j >> 7) * 64 + (f & 1) * 32 + (j & 31) : n0 + j;
+            const uint8_t *bbase = (DUAL && f >= 2) ? w_up : w_gate;
+            int cb = lc ^ ((j ^ (j >> 3)) & 7);
+            if (half_slice && cb >= 4) cb -= 4;
+            const unsigned boff =
+                (unsigned)((out < tk.n_out ? out : 0) * tk.k) + (unsigned)(k0 + cb * 16);
+            __builtin_amdgcn_global_load_lds(
+                (const __attribute__((address_space(1))) void *)(bbase + boff),
+                stage + kLdsA + blk * 1024, 16, 0, 0);
         }
     };
+    auto fetch = [&](int k0) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) ra[q] = load_global16(a_src[q] + k0);
+#pragma unroll
+        for (int q = 0; q < 2; ++q) rb[q] = load_global16(b_src[q] + k0 / 2);
+    };
     auto stash = [&](int buf) {
-        int8_t *a = &lds_a[buf][0][0];
+        int8_t *a = qg_lds + buf * kStage;
 #pragma unroll
         for (int q = 0; q < 4; ++q) *reinterpret_cast<u32x4 *>(a + a_dst[q]) = ra[q];
-        int8_t *b = &lds_b[buf][0];
-        if (FMT == kQ8) {
+        int8_t *b = a + kLdsA;
 #pragma unroll
-            for (int q = 0; q < kBChunks; ++q) *reinterpret_cast<u32x4 *>(b + b_dst[q]) = rb[q];
-        } else {
+        for (int q = 0; q < 2; ++q) {
+            const int j = b_dst[q] >> 1, part = b_dst[q] & 1;
             unsigned v[8];
-            unpack_q4_word(rb[0].x, v[0], v[1]);
-            unpack_q4_word(rb[0].y, v[2], v[3]);
-            unpack_q4_word(rb[0].z, v[4], v[5]);
-            unpack_q4_word(rb[0].w, v[6], v[7]);
-            *reinterpret_cast<u32x4 *>(b + b_dst[0]) = u32x4{v[0], v[1], v[2], v[3]};
-            *reinterpret_cast<u32x4 *>(b + b_dst[0] + 16) = u32x4{v[4], v[5], v[6], v[7]};
+            unpack_q4_word(rb[q].x, v[0], v[1]);
+            unpack_q4_word(rb[q].y, v[2], v[3]);
+            unpack_q4_word(rb[q].z, v[4], v[5]);
+            unpack_q4_word(rb[q].w, v[6], v[7]);
+            *reinterpret_cast<u32x4 *>(b + lds_off<kRB>(j, 2 * part)) =
+                u32x4{v[0], v[1], v[2], v[3]};
+            *reinterpret_cast<u32x4 *>(b + lds_off<kRB>(j, 2 * part + 1)) =
+                u32x4{v[4], v[5], v[6], v[7]};
         }
     };
 
-    i32x16 acc[2][2][2];  // [limb][row block][column block]
+    i32x16 acc[2][2][4];  // [limb][row block][weight-row block]
 #pragma unroll
     for (int a = 0; a < 2; ++a)
 #pragma unroll
         for (int i = 0; i < 2; ++i)
 #pragma unroll
-            for (int f = 0; f < 2; ++f)
+            for (int f = 0; f < 4; ++f)
 #pragma unroll
                 for (int r = 0; r < 16; ++r) acc[a][i][f][r] = 0;
 
-    const int nk = tk.k / kQgBK;
-    fetch(0);
-    stash(0);
-    __syncthreads();
-    const int arow_l = lane & 31;
-    const int kq = (lane >> 5) * 16;
-    for (int ks = 0; ks < nk; ++ks) {
-        const int cur = ks & 1;
-        if (ks + 1 < nk) fetch((ks + 1) * kQgBK);
-        const int8_t *ah = &lds_a[cur][0][0];
-        const int8_t *al = &lds_a[cur][1][0];
-        const int8_t *bb = &lds_b[cur][0];
+    const int frow = lane & 31;
+    const int half = lane >> 5;
+    // two 32-wide k steps: all fragments are read before the first MFMA so
+    // the LDS latency overlaps the MFMAs
+    auto compute_pair = [&](int buf, int ksub0) {
+        const int8_t *ah = qg_lds + buf * kStage;
+        const int8_t *al = ah + kQgBM * kRB;
+        const int8_t *bb = ah + kLdsA;
+        i32x4 fa_h[2][2], fa_l[2][2], fb[2][4];
 #pragma unroll
-        for (int ksub = 0; ksub < 2; ++ksub) {
-            const int koff = ksub * 32 + kq;
-            i32x4 fa_h[2], fa_l[2], fb[2];
+        for (int s2 = 0; s2 < 2; ++s2) {
+            const int chunk = (ksub0 + s2) * 2 + half;
 #pragma unroll
             for (int i = 0; i < 2; ++i) {
-                const int row = wm * 64 + i * 32 + arow_l;
-                fa_h[i] = *reinterpret_cast<const i32x4 *>(ah + row * kLdsRow + koff);
-                fa_l[i] = *reinterpret_cast<const i32x4 *>(al + row * kLdsRow + koff);
+                const int row = wm * 64 + i * 32 + frow;
+                fa_h[s2][i] = *reinterpret_cast<const i32x4 *>(ah + lds_off<kRB>(row, chunk));
+                fa_l[s2][i] = *reinterpret_cast<const i32x4 *>(al + lds_off<kRB>(row, chunk));
             }
 #pragma unroll
-            for (int f = 0; f < 2; ++f) {
-                const int row = wn * 64 + f * 32 + arow_l;
-                fb[f] = *reinterpret_cast<const i32x4 *>(bb + row * kLdsRow + koff);
+            for (int f = 0; f < 4; ++f) {
+                const int row = wn * 128 + f * 32 + frow;
+                fb[s2][f] = *reinterpret_cast<const i32x4 *>(bb + lds_off<kRB>(row, chunk));
             }
+        }
+#pragma unroll
+        for (int s2 = 0; s2 < 2; ++s2)
 #pragma unroll
             for (int i = 0; i < 2; ++i)
 #pragma unroll
-                for (int f = 0; f < 2; ++f) {
-                    acc[0][i][f] =
-                        __builtin_amdgcn_mfma_i32_32x32x32_i8(fa_h[i], fb[f], acc[0][i][f], 0, 0, 0);
-                    acc[1][i][f] =
-                        __builtin_amdgcn_mfma_i32_32x32x32_i8(fa_l[i], fb[f], acc[1][i][f], 0, 0, 0);
+                for (int f = 0; f < 4; ++f) {
+                    acc[0][i][f] = __builtin_amdgcn_mfma_i32_32x32x32_i8(
+                        fa_h[s2][i], fb[s2][f], acc[0][i][f], 0, 0, 0);
+                    acc[1][i][f] = __builtin_amdgcn_mfma_i32_32x32x32_i8(
+                        fa_l[s2][i], fb[s2][f], acc[1][i][f], 0, 0, 0);
                 }
+    };
+
+    if constexpr (kDma) {
+        // two buffers: slice ks + 1 streams into LDS while slice ks is
+        // multiplied; the barrier after the wait also frees the other buffer
+        const int nk = (tk.k + kRB - 1) / kRB;
+        issue_dma(0, 0, kRB > tk.k);
+        for (int ks = 0; ks < nk; ++ks) {
+            wait_vmcnt<0>();
+            // a bare barrier: __syncthreads() would also wait for the stores
+            // and loads of the fence it implies
+            __builtin_amdgcn_s_barrier();
+            if (ks + 1 < nk)
+                issue_dma((ks + 1) * kRB, (ks + 1) & 1, (ks + 2) * kRB > tk.k);
+            const int buf = ks & 1;
+            // the two 64-wide halves of the slice run as a loop, not unrolled:
+            // unrolled, the compiler keeps a second set of fragments live and
+            // spills
+            const int pairs = (ks + 1) * kRB <= tk.k ? 2 : 1;
+#pragma unroll 1
+            for (int p = 0; p < pairs; ++p) compute_pair(buf, 2 * p);
         }
-        if (ks + 1 < nk) stash(cur ^ 1);
+    } else {
+        // two buffers: slice ks + 2 is in registers while slice ks is multiplied
+        const int nk = tk.k / kRB;
+        fetch(0);
+        stash(0);
+        if (nk > 1) fetch(kRB);
         __syncthreads();
+        for (int ks = 0; ks < nk; ++ks) {
+            compute_pair(ks & 1, 0);
+            if (ks + 1 < nk) {
+                stash((ks + 1) & 1);
+                if (ks + 2 < nk) fetch((ks + 2) * kRB);
+            }
+            __syncthreads();
+        }
     }
 
-    // ---- epilogue
+    // ---- epilogue.  Every global input of the epilogue (weight scales,
+    // residual rows) is loaded before the first store: the stores may alias
+    // them as far as the compiler knows, so a load after a store would wait
+    // for it.
+    constexpr int kF = DUAL ? 2 : 4;
+    float sw[kF], su[kF];
+    int ncol[kF];
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
+    for (int f = 0; f < kF; ++f) {
+        ncol[f] = DUAL ? n0 + wn * 64 + f * 32 + frow : n0 + wn * 128 + f * 32 + frow;
+        const bool ok = ncol[f] < tk.n_out;
+        sw[f] = ok ? load_global_f32(tk.s + ncol[f]) : 0.0f;
+        su[f] = (DUAL && ok) ? load_global_f32(tk.s2 + ncol[f]) : 0.0f;
+    }
+    // row scales of the 32 result rows this lane holds
+    float sxr[2][16];
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const int ml = wm * 64 + i * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
-            const int m = m0 + ml;
-            if (m >= tk.rows) continue;
-            const float sx = lds_scale[ml];
-            float *yrow = tk.y + (long)m * tk.y_stride;
-            if (DUAL) {
-                const int n = n0 + wn * 32 + (lane & 31);
-                if (n < tk.n_out) {
-                    const float g = ((float)acc[0][i][0][r] * 256.0f + (float)acc[1][i][0][r]) *
-                                    sx * tk.s[n];
-                    const float u = ((float)acc[0][i][1][r] * 256.0f + (float)acc[1][i][1][r]) *
-                                    sx * tk.s2[n];
-                    yrow[n] = silu(g) * u;
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+            sxr[i][r] = lds_scale[wm * 64 + i * 32 + (r >> 2) * 8 + half * 4 + (r & 3)];
+    // complete the scale loads now: stores share the vector-memory counter,
+    // so a wait placed after the first store would also wait for the stores
+    __builtin_amdgcn_s_waitcnt(0);
+    // the residual and plain paths are separate instantiations, so the plain
+    // path carries no wait for residual loads (which would drain the stores)
+    auto epilogue = [&](auto with_resid) {
+        constexpr bool kResid = decltype(with_resid)::value;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+#pragma unroll
+            for (int rg = 0; rg < 16; rg += 4) {
+                // residual inputs of 4 result registers, loaded before their stores
+                float res[4][kF];
+                if (kResid) {
+#pragma unroll
+                    for (int r = rg; r < rg + 4; ++r) {
+                        const int m = m0 + wm * 64 + i * 32 + (r >> 2) * 8 + half * 4 + (r & 3);
+#pragma unroll
+                        for (int f = 0; f < kF; ++f)
+                            res[r - rg][f] = (m < tk.rows && ncol[f] < tk.n_out)
+                                                 ? load_global_f32(tk.resid +
+                                                                   (long)m * tk.resid_stride +
+                                                                   ncol[f])
+                                                 : 0.0f;
+                    }
                 }
-            } else {
 #pragma unroll
-                for (int f = 0; f < 2; ++f) {
-                    const int n = n0 + wn * 64 + f * 32 + (lane & 31);
-                    if (n < tk.n_out) {
-                        float v = ((float)acc[0][i][f][r] * 256.0f + (float)acc[1][i][f][r]) * sx *
-                                  tk.s[n];
-                        if (tk.resid) v = tk.resid[(long)m * tk.resid_stride + n] + v;
-                        yrow[n] = v;
+                for (int r = rg; r < rg + 4; ++r) {
+                    const int m = m0 + wm * 64 + i * 32 + (r >> 2) * 8 + half * 4 + (r & 3);
+                    if (m >= tk.rows) continue;
+                    const float sx = sxr[i][r];
+                    float *yrow = tk.y + (long)m * tk.y_stride;
+                    if (DUAL) {
+#pragma unroll
+                        for (int f = 0; f < 2; ++f) {
+                            if (ncol[f] < tk.n_out) {
+                                const float g = ((float)acc[0][i][f][r] * 256.0f +
+                                                 (float)acc[1][i][f][r]) * sx * sw[f];
+                                const float u = ((float)acc[0][i][f + 2][r] * 256.0f +
+                                                 (float)acc[1][i][f + 2][r]) * sx * su[f];
+                                store_global(yrow + ncol[f], silu(g) * u);
+                            }
+                        }
+                    } else {
+#pragma unroll
+                        for (int f = 0; f < 4; ++f) {
+                            if (ncol[f] < tk.n_out) {
+                                float v = ((float)acc[0][i][f][r] * 256.0f +
+                                           (float)acc[1][i][f][r]) * sx * sw[f];
+                                if (kResid) v = res[r - rg][f] + v;
+                                store_global(yrow + ncol[f], v);
+                            }
+                        }
                     }
                 }
             }
         }
-    }
+    };
+    if (!DUAL && tk.resid) epilogue(std::true_type{});
+    else epilogue(std::false_type{});
 }
 
 template <int FMT, bool DUAL>
 static void launch_qgemm(const QGemmLaunch &L, int grid, hipStream_t stream) {
-    hipLaunchKernelGGL((qgemm_kernel<FMT, DUAL>), dim3((unsigned)grid), dim3(256), 0, stream, L);
+    static const bool attr = [] {
+        return hipFuncSetAttribute(reinterpret_cast<const void *>(&qgemm_kernel<FMT, DUAL>),
+                                   hipFuncAttributeMaxDynamicSharedMemorySize,
+                                   qg_lds_bytes<FMT>()) == hipSuccess;
+    }();
+    (void)attr;
+    hipLaunchKernelGGL((qgemm_kernel<FMT, DUAL>), dim3((unsigned)grid), dim3(256),
+                       qg_lds_bytes<FMT>(), stream, L);
 }
 
 static int launch_qgemm_fmt(int fmt, bool dual, const QGemmLaunch &L, int tiles_bound,

@@ -921,8 +921,14 @@ int route(MoonlightSession *s, int layer, const float *x, int rows, const float 
           int *trace) {
     const ModelConfig &c = s->model->cfg;
     const LayerPlan &lp = s->model->layers[layer];
-    if (gemv_rows(s, lp.router, x, rows, c.hidden_size, c.expert_count, s->router_logits, norm_w))
+    if (rows >= kGemmMinRows && lp.router.fmt == kF32 && c.hidden_size % 8 == 0) {
+        if (router_logits(x, norm_w, c.rms_norm_epsilon, reinterpret_cast<const float *>(lp.router.w),
+                          rows, c.expert_count, c.hidden_size, s->router_logits, stream_of(s)))
+            return kErrLaunch;
+    } else if (gemv_rows(s, lp.router, x, rows, c.hidden_size, c.expert_count, s->router_logits,
+                         norm_w)) {
         return kErrLaunch;
+    }
     RouteParams r;
     r.logits = s->router_logits;
     r.bias = lp.bias;
@@ -1532,6 +1538,14 @@ extern "C" int moonlight_session_fix_routes(MoonlightSession *s, const int *expe
     const size_t n = (size_t)rows * c.experts_per_token;
     for (size_t i = 0; i < n; ++i)
         if (expert_ids[i] < 0 || expert_ids[i] >= c.expert_count) return 0;
+    // the experts of a row must be distinct, as a top-k selection makes them
+    // (the device route tables rely on it)
+    for (int r = 0; r < rows; ++r)
+        for (int a = 0; a < c.experts_per_token; ++a)
+            for (int b = a + 1; b < c.experts_per_token; ++b)
+                if (expert_ids[(size_t)r * c.experts_per_token + a] ==
+                    expert_ids[(size_t)r * c.experts_per_token + b])
+                    return 0;
     if (hipMemcpy(s->fixed_ids, expert_ids, n * sizeof(int), hipMemcpyHostToDevice) !=
         hipSuccess)
         return 0;

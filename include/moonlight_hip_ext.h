@@ -85,7 +85,8 @@ int moonlight_session_time_moe(MoonlightSession *session, int layer, int rows,
  * (moe_route_fixed semantics, moe_route.h:76-87: weights are the router's
  * sigmoid scores of those ids, then finalised), for batches of at most `rows`
  * rows.  expert_ids == NULL restores top-k routing.  Forward passes always
- * route by top-k.  Returns 0 for ids out of range or rows > max_batch. */
+ * route by top-k.  Returns 0 for ids out of range, an expert repeated within
+ * a row, or rows > max_batch. */
 int moonlight_session_fix_routes(MoonlightSession *session,
                                  const int *expert_ids, int rows);
 
