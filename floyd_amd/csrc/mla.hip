@@ -58,9 +58,15 @@ __device__ __forceinline__ void kvb_load8(const MatrixRef &m, int row, int col, 
     }
 }
 
+// grid (rows, 1 + heads * latent / 64): role 0 appends the cache rows; role
+// 1 + h * chunks + c ropes head h's query (c == 0) and absorbs it into the 64
+// latent columns c * 64 .. + 63: thread (i = t / 8, j = t % 8) takes kv_b
+// rows i, i + 32, ... of the head's nope part and columns 8 j .. 8 j + 7, all
+// loads of a thread issued before its FMAs; the 32 row groups meet in LDS.
+constexpr int kMlaAbsorbCols = 64;
 __global__ __launch_bounds__(256) void mla_prep_kernel(MlaParams p) {
     const int r = blockIdx.x;
-    const int role = blockIdx.y;  // 0: cache append, 1 + h: query head h
+    const int role = blockIdx.y;
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const int pos = p.position + r;
     const int hw = p.nope + p.rope;
@@ -68,15 +74,26 @@ __global__ __launch_bounds__(256) void mla_prep_kernel(MlaParams p) {
     if (role == 0) {
         __shared__ float part[4];
         const float *c = p.compressed + (long)r * p.compressed_stride;
+        float cv[kMlaMaxLatent / 256];
+#pragma unroll
+        for (int u = 0; u < kMlaMaxLatent / 256; ++u) {
+            const int i = t + 256 * u;
+            cv[u] = i < p.latent ? c[i] : 0.0f;
+        }
         float ss = 0.0f;
-        for (int i = t; i < p.latent; i += blockDim.x) ss += c[i] * c[i];
+#pragma unroll
+        for (int u = 0; u < kMlaMaxLatent / 256; ++u) ss += cv[u] * cv[u];
         ss = wave_sum(ss);
         if (lane == 0) part[wave] = ss;
         __syncthreads();
         const float total = (part[0] + part[1]) + (part[2] + part[3]);
         const float inv = 1.0f / sqrtf(total / (float)p.latent + p.eps);
         float *lat = p.latent_cache + (long)pos * p.latent;
-        for (int i = t; i < p.latent; i += blockDim.x) lat[i] = c[i] * inv * p.kv_norm[i];
+#pragma unroll
+        for (int u = 0; u < kMlaMaxLatent / 256; ++u) {
+            const int i = t + 256 * u;
+            if (i < p.latent) lat[i] = cv[u] * inv * p.kv_norm[i];
+        }
         float *rp = p.rope_cache + (long)pos * p.rope;
         if (t < half) {
             const float angle = (float)pos * p.inv_freq[t];
@@ -87,9 +104,11 @@ __global__ __launch_bounds__(256) void mla_prep_kernel(MlaParams p) {
         }
         return;
     }
-    const int h = role - 1;
+    const int chunks = p.latent / kMlaAbsorbCols;
+    const int h = (role - 1) / chunks;
+    const int col0 = ((role - 1) % chunks) * kMlaAbsorbCols;
     const float *q = p.query + (long)r * p.query_stride + (long)h * hw;
-    if (t < half) {
+    if (col0 == 0 && t < half) {
         const float angle = (float)pos * p.inv_freq[t];
         const float cs = cosf(angle), sn = sinf(angle);
         const float first = q[p.nope + 2 * t], second = q[p.nope + 2 * t + 1];
@@ -97,42 +116,37 @@ __global__ __launch_bounds__(256) void mla_prep_kernel(MlaParams p) {
         qr[t] = first * cs - second * sn;
         qr[half + t] = second * cs + first * sn;
     }
-    // qa[l] = sum_c q_nope[c] * kv_b[h*(nope+v) + c, l]: wave w takes rows
-    // c = w, w+4, ...; lane owns columns 8*lane .. 8*lane+7 (+512 per pass)
-    __shared__ float red[4][kMlaMaxLatent];
+    // qa[l] = sum_c q_nope[c] * kv_b[h*(nope+v) + c, l]
+    constexpr int kRowsPerThread = 256 / 32;  // nope <= 256
+    __shared__ float red[32][kMlaAbsorbCols + 1];
+    const int i = t >> 3, j = t & 7;
+    const int col = col0 + 8 * j;
     const int wrow = h * (p.nope + p.vdim);
-    for (int col0 = 0; col0 < p.latent; col0 += 512) {
-        const int col = col0 + 8 * lane;
-        float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-        if (col < p.latent) {
-            // 8 rows per step: all loads issued before the FMAs
-            for (int c0 = wave; c0 < p.nope; c0 += 32) {
-                float wv[8][8];
-                float qc[8];
+    float wv[kRowsPerThread][8];
+    float qc[kRowsPerThread];
 #pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    const int c = c0 + 4 * j;
-                    qc[j] = c < p.nope ? q[c] : 0.0f;
-                    if (c < p.nope) {
-                        kvb_load8(p.kv_b, wrow + c, col, p.latent, wv[j]);
-                    } else {
+    for (int u = 0; u < kRowsPerThread; ++u) {
+        const int c = i + 32 * u;
+        qc[u] = c < p.nope ? q[c] : 0.0f;
+        if (c < p.nope) {
+            kvb_load8(p.kv_b, wrow + c, col, p.latent, wv[u]);
+        } else {
 #pragma unroll
-                        for (int i = 0; i < 8; ++i) wv[j][i] = 0.0f;
-                    }
-                }
-#pragma unroll
-                for (int j = 0; j < 8; ++j)
-#pragma unroll
-                    for (int i = 0; i < 8; ++i) acc[i] = fmaf(qc[j], wv[j][i], acc[i]);
-            }
-#pragma unroll
-            for (int i = 0; i < 8; ++i) red[wave][col - col0 + i] = acc[i];
+            for (int e = 0; e < 8; ++e) wv[u][e] = 0.0f;
         }
-        __syncthreads();
-        float *qa = p.query_absorbed + ((long)r * p.heads + h) * p.latent;
-        for (int i = t; i < 512 && col0 + i < p.latent; i += blockDim.x)
-            qa[col0 + i] = (red[0][i] + red[1][i]) + (red[2][i] + red[3][i]);
-        __syncthreads();
+    }
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int u = 0; u < kRowsPerThread; ++u)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[e] = fmaf(qc[u], wv[u][e], acc[e]);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) red[i][8 * j + e] = acc[e];
+    __syncthreads();
+    if (t < kMlaAbsorbCols) {
+        float v = 0.0f;
+        for (int g = 0; g < 32; ++g) v += red[g][t];
+        p.query_absorbed[((long)r * p.heads + h) * p.latent + col0 + t] = v;
     }
 }
 
@@ -159,17 +173,19 @@ __device__ __forceinline__ void load_lat(const float *row, int lane, float (&v)[
     }
 }
 
-// One workgroup per (split of KS keys, token row).  Wave w scores heads
-// 4w..4w+3 against every key of the split (8 keys per step, all loads issued
-// first); the transposed butterfly leaves one (key, head) score per writer
-// lane.  The context pass gives each thread latent dims t, t+256 and loads
-// KB cache values of its dims at a time before their FMAs.
+// One workgroup per (split of KS keys, token row).  Wave w takes keys
+// 8w .. 8w + 7 of the split and scores them against all heads (two passes of
+// 8 heads, transposed butterfly over 64 (key, head) sums); the latent rows it
+// loads (one batch of loads per wave) also go to LDS, where the context pass
+// reads them back: thread t accumulates latent dims t, t + 256 of every head.
+constexpr int kAttendLdsBytes = kMlaKeysPerSplit * kMlaMaxLatent * 4;
 template <int LPL>
 __global__ __launch_bounds__(256) void mla_attend_kernel(MlaParams p) {
     constexpr int H = kMlaMaxHeads;
     constexpr int KS = kMlaKeysPerSplit;
-    constexpr int HW = H / 4;  // heads per wave
-    constexpr int KB = 8;      // keys per scoring step
+    constexpr int KB = KS / 4;  // keys per wave
+    constexpr int HP = 8;       // heads per scoring pass
+    extern __shared__ __attribute__((aligned(16))) float lat_s[];  // [KS][latent]
     __shared__ float prob[KS][H];  // scores, then probabilities, key-major
     __shared__ float smax[H], ssum[H];
     const int split = blockIdx.x;
@@ -186,46 +202,53 @@ __global__ __launch_bounds__(256) void mla_attend_kernel(MlaParams p) {
         }
         return;
     }
-    float qa[HW][LPL];
-    float qr[HW];
+    float lv[KB][LPL];
+    float rv[KB];
 #pragma unroll
-    for (int i = 0; i < HW; ++i) {
-        const int h = wave * HW + i;
-        const bool hv = h < p.heads;
-        if (hv) {
-            load_lat<LPL>(p.query_absorbed + ((long)r * p.heads + h) * p.latent, lane, qa[i]);
-        } else {
-#pragma unroll
-            for (int e = 0; e < LPL; ++e) qa[i][e] = 0.0f;
-        }
-        qr[i] = (hv && lane < p.rope) ? p.query_rope[((long)r * p.heads + h) * p.rope + lane]
-                                      : 0.0f;
+    for (int b = 0; b < KB; ++b) {
+        const int j = wave * KB + b < nk ? wave * KB + b : nk - 1;  // clamp: not written
+        const long k = k0 + j;
+        load_lat<LPL>(p.latent_cache + k * p.latent, lane, lv[b]);
+        rv[b] = lane < p.rope ? p.rope_cache[k * p.rope + lane] : 0.0f;
     }
-    for (int j0 = 0; j0 < nk; j0 += KB) {
-        float lv[KB][LPL];
-        float rv[KB];
 #pragma unroll
-        for (int b = 0; b < KB; ++b) {
-            const int j = j0 + b < nk ? j0 + b : nk - 1;  // clamp: duplicates are not written
-            const long k = k0 + j;
-            load_lat<LPL>(p.latent_cache + k * p.latent, lane, lv[b]);
-            rv[b] = lane < p.rope ? p.rope_cache[k * p.rope + lane] : 0.0f;
+    for (int b = 0; b < KB; ++b)
+#pragma unroll
+        for (int e = 0; e < LPL; ++e)
+            lat_s[(wave * KB + b) * p.latent + lat_index<LPL>(lane, e)] = lv[b][e];
+#pragma unroll
+    for (int hp = 0; hp < H; hp += HP) {
+        float qa[HP][LPL];
+        float qr[HP];
+#pragma unroll
+        for (int i = 0; i < HP; ++i) {
+            const int h = hp + i;
+            const bool hv = h < p.heads;
+            if (hv) {
+                load_lat<LPL>(p.query_absorbed + ((long)r * p.heads + h) * p.latent, lane, qa[i]);
+            } else {
+#pragma unroll
+                for (int e = 0; e < LPL; ++e) qa[i][e] = 0.0f;
+            }
+            qr[i] = (hv && lane < p.rope)
+                        ? p.query_rope[((long)r * p.heads + h) * p.rope + lane]
+                        : 0.0f;
         }
-        float s[KB * HW];
+        float sc[KB * HP];
 #pragma unroll
         for (int b = 0; b < KB; ++b)
 #pragma unroll
-            for (int i = 0; i < HW; ++i) {
+            for (int i = 0; i < HP; ++i) {
                 float a = qr[i] * rv[b];
 #pragma unroll
                 for (int e = 0; e < LPL; ++e) a = fmaf(qa[i][e], lv[b][e], a);
-                s[b * HW + i] = a;
+                sc[b * HP + i] = a;
             }
-        butterfly_reduce<KB * HW, 64>(s, lane);
-        const int vi = butterfly_index<KB * HW, 64>(lane);
-        const int b = vi / HW, i = vi % HW;
-        if (butterfly_writer<KB * HW, 64>(lane) && j0 + b < nk)
-            prob[j0 + b][wave * HW + i] = s[0] * p.scale;
+        butterfly_reduce<KB * HP, 64>(sc, lane);
+        const int vi = butterfly_index<KB * HP, 64>(lane);
+        const int b = vi / HP, i = vi % HP;
+        if (butterfly_writer<KB * HP, 64>(lane) && wave * KB + b < nk)
+            prob[wave * KB + b][hp + i] = sc[0] * p.scale;
     }
     __syncthreads();
     {  // local softmax statistics: 16 lanes per head
@@ -256,25 +279,16 @@ __global__ __launch_bounds__(256) void mla_attend_kernel(MlaParams p) {
         float acc[H];
 #pragma unroll
         for (int h = 0; h < H; ++h) acc[h] = 0.0f;
-        for (int j0 = 0; j0 < nk; j0 += KB) {
-            float v[KB];
+        for (int j = 0; j < nk; ++j) {
+            const float v = lat_s[j * p.latent + l];
+            const f32x4 *pj = reinterpret_cast<const f32x4 *>(prob[j]);
 #pragma unroll
-            for (int b = 0; b < KB; ++b)
-                v[b] = j0 + b < nk ? p.latent_cache[(long)(k0 + j0 + b) * p.latent + l] : 0.0f;
-#pragma unroll
-            for (int b = 0; b < KB; ++b) {
-                // probabilities past nk are never read: v is 0 and the row is skipped
-                if (j0 + b < nk) {
-                    const f32x4 *pj = reinterpret_cast<const f32x4 *>(prob[j0 + b]);
-#pragma unroll
-                    for (int g = 0; g < H / 4; ++g) {
-                        const f32x4 w = pj[g];
-                        acc[4 * g + 0] = fmaf(w.x, v[b], acc[4 * g + 0]);
-                        acc[4 * g + 1] = fmaf(w.y, v[b], acc[4 * g + 1]);
-                        acc[4 * g + 2] = fmaf(w.z, v[b], acc[4 * g + 2]);
-                        acc[4 * g + 3] = fmaf(w.w, v[b], acc[4 * g + 3]);
-                    }
-                }
+            for (int g = 0; g < H / 4; ++g) {
+                const f32x4 w = pj[g];
+                acc[4 * g + 0] = fmaf(w.x, v, acc[4 * g + 0]);
+                acc[4 * g + 1] = fmaf(w.y, v, acc[4 * g + 1]);
+                acc[4 * g + 2] = fmaf(w.z, v, acc[4 * g + 2]);
+                acc[4 * g + 3] = fmaf(w.w, v, acc[4 * g + 3]);
             }
         }
 #pragma unroll
@@ -284,22 +298,26 @@ __global__ __launch_bounds__(256) void mla_attend_kernel(MlaParams p) {
 }
 
 // lc_h = sum_s e^{m_s - M} lc_s / sum_s e^{m_s - M} l_s over the key splits.
-__global__ __launch_bounds__(128) void mla_merge_kernel(MlaParams p) {
+// Workgroup (row, head, 64 latent dims): 4 thread groups take the splits
+// g, g + 4, ... (loads in batches of 8 before their FMAs) and meet in LDS in
+// group order.
+__global__ __launch_bounds__(256) void mla_merge_kernel(MlaParams p) {
     constexpr int H = kMlaMaxHeads;
     constexpr int KS = kMlaKeysPerSplit;
     __shared__ float weight[kMlaMaxSplitsInLds];
-    __shared__ float red[2];
+    __shared__ float red[4];
+    __shared__ float part_acc[4][64];
     const int r = blockIdx.x, h = blockIdx.y;
-    const int t = threadIdx.x;
+    const int t = threadIdx.x, lane = t & 63, g = t >> 6;
     const int keys = p.position + r + 1;
     const int ns = (keys + KS - 1) / KS;
     const long base = (long)r * p.max_splits * H + h;
     float m = -INFINITY;
     for (int s = t; s < ns; s += blockDim.x) m = fmaxf(m, p.part_max[base + (long)s * H]);
     m = wave_max(m);
-    if ((t & 63) == 0) red[t >> 6] = m;
+    if (lane == 0) red[g] = m;
     __syncthreads();
-    m = fmaxf(red[0], red[1]);
+    m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
     __syncthreads();
     float l = 0.0f;
     for (int s = t; s < ns; s += blockDim.x) {
@@ -308,24 +326,30 @@ __global__ __launch_bounds__(128) void mla_merge_kernel(MlaParams p) {
         l += w * p.part_sum[base + (long)s * H];
     }
     l = wave_sum(l);
-    if ((t & 63) == 0) red[t >> 6] = l;
+    if (lane == 0) red[g] = l;
     __syncthreads();
-    const float inv = 1.0f / (red[0] + red[1]);
-    const int d = blockIdx.z * 128 + t;
+    const float inv = 1.0f / ((red[0] + red[1]) + (red[2] + red[3]));
+    const int d = blockIdx.z * 64 + lane;
+    float acc = 0.0f;
     if (d < p.latent) {
-        // 8 splits per step: loads first, then the FMAs in split order
-        float acc = 0.0f;
-        for (int s0 = 0; s0 < ns; s0 += 8) {
+        for (int s0 = g; s0 < ns; s0 += 4 * 8) {
             float v[8];
 #pragma unroll
-            for (int i = 0; i < 8; ++i)
-                v[i] = s0 + i < ns ? p.part_lc[(base + (long)(s0 + i) * H) * p.latent + d] : 0.0f;
+            for (int i = 0; i < 8; ++i) {
+                const int s = s0 + 4 * i;
+                v[i] = s < ns ? p.part_lc[(base + (long)s * H) * p.latent + d] : 0.0f;
+            }
 #pragma unroll
             for (int i = 0; i < 8; ++i)
-                if (s0 + i < ns) acc = fmaf(weight[s0 + i], v[i], acc);
+                if (s0 + 4 * i < ns) acc = fmaf(weight[s0 + 4 * i], v[i], acc);
         }
-        p.latent_context[((long)r * p.heads + h) * p.latent + d] = acc * inv;
     }
+    part_acc[g][lane] = acc;
+    __syncthreads();
+    if (g == 0 && d < p.latent)
+        p.latent_context[((long)r * p.heads + h) * p.latent + d] =
+            ((part_acc[0][lane] + part_acc[1][lane]) + (part_acc[2][lane] + part_acc[3][lane])) *
+            inv;
 }
 
 // ctx_h[v] = W_UV_h[v, :] . lc_h: one wave per 8 value rows, lanes over
@@ -359,6 +383,17 @@ __global__ __launch_bounds__(256) void mla_value_kernel(MlaParams p) {
         p.context[((long)r * p.heads + h) * p.vdim + v0 + vi] = acc[0];
 }
 
+template <int LPL>
+static void launch_attend(dim3 grid, size_t lds, hipStream_t stream, const MlaParams &p) {
+    static const bool attr = [] {
+        return hipFuncSetAttribute(reinterpret_cast<const void *>(&mla_attend_kernel<LPL>),
+                                   hipFuncAttributeMaxDynamicSharedMemorySize,
+                                   kAttendLdsBytes) == hipSuccess;
+    }();
+    (void)attr;
+    hipLaunchKernelGGL(mla_attend_kernel<LPL>, grid, dim3(256), lds, stream, p);
+}
+
 int mla_attention_core(const MlaParams &p, hipStream_t stream) {
     if (p.heads <= 0 || p.heads > kMlaMaxHeads || p.latent <= 0 || p.latent % 64 ||
         p.latent > kMlaMaxLatent || p.rope <= 0 || p.rope > 64 || (p.rope & 1) ||
@@ -368,18 +403,20 @@ int mla_attention_core(const MlaParams &p, hipStream_t stream) {
         (p.position + p.rows + kMlaKeysPerSplit - 1) / kMlaKeysPerSplit >
             (p.max_splits < kMlaMaxSplitsInLds ? p.max_splits : kMlaMaxSplitsInLds))
         return kErrArgs;
-    hipLaunchKernelGGL(mla_prep_kernel, dim3(p.rows, 1 + p.heads), dim3(256), 0, stream, p);
+    hipLaunchKernelGGL(mla_prep_kernel, dim3(p.rows, 1 + p.heads * (p.latent / kMlaAbsorbCols)),
+                       dim3(256), 0, stream, p);
     const int splits = (p.position + p.rows + kMlaKeysPerSplit - 1) / kMlaKeysPerSplit;
     const dim3 grid(splits, p.rows);
+    const size_t lds = (size_t)kMlaKeysPerSplit * p.latent * sizeof(float);
     switch (p.latent / 64) {
-    case 1: hipLaunchKernelGGL(mla_attend_kernel<1>, grid, dim3(256), 0, stream, p); break;
-    case 2: hipLaunchKernelGGL(mla_attend_kernel<2>, grid, dim3(256), 0, stream, p); break;
-    case 4: hipLaunchKernelGGL(mla_attend_kernel<4>, grid, dim3(256), 0, stream, p); break;
-    case 8: hipLaunchKernelGGL(mla_attend_kernel<8>, grid, dim3(256), 0, stream, p); break;
+    case 1: launch_attend<1>(grid, lds, stream, p); break;
+    case 2: launch_attend<2>(grid, lds, stream, p); break;
+    case 4: launch_attend<4>(grid, lds, stream, p); break;
+    case 8: launch_attend<8>(grid, lds, stream, p); break;
     default: return kErrArgs;
     }
-    hipLaunchKernelGGL(mla_merge_kernel, dim3(p.rows, p.heads, (p.latent + 127) / 128),
-                       dim3(128), 0, stream, p);
+    hipLaunchKernelGGL(mla_merge_kernel, dim3(p.rows, p.heads, (p.latent + 63) / 64), dim3(256),
+                       0, stream, p);
     hipLaunchKernelGGL(mla_value_kernel, dim3(p.rows, p.heads, (p.vdim + 31) / 32), dim3(256), 0,
                        stream, p);
     return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;

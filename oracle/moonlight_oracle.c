@@ -709,8 +709,27 @@ static int moe_layer(OrcModel *m, int layer, const float *x, int rows,
 
 /* run_tokens_fast (moonlight_metal.m:1892-1986) with the block order of
  * encode_attention_block (:678-706): h = x + attn(norm(x)); x' = h + mlp(norm(h)). */
+static int forward(OrcModel *m, const int *ids, int rows, int start_position,
+                   const int *fixed_trace, float *layer_outputs, int *route_trace,
+                   float *last_logits);
+
 int orc_forward(OrcModel *m, const int *ids, int rows, int start_position,
                 float *layer_outputs, int *route_trace, float *last_logits) {
+    return forward(m, ids, rows, start_position, NULL, layer_outputs, route_trace,
+                   last_logits);
+}
+
+/* The same forward with every MoE layer routed to the given experts
+ * (fixed_trace [layers][rows][experts_per_token], orc_moe_layer_fixed). */
+int orc_forward_routes(OrcModel *m, const int *ids, int rows, int start_position,
+                       const int *fixed_trace, float *layer_outputs, float *last_logits) {
+    return forward(m, ids, rows, start_position, fixed_trace, layer_outputs, NULL,
+                   last_logits);
+}
+
+static int forward(OrcModel *m, const int *ids, int rows, int start_position,
+                   const int *fixed_trace, float *layer_outputs, int *route_trace,
+                   float *last_logits) {
     const OrcConfig *c = &m->cfg;
     int H = c->hidden_size, K = c->experts_per_token;
     char name[512];
@@ -739,8 +758,13 @@ int orc_forward(OrcModel *m, const int *ids, int rows, int start_position,
         if (layer < c->first_dense_layer_count) {
             ok = orc_dense_mlp(m, layer, norm, rows, tmp);
         } else {
-            int *trace = route_trace ? route_trace + (int64_t)layer * rows * K : NULL;
-            ok = orc_moe_layer(m, layer, norm, rows, trace, NULL, NULL, NULL, NULL, tmp);
+            if (fixed_trace) {
+                ok = orc_moe_layer_fixed(m, layer, norm, rows,
+                                         fixed_trace + (int64_t)layer * rows * K, NULL, tmp);
+            } else {
+                int *trace = route_trace ? route_trace + (int64_t)layer * rows * K : NULL;
+                ok = orc_moe_layer(m, layer, norm, rows, trace, NULL, NULL, NULL, NULL, tmp);
+            }
         }
         if (!ok) break;
         for (int64_t i = 0; i < (int64_t)rows * H; ++i) x[i] += tmp[i];

@@ -138,6 +138,9 @@ int orc_dense_mlp(OrcModel *model, int layer, const float *x, int rows,
                   float *out);
 /* run_tokens_fast (moonlight_metal.m:1892-1986).  layer_outputs optional
  * [layers, rows, hidden]; route_trace optional [layers, rows, top_k]. */
+int orc_forward_routes(OrcModel *model, const int *ids, int rows,
+                       int start_position, const int *fixed_trace,
+                       float *layer_outputs, float *last_logits);
 int orc_forward(OrcModel *model, const int *ids, int rows, int start_position,
                 float *layer_outputs, int *route_trace, float *last_logits);
 

@@ -107,6 +107,8 @@ def lib():
                                       ctypes.c_int, ctypes.c_float, _i32p, _f32p]
         L.orc_moe_layer_fixed.argtypes = [ctypes.c_void_p, ctypes.c_int, _f32p, ctypes.c_int,
                                           _i32p, _f32p, _f32p]
+        L.orc_forward_routes.argtypes = [ctypes.c_void_p, _i32p, ctypes.c_int, ctypes.c_int,
+                                         _i32p, _f32p, _f32p]
         L.orc_dense_mlp.argtypes = [ctypes.c_void_p, ctypes.c_int, _f32p, ctypes.c_int,
                                     _f32p]
         L.orc_forward.argtypes = [ctypes.c_void_p, _i32p, ctypes.c_int, ctypes.c_int,

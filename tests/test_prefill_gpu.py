@@ -81,23 +81,37 @@ def test_tiny_prefill_gemm(tiny):
                                O.iptr(e_trace), O.fptr(e_logits))
     sess = S.Session(model, 64, 64)
     layers, logits = sess.prefill_layers(ids)
+    # The device's routes per layer.  Its selection is bit-exact on its own
+    # router logits (test_tiny_moe_gemm); against the oracle's own top-k a row
+    # can differ where two experts tie within the ~1e-4 drift of the limb
+    # GEMM, so the layer outputs are compared with the oracle forced onto the
+    # device's routes, and route mismatches must stay rare.
+    trace = np.full((L, 40, 6), -1, np.int32)
+    for l in range(cfg["first_dense_layer_count"], L):
+        trace[l] = sess.test_copy_routes(l, 40)
+        diff = [r for r in range(40) if set(trace[l, r]) != set(e_trace[l, r])]
+        print(f"[gpu] layer {l} rows routed unlike the oracle's own top-k: {diff}", flush=True)
+        assert len(diff) <= 2, (l, diff)
+    f_layers = np.empty_like(e_layers)
+    f_logits = np.empty_like(e_logits)
+    forced = CU.oracle_model(cfg, tensors, 64)
+    assert O.lib().orc_forward_routes(forced.handle, O.iptr(ids), 40, 0, O.iptr(trace),
+                                      O.fptr(f_layers), O.fptr(f_logits))
     for l in range(L):
-        err = rel_l2(layers[l], e_layers[l])
+        err = rel_l2(layers[l], f_layers[l])
         print(f"[gpu] layer {l} rel-L2 {err:.2e}", flush=True)
         assert err < 1e-3, l
-    for l in range(cfg["first_dense_layer_count"], L):
-        routes = sess.test_copy_routes(l, 40)
-        same = [set(routes[r]) == set(e_trace[l, r]) for r in range(40)]
-        assert all(same), (l, same.index(False))
-    assert rel_l2(logits, e_logits) < 1e-3
-    assert int(np.argmax(logits)) == int(np.argmax(e_logits))
-    # decode after a GEMM prefill continues from the same caches
-    greedy = int(np.argmax(e_logits))
+    assert rel_l2(logits, f_logits) < 1e-3
+    assert int(np.argmax(logits)) == int(np.argmax(f_logits))
+    # decode after a GEMM prefill continues from the same caches (the forced
+    # oracle holds the caches of the device's routes)
+    greedy = int(np.argmax(f_logits))
     dec = sess.decode(greedy)
     e_dec = np.empty_like(e_logits)
-    assert O.lib().orc_forward(orc.handle, O.iptr(np.array([greedy], np.int32)), 1, 40, None,
+    assert O.lib().orc_forward(forced.handle, O.iptr(np.array([greedy], np.int32)), 1, 40, None,
                                None, O.fptr(e_dec))
     assert rel_l2(dec, e_dec) < 1e-3
+    forced.close()
     sess.close()
     orc.close()
 
