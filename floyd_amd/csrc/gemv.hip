@@ -189,14 +189,19 @@ int gemv(const GemvParams &p_in, hipStream_t stream) {
     if (p_in.epilogue == kEpiResidual && !p_in.resid) return kErrArgs;
     const long row_bytes = row_bytes_of(p_in.fmt, p_in.I);
     const bool vector_ok =
-        row_bytes % 16 == 0 && (p_in.fmt != kQ4 || p_in.I % 2 == 0) && aligned16(p_in.w) &&
+        row_bytes % 16 == 0 && (p_in.fmt != kQ4 || p_in.I % 2 == 0) &&
+        gemv_lds_bytes_rt(p_in.fmt, 1, p_in.I) <= kMaxGemvLds && aligned16(p_in.w) &&
         (!p_in.w2 || aligned16(p_in.w2)) && aligned16(p_in.x) && p_in.x_stride % 4 == 0 &&
         (!p_in.norm_w || aligned16(p_in.norm_w));
     // token rows beyond 4 run as slices of 4 (register budget) along grid.y
     // of one launch
     bool done = false;
     if (vector_ok) {
-        const int plan_rows = p_in.rows < kMaxGemvRows ? p_in.rows : kMaxGemvRows;
+        int plan_rows = p_in.rows < kMaxGemvRows ? p_in.rows : kMaxGemvRows;
+        if (plan_rows == 3) plan_rows = 4;  // the kernel takes 1, 2 or 4 token rows
+        // the quantised x rows of a workgroup must fit its LDS
+        while (plan_rows > 1 && gemv_lds_bytes_rt(p_in.fmt, plan_rows, p_in.I) > kMaxGemvLds)
+            plan_rows /= 2;
         const GemvPlan plan = plan_gemv(p_in.fmt, p_in.O, p_in.I, plan_rows,
                                         p_in.epilogue == kEpiSiluDual);
         GemvLaunch L;

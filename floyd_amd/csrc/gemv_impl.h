@@ -274,6 +274,407 @@ __device__ __forceinline__ void gemv_block(const GemvJob<B> job) {
     }
 }
 
+// ---------------------------------------------------------------------------
+// Quantised formats (q8, q4): int8-limb dot products.
+//
+// Every workgroup first splits its token rows of x (RMSNorm'ed when norm_w is
+// set) into LDS: per 16-byte weight chunk (16 q8 or 32 q4 elements) a scale
+// sc = amax / 2^22 and three int8 limbs per element,
+//     v ~= sc * (65536 * hi + 256 * mid + lo),  |65536 hi + 256 mid + lo| <= 2^22,
+// i.e. 23 significant bits against the chunk's own max -- the precision of an
+// fp32 operand.  A chunk's share of a row is then exact integer dot products
+// of the stored weights with each limb (v_dot4_i32_i8: 4 products and their
+// sum per instruction), combined and scaled once in fp32:
+//     sum_chunk q * v ~= sc * (65536 * dot(q, hi) + (256 * dot(q, mid) + dot(q, lo))).
+// q8 weights are the stored int8 values; q4 weights enter as the stored
+// nibbles u = q + 8 (0..15, valid int8 operands) and 8 * (sum of the limb
+// values) of the chunk is subtracted once per chunk.  The rounding of v is at
+// most 0.75 * amax_chunk / 2^22 per element and the in-chunk sums are exact,
+// so results agree with the fp32 matmul to fp32 rounding (like a different
+// summation order).  The arithmetic drops from ~2.3 VALU instructions per
+// weight (convert + fma) to ~0.9 (q8) / ~1.3 (q4), which is what kept the fp32
+// form from streaming at HBM rate.
+//
+// Loads are ordered for the in-order vector memory counter: x (and norm_w),
+// the epilogue's scale / residual values, then the first weight tile, all
+// unpredicated (clamped addresses), so the prologue waits only for x while the
+// weights are in flight.
+// ---------------------------------------------------------------------------
+constexpr int kLimbQuantMax = 1 << 22;  // |65536 hi + 256 mid + lo| bound
+constexpr int kLimbPassElems = 2048;    // x elements quantised per workgroup pass
+
+struct LimbInfo {
+    float scale;
+    int bias_hi;   // q4: 8 * sum(hi) of the chunk, else 0
+    int bias_low;  // q4: 8 * sum(256 mid + lo) of the chunk, else 0
+    int pad;
+};
+
+// LDS bytes of one token row of width I: hi, mid and lo limbs (I bytes each)
+// and a LimbInfo per 16-byte weight chunk.
+__host__ __device__ constexpr int limb_row_lds(int fmt, int I) {
+    return 3 * I + 16 * (row_bytes_of(fmt, I) / 16);
+}
+
+__device__ __forceinline__ int sdot4(int a, int b, int c) {
+    return __builtin_amdgcn_sdot4(a, b, c, false);
+}
+
+__device__ __forceinline__ unsigned pack_i8x4(int a, int b, int c, int d) {
+    return (unsigned)(a & 255) | ((unsigned)(b & 255) << 8) | ((unsigned)(c & 255) << 16) |
+           ((unsigned)(d & 255) << 24);
+}
+
+// Quantises the 8 elements e0 .. e0 + 7 of one token row held by this thread
+// (TPG neighbouring threads share a chunk).  Limb layout per row: hi at 0, mid
+// at I, lo at 2 I.  q4 limbs are stored per 8 elements as the even-element
+// dword then the odd-element dword (the order the nibble masks produce), each
+// chunk's 32 bytes split in two 16-byte halves held nc * 16 bytes apart so a
+// lane's 16-byte LDS reads are contiguous across lanes.
+template <int FMT>
+__device__ __forceinline__ void limb_quantise8(const float (&v)[8], bool in, int e0,
+                                               unsigned char *row_lds, int I, int nc) {
+    constexpr int EPC = FmtTraits<FMT>::kElemsPerChunk;
+    constexpr int TPG = EPC / 8;
+    float m = 0.0f, bad = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        m = fmaxf(m, fabsf(v[i]));
+        bad = fmaf(v[i], 0.0f, bad);  // NaN when some element is not finite
+    }
+#pragma unroll
+    for (int o = 1; o < TPG; o <<= 1) {
+        m = fmaxf(m, __shfl_xor(m, o, kWave));
+        bad += __shfl_xor(bad, o, kWave);
+    }
+    const float inv = m > 0.0f ? (float)kLimbQuantMax / m : 0.0f;
+    int h[8], md[8], l[8], hs = 0, ms = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        float q = rintf(v[i] * inv);
+        q = fminf(fmaxf(q, -(float)kLimbQuantMax), (float)kLimbQuantMax);
+        const int qi = (int)q;
+        // floor divisions with offsets that keep every limb in int8:
+        // hi in [-64, 64], rem in [-32896, 32639], mid and lo in [-128, 127]
+        h[i] = (qi + 32896) >> 16;
+        const int rem = qi - h[i] * 65536;
+        md[i] = (rem + 128) >> 8;
+        l[i] = rem - md[i] * 256;
+        hs += h[i];
+        ms += rem;
+    }
+    unsigned H[2], M[2], L[2];
+    if constexpr (FMT == kQ4) {
+        H[0] = pack_i8x4(h[0], h[2], h[4], h[6]);
+        H[1] = pack_i8x4(h[1], h[3], h[5], h[7]);
+        M[0] = pack_i8x4(md[0], md[2], md[4], md[6]);
+        M[1] = pack_i8x4(md[1], md[3], md[5], md[7]);
+        L[0] = pack_i8x4(l[0], l[2], l[4], l[6]);
+        L[1] = pack_i8x4(l[1], l[3], l[5], l[7]);
+    } else {
+        H[0] = pack_i8x4(h[0], h[1], h[2], h[3]);
+        H[1] = pack_i8x4(h[4], h[5], h[6], h[7]);
+        M[0] = pack_i8x4(md[0], md[1], md[2], md[3]);
+        M[1] = pack_i8x4(md[4], md[5], md[6], md[7]);
+        L[0] = pack_i8x4(l[0], l[1], l[2], l[3]);
+        L[1] = pack_i8x4(l[4], l[5], l[6], l[7]);
+    }
+#pragma unroll
+    for (int o = 1; o < TPG; o <<= 1) {
+        hs += __shfl_xor(hs, o, kWave);
+        ms += __shfl_xor(ms, o, kWave);
+    }
+    if (!in) return;
+    const int c = e0 / EPC, g = (e0 % EPC) / 8;
+    const int off = (FMT == kQ4 ? (g >> 1) * 16 * nc : 0) + 16 * c + 8 * (g & 1);
+    typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+    *reinterpret_cast<u32x2 *>(row_lds + off) = u32x2{H[0], H[1]};
+    *reinterpret_cast<u32x2 *>(row_lds + I + off) = u32x2{M[0], M[1]};
+    *reinterpret_cast<u32x2 *>(row_lds + 2 * I + off) = u32x2{L[0], L[1]};
+    if (g == 0) {
+        LimbInfo info;
+        info.scale = m / (float)kLimbQuantMax + bad;
+        info.bias_hi = FMT == kQ4 ? 8 * hs : 0;
+        info.bias_low = FMT == kQ4 ? 8 * ms : 0;
+        info.pad = 0;
+        reinterpret_cast<LimbInfo *>(row_lds + 3 * I)[c] = info;
+    }
+}
+
+// One 16-byte weight chunk against the limbs of chunk c of one token row:
+// the chunk's integer dot product as 65536 * dot_hi + dot_low (bias removed),
+// returned in fp32.
+template <int FMT>
+__device__ __forceinline__ float limb_chunk_dot(u32x4 w, const unsigned char *row_lds, int I,
+                                                int nc, int c, const LimbInfo &info) {
+    const unsigned d[4] = {w.x, w.y, w.z, w.w};
+    int hd = 0, mdd = 0, ld = 0;
+    if constexpr (FMT == kQ4) {
+        u32x4 lv[3][2];
+#pragma unroll
+        for (int t = 0; t < 3; ++t) {
+            lv[t][0] = *reinterpret_cast<const u32x4 *>(row_lds + t * I + 16 * c);
+            lv[t][1] = *reinterpret_cast<const u32x4 *>(row_lds + t * I + 16 * nc + 16 * c);
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int ev = (int)(d[j] & 0x0F0F0F0Fu), od = (int)((d[j] >> 4) & 0x0F0F0F0Fu);
+            const int half = j >> 1, k = 2 * (j & 1);
+            hd = sdot4(ev, (int)lv[0][half][k], hd);
+            hd = sdot4(od, (int)lv[0][half][k + 1], hd);
+            mdd = sdot4(ev, (int)lv[1][half][k], mdd);
+            mdd = sdot4(od, (int)lv[1][half][k + 1], mdd);
+            ld = sdot4(ev, (int)lv[2][half][k], ld);
+            ld = sdot4(od, (int)lv[2][half][k + 1], ld);
+        }
+    } else {
+        u32x4 lv[3];
+#pragma unroll
+        for (int t = 0; t < 3; ++t) lv[t] = *reinterpret_cast<const u32x4 *>(row_lds + t * I + 16 * c);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            hd = sdot4((int)d[j], (int)lv[0][j], hd);
+            mdd = sdot4((int)d[j], (int)lv[1][j], mdd);
+            ld = sdot4((int)d[j], (int)lv[2][j], ld);
+        }
+    }
+    // |hd| <= 2^17 and |256 mdd + ld| < 2^27: exact in int32, the fp32 sum
+    // rounds once
+    return fmaf((float)(hd - info.bias_hi), 65536.0f, (float)(mdd * 256 + ld - info.bias_low));
+}
+
+// x passes held in registers across the weight issue (the rest of a wide row
+// is loaded after it).
+template <int B>
+constexpr int limb_pre_passes() {
+    return B == 1 ? 2 : 1;
+}
+
+// `after_job`: the workgroup ran another job on the same LDS just before.
+template <int FMT, int B, int KT, int LPR, int R, int KS>
+__device__ __forceinline__ void limb_block(const GemvJob<B> job, unsigned char *lds,
+                                           bool after_job) {
+    constexpr int GPW = kWave / LPR;
+    constexpr int NV = R * B;
+    constexpr int NJP = limb_pre_passes<B>();
+    static_assert(NV <= LPR, "partial sums exceed the lane group");
+    static_assert(KS == 1 || LPR == kWave, "k-split needs whole-wave row groups");
+    __shared__ float red[4][NV];
+    __shared__ float ss_red[4][B];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & (kWave - 1);
+    const int wave = tid / kWave;
+    const int group = lane / LPR;
+    const int li = lane & (LPR - 1);
+    const bool dual = job.epilogue == kEpiSiluDual;
+    const int out_per_group = dual ? R / 2 : R;
+    const int row_wave = KS == 1 ? job.row_block * 4 + wave : job.row_block;
+    const int kpart = KS == 1 ? 0 : wave;
+    const int out0 = (row_wave * GPW + group) * out_per_group;
+    // whole workgroups past the end leave (the prologue below synchronises)
+    if ((KS > 1 ? job.row_block : job.row_block * 4) * GPW * out_per_group >= job.O) return;
+
+    const int I = job.I;
+    const int row_bytes = row_bytes_of(FMT, I);
+    const int nc = row_bytes / 16;
+    const int lds_row = limb_row_lds(FMT, I);
+    const int npass = (I + kLimbPassElems - 1) / kLimbPassElems;
+
+    // ---- 1. x (and norm_w) of the first passes
+    f32x4 xv[NJP][B][2];
+    f32x4 nv[NJP][2];
+#pragma unroll
+    for (int j = 0; j < NJP; ++j) {
+        if (j < npass) {
+            const int e0 = tid * 8 + j * kLimbPassElems;
+            const int ec = e0 < I ? e0 : 0;
+#pragma unroll
+            for (int b = 0; b < B; ++b) {
+                xv[j][b][0] = load_f4(job.x[b] + ec);
+                xv[j][b][1] = load_f4(job.x[b] + ec + 4);
+            }
+            if (job.norm_w) {
+                nv[j][0] = load_f4(job.norm_w + ec);
+                nv[j][1] = load_f4(job.norm_w + ec + 4);
+            }
+        }
+    }
+    // ---- 2. epilogue operands of the value this lane will write
+    const int vi = butterfly_index<NV, LPR>(lane);
+    const int vr = vi / B, vb = vi % B;
+    const int vrow = out0 + vr;
+    const int vrow_c = vrow < job.O ? vrow : job.O - 1;
+    float *yb = job.y[0];
+    const float *rb = job.resid[0];
+#pragma unroll
+    for (int i = 1; i < B; ++i) {
+        if (vb == i) {  // compare chain: a lane-indexed pointer array would spill
+            yb = job.y[i];
+            rb = job.resid[i];
+        }
+    }
+    const float s_row = load_global_f32(job.s + vrow_c);
+    const float s2_row = dual ? load_global_f32(job.s2 + vrow_c) : 0.0f;
+    const float resid_row = job.epilogue == kEpiResidual ? load_global_f32(rb + vrow_c) : 0.0f;
+    // ---- 3. the first weight tile
+    const int step = KS * KT * LPR;
+    u32x4 wv[R][KT];
+    auto load_tile = [&](int kt0) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            int row;
+            const uint8_t *base;
+            if (dual) {
+                row = out0 + (r < R / 2 ? r : r - R / 2);
+                base = r < R / 2 ? job.w : job.w2;
+            } else {
+                row = out0 + r;
+                base = job.w;
+            }
+            const int row_c = row < job.O ? row : job.O - 1;
+#pragma unroll
+            for (int k = 0; k < KT; ++k) {
+                const int c = kt0 + li + LPR * k;
+                const u32x4 v = load_stream16(base + (long)row_c * row_bytes + (c < nc ? c : 0) * 16);
+                wv[r][k] = (row < job.O && c < nc) ? v : u32x4{0u, 0u, 0u, 0u};
+            }
+        }
+    };
+    load_tile(kpart * KT * LPR);
+    // the previous job's LDS readers are done before anything is overwritten
+    if (after_job) __syncthreads();
+
+    // ---- 4. RMSNorm statistics (workgroup reduction)
+    float inv_rms[B];
+#pragma unroll
+    for (int b = 0; b < B; ++b) inv_rms[b] = 1.0f;
+    if (job.norm_w) {
+        float ss[B];
+#pragma unroll
+        for (int b = 0; b < B; ++b) ss[b] = 0.0f;
+#pragma unroll
+        for (int j = 0; j < NJP; ++j) {
+            if (j < npass && tid * 8 + j * kLimbPassElems < I) {
+#pragma unroll
+                for (int b = 0; b < B; ++b)
+#pragma unroll
+                    for (int h = 0; h < 2; ++h)
+                        ss[b] += xv[j][b][h].x * xv[j][b][h].x + xv[j][b][h].y * xv[j][b][h].y +
+                                 xv[j][b][h].z * xv[j][b][h].z + xv[j][b][h].w * xv[j][b][h].w;
+            }
+        }
+        for (int j = NJP; j < npass; ++j) {
+            const int e0 = tid * 8 + j * kLimbPassElems;
+            if (e0 < I) {
+#pragma unroll
+                for (int b = 0; b < B; ++b)
+#pragma unroll
+                    for (int h = 0; h < 2; ++h) {
+                        const f32x4 t = load_f4(job.x[b] + e0 + 4 * h);
+                        ss[b] += t.x * t.x + t.y * t.y + t.z * t.z + t.w * t.w;
+                    }
+            }
+        }
+#pragma unroll
+        for (int b = 0; b < B; ++b) {
+            const float w_ss = wave_sum(ss[b]);
+            if (lane == 0) ss_red[wave][b] = w_ss;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int b = 0; b < B; ++b)
+            inv_rms[b] = 1.0f / sqrtf(((ss_red[0][b] + ss_red[1][b]) + (ss_red[2][b] + ss_red[3][b])) /
+                                          (float)I + job.eps);
+    }
+
+    // ---- 5. quantise x into LDS
+    auto quantise_pass = [&](const f32x4 (&xp)[2], const f32x4 (&np)[2], int b, int e0) {
+        float v[8] = {xp[0].x, xp[0].y, xp[0].z, xp[0].w, xp[1].x, xp[1].y, xp[1].z, xp[1].w};
+        if (job.norm_w) {
+            const float n[8] = {np[0].x, np[0].y, np[0].z, np[0].w,
+                                np[1].x, np[1].y, np[1].z, np[1].w};
+#pragma unroll
+            for (int i = 0; i < 8; ++i) v[i] = v[i] * inv_rms[b] * n[i];
+        }
+        limb_quantise8<FMT>(v, e0 < I && b < job.rows, e0, lds + b * lds_row, I, nc);
+    };
+#pragma unroll
+    for (int j = 0; j < NJP; ++j) {
+        if (j < npass) {
+            const int e0 = tid * 8 + j * kLimbPassElems;
+#pragma unroll
+            for (int b = 0; b < B; ++b) quantise_pass(xv[j][b], nv[j], b, e0);
+        }
+    }
+    for (int j = NJP; j < npass; ++j) {
+        const int e0 = tid * 8 + j * kLimbPassElems;
+        const int ec = e0 < I ? e0 : 0;
+        f32x4 np[2] = {f32x4{1.f, 1.f, 1.f, 1.f}, f32x4{1.f, 1.f, 1.f, 1.f}};
+        if (job.norm_w) {
+            np[0] = load_f4(job.norm_w + ec);
+            np[1] = load_f4(job.norm_w + ec + 4);
+        }
+#pragma unroll
+        for (int b = 0; b < B; ++b) {
+            const f32x4 xp[2] = {load_f4(job.x[b] + ec), load_f4(job.x[b] + ec + 4)};
+            quantise_pass(xp, np, b, e0);
+        }
+    }
+    __syncthreads();
+
+    // ---- 6. dot products
+    float acc[NV];
+#pragma unroll
+    for (int v = 0; v < NV; ++v) acc[v] = 0.0f;
+    for (int kt0 = kpart * KT * LPR; kt0 < nc; kt0 += step) {
+        if (kt0 != kpart * KT * LPR) load_tile(kt0);
+#pragma unroll
+        for (int k = 0; k < KT; ++k) {
+            const int c = kt0 + li + LPR * k;
+            const bool cok = c < nc;
+            const int cc = cok ? c : 0;
+#pragma unroll
+            for (int b = 0; b < B; ++b) {
+                if (b < job.rows) {
+                    const unsigned char *row_lds = lds + b * lds_row;
+                    const LimbInfo info = reinterpret_cast<const LimbInfo *>(row_lds + 3 * I)[cc];
+                    const float sc = cok ? info.scale : 0.0f;
+#pragma unroll
+                    for (int r = 0; r < R; ++r) {
+                        const float dot = limb_chunk_dot<FMT>(wv[r][k], row_lds, I, nc, cc, info);
+                        acc[r * B + b] = fmaf(dot, sc, acc[r * B + b]);
+                    }
+                }
+            }
+        }
+    }
+
+    // ---- 7. reduction and epilogue
+    butterfly_reduce<NV, LPR>(acc, lane);
+    const bool writer = butterfly_writer<NV, LPR>(lane);
+    float value = acc[0];
+    if constexpr (KS > 1) {
+        if (writer) red[wave][vi] = value;
+        __syncthreads();
+        value = (red[0][vi] + red[1][vi]) + (red[2][vi] + red[3][vi]);
+        if (wave != 0) return;
+    }
+    if (dual) {
+        // the up-projection partner of value index vi is vi + NV/2, held by the
+        // lane across the first butterfly offset
+        const float partner = __shfl_xor(value, LPR / 2, kWave);
+        if (writer && vr < R / 2 && vrow < job.O && vb < job.rows)
+            yb[vrow] = silu(value * s_row) * (partner * s2_row);
+        return;
+    }
+    if (writer && vrow < job.O && vb < job.rows) {
+        float out = value * s_row;
+        if (job.epilogue == kEpiResidual) out = resid_row + out;
+        yb[vrow] = out;
+    }
+}
+
 // Grouped expert launches (MoE): blockIdx.y selects a task -- one active routed
 // expert (in first-appearance order) or, last, the fused shared expert -- and
 // the workgroup loops over that task's token rows in groups of B.  Token rows are
@@ -285,9 +686,17 @@ struct ExpertWeights {
     const float *gate_s, *up_s, *down_s;
 };
 
+// One active routed expert of a batch, as the routing kernels write it: its
+// weights, its token rows and their offset in the compact lists.
+struct ExpertTask {
+    ExpertWeights w;
+    int count, offset;
+};
+
 struct ExpertGemvParams {
     int stage = 0;  // 0: gate/up + SwiGLU, 1: down
     const ExpertWeights *experts = nullptr;  // device table [E]
+    const ExpertTask *tasks = nullptr;       // optional per-task table (one lookup)
     const int *n_unique = nullptr;           // route tables (device)
     const int *unique = nullptr;
     const int *counts = nullptr;
@@ -314,7 +723,22 @@ struct GemvLaunch {
 };
 
 template <int MODE, int FMT, int B, int KT, int LPR, int R, int KS>
+__device__ __forceinline__ void run_job(const GemvJob<B> &job, unsigned char *lds, bool after_job) {
+    if constexpr (FMT == kF32)
+        gemv_block<FMT, B, KT, LPR, R, KS>(job);
+    else
+        limb_block<FMT, B, KT, LPR, R, KS>(job, lds, after_job);
+}
+
+// Dynamic LDS of a launch: the quantised x rows of its widest job.
+template <int FMT, int B>
+__host__ __device__ constexpr int gemv_lds_bytes(int max_I) {
+    return FMT == kF32 ? 0 : B * limb_row_lds(FMT, max_I);
+}
+
+template <int MODE, int FMT, int B, int KT, int LPR, int R, int KS>
 __global__ __launch_bounds__(256) void gemv_kernel(GemvLaunch L) {
+    extern __shared__ __align__(16) unsigned char gemv_lds[];
     GemvJob<B> job;
     job.row_block = blockIdx.x;
     if constexpr (MODE == 0) {
@@ -338,7 +762,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvLaunch L) {
         job.norm_w = p.norm_w;
         job.eps = p.eps;
         job.epilogue = p.epilogue;
-        gemv_block<FMT, B, KT, LPR, R, KS>(job);
+        run_job<MODE, FMT, B, KT, LPR, R, KS>(job, gemv_lds, false);
     } else {
         const ExpertGemvParams &p = L.expert;
         const int task = blockIdx.y;
@@ -354,12 +778,21 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvLaunch L) {
             job.O = p.stage == 0 ? p.shared_width : p.hidden;
             job.I = p.stage == 0 ? p.hidden : p.shared_width;
         } else {
-            if (task >= *p.n_unique) return;
-            const int e = p.unique[task];
-            n = p.counts[e];
-            off = p.offsets[e];
+            ExpertWeights ew;
+            if (p.tasks) {
+                const ExpertTask tk = p.tasks[task];
+                if (tk.count == 0) return;
+                n = tk.count;
+                off = tk.offset;
+                ew = tk.w;
+            } else {
+                if (task >= *p.n_unique) return;
+                const int e = p.unique[task];
+                n = p.counts[e];
+                off = p.offsets[e];
+                ew = p.experts[e];
+            }
             list = p.rows + off;
-            const ExpertWeights ew = p.experts[e];
             job.w = p.stage == 0 ? ew.gate : ew.down;
             job.s = p.stage == 0 ? ew.gate_s : ew.down_s;
             job.w2 = ew.up;
@@ -388,9 +821,15 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvLaunch L) {
                 }
                 job.resid[b] = nullptr;
             }
-            gemv_block<FMT, B, KT, LPR, R, KS>(job);
+            run_job<MODE, FMT, B, KT, LPR, R, KS>(job, gemv_lds, g0 > 0);
         }
     }
+}
+
+// Largest dynamic LDS a GEMV launch may ask for (the quantised x rows).
+constexpr int kMaxGemvLds = 150 * 1024;
+inline int gemv_lds_bytes_rt(int fmt, int b, int I) {
+    return fmt == kF32 ? 0 : b * limb_row_lds(fmt, I);
 }
 
 // Launch geometry chosen by the host (see gemv.hip, plan_gemv).
@@ -401,12 +840,28 @@ struct GemvPlan {
 // MODE 0 grids cover the plain matrix; MODE 1 callers pass their own grid.
 template <int MODE, int FMT, int B, int KT, int LPR, int R, int KS>
 static void launch_gemv(const GemvLaunch &L, dim3 grid, hipStream_t stream) {
+    int max_I;
     if constexpr (MODE == 0) {
         const int per_block = rows_per_block<LPR, R, KS>(L.plain.epilogue == kEpiSiluDual);
         grid = dim3((unsigned)((L.plain.O + per_block - 1) / per_block),
                     (unsigned)((L.plain.rows + B - 1) / B));
+        max_I = L.plain.I;
+    } else {
+        const ExpertGemvParams &e = L.expert;
+        max_I = e.stage == 0 ? e.hidden : (e.inter > e.shared_width ? e.inter : e.shared_width);
     }
-    hipLaunchKernelGGL((gemv_kernel<MODE, FMT, B, KT, LPR, R, KS>), grid, dim3(256), 0, stream, L);
+    const int lds = gemv_lds_bytes<FMT, B>(max_I);
+    if (lds > 64 * 1024) {
+        static bool raised = false;  // per instantiation
+        if (!raised) {
+            (void)hipFuncSetAttribute(
+                reinterpret_cast<const void *>(&gemv_kernel<MODE, FMT, B, KT, LPR, R, KS>),
+                hipFuncAttributeMaxDynamicSharedMemorySize, kMaxGemvLds);
+            raised = true;
+        }
+    }
+    hipLaunchKernelGGL((gemv_kernel<MODE, FMT, B, KT, LPR, R, KS>), grid, dim3(256), lds, stream,
+                       L);
 }
 
 template <int MODE, int FMT, int B>

@@ -25,8 +25,19 @@ struct RouteParams {
     // optional [rows, top_k] expert ids given by the caller: weights come from
     // their scores (moe_route_fixed, moe_route.h:76-87) instead of a top-k
     const int *fixed_ids = nullptr;
+    // optional: the per-task table of the grouped expert launches
+    const ExpertWeights *expert_table = nullptr;  // device [experts]
+    ExpertTask *tasks = nullptr;                  // out [task_slots]
+    int task_slots = 0;
 };
 int route_topk(const RouteParams &p, hipStream_t stream);
+
+// Router matvec (f32 router [experts][width], x RMSNorm'ed with norm_w) and
+// routing of at most kFusedRouteMaxRows token rows in one launch; `counter` is
+// a device word that is 0 between calls.
+constexpr int kFusedRouteMaxRows = 4;
+int router_route(const RouteParams &p, const float *x, const float *norm_w, float eps,
+                 const float *router, int width, unsigned *counter, hipStream_t stream);
 
 // f32 router logits of many token rows, x RMSNorm'ed with norm_w when it is
 // non-null: logits [rows, experts].
@@ -53,6 +64,7 @@ struct ExpertFfnParams {
     const float *shared_gate_s = nullptr, *shared_up_s = nullptr, *shared_down_s = nullptr;
     const int *n_unique = nullptr, *unique = nullptr, *counts = nullptr, *offsets = nullptr;
     const int *list_rows = nullptr;
+    const ExpertTask *tasks = nullptr;  // optional per-task table from the routing
     const float *x = nullptr;       // residual stream [rows, hidden] (normalised on the fly)
     const float *norm_w = nullptr;  // post-attention RMSNorm weight
     float eps = 1e-5f;

@@ -51,8 +51,9 @@ __device__ void route_row(const RouteParams &p, int r, int lane, int *lds_ids) {
             sel[j] = -INFINITY;
         }
     }
-    float wk[kMaxTopK];
-    int ids[kMaxTopK];
+    // lane k keeps the k-th id and weight; the weight sum runs in slot order
+    int my_id = -1;
+    float my_w = 0.0f, wsum = 0.0f;
     if (p.fixed_ids) {
         for (int k = 0; k < K; ++k) {
             const int e = p.fixed_ids[(long)r * K + k];
@@ -62,8 +63,12 @@ __device__ void route_row(const RouteParams &p, int r, int lane, int *lds_ids) {
 #pragma unroll
             for (int j = 0; j < kMaxExperts / 64; ++j)
                 if (lane == owner && j == slot_j) chosen = score[j];
-            ids[k] = valid ? e : -1;
-            wk[k] = __shfl(chosen, owner, 64);
+            const float w = __shfl(chosen, owner, 64);
+            if (lane == k) {
+                my_id = valid ? e : -1;
+                my_w = w;
+            }
+            wsum += w;
         }
     } else {
         unsigned taken = 0;  // bit j: lane's expert lane + 64 j already chosen
@@ -99,114 +104,130 @@ __device__ void route_row(const RouteParams &p, int r, int lane, int *lds_ids) {
                     taken |= 1u << j;
                     chosen = score[j];
                 }
-            ids[k] = best_e;
-            wk[k] = __shfl(chosen, owner, 64);
+            const float w = __shfl(chosen, owner, 64);
+            if (lane == k) {
+                my_id = best_e;
+                my_w = w;
+            }
+            wsum += w;
         }
     }
-    float wsum = 1.0f;
-    if (p.normalize) {
-        wsum = 0.0f;
-        for (int k = 0; k < K; ++k) wsum += wk[k];
+    if (p.normalize)
         wsum += 1e-20f;
-    }
+    else
+        wsum = 1.0f;
     if (lane < K) {
-        int id = ids[0];
-        float w = wk[0];
-        for (int k = 1; k < K; ++k)
-            if (lane == k) {
-                id = ids[k];
-                w = wk[k];
-            }
-        p.ids[(long)r * K + lane] = id;
-        if (lds_ids) lds_ids[r * K + lane] = id;
-        p.weights[(long)r * K + lane] = w / wsum * p.routed_scale;
-        if (p.trace) p.trace[(long)r * K + lane] = id;
+        p.ids[(long)r * K + lane] = my_id;
+        if (lds_ids) lds_ids[r * K + lane] = my_id;
+        p.weights[(long)r * K + lane] = my_w / wsum * p.routed_scale;
+        if (p.trace) p.trace[(long)r * K + lane] = my_id;
     }
 }
 
-// One workgroup: routing of every token row, then the route tables (small
-// batches: decode and short appends).
-__global__ __launch_bounds__(256) void route_kernel(RouteParams p) {
-    __shared__ int first_pos[kMaxExperts];
-    __shared__ int counts[kMaxExperts];
-    __shared__ int offsets[kMaxExperts];
-    __shared__ int lds_ids[kRouteLdsIds];  // selected ids when rows*top_k fits
-    __shared__ unsigned long long first_mask[kRouteMaxPositions / 64];
-    __shared__ int word_prefix[kRouteMaxPositions / 64];
-    __shared__ int rank_of[kMaxExperts], count_by_rank[kMaxExperts], offset_by_rank[kMaxExperts];
-    __shared__ int unique_total;
+// Route tables of a small batch (rows * top_k <= kRouteFusedMaxPositions,
+// ids already in LDS), built by one workgroup of 4 waves.
+constexpr int kRouteFusedMaxPositions = 1024;
+struct RouteLds {
+    int first_pos[kMaxExperts], counts[kMaxExperts], offsets[kMaxExperts];
+    int ids[kRouteFusedMaxPositions];
+    unsigned long long first_mask[kRouteFusedMaxPositions / 64];
+    int word_prefix[kRouteFusedMaxPositions / 64];
+    int rank_of[kMaxExperts], count_by_rank[kMaxExperts], offset_by_rank[kMaxExperts];
+    int unique_total;
+};
+
+// The per-task table of the grouped expert launches: entry u describes the
+// u-th active expert (weights, rows, list offset); entries up to task_slots
+// past the active experts get count 0.
+__device__ void write_tasks(const RouteParams &p, const int *counts, const int *offsets,
+                            const int *rank_of, int n_unique) {
+    if (!p.tasks) return;
+    for (int e = threadIdx.x; e < p.experts; e += blockDim.x) {
+        const int rk = rank_of[e];
+        if (rk >= 0 && rk < p.task_slots) {
+            ExpertTask tk;
+            tk.w = p.expert_table[e];
+            tk.count = counts[e];
+            tk.offset = offsets[e];
+            p.tasks[rk] = tk;
+        }
+    }
+    for (int u = n_unique + threadIdx.x; u < p.task_slots; u += blockDim.x) p.tasks[u] = ExpertTask{};
+}
+
+__device__ void small_tables(const RouteParams &p, RouteLds &L) {
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
     const int E = p.experts, K = p.top_k, M = p.rows;
     const int n_pos = M * K;
-    const bool ids_in_lds = n_pos <= kRouteLdsIds;
-
-    for (int r = wave; r < M; r += 4) route_row(p, r, lane, ids_in_lds ? lds_ids : nullptr);
     for (int e = tid; e < E; e += blockDim.x) {
-        first_pos[e] = INT_MAX;
-        counts[e] = 0;
+        L.first_pos[e] = INT_MAX;
+        L.counts[e] = 0;
     }
     __syncthreads();
-
-    // ---- tables: first appearance and count per expert (order-independent
-    // atomics on LDS), then ranks in first-appearance order
+    // first appearance and count per expert (order-independent LDS atomics)
     for (int q = tid; q < n_pos; q += blockDim.x) {
-        const int e = ids_in_lds ? lds_ids[q] : p.ids[q];
+        const int e = L.ids[q];
         if (e < 0 || e >= E) {
             p.list_pos[q] = -1;
             *p.error = 1;  // prepare_route_tables rejects such ids (moonlight_metal.m:545)
             continue;
         }
-        atomicMin(&first_pos[e], q);
-        atomicAdd(&counts[e], 1);
+        atomicMin(&L.first_pos[e], q);
+        atomicAdd(&L.counts[e], 1);
     }
     __syncthreads();
-    // first-appearance ranks without serial scans: a bit per list position
-    // that is the first occurrence of its expert; the rank of expert e is the
-    // number of such bits before first_pos[e]
+    // first-appearance ranks: a bit per list position that is the first
+    // occurrence of its expert; the rank of e counts those bits before it
     const int nwords = (n_pos + 63) / 64;
     for (int w = wave; w < nwords; w += 4) {
         const int q = w * 64 + lane;
         bool first = false;
         if (q < n_pos) {
-            const int e = ids_in_lds ? lds_ids[q] : p.ids[q];
-            first = e >= 0 && e < E && first_pos[e] == q;
+            const int e = L.ids[q];
+            first = e >= 0 && e < E && L.first_pos[e] == q;
         }
         const unsigned long long m = __ballot(first);
-        if (lane == 0) first_mask[w] = m;
+        if (lane == 0) L.first_mask[w] = m;
     }
     __syncthreads();
-    if (tid == 0) {
-        int acc = 0;
-        for (int w = 0; w < nwords; ++w) {
-            word_prefix[w] = acc;
-            acc += __popcll(first_mask[w]);
+    if (wave == 0) {  // word prefix (<= 16 words) by a wave scan
+        const int cnt = lane < nwords ? __popcll(L.first_mask[lane]) : 0;
+        int incl = cnt;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const int v = __shfl_up(incl, o, 64);
+            if (lane >= o) incl += v;
         }
-        unique_total = acc;
-        *p.n_unique = acc;
+        if (lane < nwords) L.word_prefix[lane] = incl - cnt;
+        const int total = __shfl(incl, 63, 64);
+        if (lane == 0) {
+            L.unique_total = total;
+            *p.n_unique = total;
+        }
     }
     __syncthreads();
     for (int e = tid; e < E; e += blockDim.x) {
-        rank_of[e] = -1;
-        if (counts[e] > 0) {
-            const int q = first_pos[e];
-            const int rank = word_prefix[q / 64] +
-                             __popcll(first_mask[q / 64] & ((1ull << (q % 64)) - 1ull));
-            rank_of[e] = rank;
-            count_by_rank[rank] = counts[e];
+        L.rank_of[e] = -1;
+        if (L.counts[e] > 0) {
+            const int q = L.first_pos[e];
+            const int rank = L.word_prefix[q / 64] +
+                             __popcll(L.first_mask[q / 64] & ((1ull << (q % 64)) - 1ull));
+            L.rank_of[e] = rank;
+            L.count_by_rank[rank] = L.counts[e];
             p.unique[rank] = e;
         }
-        p.counts[e] = counts[e];
+        p.counts[e] = L.counts[e];
     }
     __syncthreads();
     if (wave == 0) {  // exclusive scan of the counts in rank order (<= 256 ranks)
         int c4[4], local = 0;
-        const int n_unique = unique_total;
+        const int n_unique = L.unique_total;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int rk = lane * 4 + i;
-            c4[i] = rk < n_unique ? count_by_rank[rk] : 0;
+            c4[i] = rk < n_unique ? L.count_by_rank[rk] : 0;
             local += c4[i];
         }
         int incl = local;
@@ -219,27 +240,27 @@ __global__ __launch_bounds__(256) void route_kernel(RouteParams p) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int rk = lane * 4 + i;
-            if (rk < n_unique) offset_by_rank[rk] = run;
+            if (rk < n_unique) L.offset_by_rank[rk] = run;
             run += c4[i];
         }
     }
     __syncthreads();
     for (int e = tid; e < E; e += blockDim.x) {
-        if (rank_of[e] >= 0) {
-            offsets[e] = offset_by_rank[rank_of[e]];
-            p.offsets[e] = offsets[e];
+        if (L.rank_of[e] >= 0) {
+            L.offsets[e] = L.offset_by_rank[L.rank_of[e]];
+            p.offsets[e] = L.offsets[e];
         }
     }
     __syncthreads();
-
-    // ---- compact lists: entries of expert e in (row, slot) order
+    write_tasks(p, L.counts, L.offsets, L.rank_of, L.unique_total);
+    // compact lists: entries of expert e in (row, slot) order
     for (int e = wave; e < E; e += 4) {
-        if (counts[e] == 0) continue;
+        if (L.counts[e] == 0) continue;
         int running = 0;
-        const int base = offsets[e];
+        const int base = L.offsets[e];
         for (int q0 = 0; q0 < n_pos; q0 += 64) {
             const int q = q0 + lane;
-            const bool match = q < n_pos && (ids_in_lds ? lds_ids[q] : p.ids[q]) == e;
+            const bool match = q < n_pos && L.ids[q] == e;
             const unsigned long long mask = __ballot(match);
             if (match) {
                 const int j = running + __popcll(mask & ((1ull << lane) - 1ull));
@@ -250,6 +271,106 @@ __global__ __launch_bounds__(256) void route_kernel(RouteParams p) {
             running += __popcll(mask);
         }
     }
+}
+
+// One workgroup: routing of every token row, then the route tables (small
+// batches whose logits already exist).
+__global__ __launch_bounds__(256) void route_kernel(RouteParams p) {
+    __shared__ RouteLds L;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    for (int r = wave; r < p.rows; r += 4) route_row(p, r, lane, L.ids);
+    __syncthreads();
+    small_tables(p, L);
+}
+
+// Decode: the router matvec and the routing in one launch.  Workgroup g
+// computes the logits of experts 4g .. 4g + 3 for every row (a wave per
+// expert, x RMSNorm'ed on the fly, k order per lane then a wave sum); the
+// last workgroup to finish (device counter, fenced) routes the rows and builds
+// the tables, then re-arms the counter.
+__global__ __launch_bounds__(256) void router_route_kernel(RouteParams p, const float *x,
+                                                           const float *norm_w, float eps,
+                                                           const float *router, int width,
+                                                           unsigned *counter) {
+    __shared__ RouteLds L;
+    __shared__ float inv_rms[kFusedRouteMaxRows];
+    __shared__ bool last;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int e = blockIdx.x * 4 + wave;
+    float* logits = const_cast<float *>(p.logits);
+    // RMSNorm statistics of the rows (each workgroup computes them)
+    if (wave < p.rows) {
+        float ss = 0.0f;
+        if (norm_w) {
+            for (int i0 = lane * 4; i0 < width; i0 += 256 * 8) {
+                f32x4 v[8];
+#pragma unroll
+                for (int b = 0; b < 8; ++b) {
+                    const int i = i0 + 256 * b;
+                    v[b] = i < width ? load_f4(x + (long)wave * width + i)
+                                     : f32x4{0.f, 0.f, 0.f, 0.f};
+                }
+#pragma unroll
+                for (int b = 0; b < 8; ++b)
+                    ss += v[b].x * v[b].x + v[b].y * v[b].y + v[b].z * v[b].z + v[b].w * v[b].w;
+            }
+        }
+        ss = wave_sum(ss);
+        if (lane == 0) inv_rms[wave] = norm_w ? 1.0f / sqrtf(ss / (float)width + eps) : 1.0f;
+    }
+    __syncthreads();
+    if (e < p.experts) {
+        const float *wr = router + (long)e * width;
+        for (int r = 0; r < p.rows; ++r) {
+            const float *xr = x + (long)r * width;
+            float acc = 0.0f;
+            for (int i0 = lane * 4; i0 < width; i0 += 256 * 8) {
+                f32x4 wv[8], xv[8], nv[8];
+#pragma unroll
+                for (int b = 0; b < 8; ++b) {
+                    const int i = i0 + 256 * b;
+                    const bool ok = i < width;
+                    wv[b] = ok ? load_f4(wr + i) : f32x4{0.f, 0.f, 0.f, 0.f};
+                    xv[b] = ok ? load_f4(xr + i) : f32x4{0.f, 0.f, 0.f, 0.f};
+                    nv[b] = (ok && norm_w) ? load_f4(norm_w + i) : f32x4{1.f, 1.f, 1.f, 1.f};
+                }
+#pragma unroll
+                for (int b = 0; b < 8; ++b) {
+                    const float rs = inv_rms[r];
+                    acc = fmaf(xv[b].x * rs * nv[b].x, wv[b].x, acc);
+                    acc = fmaf(xv[b].y * rs * nv[b].y, wv[b].y, acc);
+                    acc = fmaf(xv[b].z * rs * nv[b].z, wv[b].z, acc);
+                    acc = fmaf(xv[b].w * rs * nv[b].w, wv[b].w, acc);
+                }
+            }
+            acc = wave_sum(acc);
+            if (lane == 0) logits[(long)r * p.experts + e] = acc;
+        }
+    }
+    // last workgroup: everything above is visible to it after the fences
+    __threadfence();
+    __syncthreads();
+    if (threadIdx.x == 0) last = atomicAdd(counter, 1u) == gridDim.x - 1;
+    __syncthreads();
+    if (!last) return;
+    __threadfence();
+    for (int r = wave; r < p.rows; r += 4) route_row(p, r, lane, L.ids);
+    __syncthreads();
+    small_tables(p, L);
+    if (threadIdx.x == 0) atomicExch(counter, 0u);
+}
+
+int router_route(const RouteParams &p, const float *x, const float *norm_w, float eps,
+                 const float *router, int width, unsigned *counter, hipStream_t stream) {
+    if (!p.logits || !p.bias || !p.ids || !p.weights || p.rows <= 0 ||
+        p.rows > kFusedRouteMaxRows || p.experts <= 0 || p.experts > kMaxExperts ||
+        p.top_k <= 0 || p.top_k > kMaxTopK || p.top_k > p.experts || !p.n_unique ||
+        !p.unique || !p.counts || !p.offsets || !p.list_rows || !p.list_slots ||
+        !p.list_pos || !p.error || !x || !router || !counter || width <= 0 || width % 4)
+        return kErrArgs;
+    hipLaunchKernelGGL(router_route_kernel, dim3((p.experts + 3) / 4), dim3(256), 0, stream, p,
+                       x, norm_w, eps, router, width, counter);
+    return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
 }
 
 // Large batches (prefill): one wave per token row over many workgroups ...
@@ -406,6 +527,8 @@ __global__ __launch_bounds__(1024) void route_tables_kernel(RouteParams p) {
             p.offsets[e] = offsets[e];
         }
     }
+    __syncthreads();
+    write_tasks(p, counts, offsets, rank_of, unique_total);
     // ---- list entries
     for (int e0 = 0; e0 < E; e0 += group) {
         const int ne = min(group, E - e0);
@@ -545,8 +668,6 @@ int router_logits(const float *x, const float *norm_w, float eps, const float *w
     return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
 }
 
-constexpr int kRouteFusedMaxPositions = 1024;
-
 int route_topk(const RouteParams &p, hipStream_t stream) {
     if (!p.logits || !p.bias || !p.ids || !p.weights || p.rows <= 0 || p.experts <= 0 ||
         p.experts > kMaxExperts || p.top_k <= 0 || p.top_k > kMaxTopK ||
@@ -604,6 +725,7 @@ int expert_ffn(const ExpertFfnParams &f, hipStream_t stream) {
         GemvLaunch L;
         ExpertGemvParams &e = L.expert;
         e.stage = stage;
+        e.tasks = f.tasks;
         e.experts = f.expert_table;
         e.n_unique = f.n_unique;
         e.unique = f.unique;

@@ -112,6 +112,8 @@ struct MoonlightSession {
     int *route_ids = nullptr, *n_unique = nullptr, *unique = nullptr, *counts = nullptr;
     int *offsets = nullptr, *list_rows = nullptr, *list_slots = nullptr, *list_pos = nullptr;
     int *route_error = nullptr, *route_trace = nullptr, *ids = nullptr;
+    ExpertTask *expert_tasks = nullptr;  // [experts] per-task table of the expert GEMVs
+    unsigned *route_counter = nullptr;   // last-workgroup counter of the fused routing
     float *expert_hidden = nullptr, *expert_out = nullptr;
     float *shared_hidden = nullptr, *shared_out = nullptr, *dense_hidden = nullptr;
     float *moe_routed = nullptr;  // routed part of moonlight_test_moe
@@ -921,13 +923,19 @@ int route(MoonlightSession *s, int layer, const float *x, int rows, const float 
           int *trace) {
     const ModelConfig &c = s->model->cfg;
     const LayerPlan &lp = s->model->layers[layer];
-    if (rows >= kGemmMinRows && lp.router.fmt == kF32 && c.hidden_size % 8 == 0) {
-        if (router_logits(x, norm_w, c.rms_norm_epsilon, reinterpret_cast<const float *>(lp.router.w),
-                          rows, c.expert_count, c.hidden_size, s->router_logits, stream_of(s)))
+    const bool f32_router = lp.router.fmt == kF32;
+    const float *router_w = reinterpret_cast<const float *>(lp.router.w);
+    // decode batches: router matvec and routing in one launch
+    const bool fused = f32_router && rows <= kFusedRouteMaxRows && c.hidden_size % 4 == 0;
+    if (!fused) {
+        if (rows >= kGemmMinRows && f32_router && c.hidden_size % 8 == 0) {
+            if (router_logits(x, norm_w, c.rms_norm_epsilon, router_w, rows, c.expert_count,
+                              c.hidden_size, s->router_logits, stream_of(s)))
+                return kErrLaunch;
+        } else if (gemv_rows(s, lp.router, x, rows, c.hidden_size, c.expert_count,
+                             s->router_logits, norm_w)) {
             return kErrLaunch;
-    } else if (gemv_rows(s, lp.router, x, rows, c.hidden_size, c.expert_count, s->router_logits,
-                         norm_w)) {
-        return kErrLaunch;
+        }
     }
     RouteParams r;
     r.logits = s->router_logits;
@@ -949,6 +957,12 @@ int route(MoonlightSession *s, int layer, const float *x, int rows, const float 
     r.list_pos = s->list_pos;
     r.error = s->route_error;
     r.fixed_ids = s->fixed_rows >= rows ? s->fixed_ids : nullptr;
+    r.expert_table = lp.expert_table;
+    r.tasks = s->expert_tasks;
+    r.task_slots = rows * r.top_k < r.experts ? rows * r.top_k : r.experts;
+    if (fused)
+        return router_route(r, x, norm_w, c.rms_norm_epsilon, router_w, c.hidden_size,
+                            s->route_counter, stream_of(s));
     return route_topk(r, stream_of(s));
 }
 
@@ -978,6 +992,7 @@ int experts(MoonlightSession *s, int layer, const float *x, int rows, const floa
     f.counts = s->counts;
     f.offsets = s->offsets;
     f.list_rows = s->list_rows;
+    f.tasks = s->expert_tasks;  // written by route()
     f.x = x;
     f.norm_w = norm_w;
     f.eps = c.rms_norm_epsilon;
@@ -1184,6 +1199,9 @@ extern "C" int moonlight_session_create(MoonlightSession **out, MoonlightModel *
         session_alloc(s, &s->list_slots, mb * K, error, error_size) &&
         session_alloc(s, &s->list_pos, mb * K, error, error_size) &&
         session_alloc(s, &s->route_error, 1, error, error_size) &&
+        session_alloc(s, &s->expert_tasks, E, error, error_size) &&
+        session_alloc(s, &s->route_counter, 1, error, error_size) &&
+        hipMemset(s->route_counter, 0, sizeof(unsigned)) == hipSuccess &&
         session_alloc(s, &s->route_trace, L * mb * K, error, error_size) &&
         session_alloc(s, &s->expert_hidden, mb * K * (size_t)c.moe_intermediate_size, error,
                       error_size) &&
