@@ -58,6 +58,73 @@ __global__ __launch_bounds__(64) void gemv_generic_kernel(GemvParams p, int fmt)
 }
 
 // ---------------------------------------------------------------------------
+// pre-split limb rows
+// ---------------------------------------------------------------------------
+
+template <int FMT>
+__device__ void limb_row(const LimbRowsParams &p, int r) {
+    __shared__ float ss_red[4];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const float *x = p.x + (long)r * p.x_stride;
+    const int nc = row_bytes_of(FMT, p.I) / 16;
+    float inv_rms = 1.0f;
+    if (p.norm_w) {
+        float ss = 0.0f;
+        for (int e0 = tid * 8; e0 < p.I; e0 += kLimbPassElems) {
+            const f32x4 a = load_f4(x + e0), b = load_f4(x + e0 + 4);
+            ss += a.x * a.x + a.y * a.y + a.z * a.z + a.w * a.w + b.x * b.x + b.y * b.y +
+                  b.z * b.z + b.w * b.w;
+        }
+        ss = wave_sum(ss);
+        if (lane == 0) ss_red[wave] = ss;
+        __syncthreads();
+        inv_rms = 1.0f / sqrtf(((ss_red[0] + ss_red[1]) + (ss_red[2] + ss_red[3])) / (float)p.I +
+                               p.eps);
+    }
+    unsigned char *out = p.out + (long)r * p.out_stride;
+    // every thread of a chunk group takes part in the shuffles of
+    // limb_quantise8, so the loop bound is the workgroup-uniform pass count
+    const int npass = (p.I + kLimbPassElems - 1) / kLimbPassElems;
+    for (int j = 0; j < npass; ++j) {
+        const int e0 = tid * 8 + j * kLimbPassElems;
+        const bool in = e0 < p.I;
+        const int ec = in ? e0 : 0;
+        const f32x4 a = load_f4(x + ec), b = load_f4(x + ec + 4);
+        float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+        if (p.norm_w) {
+            const f32x4 na = load_f4(p.norm_w + ec), nb = load_f4(p.norm_w + ec + 4);
+            const float n[8] = {na.x, na.y, na.z, na.w, nb.x, nb.y, nb.z, nb.w};
+#pragma unroll
+            for (int i = 0; i < 8; ++i) v[i] = v[i] * inv_rms * n[i];
+        }
+        limb_quantise8<FMT>(v, in, e0, out, p.I, nc);
+    }
+}
+
+__global__ __launch_bounds__(256) void limb_rows_kernel(LimbRowsParams a, LimbRowsParams b) {
+    const bool first = (int)blockIdx.x < a.rows;
+    const LimbRowsParams &p = first ? a : b;
+    const int r = first ? (int)blockIdx.x : (int)blockIdx.x - a.rows;
+    if (p.fmt == kQ4)
+        limb_row<kQ4>(p, r);
+    else
+        limb_row<kQ8>(p, r);
+}
+
+int limb_quantise_rows(const LimbRowsParams &a, const LimbRowsParams &b, hipStream_t stream) {
+    for (const LimbRowsParams *p : {&a, &b}) {
+        if (p->rows == 0) continue;
+        if (p->rows < 0 || !p->x || !p->out || (p->fmt != kQ8 && p->fmt != kQ4) || p->I <= 0 ||
+            p->I % 16 || (p->fmt == kQ4 && p->I % 32) || p->x_stride % 4 ||
+            p->out_stride < limb_row_lds(p->fmt, p->I) || p->out_stride % 16)
+            return kErrArgs;
+    }
+    if (a.rows + b.rows == 0) return kOk;
+    hipLaunchKernelGGL(limb_rows_kernel, dim3(a.rows + b.rows), dim3(256), 0, stream, a, b);
+    return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
+}
+
+// ---------------------------------------------------------------------------
 // planning
 // ---------------------------------------------------------------------------
 
@@ -89,10 +156,11 @@ struct PlanEntry {
 static const PlanEntry kMeasuredPlans[] = {
     {kQ4, 11264, 2048, 0, 1, 4, 1}, {kQ8, 11264, 2048, 0, 1, 4, 1},
     {kQ4, 2048, 11264, 0, 1, 8, 4}, {kQ8, 2048, 11264, 0, 1, 4, 4},
-    {kQ8, 3072, 2048, 0, 1, 2, 4},  {kQ8, 2048, 2048, 0, 1, 2, 4},
-    {kQ8, 2048, 1408, 0, 1, 2, 4},  {kQ8, 2048, 2816, 0, 1, 2, 4},
-    {kQ8, 576, 2048, 0, 1, 1, 4},   {kF32, 64, 2048, 0, 2, 1, 4},
-    {kQ4, 2048, 1408, 0, 1, 2, 1},
+    {kQ8, 3072, 2048, 0, 2, 1, 1},  {kQ8, 2048, 2048, 0, 2, 1, 1},
+    {kQ8, 2048, 1408, 0, 2, 1, 1},  {kQ8, 2048, 2816, 0, 1, 8, 4},
+    {kQ8, 576, 2048, 0, 2, 1, 1},   {kF32, 64, 2048, 0, 4, 1, 4},
+    {kQ4, 2048, 1408, 0, 1, 2, 1},  {kQ8, 1536, 2048, 0, 2, 1, 1},
+    {kQ8, 3072, 1536, 0, 2, 2, 1},
 };
 
 GemvPlan plan_gemv(int fmt, int O, int I, int rows, bool dual) {
@@ -124,17 +192,32 @@ GemvPlan plan_gemv(int fmt, int O, int I, int rows, bool dual) {
             }
         }
     }
-    // Fallback heuristic from the same sweeps: one chunk per lane for the
-    // quantized formats (more waves beat deeper per-wave queues), k split over
-    // the workgroup's 4 waves when the matrix is short and rows span several
-    // k-tiles, and rows per wave sized to keep ~2048+ waves in flight.
-    plan.kt = fmt == kF32 ? (nc > 64 ? 2 : 1) : 1;
+    // Fallback heuristic from the same sweeps.  Quantised formats: a lane
+    // covers its chunks of the row in one tile (KT = 1 or 2 for rows of up to
+    // 128 chunks), wider rows split k over the workgroup's 4 waves; rows per
+    // wave sized for ~700 workgroups.  f32: up to 2 chunks per lane per tile.
+    const int rmin = dual ? 2 : 1;
+    if (fmt != kF32) {
+        if (nc <= 128) {
+            plan.ks = 1;
+            plan.kt = nc > 64 ? 2 : 1;
+        } else {
+            plan.ks = 4;
+            plan.kt = nc > 256 ? 2 : 1;
+        }
+        const long per_wave_target = (long)O * (dual ? 2 : 1) / (plan.ks == 4 ? 700 : 2800);
+        int r = rmin;
+        while (r < 8 && r * 2 <= per_wave_target && r * 2 * plan.b <= 16 && r * 2 * plan.kt <= 16)
+            r *= 2;
+        plan.r = r;
+        return plan;
+    }
+    plan.kt = nc > 64 ? 2 : 1;
     const int tiles = (nc + 64 * plan.kt - 1) / (64 * plan.kt);
     const long out_rows_total = (long)O * (dual ? 2 : 1);
     // k split only pays when every wave of the workgroup gets a k-tile, or for
     // short plain matrices (few rows: more waves); not for the gate/up pairs
     plan.ks = (tiles >= 4 || (tiles >= 2 && out_rows_total <= 4096 && !dual)) ? 4 : 1;
-    const int rmin = dual ? 2 : 1;
     int chosen = 0;
     for (int r = 8; r >= rmin; r >>= 1) {
         if (r * plan.b > 16 || r * plan.kt > 16) continue;
@@ -147,11 +230,53 @@ GemvPlan plan_gemv(int fmt, int O, int I, int rows, bool dual) {
     return plan;
 }
 
-// Grouped expert launches: same core, but the work is spread over `tasks`
-// matrices, so fewer rows per wave are needed to fill the machine.
-GemvPlan plan_expert_gemv(int fmt, int O, int I, int rows, bool dual, int tasks) {
-    GemvPlan plan = plan_gemv(fmt, O, I, rows, dual);
-    if (plan.lpr < 64 || tasks <= 1) return plan;
+// Grouped expert launches: same core, the work spread over `tasks` matrices.
+// Quantised formats: one tile covers a lane's chunks of the widest row of the
+// launch (I = max_I, KT up to 3 columns of 64 chunks), 8 rows per wave when
+// the registers allow (the x prologue of every workgroup is amortised over
+// more rows; measured best for the Moonlight expert shapes).
+// MLH_EXPERT_PLAN="kt,r,ks;kt,r,ks" (stage 0; stage 1, read once) overrides.
+static bool expert_plan_override(bool dual, GemvPlan *plan) {
+    static int parsed = 0, v[2][3] = {{0, 0, 0}, {0, 0, 0}};
+    if (!parsed) {
+        const char *env = getenv("MLH_EXPERT_PLAN");
+        if (!env || sscanf(env, "%d,%d,%d;%d,%d,%d", &v[0][0], &v[0][1], &v[0][2], &v[1][0],
+                           &v[1][1], &v[1][2]) != 6)
+            v[0][0] = v[1][0] = 0;
+        parsed = 1;
+    }
+    const int *e = v[dual ? 0 : 1];
+    if (!e[0]) return false;
+    plan->kt = e[0];
+    plan->r = e[1];
+    plan->ks = e[2];
+    return true;
+}
+
+GemvPlan plan_expert_gemv(int fmt, int O, int I, int rows, bool dual, int tasks, int max_I) {
+    GemvPlan plan = plan_gemv(fmt, O, max_I, rows, dual);
+    if (plan.lpr < 64) return plan;
+    if (fmt != kF32) {
+        if (!expert_plan_override(dual, &plan)) {
+            const int nc = row_bytes_of(fmt, max_I) / 16;
+            if (nc <= 192) {
+                plan.ks = 1;
+                plan.kt = (nc + 63) / 64;
+            } else {
+                plan.ks = 4;
+                plan.kt = (nc + 255) / 256 < 3 ? (nc + 255) / 256 : 3;
+            }
+            plan.r = 8;
+            while (plan.r > 1 && (plan.r * plan.kt > 16 || plan.r * plan.b > 16)) plan.r /= 2;
+        }
+        if (plan.r * plan.b > 16) plan.r = 16 / plan.b;
+        if (plan.r * plan.kt > 16) plan.r = 16 / plan.kt;
+        if (dual && plan.r < 2) plan.r = 2;
+        (void)tasks;
+        (void)I;
+        return plan;
+    }
+    if (tasks <= 1) return plan;
     const int rmin = dual ? 2 : 1;
     for (int r = plan.r; r <= 8; r <<= 1) {
         if (r * plan.b > 16 || r * plan.kt > 16) break;

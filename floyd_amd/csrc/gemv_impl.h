@@ -92,6 +92,9 @@ struct GemvJob {
     const float *x[B];
     float *y[B];
     const float *resid[B];
+    // optional: x already split into limb rows (limb_quantise_rows), one per
+    // token row, in the LDS row layout; the prologue then only copies them
+    const unsigned char *limbs[B];
     const float *norm_w = nullptr;
     float eps = 0.0f;
     int epilogue = kEpiPlain;
@@ -310,10 +313,15 @@ struct LimbInfo {
     int pad;
 };
 
-// LDS bytes of one token row of width I: hi, mid and lo limbs (I bytes each)
-// and a LimbInfo per 16-byte weight chunk.
-__host__ __device__ constexpr int limb_row_lds(int fmt, int I) {
+// Bytes of one token row of width I in the limb layout: hi, mid and lo limbs
+// (I bytes each) and a LimbInfo per 16-byte weight chunk, padded to 1 KB (the
+// unit of the LDS DMA copy of pre-split rows).  The same layout serves the
+// LDS rows and the pre-split rows in memory.
+__host__ __device__ constexpr int limb_row_bytes(int fmt, int I) {
     return 3 * I + 16 * (row_bytes_of(fmt, I) / 16);
+}
+__host__ __device__ constexpr int limb_row_lds(int fmt, int I) {
+    return (limb_row_bytes(fmt, I) + 1023) & ~1023;
 }
 
 __device__ __forceinline__ int sdot4(int a, int b, int c) {
@@ -443,20 +451,23 @@ __device__ __forceinline__ float limb_chunk_dot(u32x4 w, const unsigned char *ro
     return fmaf((float)(hd - info.bias_hi), 65536.0f, (float)(mdd * 256 + ld - info.bias_low));
 }
 
-// x passes held in registers across the weight issue (the rest of a wide row
-// is loaded after it).
-template <int B>
+// x passes held in registers across the weight issue: as many as a row the
+// plan covers in one tile can need (KS * KT * 64 chunks), at most 6 (an
+// 11264-wide row), one for B > 1; the rest of a wider row is loaded after the
+// weights.
+template <int FMT, int B, int KT, int KS>
 constexpr int limb_pre_passes() {
-    return B == 1 ? 2 : 1;
+    constexpr int elems = KS * KT * 64 * FmtTraits<FMT>::kElemsPerChunk;
+    constexpr int passes = (elems + kLimbPassElems - 1) / kLimbPassElems;
+    return B == 1 ? (passes < 6 ? passes : 6) : 1;
 }
 
-// `after_job`: the workgroup ran another job on the same LDS just before.
+// One job: the token rows of job.x against row block job.row_block of W.
 template <int FMT, int B, int KT, int LPR, int R, int KS>
-__device__ __forceinline__ void limb_block(const GemvJob<B> job, unsigned char *lds,
-                                           bool after_job) {
+__device__ __forceinline__ void limb_block(const GemvJob<B> job, unsigned char *lds) {
     constexpr int GPW = kWave / LPR;
     constexpr int NV = R * B;
-    constexpr int NJP = limb_pre_passes<B>();
+    constexpr int NJP = limb_pre_passes<FMT, B, KT, KS>();
     static_assert(NV <= LPR, "partial sums exceed the lane group");
     static_assert(KS == 1 || LPR == kWave, "k-split needs whole-wave row groups");
     __shared__ float red[4][NV];
@@ -468,12 +479,14 @@ __device__ __forceinline__ void limb_block(const GemvJob<B> job, unsigned char *
     const int group = lane / LPR;
     const int li = lane & (LPR - 1);
     const bool dual = job.epilogue == kEpiSiluDual;
+    const bool residual = job.epilogue == kEpiResidual;
     const int out_per_group = dual ? R / 2 : R;
     const int row_wave = KS == 1 ? job.row_block * 4 + wave : job.row_block;
     const int kpart = KS == 1 ? 0 : wave;
     const int out0 = (row_wave * GPW + group) * out_per_group;
+    const int rpb = out_per_group * GPW * (KS == 1 ? 4 : 1);  // outputs per row block
     // whole workgroups past the end leave (the prologue below synchronises)
-    if ((KS > 1 ? job.row_block : job.row_block * 4) * GPW * out_per_group >= job.O) return;
+    if (job.row_block * rpb >= job.O) return;
 
     const int I = job.I;
     const int row_bytes = row_bytes_of(FMT, I);
@@ -481,18 +494,37 @@ __device__ __forceinline__ void limb_block(const GemvJob<B> job, unsigned char *
     const int lds_row = limb_row_lds(FMT, I);
     const int npass = (I + kLimbPassElems - 1) / kLimbPassElems;
 
+    const bool presplit = job.limbs[0] != nullptr;
+    if (presplit) {
+        // ---- 1'. pre-split rows: 1 KB blocks straight into LDS (DMA)
+        const int nblk = lds_row / 1024;
+#pragma unroll
+        for (int b = 0; b < B; ++b) {
+            if (b < job.rows) {
+                for (int blk = wave; blk < nblk; blk += 4) {
+                    __builtin_amdgcn_global_load_lds(
+                        (const __attribute__((address_space(1))) void *)(job.limbs[b] + blk * 1024 +
+                                                                         lane * 16),
+                        (__attribute__((address_space(3))) void *)(lds + b * lds_row + blk * 1024),
+                        16, 0, 0);
+                }
+            }
+        }
+    }
     // ---- 1. x (and norm_w) of the first passes
     f32x4 xv[NJP][B][2];
     f32x4 nv[NJP][2];
 #pragma unroll
     for (int j = 0; j < NJP; ++j) {
-        if (j < npass) {
+        if (!presplit && j < npass) {
             const int e0 = tid * 8 + j * kLimbPassElems;
             const int ec = e0 < I ? e0 : 0;
 #pragma unroll
             for (int b = 0; b < B; ++b) {
-                xv[j][b][0] = load_f4(job.x[b] + ec);
-                xv[j][b][1] = load_f4(job.x[b] + ec + 4);
+                if (b < job.rows) {  // uniform: absent token rows cost nothing
+                    xv[j][b][0] = load_f4(job.x[b] + ec);
+                    xv[j][b][1] = load_f4(job.x[b] + ec + 4);
+                }
             }
             if (job.norm_w) {
                 nv[j][0] = load_f4(job.norm_w + ec);
@@ -500,11 +532,9 @@ __device__ __forceinline__ void limb_block(const GemvJob<B> job, unsigned char *
             }
         }
     }
-    // ---- 2. epilogue operands of the value this lane will write
+    // ---- 2. the value this lane writes, and its epilogue operands
     const int vi = butterfly_index<NV, LPR>(lane);
     const int vr = vi / B, vb = vi % B;
-    const int vrow = out0 + vr;
-    const int vrow_c = vrow < job.O ? vrow : job.O - 1;
     float *yb = job.y[0];
     const float *rb = job.resid[0];
 #pragma unroll
@@ -514,42 +544,59 @@ __device__ __forceinline__ void limb_block(const GemvJob<B> job, unsigned char *
             rb = job.resid[i];
         }
     }
-    const float s_row = load_global_f32(job.s + vrow_c);
-    const float s2_row = dual ? load_global_f32(job.s2 + vrow_c) : 0.0f;
-    const float resid_row = job.epilogue == kEpiResidual ? load_global_f32(rb + vrow_c) : 0.0f;
-    // ---- 3. the first weight tile
+    struct Epi {
+        float s, s2, resid;
+    };
+    // (the conditional loads are issued before the weights, whose waits they
+    // therefore do not disturb)
+    auto load_epi = [&](int o0) {
+        const int vrow = o0 + vr;
+        const int vc = vrow < job.O ? vrow : job.O - 1;
+        Epi e{load_global_f32(job.s + vc), 0.0f, 0.0f};
+        if (dual) e.s2 = load_global_f32(job.s2 + vc);
+        if (residual) e.resid = load_global_f32(rb + vc);
+        return e;
+    };
+    const Epi epi_cur = load_epi(out0);
+    // ---- 3. the first weight tile.  Column-major issue (all rows of chunk
+    // column k, then k + 1); a column entirely past the row end is skipped --
+    // a uniform branch after the columns the compute needs first, so their
+    // waits stay exact.
     const int step = KS * KT * LPR;
-    u32x4 wv[R][KT];
-    auto load_tile = [&](int kt0) {
+    auto load_tile = [&](u32x4 (&wv)[R][KT], int kt0, int o0) {
 #pragma unroll
-        for (int r = 0; r < R; ++r) {
-            int row;
-            const uint8_t *base;
-            if (dual) {
-                row = out0 + (r < R / 2 ? r : r - R / 2);
-                base = r < R / 2 ? job.w : job.w2;
-            } else {
-                row = out0 + r;
-                base = job.w;
+        for (int k = 0; k < KT; ++k) {
+            if (k > 0 && kt0 + LPR * k >= nc) {
+#pragma unroll
+                for (int r = 0; r < R; ++r) wv[r][k] = u32x4{0u, 0u, 0u, 0u};
+                continue;
             }
-            const int row_c = row < job.O ? row : job.O - 1;
+            const int c = kt0 + li + LPR * k;
 #pragma unroll
-            for (int k = 0; k < KT; ++k) {
-                const int c = kt0 + li + LPR * k;
+            for (int r = 0; r < R; ++r) {
+                int row;
+                const uint8_t *base;
+                if (dual) {
+                    row = o0 + (r < R / 2 ? r : r - R / 2);
+                    base = r < R / 2 ? job.w : job.w2;
+                } else {
+                    row = o0 + r;
+                    base = job.w;
+                }
+                const int row_c = row < job.O ? row : job.O - 1;
                 const u32x4 v = load_stream16(base + (long)row_c * row_bytes + (c < nc ? c : 0) * 16);
                 wv[r][k] = (row < job.O && c < nc) ? v : u32x4{0u, 0u, 0u, 0u};
             }
         }
     };
-    load_tile(kpart * KT * LPR);
-    // the previous job's LDS readers are done before anything is overwritten
-    if (after_job) __syncthreads();
+    u32x4 wa[R][KT];
+    load_tile(wa, kpart * KT * LPR, out0);
 
     // ---- 4. RMSNorm statistics (workgroup reduction)
     float inv_rms[B];
 #pragma unroll
     for (int b = 0; b < B; ++b) inv_rms[b] = 1.0f;
-    if (job.norm_w) {
+    if (job.norm_w && !presplit) {
         float ss[B];
 #pragma unroll
         for (int b = 0; b < B; ++b) ss[b] = 0.0f;
@@ -558,6 +605,7 @@ __device__ __forceinline__ void limb_block(const GemvJob<B> job, unsigned char *
             if (j < npass && tid * 8 + j * kLimbPassElems < I) {
 #pragma unroll
                 for (int b = 0; b < B; ++b)
+                    if (b < job.rows)
 #pragma unroll
                     for (int h = 0; h < 2; ++h)
                         ss[b] += xv[j][b][h].x * xv[j][b][h].x + xv[j][b][h].y * xv[j][b][h].y +
@@ -569,6 +617,7 @@ __device__ __forceinline__ void limb_block(const GemvJob<B> job, unsigned char *
             if (e0 < I) {
 #pragma unroll
                 for (int b = 0; b < B; ++b)
+                    if (b < job.rows)
 #pragma unroll
                     for (int h = 0; h < 2; ++h) {
                         const f32x4 t = load_f4(job.x[b] + e0 + 4 * h);
@@ -601,13 +650,14 @@ __device__ __forceinline__ void limb_block(const GemvJob<B> job, unsigned char *
     };
 #pragma unroll
     for (int j = 0; j < NJP; ++j) {
-        if (j < npass) {
+        if (!presplit && j < npass) {
             const int e0 = tid * 8 + j * kLimbPassElems;
 #pragma unroll
-            for (int b = 0; b < B; ++b) quantise_pass(xv[j][b], nv[j], b, e0);
+            for (int b = 0; b < B; ++b)
+                if (b < job.rows) quantise_pass(xv[j][b], nv[j], b, e0);
         }
     }
-    for (int j = NJP; j < npass; ++j) {
+    for (int j = presplit ? npass : NJP; j < npass; ++j) {
         const int e0 = tid * 8 + j * kLimbPassElems;
         const int ec = e0 < I ? e0 : 0;
         f32x4 np[2] = {f32x4{1.f, 1.f, 1.f, 1.f}, f32x4{1.f, 1.f, 1.f, 1.f}};
@@ -617,18 +667,17 @@ __device__ __forceinline__ void limb_block(const GemvJob<B> job, unsigned char *
         }
 #pragma unroll
         for (int b = 0; b < B; ++b) {
-            const f32x4 xp[2] = {load_f4(job.x[b] + ec), load_f4(job.x[b] + ec + 4)};
-            quantise_pass(xp, np, b, e0);
+            if (b < job.rows) {
+                const f32x4 xp[2] = {load_f4(job.x[b] + ec), load_f4(job.x[b] + ec + 4)};
+                quantise_pass(xp, np, b, e0);
+            }
         }
     }
+    if (presplit) __builtin_amdgcn_s_waitcnt(0);  // this wave's DMA blocks have landed
     __syncthreads();
 
-    // ---- 6. dot products
-    float acc[NV];
-#pragma unroll
-    for (int v = 0; v < NV; ++v) acc[v] = 0.0f;
-    for (int kt0 = kpart * KT * LPR; kt0 < nc; kt0 += step) {
-        if (kt0 != kpart * KT * LPR) load_tile(kt0);
+    // ---- 6. dot products of one k tile into acc
+    auto dot_tile = [&](const u32x4 (&wv)[R][KT], int kt0, float (&acc)[NV]) {
 #pragma unroll
         for (int k = 0; k < KT; ++k) {
             const int c = kt0 + li + LPR * k;
@@ -648,39 +697,50 @@ __device__ __forceinline__ void limb_block(const GemvJob<B> job, unsigned char *
                 }
             }
         }
-    }
+    };
+    // ---- 7. reduction and epilogue of the row block (o0: its out0)
+    auto finish = [&](float (&acc)[NV], int o0, const Epi &ep) {
+        butterfly_reduce<NV, LPR>(acc, lane);
+        const bool writer = butterfly_writer<NV, LPR>(lane);
+        float value = acc[0];
+        if constexpr (KS > 1) {
+            if (writer) red[wave][vi] = value;
+            __syncthreads();
+            value = (red[0][vi] + red[1][vi]) + (red[2][vi] + red[3][vi]);
+            if (wave != 0) return;
+        }
+        const int vrow = o0 + vr;
+        if (dual) {
+            // the up-projection partner of value index vi is vi + NV/2, held by
+            // the lane across the first butterfly offset
+            const float partner = __shfl_xor(value, LPR / 2, kWave);
+            if (writer && vr < R / 2 && vrow < job.O && vb < job.rows)
+                yb[vrow] = silu(value * ep.s) * (partner * ep.s2);
+            return;
+        }
+        if (writer && vrow < job.O && vb < job.rows) {
+            float out = value * ep.s;
+            if (residual) out = ep.resid + out;
+            yb[vrow] = out;
+        }
+    };
 
-    // ---- 7. reduction and epilogue
-    butterfly_reduce<NV, LPR>(acc, lane);
-    const bool writer = butterfly_writer<NV, LPR>(lane);
-    float value = acc[0];
-    if constexpr (KS > 1) {
-        if (writer) red[wave][vi] = value;
-        __syncthreads();
-        value = (red[0][vi] + red[1][vi]) + (red[2][vi] + red[3][vi]);
-        if (wave != 0) return;
+    float acc[NV];
+#pragma unroll
+    for (int v = 0; v < NV; ++v) acc[v] = 0.0f;
+    for (int kt0 = kpart * KT * LPR; kt0 < nc; kt0 += step) {
+        if (kt0 != kpart * KT * LPR) load_tile(wa, kt0, out0);
+        dot_tile(wa, kt0, acc);
     }
-    if (dual) {
-        // the up-projection partner of value index vi is vi + NV/2, held by the
-        // lane across the first butterfly offset
-        const float partner = __shfl_xor(value, LPR / 2, kWave);
-        if (writer && vr < R / 2 && vrow < job.O && vb < job.rows)
-            yb[vrow] = silu(value * s_row) * (partner * s2_row);
-        return;
-    }
-    if (writer && vrow < job.O && vb < job.rows) {
-        float out = value * s_row;
-        if (job.epilogue == kEpiResidual) out = resid_row + out;
-        yb[vrow] = out;
-    }
+    finish(acc, out0, epi_cur);
 }
 
-// Grouped expert launches (MoE): blockIdx.y selects a task -- one active routed
-// expert (in first-appearance order) or, last, the fused shared expert -- and
-// the workgroup loops over that task's token rows in groups of B.  Token rows are
-// gathered / scattered through the device route tables, so no gather or scatter
-// pass exists (moonlight_metal.m:577-638 issues gather_rows / scatter_expert per
-// expert instead).
+// Grouped expert launches (MoE): blockIdx.x selects a task -- one active routed
+// expert (in first-appearance order) or, after them, the fused shared expert --
+// and its row block(s); blockIdx.y selects a group of B of that task's token
+// rows.  Token rows are gathered / scattered through the device route tables,
+// so no gather or scatter pass exists (moonlight_metal.m:577-638 issues
+// gather_rows / scatter_expert per expert instead).
 struct ExpertWeights {
     const uint8_t *gate, *up, *down;
     const float *gate_s, *up_s, *down_s;
@@ -702,8 +762,9 @@ struct ExpertGemvParams {
     const int *counts = nullptr;
     const int *offsets = nullptr;
     const int *rows = nullptr;  // token row of each compact list entry
-    int routed_tasks = 0;       // grid.y slots for routed experts
-    int shared_task = 0;        // 1: grid.y slot routed_tasks is the shared expert
+    int routed_tasks = 0;       // task slots for routed experts
+    int routed_blocks = 0;      // row blocks (workgroups) per routed task
+    int shared_task = 0;        // 1: the workgroups after the routed ones run the shared expert
     const uint8_t *sh_w = nullptr, *sh_w2 = nullptr;
     const float *sh_s = nullptr, *sh_s2 = nullptr;
     int shared_width = 0;  // fused shared FFN width (2 x moe_intermediate_size)
@@ -715,6 +776,10 @@ struct ExpertGemvParams {
     float *sh_y = nullptr;        // stage 0: shared hidden; 1: shared out [rows, hidden]
     const float *norm_w = nullptr;  // stage 0: post-attention RMSNorm weight
     float eps = 0.0f;
+    // optional pre-split limb rows (limb_quantise_rows): stage 0 by token row,
+    // stage 1 by list entry; the shared expert's rows in sh_limbs
+    const unsigned char *limbs = nullptr, *sh_limbs = nullptr;
+    long limb_stride = 0, sh_limb_stride = 0;
 };
 
 struct GemvLaunch {
@@ -722,12 +787,13 @@ struct GemvLaunch {
     ExpertGemvParams expert;
 };
 
+// MODE 0: plain GEMV; 1: grouped expert tasks.
 template <int MODE, int FMT, int B, int KT, int LPR, int R, int KS>
-__device__ __forceinline__ void run_job(const GemvJob<B> &job, unsigned char *lds, bool after_job) {
+__device__ __forceinline__ void run_job(const GemvJob<B> &job, unsigned char *lds) {
     if constexpr (FMT == kF32)
         gemv_block<FMT, B, KT, LPR, R, KS>(job);
     else
-        limb_block<FMT, B, KT, LPR, R, KS>(job, lds, after_job);
+        limb_block<FMT, B, KT, LPR, R, KS>(job, lds);
 }
 
 // Dynamic LDS of a launch: the quantised x rows of its widest job.
@@ -758,15 +824,20 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvLaunch L) {
             job.x[b] = p.x + r * p.x_stride;
             job.y[b] = p.y + r * p.y_stride;
             job.resid[b] = p.resid ? p.resid + r * p.resid_stride : nullptr;
+            job.limbs[b] = nullptr;
         }
         job.norm_w = p.norm_w;
         job.eps = p.eps;
         job.epilogue = p.epilogue;
-        run_job<MODE, FMT, B, KT, LPR, R, KS>(job, gemv_lds, false);
+        run_job<MODE, FMT, B, KT, LPR, R, KS>(job, gemv_lds);
     } else {
         const ExpertGemvParams &p = L.expert;
-        const int task = blockIdx.y;
-        const bool shared = p.shared_task && task == p.routed_tasks;
+        // flat grid: routed task t owns workgroups t * routed_blocks ..,
+        // the shared expert the ones after them (no idle workgroups)
+        const int routed_wgs = p.routed_tasks * p.routed_blocks;
+        const bool shared = (int)blockIdx.x >= routed_wgs;
+        const int task = shared ? p.routed_tasks : (int)blockIdx.x / p.routed_blocks;
+        job.row_block = shared ? (int)blockIdx.x - routed_wgs : (int)blockIdx.x % p.routed_blocks;
         int n, off = 0;
         const int *list = nullptr;
         if (shared) {
@@ -803,7 +874,10 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvLaunch L) {
         job.norm_w = p.stage == 0 ? p.norm_w : nullptr;
         job.eps = p.eps;
         job.epilogue = p.stage == 0 ? kEpiSiluDual : kEpiPlain;
-        for (int g0 = 0; g0 < n; g0 += B) {
+        // blockIdx.y selects the task's token rows g0 .. g0 + B - 1
+        const int g0 = blockIdx.y * B;
+        if (g0 >= n) return;
+        {
             job.rows = n - g0 < B ? n - g0 : B;
 #pragma unroll
             for (int b = 0; b < B; ++b) {
@@ -820,11 +894,29 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvLaunch L) {
                                       : p.y + (long)(off + j) * p.hidden;
                 }
                 job.resid[b] = nullptr;
+                // pre-split rows: token rows (stage 0) or list / shared rows
+                const long lrow = p.stage == 0 ? token : (shared ? j : off + j);
+                job.limbs[b] = shared ? (p.sh_limbs ? p.sh_limbs + lrow * p.sh_limb_stride : nullptr)
+                                      : (p.limbs ? p.limbs + lrow * p.limb_stride : nullptr);
             }
-            run_job<MODE, FMT, B, KT, LPR, R, KS>(job, gemv_lds, g0 > 0);
+            run_job<MODE, FMT, B, KT, LPR, R, KS>(job, gemv_lds);
         }
     }
 }
+
+// Splits token rows of x (RMSNorm'ed with norm_w when set) into limb rows of
+// the GEMV's LDS layout for format fmt: rows of segment a, then of segment b
+// (b.rows may be 0), one workgroup per row.
+struct LimbRowsParams {
+    int fmt = kQ8, rows = 0, I = 0;
+    const float *x = nullptr;
+    long x_stride = 0;
+    const float *norm_w = nullptr;
+    float eps = 1e-5f;
+    unsigned char *out = nullptr;
+    long out_stride = 0;  // >= limb_row_lds(fmt, I)
+};
+int limb_quantise_rows(const LimbRowsParams &a, const LimbRowsParams &b, hipStream_t stream);
 
 // Largest dynamic LDS a GEMV launch may ask for (the quantised x rows).
 constexpr int kMaxGemvLds = 150 * 1024;
@@ -889,7 +981,8 @@ bool dispatch_gemv_b(const GemvLaunch &L, const GemvPlan &plan, dim3 grid, hipSt
     MLH_GEMV_CASE(KT_, 8, 1) MLH_GEMV_CASE(KT_, 1, 4) MLH_GEMV_CASE(KT_, 2, 4)          \
     MLH_GEMV_CASE(KT_, 4, 4) MLH_GEMV_CASE(KT_, 8, 4)
     MLH_GEMV_KT(1)
-    if constexpr (FMT != kQ4) { MLH_GEMV_KT(2) }
+    MLH_GEMV_KT(2)
+    if constexpr (FMT != kF32) { MLH_GEMV_KT(3) }
     if constexpr (FMT == kF32) { MLH_GEMV_KT(4) }
 #undef MLH_GEMV_KT
 #undef MLH_GEMV_CASE

@@ -72,6 +72,12 @@ struct ExpertFfnParams {
     float *expert_out = nullptr;     // [rows*top_k, hidden]
     float *shared_hidden = nullptr;  // [rows, shared_width]
     float *shared_out = nullptr;     // [rows, hidden]
+    // optional pre-split inputs (limb_quantise_rows): when limb_x is set the
+    // token rows are split once per stage instead of in every workgroup.
+    // Row strides of all four are limb_stride_x / limb_stride_h / ...
+    unsigned char *limb_x = nullptr, *limb_xs = nullptr;  // token rows (expert / shared fmt)
+    unsigned char *limb_h = nullptr, *limb_sh = nullptr;  // list rows / shared rows
+    long limb_x_stride = 0, limb_h_stride = 0, limb_sh_stride = 0;
 };
 int expert_ffn(const ExpertFfnParams &f, hipStream_t stream);
 
@@ -84,7 +90,7 @@ int embed_rows(const float *table, const int *ids, float *out, int rows, int wid
 int add_vectors(const float *a, const float *b, float *out, long n, hipStream_t stream);
 
 // Planning helpers shared with gemv.hip.
-GemvPlan plan_expert_gemv(int fmt, int O, int I, int rows, bool dual, int tasks);
+GemvPlan plan_expert_gemv(int fmt, int O, int I, int rows, bool dual, int tasks, int max_I);
 int gemv_rows_per_block(const GemvPlan &plan, bool dual);
 
 }  // namespace mlh

@@ -14,6 +14,7 @@
 #include "moe.h"
 
 #include <climits>
+#include <cstdlib>
 
 namespace mlh {
 
@@ -124,6 +125,124 @@ __device__ void route_row(const RouteParams &p, int r, int lane, int *lds_ids) {
     }
 }
 
+// Field-wise store of a task entry (a struct copy would go through scratch).
+__device__ __forceinline__ void store_task(ExpertTask *t, const ExpertWeights &w, int count,
+                                           int offset) {
+    t->w.gate = w.gate;
+    t->w.up = w.up;
+    t->w.down = w.down;
+    t->w.gate_s = w.gate_s;
+    t->w.up_s = w.up_s;
+    t->w.down_s = w.down_s;
+    t->count = count;
+    t->offset = offset;
+}
+
+// Routing of token row r with at most 64 experts (one per lane) by one wave,
+// with no serial arg-max chain.  The top-k selection is a rank: expert e is
+// taken in slot rank(e) = #{o : sel_o > sel_e or (sel_o == sel_e and o < e)}
+// when rank(e) < top_k, which is the order the repeated arg-max of
+// moe_route.h:59-71 produces (larger first, lower index on ties).  Only
+// experts with sel > -inf can be taken (NaN never compares greater), as in
+// the arg-max.  Writes ids / weights / trace (and lds_ids); returns the slot
+// of this lane's expert (-1: not taken) and the mask of filled slots.
+struct RowSelection {
+    int slot;
+    unsigned long long filled;  // bit k: slot k holds a valid expert
+};
+
+__device__ RowSelection select_row_64(const RouteParams &p, int r, int lane, int *lds_ids) {
+    const int E = p.experts, K = p.top_k;
+    const bool have = lane < E;
+    const float logit = have ? p.logits[(long)r * E + lane] : 0.0f;
+    const float bias = have ? p.bias[lane] : 0.0f;
+    const float score = have ? sigmoid_exact(logit) : 0.0f;
+    const float sel = have ? score + bias : -INFINITY;
+    RowSelection rs{-1, 0ull};
+    if (p.fixed_ids) {
+        for (int k = 0; k < K; ++k)
+            if (p.fixed_ids[(long)r * K + k] == lane) rs.slot = k;
+    } else if (sel > -INFINITY) {
+        const int sel_bits = __float_as_int(sel);
+        int rank = 0;
+#pragma unroll 8
+        for (int o = 0; o < 64; ++o) {
+            const float so = __int_as_float(__builtin_amdgcn_readlane(sel_bits, o));
+            rank += (so > sel) || (so == sel && o < lane);
+        }
+        if (rank < K) rs.slot = rank;
+    }
+    // slot k -> expert; weights summed in slot order (moe_route_finalize)
+    int my_id = -1;
+    float my_w = 0.0f, wsum = 0.0f;
+    for (int k = 0; k < K; ++k) {
+        const unsigned long long m = __ballot(rs.slot == k);
+        const int src = m ? __ffsll((long long)m) - 1 : -1;
+        const float w = src >= 0 ? __int_as_float(__builtin_amdgcn_readlane(__float_as_int(score), src))
+                                 : 0.0f;
+        if (src >= 0) rs.filled |= 1ull << k;
+        if (lane == k) {
+            my_id = src;
+            my_w = w;
+        }
+        wsum += w;
+    }
+    if (p.normalize)
+        wsum += 1e-20f;
+    else
+        wsum = 1.0f;
+    if (lane < K) {
+        p.ids[(long)r * K + lane] = my_id;
+        if (lds_ids) lds_ids[r * K + lane] = my_id;
+        p.weights[(long)r * K + lane] = my_w / wsum * p.routed_scale;
+        if (p.trace) p.trace[(long)r * K + lane] = my_id;
+    }
+    return rs;
+}
+
+// One token row: routing and route tables by a single wave with no barrier.
+// With one row and distinct experts the tables are direct: expert e in slot k
+// is the u-th taken expert (u = k unless a fixed id was invalid), with one
+// list entry at offset u.
+__device__ void route_single_64(const RouteParams &p, int lane) {
+    const int E = p.experts, K = p.top_k;
+    const bool have = lane < E;
+    ExpertWeights ew{};
+    if (p.tasks && have) ew = p.expert_table[lane];  // in flight with the logits
+    const RowSelection rs = select_row_64(p, 0, lane, nullptr);
+    const int slot = rs.slot;
+    if (lane < K && !((rs.filled >> lane) & 1ull)) {
+        p.list_pos[lane] = -1;
+        *p.error = 1;  // prepare_route_tables rejects such ids (moonlight_metal.m:545)
+    }
+    const int n_unique = __popcll(rs.filled);
+    if (lane == 0) *p.n_unique = n_unique;
+    if (have) p.counts[lane] = slot >= 0 ? 1 : 0;
+    if (slot >= 0) {
+        const int u = __popcll(rs.filled & ((1ull << slot) - 1ull));
+        p.offsets[lane] = u;
+        p.unique[u] = lane;
+        p.list_rows[u] = 0;
+        p.list_slots[u] = slot;
+        p.list_pos[slot] = u;
+        if (p.tasks) store_task(p.tasks + u, ew, 1, u);
+    }
+    if (p.tasks && lane >= n_unique && lane < p.task_slots)
+        store_task(p.tasks + lane, ExpertWeights{}, 0, 0);
+}
+
+// Any expert count: the rank form for up to 64 experts, else the arg-max scan.
+__device__ void route_any(const RouteParams &p, int r, int lane, int *lds_ids) {
+    if (p.experts <= 64)
+        (void)select_row_64(p, r, lane, lds_ids);
+    else
+        route_row(p, r, lane, lds_ids);
+}
+
+// Rows routed inside one workgroup (2 rows per wave); larger batches select
+// with one wave per row across many workgroups.
+constexpr int kRouteOneGroupRows = 8;
+
 // Route tables of a small batch (rows * top_k <= kRouteFusedMaxPositions,
 // ids already in LDS), built by one workgroup of 4 waves.
 constexpr int kRouteFusedMaxPositions = 1024;
@@ -144,15 +263,10 @@ __device__ void write_tasks(const RouteParams &p, const int *counts, const int *
     if (!p.tasks) return;
     for (int e = threadIdx.x; e < p.experts; e += blockDim.x) {
         const int rk = rank_of[e];
-        if (rk >= 0 && rk < p.task_slots) {
-            ExpertTask tk;
-            tk.w = p.expert_table[e];
-            tk.count = counts[e];
-            tk.offset = offsets[e];
-            p.tasks[rk] = tk;
-        }
+        if (rk >= 0 && rk < p.task_slots) store_task(p.tasks + rk, p.expert_table[e], counts[e], offsets[e]);
     }
-    for (int u = n_unique + threadIdx.x; u < p.task_slots; u += blockDim.x) p.tasks[u] = ExpertTask{};
+    for (int u = n_unique + threadIdx.x; u < p.task_slots; u += blockDim.x)
+        store_task(p.tasks + u, ExpertWeights{}, 0, 0);
 }
 
 __device__ void small_tables(const RouteParams &p, RouteLds &L) {
@@ -278,7 +392,11 @@ __device__ void small_tables(const RouteParams &p, RouteLds &L) {
 __global__ __launch_bounds__(256) void route_kernel(RouteParams p) {
     __shared__ RouteLds L;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    for (int r = wave; r < p.rows; r += 4) route_row(p, r, lane, L.ids);
+    if (p.rows == 1 && p.experts <= 64) {
+        if (wave == 0) route_single_64(p, lane);
+        return;
+    }
+    for (int r = wave; r < p.rows; r += 4) route_any(p, r, lane, L.ids);
     __syncthreads();
     small_tables(p, L);
 }
@@ -354,7 +472,14 @@ __global__ __launch_bounds__(256) void router_route_kernel(RouteParams p, const 
     __syncthreads();
     if (!last) return;
     __threadfence();
-    for (int r = wave; r < p.rows; r += 4) route_row(p, r, lane, L.ids);
+    if (p.rows == 1 && p.experts <= 64) {
+        if (wave == 0) {
+            route_single_64(p, lane);
+            if (lane == 0) atomicExch(counter, 0u);
+        }
+        return;
+    }
+    for (int r = wave; r < p.rows; r += 4) route_any(p, r, lane, L.ids);
     __syncthreads();
     small_tables(p, L);
     if (threadIdx.x == 0) atomicExch(counter, 0u);
@@ -373,10 +498,20 @@ int router_route(const RouteParams &p, const float *x, const float *norm_w, floa
     return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
 }
 
-// Large batches (prefill): one wave per token row over many workgroups ...
+// Tables of a batch routed by route_select_kernel (ids in memory), one
+// workgroup, rows * top_k <= kRouteFusedMaxPositions.
+__global__ __launch_bounds__(256) void small_tables_kernel(RouteParams p) {
+    __shared__ RouteLds L;
+    const int n_pos = p.rows * p.top_k;
+    for (int q = threadIdx.x; q < n_pos; q += blockDim.x) L.ids[q] = p.ids[q];
+    __syncthreads();
+    small_tables(p, L);
+}
+
+// Larger batches: one wave per token row over many workgroups ...
 __global__ __launch_bounds__(256) void route_select_kernel(RouteParams p) {
     const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (r < p.rows) route_row(p, r, threadIdx.x & 63, nullptr);
+    if (r < p.rows) route_any(p, r, threadIdx.x & 63, nullptr);
 }
 
 // ... then the tables in one workgroup of 16 waves.  List order within an
@@ -675,11 +810,15 @@ int route_topk(const RouteParams &p, hipStream_t stream) {
         !p.list_rows || !p.list_slots || !p.list_pos || !p.error ||
         p.rows * p.top_k > kRouteMaxPositions)
         return kErrArgs;
-    if (p.rows * p.top_k <= kRouteFusedMaxPositions) {
+    if (p.rows <= kRouteOneGroupRows) {
+        // a few rows: selection and tables in one workgroup
         hipLaunchKernelGGL(route_kernel, dim3(1), dim3(256), 0, stream, p);
     } else {
         hipLaunchKernelGGL(route_select_kernel, dim3((p.rows + 3) / 4), dim3(256), 0, stream, p);
-        hipLaunchKernelGGL(route_tables_kernel, dim3(1), dim3(1024), 0, stream, p);
+        if (p.rows * p.top_k <= kRouteFusedMaxPositions)
+            hipLaunchKernelGGL(small_tables_kernel, dim3(1), dim3(256), 0, stream, p);
+        else
+            hipLaunchKernelGGL(route_tables_kernel, dim3(1), dim3(1024), 0, stream, p);
     }
     return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
 }
@@ -721,9 +860,56 @@ int moe_combine(const CombineParams &p, hipStream_t stream) {
 int expert_ffn(const ExpertFfnParams &f, hipStream_t stream) {
     const int max_tasks = f.rows * f.top_k < f.experts ? f.rows * f.top_k : f.experts;
     const int max_rows = f.rows;  // token rows any task can hold
+    const bool presplit = f.limb_x != nullptr;
+    const bool fused_fmt = f.expert_fmt == f.shared_fmt;
     for (int stage = 0; stage < 2; ++stage) {
+        if (presplit) {
+            // the stage's inputs, split once: token rows (RMSNorm'ed) for
+            // stage 0, list rows and shared rows for stage 1
+            LimbRowsParams a, b;
+            if (stage == 0) {
+                a.fmt = f.expert_fmt;
+                a.rows = f.rows;
+                a.I = f.hidden;
+                a.x = f.x;
+                a.x_stride = f.hidden;
+                a.norm_w = f.norm_w;
+                a.eps = f.eps;
+                a.out = f.limb_x;
+                a.out_stride = f.limb_x_stride;
+                if (f.has_shared && !fused_fmt) {
+                    b = a;
+                    b.fmt = f.shared_fmt;
+                    b.out = f.limb_xs;
+                }
+            } else {
+                a.fmt = f.expert_fmt;
+                a.rows = f.rows * f.top_k;
+                a.I = f.inter;
+                a.x = f.expert_hidden;
+                a.x_stride = f.inter;
+                a.out = f.limb_h;
+                a.out_stride = f.limb_h_stride;
+                if (f.has_shared) {
+                    b.fmt = f.shared_fmt;
+                    b.rows = f.rows;
+                    b.I = f.shared_width;
+                    b.x = f.shared_hidden;
+                    b.x_stride = f.shared_width;
+                    b.out = f.limb_sh;
+                    b.out_stride = f.limb_sh_stride;
+                }
+            }
+            if (int err = limb_quantise_rows(a, b, stream)) return err;
+        }
         GemvLaunch L;
         ExpertGemvParams &e = L.expert;
+        if (presplit) {
+            e.limbs = stage == 0 ? f.limb_x : f.limb_h;
+            e.limb_stride = stage == 0 ? f.limb_x_stride : f.limb_h_stride;
+            e.sh_limbs = stage == 0 ? (fused_fmt ? f.limb_x : f.limb_xs) : f.limb_sh;
+            e.sh_limb_stride = stage == 0 ? f.limb_x_stride : f.limb_sh_stride;
+        }
         e.stage = stage;
         e.tasks = f.tasks;
         e.experts = f.expert_table;
@@ -762,28 +948,29 @@ int expert_ffn(const ExpertFfnParams &f, hipStream_t stream) {
         const bool fused = f.expert_fmt == f.shared_fmt && f.has_shared;
         // routed (+ shared when the formats agree)
         {
+            const int widest_I = fused && shared_I > routed_I ? shared_I : routed_I;
             GemvPlan plan = plan_expert_gemv(f.expert_fmt, routed_O, routed_I, max_rows, dual,
-                                             max_tasks + (fused ? 2 : 0));
+                                             max_tasks + (fused ? 2 : 0), widest_I);
             GemvLaunch Lr = L;
+            const int per_block = gemv_rows_per_block(plan, dual);
             Lr.expert.routed_tasks = max_tasks;
+            Lr.expert.routed_blocks = (routed_O + per_block - 1) / per_block;
             Lr.expert.shared_task = fused ? 1 : 0;
-            int per_block = gemv_rows_per_block(plan, dual);
-            int blocks_x = (routed_O + per_block - 1) / per_block;
-            if (fused) {
-                const int sb = (shared_O + per_block - 1) / per_block;
-                if (sb > blocks_x) blocks_x = sb;
-            }
-            dim3 grid(blocks_x, max_tasks + (fused ? 1 : 0));
+            const int shared_blocks = fused ? (shared_O + per_block - 1) / per_block : 0;
+            const dim3 grid(max_tasks * Lr.expert.routed_blocks + shared_blocks,
+                            (max_rows + plan.b - 1) / plan.b);
             if (!dispatch_gemv(f.expert_fmt, Lr, 1, plan, grid, stream)) return kErrArgs;
-            (void)shared_I;
         }
         if (f.has_shared && !fused) {
-            GemvPlan plan = plan_expert_gemv(f.shared_fmt, shared_O, shared_I, max_rows, dual, 1);
+            GemvPlan plan = plan_expert_gemv(f.shared_fmt, shared_O, shared_I, max_rows, dual, 1,
+                                             shared_I);
             GemvLaunch Ls = L;
             Ls.expert.routed_tasks = 0;
+            Ls.expert.routed_blocks = 1;
             Ls.expert.shared_task = 1;
             const int per_block = gemv_rows_per_block(plan, dual);
-            dim3 grid((shared_O + per_block - 1) / per_block, 1);
+            const dim3 grid((shared_O + per_block - 1) / per_block,
+                            (max_rows + plan.b - 1) / plan.b);
             if (!dispatch_gemv(f.shared_fmt, Ls, 1, plan, grid, stream)) return kErrArgs;
         }
     }

@@ -20,6 +20,7 @@
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <ctime>
 #include <string>
@@ -113,6 +114,9 @@ struct MoonlightSession {
     int *offsets = nullptr, *list_rows = nullptr, *list_slots = nullptr, *list_pos = nullptr;
     int *route_error = nullptr, *route_trace = nullptr, *ids = nullptr;
     ExpertTask *expert_tasks = nullptr;  // [experts] per-task table of the expert GEMVs
+    // pre-split limb rows of the expert GEMV inputs (batches of 2+ rows)
+    unsigned char *limb_x = nullptr, *limb_xs = nullptr, *limb_h = nullptr, *limb_sh = nullptr;
+    long limb_x_stride = 0, limb_h_stride = 0, limb_sh_stride = 0;
     unsigned *route_counter = nullptr;   // last-workgroup counter of the fused routing
     float *expert_hidden = nullptr, *expert_out = nullptr;
     float *shared_hidden = nullptr, *shared_out = nullptr, *dense_hidden = nullptr;
@@ -919,6 +923,32 @@ int attention(MoonlightSession *s, int layer, const float *x, int rows, int posi
                      nullptr, resid);
 }
 
+// Expert GEMV batches of at least this many token rows split their inputs
+// into limb rows once per stage (limb_quantise_rows) rather than in every
+// workgroup.  MLH_PRESPLIT_MIN_ROWS overrides (read once).
+static int presplit_min_rows() {
+    static const int v = [] {
+        const char *env = getenv("MLH_PRESPLIT_MIN_ROWS");
+        return env ? atoi(env) : 2;
+    }();
+    return v;
+}
+
+// Decode batches: router matvec and routing in one launch (last-workgroup
+// pattern) or as two launches (measured faster: the fused form pays a device
+// scope release per workgroup).  MLH_FUSED_ROUTE=1 selects one (read once).
+static bool fused_route_enabled() {
+    static const bool v = [] {
+        const char *env = getenv("MLH_FUSED_ROUTE");
+        return env && atoi(env) != 0;
+    }();
+    return v;
+}
+
+// The MFMA router (32 x 32 tiles, one workgroup per tile) has the
+// parallelism for prefill batches; fewer rows take the GEMV.
+constexpr int kRouterMfmaMinRows = 256;
+
 int route(MoonlightSession *s, int layer, const float *x, int rows, const float *norm_w,
           int *trace) {
     const ModelConfig &c = s->model->cfg;
@@ -926,9 +956,10 @@ int route(MoonlightSession *s, int layer, const float *x, int rows, const float 
     const bool f32_router = lp.router.fmt == kF32;
     const float *router_w = reinterpret_cast<const float *>(lp.router.w);
     // decode batches: router matvec and routing in one launch
-    const bool fused = f32_router && rows <= kFusedRouteMaxRows && c.hidden_size % 4 == 0;
+    const bool fused = fused_route_enabled() && f32_router && rows <= kFusedRouteMaxRows &&
+                       c.hidden_size % 4 == 0;
     if (!fused) {
-        if (rows >= kGemmMinRows && f32_router && c.hidden_size % 8 == 0) {
+        if (rows >= kRouterMfmaMinRows && f32_router && c.hidden_size % 8 == 0) {
             if (router_logits(x, norm_w, c.rms_norm_epsilon, router_w, rows, c.expert_count,
                               c.hidden_size, s->router_logits, stream_of(s)))
                 return kErrLaunch;
@@ -993,6 +1024,16 @@ int experts(MoonlightSession *s, int layer, const float *x, int rows, const floa
     f.offsets = s->offsets;
     f.list_rows = s->list_rows;
     f.tasks = s->expert_tasks;  // written by route()
+    if (rows >= presplit_min_rows() && c.hidden_size % 32 == 0 &&
+        c.moe_intermediate_size % 32 == 0) {
+        f.limb_x = s->limb_x;
+        f.limb_xs = s->limb_xs;
+        f.limb_h = s->limb_h;
+        f.limb_sh = s->limb_sh;
+        f.limb_x_stride = s->limb_x_stride;
+        f.limb_h_stride = s->limb_h_stride;
+        f.limb_sh_stride = s->limb_sh_stride;
+    }
     f.x = x;
     f.norm_w = norm_w;
     f.eps = c.rms_norm_epsilon;
@@ -1200,6 +1241,14 @@ extern "C" int moonlight_session_create(MoonlightSession **out, MoonlightModel *
         session_alloc(s, &s->list_pos, mb * K, error, error_size) &&
         session_alloc(s, &s->route_error, 1, error, error_size) &&
         session_alloc(s, &s->expert_tasks, E, error, error_size) &&
+        // limb rows sized for q8 (the larger layout) so any format fits
+        (s->limb_x_stride = limb_row_lds(kQ8, c.hidden_size),
+         s->limb_h_stride = limb_row_lds(kQ8, c.moe_intermediate_size > 0 ? c.moe_intermediate_size : 16),
+         s->limb_sh_stride = limb_row_lds(kQ8, sw > 0 ? (int)sw : 16), true) &&
+        session_alloc(s, &s->limb_x, mb * s->limb_x_stride, error, error_size) &&
+        session_alloc(s, &s->limb_xs, mb * s->limb_x_stride, error, error_size) &&
+        session_alloc(s, &s->limb_h, mb * K * s->limb_h_stride, error, error_size) &&
+        session_alloc(s, &s->limb_sh, mb * s->limb_sh_stride, error, error_size) &&
         session_alloc(s, &s->route_counter, 1, error, error_size) &&
         hipMemset(s->route_counter, 0, sizeof(unsigned)) == hipSuccess &&
         session_alloc(s, &s->route_trace, L * mb * K, error, error_size) &&
