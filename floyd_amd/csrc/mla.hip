@@ -297,6 +297,184 @@ __global__ __launch_bounds__(256) void mla_attend_kernel(MlaParams p) {
     }
 }
 
+// The same split of kMlaKeysPerSplit keys on fp32 matrix cores
+// (v_mfma_f32_16x16x4_f32: fp32 products and sums, like the VALU form, in
+// another order).  Operand layout (measured on gfx950): lane l supplies
+// A[l % 16][l / 16] and B[l / 16][l % 16]; result register i of lane l is
+// D[4 (l / 16) + i][l % 16].  Four MFMAs consume one 16-byte LDS read per
+// operand: in step j lane group g = l / 16 takes k index 4 g + j.
+//   scores  S[key][head] = [lat | rope][key] . [qa | q_rope][head] over the
+//           latent + rope dims; the 4 waves split those dims and meet in LDS
+//           (sums in wave order).
+//   context LC[head][d] = sum_key P[head][key] lat[key][d]; the 4 waves split
+//           the 16-wide d tiles.
+// Rows in LDS hold latent + rope zero-padded to a multiple of 16, stride
+// kAttnRowStride floats (16-byte aligned, bank-spread).
+constexpr int kAttnDims = kMlaMaxLatent + 64;       // latent + rope
+constexpr int kAttnRowStride = kAttnDims + 4;       // floats
+constexpr int kAttnPStride = kMlaKeysPerSplit + 4;  // floats, P[head][key]
+constexpr size_t kAttnMfmaLds =
+    sizeof(float) * ((size_t)(kMlaKeysPerSplit + kMlaMaxHeads) * kAttnRowStride +
+                     4 * kMlaKeysPerSplit * kMlaMaxHeads + kMlaMaxHeads * kAttnPStride);
+
+typedef float f32x4v __attribute__((ext_vector_type(4)));
+
+__global__ __launch_bounds__(256) void mla_attend_mfma_kernel(MlaParams p) {
+    constexpr int H = kMlaMaxHeads;
+    constexpr int KS = kMlaKeysPerSplit;
+    extern __shared__ __attribute__((aligned(16))) float attn_lds[];
+    float *lat_s = attn_lds;                        // [KS][stride]
+    float *q_s = lat_s + KS * kAttnRowStride;       // [H][stride]
+    float *sc_s = q_s + H * kAttnRowStride;         // [4 waves][KS][H]
+    float *p_s = sc_s + 4 * KS * H;                 // [H][KS + 4]
+    __shared__ float smax[H], ssum[H];
+    const int split = blockIdx.x;
+    const int r = blockIdx.y;
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int g = lane >> 4, m16 = lane & 15;
+    const int keys = p.position + r + 1;
+    const int k0 = split * KS;
+    const int nk = keys - k0 < KS ? keys - k0 : KS;
+    const long part = ((long)r * p.max_splits + split) * H;
+    if (nk <= 0) {
+        if (t < H) {
+            p.part_max[part + t] = -INFINITY;
+            p.part_sum[part + t] = 0.0f;
+        }
+        return;
+    }
+    const int D = p.latent, R = p.rope;
+    const int KD = (D + R + 15) & ~15;  // padded dims
+    const int c4n = KD / 4;
+    // ---- latent + rope rows of the split, and the head queries, into LDS by
+    // DMA (global_load_lds: 16 bytes per lane into M0 + 16 * lane): a 512-wide
+    // latent row is 2 KB = two wave transfers, a rope row one partial one.
+    // Keys past the causal end and absent heads copy a valid row (finite
+    // values; their probabilities are 0 / their outputs unused).
+    {
+        const int nrows = KS + H;
+        for (int row = wave; row < nrows; row += 4) {
+            const float *lsrc, *rsrc;
+            if (row < KS) {
+                const long k = k0 + (row < nk ? row : nk - 1);
+                lsrc = p.latent_cache + k * D;
+                rsrc = p.rope_cache + k * R;
+            } else {
+                const int h = row - KS;
+                const long qh = (long)r * p.heads + (h < p.heads ? h : 0);
+                lsrc = p.query_absorbed + qh * D;
+                rsrc = p.query_rope + qh * R;
+            }
+            __attribute__((address_space(3))) float *dst =
+                (__attribute__((address_space(3))) float *)(lat_s + row * kAttnRowStride);
+            for (int c0 = 0; c0 < D; c0 += 256) {  // 64 lanes x 4 floats
+                if (c0 + 4 * lane < D)
+                    __builtin_amdgcn_global_load_lds(
+                        (const __attribute__((address_space(1))) void *)(lsrc + c0 + 4 * lane),
+                        dst + c0, 16, 0, 0);
+            }
+            if (4 * lane < R)
+                __builtin_amdgcn_global_load_lds(
+                    (const __attribute__((address_space(1))) void *)(rsrc + 4 * lane), dst + D, 16,
+                    0, 0);
+        }
+        __builtin_amdgcn_s_waitcnt(0);  // this wave's transfers have landed
+    }
+    __syncthreads();
+    // ---- scores: wave w takes the 16-dim steps w, w + 4, ...
+    {
+        // two accumulators per key tile (even / odd MFMA of a step) keep two
+        // independent chains in flight
+        f32x4v acc[KS / 16][2];
+#pragma unroll
+        for (int kt = 0; kt < KS / 16; ++kt) acc[kt][0] = acc[kt][1] = f32x4v{0.f, 0.f, 0.f, 0.f};
+        for (int d0 = wave * 16; d0 < KD; d0 += 64) {
+            const f32x4 qv = *reinterpret_cast<const f32x4 *>(q_s + m16 * kAttnRowStride + d0 + 4 * g);
+#pragma unroll
+            for (int kt = 0; kt < KS / 16; ++kt) {
+                const f32x4 av = *reinterpret_cast<const f32x4 *>(
+                    lat_s + (16 * kt + m16) * kAttnRowStride + d0 + 4 * g);
+                acc[kt][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(av.x, qv.x, acc[kt][0], 0, 0, 0);
+                acc[kt][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(av.y, qv.y, acc[kt][1], 0, 0, 0);
+                acc[kt][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(av.z, qv.z, acc[kt][0], 0, 0, 0);
+                acc[kt][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(av.w, qv.w, acc[kt][1], 0, 0, 0);
+            }
+        }
+#pragma unroll
+        for (int kt = 0; kt < KS / 16; ++kt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                sc_s[(wave * KS + 16 * kt + 4 * g + i) * H + m16] = acc[kt][0][i] + acc[kt][1][i];
+    }
+    __syncthreads();
+    // ---- local softmax statistics: 16 lanes per head, keys sub, sub + 16
+    {
+        const int h = t >> 4, sub = t & 15;
+        float sv[KS / 16];
+        float mx = -INFINITY;
+#pragma unroll
+        for (int u = 0; u < KS / 16; ++u) {
+            const int j = sub + 16 * u;
+            const float sum = (sc_s[(0 * KS + j) * H + h] + sc_s[(1 * KS + j) * H + h]) +
+                              (sc_s[(2 * KS + j) * H + h] + sc_s[(3 * KS + j) * H + h]);
+            sv[u] = j < nk ? sum * p.scale : -INFINITY;
+            mx = fmaxf(mx, sv[u]);
+        }
+#pragma unroll
+        for (int o = 8; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+        float sum = 0.0f;
+#pragma unroll
+        for (int u = 0; u < KS / 16; ++u) {
+            const int j = sub + 16 * u;
+            const float e = j < nk ? expf(sv[u] - mx) : 0.0f;
+            p_s[h * kAttnPStride + j] = e;
+            sum += e;
+        }
+#pragma unroll
+        for (int o = 8; o >= 1; o >>= 1) sum += __shfl_xor(sum, o, 64);
+        if (sub == 0) {
+            smax[h] = mx;
+            ssum[h] = sum;
+        }
+    }
+    __syncthreads();
+    if (t < H) {
+        p.part_max[part + t] = smax[t];
+        p.part_sum[part + t] = ssum[t];
+    }
+    // ---- context: wave w takes the 16-wide d tiles w, w + 4, ...
+    // (P rows are read once per pair of tiles; the two tiles' chains interleave)
+    f32x4 pv[KS / 16];
+#pragma unroll
+    for (int u = 0; u < KS / 16; ++u)
+        pv[u] = *reinterpret_cast<const f32x4 *>(p_s + m16 * kAttnPStride + 16 * u + 4 * g);
+    for (int dt = wave; dt < D / 16; dt += 8) {
+        const bool two = dt + 4 < D / 16;
+        f32x4v acc[2] = {f32x4v{0.f, 0.f, 0.f, 0.f}, f32x4v{0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+        for (int u = 0; u < KS / 16; ++u) {
+            const float *lb = lat_s + (16 * u + 4 * g) * kAttnRowStride + dt * 16 + m16;
+            const float *lb2 = two ? lb + 64 : lb;
+            const float pj[4] = {pv[u].x, pv[u].y, pv[u].z, pv[u].w};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                acc[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(pj[j], lb[j * kAttnRowStride], acc[0],
+                                                             0, 0, 0);
+                acc[1] = __builtin_amdgcn_mfma_f32_16x16x4f32(pj[j], lb2[j * kAttnRowStride],
+                                                             acc[1], 0, 0, 0);
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int h = 4 * g + i;
+            if (h < p.heads) {
+                p.part_lc[(part + h) * D + dt * 16 + m16] = acc[0][i];
+                if (two) p.part_lc[(part + h) * D + (dt + 4) * 16 + m16] = acc[1][i];
+            }
+        }
+    }
+}
+
 // lc_h = sum_s e^{m_s - M} lc_s / sum_s e^{m_s - M} l_s over the key splits.
 // Workgroup (row, head, 64 latent dims): 4 thread groups take the splits
 // g, g + 4, ... (loads in batches of 8 before their FMAs) and meet in LDS in
@@ -408,12 +586,20 @@ int mla_attention_core(const MlaParams &p, hipStream_t stream) {
     const int splits = (p.position + p.rows + kMlaKeysPerSplit - 1) / kMlaKeysPerSplit;
     const dim3 grid(splits, p.rows);
     const size_t lds = (size_t)kMlaKeysPerSplit * p.latent * sizeof(float);
-    switch (p.latent / 64) {
-    case 1: launch_attend<1>(grid, lds, stream, p); break;
-    case 2: launch_attend<2>(grid, lds, stream, p); break;
-    case 4: launch_attend<4>(grid, lds, stream, p); break;
-    case 8: launch_attend<8>(grid, lds, stream, p); break;
-    default: return kErrArgs;
+    if (p.rope % 4 == 0 && (p.latent + p.rope) % 16 == 0 && p.latent + p.rope <= kAttnDims) {
+        static const bool attr = hipFuncSetAttribute(
+            reinterpret_cast<const void *>(&mla_attend_mfma_kernel),
+            hipFuncAttributeMaxDynamicSharedMemorySize, (int)kAttnMfmaLds) == hipSuccess;
+        (void)attr;
+        hipLaunchKernelGGL(mla_attend_mfma_kernel, grid, dim3(256), kAttnMfmaLds, stream, p);
+    } else {
+        switch (p.latent / 64) {
+        case 1: launch_attend<1>(grid, lds, stream, p); break;
+        case 2: launch_attend<2>(grid, lds, stream, p); break;
+        case 4: launch_attend<4>(grid, lds, stream, p); break;
+        case 8: launch_attend<8>(grid, lds, stream, p); break;
+        default: return kErrArgs;
+        }
     }
     hipLaunchKernelGGL(mla_merge_kernel, dim3(p.rows, p.heads, (p.latent + 63) / 64), dim3(256),
                        0, stream, p);
