@@ -295,7 +295,7 @@ __device__ __forceinline__ void gemv_block(const GemvJob<B> job) {
 // most 0.75 * amax_chunk / 2^22 per element and the in-chunk sums are exact,
 // so results agree with the fp32 matmul to fp32 rounding (like a different
 // summation order).  The arithmetic drops from ~2.3 VALU instructions per
-// weight (convert + fma) to ~0.9 (q8) / ~1.3 (q4), which is what kept the fp32
+// weight (convert + fma) to ~1.1 (q8) / ~1.3 (q4), which is what kept the fp32
 // form from streaming at HBM rate.
 //
 // Loads are ordered for the in-order vector memory counter: x (and norm_w),

@@ -1,11 +1,12 @@
 // qgemm.hip -- grouped int8-MFMA GEMM for prefill (see qgemm.h for the
 // numerics).  gfx950: v_mfma_i32_32x32x32_i8, wave64.
 //
-// Workgroup: 4 waves in a 2 x 2 arrangement over a 128 (token rows) x 128
-// (weight rows) tile; each wave owns 64 x 64 = 2 x 2 MFMA blocks per limb.
-// Pipeline: the next 64-wide k slice is fetched into registers while the
-// current one is multiplied out of LDS (double-buffered, one barrier per
-// slice).  MFMA operand layout (measured on gfx950): lane l supplies row
+// Workgroup: 4 waves in a 2 x 2 arrangement over a 128 (token rows) x 256
+// (weight rows) tile; each wave owns 64 x 128 = 2 x 4 MFMA blocks per limb.
+// Pipeline: two LDS stages; while one k slice is multiplied out of LDS the
+// next is in flight (q8: 128-wide slices copied straight into LDS by
+// global_load_lds; q4: 64-wide slices unpacked in registers on the way), one
+// barrier per slice.  MFMA operand layout (measured on gfx950): lane l supplies row
 // (l % 32) and the 16-byte k chunk (l / 32) of a 32-wide k step, for A rows and
 // for B columns alike; result register r of lane l is
 // C[(r / 4) * 8 + (l / 32) * 4 + r % 4][l % 32].
