@@ -135,32 +135,35 @@ int limb_quantise_rows(const LimbRowsParams &a, const LimbRowsParams &b, hipStre
 static constexpr long kTargetWaves = 2048;
 
 static bool plan_override(GemvPlan *plan) {
-    static int parsed = 0, kt = 0, r = 0, ks = 0;
+    static int parsed = 0, kt = 0, r = 0, ks = 0, waves = 4;
     if (!parsed) {
         const char *env = getenv("MLH_GEMV_PLAN");
-        if (!env || sscanf(env, "%d,%d,%d", &kt, &r, &ks) != 3) kt = 0;
+        const int n = env ? sscanf(env, "%d,%d,%d,%d", &kt, &r, &ks, &waves) : 0;
+        if (n < 3) kt = 0;
+        if (n < 4) waves = 4;
         parsed = 1;
     }
     if (!kt) return false;
     plan->kt = kt;
     plan->r = r;
     plan->ks = ks;
+    plan->waves = waves;
     return true;
 }
 
 // Plans measured best on MI355X for the Moonlight decode shapes (batch 1):
 // sweeps over kt x r x ks of back-to-back launches, 400+ MB weight rotation.
 struct PlanEntry {
-    int fmt, O, I, dual, kt, r, ks;
+    int fmt, O, I, dual, kt, r, ks, waves;
 };
 static const PlanEntry kMeasuredPlans[] = {
-    {kQ4, 11264, 2048, 0, 1, 4, 1}, {kQ8, 11264, 2048, 0, 1, 4, 1},
-    {kQ4, 2048, 11264, 0, 1, 8, 4}, {kQ8, 2048, 11264, 0, 1, 4, 4},
-    {kQ8, 3072, 2048, 0, 2, 1, 1},  {kQ8, 2048, 2048, 0, 2, 1, 1},
-    {kQ8, 2048, 1408, 0, 2, 1, 1},  {kQ8, 2048, 2816, 0, 1, 8, 4},
-    {kQ8, 576, 2048, 0, 2, 1, 1},   {kF32, 64, 2048, 0, 4, 1, 4},
-    {kQ4, 2048, 1408, 0, 1, 2, 1},  {kQ8, 1536, 2048, 0, 2, 1, 1},
-    {kQ8, 3072, 1536, 0, 2, 2, 1},
+    {kQ4, 11264, 2048, 0, 1, 4, 1, 4}, {kQ8, 11264, 2048, 0, 1, 4, 1, 4},
+    {kQ4, 2048, 11264, 0, 2, 1, 1, 8}, {kQ8, 2048, 11264, 0, 2, 1, 1, 8},
+    {kQ8, 3072, 2048, 0, 1, 2, 1, 8},  {kQ8, 2048, 2048, 0, 2, 1, 1, 8},
+    {kQ8, 2048, 1408, 0, 2, 1, 1, 8},  {kQ8, 2048, 2816, 0, 2, 1, 1, 8},
+    {kQ8, 576, 2048, 0, 2, 1, 1, 4},   {kF32, 64, 2048, 0, 4, 1, 4, 4},
+    {kQ4, 2048, 1408, 0, 1, 2, 1, 4},  {kQ8, 1536, 2048, 0, 2, 1, 1, 8},
+    {kQ8, 3072, 1536, 0, 2, 1, 1, 8},
 };
 
 GemvPlan plan_gemv(int fmt, int O, int I, int rows, bool dual) {
@@ -180,6 +183,7 @@ GemvPlan plan_gemv(int fmt, int O, int I, int rows, bool dual) {
     if (plan_override(&plan)) {
         if (plan.r * plan.b > 16) plan.r = 16 / plan.b;
         if (dual && plan.r < 2) plan.r = 2;
+        if (fmt == kF32 || plan.ks != 1) plan.waves = 4;
         return plan;
     }
     if (plan.b == 1) {
@@ -188,6 +192,7 @@ GemvPlan plan_gemv(int fmt, int O, int I, int rows, bool dual) {
                 plan.kt = e.kt;
                 plan.r = e.r;
                 plan.ks = e.ks;
+                plan.waves = e.waves;
                 return plan;
             }
         }
@@ -255,6 +260,7 @@ static bool expert_plan_override(bool dual, GemvPlan *plan) {
 
 GemvPlan plan_expert_gemv(int fmt, int O, int I, int rows, bool dual, int tasks, int max_I) {
     GemvPlan plan = plan_gemv(fmt, O, max_I, rows, dual);
+    plan.waves = 4;  // grouped launches use 4-wave workgroups
     if (plan.lpr < 64) return plan;
     if (fmt != kF32) {
         if (!expert_plan_override(dual, &plan)) {
@@ -291,15 +297,15 @@ GemvPlan plan_expert_gemv(int fmt, int O, int I, int rows, bool dual, int tasks,
 
 int gemv_rows_per_block(const GemvPlan &plan, bool dual) {
     const int out = dual ? plan.r / 2 : plan.r;
-    return out * (64 / plan.lpr) * (plan.ks == 1 ? 4 : 1);
+    return out * (64 / plan.lpr) * (plan.ks == 1 ? plan.waves : 1);
 }
 
 // Template name of the kernel gemv() launches for this shape (vector path).
 std::string gemv_kernel_name(int fmt, int O, int I, int rows, bool dual) {
     const GemvPlan pl = plan_gemv(fmt, O, I, rows < kMaxGemvRows ? rows : kMaxGemvRows, dual);
     char buf[96];
-    snprintf(buf, sizeof(buf), "mlh::gemv_kernel<0, %d, %d, %d, %d, %d, %d>", fmt, pl.b, pl.kt,
-             pl.lpr, pl.r, pl.ks);
+    snprintf(buf, sizeof(buf), "mlh::gemv_kernel<0, %d, %d, %d, %d, %d, %d, %d>", fmt, pl.b,
+             pl.kt, pl.lpr, pl.r, pl.ks, pl.waves);
     return buf;
 }
 

@@ -455,23 +455,26 @@ __device__ __forceinline__ float limb_chunk_dot(u32x4 w, const unsigned char *ro
 // plan covers in one tile can need (KS * KT * 64 chunks), at most 6 (an
 // 11264-wide row), one for B > 1; the rest of a wider row is loaded after the
 // weights.
-template <int FMT, int B, int KT, int KS>
+template <int FMT, int B, int KT, int KS, int W>
 constexpr int limb_pre_passes() {
     constexpr int elems = KS * KT * 64 * FmtTraits<FMT>::kElemsPerChunk;
-    constexpr int passes = (elems + kLimbPassElems - 1) / kLimbPassElems;
+    constexpr int pass = W * kWave * 8;
+    constexpr int passes = (elems + pass - 1) / pass;
     return B == 1 ? (passes < 6 ? passes : 6) : 1;
 }
 
-// One job: the token rows of job.x against row block job.row_block of W.
-template <int FMT, int B, int KT, int LPR, int R, int KS>
+// One job: the token rows of job.x against row block job.row_block of the
+// weights.  W waves per workgroup (4 or 8); with KS > 1 the W waves split k.
+template <int FMT, int B, int KT, int LPR, int R, int KS, int W = 4>
 __device__ __forceinline__ void limb_block(const GemvJob<B> job, unsigned char *lds) {
     constexpr int GPW = kWave / LPR;
     constexpr int NV = R * B;
-    constexpr int NJP = limb_pre_passes<FMT, B, KT, KS>();
+    constexpr int NJP = limb_pre_passes<FMT, B, KT, KS, W>();
+    constexpr int PASS = W * kWave * 8;  // x elements split per workgroup pass
     static_assert(NV <= LPR, "partial sums exceed the lane group");
-    static_assert(KS == 1 || LPR == kWave, "k-split needs whole-wave row groups");
-    __shared__ float red[4][NV];
-    __shared__ float ss_red[4][B];
+    static_assert(KS == 1 || (LPR == kWave && KS == W), "k-split needs whole-wave row groups");
+    __shared__ float red[W][NV];
+    __shared__ float ss_red[W][B];
 
     const int tid = threadIdx.x;
     const int lane = tid & (kWave - 1);
@@ -481,10 +484,10 @@ __device__ __forceinline__ void limb_block(const GemvJob<B> job, unsigned char *
     const bool dual = job.epilogue == kEpiSiluDual;
     const bool residual = job.epilogue == kEpiResidual;
     const int out_per_group = dual ? R / 2 : R;
-    const int row_wave = KS == 1 ? job.row_block * 4 + wave : job.row_block;
+    const int row_wave = KS == 1 ? job.row_block * W + wave : job.row_block;
     const int kpart = KS == 1 ? 0 : wave;
     const int out0 = (row_wave * GPW + group) * out_per_group;
-    const int rpb = out_per_group * GPW * (KS == 1 ? 4 : 1);  // outputs per row block
+    const int rpb = out_per_group * GPW * (KS == 1 ? W : 1);  // outputs per row block
     // whole workgroups past the end leave (the prologue below synchronises)
     if (job.row_block * rpb >= job.O) return;
 
@@ -492,7 +495,7 @@ __device__ __forceinline__ void limb_block(const GemvJob<B> job, unsigned char *
     const int row_bytes = row_bytes_of(FMT, I);
     const int nc = row_bytes / 16;
     const int lds_row = limb_row_lds(FMT, I);
-    const int npass = (I + kLimbPassElems - 1) / kLimbPassElems;
+    const int npass = (I + PASS - 1) / PASS;
 
     const bool presplit = job.limbs[0] != nullptr;
     if (presplit) {
@@ -501,7 +504,7 @@ __device__ __forceinline__ void limb_block(const GemvJob<B> job, unsigned char *
 #pragma unroll
         for (int b = 0; b < B; ++b) {
             if (b < job.rows) {
-                for (int blk = wave; blk < nblk; blk += 4) {
+                for (int blk = wave; blk < nblk; blk += W) {
                     __builtin_amdgcn_global_load_lds(
                         (const __attribute__((address_space(1))) void *)(job.limbs[b] + blk * 1024 +
                                                                          lane * 16),
@@ -517,7 +520,7 @@ __device__ __forceinline__ void limb_block(const GemvJob<B> job, unsigned char *
 #pragma unroll
     for (int j = 0; j < NJP; ++j) {
         if (!presplit && j < npass) {
-            const int e0 = tid * 8 + j * kLimbPassElems;
+            const int e0 = tid * 8 + j * PASS;
             const int ec = e0 < I ? e0 : 0;
 #pragma unroll
             for (int b = 0; b < B; ++b) {
@@ -602,7 +605,7 @@ __device__ __forceinline__ void limb_block(const GemvJob<B> job, unsigned char *
         for (int b = 0; b < B; ++b) ss[b] = 0.0f;
 #pragma unroll
         for (int j = 0; j < NJP; ++j) {
-            if (j < npass && tid * 8 + j * kLimbPassElems < I) {
+            if (j < npass && tid * 8 + j * PASS < I) {
 #pragma unroll
                 for (int b = 0; b < B; ++b)
                     if (b < job.rows)
@@ -613,7 +616,7 @@ __device__ __forceinline__ void limb_block(const GemvJob<B> job, unsigned char *
             }
         }
         for (int j = NJP; j < npass; ++j) {
-            const int e0 = tid * 8 + j * kLimbPassElems;
+            const int e0 = tid * 8 + j * PASS;
             if (e0 < I) {
 #pragma unroll
                 for (int b = 0; b < B; ++b)
@@ -632,9 +635,13 @@ __device__ __forceinline__ void limb_block(const GemvJob<B> job, unsigned char *
         }
         __syncthreads();
 #pragma unroll
-        for (int b = 0; b < B; ++b)
-            inv_rms[b] = 1.0f / sqrtf(((ss_red[0][b] + ss_red[1][b]) + (ss_red[2][b] + ss_red[3][b])) /
-                                          (float)I + job.eps);
+        for (int b = 0; b < B; ++b) {
+            float tot = (ss_red[0][b] + ss_red[1][b]) + (ss_red[2][b] + ss_red[3][b]);
+#pragma unroll
+            for (int w = 4; w < W; w += 4)
+                tot += (ss_red[w][b] + ss_red[w + 1][b]) + (ss_red[w + 2][b] + ss_red[w + 3][b]);
+            inv_rms[b] = 1.0f / sqrtf(tot / (float)I + job.eps);
+        }
     }
 
     // ---- 5. quantise x into LDS
@@ -651,14 +658,14 @@ __device__ __forceinline__ void limb_block(const GemvJob<B> job, unsigned char *
 #pragma unroll
     for (int j = 0; j < NJP; ++j) {
         if (!presplit && j < npass) {
-            const int e0 = tid * 8 + j * kLimbPassElems;
+            const int e0 = tid * 8 + j * PASS;
 #pragma unroll
             for (int b = 0; b < B; ++b)
                 if (b < job.rows) quantise_pass(xv[j][b], nv[j], b, e0);
         }
     }
     for (int j = presplit ? npass : NJP; j < npass; ++j) {
-        const int e0 = tid * 8 + j * kLimbPassElems;
+        const int e0 = tid * 8 + j * PASS;
         const int ec = e0 < I ? e0 : 0;
         f32x4 np[2] = {f32x4{1.f, 1.f, 1.f, 1.f}, f32x4{1.f, 1.f, 1.f, 1.f}};
         if (job.norm_w) {
@@ -707,6 +714,9 @@ __device__ __forceinline__ void limb_block(const GemvJob<B> job, unsigned char *
             if (writer) red[wave][vi] = value;
             __syncthreads();
             value = (red[0][vi] + red[1][vi]) + (red[2][vi] + red[3][vi]);
+#pragma unroll
+            for (int w = 4; w < W; w += 4)
+                value += (red[w][vi] + red[w + 1][vi]) + (red[w + 2][vi] + red[w + 3][vi]);
             if (wave != 0) return;
         }
         const int vrow = o0 + vr;
@@ -788,12 +798,12 @@ struct GemvLaunch {
 };
 
 // MODE 0: plain GEMV; 1: grouped expert tasks.
-template <int MODE, int FMT, int B, int KT, int LPR, int R, int KS>
+template <int MODE, int FMT, int B, int KT, int LPR, int R, int KS, int W>
 __device__ __forceinline__ void run_job(const GemvJob<B> &job, unsigned char *lds) {
     if constexpr (FMT == kF32)
-        gemv_block<FMT, B, KT, LPR, R, KS>(job);
+        gemv_block<FMT, B, KT, LPR, R, KS>(job);  // 4-wave workgroups
     else
-        limb_block<FMT, B, KT, LPR, R, KS>(job, lds);
+        limb_block<FMT, B, KT, LPR, R, KS, W>(job, lds);
 }
 
 // Dynamic LDS of a launch: the quantised x rows of its widest job.
@@ -802,8 +812,8 @@ __host__ __device__ constexpr int gemv_lds_bytes(int max_I) {
     return FMT == kF32 ? 0 : B * limb_row_lds(FMT, max_I);
 }
 
-template <int MODE, int FMT, int B, int KT, int LPR, int R, int KS>
-__global__ __launch_bounds__(256) void gemv_kernel(GemvLaunch L) {
+template <int MODE, int FMT, int B, int KT, int LPR, int R, int KS, int W = 4>
+__global__ __launch_bounds__(W * 64) void gemv_kernel(GemvLaunch L) {
     extern __shared__ __align__(16) unsigned char gemv_lds[];
     GemvJob<B> job;
     job.row_block = blockIdx.x;
@@ -824,12 +834,12 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvLaunch L) {
             job.x[b] = p.x + r * p.x_stride;
             job.y[b] = p.y + r * p.y_stride;
             job.resid[b] = p.resid ? p.resid + r * p.resid_stride : nullptr;
-            job.limbs[b] = nullptr;
+            job.limbs[b] = p.limbs ? p.limbs + r * p.limb_stride : nullptr;
         }
         job.norm_w = p.norm_w;
         job.eps = p.eps;
         job.epilogue = p.epilogue;
-        run_job<MODE, FMT, B, KT, LPR, R, KS>(job, gemv_lds);
+        run_job<MODE, FMT, B, KT, LPR, R, KS, W>(job, gemv_lds);
     } else {
         const ExpertGemvParams &p = L.expert;
         // flat grid: routed task t owns workgroups t * routed_blocks ..,
@@ -899,7 +909,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvLaunch L) {
                 job.limbs[b] = shared ? (p.sh_limbs ? p.sh_limbs + lrow * p.sh_limb_stride : nullptr)
                                       : (p.limbs ? p.limbs + lrow * p.limb_stride : nullptr);
             }
-            run_job<MODE, FMT, B, KT, LPR, R, KS>(job, gemv_lds);
+            run_job<MODE, FMT, B, KT, LPR, R, KS, W>(job, gemv_lds);
         }
     }
 }
@@ -927,14 +937,16 @@ inline int gemv_lds_bytes_rt(int fmt, int b, int I) {
 // Launch geometry chosen by the host (see gemv.hip, plan_gemv).
 struct GemvPlan {
     int b = 1, kt = 1, lpr = 64, r = 4, ks = 1;
+    int waves = 4;  // per workgroup (8: plain q8 / q4 launches without k split)
 };
 
 // MODE 0 grids cover the plain matrix; MODE 1 callers pass their own grid.
-template <int MODE, int FMT, int B, int KT, int LPR, int R, int KS>
+template <int MODE, int FMT, int B, int KT, int LPR, int R, int KS, int W = 4>
 static void launch_gemv(const GemvLaunch &L, dim3 grid, hipStream_t stream) {
     int max_I;
     if constexpr (MODE == 0) {
-        const int per_block = rows_per_block<LPR, R, KS>(L.plain.epilogue == kEpiSiluDual);
+        const int per_block =
+            rows_per_block<LPR, R, KS>(L.plain.epilogue == kEpiSiluDual) * (KS == 1 ? W / 4 : 1);
         grid = dim3((unsigned)((L.plain.O + per_block - 1) / per_block),
                     (unsigned)((L.plain.rows + B - 1) / B));
         max_I = L.plain.I;
@@ -947,13 +959,13 @@ static void launch_gemv(const GemvLaunch &L, dim3 grid, hipStream_t stream) {
         static bool raised = false;  // per instantiation
         if (!raised) {
             (void)hipFuncSetAttribute(
-                reinterpret_cast<const void *>(&gemv_kernel<MODE, FMT, B, KT, LPR, R, KS>),
+                reinterpret_cast<const void *>(&gemv_kernel<MODE, FMT, B, KT, LPR, R, KS, W>),
                 hipFuncAttributeMaxDynamicSharedMemorySize, kMaxGemvLds);
             raised = true;
         }
     }
-    hipLaunchKernelGGL((gemv_kernel<MODE, FMT, B, KT, LPR, R, KS>), grid, dim3(256), lds, stream,
-                       L);
+    hipLaunchKernelGGL((gemv_kernel<MODE, FMT, B, KT, LPR, R, KS, W>), grid, dim3(W * 64), lds,
+                       stream, L);
 }
 
 template <int MODE, int FMT, int B>
@@ -968,6 +980,23 @@ bool dispatch_gemv_b(const GemvLaunch &L, const GemvPlan &plan, dim3 grid, hipSt
         case 32: launch_gemv<MODE, FMT, B, 1, 32, RS32, 1>(L, grid, stream); return true;
         }
         return false;
+    }
+    if constexpr (MODE == 0 && FMT != kF32) {
+        // 8-wave workgroups: half the per-row share of the x split
+        if (plan.waves == 8) {
+            if (plan.ks != 1) return false;
+#define MLH_GEMV_W8(KT_, R_)                                                             \
+            if (plan.kt == KT_ && plan.r == R_) {                                        \
+                if constexpr (R_ * B <= 16) {                                            \
+                    launch_gemv<MODE, FMT, B, KT_, 64, R_, 1, 8>(L, grid, stream);       \
+                    return true;                                                         \
+                }                                                                        \
+            }
+            MLH_GEMV_W8(1, 2) MLH_GEMV_W8(1, 4) MLH_GEMV_W8(2, 1) MLH_GEMV_W8(2, 2)
+            MLH_GEMV_W8(2, 4)
+#undef MLH_GEMV_W8
+            return false;
+        }
     }
 #define MLH_GEMV_CASE(KT_, R_, KS_)                                                      \
     if (plan.kt == KT_ && plan.r == R_ && plan.ks == KS_) {                              \

@@ -35,6 +35,11 @@ struct GemvParams {
     const float *resid = nullptr;  // kEpiResidual: y = resid + result
     long resid_stride = 0;
     int epilogue = kEpiPlain;
+    // optional (q8 / q4): x already split into limb rows (limb_quantise_rows,
+    // same format and width), row stride limb_stride bytes; norm_w is then
+    // already applied
+    const unsigned char *limbs = nullptr;
+    long limb_stride = 0;
 };
 
 int gemv(const GemvParams &p, hipStream_t stream);
