@@ -83,7 +83,7 @@ __device__ void limb_row(const LimbRowsParams &p, int r) {
     }
     unsigned char *out = p.out + (long)r * p.out_stride;
     // every thread of a chunk group takes part in the shuffles of
-    // limb_quantise8, so the loop bound is the workgroup-uniform pass count
+    // limb_quantise, so the loop bound is the workgroup-uniform pass count
     const int npass = (p.I + kLimbPassElems - 1) / kLimbPassElems;
     for (int j = 0; j < npass; ++j) {
         const int e0 = tid * 8 + j * kLimbPassElems;
@@ -97,7 +97,7 @@ __device__ void limb_row(const LimbRowsParams &p, int r) {
 #pragma unroll
             for (int i = 0; i < 8; ++i) v[i] = v[i] * inv_rms * n[i];
         }
-        limb_quantise8<FMT>(v, in, e0, out, p.I, nc);
+        limb_quantise<FMT>(v, in, e0, out, p.I, nc);
     }
 }
 

@@ -338,15 +338,18 @@ __device__ __forceinline__ unsigned pack_i8x4(int a, int b, int c, int d) {
 // at I, lo at 2 I.  q4 limbs are stored per 8 elements as the even-element
 // dword then the odd-element dword (the order the nibble masks produce), each
 // chunk's 32 bytes split in two 16-byte halves held nc * 16 bytes apart so a
-// lane's 16-byte LDS reads are contiguous across lanes.
+// lane's 16-byte LDS reads are contiguous across lanes.  The quantisation step
+// is 1 / rcp(amax / 2^22) (any step works: the stored scale amax / 2^22 is
+// exact and the limbs are clamped).
 template <int FMT>
-__device__ __forceinline__ void limb_quantise8(const float (&v)[8], bool in, int e0,
-                                               unsigned char *row_lds, int I, int nc) {
+__device__ __forceinline__ void limb_quantise(const float (&v)[8], bool in, int e0,
+                                              unsigned char *row_lds, int I, int nc) {
+    constexpr int EPT = 8;
     constexpr int EPC = FmtTraits<FMT>::kElemsPerChunk;
-    constexpr int TPG = EPC / 8;
+    constexpr int TPG = EPC / EPT;
     float m = 0.0f, bad = 0.0f;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
+    for (int i = 0; i < EPT; ++i) {
         m = fmaxf(m, fabsf(v[i]));
         bad = fmaf(v[i], 0.0f, bad);  // NaN when some element is not finite
     }
@@ -355,57 +358,68 @@ __device__ __forceinline__ void limb_quantise8(const float (&v)[8], bool in, int
         m = fmaxf(m, __shfl_xor(m, o, kWave));
         bad += __shfl_xor(bad, o, kWave);
     }
-    const float inv = m > 0.0f ? (float)kLimbQuantMax / m : 0.0f;
-    int h[8], md[8], l[8], hs = 0, ms = 0;
+    // rows with amax below 1e-30 (where the step would overflow) quantise to 0
+    const float inv = m > 1e-30f ? (float)kLimbQuantMax * __builtin_amdgcn_rcpf(m) : 0.0f;
+    // q = 65536 hi + 256 mid + lo with hi in [-64, 64], mid and lo in
+    // [-128, 127] is the base-256 form of U = q + 128 (65536 + 256 + 1):
+    // U < 2^24 is exact in fp32 and the limbs are its bytes, each XOR 0x80
+    // (the byte minus 128 in two's complement).
+    unsigned U[EPT];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
+    for (int i = 0; i < EPT; ++i) {
         float q = rintf(v[i] * inv);
         q = fminf(fmaxf(q, -(float)kLimbQuantMax), (float)kLimbQuantMax);
-        const int qi = (int)q;
-        // floor divisions with offsets that keep every limb in int8:
-        // hi in [-64, 64], rem in [-32896, 32639], mid and lo in [-128, 127]
-        h[i] = (qi + 32896) >> 16;
-        const int rem = qi - h[i] * 65536;
-        md[i] = (rem + 128) >> 8;
-        l[i] = rem - md[i] * 256;
-        hs += h[i];
-        ms += rem;
+        U[i] = (unsigned)(q + 8421504.0f);
     }
-    unsigned H[2], M[2], L[2];
-    if constexpr (FMT == kQ4) {
-        H[0] = pack_i8x4(h[0], h[2], h[4], h[6]);
-        H[1] = pack_i8x4(h[1], h[3], h[5], h[7]);
-        M[0] = pack_i8x4(md[0], md[2], md[4], md[6]);
-        M[1] = pack_i8x4(md[1], md[3], md[5], md[7]);
-        L[0] = pack_i8x4(l[0], l[2], l[4], l[6]);
-        L[1] = pack_i8x4(l[1], l[3], l[5], l[7]);
-    } else {
-        H[0] = pack_i8x4(h[0], h[1], h[2], h[3]);
-        H[1] = pack_i8x4(h[4], h[5], h[6], h[7]);
-        M[0] = pack_i8x4(md[0], md[1], md[2], md[3]);
-        M[1] = pack_i8x4(md[4], md[5], md[6], md[7]);
-        L[0] = pack_i8x4(l[0], l[1], l[2], l[3]);
-        L[1] = pack_i8x4(l[4], l[5], l[6], l[7]);
-    }
+    // byte k of a, b, c, d (in that order) as one signed-limb dword
+    auto gather = [](unsigned a, unsigned b, unsigned c, unsigned d, int k) -> unsigned {
+        const unsigned lo = __builtin_amdgcn_perm(b, a, (unsigned)(k | ((4 + k) << 8)) | 0x0c0c0000u);
+        const unsigned hi = __builtin_amdgcn_perm(d, c, 0x00000c0cu | (unsigned)((k << 16) | ((4 + k) << 24)));
+        return (lo | hi) ^ 0x80808080u;
+    };
+    constexpr int ND = EPT / 4;  // limb dwords per limb
+    unsigned H[ND], M[ND], L[ND];
 #pragma unroll
-    for (int o = 1; o < TPG; o <<= 1) {
-        hs += __shfl_xor(hs, o, kWave);
-        ms += __shfl_xor(ms, o, kWave);
+    for (int d = 0; d < ND; ++d) {
+        // q8: elements 4d .. 4d + 3; q4: dword 0 the even, dword 1 the odd
+        // elements
+        int e[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) e[j] = FMT == kQ4 ? 2 * j + d : 4 * d + j;
+        H[d] = gather(U[e[0]], U[e[1]], U[e[2]], U[e[3]], 2);
+        M[d] = gather(U[e[0]], U[e[1]], U[e[2]], U[e[3]], 1);
+        L[d] = gather(U[e[0]], U[e[1]], U[e[2]], U[e[3]], 0);
     }
-    if (!in) return;
-    const int c = e0 / EPC, g = (e0 % EPC) / 8;
-    const int off = (FMT == kQ4 ? (g >> 1) * 16 * nc : 0) + 16 * c + 8 * (g & 1);
-    typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
-    *reinterpret_cast<u32x2 *>(row_lds + off) = u32x2{H[0], H[1]};
-    *reinterpret_cast<u32x2 *>(row_lds + I + off) = u32x2{M[0], M[1]};
-    *reinterpret_cast<u32x2 *>(row_lds + 2 * I + off) = u32x2{L[0], L[1]};
-    if (g == 0) {
-        LimbInfo info;
-        info.scale = m / (float)kLimbQuantMax + bad;
-        info.bias_hi = FMT == kQ4 ? 8 * hs : 0;
-        info.bias_low = FMT == kQ4 ? 8 * ms : 0;
-        info.pad = 0;
-        reinterpret_cast<LimbInfo *>(row_lds + 3 * I)[c] = info;
+    // q4 bias terms: sum of hi and of 256 mid + lo over the chunk
+    int hs = 0, ms = 0;
+    if constexpr (FMT == kQ4) {
+#pragma unroll
+        for (int d = 0; d < ND; ++d) {
+            hs = sdot4((int)H[d], 0x01010101, hs);
+            ms += 256 * sdot4((int)M[d], 0x01010101, 0) + sdot4((int)L[d], 0x01010101, 0);
+        }
+#pragma unroll
+        for (int o = 1; o < TPG; o <<= 1) {
+            hs += __shfl_xor(hs, o, kWave);
+            ms += __shfl_xor(ms, o, kWave);
+        }
+    }
+    const int c = e0 / EPC, within = e0 % EPC;
+    if (in) {
+        const int g = within / 8;
+        const int off = (FMT == kQ4 ? (g >> 1) * 16 * nc : 0) + 16 * c + 8 * (g & 1);
+        typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+        *reinterpret_cast<u32x2 *>(row_lds + off) = u32x2{H[0], H[1]};
+        *reinterpret_cast<u32x2 *>(row_lds + I + off) = u32x2{M[0], M[1]};
+        *reinterpret_cast<u32x2 *>(row_lds + 2 * I + off) = u32x2{L[0], L[1]};
+        if (within == 0) {
+            LimbInfo info;
+            info.scale = m / (float)kLimbQuantMax + bad;
+            info.bias_hi = FMT == kQ4 ? 8 * hs : 0;
+            info.bias_low = FMT == kQ4 ? 8 * ms : 0;
+            info.pad = 0;
+            reinterpret_cast<LimbInfo *>(row_lds + 3 * I)[c] = info;
+        }
     }
 }
 
@@ -470,7 +484,9 @@ __device__ __forceinline__ void limb_block(const GemvJob<B> job, unsigned char *
     constexpr int GPW = kWave / LPR;
     constexpr int NV = R * B;
     constexpr int NJP = limb_pre_passes<FMT, B, KT, KS, W>();
-    constexpr int PASS = W * kWave * 8;  // x elements split per workgroup pass
+    constexpr int EPT = 8;                 // x elements per thread per pass
+    constexpr int XV = EPT / 4;            // float4 loads per thread per pass and row
+    constexpr int PASS = W * kWave * EPT;  // x elements split per workgroup pass
     static_assert(NV <= LPR, "partial sums exceed the lane group");
     static_assert(KS == 1 || (LPR == kWave && KS == W), "k-split needs whole-wave row groups");
     __shared__ float red[W][NV];
@@ -515,23 +531,23 @@ __device__ __forceinline__ void limb_block(const GemvJob<B> job, unsigned char *
         }
     }
     // ---- 1. x (and norm_w) of the first passes
-    f32x4 xv[NJP][B][2];
-    f32x4 nv[NJP][2];
+    f32x4 xv[NJP][B][XV];
+    f32x4 nv[NJP][XV];
 #pragma unroll
     for (int j = 0; j < NJP; ++j) {
         if (!presplit && j < npass) {
-            const int e0 = tid * 8 + j * PASS;
+            const int e0 = tid * EPT + j * PASS;
             const int ec = e0 < I ? e0 : 0;
 #pragma unroll
             for (int b = 0; b < B; ++b) {
                 if (b < job.rows) {  // uniform: absent token rows cost nothing
-                    xv[j][b][0] = load_f4(job.x[b] + ec);
-                    xv[j][b][1] = load_f4(job.x[b] + ec + 4);
+#pragma unroll
+                    for (int h = 0; h < XV; ++h) xv[j][b][h] = load_f4(job.x[b] + ec + 4 * h);
                 }
             }
             if (job.norm_w) {
-                nv[j][0] = load_f4(job.norm_w + ec);
-                nv[j][1] = load_f4(job.norm_w + ec + 4);
+#pragma unroll
+                for (int h = 0; h < XV; ++h) nv[j][h] = load_f4(job.norm_w + ec + 4 * h);
             }
         }
     }
@@ -605,24 +621,24 @@ __device__ __forceinline__ void limb_block(const GemvJob<B> job, unsigned char *
         for (int b = 0; b < B; ++b) ss[b] = 0.0f;
 #pragma unroll
         for (int j = 0; j < NJP; ++j) {
-            if (j < npass && tid * 8 + j * PASS < I) {
+            if (j < npass && tid * EPT + j * PASS < I) {
 #pragma unroll
                 for (int b = 0; b < B; ++b)
                     if (b < job.rows)
 #pragma unroll
-                    for (int h = 0; h < 2; ++h)
+                    for (int h = 0; h < XV; ++h)
                         ss[b] += xv[j][b][h].x * xv[j][b][h].x + xv[j][b][h].y * xv[j][b][h].y +
                                  xv[j][b][h].z * xv[j][b][h].z + xv[j][b][h].w * xv[j][b][h].w;
             }
         }
         for (int j = NJP; j < npass; ++j) {
-            const int e0 = tid * 8 + j * PASS;
+            const int e0 = tid * EPT + j * PASS;
             if (e0 < I) {
 #pragma unroll
                 for (int b = 0; b < B; ++b)
                     if (b < job.rows)
 #pragma unroll
-                    for (int h = 0; h < 2; ++h) {
+                    for (int h = 0; h < XV; ++h) {
                         const f32x4 t = load_f4(job.x[b] + e0 + 4 * h);
                         ss[b] += t.x * t.x + t.y * t.y + t.z * t.z + t.w * t.w;
                     }
@@ -645,37 +661,48 @@ __device__ __forceinline__ void limb_block(const GemvJob<B> job, unsigned char *
     }
 
     // ---- 5. quantise x into LDS
-    auto quantise_pass = [&](const f32x4 (&xp)[2], const f32x4 (&np)[2], int b, int e0) {
-        float v[8] = {xp[0].x, xp[0].y, xp[0].z, xp[0].w, xp[1].x, xp[1].y, xp[1].z, xp[1].w};
-        if (job.norm_w) {
-            const float n[8] = {np[0].x, np[0].y, np[0].z, np[0].w,
-                                np[1].x, np[1].y, np[1].z, np[1].w};
+    auto quantise_pass = [&](const f32x4 (&xp)[XV], const f32x4 (&np)[XV], int b, int e0) {
+        float v[EPT];
 #pragma unroll
-            for (int i = 0; i < 8; ++i) v[i] = v[i] * inv_rms[b] * n[i];
+        for (int h = 0; h < XV; ++h) {
+            v[4 * h + 0] = xp[h].x;
+            v[4 * h + 1] = xp[h].y;
+            v[4 * h + 2] = xp[h].z;
+            v[4 * h + 3] = xp[h].w;
         }
-        limb_quantise8<FMT>(v, e0 < I && b < job.rows, e0, lds + b * lds_row, I, nc);
+        if (job.norm_w) {
+#pragma unroll
+            for (int h = 0; h < XV; ++h) {
+                v[4 * h + 0] = v[4 * h + 0] * inv_rms[b] * np[h].x;
+                v[4 * h + 1] = v[4 * h + 1] * inv_rms[b] * np[h].y;
+                v[4 * h + 2] = v[4 * h + 2] * inv_rms[b] * np[h].z;
+                v[4 * h + 3] = v[4 * h + 3] * inv_rms[b] * np[h].w;
+            }
+        }
+        limb_quantise<FMT>(v, e0 < I && b < job.rows, e0, lds + b * lds_row, I, nc);
     };
 #pragma unroll
     for (int j = 0; j < NJP; ++j) {
         if (!presplit && j < npass) {
-            const int e0 = tid * 8 + j * PASS;
+            const int e0 = tid * EPT + j * PASS;
 #pragma unroll
             for (int b = 0; b < B; ++b)
                 if (b < job.rows) quantise_pass(xv[j][b], nv[j], b, e0);
         }
     }
     for (int j = presplit ? npass : NJP; j < npass; ++j) {
-        const int e0 = tid * 8 + j * PASS;
+        const int e0 = tid * EPT + j * PASS;
         const int ec = e0 < I ? e0 : 0;
-        f32x4 np[2] = {f32x4{1.f, 1.f, 1.f, 1.f}, f32x4{1.f, 1.f, 1.f, 1.f}};
-        if (job.norm_w) {
-            np[0] = load_f4(job.norm_w + ec);
-            np[1] = load_f4(job.norm_w + ec + 4);
-        }
+        f32x4 np[XV];
+#pragma unroll
+        for (int h = 0; h < XV; ++h)
+            np[h] = job.norm_w ? load_f4(job.norm_w + ec + 4 * h) : f32x4{1.f, 1.f, 1.f, 1.f};
 #pragma unroll
         for (int b = 0; b < B; ++b) {
             if (b < job.rows) {
-                const f32x4 xp[2] = {load_f4(job.x[b] + ec), load_f4(job.x[b] + ec + 4)};
+                f32x4 xp[XV];
+#pragma unroll
+                for (int h = 0; h < XV; ++h) xp[h] = load_f4(job.x[b] + ec + 4 * h);
                 quantise_pass(xp, np, b, e0);
             }
         }
