@@ -22,6 +22,12 @@ struct MatrixRef {
 // layer: caches point at that layer's [context][latent] / [context][rope].
 struct MlaParams {
     int rows = 0, position = 0, heads = 0;
+    // When set, the kernels read the position from this device int instead
+    // of `position` (a captured decode graph replays at every position), and
+    // the attend grid is grid_splits key splits (splits past the causal end
+    // exit at once).
+    const int *position_dev = nullptr;
+    int grid_splits = 0;
     int nope = 0, rope = 0, vdim = 0, latent = 0;
     float eps = 1e-5f, scale = 1.0f;
     const float *query = nullptr;       // [rows][heads * (nope + rope)] (q_proj output)

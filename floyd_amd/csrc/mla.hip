@@ -28,6 +28,12 @@
 
 namespace mlh {
 
+// The attention call's first position: from device memory when the call is
+// part of a replayed graph, else the launch argument.
+__device__ __forceinline__ int mla_position(const MlaParams &p) {
+    return p.position_dev ? *p.position_dev : p.position;
+}
+
 // Eight consecutive dequantised kv_b values w[row, col..col+7] (col % 8 == 0),
 // moonlight_weight_value (moonlight_kernels.metal:202-216) applied per element.
 __device__ __forceinline__ void kvb_load8(const MatrixRef &m, int row, int col, int width,
@@ -68,7 +74,7 @@ __global__ __launch_bounds__(256) void mla_prep_kernel(MlaParams p) {
     const int r = blockIdx.x;
     const int role = blockIdx.y;
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-    const int pos = p.position + r;
+    const int pos = mla_position(p) + r;
     const int hw = p.nope + p.rope;
     const int half = p.rope / 2;
     if (role == 0) {
@@ -191,7 +197,7 @@ __global__ __launch_bounds__(256) void mla_attend_kernel(MlaParams p) {
     const int split = blockIdx.x;
     const int r = blockIdx.y;
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-    const int keys = p.position + r + 1;
+    const int keys = mla_position(p) + r + 1;
     const int k0 = split * KS;
     const int nk = keys - k0 < KS ? keys - k0 : KS;
     const long part = ((long)r * p.max_splits + split) * H;
@@ -332,7 +338,7 @@ __global__ __launch_bounds__(256) void mla_attend_mfma_kernel(MlaParams p) {
     const int r = blockIdx.y;
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const int g = lane >> 4, m16 = lane & 15;
-    const int keys = p.position + r + 1;
+    const int keys = mla_position(p) + r + 1;
     const int k0 = split * KS;
     const int nk = keys - k0 < KS ? keys - k0 : KS;
     const long part = ((long)r * p.max_splits + split) * H;
@@ -487,7 +493,7 @@ __global__ __launch_bounds__(256) void mla_merge_kernel(MlaParams p) {
     __shared__ float part_acc[4][64];
     const int r = blockIdx.x, h = blockIdx.y;
     const int t = threadIdx.x, lane = t & 63, g = t >> 6;
-    const int keys = p.position + r + 1;
+    const int keys = mla_position(p) + r + 1;
     const int ns = (keys + KS - 1) / KS;
     const long base = (long)r * p.max_splits * H + h;
     float m = -INFINITY;
@@ -579,11 +585,14 @@ int mla_attention_core(const MlaParams &p, hipStream_t stream) {
         !p.latent_context || p.position < 0 || p.query_stride < (long)p.heads * (p.nope + p.rope) ||
         p.compressed_stride < p.latent + p.rope ||
         (p.position + p.rows + kMlaKeysPerSplit - 1) / kMlaKeysPerSplit >
-            (p.max_splits < kMlaMaxSplitsInLds ? p.max_splits : kMlaMaxSplitsInLds))
+            (p.max_splits < kMlaMaxSplitsInLds ? p.max_splits : kMlaMaxSplitsInLds) ||
+        (p.grid_splits && (!p.position_dev || p.grid_splits > p.max_splits ||
+                           p.grid_splits > kMlaMaxSplitsInLds)))
         return kErrArgs;
     hipLaunchKernelGGL(mla_prep_kernel, dim3(p.rows, 1 + p.heads * (p.latent / kMlaAbsorbCols)),
                        dim3(256), 0, stream, p);
-    const int splits = (p.position + p.rows + kMlaKeysPerSplit - 1) / kMlaKeysPerSplit;
+    const int splits = p.grid_splits ? p.grid_splits
+                                     : (p.position + p.rows + kMlaKeysPerSplit - 1) / kMlaKeysPerSplit;
     const dim3 grid(splits, p.rows);
     const size_t lds = (size_t)kMlaKeysPerSplit * p.latent * sizeof(float);
     if (p.rope % 4 == 0 && (p.latent + p.rope) % 16 == 0 && p.latent + p.rope <= kAttnDims) {

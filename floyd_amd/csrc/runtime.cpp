@@ -132,9 +132,16 @@ struct MoonlightSession {
     // caller-given expert ids for the MoE test / timing hooks
     int *fixed_ids = nullptr;
     int fixed_rows = 0;
-    // pinned host mirrors
-    int *host_ids = nullptr;
+    // [position, ids...] of the current forward, on the device (pos_dev =
+    // step_dev, ids = step_dev + 1) and in pinned host memory (one copy)
+    int *step_dev = nullptr, *pos_dev = nullptr;
+    int *host_step = nullptr, *host_ids = nullptr;
     int *host_flag = nullptr;
+    // one-row decode step (embed .. lm_head) as a graph: captured on the
+    // second decode of the session, replayed at every later position
+    hipGraphExec_t decode_exec = nullptr;
+    int eager_decodes = 0;
+    bool decode_graph_failed = false, decode_graph_off = false;
     std::vector<int> kv_lengths;
     int last_forward_rows = 0;
     int position = 0;
@@ -764,7 +771,8 @@ bool session_alloc(MoonlightSession *s, T **ptr, size_t elems, char *error, size
 void free_session(MoonlightSession *s) {
     if (!s) return;
     for (void *p : s->allocations) (void)hipFree(p);
-    if (s->host_ids) (void)hipHostFree(s->host_ids);
+    if (s->decode_exec) (void)hipGraphExecDestroy(s->decode_exec);
+    if (s->host_step) (void)hipHostFree(s->host_step);
     if (s->host_flag) (void)hipHostFree(s->host_flag);
     if (s->ev_start) (void)hipEventDestroy(s->ev_start);
     if (s->ev_stop) (void)hipEventDestroy(s->ev_stop);
@@ -870,8 +878,11 @@ int swiglu_rows(MoonlightSession *s, const Matrix &g, const Matrix &u, const flo
 
 // Attention of `layer` for `rows` rows of (already normalised) x at
 // `position`; writes o_proj(ctx) (+ resid) into out.
+// position_dev: the position in device memory (forward); with grid_splits
+// the attend grid is fixed (decode graph capture).
 int attention(MoonlightSession *s, int layer, const float *x, int rows, int position,
-              float *out, const float *norm_w, const float *resid) {
+              float *out, const float *norm_w, const float *resid,
+              const int *position_dev = nullptr, int grid_splits = 0) {
     const ModelConfig &c = s->model->cfg;
     const LayerPlan &lp = s->model->layers[layer];
     const int qw = c.head_count * (c.qk_nope_dim + c.qk_rope_dim);
@@ -896,6 +907,8 @@ int attention(MoonlightSession *s, int layer, const float *x, int rows, int posi
     }
     p.rows = rows;
     p.position = position;
+    p.position_dev = position_dev;
+    p.grid_splits = grid_splits;
     p.heads = c.head_count;
     p.nope = c.qk_nope_dim;
     p.rope = c.qk_rope_dim;
@@ -949,8 +962,10 @@ static bool fused_route_enabled() {
 // parallelism for prefill batches; fewer rows take the GEMV.
 constexpr int kRouterMfmaMinRows = 256;
 
+// fixed: the MoE test / timing hooks take the caller's expert ids when set
+// (moonlight_session_fix_routes); forward passes always route by top-k.
 int route(MoonlightSession *s, int layer, const float *x, int rows, const float *norm_w,
-          int *trace) {
+          int *trace, bool fixed = false) {
     const ModelConfig &c = s->model->cfg;
     const LayerPlan &lp = s->model->layers[layer];
     const bool f32_router = lp.router.fmt == kF32;
@@ -987,7 +1002,7 @@ int route(MoonlightSession *s, int layer, const float *x, int rows, const float 
     r.list_slots = s->list_slots;
     r.list_pos = s->list_pos;
     r.error = s->route_error;
-    r.fixed_ids = s->fixed_rows >= rows ? s->fixed_ids : nullptr;
+    r.fixed_ids = fixed && s->fixed_rows >= rows ? s->fixed_ids : nullptr;
     r.expert_table = lp.expert_table;
     r.tasks = s->expert_tasks;
     r.task_slots = rows * r.top_k < r.experts ? rows * r.top_k : r.experts;
@@ -1105,7 +1120,75 @@ int experts(MoonlightSession *s, int layer, const float *x, int rows, const floa
     return moe_combine(cb, stream_of(s));
 }
 
-// run_tokens_fast (moonlight_metal.m:1892-1986) as one device submission.
+// The kernels of one forward over `count` token rows at `start` (embed,
+// layers, final norm + lm_head), reading the ids and the position uploaded
+// to step_dev.  With `graph` the attend grids are sized for the whole
+// context so the captured launches fit every later position.
+bool enqueue_forward(MoonlightSession *s, int count, int start, float *layer_outputs, bool graph) {
+    MoonlightModel *m = s->model;
+    const ModelConfig &c = m->cfg;
+    hipStream_t st = stream_of(s);
+    const size_t H = (size_t)c.hidden_size;
+    const int grid_splits = graph ? s->max_splits : 0;
+    bool ok = embed_rows(m->embed, s->ids, s->h, count, c.hidden_size, c.vocab_size,
+                         s->route_error, st) == kOk;
+    for (int l = 0; ok && l < c.layer_count; ++l) {
+        const LayerPlan &lp = m->layers[l];
+        ok = attention(s, l, s->h, count, start, s->h, lp.input_norm, s->h, s->pos_dev,
+                       grid_splits) == kOk;
+        if (ok && lp.dense) {
+            ok = swiglu_rows(s, lp.gate, lp.up, s->h, count, c.hidden_size,
+                             c.dense_intermediate_size, s->dense_hidden, lp.post_norm) == kOk &&
+                 gemv_rows(s, lp.down, s->dense_hidden, count, c.dense_intermediate_size,
+                           c.hidden_size, s->h, nullptr, s->h) == kOk;
+        } else if (ok) {
+            int *trace = s->route_trace + (size_t)l * s->options.max_batch * c.experts_per_token;
+            ok = route(s, l, s->h, count, lp.post_norm, trace) == kOk &&
+                 experts(s, l, s->h, count, lp.post_norm, s->h, s->h, nullptr) == kOk;
+        }
+        if (ok && layer_outputs)
+            ok = to_host(s, layer_outputs + (size_t)l * count * H, s->h, (size_t)count * H * 4);
+    }
+    return ok && gemv_rows(s, m->lm_head, s->h + (size_t)(count - 1) * H, 1, c.hidden_size,
+                           c.vocab_size, s->logits, m->final_norm) == kOk;
+}
+
+// Decode steps replay one captured graph unless MLH_DECODE_GRAPH=0 (read
+// once).
+static bool decode_graph_enabled() {
+    static const bool v = [] {
+        const char *env = getenv("MLH_DECODE_GRAPH");
+        return !env || atoi(env) != 0;
+    }();
+    return v;
+}
+
+// Captures the one-row decode kernels into s->decode_exec.  The capture runs
+// nothing; a failure leaves the session on the eager path.
+bool capture_decode(MoonlightSession *s, int start) {
+    hipStream_t st = stream_of(s);
+    if (hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal) != hipSuccess) return false;
+    const bool ok = enqueue_forward(s, 1, start, nullptr, true);
+    hipGraph_t graph = nullptr;
+    const bool ended = hipStreamEndCapture(st, &graph) == hipSuccess;
+    hipGraphExec_t exec = nullptr;
+    const bool built = ok && ended && graph &&
+                       hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0) == hipSuccess;
+    if (graph) (void)hipGraphDestroy(graph);
+    (void)hipGetLastError();
+    if (!built) return false;
+    s->decode_exec = exec;
+    return true;
+}
+
+// Drops the captured decode graph (its launches baked in state that changed).
+void drop_decode_graph(MoonlightSession *s) {
+    if (s->decode_exec) (void)hipGraphExecDestroy(s->decode_exec);
+    s->decode_exec = nullptr;
+}
+
+// run_tokens_fast (moonlight_metal.m:1892-1986) as one device submission: a
+// graph replay for one-row decode steps, else the launches in stream order.
 int forward(MoonlightSession *s, const int *ids, int count, int start, float *last_logits,
             float *layer_outputs, char *error, size_t error_size) {
     MoonlightModel *m = s->model;
@@ -1126,35 +1209,25 @@ int forward(MoonlightSession *s, const int *ids, int count, int start, float *la
                              "Moonlight fast sparse attention failed at layer %d", l);
     }
     hipStream_t st = stream_of(s);
+    s->host_step[0] = start;
     memcpy(s->host_ids, ids, (size_t)count * sizeof(int));
-    const size_t H = (size_t)c.hidden_size;
+    const bool decode = count == 1 && !layer_outputs && decode_graph_enabled() &&
+                        !s->decode_graph_off && !s->decode_graph_failed;
+    // the first decode runs eagerly (lazy per-kernel set-up happens outside
+    // any capture); the second captures
+    if (decode && !s->decode_exec && s->eager_decodes >= 1 && !capture_decode(s, start))
+        s->decode_graph_failed = true;
     bool ok = hipEventRecord(s->ev_start, st) == hipSuccess &&
-              to_device(s, s->ids, s->host_ids, (size_t)count * sizeof(int)) &&
-              embed_rows(m->embed, s->ids, s->h, count, c.hidden_size, c.vocab_size,
-                         s->route_error, st) == kOk;
-    for (int l = 0; ok && l < c.layer_count; ++l) {
-        const LayerPlan &lp = m->layers[l];
-        ok = attention(s, l, s->h, count, start, s->h, lp.input_norm, s->h) == kOk;
-        if (ok && lp.dense) {
-            ok = swiglu_rows(s, lp.gate, lp.up, s->h, count, c.hidden_size,
-                             c.dense_intermediate_size, s->dense_hidden, lp.post_norm) == kOk &&
-                 gemv_rows(s, lp.down, s->dense_hidden, count, c.dense_intermediate_size,
-                           c.hidden_size, s->h, nullptr, s->h) == kOk;
-        } else if (ok) {
-            int *trace = s->route_trace + (size_t)l * s->options.max_batch * c.experts_per_token;
-            ok = route(s, l, s->h, count, lp.post_norm, trace) == kOk &&
-                 experts(s, l, s->h, count, lp.post_norm, s->h, s->h, nullptr) == kOk;
-        }
-        if (ok && layer_outputs)
-            ok = to_host(s, layer_outputs + (size_t)l * count * H, s->h, (size_t)count * H * 4);
-        if (ok) s->kv_lengths[l] = start + count;
+              to_device(s, s->step_dev, s->host_step, (size_t)(count + 1) * sizeof(int));
+    if (ok && decode && s->decode_exec) {
+        ok = hipGraphLaunch(s->decode_exec, st) == hipSuccess;
+    } else if (ok) {
+        ok = enqueue_forward(s, count, start, layer_outputs, false);
+        if (decode) s->eager_decodes++;
     }
-    if (ok)
-        ok = gemv_rows(s, m->lm_head, s->h + (size_t)(count - 1) * H, 1, c.hidden_size,
-                       c.vocab_size, s->logits, m->final_norm) == kOk &&
-             hipEventRecord(s->ev_stop, st) == hipSuccess &&
-             to_host(s, last_logits, s->logits, (size_t)c.vocab_size * sizeof(float)) &&
-             to_host(s, s->host_flag, s->route_error, sizeof(int));
+    ok = ok && hipEventRecord(s->ev_stop, st) == hipSuccess &&
+         to_host(s, last_logits, s->logits, (size_t)c.vocab_size * sizeof(float)) &&
+         to_host(s, s->host_flag, s->route_error, sizeof(int));
     if (!finish(s) || !ok) {
         // the device state of a partial forward is unusable: invalidate the caches
         for (int l = 0; l < c.layer_count; ++l)
@@ -1162,6 +1235,7 @@ int forward(MoonlightSession *s, const int *ids, int count, int start, float *la
         return set_error(error, error_size, "Moonlight forward failed on the device: %s",
                          hipGetErrorString(hipGetLastError()));
     }
+    for (int l = 0; l < c.layer_count; ++l) s->kv_lengths[l] = start + count;
     if (*s->host_flag) return set_error(error, error_size, "Moonlight fast route table failed");
     float ms = 0.0f;
     if (hipEventElapsedTime(&ms, s->ev_start, s->ev_stop) == hipSuccess) s->last_device_ms = ms;
@@ -1214,7 +1288,8 @@ extern "C" int moonlight_session_create(MoonlightSession **out, MoonlightModel *
         session_alloc(s, &s->tmp, mb * H, error, error_size) &&
         session_alloc(s, &s->latent_kv, lat_elems, error, error_size) &&
         session_alloc(s, &s->rope_kv, rope_elems, error, error_size) &&
-        session_alloc(s, &s->ids, mb, error, error_size) &&
+        session_alloc(s, &s->step_dev, mb + 1, error, error_size) &&
+        (s->pos_dev = s->step_dev, s->ids = s->step_dev + 1, true) &&
         session_alloc(s, &s->logits, logit_elems, error, error_size) &&
         session_alloc(s, &s->query,
                       mb * (heads * (c.qk_nope_dim + c.qk_rope_dim) + c.kv_lora_rank +
@@ -1262,8 +1337,9 @@ extern "C" int moonlight_session_create(MoonlightSession **out, MoonlightModel *
                       mb * (size_t)(c.dense_intermediate_size > 0 ? c.dense_intermediate_size : 1),
                       error, error_size) &&
         session_alloc(s, &s->fixed_ids, mb * K, error, error_size) &&
-        hipHostMalloc((void **)&s->host_ids, mb * sizeof(int), hipHostMallocDefault) ==
+        hipHostMalloc((void **)&s->host_step, (mb + 1) * sizeof(int), hipHostMallocDefault) ==
             hipSuccess &&
+        (s->host_ids = s->host_step + 1, true) &&
         hipHostMalloc((void **)&s->host_flag, sizeof(int), hipHostMallocDefault) == hipSuccess &&
         hipEventCreate(&s->ev_start) == hipSuccess && hipEventCreate(&s->ev_stop) == hipSuccess;
     bool gemm_ok = ok;
@@ -1487,7 +1563,7 @@ extern "C" int moonlight_test_moe(MoonlightSession *s, int layer, const float *i
     // submission 1: router + top-k (+ device route tables)
     bool ok = to_device(s, s->tmp, input, hidden_bytes) &&
               hipMemsetAsync(s->route_error, 0, sizeof(int), st) == hipSuccess &&
-              route(s, layer, s->tmp, rows, nullptr, nullptr) == kOk &&
+              route(s, layer, s->tmp, rows, nullptr, nullptr, true) == kOk &&
               to_host(s, s->host_flag, s->route_error, sizeof(int));
     if (!finish(s) || !ok || *s->host_flag) return 0;
     // submission 2: experts, shared expert, routed + shared (no residual)
@@ -1575,7 +1651,7 @@ extern "C" int moonlight_session_time_moe(MoonlightSession *s, int layer, int ro
     if (fill_normal(s->tmp, (int64_t)rows * c.hidden_size, seed, 0.0f, 1.0f, 0, st) != kOk)
         return 0;
     auto pass = [&]() {
-        return route(s, layer, s->tmp, rows, lp.post_norm, nullptr) == kOk &&
+        return route(s, layer, s->tmp, rows, lp.post_norm, nullptr, true) == kOk &&
                experts(s, layer, s->tmp, rows, lp.post_norm, s->tmp, s->h, nullptr) == kOk;
     };
     bool ok = hipMemsetAsync(s->route_error, 0, sizeof(int), st) == hipSuccess;
@@ -1618,6 +1694,17 @@ extern "C" int moonlight_session_fix_routes(MoonlightSession *s, const int *expe
         return 0;
     s->fixed_rows = rows;
     return 1;
+}
+
+extern "C" int moonlight_session_decode_graph(MoonlightSession *s, int enable) {
+    if (!s) return 0;
+    if (enable == 0) {
+        s->decode_graph_off = true;
+        drop_decode_graph(s);
+    } else if (enable > 0) {
+        s->decode_graph_off = false;
+    }
+    return s->decode_exec ? 1 : 0;
 }
 
 extern "C" int moonlight_session_device_time(MoonlightSession *s, double *ms) {

@@ -85,6 +85,7 @@ SIGNATURES = {
     "moonlight_model_tensor_info": (C.c_int, [_vp, _cp, _vp, _vp, _vp]),
     "moonlight_session_fill_kv": (C.c_int, [_vp, C.c_int, C.c_int, C.c_uint64]),
     "moonlight_session_device_time": (C.c_int, [_vp, C.POINTER(C.c_double)]),
+    "moonlight_session_decode_graph": (C.c_int, [_vp, C.c_int]),
     "moonlight_session_fix_routes": (C.c_int, [_vp, _vp, C.c_int]),
     "moonlight_session_time_moe": (C.c_int, [_vp, C.c_int, C.c_int, C.c_uint64, C.c_int,
                                              C.c_int, C.POINTER(C.c_double),
@@ -252,6 +253,12 @@ class Session:
         v = C.c_double()
         lib().moonlight_session_device_time(self.handle, C.byref(v))
         return v.value
+
+    def decode_graph(self, enable=None):
+        """Switches the decode-step graph on / off (None: query); returns
+        whether decode steps replay a captured graph."""
+        return bool(lib().moonlight_session_decode_graph(
+            self.handle, -1 if enable is None else int(bool(enable))))
 
     def fill_kv(self, length, seed, layer=-1):
         if not lib().moonlight_session_fill_kv(self.handle, layer, length, seed):

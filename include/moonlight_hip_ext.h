@@ -94,6 +94,15 @@ int moonlight_session_fix_routes(MoonlightSession *session,
  * prefill / append / decode of the session. */
 int moonlight_session_device_time(MoonlightSession *session, double *ms);
 
+/* One-row decode steps run as one graph replay (captured on the session's
+ * second decode; the attention kernels read the position from device memory
+ * so the same launches serve every position).  enable = 0 turns this off for
+ * the session (every decode launches its kernels in stream order, and a
+ * captured graph is dropped), 1 turns it back on, < 0 only queries.  Returns
+ * 1 when decode steps replay a captured graph, else 0.  No counterpart in
+ * the reference (its decode encodes every layer each step). */
+int moonlight_session_decode_graph(MoonlightSession *session, int enable);
+
 #ifdef __cplusplus
 }
 #endif

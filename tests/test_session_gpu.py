@@ -245,3 +245,42 @@ def test_runtime(tiny):
         sess.prefill(np.zeros(33, np.int32))
     sess.close()
     orc.close()
+
+
+def test_decode_graph(tiny):
+    """One-row decode steps replay a captured graph from the second decode on;
+    its logits equal the stream-ordered launches bit for bit at every
+    position, also after a reset, and match the oracle."""
+    cfg, tensors, model = tiny
+    rng = np.random.default_rng(11)
+    ids = rng.integers(0, cfg["vocab_size"], 9).astype(np.int32)
+    eager = S.Session(model, 64, 32)
+    graph = S.Session(model, 64, 32)
+    assert not eager.decode_graph(False)
+    orc = CU.oracle_model(cfg, tensors, 64)
+    for rnd in range(2):
+        print(f"[gpu] decode graph vs eager, pass {rnd}", flush=True)
+        eager.reset()
+        graph.reset()
+        prompt = ids[: 5 + 2 * rnd]
+        eager.prefill(prompt)
+        graph.prefill(prompt)
+        token = int(ids[-1])
+        seq = list(prompt)
+        for step in range(6):
+            a = eager.decode(token)
+            b = graph.decode(token)
+            assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), (rnd, step)
+            seq.append(token)
+            token = int(np.argmax(a))
+        assert graph.decode_graph() and not eager.decode_graph()
+        assert graph.position() == len(seq)
+        O.lib().orc_model_reset(orc.handle)
+        _, _, e_last = oracle_forward(orc, cfg, seq, 0)
+        assert rel_l2(b, e_last) < 1e-3
+        assert int(np.argmax(b)) == int(np.argmax(e_last))
+    st = graph.stats()
+    assert st["cpu_fallbacks"] == 0 and st["decode_tokens"] == 6
+    eager.close()
+    graph.close()
+    orc.close()
