@@ -8,7 +8,6 @@ namespace mlh {
 constexpr int kMlaMaxHeads = 16;        // Moonlight: 16 heads
 constexpr int kMlaKeysPerSplit = 32;    // keys per workgroup in mla_attend
 constexpr int kMlaMaxLatent = 512;      // kv_lora_rank limit (moonlight_metal.m:1041)
-constexpr int kMlaMaxSplitsInLds = 1024;
 
 // A weight matrix in one of the container formats (f32 / int8 / packed int4)
 // with its per-row scales.

@@ -17,10 +17,9 @@
 //   mla_attend  (key split of kMlaKeysPerSplit keys, row): every latent row
 //               read once scores ALL heads (the reference re-reads the cache
 //               per head); per split a local max / exp-sum and the partial
-//               latent context of every head (the split's latent rows are
-//               re-read from L2 for the context pass).
-//   mla_merge   (row, head, 128-wide latent chunk): log-sum-exp merge of the
-//               splits into lc_h.
+//               latent context of every head, from the split's rows in LDS.
+//   mla_merge   (row, head, 32-wide latent chunk): one-pass log-sum-exp
+//               merge of the splits into lc_h.
 //   mla_value   (row, head, 32 value rows): ctx_h = W_UV_h lc_h.
 #include "mla.h"
 
@@ -307,111 +306,126 @@ __global__ __launch_bounds__(256) void mla_attend_kernel(MlaParams p) {
 // (v_mfma_f32_16x16x4_f32: fp32 products and sums, like the VALU form, in
 // another order).  Operand layout (measured on gfx950): lane l supplies
 // A[l % 16][l / 16] and B[l / 16][l % 16]; result register i of lane l is
-// D[4 (l / 16) + i][l % 16].  Four MFMAs consume one 16-byte LDS read per
-// operand: in step j lane group g = l / 16 takes k index 4 g + j.
+// D[4 (l / 16) + i][l % 16].  Four MFMAs consume one 16-byte operand read:
+// in step j lane group g = l / 16 takes k index 4 g + j.
 //   scores  S[key][head] = [lat | rope][key] . [qa | q_rope][head] over the
-//           latent + rope dims; the 4 waves split those dims and meet in LDS
-//           (sums in wave order).
-//   context LC[head][d] = sum_key P[head][key] lat[key][d]; the 4 waves split
-//           the 16-wide d tiles.
-// Rows in LDS hold latent + rope zero-padded to a multiple of 16, stride
-// kAttnRowStride floats (16-byte aligned, bank-spread).
+//           latent + rope dims; the 4 compute waves split those dims (each
+//           holds its query slices in registers, read once from L2) and meet
+//           in LDS (sums in wave order).
+//   context LC[head][d] = sum_key P[head][key] lat[key][d]; the 4 compute
+//           waves split the 16-wide d tiles.
+// 512 threads: waves 4..7 only share the DMA of the split's key rows into
+// LDS (the load is per-CU issue bound), then leave.  LDS holds the key rows
+// (latent + rope, stride kAttnRowStride floats: 16-byte aligned,
+// bank-spread) and P; the cross-wave score partials reuse the rope columns
+// once every wave is done with them.  76.5 KB: two workgroups per CU.
 constexpr int kAttnDims = kMlaMaxLatent + 64;       // latent + rope
 constexpr int kAttnRowStride = kAttnDims + 4;       // floats
 constexpr int kAttnPStride = kMlaKeysPerSplit + 4;  // floats, P[head][key]
 constexpr size_t kAttnMfmaLds =
-    sizeof(float) * ((size_t)(kMlaKeysPerSplit + kMlaMaxHeads) * kAttnRowStride +
-                     4 * kMlaKeysPerSplit * kMlaMaxHeads + kMlaMaxHeads * kAttnPStride);
+    sizeof(float) * ((size_t)kMlaKeysPerSplit * kAttnRowStride + kMlaMaxHeads * kAttnPStride);
+static_assert(4 * kMlaKeysPerSplit * kMlaMaxHeads <= kMlaKeysPerSplit * 64,
+              "score partials fit the rope columns");
 
 typedef float f32x4v __attribute__((ext_vector_type(4)));
 
-__global__ __launch_bounds__(256) void mla_attend_mfma_kernel(MlaParams p) {
+__global__ __launch_bounds__(512) void mla_attend_mfma_kernel(MlaParams p) {
     constexpr int H = kMlaMaxHeads;
     constexpr int KS = kMlaKeysPerSplit;
+    constexpr int NJ = kAttnDims / 64;  // 16-dim steps per compute wave
     extern __shared__ __attribute__((aligned(16))) float attn_lds[];
-    float *lat_s = attn_lds;                        // [KS][stride]
-    float *q_s = lat_s + KS * kAttnRowStride;       // [H][stride]
-    float *sc_s = q_s + H * kAttnRowStride;         // [4 waves][KS][H]
-    float *p_s = sc_s + 4 * KS * H;                 // [H][KS + 4]
+    float *lat_s = attn_lds;                   // [KS][stride]
+    float *p_s = lat_s + KS * kAttnRowStride;  // [H][KS + 4]
     __shared__ float smax[H], ssum[H];
     const int split = blockIdx.x;
     const int r = blockIdx.y;
-    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int t = threadIdx.x & 255, lane = t & 63, wave = t >> 6;
+    const bool loader = threadIdx.x >= 256;  // waves 4..7: DMA only
     const int g = lane >> 4, m16 = lane & 15;
     const int keys = mla_position(p) + r + 1;
     const int k0 = split * KS;
     const int nk = keys - k0 < KS ? keys - k0 : KS;
     const long part = ((long)r * p.max_splits + split) * H;
     if (nk <= 0) {
-        if (t < H) {
+        if (threadIdx.x < H) {
             p.part_max[part + t] = -INFINITY;
             p.part_sum[part + t] = 0.0f;
         }
         return;
     }
     const int D = p.latent, R = p.rope;
-    const int KD = (D + R + 15) & ~15;  // padded dims
-    const int c4n = KD / 4;
-    // ---- latent + rope rows of the split, and the head queries, into LDS by
-    // DMA (global_load_lds: 16 bytes per lane into M0 + 16 * lane): a 512-wide
-    // latent row is 2 KB = two wave transfers, a rope row one partial one.
-    // Keys past the causal end and absent heads copy a valid row (finite
-    // values; their probabilities are 0 / their outputs unused).
-    {
-        const int nrows = KS + H;
-        for (int row = wave; row < nrows; row += 4) {
-            const float *lsrc, *rsrc;
-            if (row < KS) {
-                const long k = k0 + (row < nk ? row : nk - 1);
-                lsrc = p.latent_cache + k * D;
-                rsrc = p.rope_cache + k * R;
-            } else {
-                const int h = row - KS;
-                const long qh = (long)r * p.heads + (h < p.heads ? h : 0);
-                lsrc = p.query_absorbed + qh * D;
-                rsrc = p.query_rope + qh * R;
-            }
-            __attribute__((address_space(3))) float *dst =
-                (__attribute__((address_space(3))) float *)(lat_s + row * kAttnRowStride);
-            for (int c0 = 0; c0 < D; c0 += 256) {  // 64 lanes x 4 floats
-                if (c0 + 4 * lane < D)
-                    __builtin_amdgcn_global_load_lds(
-                        (const __attribute__((address_space(1))) void *)(lsrc + c0 + 4 * lane),
-                        dst + c0, 16, 0, 0);
-            }
-            if (4 * lane < R)
-                __builtin_amdgcn_global_load_lds(
-                    (const __attribute__((address_space(1))) void *)(rsrc + 4 * lane), dst + D, 16,
-                    0, 0);
-        }
-        __builtin_amdgcn_s_waitcnt(0);  // this wave's transfers have landed
-    }
-    __syncthreads();
-    // ---- scores: wave w takes the 16-dim steps w, w + 4, ...
-    {
-        // two accumulators per key tile (even / odd MFMA of a step) keep two
-        // independent chains in flight
-        f32x4v acc[KS / 16][2];
+    const int KD = D + R;  // a multiple of 16 (launch condition)
+    // ---- this compute wave's query slices: dims wave * 16 + 64 j + 4 g ..
+    // + 3 of head m16 (absent heads read head 0; their outputs are unused)
+    f32x4 qv[NJ];
+    if (!loader) {
+        const long qh = (long)r * p.heads + (m16 < p.heads ? m16 : 0);
+        const float *qa = p.query_absorbed + qh * D;
+        const float *qr = p.query_rope + qh * R;
 #pragma unroll
-        for (int kt = 0; kt < KS / 16; ++kt) acc[kt][0] = acc[kt][1] = f32x4v{0.f, 0.f, 0.f, 0.f};
-        for (int d0 = wave * 16; d0 < KD; d0 += 64) {
-            const f32x4 qv = *reinterpret_cast<const f32x4 *>(q_s + m16 * kAttnRowStride + d0 + 4 * g);
+        for (int j = 0; j < NJ; ++j) {
+            const int d = wave * 16 + 64 * j + 4 * g;
+            if (d < KD) qv[j] = d < D ? load_f4(qa + d) : load_f4(qr + (d - D));
+        }
+    }
+    // ---- the split's latent + rope rows into LDS by DMA (global_load_lds:
+    // 16 bytes per lane into M0 + 16 * lane), 8 waves on rows w, w + 8, ...;
+    // keys past the causal end copy the last valid row (finite values, zero
+    // probability)
+    for (int row = threadIdx.x >> 6; row < KS; row += 8) {
+        const long k = k0 + (row < nk ? row : nk - 1);
+        const float *lsrc = p.latent_cache + k * D;
+        const float *rsrc = p.rope_cache + k * R;
+        __attribute__((address_space(3))) float *dst =
+            (__attribute__((address_space(3))) float *)(lat_s + row * kAttnRowStride);
+        for (int c0 = 0; c0 < D; c0 += 256) {  // 64 lanes x 4 floats
+            if (c0 + 4 * lane < D)
+                __builtin_amdgcn_global_load_lds(
+                    (const __attribute__((address_space(1))) void *)(lsrc + c0 + 4 * lane),
+                    dst + c0, 16, 0, 0);
+        }
+        if (4 * lane < R)
+            __builtin_amdgcn_global_load_lds(
+                (const __attribute__((address_space(1))) void *)(rsrc + 4 * lane), dst + D, 16, 0,
+                0);
+    }
+    __builtin_amdgcn_s_waitcnt(0);  // this wave's transfers have landed
+    __syncthreads();
+    if (loader) {  // the three barriers the compute waves still pass, then done
+        __syncthreads();
+        __syncthreads();
+        __syncthreads();
+        return;
+    }
+    // ---- scores: compute wave w takes the 16-dim steps w, w + 4, ...; two
+    // accumulators per key tile keep two independent chains in flight
+    f32x4v acc[KS / 16][2];
+#pragma unroll
+    for (int kt = 0; kt < KS / 16; ++kt) acc[kt][0] = acc[kt][1] = f32x4v{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+        const int d0 = wave * 16 + 64 * j;
+        if (d0 < KD) {
 #pragma unroll
             for (int kt = 0; kt < KS / 16; ++kt) {
                 const f32x4 av = *reinterpret_cast<const f32x4 *>(
                     lat_s + (16 * kt + m16) * kAttnRowStride + d0 + 4 * g);
-                acc[kt][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(av.x, qv.x, acc[kt][0], 0, 0, 0);
-                acc[kt][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(av.y, qv.y, acc[kt][1], 0, 0, 0);
-                acc[kt][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(av.z, qv.z, acc[kt][0], 0, 0, 0);
-                acc[kt][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(av.w, qv.w, acc[kt][1], 0, 0, 0);
+                acc[kt][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(av.x, qv[j].x, acc[kt][0], 0, 0, 0);
+                acc[kt][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(av.y, qv[j].y, acc[kt][1], 0, 0, 0);
+                acc[kt][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(av.z, qv[j].z, acc[kt][0], 0, 0, 0);
+                acc[kt][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(av.w, qv[j].w, acc[kt][1], 0, 0, 0);
             }
         }
-#pragma unroll
-        for (int kt = 0; kt < KS / 16; ++kt)
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-                sc_s[(wave * KS + 16 * kt + 4 * g + i) * H + m16] = acc[kt][0][i] + acc[kt][1][i];
     }
+    __syncthreads();  // every wave is done with the rope columns
+    // score partial (wave, key j, head h) at i = (wave * KS + j) * H + h, in
+    // row i / 64, column D + i % 64 (the rope part; D + 64 <= the row stride)
+    auto sc_at = [&](int i) -> float & { return lat_s[(i >> 6) * kAttnRowStride + D + (i & 63)]; };
+#pragma unroll
+    for (int kt = 0; kt < KS / 16; ++kt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            sc_at((wave * KS + 16 * kt + 4 * g + i) * H + m16) = acc[kt][0][i] + acc[kt][1][i];
     __syncthreads();
     // ---- local softmax statistics: 16 lanes per head, keys sub, sub + 16
     {
@@ -421,8 +435,8 @@ __global__ __launch_bounds__(256) void mla_attend_mfma_kernel(MlaParams p) {
 #pragma unroll
         for (int u = 0; u < KS / 16; ++u) {
             const int j = sub + 16 * u;
-            const float sum = (sc_s[(0 * KS + j) * H + h] + sc_s[(1 * KS + j) * H + h]) +
-                              (sc_s[(2 * KS + j) * H + h] + sc_s[(3 * KS + j) * H + h]);
+            const float sum = (sc_at((0 * KS + j) * H + h) + sc_at((1 * KS + j) * H + h)) +
+                              (sc_at((2 * KS + j) * H + h) + sc_at((3 * KS + j) * H + h));
             sv[u] = j < nk ? sum * p.scale : -INFINITY;
             mx = fmaxf(mx, sv[u]);
         }
@@ -448,7 +462,7 @@ __global__ __launch_bounds__(256) void mla_attend_mfma_kernel(MlaParams p) {
         p.part_max[part + t] = smax[t];
         p.part_sum[part + t] = ssum[t];
     }
-    // ---- context: wave w takes the 16-wide d tiles w, w + 4, ...
+    // ---- context: compute wave w takes the 16-wide d tiles w, w + 4, ...
     // (P rows are read once per pair of tiles; the two tiles' chains interleave)
     f32x4 pv[KS / 16];
 #pragma unroll
@@ -456,7 +470,7 @@ __global__ __launch_bounds__(256) void mla_attend_mfma_kernel(MlaParams p) {
         pv[u] = *reinterpret_cast<const f32x4 *>(p_s + m16 * kAttnPStride + 16 * u + 4 * g);
     for (int dt = wave; dt < D / 16; dt += 8) {
         const bool two = dt + 4 < D / 16;
-        f32x4v acc[2] = {f32x4v{0.f, 0.f, 0.f, 0.f}, f32x4v{0.f, 0.f, 0.f, 0.f}};
+        f32x4v cacc[2] = {f32x4v{0.f, 0.f, 0.f, 0.f}, f32x4v{0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
         for (int u = 0; u < KS / 16; ++u) {
             const float *lb = lat_s + (16 * u + 4 * g) * kAttnRowStride + dt * 16 + m16;
@@ -464,76 +478,89 @@ __global__ __launch_bounds__(256) void mla_attend_mfma_kernel(MlaParams p) {
             const float pj[4] = {pv[u].x, pv[u].y, pv[u].z, pv[u].w};
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                acc[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(pj[j], lb[j * kAttnRowStride], acc[0],
-                                                             0, 0, 0);
-                acc[1] = __builtin_amdgcn_mfma_f32_16x16x4f32(pj[j], lb2[j * kAttnRowStride],
-                                                             acc[1], 0, 0, 0);
+                cacc[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(pj[j], lb[j * kAttnRowStride],
+                                                              cacc[0], 0, 0, 0);
+                cacc[1] = __builtin_amdgcn_mfma_f32_16x16x4f32(pj[j], lb2[j * kAttnRowStride],
+                                                              cacc[1], 0, 0, 0);
             }
         }
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int h = 4 * g + i;
             if (h < p.heads) {
-                p.part_lc[(part + h) * D + dt * 16 + m16] = acc[0][i];
-                if (two) p.part_lc[(part + h) * D + (dt + 4) * 16 + m16] = acc[1][i];
+                p.part_lc[(part + h) * D + dt * 16 + m16] = cacc[0][i];
+                if (two) p.part_lc[(part + h) * D + (dt + 4) * 16 + m16] = cacc[1][i];
             }
         }
     }
 }
 
-// lc_h = sum_s e^{m_s - M} lc_s / sum_s e^{m_s - M} l_s over the key splits.
-// Workgroup (row, head, 64 latent dims): 4 thread groups take the splits
-// g, g + 4, ... (loads in batches of 8 before their FMAs) and meet in LDS in
-// group order.
-__global__ __launch_bounds__(256) void mla_merge_kernel(MlaParams p) {
+// lc_h = sum_s e^{m_s - M} lc_s / sum_s e^{m_s - M} l_s over the key splits,
+// in one pass.  Workgroup (row, head, kMergeDims latent dims), 8 waves; a
+// wave's lanes form 64 / kMergeDims groups, so 16 lane groups take the splits
+// g, g + 16, ... with a running max (rescaling on a new max), loading
+// kMergeBatch splits before using them; the groups meet in LDS.
+constexpr int kMergeDims = 32;
+constexpr int kMergeBatch = 8;
+__global__ __launch_bounds__(512) void mla_merge_kernel(MlaParams p) {
     constexpr int H = kMlaMaxHeads;
     constexpr int KS = kMlaKeysPerSplit;
-    __shared__ float weight[kMlaMaxSplitsInLds];
-    __shared__ float red[4];
-    __shared__ float part_acc[4][64];
+    constexpr int DL = kMergeDims, NB = kMergeBatch;
+    constexpr int NG = 8 * (64 / DL);  // lane groups
+    __shared__ float gm[NG], gl[NG];
+    __shared__ float gacc[NG][DL];
     const int r = blockIdx.x, h = blockIdx.y;
-    const int t = threadIdx.x, lane = t & 63, g = t >> 6;
+    const int t = threadIdx.x, lane = t & 63;
+    const int dl = lane % DL, grp = (t >> 6) * (64 / DL) + lane / DL;
     const int keys = mla_position(p) + r + 1;
     const int ns = (keys + KS - 1) / KS;
     const long base = (long)r * p.max_splits * H + h;
-    float m = -INFINITY;
-    for (int s = t; s < ns; s += blockDim.x) m = fmaxf(m, p.part_max[base + (long)s * H]);
-    m = wave_max(m);
-    if (lane == 0) red[g] = m;
-    __syncthreads();
-    m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-    __syncthreads();
-    float l = 0.0f;
-    for (int s = t; s < ns; s += blockDim.x) {
-        const float w = expf(p.part_max[base + (long)s * H] - m);
-        weight[s] = w;
-        l += w * p.part_sum[base + (long)s * H];
-    }
-    l = wave_sum(l);
-    if (lane == 0) red[g] = l;
-    __syncthreads();
-    const float inv = 1.0f / ((red[0] + red[1]) + (red[2] + red[3]));
-    const int d = blockIdx.z * 64 + lane;
-    float acc = 0.0f;
-    if (d < p.latent) {
-        for (int s0 = g; s0 < ns; s0 += 4 * 8) {
-            float v[8];
+    const float *lc = p.part_lc + base * p.latent + blockIdx.z * DL + dl;
+    const long lc_step = (long)H * p.latent;
+    float M = -INFINITY, L = 0.0f, acc = 0.0f;
+    for (int s0 = grp; s0 < ns; s0 += NG * NB) {
+        float mv[NB], lv[NB], v[NB];
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const int s = s0 + 4 * i;
-                v[i] = s < ns ? p.part_lc[(base + (long)s * H) * p.latent + d] : 0.0f;
-            }
-#pragma unroll
-            for (int i = 0; i < 8; ++i)
-                if (s0 + 4 * i < ns) acc = fmaf(weight[s0 + 4 * i], v[i], acc);
+        for (int i = 0; i < NB; ++i) {
+            const int s = s0 + NG * i < ns ? s0 + NG * i : s0;  // clamped: loaded, unused
+            mv[i] = p.part_max[base + (long)s * H];
+            lv[i] = p.part_sum[base + (long)s * H];
+            v[i] = lc[(long)s * lc_step];
         }
+        float mn = M;
+#pragma unroll
+        for (int i = 0; i < NB; ++i)
+            if (s0 + NG * i < ns) mn = fmaxf(mn, mv[i]);
+        const float sc = expf(M - mn);  // 0 while M is -inf
+        acc *= sc;
+        L *= sc;
+#pragma unroll
+        for (int i = 0; i < NB; ++i) {
+            if (s0 + NG * i < ns) {
+                const float e = expf(mv[i] - mn);
+                acc = fmaf(e, v[i], acc);
+                L = fmaf(e, lv[i], L);
+            }
+        }
+        M = mn;
     }
-    part_acc[g][lane] = acc;
+    if (dl == 0) {
+        gm[grp] = M;
+        gl[grp] = L;
+    }
+    gacc[grp][dl] = acc;
     __syncthreads();
-    if (g == 0 && d < p.latent)
-        p.latent_context[((long)r * p.heads + h) * p.latent + d] =
-            ((part_acc[0][lane] + part_acc[1][lane]) + (part_acc[2][lane] + part_acc[3][lane])) *
-            inv;
+    if (t < DL) {
+        float mt = gm[0];  // group 0 holds split 0: finite
+        for (int i = 1; i < NG; ++i) mt = fmaxf(mt, gm[i]);
+        float a = 0.0f, l = 0.0f;
+        for (int i = 0; i < NG; ++i) {
+            const float e = gm[i] == -INFINITY ? 0.0f : expf(gm[i] - mt);
+            a = fmaf(e, gacc[i][t], a);
+            l = fmaf(e, gl[i], l);
+        }
+        p.latent_context[((long)r * p.heads + h) * p.latent + blockIdx.z * DL + t] = a / l;
+    }
 }
 
 // ctx_h[v] = W_UV_h[v, :] . lc_h: one wave per 8 value rows, lanes over
@@ -584,10 +611,8 @@ int mla_attention_core(const MlaParams &p, hipStream_t stream) {
         p.nope <= 0 || p.nope > 256 || p.vdim <= 0 || p.rows <= 0 || p.max_splits <= 0 ||
         !p.latent_context || p.position < 0 || p.query_stride < (long)p.heads * (p.nope + p.rope) ||
         p.compressed_stride < p.latent + p.rope ||
-        (p.position + p.rows + kMlaKeysPerSplit - 1) / kMlaKeysPerSplit >
-            (p.max_splits < kMlaMaxSplitsInLds ? p.max_splits : kMlaMaxSplitsInLds) ||
-        (p.grid_splits && (!p.position_dev || p.grid_splits > p.max_splits ||
-                           p.grid_splits > kMlaMaxSplitsInLds)))
+        (p.position + p.rows + kMlaKeysPerSplit - 1) / kMlaKeysPerSplit > p.max_splits ||
+        (p.grid_splits && (!p.position_dev || p.grid_splits > p.max_splits)))
         return kErrArgs;
     hipLaunchKernelGGL(mla_prep_kernel, dim3(p.rows, 1 + p.heads * (p.latent / kMlaAbsorbCols)),
                        dim3(256), 0, stream, p);
@@ -600,7 +625,7 @@ int mla_attention_core(const MlaParams &p, hipStream_t stream) {
             reinterpret_cast<const void *>(&mla_attend_mfma_kernel),
             hipFuncAttributeMaxDynamicSharedMemorySize, (int)kAttnMfmaLds) == hipSuccess;
         (void)attr;
-        hipLaunchKernelGGL(mla_attend_mfma_kernel, grid, dim3(256), kAttnMfmaLds, stream, p);
+        hipLaunchKernelGGL(mla_attend_mfma_kernel, grid, dim3(512), kAttnMfmaLds, stream, p);
     } else {
         switch (p.latent / 64) {
         case 1: launch_attend<1>(grid, lds, stream, p); break;
@@ -610,7 +635,7 @@ int mla_attention_core(const MlaParams &p, hipStream_t stream) {
         default: return kErrArgs;
         }
     }
-    hipLaunchKernelGGL(mla_merge_kernel, dim3(p.rows, p.heads, (p.latent + 63) / 64), dim3(256),
+    hipLaunchKernelGGL(mla_merge_kernel, dim3(p.rows, p.heads, p.latent / kMergeDims), dim3(512),
                        0, stream, p);
     hipLaunchKernelGGL(mla_value_kernel, dim3(p.rows, p.heads, (p.vdim + 31) / 32), dim3(256), 0,
                        stream, p);
