@@ -790,6 +790,31 @@ struct ExpertTask {
     int count, offset;
 };
 
+// Sigmoid top-k + route tables for `rows` token rows (one workgroup).
+struct RouteParams {
+    const float *logits = nullptr;  // [rows, experts] router logits
+    const float *bias = nullptr;    // [experts] e_score_correction_bias (selection only)
+    int rows = 0, experts = 0, top_k = 0, normalize = 1;
+    float routed_scale = 1.0f;
+    int *ids = nullptr;        // [rows, top_k] selection order
+    float *weights = nullptr;  // [rows, top_k] finalised weights
+    int *trace = nullptr;      // optional copy of ids (per-layer route trace)
+    int *n_unique = nullptr;   // [1]
+    int *unique = nullptr;     // [experts] active experts, first-appearance order
+    int *counts = nullptr;     // [experts] entries per expert
+    int *offsets = nullptr;    // [experts] start of each expert's compact list
+    int *list_rows = nullptr;  // [rows*top_k] token row per list entry
+    int *list_slots = nullptr; // [rows*top_k] slot per list entry
+    int *list_pos = nullptr;   // [rows*top_k] list entry of (row, slot), -1 if invalid
+    int *error = nullptr;      // [1] set to 1 when an id is out of range
+    // optional [rows, top_k] expert ids given by the caller: weights come from
+    // their scores (moe_route_fixed, moe_route.h:76-87) instead of a top-k
+    const int *fixed_ids = nullptr;
+    // optional: the per-task table of the grouped expert launches
+    const ExpertWeights *expert_table = nullptr;  // device [experts]
+    ExpertTask *tasks = nullptr;                  // out [task_slots]
+    int task_slots = 0;
+};
 struct ExpertGemvParams {
     int stage = 0;  // 0: gate/up + SwiGLU, 1: down
     const ExpertWeights *experts = nullptr;  // device table [E]
@@ -817,7 +842,18 @@ struct ExpertGemvParams {
     // stage 1 by list entry; the shared expert's rows in sh_limbs
     const unsigned char *limbs = nullptr, *sh_limbs = nullptr;
     long limb_stride = 0, sh_limb_stride = 0;
+    // stage 0 of a one-row batch with at most 64 experts: when route.logits
+    // is set, every routed workgroup selects its expert from the router
+    // logits itself (the route tables, which stage 1 and the combine read,
+    // are written by workgroup 0), so no routing launch precedes stage 0
+    RouteParams route;
 };
+
+}  // namespace mlh
+
+#include "route_impl.h"
+
+namespace mlh {
 
 struct GemvLaunch {
     GemvParams plain;
@@ -887,7 +923,15 @@ __global__ __launch_bounds__(W * 64) void gemv_kernel(GemvLaunch L) {
             job.I = p.stage == 0 ? p.hidden : p.shared_width;
         } else {
             ExpertWeights ew;
-            if (p.tasks) {
+            if (p.route.logits) {
+                // one token row: the tables for the later launches, then this
+                // workgroup's own selection (every wave, no barrier)
+                if (blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x < 64)
+                    route_single_64(p.route, threadIdx.x);
+                if (inline_task_expert(p.route, task, &ew) < 0) return;
+                n = 1;
+                off = task;
+            } else if (p.tasks) {
                 const ExpertTask tk = p.tasks[task];
                 if (tk.count == 0) return;
                 n = tk.count;
@@ -900,7 +944,7 @@ __global__ __launch_bounds__(W * 64) void gemv_kernel(GemvLaunch L) {
                 off = p.offsets[e];
                 ew = p.experts[e];
             }
-            list = p.rows + off;
+            list = p.route.logits ? nullptr : p.rows + off;  // inline: token row 0
             job.w = p.stage == 0 ? ew.gate : ew.down;
             job.s = p.stage == 0 ? ew.gate_s : ew.down_s;
             job.w2 = ew.up;
@@ -919,7 +963,7 @@ __global__ __launch_bounds__(W * 64) void gemv_kernel(GemvLaunch L) {
 #pragma unroll
             for (int b = 0; b < B; ++b) {
                 const int j = g0 + (b < job.rows ? b : 0);  // list entry
-                const int token = shared ? j : list[j];
+                const int token = shared || !list ? j : list[j];
                 if (p.stage == 0) {
                     job.x[b] = p.x + (long)token * p.hidden;
                     job.y[b] = shared ? p.sh_y + (long)j * p.shared_width

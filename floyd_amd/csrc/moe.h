@@ -5,31 +5,8 @@
 
 namespace mlh {
 
-// Sigmoid top-k + route tables for `rows` token rows (one workgroup).
-struct RouteParams {
-    const float *logits = nullptr;  // [rows, experts] router logits
-    const float *bias = nullptr;    // [experts] e_score_correction_bias (selection only)
-    int rows = 0, experts = 0, top_k = 0, normalize = 1;
-    float routed_scale = 1.0f;
-    int *ids = nullptr;        // [rows, top_k] selection order
-    float *weights = nullptr;  // [rows, top_k] finalised weights
-    int *trace = nullptr;      // optional copy of ids (per-layer route trace)
-    int *n_unique = nullptr;   // [1]
-    int *unique = nullptr;     // [experts] active experts, first-appearance order
-    int *counts = nullptr;     // [experts] entries per expert
-    int *offsets = nullptr;    // [experts] start of each expert's compact list
-    int *list_rows = nullptr;  // [rows*top_k] token row per list entry
-    int *list_slots = nullptr; // [rows*top_k] slot per list entry
-    int *list_pos = nullptr;   // [rows*top_k] list entry of (row, slot), -1 if invalid
-    int *error = nullptr;      // [1] set to 1 when an id is out of range
-    // optional [rows, top_k] expert ids given by the caller: weights come from
-    // their scores (moe_route_fixed, moe_route.h:76-87) instead of a top-k
-    const int *fixed_ids = nullptr;
-    // optional: the per-task table of the grouped expert launches
-    const ExpertWeights *expert_table = nullptr;  // device [experts]
-    ExpertTask *tasks = nullptr;                  // out [task_slots]
-    int task_slots = 0;
-};
+// Sigmoid top-k + route tables for `rows` token rows (one workgroup); the
+// RouteParams type is shared with the grouped expert launches (gemv_impl.h).
 int route_topk(const RouteParams &p, hipStream_t stream);
 
 // Router matvec (f32 router [experts][width], x RMSNorm'ed with norm_w) and
@@ -59,6 +36,10 @@ int moe_combine(const CombineParams &p, hipStream_t stream);
 struct ExpertFfnParams {
     int rows = 0, experts = 0, top_k = 0, hidden = 0, inter = 0, shared_width = 0;
     int expert_fmt = kQ8, shared_fmt = kQ8, has_shared = 1;
+    // one token row, at most 64 experts: with route.logits set, stage 0
+    // routes inline (see ExpertGemvParams::route) and no routing launch is
+    // needed before expert_ffn
+    RouteParams route;
     const ExpertWeights *expert_table = nullptr;  // device [experts]
     const uint8_t *shared_gate = nullptr, *shared_up = nullptr, *shared_down = nullptr;
     const float *shared_gate_s = nullptr, *shared_up_s = nullptr, *shared_down_s = nullptr;

@@ -18,16 +18,6 @@
 
 namespace mlh {
 
-// Router score 1 / (1 + e^-x) (moe_route.h:12-14) with e^-x correctly
-// rounded to f32: exp is evaluated in double and rounded once.  Host glibc
-// expf, which the reference's CPU twin calls, misrounds ~0.06 % of inputs by
-// one ulp; a selection can only change where two selection scores tie within
-// that ulp.
-__device__ __forceinline__ float sigmoid_exact(float logit) {
-    const float e = (float)exp(-(double)logit);
-    return 1.0f / (1.0f + e);
-}
-
 constexpr int kMaxExperts = 256;
 constexpr int kMaxTopK = 16;
 constexpr int kRouteLdsIds = 4096;
@@ -123,112 +113,6 @@ __device__ void route_row(const RouteParams &p, int r, int lane, int *lds_ids) {
         p.weights[(long)r * K + lane] = my_w / wsum * p.routed_scale;
         if (p.trace) p.trace[(long)r * K + lane] = my_id;
     }
-}
-
-// Field-wise store of a task entry (a struct copy would go through scratch).
-__device__ __forceinline__ void store_task(ExpertTask *t, const ExpertWeights &w, int count,
-                                           int offset) {
-    t->w.gate = w.gate;
-    t->w.up = w.up;
-    t->w.down = w.down;
-    t->w.gate_s = w.gate_s;
-    t->w.up_s = w.up_s;
-    t->w.down_s = w.down_s;
-    t->count = count;
-    t->offset = offset;
-}
-
-// Routing of token row r with at most 64 experts (one per lane) by one wave,
-// with no serial arg-max chain.  The top-k selection is a rank: expert e is
-// taken in slot rank(e) = #{o : sel_o > sel_e or (sel_o == sel_e and o < e)}
-// when rank(e) < top_k, which is the order the repeated arg-max of
-// moe_route.h:59-71 produces (larger first, lower index on ties).  Only
-// experts with sel > -inf can be taken (NaN never compares greater), as in
-// the arg-max.  Writes ids / weights / trace (and lds_ids); returns the slot
-// of this lane's expert (-1: not taken) and the mask of filled slots.
-struct RowSelection {
-    int slot;
-    unsigned long long filled;  // bit k: slot k holds a valid expert
-};
-
-__device__ RowSelection select_row_64(const RouteParams &p, int r, int lane, int *lds_ids) {
-    const int E = p.experts, K = p.top_k;
-    const bool have = lane < E;
-    const float logit = have ? p.logits[(long)r * E + lane] : 0.0f;
-    const float bias = have ? p.bias[lane] : 0.0f;
-    const float score = have ? sigmoid_exact(logit) : 0.0f;
-    const float sel = have ? score + bias : -INFINITY;
-    RowSelection rs{-1, 0ull};
-    if (p.fixed_ids) {
-        for (int k = 0; k < K; ++k)
-            if (p.fixed_ids[(long)r * K + k] == lane) rs.slot = k;
-    } else if (sel > -INFINITY) {
-        const int sel_bits = __float_as_int(sel);
-        int rank = 0;
-#pragma unroll 8
-        for (int o = 0; o < 64; ++o) {
-            const float so = __int_as_float(__builtin_amdgcn_readlane(sel_bits, o));
-            rank += (so > sel) || (so == sel && o < lane);
-        }
-        if (rank < K) rs.slot = rank;
-    }
-    // slot k -> expert; weights summed in slot order (moe_route_finalize)
-    int my_id = -1;
-    float my_w = 0.0f, wsum = 0.0f;
-    for (int k = 0; k < K; ++k) {
-        const unsigned long long m = __ballot(rs.slot == k);
-        const int src = m ? __ffsll((long long)m) - 1 : -1;
-        const float w = src >= 0 ? __int_as_float(__builtin_amdgcn_readlane(__float_as_int(score), src))
-                                 : 0.0f;
-        if (src >= 0) rs.filled |= 1ull << k;
-        if (lane == k) {
-            my_id = src;
-            my_w = w;
-        }
-        wsum += w;
-    }
-    if (p.normalize)
-        wsum += 1e-20f;
-    else
-        wsum = 1.0f;
-    if (lane < K) {
-        p.ids[(long)r * K + lane] = my_id;
-        if (lds_ids) lds_ids[r * K + lane] = my_id;
-        p.weights[(long)r * K + lane] = my_w / wsum * p.routed_scale;
-        if (p.trace) p.trace[(long)r * K + lane] = my_id;
-    }
-    return rs;
-}
-
-// One token row: routing and route tables by a single wave with no barrier.
-// With one row and distinct experts the tables are direct: expert e in slot k
-// is the u-th taken expert (u = k unless a fixed id was invalid), with one
-// list entry at offset u.
-__device__ void route_single_64(const RouteParams &p, int lane) {
-    const int E = p.experts, K = p.top_k;
-    const bool have = lane < E;
-    ExpertWeights ew{};
-    if (p.tasks && have) ew = p.expert_table[lane];  // in flight with the logits
-    const RowSelection rs = select_row_64(p, 0, lane, nullptr);
-    const int slot = rs.slot;
-    if (lane < K && !((rs.filled >> lane) & 1ull)) {
-        p.list_pos[lane] = -1;
-        *p.error = 1;  // prepare_route_tables rejects such ids (moonlight_metal.m:545)
-    }
-    const int n_unique = __popcll(rs.filled);
-    if (lane == 0) *p.n_unique = n_unique;
-    if (have) p.counts[lane] = slot >= 0 ? 1 : 0;
-    if (slot >= 0) {
-        const int u = __popcll(rs.filled & ((1ull << slot) - 1ull));
-        p.offsets[lane] = u;
-        p.unique[u] = lane;
-        p.list_rows[u] = 0;
-        p.list_slots[u] = slot;
-        p.list_pos[slot] = u;
-        if (p.tasks) store_task(p.tasks + u, ew, 1, u);
-    }
-    if (p.tasks && lane >= n_unique && lane < p.task_slots)
-        store_task(p.tasks + lane, ExpertWeights{}, 0, 0);
 }
 
 // Any expert count: the rank form for up to 64 experts, else the arg-max scan.
@@ -862,6 +746,11 @@ int expert_ffn(const ExpertFfnParams &f, hipStream_t stream) {
     const int max_rows = f.rows;  // token rows any task can hold
     const bool presplit = f.limb_x != nullptr;
     const bool fused_fmt = f.expert_fmt == f.shared_fmt;
+    if (f.route.logits &&
+        (f.rows != 1 || f.route.rows != 1 || f.route.experts > 64 || f.route.experts < 1 ||
+         f.route.top_k < 1 || f.route.top_k > f.route.experts || presplit || !f.route.tasks ||
+         !f.route.expert_table))
+        return kErrArgs;
     for (int stage = 0; stage < 2; ++stage) {
         if (presplit) {
             // the stage's inputs, split once: token rows (RMSNorm'ed) for
@@ -911,6 +800,7 @@ int expert_ffn(const ExpertFfnParams &f, hipStream_t stream) {
             e.sh_limb_stride = stage == 0 ? f.limb_x_stride : f.limb_sh_stride;
         }
         e.stage = stage;
+        if (stage == 0) e.route = f.route;  // stage 1 reads the tables it wrote
         e.tasks = f.tasks;
         e.experts = f.expert_table;
         e.n_unique = f.n_unique;

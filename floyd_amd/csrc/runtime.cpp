@@ -964,8 +964,22 @@ constexpr int kRouterMfmaMinRows = 256;
 
 // fixed: the MoE test / timing hooks take the caller's expert ids when set
 // (moonlight_session_fix_routes); forward passes always route by top-k.
+// Single-row batches with at most 64 experts route inside the first expert
+// launch unless MLH_INLINE_ROUTE=0 (read once).
+static bool inline_route_enabled() {
+    static const bool v = [] {
+        const char *env = getenv("MLH_INLINE_ROUTE");
+        return !env || atoi(env) != 0;
+    }();
+    return v;
+}
+
+// With `inline_route`, a single-row batch with at most 64 experts gets only
+// its router logits here; the selection and the route tables are left to
+// the first expert launch, which takes *inline_route (route.logits unset
+// when routing ran here).
 int route(MoonlightSession *s, int layer, const float *x, int rows, const float *norm_w,
-          int *trace, bool fixed = false) {
+          int *trace, bool fixed = false, RouteParams *inline_route = nullptr) {
     const ModelConfig &c = s->model->cfg;
     const LayerPlan &lp = s->model->layers[layer];
     const bool f32_router = lp.router.fmt == kF32;
@@ -1009,11 +1023,18 @@ int route(MoonlightSession *s, int layer, const float *x, int rows, const float 
     if (fused)
         return router_route(r, x, norm_w, c.rms_norm_epsilon, router_w, c.hidden_size,
                             s->route_counter, stream_of(s));
+    if (inline_route) *inline_route = RouteParams{};
+    if (inline_route && inline_route_enabled() && rows == 1 && c.expert_count <= 64 &&
+        rows < presplit_min_rows()) {
+        *inline_route = r;
+        return kOk;
+    }
     return route_topk(r, stream_of(s));
 }
 
 int experts(MoonlightSession *s, int layer, const float *x, int rows, const float *norm_w,
-            const float *resid, float *out, float *routed_copy) {
+            const float *resid, float *out, float *routed_copy,
+            const RouteParams *inline_route = nullptr) {
     const ModelConfig &c = s->model->cfg;
     const LayerPlan &lp = s->model->layers[layer];
     ExpertFfnParams f;
@@ -1038,7 +1059,8 @@ int experts(MoonlightSession *s, int layer, const float *x, int rows, const floa
     f.counts = s->counts;
     f.offsets = s->offsets;
     f.list_rows = s->list_rows;
-    f.tasks = s->expert_tasks;  // written by route()
+    f.tasks = s->expert_tasks;  // written by route() (or by stage 0 routing inline)
+    if (inline_route && inline_route->logits) f.route = *inline_route;
     if (rows >= presplit_min_rows() && c.hidden_size % 32 == 0 &&
         c.moe_intermediate_size % 32 == 0) {
         f.limb_x = s->limb_x;
@@ -1143,8 +1165,9 @@ bool enqueue_forward(MoonlightSession *s, int count, int start, float *layer_out
                            c.hidden_size, s->h, nullptr, s->h) == kOk;
         } else if (ok) {
             int *trace = s->route_trace + (size_t)l * s->options.max_batch * c.experts_per_token;
-            ok = route(s, l, s->h, count, lp.post_norm, trace) == kOk &&
-                 experts(s, l, s->h, count, lp.post_norm, s->h, s->h, nullptr) == kOk;
+            RouteParams inline_r;
+            ok = route(s, l, s->h, count, lp.post_norm, trace, false, &inline_r) == kOk &&
+                 experts(s, l, s->h, count, lp.post_norm, s->h, s->h, nullptr, &inline_r) == kOk;
         }
         if (ok && layer_outputs)
             ok = to_host(s, layer_outputs + (size_t)l * count * H, s->h, (size_t)count * H * 4);
@@ -1651,8 +1674,10 @@ extern "C" int moonlight_session_time_moe(MoonlightSession *s, int layer, int ro
     if (fill_normal(s->tmp, (int64_t)rows * c.hidden_size, seed, 0.0f, 1.0f, 0, st) != kOk)
         return 0;
     auto pass = [&]() {
-        return route(s, layer, s->tmp, rows, lp.post_norm, nullptr, true) == kOk &&
-               experts(s, layer, s->tmp, rows, lp.post_norm, s->tmp, s->h, nullptr) == kOk;
+        RouteParams inline_r;
+        return route(s, layer, s->tmp, rows, lp.post_norm, nullptr, true, &inline_r) == kOk &&
+               experts(s, layer, s->tmp, rows, lp.post_norm, s->tmp, s->h, nullptr, &inline_r) ==
+                   kOk;
     };
     bool ok = hipMemsetAsync(s->route_error, 0, sizeof(int), st) == hipSuccess;
     for (int i = 0; ok && i < warmup; ++i) ok = pass();
