@@ -382,203 +382,110 @@ int router_route(const RouteParams &p, const float *x, const float *norm_w, floa
     return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
 }
 
-// Tables of a batch routed by route_select_kernel (ids in memory), one
-// workgroup, rows * top_k <= kRouteFusedMaxPositions.
-__global__ __launch_bounds__(256) void small_tables_kernel(RouteParams p) {
-    __shared__ RouteLds L;
-    const int n_pos = p.rows * p.top_k;
-    for (int q = threadIdx.x; q < n_pos; q += blockDim.x) L.ids[q] = p.ids[q];
-    __syncthreads();
-    small_tables(p, L);
-}
-
-// Larger batches: one wave per token row over many workgroups ...
+// Larger batches: one wave per token row over many workgroups; the tables
+// follow in route_lists_kernel.
 __global__ __launch_bounds__(256) void route_select_kernel(RouteParams p) {
     const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (r < p.rows) route_any(p, r, threadIdx.x & 63, nullptr);
 }
 
-// ... then the tables in one workgroup of 16 waves.  List order within an
-// expert is (row, slot) order, and the experts of one row are distinct (top-k
-// selection; fixed routes are checked on the host), so the list entry of
-// (row r, expert e) is offsets[e] + the number of earlier rows that route to
-// e.  Rows are taken in chunks of 64 (one per lane): a ballot per (chunk,
-// expert) gives the rows of the chunk that use e.  From these masks come the
-// counts (popcounts), the first appearance (first set bit, then the slot in
-// that row), the first-appearance ranks (experts that appear earlier) and,
-// after a scan over the chunks, the list entries -- no atomics and no serial
-// pass over the positions.
-constexpr int kTableWaves = 16;
-constexpr int kTableMasks = 2048;  // (row chunks) x experts held in LDS
-__global__ __launch_bounds__(1024) void route_tables_kernel(RouteParams p) {
-    __shared__ int first_pos[kMaxExperts];
-    __shared__ int counts[kMaxExperts];
-    __shared__ int offsets[kMaxExperts];
-    __shared__ int rank_of[kMaxExperts], count_by_rank[kMaxExperts], offset_by_rank[kMaxExperts];
-    __shared__ unsigned long long row_mask[kTableMasks];  // [chunk][expert of the group]
-    __shared__ int before[kTableMasks];                   // [chunk][expert of the group]
-    __shared__ unsigned char ids8[kRouteMaxPositions];
-    __shared__ unsigned long long bad_mask[kRouteMaxPositions / 64];
-    __shared__ int unique_total;
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int wave = tid >> 6;
-    const int E = p.experts, K = p.top_k, M = p.rows;
-    const int n_pos = M * K;
-    const int nchunks = (M + 63) / 64;
-    const int nwords = (n_pos + 63) / 64;
-    // ids in batches of 16 words per wave (loads issued before their use)
-    for (int w0 = wave; w0 < nwords; w0 += kTableWaves * 16) {
-        int ev[16];
-#pragma unroll
-        for (int b = 0; b < 16; ++b) {
-            const int q = (w0 + kTableWaves * b) * 64 + lane;
-            ev[b] = q < n_pos ? p.ids[q] : 0;
-        }
-#pragma unroll
-        for (int b = 0; b < 16; ++b) {
-            const int w = w0 + kTableWaves * b;
-            if (w >= nwords) break;
-            const int q = w * 64 + lane;
-            bool bad = false;
-            if (q < n_pos) {
-                bad = ev[b] < 0 || ev[b] >= E;
-                ids8[q] = (unsigned char)(bad ? 0 : ev[b]);
-                if (bad) p.list_pos[q] = -1;
-            }
-            const unsigned long long m = __ballot(bad);
-            if (lane == 0) {
-                bad_mask[w] = m;
-                if (m) *p.error = 1;  // prepare_route_tables rejects such ids (moonlight_metal.m:545)
-            }
+// Route tables of a batch of more than a few rows (prepare_route_tables,
+// moonlight_metal.m:525-559) with one workgroup per expert.  Every workgroup
+// histograms all positions (counts and first appearance through LDS atomics,
+// which do not depend on order), so each derives its expert's rank in
+// first-appearance order and its list offset without waiting for another
+// workgroup, then writes its expert's list entries in position order.
+// Workgroup 0 also writes the batch-wide outputs (n_unique, invalid-id marks,
+// the tail of the task table).
+constexpr unsigned short kNoExpert = 0xFFFF;
+__global__ __launch_bounds__(1024) void route_lists_kernel(RouteParams p) {
+    __shared__ int counts[kMaxExperts], first_pos[kMaxExperts];
+    __shared__ unsigned short ids16[kRouteMaxPositions];
+    __shared__ int wave_count[16];
+    __shared__ int s_rank, s_offset, s_unique;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int E = p.experts, K = p.top_k, n_pos = p.rows * p.top_k;
+    const int e = blockIdx.x;
+    for (int i = tid; i < E; i += blockDim.x) {
+        counts[i] = 0;
+        first_pos[i] = INT_MAX;
+    }
+    __syncthreads();
+    for (int q = tid; q < n_pos; q += blockDim.x) {
+        const int id = p.ids[q];
+        const bool ok = id >= 0 && id < E;
+        ids16[q] = ok ? (unsigned short)id : kNoExpert;
+        if (ok) {
+            atomicAdd(&counts[id], 1);
+            atomicMin(&first_pos[id], q);
+        } else if (e == 0) {
+            p.list_pos[q] = -1;
+            *p.error = 1;  // prepare_route_tables rejects such ids (moonlight_metal.m:545)
         }
     }
     __syncthreads();
-    auto id_at = [&](int q) -> int {
-        return ((bad_mask[q >> 6] >> (q & 63)) & 1ull) ? -1 : (int)ids8[q];
-    };
-    // masks of the experts e0 .. e0 + ne - 1 for every row chunk
-    auto build_masks = [&](int e0, int ne) {
-        for (int c = wave; c < nchunks; c += kTableWaves) {
-            const int r = c * 64 + lane;
-            int ids[kMaxTopK];
-#pragma unroll
-            for (int k = 0; k < kMaxTopK; ++k) ids[k] = (k < K && r < M) ? id_at(r * K + k) : -1;
-            for (int ei = 0; ei < ne; ++ei) {
-                bool has = false;
-#pragma unroll
-                for (int k = 0; k < kMaxTopK; ++k) has |= ids[k] == e0 + ei;
-                const unsigned long long m = __ballot(has);
-                if (lane == 0) row_mask[c * ne + ei] = m;
-            }
-        }
-    };
-    const int group = max(1, kTableMasks / nchunks);
-    const bool one_group = group >= E;
-    // ---- counts and first appearance (position index row * K + slot)
-    for (int e0 = 0; e0 < E; e0 += group) {
-        const int ne = min(group, E - e0);
-        __syncthreads();
-        build_masks(e0, ne);
-        __syncthreads();
-        for (int ei = tid; ei < ne; ei += blockDim.x) {
-            int cnt = 0, first = INT_MAX;
-            for (int c = 0; c < nchunks; ++c) {
-                const unsigned long long m = row_mask[c * ne + ei];
-                if (m && first == INT_MAX) {
-                    const int r = c * 64 + __ffsll((long long)m) - 1;
-                    for (int k = 0; k < K; ++k)
-                        if (id_at(r * K + k) == e0 + ei) first = r * K + k;
+    if (wave == 0) {  // rank and offset of e: active experts that appear first
+        const int fe = first_pos[e];
+        int rk = 0, off = 0, nu = 0;
+        for (int i = lane; i < E; i += 64) {
+            const int c = counts[i];
+            if (c > 0) {
+                ++nu;
+                if (first_pos[i] < fe) {
+                    ++rk;
+                    off += c;
                 }
-                cnt += __popcll(m);
             }
-            counts[e0 + ei] = cnt;
-            first_pos[e0 + ei] = first;
+        }
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) {
+            rk += __shfl_xor(rk, o, 64);
+            off += __shfl_xor(off, o, 64);
+            nu += __shfl_xor(nu, o, 64);
+        }
+        if (lane == 0) {
+            s_rank = counts[e] > 0 ? rk : -1;
+            s_offset = off;
+            s_unique = nu;
         }
     }
     __syncthreads();
-    // ---- ranks in first-appearance order
-    for (int e = tid; e < E; e += blockDim.x) {
-        rank_of[e] = -1;
-        if (counts[e] > 0) {
-            int rank = 0;
-            for (int o = 0; o < E; ++o) rank += counts[o] > 0 && first_pos[o] < first_pos[e];
-            rank_of[e] = rank;
-            count_by_rank[rank] = counts[e];
+    const int rank = s_rank, offset = s_offset, n_unique = s_unique;
+    if (tid == 0) {
+        p.counts[e] = counts[e];
+        if (rank >= 0) {
+            p.offsets[e] = offset;
             p.unique[rank] = e;
         }
-        p.counts[e] = counts[e];
+        if (e == 0) *p.n_unique = n_unique;
+        if (p.tasks && rank >= 0 && rank < p.task_slots)
+            store_task(p.tasks + rank, p.expert_table[e], counts[e], offset);
     }
-    if (tid == 0) {
-        int n = 0;
-        for (int e = 0; e < E; ++e) n += counts[e] > 0;
-        unique_total = n;
-        *p.n_unique = n;
-    }
-    __syncthreads();
-    if (wave == 0) {  // exclusive scan of the counts in rank order (<= 256 ranks)
-        int c4[4], local = 0;
-        const int n_unique = unique_total;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int rk = lane * 4 + i;
-            c4[i] = rk < n_unique ? count_by_rank[rk] : 0;
-            local += c4[i];
-        }
-        int incl = local;
-#pragma unroll
-        for (int o = 1; o < 64; o <<= 1) {
-            const int v = __shfl_up(incl, o, 64);
-            if (lane >= o) incl += v;
-        }
-        int run = incl - local;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int rk = lane * 4 + i;
-            if (rk < n_unique) offset_by_rank[rk] = run;
-            run += c4[i];
-        }
-    }
-    __syncthreads();
-    for (int e = tid; e < E; e += blockDim.x) {
-        if (rank_of[e] >= 0) {
-            offsets[e] = offset_by_rank[rank_of[e]];
-            p.offsets[e] = offsets[e];
-        }
-    }
-    __syncthreads();
-    write_tasks(p, counts, offsets, rank_of, unique_total);
-    // ---- list entries
-    for (int e0 = 0; e0 < E; e0 += group) {
-        const int ne = min(group, E - e0);
-        if (!one_group) {
-            __syncthreads();
-            build_masks(e0, ne);
-        }
+    if (p.tasks && e == 0)
+        for (int u = n_unique + tid; u < p.task_slots; u += blockDim.x)
+            store_task(p.tasks + u, ExpertWeights{}, 0, 0);
+    if (rank < 0) return;  // the whole workgroup: no list entries
+    // list entries of e in position order, blockDim.x positions per round
+    int base = offset;
+    for (int q0 = 0; q0 < n_pos; q0 += blockDim.x) {
+        const int q = q0 + tid;
+        const bool mine = q < n_pos && ids16[q] == e;
+        const unsigned long long m = __ballot(mine);
+        if (lane == 0) wave_count[wave] = __popcll(m);
         __syncthreads();
-        for (int ei = tid; ei < ne; ei += blockDim.x) {
-            int run = offsets[e0 + ei];  // list entries before each chunk
-            for (int c = 0; c < nchunks; ++c) {
-                before[c * ne + ei] = run;
-                run += __popcll(row_mask[c * ne + ei]);
-            }
+        int before = base, total = 0;
+        for (int w = 0; w < (int)(blockDim.x >> 6); ++w) {
+            if (w < wave) before += wave_count[w];
+            total += wave_count[w];
         }
-        __syncthreads();
-        for (int c = wave; c < nchunks; c += kTableWaves) {
-            const int r = c * 64 + lane;
-            if (r >= M) continue;
-            const unsigned long long below = (1ull << lane) - 1ull;
-            for (int k = 0; k < K; ++k) {
-                const int q = r * K + k;
-                const int e = id_at(q);
-                if (e < e0 || e >= e0 + ne) continue;
-                const int slot = c * ne + (e - e0);
-                const int j = before[slot] + __popcll(row_mask[slot] & below);
-                p.list_rows[j] = r;
-                p.list_slots[j] = k;
-                p.list_pos[q] = j;
-            }
+        if (mine) {
+            const int j = before + __popcll(m & ((1ull << lane) - 1ull));
+            p.list_rows[j] = q / K;
+            p.list_slots[j] = q % K;
+            p.list_pos[q] = j;
         }
+        base += total;
+        __syncthreads();  // wave_count is rewritten next round
     }
 }
 
@@ -699,10 +606,7 @@ int route_topk(const RouteParams &p, hipStream_t stream) {
         hipLaunchKernelGGL(route_kernel, dim3(1), dim3(256), 0, stream, p);
     } else {
         hipLaunchKernelGGL(route_select_kernel, dim3((p.rows + 3) / 4), dim3(256), 0, stream, p);
-        if (p.rows * p.top_k <= kRouteFusedMaxPositions)
-            hipLaunchKernelGGL(small_tables_kernel, dim3(1), dim3(256), 0, stream, p);
-        else
-            hipLaunchKernelGGL(route_tables_kernel, dim3(1), dim3(1024), 0, stream, p);
+        hipLaunchKernelGGL(route_lists_kernel, dim3(p.experts), dim3(1024), 0, stream, p);
     }
     return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
 }
