@@ -492,105 +492,92 @@ __global__ __launch_bounds__(1024) void route_lists_kernel(RouteParams p) {
 // Router logits for many token rows (prefill): logits[r][e] = RMSNorm(x[r]) .
 // W[e] with an f32 router [experts][width] (moonlight_kernels.metal:43-60, the
 // post-attention norm of :23-41 applied to x), on fp32 MFMA
-// (v_mfma_f32_32x32x2_f32: fp32 products and sums, like the VALU matmul, in
-// another order).  A workgroup owns 32 rows x 32 experts; its 8 waves split k
-// and their partial tiles are summed in wave order through LDS, so the result
-// is deterministic.  Lane l feeds row / expert l % 32 and, per group of 4
-// MFMAs, the 4 consecutive k values (l / 32) * 4 .. + 3 of an 8-wide k step.
-typedef float f32x16 __attribute__((ext_vector_type(16)));
-constexpr int kRouterTile = 32;
-constexpr int kRouterWaves = 8;
-__global__ __launch_bounds__(512) void router_logits_kernel(const float *x, const float *norm_w,
+// (v_mfma_f32_16x16x4_f32: fp32 products and sums, like the VALU matmul, in
+// another order).  The norm's 1 / rms is a per-row factor of the dot product,
+// so one pass accumulates sum_k (x n)[k] w[e][k] and sum_k x[k]^2 together and
+// scales at the end.  A workgroup owns 16 rows x 32 experts (two 16 x 16
+// tiles); its 4 waves take the 16-wide k steps w, w + 4, ... and meet in LDS
+// in wave order (deterministic).  Lane l feeds row / expert l % 16 and, per
+// group of 4 MFMAs, the k values 4 (l / 16) .. + 3 of a 16-wide step; a
+// wave's loads go out kRouterBatch steps ahead of their MFMAs.
+typedef float f32x4v_r __attribute__((ext_vector_type(4)));
+constexpr int kRouterRows = 16, kRouterCols = 32, kRouterBatch = 4;
+__global__ __launch_bounds__(256) void router_logits_kernel(const float *x, const float *norm_w,
                                                             float eps, const float *w, int rows,
                                                             int experts, int width,
                                                             float *logits) {
-    __shared__ float inv_rms[kRouterTile];
-    __shared__ float part[kRouterWaves][kRouterTile * kRouterTile];
+    __shared__ float part[4][2][16][16];  // [wave][tile][row][expert]
+    __shared__ float ssq[4][16];          // [wave][row]
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int r0 = blockIdx.x * kRouterTile, e0 = blockIdx.y * kRouterTile;
-    // sums of squares: the loads of a row are issued in batches of 8 before
-    // they are used (a load-use chain per iteration would serialise latency)
-    for (int rr = wave; rr < kRouterTile; rr += kRouterWaves) {
-        const int r = r0 + rr;
-        float ss = 0.0f;
-        if (norm_w && r < rows) {
-            for (int i0 = lane * 4; i0 < width; i0 += 256 * 8) {
-                f32x4 v[8];
-#pragma unroll
-                for (int b = 0; b < 8; ++b) {
-                    const int i = i0 + 256 * b;
-                    v[b] = i < width ? load_f4(x + (long)r * width + i) : f32x4{0.f, 0.f, 0.f, 0.f};
-                }
-#pragma unroll
-                for (int b = 0; b < 8; ++b)
-                    ss += v[b].x * v[b].x + v[b].y * v[b].y + v[b].z * v[b].z + v[b].w * v[b].w;
-            }
-        }
-        ss = wave_sum(ss);
-        if (lane == 0) inv_rms[rr] = norm_w ? 1.0f / sqrtf(ss / (float)width + eps) : 1.0f;
-    }
-    __syncthreads();
-    const int col = lane & 31, h = lane >> 5;
-    const int row = min(r0 + col, rows - 1);  // rows past the end are never stored
-    const int ex = min(e0 + col, experts - 1);
-    const float rs = inv_rms[col];
-    const int kper = ((width + 8 * kRouterWaves - 1) / (8 * kRouterWaves)) * 8;
-    const int kbeg = wave * kper, kend = min(width, kbeg + kper);
+    const int g = lane >> 4, m16 = lane & 15;
+    const int r0 = blockIdx.x * kRouterRows, e0 = blockIdx.y * kRouterCols;
+    const int row = min(r0 + m16, rows - 1);  // rows / experts past the end are never stored
     const float *xr = x + (long)row * width;
-    const float *wr = w + (long)ex * width;
-    f32x16 acc;
+    const float *wr0 = w + (long)min(e0 + m16, experts - 1) * width;
+    const float *wr1 = w + (long)min(e0 + 16 + m16, experts - 1) * width;
+    f32x4v_r acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
+    float ss = 0.0f;
+    const int steps = width / 16;
+    for (int s0 = wave; s0 < steps; s0 += 4 * kRouterBatch) {
+        f32x4 xv[kRouterBatch], nv[kRouterBatch], w0[kRouterBatch], w1[kRouterBatch];
 #pragma unroll
-    for (int i = 0; i < 16; ++i) acc[i] = 0.0f;
-    // batches of 8 k steps: all loads of a batch are issued before its MFMAs
-    constexpr int kBatch = 8;
-    for (int kb = kbeg + h * 4; kb < kend; kb += 8 * kBatch) {
-        f32x4 xv[kBatch], wv[kBatch], nv[kBatch];
-#pragma unroll
-        for (int b = 0; b < kBatch; ++b) {
-            const int k = kb + 8 * b;
-            const bool ok = k < kend;
-            xv[b] = ok ? load_f4(xr + k) : f32x4{0.f, 0.f, 0.f, 0.f};
-            wv[b] = ok ? load_f4(wr + k) : f32x4{0.f, 0.f, 0.f, 0.f};
-            nv[b] = (ok && norm_w) ? load_f4(norm_w + k) : f32x4{1.f, 1.f, 1.f, 1.f};
+        for (int b = 0; b < kRouterBatch; ++b) {
+            const int st = s0 + 4 * b;
+            const int k = (st < steps ? st : s0) * 16 + 4 * g;  // clamped: loaded, unused
+            xv[b] = load_f4(xr + k);
+            w0[b] = load_f4(wr0 + k);
+            w1[b] = load_f4(wr1 + k);
+            nv[b] = norm_w ? load_f4(norm_w + k) : f32x4{1.f, 1.f, 1.f, 1.f};
         }
 #pragma unroll
-        for (int b = 0; b < kBatch; ++b) {
-            f32x4 x4 = xv[b];
-            if (norm_w) {
-                x4.x = x4.x * rs * nv[b].x;
-                x4.y = x4.y * rs * nv[b].y;
-                x4.z = x4.z * rs * nv[b].z;
-                x4.w = x4.w * rs * nv[b].w;
+        for (int b = 0; b < kRouterBatch; ++b) {
+            if (s0 + 4 * b < steps) {
+                const f32x4 v = xv[b];
+                ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+                const float a[4] = {v.x * nv[b].x, v.y * nv[b].y, v.z * nv[b].z, v.w * nv[b].w};
+                const float b0[4] = {w0[b].x, w0[b].y, w0[b].z, w0[b].w};
+                const float b1[4] = {w1[b].x, w1[b].y, w1[b].z, w1[b].w};
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    acc0 = __builtin_amdgcn_mfma_f32_16x16x4f32(a[j], b0[j], acc0, 0, 0, 0);
+                    acc1 = __builtin_amdgcn_mfma_f32_16x16x4f32(a[j], b1[j], acc1, 0, 0, 0);
+                }
             }
-            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(x4.x, wv[b].x, acc, 0, 0, 0);
-            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(x4.y, wv[b].y, acc, 0, 0, 0);
-            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(x4.z, wv[b].z, acc, 0, 0, 0);
-            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(x4.w, wv[b].w, acc, 0, 0, 0);
         }
     }
+    // the 4 lane groups of a row hold disjoint k: sum them (row m16)
+    ss += __shfl_xor(ss, 16, 64);
+    ss += __shfl_xor(ss, 32, 64);
+    if (g == 0) ssq[wave][m16] = ss;
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-        const int r = (i >> 2) * 8 + h * 4 + (i & 3);
-        part[wave][r * kRouterTile + col] = acc[i];
+    for (int i = 0; i < 4; ++i) {
+        part[wave][0][4 * g + i][m16] = acc0[i];
+        part[wave][1][4 * g + i][m16] = acc1[i];
     }
     __syncthreads();
-    for (int o = tid; o < kRouterTile * kRouterTile; o += blockDim.x) {
-        float v = 0.0f;
-#pragma unroll
-        for (int wv = 0; wv < kRouterWaves; ++wv) v += part[wv][o];
-        const int r = r0 + o / kRouterTile, e = e0 + o % kRouterTile;
-        if (r < rows && e < experts) logits[(long)r * experts + e] = v;
+    for (int o = tid; o < kRouterRows * kRouterCols; o += blockDim.x) {
+        const int rr = o / kRouterCols, c = o % kRouterCols;
+        const int r = r0 + rr, e = e0 + c;
+        if (r >= rows || e >= experts) continue;
+        const int t = c >> 4, ec = c & 15;
+        const float v = (part[0][t][rr][ec] + part[1][t][rr][ec]) +
+                        (part[2][t][rr][ec] + part[3][t][rr][ec]);
+        float inv = 1.0f;
+        if (norm_w) {
+            const float sq = (ssq[0][rr] + ssq[1][rr]) + (ssq[2][rr] + ssq[3][rr]);
+            inv = 1.0f / sqrtf(sq / (float)width + eps);
+        }
+        logits[(long)r * experts + e] = v * inv;
     }
 }
 
 int router_logits(const float *x, const float *norm_w, float eps, const float *w, int rows,
                   int experts, int width, float *logits, hipStream_t stream) {
-    if (!x || !w || !logits || rows <= 0 || experts <= 0 || width <= 0 || width % 8) return kErrArgs;
+    if (!x || !w || !logits || rows <= 0 || experts <= 0 || width <= 0 || width % 16) return kErrArgs;
     hipLaunchKernelGGL(router_logits_kernel,
-                       dim3((rows + kRouterTile - 1) / kRouterTile,
-                            (experts + kRouterTile - 1) / kRouterTile),
-                       dim3(64 * kRouterWaves), 0, stream, x, norm_w, eps, w, rows, experts,
-                       width, logits);
+                       dim3((rows + kRouterRows - 1) / kRouterRows,
+                            (experts + kRouterCols - 1) / kRouterCols),
+                       dim3(256), 0, stream, x, norm_w, eps, w, rows, experts, width, logits);
     return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
 }
 

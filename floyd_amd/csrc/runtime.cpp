@@ -988,7 +988,7 @@ int route(MoonlightSession *s, int layer, const float *x, int rows, const float 
     const bool fused = fused_route_enabled() && f32_router && rows <= kFusedRouteMaxRows &&
                        c.hidden_size % 4 == 0;
     if (!fused) {
-        if (rows >= kRouterMfmaMinRows && f32_router && c.hidden_size % 8 == 0) {
+        if (rows >= kRouterMfmaMinRows && f32_router && c.hidden_size % 16 == 0) {
             if (router_logits(x, norm_w, c.rms_norm_epsilon, router_w, rows, c.expert_count,
                               c.hidden_size, s->router_logits, stream_of(s)))
                 return kErrLaunch;
