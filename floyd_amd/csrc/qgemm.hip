@@ -3,10 +3,10 @@
 //
 // Workgroup: 4 waves in a 2 x 2 arrangement over a 128 (token rows) x 256
 // (weight rows) tile; each wave owns 64 x 128 = 2 x 4 MFMA blocks per limb.
-// Pipeline: two LDS stages; while one k slice is multiplied out of LDS the
-// next is in flight (q8: 128-wide slices copied straight into LDS by
-// global_load_lds; q4: 64-wide slices unpacked in registers on the way), one
-// barrier per slice.  MFMA operand layout (measured on gfx950): lane l supplies row
+// Pipeline: q8 has four LDS stages of 64-wide k slices copied straight into
+// LDS by global_load_lds, three in flight while one is multiplied; q4 has two
+// stages, 64-wide slices unpacked in registers on the way.  One barrier per
+// slice.  MFMA operand layout (measured on gfx950): lane l supplies row
 // (l % 32) and the 16-byte k chunk (l / 32) of a 32-wide k step, for A rows and
 // for B columns alike; result register r of lane l is
 // C[(r / 4) * 8 + (l / 32) * 4 + r % 4][l % 32].
@@ -173,7 +173,7 @@ __host__ __device__ __forceinline__ int tiles_of(int rows, int n_out) {
 // 128-bit access per cycle.
 template <int FMT> struct QgCfg;
 template <> struct QgCfg<kQ8> {
-    static constexpr int kRB = 128, kStages = 2;
+    static constexpr int kRB = 64, kStages = 4;
 };
 template <> struct QgCfg<kQ4> {
     static constexpr int kRB = 64, kStages = 2;
@@ -287,14 +287,13 @@ __global__ __launch_bounds__(256, 1) void qgemm_kernel(QGemmLaunch L) {
         return (limb ? tk.a_lo : tk.a_hi) + (long)arow * tk.a_stride;
     };
 
-    // DMA path (q8, 128-byte rows): wave w issues the 1 KB blocks
-    // blk = w + 4 q, q = 0..7, of A (blocks 0..15: rows (blk % 16) * 8 .. + 8 of
-    // limb blk / 16) and of B (rows blk * 8 .. + 8); lane l fills LDS row
-    // (block row 0 + l / 8), physical chunk l % 8, so it loads the logical
-    // chunk (l % 8) ^ g(row).  Only four distinct A rows per lane exist (both
-    // limbs share them); the B rows follow from q at compile time.
-    const int lr = lane >> 3, lc = lane & 7;
-    unsigned a_off[4] = {0u, 0u, 0u, 0u};  // byte offsets of this lane's A rows
+    // DMA path (q8, 64-byte rows): wave w issues 8 blocks of 1 KB per slice:
+    // A blocks (limb h / 2, rows (w + 4 (h % 2)) * 16 + l / 4) for h = 0..3
+    // and B blocks (rows (w + 4 q) * 16 + l / 4) for q = 0..3; lane l fills LDS
+    // row (block row 0 + l / 4), physical chunk l % 4, so it loads the logical
+    // chunk (l % 4) ^ g(row).  Both limbs share a lane's two A rows.
+    const int lr = lane >> 2, lc = lane & 3;
+    unsigned a_off[2] = {0u, 0u};  // byte offsets of this lane's A rows
     // register path (q4, 64-byte rows): 4 A chunks and 2 packed B chunks
     const int8_t *a_src[4];
     int a_dst[4];
@@ -303,10 +302,10 @@ __global__ __launch_bounds__(256, 1) void qgemm_kernel(QGemmLaunch L) {
     u32x4 ra[4], rb[2];
     if constexpr (kDma) {
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const int r = (wave + 4 * q) * 8 + lr;
+        for (int h = 0; h < 2; ++h) {
+            const int r = (wave + 4 * h) * 16 + lr;
             const int arow = lds_arow[r] >= 0 ? lds_arow[r] : lds_arow[0];
-            a_off[q] = (unsigned)(arow * tk.a_stride);
+            a_off[h] = (unsigned)(arow * tk.a_stride);
         }
     } else {
 #pragma unroll
@@ -325,34 +324,35 @@ __global__ __launch_bounds__(256, 1) void qgemm_kernel(QGemmLaunch L) {
         }
     }
 
-    // one k slice of 128 (or, when k % 128 == 64, a last slice of 64: lanes
-    // whose chunk is 4..7 then re-read chunk - 4, in bounds, unused)
-    auto issue_dma = [&](int k0, int buf, bool half_slice) {
+    // one k slice of 64 into LDS stage buf (8 DMA instructions per wave)
+    auto issue_dma = [&](int k0, int buf) {
         __attribute__((address_space(3))) int8_t *stage =
             (__attribute__((address_space(3))) int8_t *)(qg_lds + buf * kStage);
 #pragma unroll
-        for (int q = 0; q < 8; ++q) {
-            const int blk = wave + 4 * q;
-            const int r = (blk & 15) * 8 + lr;  // A row of this lane
-            int ca = lc ^ ((r ^ (r >> 3)) & 7);
-            if (half_slice && ca >= 4) ca -= 4;
+        for (int h = 0; h < 4; ++h) {
+            const int rb = wave + 4 * (h & 1), limb = h >> 1;
+            const int r = rb * 16 + lr;  // A row of this lane
+            const int ca = lc ^ (((r >> 1) ^ (r >> 3)) & 3);
             // uniform base + 32-bit lane offset: one VGPR per address
-            const int8_t *abase = q >= 4 ? tk.a_lo : tk.a_hi;
-            const unsigned aoff = a_off[q & 3] + (unsigned)(k0 + ca * 16);
+            const int8_t *abase = limb ? tk.a_lo : tk.a_hi;
+            const unsigned aoff = a_off[h & 1] + (unsigned)(k0 + ca * 16);
             __builtin_amdgcn_global_load_lds(
                 (const __attribute__((address_space(1))) void *)(abase + aoff),
-                stage + (q >> 2) * (kQgBM * kRB) + (blk & 15) * 1024, 16, 0, 0);
-            const int j = blk * 8 + lr;  // B row of this lane
+                stage + limb * (kQgBM * kRB) + rb * 1024, 16, 0, 0);
+        }
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int bb = wave + 4 * q;
+            const int j = bb * 16 + lr;  // B row of this lane
             const int f = (j >> 5) & 3;
             const int out = DUAL ? n0 + (j >> 7) * 64 + (f & 1) * 32 + (j & 31) : n0 + j;
             const uint8_t *bbase = (DUAL && f >= 2) ? w_up : w_gate;
-            int cb = lc ^ ((j ^ (j >> 3)) & 7);
-            if (half_slice && cb >= 4) cb -= 4;
+            const int cb = lc ^ (((j >> 1) ^ (j >> 3)) & 3);
             const unsigned boff =
                 (unsigned)((out < tk.n_out ? out : 0) * tk.k) + (unsigned)(k0 + cb * 16);
             __builtin_amdgcn_global_load_lds(
                 (const __attribute__((address_space(1))) void *)(bbase + boff),
-                stage + kLdsA + blk * 1024, 16, 0, 0);
+                stage + kLdsA + bb * 1024, 16, 0, 0);
         }
     };
     auto fetch = [&](int k0) {
@@ -429,24 +429,26 @@ __global__ __launch_bounds__(256, 1) void qgemm_kernel(QGemmLaunch L) {
     };
 
     if constexpr (kDma) {
-        // two buffers: slice ks + 1 streams into LDS while slice ks is
-        // multiplied; the barrier after the wait also frees the other buffer
-        const int nk = (tk.k + kRB - 1) / kRB;
-        issue_dma(0, 0, kRB > tk.k);
+        // four stages: slices ks + 1 .. ks + 3 stream into LDS while slice ks
+        // is multiplied.  A wave's DMA completes in order, 8 instructions per
+        // slice, so slice ks has landed when at most 8 per later slice in
+        // flight remain; the barrier after the wait makes every wave's part
+        // visible and frees the stage of slice ks - 1 for slice ks + 3.
+        const int nk = tk.k / kRB;  // k % 64 == 0 (qgemm_shape_ok)
+        for (int st = 0; st < 3 && st < nk; ++st) issue_dma(st * kRB, st);
         for (int ks = 0; ks < nk; ++ks) {
-            wait_vmcnt<0>();
+            const int later = nk - 1 - ks;
+            if (later >= 2)
+                wait_vmcnt<16>();
+            else if (later == 1)
+                wait_vmcnt<8>();
+            else
+                wait_vmcnt<0>();
             // a bare barrier: __syncthreads() would also wait for the stores
             // and loads of the fence it implies
             __builtin_amdgcn_s_barrier();
-            if (ks + 1 < nk)
-                issue_dma((ks + 1) * kRB, (ks + 1) & 1, (ks + 2) * kRB > tk.k);
-            const int buf = ks & 1;
-            // the two 64-wide halves of the slice run as a loop, not unrolled:
-            // unrolled, the compiler keeps a second set of fragments live and
-            // spills
-            const int pairs = (ks + 1) * kRB <= tk.k ? 2 : 1;
-#pragma unroll 1
-            for (int p = 0; p < pairs; ++p) compute_pair(buf, 2 * p);
+            if (ks + 3 < nk) issue_dma((ks + 3) * kRB, (ks + 3) & 3);
+            compute_pair(ks & 3, 0);
         }
     } else {
         // two buffers: slice ks + 2 is in registers while slice ks is multiplied
