@@ -239,6 +239,25 @@ def cpu_baseline(case, budget_s=10.0):
             "ms_per_step": round(per * 1e3, 4), "parity_rel_l2": err}
 
 
+def decode_only(ctx, tokens):
+    """Greedy decode steps of the synthetic q8 model at context ctx, one line
+    per token (wall and device time): the workload of a decode profile."""
+    from floyd_amd import session as S
+    model = S.Model.synthetic()
+    sess = S.Session(model, ctx + tokens + 8, 1)
+    sess.fill_kv(ctx, seed=ctx)
+    token = 1
+    for i in range(tokens):
+        t1 = time.perf_counter()
+        logits = sess.decode(token)
+        wall = (time.perf_counter() - t1) * 1e3
+        token = int(logits.argmax())
+        print(f"[bench] decode {i}: {wall:.3f} ms wall, {sess.device_time_ms():.3f} ms device",
+              file=sys.stderr, flush=True)
+    sess.close()
+    model.close()
+
+
 def main():
     parser = argparse.ArgumentParser()
     parser.add_argument("--gpus", type=int, default=1)
@@ -251,6 +270,9 @@ def main():
     parser.add_argument("--decode-tokens", type=int, default=20)
     parser.add_argument("--only-headline", action="store_true",
                         help="headline GEMV and the copy yardstick only (profiler runs)")
+    parser.add_argument("--decode-only", type=int, default=0, metavar="CTX",
+                        help="only greedy decode steps of the synthetic model at context "
+                             "CTX, printed per token (profiler runs)")
     args = parser.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: the hot path is single-device "
@@ -261,6 +283,9 @@ def main():
     from floyd_amd import native
     device = native.init()
     print(f"[bench] device {device}", file=sys.stderr, flush=True)
+    if args.decode_only:
+        decode_only(args.decode_only, args.decode_tokens)
+        return
 
     # headline: benchmark config 1, q4 [11264 x 2048], batch 1
     head = GemvCase(native, 2, 11264, 2048, 1, seed=101)

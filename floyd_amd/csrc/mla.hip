@@ -318,12 +318,13 @@ __global__ __launch_bounds__(256) void mla_attend_kernel(MlaParams p) {
 // LDS (the load is per-CU issue bound), then leave.  LDS holds the key rows
 // (latent + rope, stride kAttnRowStride floats: 16-byte aligned,
 // bank-spread) and P; the cross-wave score partials reuse the rope columns
-// once every wave is done with them.  76.5 KB: two workgroups per CU.
+// once every wave is done with them.  77.5 KB: two workgroups per CU.
 constexpr int kAttnDims = kMlaMaxLatent + 64;       // latent + rope
 constexpr int kAttnRowStride = kAttnDims + 4;       // floats
 constexpr int kAttnPStride = kMlaKeysPerSplit + 4;  // floats, P[head][key]
 constexpr size_t kAttnMfmaLds =
-    sizeof(float) * ((size_t)kMlaKeysPerSplit * kAttnRowStride + kMlaMaxHeads * kAttnPStride);
+    sizeof(float) * ((size_t)kMlaKeysPerSplit * kAttnRowStride + kMlaMaxHeads * kAttnPStride) +
+    1024;  // + the prefetch sink
 static_assert(4 * kMlaKeysPerSplit * kMlaMaxHeads <= kMlaKeysPerSplit * 64,
               "score partials fit the rope columns");
 
@@ -391,10 +392,35 @@ __global__ __launch_bounds__(512) void mla_attend_mfma_kernel(MlaParams p) {
     }
     __builtin_amdgcn_s_waitcnt(0);  // this wave's transfers have landed
     __syncthreads();
-    if (loader) {  // the three barriers the compute waves still pass, then done
-        __syncthreads();
-        __syncthreads();
-        __syncthreads();
+    if (loader) {
+        // Prefetch of the value rows of kv_b (W_UV, which mla_value reads two
+        // launches later) into L2 / the last-level cache while the compute
+        // waves work: this split's share, by DMA into a scratch LDS block
+        // nobody reads.  Bare barriers (no wait for the prefetch) match the
+        // three the compute waves still pass; the wait comes before exit.
+        if (r == 0) {
+            const long row_bytes = p.kv_b.fmt == kF32   ? (long)D * 4
+                                   : p.kv_b.fmt == kQ4 ? (long)(D + 1) / 2
+                                                        : (long)D;
+            const long per_head = (long)p.vdim * row_bytes;  // contiguous value rows
+            const long total = (long)p.heads * per_head;
+            const long share = ((total + gridDim.x - 1) / gridDim.x + 15) & ~15L;
+            const long begin = (long)split * share;
+            const long end = begin + share < total ? begin + share : total;
+            __attribute__((address_space(3))) void *sink =
+                (__attribute__((address_space(3))) void *)(p_s + H * kAttnPStride);
+            for (long o = begin + 16L * t; o + 16 <= end; o += 16L * 256) {
+                const long hh = o / per_head, within = o - hh * per_head;
+                const uint8_t *src = p.kv_b.w + (hh * (p.nope + p.vdim) + p.nope) * row_bytes + within;
+                if (within + 16 <= per_head)
+                    __builtin_amdgcn_global_load_lds(
+                        (const __attribute__((address_space(1))) void *)src, sink, 16, 0, 0);
+            }
+        }
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_s_waitcnt(0);
         return;
     }
     // ---- scores: compute wave w takes the 16-dim steps w, w + 4, ...; two
