@@ -521,6 +521,196 @@ __global__ __launch_bounds__(512) void mla_attend_mfma_kernel(MlaParams p) {
     }
 }
 
+// Prefill attention (rows > 1, causal; moonlight_kernels.metal:247-343 with
+// key_count = position + row + 1), flash form: a workgroup takes RB query
+// rows and every head, and streams key tiles of kPfKeys cache rows
+// through two LDS buffers (DMA of tile t + 1 in flight while tile t is
+// used).  Per tile and row, on fp32 MFMA with the operand layouts of
+// mla_attend_mfma_kernel: scores S[key][head] (the 4 waves split the latent +
+// rope dims; partials summed in LDS in wave order), the causal mask, an
+// online softmax (running max and sum per row and head; the context is
+// rescaled when the max grows), and the context LC[head][d] += P . lat (the
+// waves split the 16-wide d tiles).  The normalised lc goes straight to
+// latent_context: no split partials, no merge launch, and every key tile is
+// read once per RB rows instead of once per row.
+constexpr int kPfRowsPerGroup = 2;  // measured: 2 rows per workgroup beat 4
+constexpr int kPfKeys = 16;
+template <int RB>
+constexpr size_t pf_lds_bytes() {
+    return sizeof(float) * (2 * (size_t)kPfKeys * kAttnRowStride +   // key tiles
+                            4 * RB * kPfKeys * kMlaMaxHeads +        // score partials
+                            RB * kMlaMaxHeads * (kPfKeys + 4) +      // P [row][head][key]
+                            3 * RB * kMlaMaxHeads);                  // max, sum, rescale
+}
+
+template <int RB>
+__global__ __launch_bounds__(256) void mla_prefill_attend_kernel(MlaParams p) {
+    constexpr int H = kMlaMaxHeads, KS = kPfKeys;
+    constexpr int NJ = kAttnDims / 64;         // 16-dim score steps per wave
+    constexpr int NQ = kMlaMaxLatent / 64;     // d tiles per wave
+    constexpr int PS = KS + 4;                 // P row stride
+    extern __shared__ __attribute__((aligned(16))) float pf_lds[];
+    float *kbuf = pf_lds;                            // [2][KS][stride]
+    float *part = kbuf + 2 * KS * kAttnRowStride;    // [4 waves][RB][KS][H]
+    float *p_s = part + 4 * RB * KS * H;             // [RB][H][PS]
+    float *m_s = p_s + RB * H * PS;                  // [RB][H]
+    float *l_s = m_s + RB * H;
+    float *sc_s = l_s + RB * H;
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int g = lane >> 4, m16 = lane & 15;
+    const int r0 = blockIdx.x * RB;
+    const int nrow = p.rows - r0 < RB ? p.rows - r0 : RB;
+    const int pos0 = mla_position(p) + r0;  // position of row r0; row b sees keys <= pos0 + b
+    const int keys = pos0 + nrow;
+    const int ntiles = (keys + KS - 1) / KS;
+    const int D = p.latent, R = p.rope, KD = D + R;  // KD a multiple of 16 (launch condition)
+    // ---- queries of the rows (absent rows repeat row r0, absent heads head 0)
+    f32x4 qv[RB][NJ];
+#pragma unroll
+    for (int b = 0; b < RB; ++b) {
+        const long qh = (long)(r0 + (b < nrow ? b : 0)) * p.heads + (m16 < p.heads ? m16 : 0);
+        const float *qa = p.query_absorbed + qh * D;
+        const float *qr = p.query_rope + qh * R;
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) {
+            const int d = wave * 16 + 64 * j + 4 * g;
+            if (d < KD) qv[b][j] = d < D ? load_f4(qa + d) : load_f4(qr + (d - D));
+        }
+    }
+    for (int i = t; i < RB * H; i += blockDim.x) {
+        m_s[i] = -INFINITY;
+        l_s[i] = 0.0f;
+    }
+    // ---- key tile -> LDS buffer by DMA (16 bytes per lane into M0 + 16 lane);
+    // rows past the last key copy the last key (finite, masked)
+    auto issue = [&](int tile, int buf) {
+        float *kb = kbuf + buf * KS * kAttnRowStride;
+        for (int row = wave; row < KS; row += 4) {
+            const int k = tile * KS + row < keys ? tile * KS + row : keys - 1;
+            const float *lsrc = p.latent_cache + (long)k * D;
+            const float *rsrc = p.rope_cache + (long)k * R;
+            __attribute__((address_space(3))) float *dst =
+                (__attribute__((address_space(3))) float *)(kb + row * kAttnRowStride);
+            for (int c0 = 0; c0 < D; c0 += 256)
+                if (c0 + 4 * lane < D)
+                    __builtin_amdgcn_global_load_lds(
+                        (const __attribute__((address_space(1))) void *)(lsrc + c0 + 4 * lane),
+                        dst + c0, 16, 0, 0);
+            if (4 * lane < R)
+                __builtin_amdgcn_global_load_lds(
+                    (const __attribute__((address_space(1))) void *)(rsrc + 4 * lane), dst + D,
+                    16, 0, 0);
+        }
+    };
+    f32x4v acc[RB][NQ];
+#pragma unroll
+    for (int b = 0; b < RB; ++b)
+#pragma unroll
+        for (int q = 0; q < NQ; ++q) acc[b][q] = f32x4v{0.f, 0.f, 0.f, 0.f};
+    issue(0, 0);
+    for (int kt = 0; kt < ntiles; ++kt) {
+        __builtin_amdgcn_s_waitcnt(0);  // this wave's part of tile kt has landed
+        __syncthreads();                // every part visible; tile kt - 1 and P free
+        if (kt + 1 < ntiles) issue(kt + 1, (kt + 1) & 1);
+        const float *kb = kbuf + (kt & 1) * KS * kAttnRowStride;
+        // ---- scores of the tile: wave w takes the 16-dim steps w, w + 4, ...
+        {
+            f32x4v sacc[RB][2];
+#pragma unroll
+            for (int b = 0; b < RB; ++b) sacc[b][0] = sacc[b][1] = f32x4v{0.f, 0.f, 0.f, 0.f};
+            // two accumulators per row (even / odd MFMA of a step); grouping
+            // all rows' MFMAs of one component measured slower
+#pragma unroll
+            for (int j = 0; j < NJ; ++j) {
+                const int d0 = wave * 16 + 64 * j;
+                if (d0 < KD) {
+                    const f32x4 av = *reinterpret_cast<const f32x4 *>(
+                        kb + m16 * kAttnRowStride + d0 + 4 * g);
+#pragma unroll
+                    for (int b = 0; b < RB; ++b) {
+                        sacc[b][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(av.x, qv[b][j].x, sacc[b][0], 0, 0, 0);
+                        sacc[b][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(av.y, qv[b][j].y, sacc[b][1], 0, 0, 0);
+                        sacc[b][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(av.z, qv[b][j].z, sacc[b][0], 0, 0, 0);
+                        sacc[b][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(av.w, qv[b][j].w, sacc[b][1], 0, 0, 0);
+                    }
+                }
+            }
+#pragma unroll
+            for (int b = 0; b < RB; ++b)
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    part[((wave * RB + b) * KS + 4 * g + i) * H + m16] = sacc[b][0][i] + sacc[b][1][i];
+        }
+        __syncthreads();
+        // ---- causal mask and online softmax: 16 lanes per (row, head), one key each
+        for (int idx = t; idx < RB * H * KS; idx += blockDim.x) {
+            const int b = idx / (H * KS), h = (idx / KS) % H, k = idx % KS;
+            const float sum = (part[((0 * RB + b) * KS + k) * H + h] + part[((1 * RB + b) * KS + k) * H + h]) +
+                              (part[((2 * RB + b) * KS + k) * H + h] + part[((3 * RB + b) * KS + k) * H + h]);
+            const int key = kt * KS + k;
+            const bool valid = b < nrow && key <= pos0 + b;
+            const float sv = valid ? sum * p.scale : -INFINITY;
+            float mt = sv;
+#pragma unroll
+            for (int o = 8; o >= 1; o >>= 1) mt = fmaxf(mt, __shfl_xor(mt, o, 64));
+            const float mo = m_s[b * H + h];
+            const float mn = fmaxf(mo, mt);
+            const float e = valid ? expf(sv - mn) : 0.0f;
+            float es = e;
+#pragma unroll
+            for (int o = 8; o >= 1; o >>= 1) es += __shfl_xor(es, o, 64);
+            p_s[(b * H + h) * PS + k] = e;
+            if (k == 0) {
+                const float sc = mn == -INFINITY ? 1.0f : expf(mo - mn);  // 0 while mo is -inf
+                l_s[b * H + h] = l_s[b * H + h] * sc + es;
+                m_s[b * H + h] = mn;
+                sc_s[b * H + h] = sc;
+            }
+        }
+        __syncthreads();
+        // ---- context: wave w takes the d tiles w, w + 4, ...
+#pragma unroll
+        for (int b = 0; b < RB; ++b) {
+            const f32x4 pv = *reinterpret_cast<const f32x4 *>(p_s + (b * H + m16) * PS + 4 * g);
+            const float pj[4] = {pv.x, pv.y, pv.z, pv.w};
+            float scl[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) scl[i] = sc_s[b * H + 4 * g + i];
+#pragma unroll
+            for (int q = 0; q < NQ; ++q) {
+                const int dt = wave + 4 * q;
+                if (dt < D / 16) {
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) acc[b][q][i] *= scl[i];
+                    const float *lb = kb + (4 * g) * kAttnRowStride + dt * 16 + m16;
+#pragma unroll
+                    for (int j = 0; j < 4; ++j)
+                        acc[b][q] = __builtin_amdgcn_mfma_f32_16x16x4f32(pj[j], lb[j * kAttnRowStride],
+                                                                        acc[b][q], 0, 0, 0);
+                }
+            }
+        }
+    }
+    __syncthreads();  // the last tile's sums in l_s
+    // ---- normalised latent context of each row and head
+#pragma unroll
+    for (int b = 0; b < RB; ++b) {
+        if (b >= nrow) continue;
+#pragma unroll
+        for (int q = 0; q < NQ; ++q) {
+            const int dt = wave + 4 * q;
+            if (dt >= D / 16) continue;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int h = 4 * g + i;
+                if (h < p.heads)
+                    p.latent_context[((long)(r0 + b) * p.heads + h) * D + dt * 16 + m16] =
+                        acc[b][q][i] / l_s[b * H + h];
+            }
+        }
+    }
+}
+
 // lc_h = sum_s e^{m_s - M} lc_s / sum_s e^{m_s - M} l_s over the key splits,
 // in one pass.  Workgroup (row, head, kMergeDims latent dims), 8 waves; a
 // wave's lanes form 64 / kMergeDims groups, so 16 lane groups take the splits
@@ -646,7 +836,22 @@ int mla_attention_core(const MlaParams &p, hipStream_t stream) {
                                      : (p.position + p.rows + kMlaKeysPerSplit - 1) / kMlaKeysPerSplit;
     const dim3 grid(splits, p.rows);
     const size_t lds = (size_t)kMlaKeysPerSplit * p.latent * sizeof(float);
-    if (p.rope % 4 == 0 && (p.latent + p.rope) % 16 == 0 && p.latent + p.rope <= kAttnDims) {
+    const bool mfma = p.rope % 4 == 0 && (p.latent + p.rope) % 16 == 0 &&
+                      p.latent + p.rope <= kAttnDims;
+    if (mfma && p.rows > 1 && !p.grid_splits) {
+        // prefill: flash form, lc written directly (no merge)
+        constexpr int RB = kPfRowsPerGroup;
+        static const bool attr = hipFuncSetAttribute(
+            reinterpret_cast<const void *>(&mla_prefill_attend_kernel<RB>),
+            hipFuncAttributeMaxDynamicSharedMemorySize, (int)pf_lds_bytes<RB>()) == hipSuccess;
+        (void)attr;
+        hipLaunchKernelGGL(mla_prefill_attend_kernel<RB>, dim3((p.rows + RB - 1) / RB), dim3(256),
+                           pf_lds_bytes<RB>(), stream, p);
+        hipLaunchKernelGGL(mla_value_kernel, dim3(p.rows, p.heads, (p.vdim + 31) / 32), dim3(256),
+                           0, stream, p);
+        return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
+    }
+    if (mfma) {
         static const bool attr = hipFuncSetAttribute(
             reinterpret_cast<const void *>(&mla_attend_mfma_kernel),
             hipFuncAttributeMaxDynamicSharedMemorySize, (int)kAttnMfmaLds) == hipSuccess;
