@@ -63,13 +63,14 @@ __device__ __forceinline__ void kvb_load8(const MatrixRef &m, int row, int col, 
     }
 }
 
-// grid (rows, 1 + heads * latent / 64): role 0 appends the cache rows; role
+// grid (rows, 1 + heads * chunks), chunks = latent / 64 (or 0: grid
+// (rows, 1 + heads), the query rope only): role 0 appends the cache rows; role
 // 1 + h * chunks + c ropes head h's query (c == 0) and absorbs it into the 64
 // latent columns c * 64 .. + 63: thread (i = t / 8, j = t % 8) takes kv_b
 // rows i, i + 32, ... of the head's nope part and columns 8 j .. 8 j + 7, all
 // loads of a thread issued before its FMAs; the 32 row groups meet in LDS.
 constexpr int kMlaAbsorbCols = 64;
-__global__ __launch_bounds__(256) void mla_prep_kernel(MlaParams p) {
+__global__ __launch_bounds__(256) void mla_prep_kernel(MlaParams p, int chunks) {
     const int r = blockIdx.x;
     const int role = blockIdx.y;
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
@@ -109,9 +110,9 @@ __global__ __launch_bounds__(256) void mla_prep_kernel(MlaParams p) {
         }
         return;
     }
-    const int chunks = p.latent / kMlaAbsorbCols;
-    const int h = (role - 1) / chunks;
-    const int col0 = ((role - 1) % chunks) * kMlaAbsorbCols;
+    // chunks == 0: the query rope only (prefill absorbs with mla_head_gemm)
+    const int h = chunks ? (role - 1) / chunks : role - 1;
+    const int col0 = chunks ? ((role - 1) % chunks) * kMlaAbsorbCols : 0;
     const float *q = p.query + (long)r * p.query_stride + (long)h * hw;
     if (col0 == 0 && t < half) {
         const float angle = (float)pos * p.inv_freq[t];
@@ -121,6 +122,7 @@ __global__ __launch_bounds__(256) void mla_prep_kernel(MlaParams p) {
         qr[t] = first * cs - second * sn;
         qr[half + t] = second * cs + first * sn;
     }
+    if (!chunks) return;
     // qa[l] = sum_c q_nope[c] * kv_b[h*(nope+v) + c, l]
     constexpr int kRowsPerThread = 256 / 32;  // nope <= 256
     __shared__ float red[32][kMlaAbsorbCols + 1];
@@ -521,6 +523,106 @@ __global__ __launch_bounds__(512) void mla_attend_mfma_kernel(MlaParams p) {
     }
 }
 
+// Four consecutive dequantised kv_b values w[row, col..col+3] (col % 4 == 0),
+// moonlight_weight_value (moonlight_kernels.metal:202-216) per element.
+__device__ __forceinline__ f32x4 kvb_load4(const MatrixRef &m, long row, int col, int width) {
+    if (m.fmt == kF32) return load_f4(reinterpret_cast<const float *>(m.w) + row * width + col);
+    const float s = m.s[row];
+    if (m.fmt == kQ8) {
+        const unsigned v = *reinterpret_cast<const unsigned *>(m.w + row * width + col);
+        return f32x4{(float)(int8_t)(v & 0xFF) * s, (float)(int8_t)((v >> 8) & 0xFF) * s,
+                     (float)(int8_t)((v >> 16) & 0xFF) * s, (float)(int8_t)(v >> 24) * s};
+    }
+    const unsigned v =
+        *reinterpret_cast<const unsigned short *>(m.w + row * ((width + 1) / 2) + col / 2);
+    return f32x4{(float)((int)(v & 15) - 8) * s, (float)((int)((v >> 4) & 15) - 8) * s,
+                 (float)((int)((v >> 8) & 15) - 8) * s, (float)((int)((v >> 12) & 15) - 8) * s};
+}
+
+// Per-head products of the prefill path on fp32 MFMA (16x16x4), kv_b
+// dequantised on its way into LDS:
+//   ABSORB (moonlight_attention_absorb_query, moonlight_kernels.metal:218-245):
+//     qa[r][h][n] = sum_k q_nope[r][h][k] kv_b[h (nope + v) + k][n]   K = nope, N = latent
+//   value (moonlight_attention_decode_value, :345-375):
+//     ctx[r][h][n] = sum_k lc[r][h][k] kv_b[h (nope + v) + nope + n][k] K = latent, N = vdim
+// Workgroup: 64 token rows x 64 outputs of one head (grid z); wave w owns
+// rows 16 w .. + 15 as four 16 x 16 tiles; k in steps of 16 through LDS, the
+// next step's loads in flight during the MFMAs.  fp32 products and sums, in
+// another order than the per-row kernels.
+template <bool ABSORB>
+__global__ __launch_bounds__(256) void mla_head_gemm_kernel(MlaParams p) {
+    constexpr int BM = 64, BK = 16, LS = BK + 4;
+    __shared__ __attribute__((aligned(16))) float xs[BM][LS];
+    __shared__ __attribute__((aligned(16))) float ws[64][LS];
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int g = lane >> 4, m16 = lane & 15;
+    const int m0 = blockIdx.x * BM, n0 = blockIdx.y * 64, h = blockIdx.z;
+    const int K = ABSORB ? p.nope : p.latent;
+    const int N = ABSORB ? p.latent : p.vdim;
+    const long wrow0 = (long)h * (p.nope + p.vdim) + (ABSORB ? 0 : p.nope);
+    // staging: thread t copies x[m0 + t / 4][k0 + 4 (t % 4) .. + 3] and 4 weights
+    const int xr = t >> 2, xc = 4 * (t & 3);
+    const long xrow = m0 + xr < p.rows ? m0 + xr : p.rows - 1;  // past the end: loaded, unused
+    const float *xsrc = ABSORB ? p.query + xrow * p.query_stride + (long)h * (p.nope + p.rope)
+                               : p.latent_context + (xrow * p.heads + h) * p.latent;
+    f32x4 xv, wv;
+    auto fetch = [&](int k0) {
+        xv = load_f4(xsrc + k0 + xc);
+        if constexpr (ABSORB) {  // 4 outputs n of one k: a kv_b row segment
+            const int n = n0 + 4 * (t & 15);
+            wv = kvb_load4(p.kv_b, wrow0 + k0 + (t >> 4), n + 4 <= N ? n : N - 4, p.latent);
+        } else {  // 4 k of one output n: a kv_b row segment
+            const int n = n0 + (t >> 2) < N ? n0 + (t >> 2) : N - 1;
+            wv = kvb_load4(p.kv_b, wrow0 + n, k0 + 4 * (t & 3), p.latent);
+        }
+    };
+    auto stash = [&]() {
+        *reinterpret_cast<f32x4 *>(&xs[xr][xc]) = xv;
+        if constexpr (ABSORB) {
+            const int k = t >> 4, n = 4 * (t & 15);
+            ws[n][k] = wv.x;
+            ws[n + 1][k] = wv.y;
+            ws[n + 2][k] = wv.z;
+            ws[n + 3][k] = wv.w;
+        } else {
+            *reinterpret_cast<f32x4 *>(&ws[t >> 2][4 * (t & 3)]) = wv;
+        }
+    };
+    f32x4v acc[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) acc[q] = f32x4v{0.f, 0.f, 0.f, 0.f};
+    fetch(0);
+    for (int k0 = 0; k0 < K; k0 += BK) {
+        __syncthreads();  // the previous step's LDS reads are done
+        stash();
+        __syncthreads();
+        if (k0 + BK < K) fetch(k0 + BK);
+        const f32x4 a = *reinterpret_cast<const f32x4 *>(&xs[16 * wave + m16][4 * g]);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const f32x4 b = *reinterpret_cast<const f32x4 *>(&ws[16 * q + m16][4 * g]);
+            acc[q] = __builtin_amdgcn_mfma_f32_16x16x4f32(a.x, b.x, acc[q], 0, 0, 0);
+            acc[q] = __builtin_amdgcn_mfma_f32_16x16x4f32(a.y, b.y, acc[q], 0, 0, 0);
+            acc[q] = __builtin_amdgcn_mfma_f32_16x16x4f32(a.z, b.z, acc[q], 0, 0, 0);
+            acc[q] = __builtin_amdgcn_mfma_f32_16x16x4f32(a.w, b.w, acc[q], 0, 0, 0);
+        }
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const int n = n0 + 16 * q + m16;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const long r = m0 + 16 * wave + 4 * g + i;
+            if (r < p.rows && n < N) {
+                if constexpr (ABSORB)
+                    p.query_absorbed[(r * p.heads + h) * p.latent + n] = acc[q][i];
+                else
+                    p.context[(r * p.heads + h) * p.vdim + n] = acc[q][i];
+            }
+        }
+    }
+}
+
 // Prefill attention (rows > 1, causal; moonlight_kernels.metal:247-343 with
 // key_count = position + row + 1), flash form: a workgroup takes RB query
 // rows and every head, and streams key tiles of kPfKeys cache rows
@@ -830,27 +932,34 @@ int mla_attention_core(const MlaParams &p, hipStream_t stream) {
         (p.position + p.rows + kMlaKeysPerSplit - 1) / kMlaKeysPerSplit > p.max_splits ||
         (p.grid_splits && (!p.position_dev || p.grid_splits > p.max_splits)))
         return kErrArgs;
-    hipLaunchKernelGGL(mla_prep_kernel, dim3(p.rows, 1 + p.heads * (p.latent / kMlaAbsorbCols)),
-                       dim3(256), 0, stream, p);
-    const int splits = p.grid_splits ? p.grid_splits
-                                     : (p.position + p.rows + kMlaKeysPerSplit - 1) / kMlaKeysPerSplit;
-    const dim3 grid(splits, p.rows);
-    const size_t lds = (size_t)kMlaKeysPerSplit * p.latent * sizeof(float);
     const bool mfma = p.rope % 4 == 0 && (p.latent + p.rope) % 16 == 0 &&
                       p.latent + p.rope <= kAttnDims;
-    if (mfma && p.rows > 1 && !p.grid_splits) {
-        // prefill: flash form, lc written directly (no merge)
+    if (mfma && p.rows > 1 && !p.grid_splits && p.nope % 16 == 0 && p.vdim % 16 == 0) {
+        // prefill: cache append + query rope, the absorb as a per-head GEMM,
+        // flash attention writing lc directly, the value as a per-head GEMM
         constexpr int RB = kPfRowsPerGroup;
         static const bool attr = hipFuncSetAttribute(
             reinterpret_cast<const void *>(&mla_prefill_attend_kernel<RB>),
             hipFuncAttributeMaxDynamicSharedMemorySize, (int)pf_lds_bytes<RB>()) == hipSuccess;
         (void)attr;
+        const unsigned mt = (unsigned)((p.rows + 63) / 64);
+        hipLaunchKernelGGL(mla_prep_kernel, dim3(p.rows, 1 + p.heads), dim3(256), 0, stream, p, 0);
+        hipLaunchKernelGGL(mla_head_gemm_kernel<true>,
+                           dim3(mt, (unsigned)((p.latent + 63) / 64), (unsigned)p.heads), dim3(256),
+                           0, stream, p);
         hipLaunchKernelGGL(mla_prefill_attend_kernel<RB>, dim3((p.rows + RB - 1) / RB), dim3(256),
                            pf_lds_bytes<RB>(), stream, p);
-        hipLaunchKernelGGL(mla_value_kernel, dim3(p.rows, p.heads, (p.vdim + 31) / 32), dim3(256),
+        hipLaunchKernelGGL(mla_head_gemm_kernel<false>,
+                           dim3(mt, (unsigned)((p.vdim + 63) / 64), (unsigned)p.heads), dim3(256),
                            0, stream, p);
         return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
     }
+    hipLaunchKernelGGL(mla_prep_kernel, dim3(p.rows, 1 + p.heads * (p.latent / kMlaAbsorbCols)),
+                       dim3(256), 0, stream, p, p.latent / kMlaAbsorbCols);
+    const int splits = p.grid_splits ? p.grid_splits
+                                     : (p.position + p.rows + kMlaKeysPerSplit - 1) / kMlaKeysPerSplit;
+    const dim3 grid(splits, p.rows);
+    const size_t lds = (size_t)kMlaKeysPerSplit * p.latent * sizeof(float);
     if (mfma) {
         static const bool attr = hipFuncSetAttribute(
             reinterpret_cast<const void *>(&mla_attend_mfma_kernel),
