@@ -637,23 +637,36 @@ __global__ __launch_bounds__(256) void mla_head_gemm_kernel(MlaParams p) {
 // read once per RB rows instead of once per row.
 constexpr int kPfRowsPerGroup = 2;  // measured: 2 rows per workgroup beat 4
 constexpr int kPfKeys = 16;
+constexpr int kPfRowStride = kMlaMaxLatent + 4;  // latent rows in LDS (rope in registers)
+// The running max of a (row, head) moves only when a tile's max exceeds it
+// by more than this (e^8 ~ 3e3 keeps every exp term and sum far inside fp32);
+// the context rescale then runs on few tiles.
+constexpr float kPfLazyMax = 8.0f;
 template <int RB>
 constexpr size_t pf_lds_bytes() {
-    return sizeof(float) * (2 * (size_t)kPfKeys * kAttnRowStride +   // key tiles
+    return sizeof(float) * (2 * (size_t)kPfKeys * kPfRowStride +     // key tiles (latent)
                             4 * RB * kPfKeys * kMlaMaxHeads +        // score partials
                             RB * kMlaMaxHeads * (kPfKeys + 4) +      // P [row][head][key]
                             3 * RB * kMlaMaxHeads);                  // max, sum, rescale
 }
 
+// Workgroup barrier for LDS traffic only: waits for this wave's LDS
+// operations, not for its loads in flight (__syncthreads() would also wait
+// for the next key tile's DMA and serialise the double buffering).
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0); vmcnt, expcnt not waited
+    __builtin_amdgcn_s_barrier();
+}
+
 template <int RB>
-__global__ __launch_bounds__(256) void mla_prefill_attend_kernel(MlaParams p) {
+__global__ __launch_bounds__(256, 2) void mla_prefill_attend_kernel(MlaParams p) {
     constexpr int H = kMlaMaxHeads, KS = kPfKeys;
     constexpr int NJ = kAttnDims / 64;         // 16-dim score steps per wave
     constexpr int NQ = kMlaMaxLatent / 64;     // d tiles per wave
     constexpr int PS = KS + 4;                 // P row stride
     extern __shared__ __attribute__((aligned(16))) float pf_lds[];
-    float *kbuf = pf_lds;                            // [2][KS][stride]
-    float *part = kbuf + 2 * KS * kAttnRowStride;    // [4 waves][RB][KS][H]
+    float *kbuf = pf_lds;                            // [2][KS][kPfRowStride]
+    float *part = kbuf + 2 * KS * kPfRowStride;      // [4 waves][RB][KS][H]
     float *p_s = part + 4 * RB * KS * H;             // [RB][H][PS]
     float *m_s = p_s + RB * H * PS;                  // [RB][H]
     float *l_s = m_s + RB * H;
@@ -683,25 +696,27 @@ __global__ __launch_bounds__(256) void mla_prefill_attend_kernel(MlaParams p) {
         m_s[i] = -INFINITY;
         l_s[i] = 0.0f;
     }
-    // ---- key tile -> LDS buffer by DMA (16 bytes per lane into M0 + 16 lane);
-    // rows past the last key copy the last key (finite, masked)
-    auto issue = [&](int tile, int buf) {
-        float *kb = kbuf + buf * KS * kAttnRowStride;
+    // ---- latent rows of a key tile -> LDS buffer by DMA (16 bytes per lane
+    // into M0 + 16 lane); the rope part goes to registers: a wave's one rope
+    // step (dims D + 16 w ..) of key m16 as a float4 per lane.  Rows past the
+    // last key copy the last key (finite, masked).
+    const bool has_rope = 16 * wave < R;  // D % 64 == 0: step j = D / 64
+    auto issue = [&](int tile, int buf, f32x4 &rope_next) {
+        float *kb = kbuf + buf * KS * kPfRowStride;
         for (int row = wave; row < KS; row += 4) {
             const int k = tile * KS + row < keys ? tile * KS + row : keys - 1;
             const float *lsrc = p.latent_cache + (long)k * D;
-            const float *rsrc = p.rope_cache + (long)k * R;
             __attribute__((address_space(3))) float *dst =
-                (__attribute__((address_space(3))) float *)(kb + row * kAttnRowStride);
+                (__attribute__((address_space(3))) float *)(kb + row * kPfRowStride);
             for (int c0 = 0; c0 < D; c0 += 256)
                 if (c0 + 4 * lane < D)
                     __builtin_amdgcn_global_load_lds(
                         (const __attribute__((address_space(1))) void *)(lsrc + c0 + 4 * lane),
                         dst + c0, 16, 0, 0);
-            if (4 * lane < R)
-                __builtin_amdgcn_global_load_lds(
-                    (const __attribute__((address_space(1))) void *)(rsrc + 4 * lane), dst + D,
-                    16, 0, 0);
+        }
+        if (has_rope) {
+            const int k = tile * KS + m16 < keys ? tile * KS + m16 : keys - 1;
+            rope_next = load_f4(p.rope_cache + (long)k * R + 16 * wave + 4 * g);
         }
     };
     f32x4v acc[RB][NQ];
@@ -709,12 +724,14 @@ __global__ __launch_bounds__(256) void mla_prefill_attend_kernel(MlaParams p) {
     for (int b = 0; b < RB; ++b)
 #pragma unroll
         for (int q = 0; q < NQ; ++q) acc[b][q] = f32x4v{0.f, 0.f, 0.f, 0.f};
-    issue(0, 0);
+    f32x4 rope_cur = {0.f, 0.f, 0.f, 0.f}, rope_next = {0.f, 0.f, 0.f, 0.f};
+    issue(0, 0, rope_next);
     for (int kt = 0; kt < ntiles; ++kt) {
         __builtin_amdgcn_s_waitcnt(0);  // this wave's part of tile kt has landed
         __syncthreads();                // every part visible; tile kt - 1 and P free
-        if (kt + 1 < ntiles) issue(kt + 1, (kt + 1) & 1);
-        const float *kb = kbuf + (kt & 1) * KS * kAttnRowStride;
+        rope_cur = rope_next;
+        if (kt + 1 < ntiles) issue(kt + 1, (kt + 1) & 1, rope_next);
+        const float *kb = kbuf + (kt & 1) * KS * kPfRowStride;
         // ---- scores of the tile: wave w takes the 16-dim steps w, w + 4, ...
         {
             f32x4v sacc[RB][2];
@@ -726,8 +743,9 @@ __global__ __launch_bounds__(256) void mla_prefill_attend_kernel(MlaParams p) {
             for (int j = 0; j < NJ; ++j) {
                 const int d0 = wave * 16 + 64 * j;
                 if (d0 < KD) {
-                    const f32x4 av = *reinterpret_cast<const f32x4 *>(
-                        kb + m16 * kAttnRowStride + d0 + 4 * g);
+                    const f32x4 av = d0 < D ? *reinterpret_cast<const f32x4 *>(
+                                                  kb + m16 * kPfRowStride + d0 + 4 * g)
+                                            : rope_cur;
 #pragma unroll
                     for (int b = 0; b < RB; ++b) {
                         sacc[b][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(av.x, qv[b][j].x, sacc[b][0], 0, 0, 0);
@@ -743,7 +761,7 @@ __global__ __launch_bounds__(256) void mla_prefill_attend_kernel(MlaParams p) {
                 for (int i = 0; i < 4; ++i)
                     part[((wave * RB + b) * KS + 4 * g + i) * H + m16] = sacc[b][0][i] + sacc[b][1][i];
         }
-        __syncthreads();
+        lds_barrier();
         // ---- causal mask and online softmax: 16 lanes per (row, head), one key each
         for (int idx = t; idx < RB * H * KS; idx += blockDim.x) {
             const int b = idx / (H * KS), h = (idx / KS) % H, k = idx % KS;
@@ -756,38 +774,46 @@ __global__ __launch_bounds__(256) void mla_prefill_attend_kernel(MlaParams p) {
 #pragma unroll
             for (int o = 8; o >= 1; o >>= 1) mt = fmaxf(mt, __shfl_xor(mt, o, 64));
             const float mo = m_s[b * H + h];
-            const float mn = fmaxf(mo, mt);
-            const float e = valid ? expf(sv - mn) : 0.0f;
+            const float mn = mt > mo + kPfLazyMax ? mt : mo;  // -inf mo: the tile max
+            const float e = valid ? __expf(sv - mn) : 0.0f;
             float es = e;
 #pragma unroll
             for (int o = 8; o >= 1; o >>= 1) es += __shfl_xor(es, o, 64);
             p_s[(b * H + h) * PS + k] = e;
             if (k == 0) {
-                const float sc = mn == -INFINITY ? 1.0f : expf(mo - mn);  // 0 while mo is -inf
+                const float sc = mn == mo ? 1.0f : __expf(mo - mn);  // 0 while mo is -inf
                 l_s[b * H + h] = l_s[b * H + h] * sc + es;
                 m_s[b * H + h] = mn;
                 sc_s[b * H + h] = sc;
             }
         }
-        __syncthreads();
+        lds_barrier();
         // ---- context: wave w takes the d tiles w, w + 4, ...
 #pragma unroll
         for (int b = 0; b < RB; ++b) {
             const f32x4 pv = *reinterpret_cast<const f32x4 *>(p_s + (b * H + m16) * PS + 4 * g);
             const float pj[4] = {pv.x, pv.y, pv.z, pv.w};
             float scl[4];
+            bool rescale = false;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) scl[i] = sc_s[b * H + 4 * g + i];
+            for (int i = 0; i < 4; ++i) {
+                scl[i] = sc_s[b * H + 4 * g + i];
+                rescale |= scl[i] != 1.0f;
+            }
+            if (rescale) {  // rare: the lazy max moved for one of this lane's heads
+#pragma unroll
+                for (int q = 0; q < NQ; ++q)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) acc[b][q][i] *= scl[i];
+            }
 #pragma unroll
             for (int q = 0; q < NQ; ++q) {
                 const int dt = wave + 4 * q;
                 if (dt < D / 16) {
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) acc[b][q][i] *= scl[i];
-                    const float *lb = kb + (4 * g) * kAttnRowStride + dt * 16 + m16;
+                    const float *lb = kb + (4 * g) * kPfRowStride + dt * 16 + m16;
 #pragma unroll
                     for (int j = 0; j < 4; ++j)
-                        acc[b][q] = __builtin_amdgcn_mfma_f32_16x16x4f32(pj[j], lb[j * kAttnRowStride],
+                        acc[b][q] = __builtin_amdgcn_mfma_f32_16x16x4f32(pj[j], lb[j * kPfRowStride],
                                                                         acc[b][q], 0, 0, 0);
                 }
             }
