@@ -188,6 +188,24 @@ def moonlight_extras(native, extra, decode_tokens):
               f"({1e3 / wall_ms:.1f} tok/s), device {dev_ms:.3f} ms",
               file=sys.stderr, flush=True)
         sess.close()
+    # full-model prefill of 2048 tokens (27 layers + lm_head of the last row)
+    rows = 2048
+    sess = S.Session(model, rows + 16, rows)
+    ids = [(7919 * i + 17) % 163840 for i in range(rows)]
+    dev = []
+    for _ in range(3):
+        sess.reset()
+        t1 = time.perf_counter()
+        sess.prefill(ids)
+        wall = time.perf_counter() - t1
+        dev.append(sess.device_time_ms())
+    dev_ms = sorted(dev)[1]
+    extra[f"prefill_q8_T{rows}"] = {"ms_device": round(dev_ms, 2),
+                                     "tok_per_s": round(rows / (dev_ms * 1e-3), 1),
+                                     "ms_wall_last": round(wall * 1e3, 2)}
+    print(f"[bench] prefill T={rows}: {dev_ms:.2f} ms device ({rows / (dev_ms * 1e-3):.0f} tok/s)",
+          file=sys.stderr, flush=True)
+    sess.close()
     model.close()
     model = S.Model.synthetic(expert_bits=4, dense_bits=4)
     prefill_moe(model, 4, extra)
