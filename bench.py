@@ -165,13 +165,15 @@ def moonlight_extras(native, extra, decode_tokens):
         sess = S.Session(model, ctx + decode_tokens + 8, 1)
         sess.fill_kv(ctx, seed=ctx)
         token = 1
+        import numpy as np
+        logits = np.empty(163840, np.float32)  # reused output buffer
         for _ in range(3):
-            logits = sess.decode(token)
+            sess.decode(token, logits)
             token = int(logits.argmax())
         dev, wall = [], []
         for _ in range(decode_tokens):
             t1 = time.perf_counter()
-            logits = sess.decode(token)
+            sess.decode(token, logits)
             wall.append(time.perf_counter() - t1)
             dev.append(sess.device_time_ms())
             token = int(logits.argmax())
@@ -183,7 +185,7 @@ def moonlight_extras(native, extra, decode_tokens):
             "ms_per_token_device": round(dev_ms, 3), "bytes": nbytes,
             "GB/s_device": round(nbytes / (dev_ms * 1e-3) / 1e9, 1),
             "frac_device": round(nbytes / (dev_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-            "tokens": decode_tokens}
+            "tokens": decode_tokens, "graph": sess.decode_graph()}
         print(f"[bench] decode ctx {ctx}: {wall_ms:.3f} ms/token wall "
               f"({1e3 / wall_ms:.1f} tok/s), device {dev_ms:.3f} ms",
               file=sys.stderr, flush=True)

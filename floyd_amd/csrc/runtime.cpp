@@ -137,6 +137,7 @@ struct MoonlightSession {
     int *step_dev = nullptr, *pos_dev = nullptr;
     int *host_step = nullptr, *host_ids = nullptr;
     int *host_flag = nullptr;
+    float *host_logits = nullptr;  // pinned [vocab]: the D2H target, copied to the caller
     // one-row decode step (embed .. lm_head) as a graph: captured on the
     // second decode of the session, replayed at every later position
     hipGraphExec_t decode_exec = nullptr;
@@ -773,6 +774,7 @@ void free_session(MoonlightSession *s) {
     for (void *p : s->allocations) (void)hipFree(p);
     if (s->decode_exec) (void)hipGraphExecDestroy(s->decode_exec);
     if (s->host_step) (void)hipHostFree(s->host_step);
+    if (s->host_logits) (void)hipHostFree(s->host_logits);
     if (s->host_flag) (void)hipHostFree(s->host_flag);
     if (s->ev_start) (void)hipEventDestroy(s->ev_start);
     if (s->ev_stop) (void)hipEventDestroy(s->ev_stop);
@@ -1249,7 +1251,7 @@ int forward(MoonlightSession *s, const int *ids, int count, int start, float *la
         if (decode) s->eager_decodes++;
     }
     ok = ok && hipEventRecord(s->ev_stop, st) == hipSuccess &&
-         to_host(s, last_logits, s->logits, (size_t)c.vocab_size * sizeof(float)) &&
+         to_host(s, s->host_logits, s->logits, (size_t)c.vocab_size * sizeof(float)) &&
          to_host(s, s->host_flag, s->route_error, sizeof(int));
     if (!finish(s) || !ok) {
         // the device state of a partial forward is unusable: invalidate the caches
@@ -1259,6 +1261,7 @@ int forward(MoonlightSession *s, const int *ids, int count, int start, float *la
                          hipGetErrorString(hipGetLastError()));
     }
     for (int l = 0; l < c.layer_count; ++l) s->kv_lengths[l] = start + count;
+    memcpy(last_logits, s->host_logits, (size_t)c.vocab_size * sizeof(float));
     if (*s->host_flag) return set_error(error, error_size, "Moonlight fast route table failed");
     float ms = 0.0f;
     if (hipEventElapsedTime(&ms, s->ev_start, s->ev_stop) == hipSuccess) s->last_device_ms = ms;
@@ -1364,6 +1367,8 @@ extern "C" int moonlight_session_create(MoonlightSession **out, MoonlightModel *
             hipSuccess &&
         (s->host_ids = s->host_step + 1, true) &&
         hipHostMalloc((void **)&s->host_flag, sizeof(int), hipHostMallocDefault) == hipSuccess &&
+        hipHostMalloc((void **)&s->host_logits, (size_t)c.vocab_size * sizeof(float),
+                      hipHostMallocDefault) == hipSuccess &&
         hipEventCreate(&s->ev_start) == hipSuccess && hipEventCreate(&s->ev_stop) == hipSuccess;
     bool gemm_ok = ok;
     if (ok && options->max_batch >= kGemmMinRows) {

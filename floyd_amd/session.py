@@ -225,8 +225,14 @@ class Session:
         self._call(lib().moonlight_session_append, p, ids.size, out.ctypes.data)
         return out
 
-    def decode(self, token):
-        out = np.empty(self.info["vocab_size"], np.float32)
+    def decode(self, token, out=None):
+        """Logits of one decode step; `out` (float32 [vocab], C-contiguous) is
+        reused when given, as a serving loop would."""
+        if out is None:
+            out = np.empty(self.info["vocab_size"], np.float32)
+        elif (out.dtype != np.float32 or out.shape != (self.info["vocab_size"],) or
+              not out.flags["C_CONTIGUOUS"]):
+            raise ValueError("out must be a C-contiguous float32 array of vocab_size")
         self._call(lib().moonlight_session_decode, int(token), out.ctypes.data)
         return out
 
