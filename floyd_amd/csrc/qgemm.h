@@ -13,7 +13,8 @@
 // A launch covers a table of independent tasks (one per active routed expert
 // plus the shared expert, or one dense matrix).  Tiles are 128 token rows x
 // 256 weight rows (SwiGLU pairs: 128 gate + 128 matching up rows, 128
-// outputs); the tile order groups 4 row tiles of a task so that consecutive
+// outputs), or 32 token rows x 256 weight rows where a launch's tasks hold
+// few rows each; the tile order groups 4 row tiles of a task so that consecutive
 // workgroups on one XCD share weight tiles in that XCD's L2.
 #pragma once
 
@@ -22,6 +23,7 @@
 namespace mlh {
 
 constexpr int kQgBM = 128;  // token rows per tile
+constexpr int kQgBMSmall = 32;  // token rows per tile of few-row launches
 constexpr int kQgBW = 256;  // weight rows per tile
 constexpr int kQgBK = 64;   // k per pipeline stage
 constexpr int kQgGroup = 4; // row tiles per locality group

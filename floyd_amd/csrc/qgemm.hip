@@ -155,10 +155,10 @@ __device__ __forceinline__ int find_task(const int *tile_start, int n, int tile)
     return lo;
 }
 
-template <bool DUAL>
+template <bool DUAL, int BM>
 __host__ __device__ __forceinline__ int tiles_of(int rows, int n_out) {
     constexpr int outw = DUAL ? kQgBW / 2 : kQgBW;
-    return ((rows + kQgBM - 1) / kQgBM) * ((n_out + outw - 1) / outw);
+    return ((rows + BM - 1) / BM) * ((n_out + outw - 1) / outw);
 }
 
 // LDS tiles hold one k slice per stage as rows of RB bytes (RB / 16 chunks of
@@ -173,10 +173,10 @@ __host__ __device__ __forceinline__ int tiles_of(int rows, int n_out) {
 // 128-bit access per cycle.
 template <int FMT> struct QgCfg;
 template <> struct QgCfg<kQ8> {
-    static constexpr int kRB = 64, kStages = 4;
+    static constexpr int kRB = 64;
 };
 template <> struct QgCfg<kQ4> {
-    static constexpr int kRB = 64, kStages = 2;
+    static constexpr int kRB = 64;
 };
 
 template <int RB>
@@ -185,13 +185,19 @@ __device__ __forceinline__ int lds_off(int row, int chunk) {
     else return row * 128 + ((chunk ^ ((row ^ (row >> 3)) & 7)) << 4);
 }
 
-template <int FMT> constexpr int qg_lds_a() { return 2 * kQgBM * QgCfg<FMT>::kRB; }
-template <int FMT> constexpr int qg_lds_stage() {
-    return (2 * kQgBM + kQgBW) * QgCfg<FMT>::kRB;
-}
-template <int FMT> constexpr int qg_lds_bytes() {
-    return QgCfg<FMT>::kStages * qg_lds_stage<FMT>() + kQgBM * 8;  // + scales and row map
-}
+// Tile shape of a BM-row tile (BM = 128 or kQgBMSmall = 32): MI x NF blocks
+// of 32 x 32 per wave and limb, LDS stages, DMA instructions per wave and
+// slice (q8).
+template <int FMT, int BM> struct QgShape {
+    static constexpr int kRB = QgCfg<FMT>::kRB;
+    static constexpr int kStages = FMT == kQ8 ? (BM == 128 ? 4 : 3) : 2;
+    static constexpr int kMI = BM == 128 ? 2 : 1;
+    static constexpr int kNF = BM == 128 ? 4 : 2;
+    static constexpr int kLdsA = 2 * BM * kRB;
+    static constexpr int kStage = (2 * BM + kQgBW) * kRB;
+    static constexpr int kLds = kStages * kStage + BM * 8;  // + scales and row map
+    static constexpr int kDmaPerSlice = (2 * BM / 16 + kQgBW / 16) / 4;
+};
 
 // s_waitcnt on the vector-memory counter only (gfx9 encoding: vmcnt in bits
 // 3:0 and 15:14, expcnt 6:4 and lgkmcnt 11:8 left at their no-wait maxima).
@@ -199,19 +205,24 @@ template <int N> __device__ __forceinline__ void wait_vmcnt() {
     __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
-// Workgroup: 4 waves in a 2 (rows) x 2 (weight rows) arrangement over a 128 x
-// 256 tile; a wave owns 64 token rows x 128 weight rows = 2 x 4 blocks of
-// 32 x 32 per limb (256 int32 accumulators, kept in AGPRs).
-template <int FMT, bool DUAL>
-__global__ __launch_bounds__(256, 1) void qgemm_kernel(QGemmLaunch L) {
+// Workgroup over a BM x 256 tile.  BM = 128: 4 waves in a 2 (rows) x 2
+// (weight rows) arrangement, a wave owning 64 token rows x 128 weight rows =
+// 2 x 4 blocks of 32 x 32 per limb (256 int32 accumulators, in AGPRs).  BM =
+// 32 (batches whose experts hold few rows each): the 4 waves side by side, a
+// wave owning 32 x 64 = 1 x 2 blocks, so the MFMA work per weight byte is a
+// quarter and the tile is bound by the weight stream instead of by padding.
+template <int FMT, bool DUAL, int BM>
+__global__ __launch_bounds__(256, BM == 128 ? 1 : 2) void qgemm_kernel(QGemmLaunch L) {
     extern __shared__ __attribute__((aligned(16))) int8_t qg_lds[];
-    constexpr int kRB = QgCfg<FMT>::kRB;
-    constexpr int kStages = QgCfg<FMT>::kStages;
-    constexpr int kStage = qg_lds_stage<FMT>();
-    constexpr int kLdsA = qg_lds_a<FMT>();
+    using Sh = QgShape<FMT, BM>;
+    constexpr int kRB = Sh::kRB;
+    constexpr int kStages = Sh::kStages;
+    constexpr int kStage = Sh::kStage;
+    constexpr int kLdsA = Sh::kLdsA;
+    constexpr int kMI = Sh::kMI, kNF = Sh::kNF;
     constexpr bool kDma = FMT == kQ8;
     float *lds_scale = reinterpret_cast<float *>(qg_lds + kStages * kStage);
-    int *lds_arow = reinterpret_cast<int *>(qg_lds + kStages * kStage + kQgBM * 4);
+    int *lds_arow = reinterpret_cast<int *>(qg_lds + kStages * kStage + BM * 4);
     // ---- tile -> (task, row tile, column tile), XCD-contiguous order
     GemmTask tk;
     int local;
@@ -224,7 +235,7 @@ __global__ __launch_bounds__(256, 1) void qgemm_kernel(QGemmLaunch L) {
             end = L.range == 1 ? L.tile_start[nr] : L.tile_start[nr + 1];
             if (L.range == 2) begin = L.tile_start[nr];
         } else {
-            end = tiles_of<DUAL>(L.single.rows, L.single.n_out);
+            end = tiles_of<DUAL, BM>(L.single.rows, L.single.n_out);
         }
         const int total = end - begin;
         const int per = (total + 7) >> 3;
@@ -243,20 +254,20 @@ __global__ __launch_bounds__(256, 1) void qgemm_kernel(QGemmLaunch L) {
     }
     constexpr int outw = DUAL ? kQgBW / 2 : kQgBW;
     const int n_tiles = (tk.n_out + outw - 1) / outw;
-    const int m_tiles = (tk.rows + kQgBM - 1) / kQgBM;
+    const int m_tiles = (tk.rows + BM - 1) / BM;
     const int per_group = kQgGroup * n_tiles;
     const int grp = local / per_group;
     const int gsize = min(kQgGroup, m_tiles - grp * kQgGroup);
     const int rem = local - grp * per_group;
-    const int m0 = (grp * kQgGroup + rem % gsize) * kQgBM;
+    const int m0 = (grp * kQgGroup + rem % gsize) * BM;
     const int n0 = (rem / gsize) * outw;
 
     const int tid = threadIdx.x;
     const int lane = tid & (kWave - 1);
     const int wave = tid >> 6;
-    const int wm = wave & 1, wn = wave >> 1;
+    const int wm = BM == 128 ? (wave & 1) : 0, wn = BM == 128 ? (wave >> 1) : wave;
 
-    if (tid < kQgBM) {
+    if (tid < BM) {
         const int m = m0 + tid;
         int arow = -1;
         float sc = 0.0f;
@@ -274,46 +285,62 @@ __global__ __launch_bounds__(256, 1) void qgemm_kernel(QGemmLaunch L) {
     const long w_row_bytes = FMT == kQ8 ? tk.k : tk.k / 2;
     const uint8_t *const w_gate = tk.w;
     const uint8_t *const w_up = tk.w2;
-    // weight row held by LDS B row j: SwiGLU tiles put gate rows in blocks
-    // f = 0, 1 and the matching up rows in blocks f = 2, 3 of each wave half
+    // output / weight row held by LDS B row j: SwiGLU tiles give each wave
+    // its gate blocks and then the matching up blocks (BM = 128: blocks
+    // f = 0, 1 gate, 2, 3 up of a 128-row wave half; BM = 32: block 0 gate,
+    // 1 up of a 64-row wave quarter)
+    auto b_out = [&](int j, bool &up) -> int {
+        if (!DUAL) {
+            up = false;
+            return n0 + j;
+        }
+        if (BM == 128) {
+            const int f = (j >> 5) & 3;
+            up = f >= 2;
+            return n0 + (j >> 7) * 64 + (f & 1) * 32 + (j & 31);
+        }
+        up = ((j >> 5) & 1) != 0;
+        return n0 + (j >> 6) * 32 + (j & 31);
+    };
     auto b_row_src = [&](int j) -> const uint8_t * {
-        const int f = (j >> 5) & 3;
-        const int out = DUAL ? n0 + (j >> 7) * 64 + (f & 1) * 32 + (j & 31) : n0 + j;
-        const uint8_t *base = (DUAL && f >= 2) ? w_up : w_gate;
-        return base + (long)(out < tk.n_out ? out : 0) * w_row_bytes;
+        bool up;
+        const int out = b_out(j, up);
+        return (up ? w_up : w_gate) + (long)(out < tk.n_out ? out : 0) * w_row_bytes;
     };
     auto a_row_src = [&](int limb, int r) -> const int8_t * {
         const int arow = lds_arow[r] >= 0 ? lds_arow[r] : lds_arow[0];
         return (limb ? tk.a_lo : tk.a_hi) + (long)arow * tk.a_stride;
     };
 
-    // DMA path (q8, 64-byte rows): wave w issues 8 blocks of 1 KB per slice:
-    // A blocks (limb h / 2, rows (w + 4 (h % 2)) * 16 + l / 4) for h = 0..3
-    // and B blocks (rows (w + 4 q) * 16 + l / 4) for q = 0..3; lane l fills LDS
-    // row (block row 0 + l / 4), physical chunk l % 4, so it loads the logical
-    // chunk (l % 4) ^ g(row).  Both limbs share a lane's two A rows.
+    // DMA path (q8, 64-byte rows), blocks of 16 rows = 1 KB: wave w issues
+    // the A blocks (BM = 128: limb h / 2, rows (w + 4 (h % 2)) * 16 + l / 4 for
+    // h = 0..3; BM = 32: limb w / 2, rows (w % 2) * 16 + l / 4) and the B
+    // blocks (rows (w + 4 q) * 16 + l / 4) for q = 0..3; lane l fills LDS row
+    // (block row 0 + l / 4), physical chunk l % 4, so it loads the logical
+    // chunk (l % 4) ^ g(row).  Both limbs share a lane's A rows.
     const int lr = lane >> 2, lc = lane & 3;
     unsigned a_off[2] = {0u, 0u};  // byte offsets of this lane's A rows
-    // register path (q4, 64-byte rows): 4 A chunks and 2 packed B chunks
-    const int8_t *a_src[4];
-    int a_dst[4];
+    // register path (q4, 64-byte rows): BM / 32 A chunks and 2 packed B chunks
+    constexpr int kNA = BM / 32;
+    const int8_t *a_src[kNA];
+    int a_dst[kNA];
     const uint8_t *b_src[2];
     int b_dst[2];
-    u32x4 ra[4], rb[2];
+    u32x4 ra[kNA], rb[2];
     if constexpr (kDma) {
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            const int r = (wave + 4 * h) * 16 + lr;
+        for (int h = 0; h < (BM == 128 ? 2 : 1); ++h) {
+            const int r = (BM == 128 ? (wave + 4 * h) : (wave & 1)) * 16 + lr;
             const int arow = lds_arow[r] >= 0 ? lds_arow[r] : lds_arow[0];
             a_off[h] = (unsigned)(arow * tk.a_stride);
         }
     } else {
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
+        for (int q = 0; q < kNA; ++q) {
             const int c = tid + 256 * q;
-            const int limb = c >> 9, r = (c >> 2) & (kQgBM - 1), kc = c & 3;
+            const int limb = c / (4 * BM), r = (c >> 2) & (BM - 1), kc = c & 3;
             a_src[q] = a_row_src(limb, r) + kc * 16;
-            a_dst[q] = limb * (kQgBM * kRB) + lds_off<kRB>(r, kc);
+            a_dst[q] = limb * (BM * kRB) + lds_off<kRB>(r, kc);
         }
 #pragma unroll
         for (int q = 0; q < 2; ++q) {
@@ -329,8 +356,9 @@ __global__ __launch_bounds__(256, 1) void qgemm_kernel(QGemmLaunch L) {
         __attribute__((address_space(3))) int8_t *stage =
             (__attribute__((address_space(3))) int8_t *)(qg_lds + buf * kStage);
 #pragma unroll
-        for (int h = 0; h < 4; ++h) {
-            const int rb = wave + 4 * (h & 1), limb = h >> 1;
+        for (int h = 0; h < (BM == 128 ? 4 : 1); ++h) {
+            const int rb = BM == 128 ? wave + 4 * (h & 1) : (wave & 1);
+            const int limb = BM == 128 ? h >> 1 : wave >> 1;
             const int r = rb * 16 + lr;  // A row of this lane
             const int ca = lc ^ (((r >> 1) ^ (r >> 3)) & 3);
             // uniform base + 32-bit lane offset: one VGPR per address
@@ -338,15 +366,15 @@ __global__ __launch_bounds__(256, 1) void qgemm_kernel(QGemmLaunch L) {
             const unsigned aoff = a_off[h & 1] + (unsigned)(k0 + ca * 16);
             __builtin_amdgcn_global_load_lds(
                 (const __attribute__((address_space(1))) void *)(abase + aoff),
-                stage + limb * (kQgBM * kRB) + rb * 1024, 16, 0, 0);
+                stage + limb * (BM * kRB) + rb * 1024, 16, 0, 0);
         }
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
             const int bb = wave + 4 * q;
             const int j = bb * 16 + lr;  // B row of this lane
-            const int f = (j >> 5) & 3;
-            const int out = DUAL ? n0 + (j >> 7) * 64 + (f & 1) * 32 + (j & 31) : n0 + j;
-            const uint8_t *bbase = (DUAL && f >= 2) ? w_up : w_gate;
+            bool up;
+            const int out = b_out(j, up);
+            const uint8_t *bbase = up ? w_up : w_gate;
             const int cb = lc ^ (((j >> 1) ^ (j >> 3)) & 3);
             const unsigned boff =
                 (unsigned)((out < tk.n_out ? out : 0) * tk.k) + (unsigned)(k0 + cb * 16);
@@ -357,14 +385,14 @@ __global__ __launch_bounds__(256, 1) void qgemm_kernel(QGemmLaunch L) {
     };
     auto fetch = [&](int k0) {
 #pragma unroll
-        for (int q = 0; q < 4; ++q) ra[q] = load_global16(a_src[q] + k0);
+        for (int q = 0; q < kNA; ++q) ra[q] = load_global16(a_src[q] + k0);
 #pragma unroll
         for (int q = 0; q < 2; ++q) rb[q] = load_global16(b_src[q] + k0 / 2);
     };
     auto stash = [&](int buf) {
         int8_t *a = qg_lds + buf * kStage;
 #pragma unroll
-        for (int q = 0; q < 4; ++q) *reinterpret_cast<u32x4 *>(a + a_dst[q]) = ra[q];
+        for (int q = 0; q < kNA; ++q) *reinterpret_cast<u32x4 *>(a + a_dst[q]) = ra[q];
         int8_t *b = a + kLdsA;
 #pragma unroll
         for (int q = 0; q < 2; ++q) {
@@ -381,13 +409,13 @@ __global__ __launch_bounds__(256, 1) void qgemm_kernel(QGemmLaunch L) {
         }
     };
 
-    i32x16 acc[2][2][4];  // [limb][row block][weight-row block]
+    i32x16 acc[2][kMI][kNF];  // [limb][row block][weight-row block]
 #pragma unroll
     for (int a = 0; a < 2; ++a)
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
+        for (int i = 0; i < kMI; ++i)
 #pragma unroll
-            for (int f = 0; f < 4; ++f)
+            for (int f = 0; f < kNF; ++f)
 #pragma unroll
                 for (int r = 0; r < 16; ++r) acc[a][i][f][r] = 0;
 
@@ -397,30 +425,30 @@ __global__ __launch_bounds__(256, 1) void qgemm_kernel(QGemmLaunch L) {
     // the LDS latency overlaps the MFMAs
     auto compute_pair = [&](int buf, int ksub0) {
         const int8_t *ah = qg_lds + buf * kStage;
-        const int8_t *al = ah + kQgBM * kRB;
+        const int8_t *al = ah + BM * kRB;
         const int8_t *bb = ah + kLdsA;
-        i32x4 fa_h[2][2], fa_l[2][2], fb[2][4];
+        i32x4 fa_h[2][kMI], fa_l[2][kMI], fb[2][kNF];
 #pragma unroll
         for (int s2 = 0; s2 < 2; ++s2) {
             const int chunk = (ksub0 + s2) * 2 + half;
 #pragma unroll
-            for (int i = 0; i < 2; ++i) {
-                const int row = wm * 64 + i * 32 + frow;
+            for (int i = 0; i < kMI; ++i) {
+                const int row = wm * (kMI * 32) + i * 32 + frow;
                 fa_h[s2][i] = *reinterpret_cast<const i32x4 *>(ah + lds_off<kRB>(row, chunk));
                 fa_l[s2][i] = *reinterpret_cast<const i32x4 *>(al + lds_off<kRB>(row, chunk));
             }
 #pragma unroll
-            for (int f = 0; f < 4; ++f) {
-                const int row = wn * 128 + f * 32 + frow;
+            for (int f = 0; f < kNF; ++f) {
+                const int row = wn * (kNF * 32) + f * 32 + frow;
                 fb[s2][f] = *reinterpret_cast<const i32x4 *>(bb + lds_off<kRB>(row, chunk));
             }
         }
 #pragma unroll
         for (int s2 = 0; s2 < 2; ++s2)
 #pragma unroll
-            for (int i = 0; i < 2; ++i)
+            for (int i = 0; i < kMI; ++i)
 #pragma unroll
-                for (int f = 0; f < 4; ++f) {
+                for (int f = 0; f < kNF; ++f) {
                     acc[0][i][f] = __builtin_amdgcn_mfma_i32_32x32x32_i8(
                         fa_h[s2][i], fb[s2][f], acc[0][i][f], 0, 0, 0);
                     acc[1][i][f] = __builtin_amdgcn_mfma_i32_32x32x32_i8(
@@ -429,26 +457,28 @@ __global__ __launch_bounds__(256, 1) void qgemm_kernel(QGemmLaunch L) {
     };
 
     if constexpr (kDma) {
-        // four stages: slices ks + 1 .. ks + 3 stream into LDS while slice ks
-        // is multiplied.  A wave's DMA completes in order, 8 instructions per
-        // slice, so slice ks has landed when at most 8 per later slice in
-        // flight remain; the barrier after the wait makes every wave's part
-        // visible and frees the stage of slice ks - 1 for slice ks + 3.
+        // kStages stages: slices ks + 1 .. ks + kStages - 1 stream into LDS
+        // while slice ks is multiplied.  A wave's DMA completes in order,
+        // kDmaPerSlice instructions per slice, so slice ks has landed when at
+        // most that many per later slice in flight remain; the barrier after
+        // the wait makes every wave's part visible and frees the stage of
+        // slice ks - 1 for slice ks + kStages - 1.
+        constexpr int NPS = Sh::kDmaPerSlice;
         const int nk = tk.k / kRB;  // k % 64 == 0 (qgemm_shape_ok)
-        for (int st = 0; st < 3 && st < nk; ++st) issue_dma(st * kRB, st);
+        for (int st = 0; st < kStages - 1 && st < nk; ++st) issue_dma(st * kRB, st);
         for (int ks = 0; ks < nk; ++ks) {
             const int later = nk - 1 - ks;
-            if (later >= 2)
-                wait_vmcnt<16>();
-            else if (later == 1)
-                wait_vmcnt<8>();
+            if (kStages >= 4 && later >= 2)
+                wait_vmcnt<2 * NPS>();
+            else if (later >= 1)
+                wait_vmcnt<NPS>();
             else
                 wait_vmcnt<0>();
             // a bare barrier: __syncthreads() would also wait for the stores
             // and loads of the fence it implies
             __builtin_amdgcn_s_barrier();
-            if (ks + 3 < nk) issue_dma((ks + 3) * kRB, (ks + 3) & 3);
-            compute_pair(ks & 3, 0);
+            if (ks + kStages - 1 < nk) issue_dma((ks + kStages - 1) * kRB, (ks + kStages - 1) % kStages);
+            compute_pair(ks % kStages, 0);
         }
     } else {
         // two buffers: slice ks + 2 is in registers while slice ks is multiplied
@@ -471,23 +501,23 @@ __global__ __launch_bounds__(256, 1) void qgemm_kernel(QGemmLaunch L) {
     // residual rows) is loaded before the first store: the stores may alias
     // them as far as the compiler knows, so a load after a store would wait
     // for it.
-    constexpr int kF = DUAL ? 2 : 4;
+    constexpr int kF = DUAL ? kNF / 2 : kNF;
     float sw[kF], su[kF];
     int ncol[kF];
 #pragma unroll
     for (int f = 0; f < kF; ++f) {
-        ncol[f] = DUAL ? n0 + wn * 64 + f * 32 + frow : n0 + wn * 128 + f * 32 + frow;
+        ncol[f] = n0 + wn * kF * 32 + f * 32 + frow;
         const bool ok = ncol[f] < tk.n_out;
         sw[f] = ok ? load_global_f32(tk.s + ncol[f]) : 0.0f;
         su[f] = (DUAL && ok) ? load_global_f32(tk.s2 + ncol[f]) : 0.0f;
     }
-    // row scales of the 32 result rows this lane holds
-    float sxr[2][16];
+    // row scales of the result rows this lane holds
+    float sxr[kMI][16];
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < kMI; ++i)
 #pragma unroll
         for (int r = 0; r < 16; ++r)
-            sxr[i][r] = lds_scale[wm * 64 + i * 32 + (r >> 2) * 8 + half * 4 + (r & 3)];
+            sxr[i][r] = lds_scale[wm * (kMI * 32) + i * 32 + (r >> 2) * 8 + half * 4 + (r & 3)];
     // complete the scale loads now: stores share the vector-memory counter,
     // so a wait placed after the first store would also wait for the stores
     __builtin_amdgcn_s_waitcnt(0);
@@ -496,7 +526,7 @@ __global__ __launch_bounds__(256, 1) void qgemm_kernel(QGemmLaunch L) {
     auto epilogue = [&](auto with_resid) {
         constexpr bool kResid = decltype(with_resid)::value;
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
+        for (int i = 0; i < kMI; ++i) {
 #pragma unroll
             for (int rg = 0; rg < 16; rg += 4) {
                 // residual inputs of 4 result registers, loaded before their stores
@@ -504,7 +534,7 @@ __global__ __launch_bounds__(256, 1) void qgemm_kernel(QGemmLaunch L) {
                 if (kResid) {
 #pragma unroll
                     for (int r = rg; r < rg + 4; ++r) {
-                        const int m = m0 + wm * 64 + i * 32 + (r >> 2) * 8 + half * 4 + (r & 3);
+                        const int m = m0 + wm * (kMI * 32) + i * 32 + (r >> 2) * 8 + half * 4 + (r & 3);
 #pragma unroll
                         for (int f = 0; f < kF; ++f)
                             res[r - rg][f] = (m < tk.rows && ncol[f] < tk.n_out)
@@ -516,24 +546,24 @@ __global__ __launch_bounds__(256, 1) void qgemm_kernel(QGemmLaunch L) {
                 }
 #pragma unroll
                 for (int r = rg; r < rg + 4; ++r) {
-                    const int m = m0 + wm * 64 + i * 32 + (r >> 2) * 8 + half * 4 + (r & 3);
+                    const int m = m0 + wm * (kMI * 32) + i * 32 + (r >> 2) * 8 + half * 4 + (r & 3);
                     if (m >= tk.rows) continue;
                     const float sx = sxr[i][r];
                     float *yrow = tk.y + (long)m * tk.y_stride;
                     if (DUAL) {
 #pragma unroll
-                        for (int f = 0; f < 2; ++f) {
+                        for (int f = 0; f < kF; ++f) {
                             if (ncol[f] < tk.n_out) {
                                 const float g = ((float)acc[0][i][f][r] * 256.0f +
                                                  (float)acc[1][i][f][r]) * sx * sw[f];
-                                const float u = ((float)acc[0][i][f + 2][r] * 256.0f +
-                                                 (float)acc[1][i][f + 2][r]) * sx * su[f];
+                                const float u = ((float)acc[0][i][f + kF][r] * 256.0f +
+                                                 (float)acc[1][i][f + kF][r]) * sx * su[f];
                                 store_global(yrow + ncol[f], silu(g) * u);
                             }
                         }
                     } else {
 #pragma unroll
-                        for (int f = 0; f < 4; ++f) {
+                        for (int f = 0; f < kF; ++f) {
                             if (ncol[f] < tk.n_out) {
                                 float v = ((float)acc[0][i][f][r] * 256.0f +
                                            (float)acc[1][i][f][r]) * sx * sw[f];
@@ -550,37 +580,44 @@ __global__ __launch_bounds__(256, 1) void qgemm_kernel(QGemmLaunch L) {
     else epilogue(std::false_type{});
 }
 
-template <int FMT, bool DUAL>
+template <int FMT, bool DUAL, int BM>
 static void launch_qgemm(const QGemmLaunch &L, int grid, hipStream_t stream) {
+    constexpr int kLds = QgShape<FMT, BM>::kLds;
     static const bool attr = [] {
-        return hipFuncSetAttribute(reinterpret_cast<const void *>(&qgemm_kernel<FMT, DUAL>),
+        return hipFuncSetAttribute(reinterpret_cast<const void *>(&qgemm_kernel<FMT, DUAL, BM>),
                                    hipFuncAttributeMaxDynamicSharedMemorySize,
-                                   qg_lds_bytes<FMT>()) == hipSuccess;
+                                   kLds) == hipSuccess;
     }();
     (void)attr;
-    hipLaunchKernelGGL((qgemm_kernel<FMT, DUAL>), dim3((unsigned)grid), dim3(256),
-                       qg_lds_bytes<FMT>(), stream, L);
+    hipLaunchKernelGGL((qgemm_kernel<FMT, DUAL, BM>), dim3((unsigned)grid), dim3(256), kLds,
+                       stream, L);
 }
 
-static int launch_qgemm_fmt(int fmt, bool dual, const QGemmLaunch &L, int tiles_bound,
+template <int BM>
+static void launch_qgemm_bm(int fmt, bool dual, const QGemmLaunch &L, int grid,
+                            hipStream_t stream) {
+    if (fmt == kQ8) {
+        if (dual) launch_qgemm<kQ8, true, BM>(L, grid, stream);
+        else launch_qgemm<kQ8, false, BM>(L, grid, stream);
+    } else {
+        if (dual) launch_qgemm<kQ4, true, BM>(L, grid, stream);
+        else launch_qgemm<kQ4, false, BM>(L, grid, stream);
+    }
+}
+
+static int launch_qgemm_fmt(int fmt, bool dual, int bm, const QGemmLaunch &L, int tiles_bound,
                             hipStream_t stream) {
     if (tiles_bound <= 0) return kOk;
+    if ((fmt != kQ8 && fmt != kQ4) || (bm != kQgBM && bm != kQgBMSmall)) return kErrArgs;
     const int grid = ((tiles_bound + 7) / 8) * 8;
-    if (fmt == kQ8) {
-        if (dual) launch_qgemm<kQ8, true>(L, grid, stream);
-        else launch_qgemm<kQ8, false>(L, grid, stream);
-    } else if (fmt == kQ4) {
-        if (dual) launch_qgemm<kQ4, true>(L, grid, stream);
-        else launch_qgemm<kQ4, false>(L, grid, stream);
-    } else {
-        return kErrArgs;
-    }
+    if (bm == kQgBM) launch_qgemm_bm<kQgBM>(fmt, dual, L, grid, stream);
+    else launch_qgemm_bm<kQgBMSmall>(fmt, dual, L, grid, stream);
     return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
 }
 
-static int host_tiles(bool dual, int rows, int n_out) {
+static int host_tiles(bool dual, int rows, int n_out, int bm) {
     const int outw = dual ? kQgBW / 2 : kQgBW;
-    return ((rows + kQgBM - 1) / kQgBM) * ((n_out + outw - 1) / outw);
+    return ((rows + bm - 1) / bm) * ((n_out + outw - 1) / outw);
 }
 
 int qgemm_single(int fmt, bool dual, const GemmTask &task, hipStream_t stream) {
@@ -590,7 +627,10 @@ int qgemm_single(int fmt, bool dual, const GemmTask &task, hipStream_t stream) {
         return kErrArgs;
     QGemmLaunch L;
     L.single = task;
-    return launch_qgemm_fmt(fmt, dual, L, host_tiles(dual, task.rows, task.n_out), stream);
+    // few rows: the 32-row tile spends a quarter of the MFMA work per weight byte
+    const int bm = task.rows <= 2 * kQgBMSmall ? kQgBMSmall : kQgBM;
+    return launch_qgemm_fmt(fmt, dual, bm, L, host_tiles(dual, task.rows, task.n_out, bm),
+                            stream);
 }
 
 // ---------------------------------------------------------------------------
@@ -599,10 +639,12 @@ int qgemm_single(int fmt, bool dual, const GemmTask &task, hipStream_t stream) {
 
 struct MoeScheduleParams {
     MoeGemmParams p;
+    int bm;  // token rows per tile of the launches that read the tables
 };
 
 __global__ __launch_bounds__(256) void moe_schedule_kernel(MoeScheduleParams sp) {
     const MoeGemmParams &p = sp.p;
+    const bool small = sp.bm == kQgBMSmall;
     __shared__ int tiles[2][kQgMaxTasks];
     const int nr = *p.n_unique;
     GemmTask *t0 = p.tasks;
@@ -627,7 +669,8 @@ __global__ __launch_bounds__(256) void moe_schedule_kernel(MoeScheduleParams sp)
         a.y = p.expert_hidden + (long)off * p.inter;
         a.y_stride = p.inter;
         t0[u] = a;
-        tiles[0][u] = tiles_of<true>(cnt, p.inter);
+        tiles[0][u] = small ? tiles_of<true, kQgBMSmall>(cnt, p.inter)
+                            : tiles_of<true, kQgBM>(cnt, p.inter);
         GemmTask b;
         b.w = ew.down;
         b.s = ew.down_s;
@@ -641,7 +684,8 @@ __global__ __launch_bounds__(256) void moe_schedule_kernel(MoeScheduleParams sp)
         b.y = p.expert_out + (long)off * p.hidden;
         b.y_stride = p.hidden;
         t1[u] = b;
-        tiles[1][u] = tiles_of<false>(cnt, p.hidden);
+        tiles[1][u] = small ? tiles_of<false, kQgBMSmall>(cnt, p.hidden)
+                            : tiles_of<false, kQgBM>(cnt, p.hidden);
     }
     if (threadIdx.x == 0) {
         tiles[0][nr] = 0;
@@ -662,7 +706,8 @@ __global__ __launch_bounds__(256) void moe_schedule_kernel(MoeScheduleParams sp)
             a.y = p.shared_hidden;
             a.y_stride = p.shared_width;
             t0[nr] = a;
-            tiles[0][nr] = tiles_of<true>(p.rows, p.shared_width);
+            tiles[0][nr] = small ? tiles_of<true, kQgBMSmall>(p.rows, p.shared_width)
+                                 : tiles_of<true, kQgBM>(p.rows, p.shared_width);
             GemmTask b;
             b.w = p.shared_down;
             b.s = p.shared_down_s;
@@ -676,7 +721,8 @@ __global__ __launch_bounds__(256) void moe_schedule_kernel(MoeScheduleParams sp)
             b.y = p.shared_out;
             b.y_stride = p.hidden;
             t1[nr] = b;
-            tiles[1][nr] = tiles_of<false>(p.rows, p.hidden);
+            tiles[1][nr] = small ? tiles_of<false, kQgBMSmall>(p.rows, p.hidden)
+                                 : tiles_of<false, kQgBM>(p.rows, p.hidden);
         }
     }
     __syncthreads();
@@ -701,13 +747,16 @@ int moe_gemm(const MoeGemmParams &p, hipStream_t stream) {
     int st = quantize_activations(p.x, p.hidden, p.rows, p.hidden, p.norm_w, p.eps, p.xq_hi,
                                   p.xq_lo, p.xq_scale, stream);
     if (st) return st;
+    const int entries = p.rows * p.top_k;
+    const int max_tasks = entries < p.experts ? entries : p.experts;
+    // experts holding about 32 rows or fewer on average: 32-row tiles
+    const int bm = entries <= kQgBMSmall * p.experts ? kQgBMSmall : kQgBM;
     MoeScheduleParams sp;
     sp.p = p;
+    sp.bm = bm;
     hipLaunchKernelGGL(moe_schedule_kernel, dim3(1), dim3(256), 0, stream, sp);
     if (hipGetLastError() != hipSuccess) return kErrLaunch;
 
-    const int entries = p.rows * p.top_k;
-    const int max_tasks = entries < p.experts ? entries : p.experts;
     const bool same = !p.has_shared || p.shared_fmt == p.expert_fmt;
     for (int stage = 0; stage < 2; ++stage) {
         const bool dual = stage == 0;
@@ -716,19 +765,20 @@ int moe_gemm(const MoeGemmParams &p, hipStream_t stream) {
         L.tile_start = p.tile_start + stage * (kQgMaxTasks + 1);
         L.n_routed = p.n_unique;
         // upper bounds of the tile counts: sum_e ceil(n_e / BM) <= entries / BM + tasks
-        const int routed_mt = entries / kQgBM + max_tasks;
-        const int routed_nt = host_tiles(dual, 1, dual ? p.inter : p.hidden);
+        const int routed_mt = entries / bm + max_tasks;
+        const int routed_nt = host_tiles(dual, 1, dual ? p.inter : p.hidden, bm);
         const int shared_t =
-            p.has_shared ? host_tiles(dual, p.rows, dual ? p.shared_width : p.hidden) : 0;
+            p.has_shared ? host_tiles(dual, p.rows, dual ? p.shared_width : p.hidden, bm) : 0;
         if (same) {
             L.range = 0;
-            st = launch_qgemm_fmt(p.expert_fmt, dual, L, routed_mt * routed_nt + shared_t, stream);
+            st = launch_qgemm_fmt(p.expert_fmt, dual, bm, L, routed_mt * routed_nt + shared_t,
+                                  stream);
         } else {
             L.range = 1;
-            st = launch_qgemm_fmt(p.expert_fmt, dual, L, routed_mt * routed_nt, stream);
+            st = launch_qgemm_fmt(p.expert_fmt, dual, bm, L, routed_mt * routed_nt, stream);
             if (!st) {
                 L.range = 2;
-                st = launch_qgemm_fmt(p.shared_fmt, dual, L, shared_t, stream);
+                st = launch_qgemm_fmt(p.shared_fmt, dual, bm, L, shared_t, stream);
             }
         }
         if (st) return st;

@@ -127,7 +127,7 @@ def moon(request, device):
     model.close()
 
 
-@pytest.mark.parametrize("rows", [512, 2048])
+@pytest.mark.parametrize("rows", [64, 512, 2048])
 def test_moonlight_moe_fixed(moon, rows):
     print(f"[gpu] Moonlight MoE layer, Zipf routes, T={rows}", flush=True)
     ids = O.zipf_routes(rows, 64, 6, seed=1100 + rows)
