@@ -121,7 +121,7 @@ struct MoonlightSession {
     float *expert_hidden = nullptr, *expert_out = nullptr;
     float *shared_hidden = nullptr, *shared_out = nullptr, *dense_hidden = nullptr;
     float *moe_routed = nullptr;  // routed part of moonlight_test_moe
-    // MFMA path for batches of >= kGemmMinRows token rows (prefill)
+    // MFMA path for batches of >= kMoeGemmMinRows token rows (prefill)
     int8_t *aq_hi = nullptr, *aq_lo = nullptr;  // quantised activations [max_batch][aq_width]
     float *aq_scale = nullptr;
     int aq_width = 0;
@@ -798,8 +798,14 @@ bool to_host(MoonlightSession *s, void *dst, const void *src, size_t bytes) {
 }
 
 // Batches of at least this many token rows take the int8-MFMA GEMM (weights
-// read once per 128 rows) instead of the GEMV (once per 4 rows).
+// read once per 32 or 128 rows) instead of the GEMV (once per 4 rows).  The
+// MoE layer switches earlier: its GEMV reads each active expert once per 4
+// of that expert's rows in separate launches per stage, while the grouped
+// GEMM covers all experts in one launch per stage (measured on MI355X at
+// T = 4 .. 7: equal at 4, 96 against 112 us at 5, 106 against 129 us at 7).
+// The dense projections keep the GEMV up to 16 rows.
 constexpr int kGemmMinRows = 16;
+constexpr int kMoeGemmMinRows = 5;
 
 bool use_gemm(const MoonlightSession *s, int fmt, int rows, int in_w) {
     return rows >= kGemmMinRows && s->aq_hi && in_w <= s->aq_width && qgemm_shape_ok(fmt, in_w);
@@ -1080,7 +1086,7 @@ int experts(MoonlightSession *s, int layer, const float *x, int rows, const floa
     f.expert_out = s->expert_out;
     f.shared_hidden = s->shared_hidden;
     f.shared_out = s->shared_out;
-    const bool gemm = rows >= kGemmMinRows && s->hq_hi &&
+    const bool gemm = rows >= kMoeGemmMinRows && s->hq_hi &&
                       qgemm_shape_ok(f.expert_fmt, f.hidden) &&
                       qgemm_shape_ok(f.expert_fmt, f.inter) &&
                       qgemm_shape_ok(f.shared_fmt, f.hidden) &&
@@ -1371,7 +1377,7 @@ extern "C" int moonlight_session_create(MoonlightSession **out, MoonlightModel *
                       hipHostMallocDefault) == hipSuccess &&
         hipEventCreate(&s->ev_start) == hipSuccess && hipEventCreate(&s->ev_stop) == hipSuccess;
     bool gemm_ok = ok;
-    if (ok && options->max_batch >= kGemmMinRows) {
+    if (ok && options->max_batch >= kMoeGemmMinRows) {
         // MFMA prefill scratch: quantised activations of the widest matmul
         // input, quantised expert hidden rows, per-stage task tables
         const int widths[] = {c.hidden_size, c.head_count * c.value_dim,

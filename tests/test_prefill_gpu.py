@@ -1,15 +1,17 @@
-"""GPU parity of the prefill path: batches of >= 16 token rows run every q8/q4
-matmul on the int8-limb MFMA GEMM (floyd_amd/csrc/qgemm.hip) and route
-through the multi-workgroup routing kernels when rows * top_k > 1024.
+"""GPU parity of the prefill path: batches of >= 16 token rows (>= 5 in the
+MoE layer) run every q8/q4 matmul on the int8-limb MFMA GEMM
+(floyd_amd/csrc/qgemm.hip), in 32-row tiles where the tasks hold few rows and
+128-row tiles otherwise, and route through the multi-workgroup routing kernels
+when rows * top_k > 1024.
 
-  test_tiny_moe_gemm         one MoE layer at 40 and 200 rows, top-k routing,
+  test_tiny_moe_gemm         one MoE layer at 5, 40 and 200 rows, top-k routing,
                              three format mixes (tests/test_moonlight_metal_moe.c
                              semantics)
   test_tiny_prefill_gemm     a 40-token prefill through every GEMM path (q/kv_a,
                              o_proj, dense SwiGLU + down, experts) vs orc_forward
   test_moonlight_moe_fixed   the Moonlight MoE layer (config 3 shape) with Zipf
                              routes fixed per token (moe_route_fixed), q8 and q4,
-                             T = 512 and the full T = 2048
+                             T = 64 (32-row tiles), 512 and the full T = 2048
 
 Tolerance: rel-L2 <= 1e-3 against the fp32 oracle;
 the limb quantisation keeps the measured error near 1e-4.
@@ -39,7 +41,7 @@ def tiny(request, tmp_path_factory, device):
     model.close()
 
 
-@pytest.mark.parametrize("rows", [40, 200])
+@pytest.mark.parametrize("rows", [5, 40, 200])
 def test_tiny_moe_gemm(tiny, rows):
     cfg, tensors, model = tiny
     print(f"[gpu] tiny MoE GEMM rows={rows}", flush=True)
