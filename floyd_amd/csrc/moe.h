@@ -59,7 +59,23 @@ struct ExpertFfnParams {
     unsigned char *limb_x = nullptr, *limb_xs = nullptr;  // token rows (expert / shared fmt)
     unsigned char *limb_h = nullptr, *limb_sh = nullptr;  // list rows / shared rows
     long limb_x_stride = 0, limb_h_stride = 0, limb_sh_stride = 0;
+    // one token row (down_combine_ok): with `combine_out` set, the down
+    // projections and the combine run as one launch (moe_down_combine_kernel)
+    // and write combine_out = combine_resid + (routed + shared); moe_combine
+    // is then not needed.  route_weights / list_pos are the route tables.
+    float *combine_out = nullptr;
+    const float *combine_resid = nullptr;  // optional
+    float *combine_routed = nullptr;       // optional copy of the routed sum
+    float *combine_shared = nullptr;       // optional copy of the shared expert output
+    const float *route_weights = nullptr;
+    const int *list_pos = nullptr;
 };
+
+// Whether a one-row layer of this shape can take the fused down + combine
+// launch: one format for routed and shared experts, shared width a multiple
+// of the expert width, at most 16 units (top_k + shared_width / inter), an
+// expert row of at most kDownCombineChunks 16-byte chunks per lane group.
+bool down_combine_ok(const ExpertFfnParams &f);
 int expert_ffn(const ExpertFfnParams &f, hipStream_t stream);
 
 int rmsnorm_rows(const float *x, const float *w, float *y, int rows, int width, float eps,

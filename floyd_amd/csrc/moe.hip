@@ -629,6 +629,166 @@ int moe_combine(const CombineParams &p, hipStream_t stream) {
     return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
 }
 
+// One-row MoE layer: the down projections and the combine in one launch.
+// out = resid + (sum over slots k of w_k * down_k(h_k) + down_sh(h_sh)), the
+// routed sum in slot order as in combine_kernel.  Workgroup over RPB output
+// rows, one wave per unit: unit k < top_k is slot k's expert (list entry
+// list_pos[k], weights from the task table), unit top_k + j the j-th
+// inter-wide column slice of the shared down projection.  A wave splits its
+// own input vector into limbs in its LDS row (per-chunk scales, as in the
+// GEMV), multiplies its RPB x inter weight block (64 / RPB lanes per row, NJ
+// chunks per lane, all loads issued first), and the units' rows meet in LDS.
+constexpr int kDownCombineRows = 4;    // output rows per workgroup
+constexpr int kDownCombineChunks = 6;  // 16-byte chunks per lane and row (q8: inter <= 1536)
+constexpr int kDownCombineMaxUnits = 16;
+
+struct DownCombineParams {
+    int hidden = 0, inter = 0, top_k = 0, units = 0, shared_width = 0;
+    const ExpertTask *tasks = nullptr;
+    const int *list_pos = nullptr;
+    const float *weights = nullptr;
+    const float *expert_hidden = nullptr;  // [top_k][inter] list entries
+    const float *shared_hidden = nullptr;  // [shared_width]
+    const uint8_t *shared_down = nullptr;
+    const float *shared_down_s = nullptr;
+    const float *resid = nullptr;
+    float *routed_copy = nullptr, *shared_copy = nullptr;
+    float *out = nullptr;
+};
+
+template <int FMT, int RPB, int NJ>
+__global__ __launch_bounds__(1024) void moe_down_combine_kernel(DownCombineParams p) {
+    extern __shared__ __align__(16) unsigned char dc_lds[];
+    constexpr int LPR = 64 / RPB;
+    __shared__ float part[kDownCombineMaxUnits][RPB];
+    const int lane = threadIdx.x & 63;
+    const int u = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int rr = lane / LPR, li = lane % LPR;
+    const int d0 = blockIdx.x * RPB;
+    const int row = d0 + rr < p.hidden ? d0 + rr : p.hidden - 1;
+    const int I = p.inter;
+    const int nc = row_bytes_of(FMT, I) / 16;
+    // ---- the unit: weights, row stride, scales, input vector
+    const uint8_t *w;
+    const float *s, *x;
+    long stride;
+    bool active = true;
+    if (u < p.top_k) {
+        const int pos = p.list_pos[u];
+        active = pos >= 0;
+        const ExpertTask tk = p.tasks[active ? pos : 0];
+        w = tk.w.down;
+        s = tk.w.down_s;
+        stride = row_bytes_of(FMT, I);
+        x = p.expert_hidden + (long)(active ? pos : 0) * I;
+    } else {
+        const int j = u - p.top_k;
+        w = p.shared_down + (long)j * row_bytes_of(FMT, I);
+        s = p.shared_down_s;
+        stride = row_bytes_of(FMT, p.shared_width);
+        x = p.shared_hidden + (long)j * I;
+    }
+    // ---- weights first (clamped addresses, zero past the row end)
+    u32x4 wv[NJ];
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+        const int c = li + LPR * j;
+        const u32x4 v = load_stream16(w + (long)row * stride + (c < nc ? c : 0) * 16);
+        wv[j] = c < nc ? v : u32x4{0u, 0u, 0u, 0u};
+    }
+    const float sw = load_global_f32(s + row);
+    // ---- this wave's input vector into limbs
+    unsigned char *my = dc_lds + u * limb_row_lds(FMT, I);
+    for (int e0 = lane * 8; e0 - lane * 8 < I; e0 += 64 * 8) {
+        const bool in = e0 < I;
+        const int ec = in ? e0 : 0;
+        const f32x4 a = load_f4(x + ec), b = load_f4(x + ec + 4);
+        const float v[8] = {in ? a.x : 0.f, in ? a.y : 0.f, in ? a.z : 0.f, in ? a.w : 0.f,
+                            in ? b.x : 0.f, in ? b.y : 0.f, in ? b.z : 0.f, in ? b.w : 0.f};
+        limb_quantise<FMT>(v, in, e0, my, I, nc);
+    }
+    __syncthreads();
+    // ---- the wave's RPB rows
+    float acc = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+        const int c = li + LPR * j;
+        if (c < nc) {
+            const LimbInfo info = reinterpret_cast<const LimbInfo *>(my + 3 * I)[c];
+            acc = fmaf(limb_chunk_dot<FMT>(wv[j], my, I, nc, c, info), info.scale, acc);
+        }
+    }
+#pragma unroll
+    for (int o = LPR / 2; o > 0; o >>= 1) acc += __shfl_xor(acc, o, kWave);
+    if (li == 0) part[u][rr] = active ? acc * sw : 0.0f;
+    __syncthreads();
+    if ((int)threadIdx.x < RPB && d0 + (int)threadIdx.x < p.hidden) {
+        const int t = threadIdx.x, d = d0 + t;
+        float routed = 0.0f;
+        for (int k = 0; k < p.top_k; ++k) routed += p.weights[k] * part[k][t];
+        float shared = 0.0f;
+        for (int k = p.top_k; k < p.units; ++k) shared += part[k][t];
+        if (p.routed_copy) p.routed_copy[d] = routed;
+        if (p.shared_copy) p.shared_copy[d] = shared;
+        float out = routed + shared;
+        if (p.resid) out = p.resid[d] + out;
+        p.out[d] = out;
+    }
+}
+
+bool down_combine_ok(const ExpertFfnParams &f) {
+    if (f.rows != 1 || !f.has_shared || f.expert_fmt != f.shared_fmt ||
+        (f.expert_fmt != kQ8 && f.expert_fmt != kQ4) || f.limb_x || !f.tasks || f.inter <= 0 ||
+        f.shared_width % f.inter || f.top_k < 1 || f.hidden <= 0)
+        return false;
+    const int epc = f.expert_fmt == kQ8 ? 16 : 32;
+    if (f.inter % epc) return false;
+    const int units = f.top_k + f.shared_width / f.inter;
+    const int nc = row_bytes_of(f.expert_fmt, f.inter) / 16;
+    return units <= kDownCombineMaxUnits &&
+           nc <= (64 / kDownCombineRows) * kDownCombineChunks &&
+           units * limb_row_lds(f.expert_fmt, f.inter) <= 96 * 1024;
+}
+
+static int moe_down_combine(const ExpertFfnParams &f, hipStream_t stream) {
+    DownCombineParams p;
+    p.hidden = f.hidden;
+    p.inter = f.inter;
+    p.top_k = f.top_k;
+    p.units = f.top_k + f.shared_width / f.inter;
+    p.shared_width = f.shared_width;
+    p.tasks = f.tasks;
+    p.list_pos = f.list_pos;
+    p.weights = f.route_weights;
+    p.expert_hidden = f.expert_hidden;
+    p.shared_hidden = f.shared_hidden;
+    p.shared_down = f.shared_down;
+    p.shared_down_s = f.shared_down_s;
+    p.resid = f.combine_resid;
+    p.routed_copy = f.combine_routed;
+    p.shared_copy = f.combine_shared;
+    p.out = f.combine_out;
+    const int lds = p.units * limb_row_lds(f.expert_fmt, f.inter);
+    const dim3 grid((unsigned)((f.hidden + kDownCombineRows - 1) / kDownCombineRows));
+    const dim3 block((unsigned)(64 * p.units));
+    if (f.expert_fmt == kQ8) {
+        auto *k = &moe_down_combine_kernel<kQ8, kDownCombineRows, kDownCombineChunks>;
+        static const bool attr = hipFuncSetAttribute(reinterpret_cast<const void *>(k),
+                                                     hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                     96 * 1024) == hipSuccess;
+        (void)attr;
+        hipLaunchKernelGGL(k, grid, block, lds, stream, p);
+    } else {
+        auto *k = &moe_down_combine_kernel<kQ4, kDownCombineRows, kDownCombineChunks>;
+        static const bool attr = hipFuncSetAttribute(reinterpret_cast<const void *>(k),
+                                                     hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                     96 * 1024) == hipSuccess;
+        (void)attr;
+        hipLaunchKernelGGL(k, grid, block, lds, stream, p);
+    }
+    return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
+}
+
 // Both grouped expert launches (gate/up + SwiGLU, then down).  The routed
 // experts use one format (ebits) and the shared expert possibly another
 // (dbits); one launch covers both when the formats agree.
@@ -642,7 +802,10 @@ int expert_ffn(const ExpertFfnParams &f, hipStream_t stream) {
          f.route.top_k < 1 || f.route.top_k > f.route.experts || presplit || !f.route.tasks ||
          !f.route.expert_table))
         return kErrArgs;
+    const bool fused_down = f.combine_out != nullptr;
+    if (fused_down && (!down_combine_ok(f) || !f.route_weights || !f.list_pos)) return kErrArgs;
     for (int stage = 0; stage < 2; ++stage) {
+        if (stage == 1 && fused_down) return moe_down_combine(f, stream);
         if (presplit) {
             // the stage's inputs, split once: token rows (RMSNorm'ed) for
             // stage 0, list rows and shared rows for stage 1

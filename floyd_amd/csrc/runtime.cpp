@@ -974,6 +974,16 @@ constexpr int kRouterMfmaMinRows = 256;
 // (moonlight_session_fix_routes); forward passes always route by top-k.
 // Single-row batches with at most 64 experts route inside the first expert
 // launch unless MLH_INLINE_ROUTE=0 (read once).
+// One-row MoE layers run the down projections and the combine as one launch
+// (MLH_FUSED_DOWN=0: the grouped down GEMV and a separate combine).
+static bool fused_down_enabled() {
+    static const bool v = [] {
+        const char *env = getenv("MLH_FUSED_DOWN");
+        return !env || atoi(env) != 0;
+    }();
+    return v;
+}
+
 static bool inline_route_enabled() {
     static const bool v = [] {
         const char *env = getenv("MLH_INLINE_ROUTE");
@@ -1133,8 +1143,18 @@ int experts(MoonlightSession *s, int layer, const float *x, int rows, const floa
         g.shared_hidden = f.shared_hidden;
         g.shared_out = f.shared_out;
         if (int e = moe_gemm(g, stream_of(s))) return e;
-    } else if (int e = expert_ffn(f, stream_of(s))) {
-        return e;
+    } else {
+        const bool fused_down = fused_down_enabled() && down_combine_ok(f);
+        if (fused_down) {
+            f.combine_out = out;
+            f.combine_resid = resid;
+            f.combine_routed = routed_copy;
+            f.combine_shared = routed_copy ? s->shared_out : nullptr;  // test hook reads it
+            f.route_weights = s->route_weights;
+            f.list_pos = s->list_pos;
+        }
+        if (int e = expert_ffn(f, stream_of(s))) return e;
+        if (fused_down) return kOk;
     }
     CombineParams cb;
     cb.rows = rows;
