@@ -638,8 +638,8 @@ int moe_combine(const CombineParams &p, hipStream_t stream) {
 // own input vector into limbs in its LDS row (per-chunk scales, as in the
 // GEMV), multiplies its RPB x inter weight block (64 / RPB lanes per row, NJ
 // chunks per lane, all loads issued first), and the units' rows meet in LDS.
-constexpr int kDownCombineRows = 4;    // output rows per workgroup
-constexpr int kDownCombineChunks = 6;  // 16-byte chunks per lane and row (q8: inter <= 1536)
+constexpr int kDownCombineRows = 8;     // output rows per workgroup
+constexpr int kDownCombineChunks = 11;  // 16-byte chunks per lane and row (q8: inter <= 1408)
 constexpr int kDownCombineMaxUnits = 16;
 
 struct DownCombineParams {
