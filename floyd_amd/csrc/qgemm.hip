@@ -41,15 +41,28 @@ __device__ __forceinline__ void quant_pair(float v, float inv, int &h, int &l) {
 // the row); wider rows (the 11264-wide dense down input) are read per pass.
 constexpr int kQuantRegChunks = 16;
 
+// One set of rows to quantise: x (row stride x_stride, optionally
+// RMSNorm'ed with norm_w) -> hi / lo limbs (row stride width) and scales.
+struct QuantSeg {
+    const float *x = nullptr;
+    long x_stride = 0;
+    int rows = 0, width = 0;
+    const float *norm_w = nullptr;
+    float eps = 0.0f;
+    int8_t *hi = nullptr, *lo = nullptr;
+    float *scale = nullptr;
+};
+
+// Row `row` of a segment by one wave.
 template <bool REG>
-__global__ __launch_bounds__(256) void quantize_act_kernel(const float *x, long x_stride, int rows,
-                                                           int width, const float *norm_w,
-                                                           float eps, int8_t *hi, int8_t *lo,
-                                                           float *scale) {
+__device__ __forceinline__ void quantize_row(const QuantSeg &s, int row) {
+    const float *x = s.x, *norm_w = s.norm_w;
+    const int width = s.width;
+    const float eps = s.eps;
+    int8_t *hi = s.hi, *lo = s.lo;
+    float *scale = s.scale;
     const int lane = threadIdx.x & (kWave - 1);
-    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (row >= rows) return;
-    const float *xr = x + (long)row * x_stride;
+    const float *xr = x + (long)row * s.x_stride;
     const int nchunks = (width / 4 + kWave - 1) / kWave;  // float4 chunks per lane (upper)
     f32x4 v[REG ? kQuantRegChunks : 1];
     if constexpr (REG) {
@@ -115,17 +128,50 @@ __global__ __launch_bounds__(256) void quantize_act_kernel(const float *x, long 
     }
 }
 
+// Workgroups [0, blocks_a) take 4 rows of segment a each, the rest 4 rows of
+// segment b (two segments in one launch).
+template <bool REG>
+__global__ __launch_bounds__(256) void quantize_act_kernel(QuantSeg a, QuantSeg b, int blocks_a) {
+    const bool in_b = (int)blockIdx.x >= blocks_a;
+    const QuantSeg s = in_b ? b : a;
+    const int row = ((int)blockIdx.x - (in_b ? blocks_a : 0)) * 4 + (int)(threadIdx.x >> 6);
+    if (row >= s.rows) return;
+    quantize_row<REG>(s, row);
+}
+
+static bool quant_seg_ok(const QuantSeg &s) {
+    return s.rows == 0 || (s.x && s.hi && s.lo && s.scale && s.rows > 0 && s.width > 0 &&
+                           s.width % 4 == 0 && s.x_stride % 4 == 0);
+}
+
+static int quantize_segments(const QuantSeg &a, const QuantSeg &b, hipStream_t stream) {
+    if (a.rows <= 0 || !quant_seg_ok(a) || !quant_seg_ok(b)) return kErrArgs;
+    const int blocks_a = (a.rows + 3) / 4, blocks_b = (b.rows + 3) / 4;
+    const bool reg = a.width <= kQuantRegChunks * kWave * 4 &&
+                     (b.rows == 0 || b.width <= kQuantRegChunks * kWave * 4);
+    if (reg)
+        hipLaunchKernelGGL(quantize_act_kernel<true>, dim3(blocks_a + blocks_b), dim3(256), 0,
+                           stream, a, b, blocks_a);
+    else
+        hipLaunchKernelGGL(quantize_act_kernel<false>, dim3(blocks_a + blocks_b), dim3(256), 0,
+                           stream, a, b, blocks_a);
+    return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
+}
+
 int quantize_activations(const float *x, long x_stride, int rows, int width, const float *norm_w,
                          float eps, int8_t *hi, int8_t *lo, float *scale, hipStream_t stream) {
-    if (!x || !hi || !lo || !scale || rows <= 0 || width <= 0 || width % 4 || x_stride % 4)
-        return kErrArgs;
-    if (width <= kQuantRegChunks * kWave * 4)
-        hipLaunchKernelGGL(quantize_act_kernel<true>, dim3((rows + 3) / 4), dim3(256), 0, stream,
-                           x, x_stride, rows, width, norm_w, eps, hi, lo, scale);
-    else
-        hipLaunchKernelGGL(quantize_act_kernel<false>, dim3((rows + 3) / 4), dim3(256), 0, stream,
-                           x, x_stride, rows, width, norm_w, eps, hi, lo, scale);
-    return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
+    if (!x || !hi || !lo || !scale || rows <= 0 || width <= 0) return kErrArgs;
+    QuantSeg a;
+    a.x = x;
+    a.x_stride = x_stride;
+    a.rows = rows;
+    a.width = width;
+    a.norm_w = norm_w;
+    a.eps = eps;
+    a.hi = hi;
+    a.lo = lo;
+    a.scale = scale;
+    return quantize_segments(a, QuantSeg{}, stream);
 }
 
 // ---------------------------------------------------------------------------
@@ -642,7 +688,7 @@ struct MoeScheduleParams {
     int bm;  // token rows per tile of the launches that read the tables
 };
 
-__global__ __launch_bounds__(256) void moe_schedule_kernel(MoeScheduleParams sp) {
+__device__ __forceinline__ void moe_schedule_body(const MoeScheduleParams &sp) {
     const MoeGemmParams &p = sp.p;
     const bool small = sp.bm == kQgBMSmall;
     __shared__ int tiles[2][kQgMaxTasks];
@@ -738,15 +784,27 @@ __global__ __launch_bounds__(256) void moe_schedule_kernel(MoeScheduleParams sp)
     }
 }
 
+// The token-row quantisation of the MoE input (RMSNorm'ed) and, in the last
+// workgroup, the GEMM task and tile tables: one launch before stage 0.
+template <bool REG>
+__global__ __launch_bounds__(256) void moe_prep_kernel(QuantSeg a, MoeScheduleParams sp,
+                                                       int blocks_a) {
+    if ((int)blockIdx.x == blocks_a) {
+        moe_schedule_body(sp);
+        return;
+    }
+    const int row = (int)blockIdx.x * 4 + (int)(threadIdx.x >> 6);
+    if (row >= a.rows) return;
+    quantize_row<REG>(a, row);
+}
+
+
 int moe_gemm(const MoeGemmParams &p, hipStream_t stream) {
     if (p.rows <= 0 || p.experts <= 0 || p.experts + 1 > kQgMaxTasks || p.top_k <= 0 ||
         !qgemm_shape_ok(p.expert_fmt, p.hidden) || !qgemm_shape_ok(p.expert_fmt, p.inter) ||
         (p.has_shared && (!qgemm_shape_ok(p.shared_fmt, p.hidden) ||
                           !qgemm_shape_ok(p.shared_fmt, p.shared_width))))
         return kErrArgs;
-    int st = quantize_activations(p.x, p.hidden, p.rows, p.hidden, p.norm_w, p.eps, p.xq_hi,
-                                  p.xq_lo, p.xq_scale, stream);
-    if (st) return st;
     const int entries = p.rows * p.top_k;
     const int max_tasks = entries < p.experts ? entries : p.experts;
     // experts holding at most 80 rows on average take 32-row tiles: measured
@@ -756,8 +814,28 @@ int moe_gemm(const MoeGemmParams &p, hipStream_t stream) {
     MoeScheduleParams sp;
     sp.p = p;
     sp.bm = bm;
-    hipLaunchKernelGGL(moe_schedule_kernel, dim3(1), dim3(256), 0, stream, sp);
+    // token rows (RMSNorm'ed) into limbs, and the task / tile tables in the
+    // launch's last workgroup
+    QuantSeg xs;
+    xs.x = p.x;
+    xs.x_stride = p.hidden;
+    xs.rows = p.rows;
+    xs.width = p.hidden;
+    xs.norm_w = p.norm_w;
+    xs.eps = p.eps;
+    xs.hi = p.xq_hi;
+    xs.lo = p.xq_lo;
+    xs.scale = p.xq_scale;
+    if (!p.x || !p.xq_hi || !p.xq_lo || !p.xq_scale || !quant_seg_ok(xs)) return kErrArgs;
+    const int blocks_x = (p.rows + 3) / 4;
+    if (p.hidden <= kQuantRegChunks * kWave * 4)
+        hipLaunchKernelGGL(moe_prep_kernel<true>, dim3(blocks_x + 1), dim3(256), 0, stream, xs,
+                           sp, blocks_x);
+    else
+        hipLaunchKernelGGL(moe_prep_kernel<false>, dim3(blocks_x + 1), dim3(256), 0, stream, xs,
+                           sp, blocks_x);
     if (hipGetLastError() != hipSuccess) return kErrLaunch;
+    int st = kOk;
 
     const bool same = !p.has_shared || p.shared_fmt == p.expert_fmt;
     for (int stage = 0; stage < 2; ++stage) {
@@ -785,12 +863,25 @@ int moe_gemm(const MoeGemmParams &p, hipStream_t stream) {
         }
         if (st) return st;
         if (stage == 0) {
-            st = quantize_activations(p.expert_hidden, p.inter, entries, p.inter, nullptr, 0.0f,
-                                      p.hq_hi, p.hq_lo, p.hq_scale, stream);
-            if (!st && p.has_shared)
-                st = quantize_activations(p.shared_hidden, p.shared_width, p.rows,
-                                          p.shared_width, nullptr, 0.0f, p.sq_hi, p.sq_lo,
-                                          p.sq_scale, stream);
+            // the expert hidden rows and the shared hidden rows in one launch
+            QuantSeg hs, ss;
+            hs.x = p.expert_hidden;
+            hs.x_stride = p.inter;
+            hs.rows = entries;
+            hs.width = p.inter;
+            hs.hi = p.hq_hi;
+            hs.lo = p.hq_lo;
+            hs.scale = p.hq_scale;
+            if (p.has_shared) {
+                ss.x = p.shared_hidden;
+                ss.x_stride = p.shared_width;
+                ss.rows = p.rows;
+                ss.width = p.shared_width;
+                ss.hi = p.sq_hi;
+                ss.lo = p.sq_lo;
+                ss.scale = p.sq_scale;
+            }
+            st = quantize_segments(hs, ss, stream);
             if (st) return st;
         }
     }
