@@ -66,6 +66,11 @@ int qgemm_single(int fmt, bool dual, const GemmTask &task, hipStream_t stream);
 // and runs both expert stages for all active experts plus the shared expert.
 struct MoeGemmParams {
     int rows = 0, experts = 0, top_k = 0, hidden = 0, inter = 0, shared_width = 0;
+    // with route_in_prep (rows <= kRouteOneGroupRows, experts <= 64 not
+    // required): the routing of the batch from route.logits and its tables
+    // run in the first launch (no routing launch before moe_gemm)
+    int route_in_prep = 0;
+    RouteParams route;
     int expert_fmt = kQ8, shared_fmt = kQ8, has_shared = 1;
     const ExpertWeights *expert_table = nullptr;
     const uint8_t *shared_gate = nullptr, *shared_up = nullptr, *shared_down = nullptr;

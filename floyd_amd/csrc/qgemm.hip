@@ -790,6 +790,16 @@ template <bool REG>
 __global__ __launch_bounds__(256) void moe_prep_kernel(QuantSeg a, MoeScheduleParams sp,
                                                        int blocks_a) {
     if ((int)blockIdx.x == blocks_a) {
+        if (sp.p.route_in_prep) {
+            // route_kernel's work: selection per row, then the route tables
+            // (read back below after the barrier, as the next launch would)
+            __shared__ RouteLds L;
+            const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+            for (int r = wave; r < sp.p.route.rows; r += 4) route_any(sp.p.route, r, lane, L.ids);
+            __syncthreads();
+            small_tables(sp.p.route, L);
+            __syncthreads();
+        }
         moe_schedule_body(sp);
         return;
     }
@@ -827,6 +837,14 @@ int moe_gemm(const MoeGemmParams &p, hipStream_t stream) {
     xs.lo = p.xq_lo;
     xs.scale = p.xq_scale;
     if (!p.x || !p.xq_hi || !p.xq_lo || !p.xq_scale || !quant_seg_ok(xs)) return kErrArgs;
+    if (p.route_in_prep &&
+        (p.route.rows != p.rows || p.rows > kRouteOneGroupRows || !p.route.logits ||
+         p.route.experts != p.experts || p.route.top_k != p.top_k || p.top_k > kMaxTopK ||
+         p.experts > kMaxExperts || p.rows * p.top_k > kRouteFusedMaxPositions ||
+         !p.route.ids || !p.route.weights || !p.route.n_unique || !p.route.unique ||
+         !p.route.counts || !p.route.offsets || !p.route.list_rows || !p.route.list_slots ||
+         !p.route.list_pos || !p.route.error))
+        return kErrArgs;
     const int blocks_x = (p.rows + 3) / 4;
     if (p.hidden <= kQuantRegChunks * kWave * 4)
         hipLaunchKernelGGL(moe_prep_kernel<true>, dim3(blocks_x + 1), dim3(256), 0, stream, xs,

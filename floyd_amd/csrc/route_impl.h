@@ -10,6 +10,8 @@
 // RouteParams) it uses.
 #pragma once
 
+#include <climits>
+
 namespace mlh {
 
 // Router score 1 / (1 + e^-x) (moe_route.h:12-14) with e^-x correctly
@@ -165,5 +167,262 @@ __device__ __forceinline__ int inline_task_expert(const RouteParams &p, int task
     ew->down_s = static_cast<const float *>(pick(mine.down_s));
     return src;
 }
+
+// ---------------------------------------------------------------------------
+// Any expert count and small batches (one workgroup): the arg-max scan, the
+// route tables.
+// ---------------------------------------------------------------------------
+
+constexpr int kMaxExperts = 256;
+constexpr int kMaxTopK = 16;
+
+// Routing of one token row by one wave: sigmoid scores, top-k selection (or
+// the given expert ids, moe_route_fixed, moe_route.h:76-87), finalised
+// weights (moe_route_finalize, moe_route.h:89-99).  Writes ids / weights /
+// trace, and the ids into lds_ids when it is non-null.
+__device__ inline void route_row(const RouteParams &p, int r, int lane, int *lds_ids) {
+    const int E = p.experts, K = p.top_k;
+    float score[kMaxExperts / 64];
+    float sel[kMaxExperts / 64];
+#pragma unroll
+    for (int j = 0; j < kMaxExperts / 64; ++j) {
+        const int e = lane + 64 * j;
+        if (e < E) {
+            score[j] = sigmoid_exact(p.logits[(long)r * E + e]);
+            sel[j] = score[j] + p.bias[e];
+        } else {
+            score[j] = 0.0f;
+            sel[j] = -INFINITY;
+        }
+    }
+    // lane k keeps the k-th id and weight; the weight sum runs in slot order
+    int my_id = -1;
+    float my_w = 0.0f, wsum = 0.0f;
+    if (p.fixed_ids) {
+        for (int k = 0; k < K; ++k) {
+            const int e = p.fixed_ids[(long)r * K + k];
+            const bool valid = e >= 0 && e < E;
+            const int owner = valid ? (e & 63) : 0, slot_j = valid ? e >> 6 : -1;
+            float chosen = 0.0f;
+#pragma unroll
+            for (int j = 0; j < kMaxExperts / 64; ++j)
+                if (lane == owner && j == slot_j) chosen = score[j];
+            const float w = __shfl(chosen, owner, 64);
+            if (lane == k) {
+                my_id = valid ? e : -1;
+                my_w = w;
+            }
+            wsum += w;
+        }
+    } else {
+        unsigned taken = 0;  // bit j: lane's expert lane + 64 j already chosen
+        for (int k = 0; k < K; ++k) {
+            // lane-local scan in increasing expert order, strict '>' keeps the
+            // lower index on ties (moe_route.h:59-71)
+            float best_v = -INFINITY;
+            int best_e = INT_MAX;
+#pragma unroll
+            for (int j = 0; j < kMaxExperts / 64; ++j) {
+                const int e = lane + 64 * j;
+                if (e < E && !(taken & (1u << j)) && sel[j] > best_v) {
+                    best_v = sel[j];
+                    best_e = e;
+                }
+            }
+            // wave arg-max: larger value wins, equal values keep the lower id
+#pragma unroll
+            for (int o = 32; o >= 1; o >>= 1) {
+                const float ov = __shfl_xor(best_v, o, 64);
+                const int oe = __shfl_xor(best_e, o, 64);
+                if (ov > best_v || (ov == best_v && oe < best_e)) {
+                    best_v = ov;
+                    best_e = oe;
+                }
+            }
+            if (best_e == INT_MAX) best_e = -1;  // only NaN scores remain
+            const int owner = best_e < 0 ? 0 : (best_e & 63), slot_j = best_e < 0 ? -1 : best_e >> 6;
+            float chosen = 0.0f;
+#pragma unroll
+            for (int j = 0; j < kMaxExperts / 64; ++j)
+                if (lane == owner && j == slot_j) {
+                    taken |= 1u << j;
+                    chosen = score[j];
+                }
+            const float w = __shfl(chosen, owner, 64);
+            if (lane == k) {
+                my_id = best_e;
+                my_w = w;
+            }
+            wsum += w;
+        }
+    }
+    if (p.normalize)
+        wsum += 1e-20f;
+    else
+        wsum = 1.0f;
+    if (lane < K) {
+        p.ids[(long)r * K + lane] = my_id;
+        if (lds_ids) lds_ids[r * K + lane] = my_id;
+        p.weights[(long)r * K + lane] = my_w / wsum * p.routed_scale;
+        if (p.trace) p.trace[(long)r * K + lane] = my_id;
+    }
+}
+
+// Any expert count: the rank form for up to 64 experts, else the arg-max scan.
+__device__ inline void route_any(const RouteParams &p, int r, int lane, int *lds_ids) {
+    if (p.experts <= 64)
+        (void)select_row_64(p, r, lane, lds_ids);
+    else
+        route_row(p, r, lane, lds_ids);
+}
+
+// Rows routed inside one workgroup (2 rows per wave); larger batches select
+// with one wave per row across many workgroups.
+constexpr int kRouteOneGroupRows = 8;
+
+// Route tables of a small batch (rows * top_k <= kRouteFusedMaxPositions,
+// ids already in LDS), built by one workgroup of 4 waves.
+constexpr int kRouteFusedMaxPositions = 1024;
+struct RouteLds {
+    int first_pos[kMaxExperts], counts[kMaxExperts], offsets[kMaxExperts];
+    int ids[kRouteFusedMaxPositions];
+    unsigned long long first_mask[kRouteFusedMaxPositions / 64];
+    int word_prefix[kRouteFusedMaxPositions / 64];
+    int rank_of[kMaxExperts], count_by_rank[kMaxExperts], offset_by_rank[kMaxExperts];
+    int unique_total;
+};
+
+// The per-task table of the grouped expert launches: entry u describes the
+// u-th active expert (weights, rows, list offset); entries up to task_slots
+// past the active experts get count 0.
+__device__ inline void write_tasks(const RouteParams &p, const int *counts, const int *offsets,
+                            const int *rank_of, int n_unique) {
+    if (!p.tasks) return;
+    for (int e = threadIdx.x; e < p.experts; e += blockDim.x) {
+        const int rk = rank_of[e];
+        if (rk >= 0 && rk < p.task_slots) store_task(p.tasks + rk, p.expert_table[e], counts[e], offsets[e]);
+    }
+    for (int u = n_unique + threadIdx.x; u < p.task_slots; u += blockDim.x)
+        store_task(p.tasks + u, ExpertWeights{}, 0, 0);
+}
+
+__device__ inline void small_tables(const RouteParams &p, RouteLds &L) {
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int E = p.experts, K = p.top_k, M = p.rows;
+    const int n_pos = M * K;
+    for (int e = tid; e < E; e += blockDim.x) {
+        L.first_pos[e] = INT_MAX;
+        L.counts[e] = 0;
+    }
+    __syncthreads();
+    // first appearance and count per expert (order-independent LDS atomics)
+    for (int q = tid; q < n_pos; q += blockDim.x) {
+        const int e = L.ids[q];
+        if (e < 0 || e >= E) {
+            p.list_pos[q] = -1;
+            *p.error = 1;  // prepare_route_tables rejects such ids (moonlight_metal.m:545)
+            continue;
+        }
+        atomicMin(&L.first_pos[e], q);
+        atomicAdd(&L.counts[e], 1);
+    }
+    __syncthreads();
+    // first-appearance ranks: a bit per list position that is the first
+    // occurrence of its expert; the rank of e counts those bits before it
+    const int nwords = (n_pos + 63) / 64;
+    for (int w = wave; w < nwords; w += 4) {
+        const int q = w * 64 + lane;
+        bool first = false;
+        if (q < n_pos) {
+            const int e = L.ids[q];
+            first = e >= 0 && e < E && L.first_pos[e] == q;
+        }
+        const unsigned long long m = __ballot(first);
+        if (lane == 0) L.first_mask[w] = m;
+    }
+    __syncthreads();
+    if (wave == 0) {  // word prefix (<= 16 words) by a wave scan
+        const int cnt = lane < nwords ? __popcll(L.first_mask[lane]) : 0;
+        int incl = cnt;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const int v = __shfl_up(incl, o, 64);
+            if (lane >= o) incl += v;
+        }
+        if (lane < nwords) L.word_prefix[lane] = incl - cnt;
+        const int total = __shfl(incl, 63, 64);
+        if (lane == 0) {
+            L.unique_total = total;
+            *p.n_unique = total;
+        }
+    }
+    __syncthreads();
+    for (int e = tid; e < E; e += blockDim.x) {
+        L.rank_of[e] = -1;
+        if (L.counts[e] > 0) {
+            const int q = L.first_pos[e];
+            const int rank = L.word_prefix[q / 64] +
+                             __popcll(L.first_mask[q / 64] & ((1ull << (q % 64)) - 1ull));
+            L.rank_of[e] = rank;
+            L.count_by_rank[rank] = L.counts[e];
+            p.unique[rank] = e;
+        }
+        p.counts[e] = L.counts[e];
+    }
+    __syncthreads();
+    if (wave == 0) {  // exclusive scan of the counts in rank order (<= 256 ranks)
+        int c4[4], local = 0;
+        const int n_unique = L.unique_total;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int rk = lane * 4 + i;
+            c4[i] = rk < n_unique ? L.count_by_rank[rk] : 0;
+            local += c4[i];
+        }
+        int incl = local;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const int v = __shfl_up(incl, o, 64);
+            if (lane >= o) incl += v;
+        }
+        int run = incl - local;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int rk = lane * 4 + i;
+            if (rk < n_unique) L.offset_by_rank[rk] = run;
+            run += c4[i];
+        }
+    }
+    __syncthreads();
+    for (int e = tid; e < E; e += blockDim.x) {
+        if (L.rank_of[e] >= 0) {
+            L.offsets[e] = L.offset_by_rank[L.rank_of[e]];
+            p.offsets[e] = L.offsets[e];
+        }
+    }
+    __syncthreads();
+    write_tasks(p, L.counts, L.offsets, L.rank_of, L.unique_total);
+    // compact lists: entries of expert e in (row, slot) order
+    for (int e = wave; e < E; e += 4) {
+        if (L.counts[e] == 0) continue;
+        int running = 0;
+        const int base = L.offsets[e];
+        for (int q0 = 0; q0 < n_pos; q0 += 64) {
+            const int q = q0 + lane;
+            const bool match = q < n_pos && L.ids[q] == e;
+            const unsigned long long mask = __ballot(match);
+            if (match) {
+                const int j = running + __popcll(mask & ((1ull << lane) - 1ull));
+                p.list_rows[base + j] = q / K;
+                p.list_slots[base + j] = q % K;
+                p.list_pos[q] = base + j;
+            }
+            running += __popcll(mask);
+        }
+    }
+}
+
 
 }  // namespace mlh

@@ -996,6 +996,18 @@ static bool inline_route_enabled() {
 // its router logits here; the selection and the route tables are left to
 // the first expert launch, which takes *inline_route (route.logits unset
 // when routing ran here).
+// Whether the MoE layer of a batch of `rows` token rows runs on the grouped
+// int8-MFMA GEMM (moe_gemm) rather than the grouped GEMV.
+static bool moe_uses_gemm(const MoonlightSession *s, int layer, int rows) {
+    const ModelConfig &c = s->model->cfg;
+    const LayerPlan &lp = s->model->layers[layer];
+    const int sw = c.moe_intermediate_size * c.shared_expert_count;
+    return rows >= kMoeGemmMinRows && s->hq_hi && qgemm_shape_ok(lp.expert_fmt, c.hidden_size) &&
+           qgemm_shape_ok(lp.expert_fmt, c.moe_intermediate_size) &&
+           qgemm_shape_ok(lp.sh_gate.fmt, c.hidden_size) && qgemm_shape_ok(lp.sh_gate.fmt, sw) &&
+           c.hidden_size <= s->aq_width && sw <= s->aq_width;
+}
+
 int route(MoonlightSession *s, int layer, const float *x, int rows, const float *norm_w,
           int *trace, bool fixed = false, RouteParams *inline_route = nullptr) {
     const ModelConfig &c = s->model->cfg;
@@ -1044,6 +1056,13 @@ int route(MoonlightSession *s, int layer, const float *x, int rows, const float 
     if (inline_route) *inline_route = RouteParams{};
     if (inline_route && inline_route_enabled() && rows == 1 && c.expert_count <= 64 &&
         rows < presplit_min_rows()) {
+        *inline_route = r;
+        return kOk;
+    }
+    // a few rows on the GEMM path: the first GEMM launch routes them
+    if (inline_route && inline_route_enabled() && rows <= kRouteOneGroupRows &&
+        rows * r.top_k <= kRouteFusedMaxPositions && r.top_k <= kMaxTopK &&
+        r.experts <= kMaxExperts && moe_uses_gemm(s, layer, rows)) {
         *inline_route = r;
         return kOk;
     }
@@ -1096,12 +1115,7 @@ int experts(MoonlightSession *s, int layer, const float *x, int rows, const floa
     f.expert_out = s->expert_out;
     f.shared_hidden = s->shared_hidden;
     f.shared_out = s->shared_out;
-    const bool gemm = rows >= kMoeGemmMinRows && s->hq_hi &&
-                      qgemm_shape_ok(f.expert_fmt, f.hidden) &&
-                      qgemm_shape_ok(f.expert_fmt, f.inter) &&
-                      qgemm_shape_ok(f.shared_fmt, f.hidden) &&
-                      qgemm_shape_ok(f.shared_fmt, f.shared_width) &&
-                      f.hidden <= s->aq_width && f.shared_width <= s->aq_width;
+    const bool gemm = moe_uses_gemm(s, layer, rows);
     if (gemm) {
         MoeGemmParams g;
         g.rows = f.rows;
@@ -1113,6 +1127,10 @@ int experts(MoonlightSession *s, int layer, const float *x, int rows, const floa
         g.expert_fmt = f.expert_fmt;
         g.shared_fmt = f.shared_fmt;
         g.has_shared = 1;
+        if (inline_route && inline_route->logits) {
+            g.route = *inline_route;  // route() left the routing to the first launch
+            g.route_in_prep = 1;
+        }
         g.expert_table = f.expert_table;
         g.shared_gate = f.shared_gate;
         g.shared_up = f.shared_up;
