@@ -162,7 +162,7 @@ def moonlight_extras(native, extra, decode_tokens):
     sess.close()
     prefill_moe(model, 8, extra)
     for ctx in (4096, 16384):
-        sess = S.Session(model, ctx + decode_tokens + 8, 1)
+        sess = S.Session(model, ctx + 2 * decode_tokens + 8, 1)
         sess.fill_kv(ctx, seed=ctx)
         token = 1
         import numpy as np
@@ -187,6 +187,22 @@ def moonlight_extras(native, extra, decode_tokens):
             "frac_device": round(nbytes / (dev_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
             "tokens": decode_tokens, "graph": sess.decode_graph()}
         print(f"[bench] decode ctx {ctx}: {wall_ms:.3f} ms/token wall "
+              f"({1e3 / wall_ms:.1f} tok/s), device {dev_ms:.3f} ms",
+              file=sys.stderr, flush=True)
+        # the same steps ending in the device arg-max (greedy next token on
+        # the GPU; only the token id crosses PCIe)
+        dev, wall = [], []
+        for _ in range(decode_tokens):
+            t1 = time.perf_counter()
+            token, _ = sess.decode_sample(token)
+            wall.append(time.perf_counter() - t1)
+            dev.append(sess.device_time_ms())
+        dev_ms = sorted(dev)[len(dev) // 2]
+        wall_ms = sorted(wall)[len(wall) // 2] * 1e3
+        extra[f"cfg4_decode_q8_ctx{ctx}"]["device_greedy"] = {
+            "tok_per_s": round(1e3 / wall_ms, 2), "ms_per_token_wall": round(wall_ms, 3),
+            "ms_per_token_device": round(dev_ms, 3)}
+        print(f"[bench] decode ctx {ctx} + device greedy: {wall_ms:.3f} ms/token wall "
               f"({1e3 / wall_ms:.1f} tok/s), device {dev_ms:.3f} ms",
               file=sys.stderr, flush=True)
         sess.close()

@@ -14,6 +14,7 @@
 #include "mla.h"
 #include "moe.h"
 #include "qgemm.h"
+#include "sample.h"
 #include "../../include/moonlight_hip.h"
 #include "../../include/moonlight_hip_ext.h"
 
@@ -138,6 +139,8 @@ struct MoonlightSession {
     int *host_step = nullptr, *host_ids = nullptr;
     int *host_flag = nullptr;
     float *host_logits = nullptr;  // pinned [vocab]: the D2H target, copied to the caller
+    mlh::SampleWork sample;        // device sampler buffers (allocated on first use)
+    int *host_sample = nullptr;    // pinned: sampler flag and token
     // one-row decode step (embed .. lm_head) as a graph: captured on the
     // second decode of the session, replayed at every later position
     hipGraphExec_t decode_exec = nullptr;
@@ -776,6 +779,8 @@ void free_session(MoonlightSession *s) {
     if (s->host_step) (void)hipHostFree(s->host_step);
     if (s->host_logits) (void)hipHostFree(s->host_logits);
     if (s->host_flag) (void)hipHostFree(s->host_flag);
+    if (s->host_sample) (void)hipHostFree(s->host_sample);
+    mlh::sample_free(&s->sample);
     if (s->ev_start) (void)hipEventDestroy(s->ev_start);
     if (s->ev_stop) (void)hipEventDestroy(s->ev_stop);
     delete s;
@@ -1256,10 +1261,31 @@ void drop_decode_graph(MoonlightSession *s) {
     s->decode_exec = nullptr;
 }
 
+// A next-token choice made on the device after the forward (choose_token,
+// moonlight_chat.c:96-131); u is the caller's draw.
+struct SampleRequest {
+    float temperature = 0.0f, top_p = 1.0f;
+    double u = 0.0;
+    int *token = nullptr;
+};
+
+static bool sampler_ready(MoonlightSession *s) {
+    if (s->sample.ctl && s->host_sample) return true;
+    if (!s->host_sample &&
+        hipHostMalloc((void **)&s->host_sample, 2 * sizeof(int), hipHostMallocDefault) != hipSuccess) {
+        s->host_sample = nullptr;
+        return false;
+    }
+    return mlh::sample_alloc(&s->sample, s->model->cfg.vocab_size) == 0;
+}
+
 // run_tokens_fast (moonlight_metal.m:1892-1986) as one device submission: a
 // graph replay for one-row decode steps, else the launches in stream order.
+// With `pick` the step ends in a device-side token choice and the logits stay
+// on the device (last_logits may then be null).
 int forward(MoonlightSession *s, const int *ids, int count, int start, float *last_logits,
-            float *layer_outputs, char *error, size_t error_size) {
+            float *layer_outputs, char *error, size_t error_size,
+            const SampleRequest *pick = nullptr) {
     MoonlightModel *m = s->model;
     const ModelConfig &c = m->cfg;
     if (!m->head_error.empty())
@@ -1277,6 +1303,8 @@ int forward(MoonlightSession *s, const int *ids, int count, int start, float *la
             return set_error(error, error_size,
                              "Moonlight fast sparse attention failed at layer %d", l);
     }
+    if (pick && !sampler_ready(s))
+        return set_error(error, error_size, "Moonlight sampler allocation failed");
     hipStream_t st = stream_of(s);
     s->host_step[0] = start;
     memcpy(s->host_ids, ids, (size_t)count * sizeof(int));
@@ -1294,8 +1322,13 @@ int forward(MoonlightSession *s, const int *ids, int count, int start, float *la
         ok = enqueue_forward(s, count, start, layer_outputs, false);
         if (decode) s->eager_decodes++;
     }
+    if (ok && pick)
+        ok = mlh::sample_enqueue(&s->sample, s->logits, pick->temperature, pick->top_p, pick->u,
+                                 st) == kOk &&
+             to_host(s, s->host_sample, s->sample.ctl + 2, 2 * sizeof(int));
     ok = ok && hipEventRecord(s->ev_stop, st) == hipSuccess &&
-         to_host(s, s->host_logits, s->logits, (size_t)c.vocab_size * sizeof(float)) &&
+         (!last_logits ||
+          to_host(s, s->host_logits, s->logits, (size_t)c.vocab_size * sizeof(float))) &&
          to_host(s, s->host_flag, s->route_error, sizeof(int));
     if (!finish(s) || !ok) {
         // the device state of a partial forward is unusable: invalidate the caches
@@ -1305,8 +1338,13 @@ int forward(MoonlightSession *s, const int *ids, int count, int start, float *la
                          hipGetErrorString(hipGetLastError()));
     }
     for (int l = 0; l < c.layer_count; ++l) s->kv_lengths[l] = start + count;
-    memcpy(last_logits, s->host_logits, (size_t)c.vocab_size * sizeof(float));
+    if (last_logits) memcpy(last_logits, s->host_logits, (size_t)c.vocab_size * sizeof(float));
     if (*s->host_flag) return set_error(error, error_size, "Moonlight fast route table failed");
+    if (pick) {
+        if (s->host_sample[0])
+            return set_error(error, error_size, "Moonlight sampler: logits are not finite");
+        *pick->token = s->host_sample[1];
+    }
     float ms = 0.0f;
     if (hipEventElapsedTime(&ms, s->ev_start, s->ev_stop) == hipSuccess) s->last_device_ms = ms;
     s->position = start + count;
@@ -1502,6 +1540,58 @@ extern "C" int moonlight_session_decode(MoonlightSession *s, int token, float *l
         return set_error(error, error_size, "invalid Moonlight decode request");
     const double t0 = monotonic_seconds();
     if (!forward(s, &token, 1, s->position, logits, nullptr, error, error_size)) return 0;
+    s->stats.decode_tokens++;
+    s->stats.decode_ms += (monotonic_seconds() - t0) * 1000.0;
+    return 1;
+}
+
+// random_unit (moonlight_chat.c:89-94): one xorshift64 (13, 7, 17) step, top
+// 53 bits as a double in [0, 1).
+static double random_unit(uint64_t *state) {
+    uint64_t x = *state;
+    x ^= x << 13;
+    x ^= x >> 7;
+    x ^= x << 17;
+    *state = x;
+    return (double)(x >> 11) * (1.0 / 9007199254740992.0);
+}
+
+extern "C" int moonlight_session_sample(MoonlightSession *s, float temperature, float top_p,
+                                        uint64_t *rng_state, int *token, char *error,
+                                        size_t error_size) {
+    if (!s || !token || s->position <= 0 || (temperature > 0.0f && !rng_state))
+        return set_error(error, error_size, "invalid Moonlight sample request");
+    if (!sampler_ready(s)) return set_error(error, error_size, "Moonlight sampler allocation failed");
+    // the caller's state advances only when a token is returned
+    uint64_t state = rng_state ? *rng_state : 0;
+    const double u = temperature > 0.0f ? random_unit(&state) : 0.0;
+    bool ok = mlh::sample_enqueue(&s->sample, s->logits, temperature, top_p, u, stream_of(s)) ==
+                  kOk &&
+              to_host(s, s->host_sample, s->sample.ctl + 2, 2 * sizeof(int));
+    if (!finish(s) || !ok)
+        return set_error(error, error_size, "Moonlight sampler failed on the device: %s",
+                         hipGetErrorString(hipGetLastError()));
+    if (s->host_sample[0]) return set_error(error, error_size, "Moonlight sampler: logits are not finite");
+    *token = s->host_sample[1];
+    if (temperature > 0.0f) *rng_state = state;
+    return 1;
+}
+
+extern "C" int moonlight_session_decode_sample(MoonlightSession *s, int token, float temperature,
+                                               float top_p, uint64_t *rng_state, int *next_token,
+                                               char *error, size_t error_size) {
+    if (!s || !next_token || s->position < 0 || s->position >= s->options.context_size ||
+        (temperature > 0.0f && !rng_state))
+        return set_error(error, error_size, "invalid Moonlight decode request");
+    SampleRequest pick;
+    pick.temperature = temperature;
+    pick.top_p = top_p;
+    uint64_t state = rng_state ? *rng_state : 0;
+    pick.u = temperature > 0.0f ? random_unit(&state) : 0.0;
+    pick.token = next_token;
+    const double t0 = monotonic_seconds();
+    if (!forward(s, &token, 1, s->position, nullptr, nullptr, error, error_size, &pick)) return 0;
+    if (temperature > 0.0f) *rng_state = state;
     s->stats.decode_tokens++;
     s->stats.decode_ms += (monotonic_seconds() - t0) * 1000.0;
     return 1;

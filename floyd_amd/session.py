@@ -86,6 +86,11 @@ SIGNATURES = {
     "moonlight_session_fill_kv": (C.c_int, [_vp, C.c_int, C.c_int, C.c_uint64]),
     "moonlight_session_device_time": (C.c_int, [_vp, C.POINTER(C.c_double)]),
     "moonlight_session_decode_graph": (C.c_int, [_vp, C.c_int]),
+    "moonlight_session_sample": (C.c_int, [_vp, C.c_float, C.c_float,
+                                           C.POINTER(C.c_uint64), C.POINTER(C.c_int), _cp, _sz]),
+    "moonlight_session_decode_sample": (C.c_int, [_vp, C.c_int, C.c_float, C.c_float,
+                                                  C.POINTER(C.c_uint64), C.POINTER(C.c_int),
+                                                  _cp, _sz]),
     "moonlight_session_fix_routes": (C.c_int, [_vp, _vp, C.c_int]),
     "moonlight_session_time_moe": (C.c_int, [_vp, C.c_int, C.c_int, C.c_uint64, C.c_int,
                                              C.c_int, C.POINTER(C.c_double),
@@ -235,6 +240,25 @@ class Session:
             raise ValueError("out must be a C-contiguous float32 array of vocab_size")
         self._call(lib().moonlight_session_decode, int(token), out.ctypes.data)
         return out
+
+    def sample(self, temperature=0.0, top_p=1.0, rng=None):
+        """Next token from the last forward's logits, chosen on the device
+        (choose_token, moonlight_chat.c:96-131).  `rng` is the caller's
+        xorshift64 state as an int; returns (token, advanced state)."""
+        state = C.c_uint64(rng or 0)
+        tok = C.c_int(-1)
+        self._call(lib().moonlight_session_sample, float(temperature), float(top_p),
+                   C.byref(state), C.byref(tok))
+        return tok.value, state.value
+
+    def decode_sample(self, token, temperature=0.0, top_p=1.0, rng=None):
+        """One decode step ending in a device-side token choice: only the
+        token id comes back.  Returns (next token, advanced rng state)."""
+        state = C.c_uint64(rng or 0)
+        tok = C.c_int(-1)
+        self._call(lib().moonlight_session_decode_sample, int(token), float(temperature),
+                   float(top_p), C.byref(state), C.byref(tok))
+        return tok.value, state.value
 
     def prefill_layers(self, ids):
         ids, p = _arr(ids, np.int32)

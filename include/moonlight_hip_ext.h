@@ -103,6 +103,29 @@ int moonlight_session_device_time(MoonlightSession *session, double *ms);
  * the reference (its decode encodes every layer each step). */
 int moonlight_session_decode_graph(MoonlightSession *session, int enable);
 
+/* Next token from the logits of the session's last prefill / append / decode,
+ * chosen on the device as choose_token does on the host
+ * (moonlight_chat.c:96-131, draw from random_unit at :89-94): temperature <= 0
+ * takes the first index of the maximum; otherwise softmax at `temperature`,
+ * candidates by descending probability (equal probabilities in token order),
+ * the smallest prefix whose sum reaches top_p, one draw.  *rng_state is the
+ * caller's xorshift64 state (the reference's chat->rng); it advances once when
+ * temperature > 0 and a token is returned, and may be NULL otherwise.
+ * Returns 1 and *token, or 0 with an error (no forward yet, non-finite
+ * logits).  Replaces the host qsort of 163,840 candidates per token. */
+int moonlight_session_sample(MoonlightSession *session, float temperature,
+                             float top_p, uint64_t *rng_state, int *token,
+                             char *error, size_t error_size);
+
+/* moonlight_session_decode (moonlight_metal.h) followed by
+ * moonlight_session_sample in the same device submission: the logits stay in
+ * HBM and only the 4-byte token comes back.  Same preconditions and errors as
+ * the two calls it combines. */
+int moonlight_session_decode_sample(MoonlightSession *session, int token,
+                                    float temperature, float top_p,
+                                    uint64_t *rng_state, int *next_token,
+                                    char *error, size_t error_size);
+
 #ifdef __cplusplus
 }
 #endif

@@ -781,3 +781,64 @@ static int forward(OrcModel *m, const int *ids, int rows, int start_position,
     free(tmp);
     return ok;
 }
+
+/* ---- next-token choice (moonlight_chat.c:89-131) -------------------------- */
+
+double orc_random_unit(uint64_t *state) {
+    uint64_t x = *state;
+    x ^= x << 13;
+    x ^= x >> 7;
+    x ^= x << 17;
+    *state = x;
+    return (double)(x >> 11) * (1.0 / 9007199254740992.0);
+}
+
+typedef struct {
+    float p;
+    int token;
+} OrcCandidate;
+
+/* descending probability; equal probabilities keep token order */
+static int orc_candidate_cmp(const void *left, const void *right) {
+    const OrcCandidate *a = (const OrcCandidate *)left, *b = (const OrcCandidate *)right;
+    if (a->p < b->p) return 1;
+    if (a->p > b->p) return -1;
+    return (a->token > b->token) - (a->token < b->token);
+}
+
+int orc_choose_token(const float *logits, int vocab, float temperature, float top_p,
+                     uint64_t *rng) {
+    int best = 0;
+    for (int t = 1; t < vocab; ++t)
+        if (logits[t] > logits[best]) best = t;
+    if (temperature <= 0.0f) return best;
+    const float maximum = logits[best];
+    OrcCandidate *c = (OrcCandidate *)malloc((size_t)vocab * sizeof(OrcCandidate));
+    if (!c) return -1;
+    double total = 0.0;
+    for (int t = 0; t < vocab; ++t) {
+        c[t].p = expf((logits[t] - maximum) / temperature);
+        c[t].token = t;
+        total += c[t].p;
+    }
+    const float ftotal = (float)total;
+    for (int t = 0; t < vocab; ++t) c[t].p /= ftotal;
+    qsort(c, (size_t)vocab, sizeof(*c), orc_candidate_cmp);
+    double kept = 0.0;
+    int count = 0;
+    do {
+        kept += c[count++].p;
+    } while (count < vocab && kept < top_p);
+    const double sample = orc_random_unit(rng) * kept;
+    double cumulative = 0.0;
+    int token = c[count - 1].token;
+    for (int i = 0; i < count; ++i) {
+        cumulative += c[i].p;
+        if (cumulative >= sample) {
+            token = c[i].token;
+            break;
+        }
+    }
+    free(c);
+    return token;
+}

@@ -35,6 +35,13 @@
  *                    (f32 SwiGLU MoE) on dequantised weights.
  *   orc_forward    : composition of the above; split prefill+append equals full
  *                    prefill; routing equals orc_route on the same logits.
+ *   orc_random_unit / orc_choose_token : Marsaglia's xorshift64 (13, 7, 17)
+ *                    restated independently in the test; greedy = numpy's
+ *                    first-index argmax; sampling against closed forms
+ *                    (top_p below the largest probability returns the argmax
+ *                    for every draw, equal logits return floor(u * count) of
+ *                    the nucleus in token order, draw 0 returns the argmax) and
+ *                    against an independent numpy form (lexsort + cumsum).
  */
 #ifndef MOONLIGHT_ORACLE_H
 #define MOONLIGHT_ORACLE_H
@@ -143,6 +150,20 @@ int orc_forward_routes(OrcModel *model, const int *ids, int rows,
                        float *layer_outputs, float *last_logits);
 int orc_forward(OrcModel *model, const int *ids, int rows, int start_position,
                 float *layer_outputs, int *route_trace, float *last_logits);
+
+/* ---- next-token choice (caller-side sampler) ------------------------- */
+/* random_unit (moonlight_chat.c:89-94): one xorshift64 step of *state, then
+ * the top 53 bits as a double in [0, 1). */
+double orc_random_unit(uint64_t *state);
+/* choose_token (moonlight_chat.c:96-131).  temperature <= 0: the first index
+ * of the maximum (strict > scan).  Otherwise p = expf((logit - max) / T),
+ * normalised by their double sum, sorted by descending p with equal p in
+ * ascending token order (what glibc 2.35's qsort, a stable merge sort at this
+ * size, gives the reference), the smallest prefix whose double sum reaches
+ * top_p kept, and one draw random_unit * kept located in the prefix sums.
+ * *rng advances once when temperature > 0. */
+int orc_choose_token(const float *logits, int vocab, float temperature, float top_p,
+                     uint64_t *rng);
 
 #ifdef __cplusplus
 }

@@ -73,6 +73,10 @@ def lib():
         L.orc_matmul.argtypes = [ctypes.c_int, ctypes.c_void_p, _f32p, _f32p, _f32p,
                                  ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int]
         L.orc_set_threads.argtypes = [ctypes.c_int]
+        L.orc_random_unit.argtypes = [ctypes.POINTER(ctypes.c_uint64)]
+        L.orc_random_unit.restype = ctypes.c_double
+        L.orc_choose_token.argtypes = [_f32p, ctypes.c_int, ctypes.c_float, ctypes.c_float,
+                                       ctypes.POINTER(ctypes.c_uint64)]
         L.orc_detect_format.argtypes = [ctypes.c_int64, ctypes.c_int, ctypes.c_int]
         L.orc_rmsnorm.argtypes = [_f32p, _f32p, _f32p, ctypes.c_int, ctypes.c_int,
                                   ctypes.c_float]
@@ -214,3 +218,12 @@ def zipf_routes(rows, experts, top_k, seed, s=1.1):
     return np.stack([rng.choice(experts, top_k, replace=False, p=p)
                      for _ in range(rows)]).astype(np.int32)
 
+
+
+def choose_token(logits, temperature, top_p, rng=0):
+    """choose_token (moonlight_chat.c:96-131) on the CPU: (token, new rng)."""
+    logits = np.ascontiguousarray(logits, np.float32)
+    state = ctypes.c_uint64(rng)
+    tok = lib().orc_choose_token(fptr(logits), logits.size, temperature, top_p,
+                                 ctypes.byref(state))
+    return tok, state.value

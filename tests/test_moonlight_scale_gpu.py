@@ -152,5 +152,20 @@ def test_decode_step(moon):
     assert int(np.argmax(logits)) == int(np.argmax(e_logits))
     for l, r in zip(range(1, 27), routes):
         assert set(r[0]) == set(trace[l, 0]), l
+    # the device sampler over the full 163,840-token vocabulary
+    from sampler_util import nucleus_choice, xorshift_unit
+    assert sess.sample(0.0)[0] == int(np.argmax(logits))
+    state, compared = 2024, 0
+    for temperature, top_p in ((1.0, 0.9), (0.6, 0.95), (1.0, 1.0)):
+        for _ in range(4):
+            u = xorshift_unit(state)[0]
+            want, margin, _ = nucleus_choice(logits, temperature, top_p, u)
+            e_tok, e_state = O.choose_token(logits, temperature, top_p, state)
+            tok, state = sess.sample(temperature, top_p, state)
+            assert state == e_state
+            if margin > 1e-6:
+                assert tok == e_tok == want, (temperature, top_p, u)
+                compared += 1
+    assert compared >= 10
     sess.close()
     orc.close()

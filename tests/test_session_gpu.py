@@ -293,3 +293,54 @@ def test_decode_graph(tiny):
     eager.close()
     graph.close()
     orc.close()
+
+
+def test_sampler(tiny):
+    """Device token choice (choose_token, moonlight_chat.c:96-131) against the
+    oracle on the same logits: greedy always, sampled draws wherever the draw
+    is not within 1e-6 of a cumulative boundary; the caller's xorshift state
+    advances exactly as random_unit's; decode_sample equals decode followed by
+    the host choice, across graph-replayed steps."""
+    from sampler_util import nucleus_choice, xorshift_unit
+    cfg, tensors, model = tiny
+    rng = np.random.default_rng(21)
+    ids = rng.integers(0, cfg["vocab_size"], 6).astype(np.int32)
+    sess = S.Session(model, 64, 32)
+    with pytest.raises(S.SessionError, match="invalid Moonlight sample request"):
+        sess.sample()
+    logits = sess.prefill(ids)
+    tok, st = sess.sample(0.0, 0.9, 5)
+    assert tok == int(np.argmax(logits)) and st == 5
+    # sharpen the tiny model's flat logits so the nucleus varies with top_p
+    compared = 0
+    for temperature, top_p in ((1.0, 0.9), (0.05, 0.5), (0.02, 0.95), (0.01, 1.0)):
+        state = 1000 + int(top_p * 100)
+        for _ in range(12):
+            u, nxt = xorshift_unit(state)
+            want, margin, count = nucleus_choice(logits, temperature, top_p, u)
+            e_tok, e_state = O.choose_token(logits, temperature, top_p, state)
+            tok, state = sess.sample(temperature, top_p, state)
+            assert state == e_state == nxt
+            if margin > 1e-6:
+                assert tok == e_tok == want, (temperature, top_p, u, count)
+                compared += 1
+    assert compared >= 40
+    # decode_sample against decode + the oracle's choice, greedy and sampled
+    other = S.Session(model, 64, 32)
+    other.prefill(ids)
+    t_a = t_b = int(ids[-1])
+    s_a = s_b = 31337
+    for step in range(5):
+        temperature = 0.0 if step % 2 == 0 else 0.03
+        lg = sess.decode(t_a)
+        t_a, s_a = O.choose_token(lg, temperature, 0.9, s_a)
+        t_b, s_b = other.decode_sample(t_b, temperature, 0.9, s_b)
+        assert s_a == s_b
+        u = xorshift_unit(s_a)[0]
+        if temperature == 0.0 or nucleus_choice(lg, temperature, 0.9, u)[1] > 1e-6:
+            assert t_a == t_b, step
+        t_b = t_a
+    assert other.position() == sess.position() == len(ids) + 5
+    assert other.decode_graph()
+    sess.close()
+    other.close()
