@@ -139,6 +139,36 @@ def prefill_moe(model, bits, extra, rows=2048):
           f"(int8 MFMA busy {ops / (us * 1e-6) / 5.0e15:.2%})", file=sys.stderr, flush=True)
 
 
+def sampler_timing(sess, logits, reps=50):
+    """Wall time of one device token choice on the session's last logits
+    (163,840 entries) against the CPU restatement of choose_token
+    (moonlight_chat.c:96-131, glibc qsort, one thread) on the same logits."""
+    out = {}
+    for name, temperature, top_p in (("greedy", 0.0, 1.0), ("t1_topp0.9", 1.0, 0.9)):
+        state = 12345
+        for _ in range(3):
+            sess.sample(temperature, top_p, state)
+        t = []
+        for _ in range(reps):
+            t1 = time.perf_counter()
+            _, state = sess.sample(temperature, top_p, state)
+            t.append(time.perf_counter() - t1)
+        out[name + "_us_wall"] = round(sorted(t)[len(t) // 2] * 1e6, 1)
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import oracle_lib as O
+    state, t = 12345, []
+    for _ in range(5):
+        t1 = time.perf_counter()
+        _, state = O.choose_token(logits, 1.0, 0.9, state)
+        t.append(time.perf_counter() - t1)
+    out["cpu_t1_topp0.9_us"] = round(sorted(t)[len(t) // 2] * 1e6, 1)
+    out["cpu_threads"] = 1
+    print(f"[bench] sampler: greedy {out['greedy_us_wall']} us, top-p {out['t1_topp0.9_us_wall']}"
+          f" us wall on the GPU; CPU choose_token {out['cpu_t1_topp0.9_us']} us",
+          file=sys.stderr, flush=True)
+    return out
+
+
 def moonlight_extras(native, extra, decode_tokens):
     """Benchmark configs 2 and 4 on a synthetic Moonlight-16B-A3B q8 model built
     in HBM: one MoE layer at T = 1, 8, 64 and a full decode step at ctx 4096
@@ -205,6 +235,8 @@ def moonlight_extras(native, extra, decode_tokens):
         print(f"[bench] decode ctx {ctx} + device greedy: {wall_ms:.3f} ms/token wall "
               f"({1e3 / wall_ms:.1f} tok/s), device {dev_ms:.3f} ms",
               file=sys.stderr, flush=True)
+        if ctx == 4096:
+            extra["sampler_vocab163840"] = sampler_timing(sess, logits)
         sess.close()
     # full-model prefill of 2048 tokens (27 layers + lm_head of the last row)
     rows = 2048
@@ -277,17 +309,24 @@ def cpu_baseline(case, budget_s=10.0):
 
 def decode_only(ctx, tokens):
     """Greedy decode steps of the synthetic q8 model at context ctx, one line
-    per token (wall and device time): the workload of a decode profile."""
+    per token (wall and device time): the workload of a decode profile.  Even
+    steps copy the logits back and take the arg-max on the host; odd steps
+    take it on the device and add one top-p draw (the sampler kernels)."""
     from floyd_amd import session as S
     model = S.Model.synthetic()
     sess = S.Session(model, ctx + tokens + 8, 1)
     sess.fill_kv(ctx, seed=ctx)
-    token = 1
+    token, state = 1, 12345
     for i in range(tokens):
         t1 = time.perf_counter()
-        logits = sess.decode(token)
-        wall = (time.perf_counter() - t1) * 1e3
-        token = int(logits.argmax())
+        if i % 2 == 0:  # logits back to the host, greedy there
+            logits = sess.decode(token)
+            wall = (time.perf_counter() - t1) * 1e3
+            token = int(logits.argmax())
+        else:  # greedy on the device, then one top-p draw on the same logits
+            token, _ = sess.decode_sample(token)
+            wall = (time.perf_counter() - t1) * 1e3
+            _, state = sess.sample(1.0, 0.9, state)
         print(f"[bench] decode {i}: {wall:.3f} ms wall, {sess.device_time_ms():.3f} ms device",
               file=sys.stderr, flush=True)
     sess.close()
