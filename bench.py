@@ -333,6 +333,66 @@ def decode_only(ctx, tokens):
     model.close()
 
 
+def load_only(layers):
+    """Model open from a container: a Moonlight-shaped q8 container with
+    `layers` layers (random bytes: the loader never looks at values) is written
+    under $TMPDIR, then moonlight_model_open is timed (page-cache preads into
+    pinned staging, H2D copies, plan building) with one reader thread and with
+    the default pool, alternating."""
+    import shutil
+    import tempfile
+    import numpy as np
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import container_util as CU
+    from floyd_amd import session as S
+    cfg = dict(hidden_size=2048, layer_count=layers, head_count=16, expert_count=64,
+               experts_per_token=6, dense_intermediate_size=11264, moe_intermediate_size=1408,
+               first_dense_layer_count=1, q_lora_rank=0, kv_lora_rank=512, qk_nope_dim=128,
+               qk_rope_dim=64, value_dim=128, shared_expert_count=2, normalize_topk=1,
+               vocab_size=163840, rms_norm_epsilon=1e-5, rope_theta=50000.0,
+               routed_scale=2.446)
+    rng = np.random.default_rng(1)
+    tensors = {}
+    for name, kind, rows, cols in CU.tensor_specs(cfg):
+        if kind == "n":
+            tensors[name] = np.ones(cols, np.float32)
+        elif kind == "b":
+            tensors[name] = np.linspace(-0.1, 0.1, cols).astype(np.float32)
+        elif kind == "f":
+            tensors[name] = rng.standard_normal((rows, cols), dtype=np.float32) * 0.02
+        else:
+            tensors[name] = rng.integers(-127, 128, (rows, cols), dtype=np.int8)
+            tensors[name + ".qs"] = np.full(rows, 1e-3, np.float32)
+    root = tempfile.mkdtemp(prefix="mlh_load_")
+    try:
+        t0 = time.perf_counter()
+        path = CU.write_container(os.path.join(root, "m"), cfg, tensors, shards=4)
+        nbytes = sum(os.path.getsize(os.path.join(path, f)) for f in os.listdir(path))
+        print(f"[bench] container: {len(tensors)} tensors, {nbytes / 1e9:.2f} GB written in "
+              f"{time.perf_counter() - t0:.1f} s", file=sys.stderr, flush=True)
+        n_tensors = len(tensors)
+        del tensors
+        result = {}
+        for rnd in range(2):
+            for threads in ("1", ""):
+                os.environ["MLH_LOAD_THREADS"] = threads
+                t1 = time.perf_counter()
+                model = S.Model.open(path)
+                dt = time.perf_counter() - t1
+                model.close()
+                key = "1 thread" if threads else "default pool"
+                result.setdefault(key, []).append(dt)
+                print(f"[bench] load ({key}, pass {rnd}): {dt:.3f} s, "
+                      f"{nbytes / dt / 1e9:.2f} GB/s", file=sys.stderr, flush=True)
+        os.environ.pop("MLH_LOAD_THREADS", None)
+        print(json.dumps({"container_bytes": nbytes, "tensors": n_tensors,
+                          "open_s": {k: round(min(v), 3) for k, v in result.items()},
+                          "GB/s": {k: round(nbytes / min(v) / 1e9, 2)
+                                   for k, v in result.items()}}), flush=True)
+    finally:
+        shutil.rmtree(root, ignore_errors=True)
+
+
 def main():
     parser = argparse.ArgumentParser()
     parser.add_argument("--gpus", type=int, default=1)
@@ -345,6 +405,9 @@ def main():
     parser.add_argument("--decode-tokens", type=int, default=20)
     parser.add_argument("--only-headline", action="store_true",
                         help="headline GEMV and the copy yardstick only (profiler runs)")
+    parser.add_argument("--load-only", type=int, default=0, metavar="LAYERS",
+                        help="only time moonlight_model_open on a Moonlight-shaped q8 "
+                             "container of LAYERS layers written under $TMPDIR")
     parser.add_argument("--decode-only", type=int, default=0, metavar="CTX",
                         help="only greedy decode steps of the synthetic model at context "
                              "CTX, printed per token (profiler runs)")
@@ -358,6 +421,9 @@ def main():
     from floyd_amd import native
     device = native.init()
     print(f"[bench] device {device}", file=sys.stderr, flush=True)
+    if args.load_only:
+        load_only(args.load_only)
+        return
     if args.decode_only:
         decode_only(args.decode_only, args.decode_tokens)
         return

@@ -24,6 +24,9 @@
 #include <cstdlib>
 #include <cstring>
 #include <ctime>
+#include <algorithm>
+#include <atomic>
+#include <thread>
 #include <string>
 #include <unordered_map>
 #include <vector>
@@ -382,10 +385,51 @@ bool place_tensors(MoonlightModel *m, std::string *error) {
     return true;
 }
 
-// Container upload: pread into two pinned staging buffers alternately while
-// the previous one is copied to HBM.
+// Container upload (moonlight_metal.m:850-871 uploads tensor by tensor).  The
+// arena places tensors in container order, contiguous up to 256-byte
+// alignment, so a run of consecutive tensors fills one 64 MiB pinned staging
+// buffer at its arena offsets (padding bytes are don't-care) and moves to HBM
+// in one copy.  A pool of reader threads preads a stage's pieces (at most
+// 4 MiB each) in parallel while the other buffer's copy runs.
+// MLH_LOAD_THREADS overrides the reader count (default: up to 8).
+static int load_threads() {
+    const char *env = getenv("MLH_LOAD_THREADS");
+    int n = env ? atoi(env) : 0;
+    if (n <= 0) {
+        const unsigned hw = std::thread::hardware_concurrency();
+        n = hw == 0 ? 4 : (int)std::min(8u, hw);
+    }
+    return std::max(1, std::min(n, 64));
+}
+
 bool upload_container(MoonlightModel *m, const Container &ct, std::string *error) {
     constexpr size_t kStage = 64u << 20;
+    constexpr size_t kPiece = 4u << 20;
+    struct Piece {
+        int tensor;
+        int64_t offset;  // within the tensor
+        size_t bytes;
+        size_t arena;    // arena offset of the first byte
+    };
+    struct Stage {
+        size_t first, last;  // pieces [first, last)
+        size_t lo, hi;       // arena range
+    };
+    std::vector<Piece> pieces;
+    std::vector<Stage> stages;
+    for (size_t i = 0; i < m->tensors.size(); ++i) {
+        const int64_t nbytes = ct.tensors()[i].nbytes;
+        const size_t base = (size_t)(m->tensors[i].dev - m->arena);
+        for (int64_t off = 0; off < nbytes; off += (int64_t)kPiece) {
+            const size_t n = (size_t)std::min<int64_t>((int64_t)kPiece, nbytes - off);
+            const size_t a = base + (size_t)off;
+            if (stages.empty() || a + n - stages.back().lo > kStage)
+                stages.push_back(Stage{pieces.size(), pieces.size(), a, a});
+            pieces.push_back(Piece{(int)i, off, n, a});
+            stages.back().last = pieces.size();
+            stages.back().hi = a + n;
+        }
+    }
     DeviceContext *ctx = context();
     void *stage[2] = {nullptr, nullptr};
     hipEvent_t done[2] = {nullptr, nullptr};
@@ -393,28 +437,44 @@ bool upload_container(MoonlightModel *m, const Container &ct, std::string *error
               hipHostMalloc(&stage[1], kStage, hipHostMallocDefault) == hipSuccess &&
               hipEventCreateWithFlags(&done[0], hipEventDisableTiming) == hipSuccess &&
               hipEventCreateWithFlags(&done[1], hipEventDisableTiming) == hipSuccess;
-    int which = 0;
+    const int nthreads = load_threads();
     bool pending[2] = {false, false};
-    for (size_t i = 0; ok && i < m->tensors.size(); ++i) {
-        const TensorEntry &te = ct.tensors()[i];
-        const DeviceTensor &t = m->tensors[i];
-        int64_t done_bytes = 0;
-        while (ok && done_bytes < te.nbytes) {
-            const size_t n = (size_t)std::min<int64_t>((int64_t)kStage, te.nbytes - done_bytes);
-            if (pending[which]) {
-                ok = hipEventSynchronize(done[which]) == hipSuccess;
-                pending[which] = false;
-            }
-            if (ok) ok = ct.read_slice(i, done_bytes, n, stage[which]);
-            if (ok)
-                ok = hipMemcpyAsync(t.dev + done_bytes, stage[which], n, hipMemcpyHostToDevice,
-                                    ctx->stream) == hipSuccess &&
-                     hipEventRecord(done[which], ctx->stream) == hipSuccess;
-            pending[which] = ok;
-            which ^= 1;
-            done_bytes += (int64_t)n;
+    int which = 0;
+    for (size_t si = 0; ok && si < stages.size(); ++si) {
+        const Stage &sg = stages[si];
+        if (pending[which]) {
+            ok = hipEventSynchronize(done[which]) == hipSuccess;
+            pending[which] = false;
+            if (!ok) break;
         }
-        if (!ok) *error = "cannot upload tensor " + te.name;
+        unsigned char *buf = static_cast<unsigned char *>(stage[which]);
+        std::atomic<size_t> next(sg.first);
+        std::atomic<int> failed(-1);
+        auto reader = [&]() {
+            for (size_t k = next++; k < sg.last; k = next++) {
+                const Piece &pc = pieces[k];
+                if (!ct.read_slice(pc.tensor, pc.offset, pc.bytes, buf + (pc.arena - sg.lo))) {
+                    failed = pc.tensor;
+                    return;
+                }
+            }
+        };
+        const size_t work = sg.last - sg.first;
+        const int extra = (int)std::min<size_t>((size_t)nthreads, work) - 1;
+        std::vector<std::thread> pool;
+        for (int t = 0; t < extra; ++t) pool.emplace_back(reader);
+        reader();
+        for (std::thread &t : pool) t.join();
+        if (failed >= 0) {
+            *error = "cannot upload tensor " + ct.tensors()[(size_t)failed.load()].name;
+            ok = false;
+            break;
+        }
+        ok = hipMemcpyAsync(m->arena + sg.lo, buf, sg.hi - sg.lo, hipMemcpyHostToDevice,
+                            ctx->stream) == hipSuccess &&
+             hipEventRecord(done[which], ctx->stream) == hipSuccess;
+        pending[which] = ok;
+        which ^= 1;
     }
     if (ok) ok = hipStreamSynchronize(ctx->stream) == hipSuccess;
     for (int i = 0; i < 2; ++i) {
