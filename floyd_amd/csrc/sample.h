@@ -15,7 +15,7 @@ namespace mlh {
 struct SampleWork {
     int vocab = 0;
     int blocks = 0;      // workgroups of the element-wise passes
-    int index_bits = 0;  // sort key = (~bits(p) << index_bits) | token
+    int index_bits = 0;  // sort key = ((~bits(p) & 0x3fffffff) << index_bits) | token
     float *probs = nullptr;
     uint64_t *keys = nullptr, *sorted = nullptr;
     double *scan = nullptr;

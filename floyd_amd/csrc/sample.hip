@@ -15,7 +15,9 @@
 //   prob_kernel   every workgroup folds the partials (the same total order), p in
 //                 fp32 from an exp in double rounded once, per-workgroup double sums
 //   key_kernel    every workgroup folds the sums in the same order, p /= (float)
-//                 total, sort key (~bits(p) << index_bits) | token: ascending keys
+//                 total, sort key (~bits(p) << index_bits) | token over the 30 low
+//                 bits of p's pattern (0 <= p <= 1 keeps the top two at 0):
+//                 ascending keys
 //                 are descending p with equal p in token order, which is what the
 //                 reference's qsort yields (glibc 2.35 sorts arrays of this size
 //                 with a stable merge sort)
@@ -42,6 +44,9 @@ constexpr int kThreads = 256;
 constexpr int kPerThread = 4;
 constexpr int kPerBlock = kThreads * kPerThread;
 constexpr int kWaves = kThreads / 64;
+// p lies in [0, 1]: bit patterns up to 0x3f800000, so 30 bits order them
+constexpr uint32_t kRankMask = 0x3fffffffu;
+constexpr int kRankBits = 30;
 
 struct Best {
     float v;
@@ -169,7 +174,7 @@ __global__ __launch_bounds__(kThreads) void key_kernel(const float *probs, int V
     for (int k = 0; k < kPerThread; ++k) {
         if (base + k < V) {
             const float p = probs[base + k] / total;
-            const uint64_t rank = (uint64_t)(~__float_as_uint(p));
+            const uint64_t rank = (uint64_t)(~__float_as_uint(p) & kRankMask);
             keys[base + k] = (rank << index_bits) | (uint64_t)(base + k);
         }
     }
@@ -212,7 +217,7 @@ __global__ void finish_kernel(const uint64_t *sorted, int index_bits, int *ctl) 
 struct KeyProb {
     int index_bits;
     __host__ __device__ double operator()(uint64_t key) const {
-        const uint32_t bits = ~(uint32_t)(key >> index_bits);
+        const uint32_t bits = ~(uint32_t)(key >> index_bits) & kRankMask;
         return (double)__builtin_bit_cast(float, bits);
     }
 };
@@ -249,7 +254,7 @@ int sample_alloc(SampleWork *w, int vocab) {
         hipMalloc((void **)&w->part_sum, nb * sizeof(double)) == hipSuccess &&
         hipMalloc((void **)&w->ctl, 4 * sizeof(int)) == hipSuccess &&
         rocprim::radix_sort_keys(nullptr, sort_bytes, w->keys, w->sorted, (unsigned)V, 0,
-                                 32 + bits) == hipSuccess &&
+                                 kRankBits + bits) == hipSuccess &&
         rocprim::inclusive_scan(nullptr, scan_bytes, ProbIter(w->sorted, KeyProb{bits}), w->scan,
                                 V, rocprim::plus<double>()) == hipSuccess;
     if (ok) {
@@ -280,7 +285,7 @@ int sample_enqueue(SampleWork *w, const float *logits, float temperature, float 
                        nb, w->index_bits, w->keys);
     size_t bytes = w->temp_bytes;
     if (rocprim::radix_sort_keys(w->temp, bytes, w->keys, w->sorted, (unsigned)V, 0,
-                                 32 + w->index_bits, stream) != hipSuccess)
+                                 kRankBits + w->index_bits, stream) != hipSuccess)
         return -2;
     bytes = w->temp_bytes;
     if (rocprim::inclusive_scan(w->temp, bytes, ProbIter(w->sorted, KeyProb{w->index_bits}),
