@@ -7,6 +7,8 @@ namespace mlh {
 
 // Sigmoid top-k + route tables for `rows` token rows (one workgroup); the
 // RouteParams type is shared with the grouped expert launches (gemv_impl.h).
+// A call routes at most kRouteMaxPositions (row, slot) positions.
+constexpr int kRouteMaxPositions = 16384;
 int route_topk(const RouteParams &p, hipStream_t stream);
 
 // Router matvec (f32 router [experts][width], x RMSNorm'ed with norm_w) and

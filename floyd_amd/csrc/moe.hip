@@ -19,7 +19,6 @@
 namespace mlh {
 
 constexpr int kRouteLdsIds = 4096;
-constexpr int kRouteMaxPositions = 16384;  // rows * top_k per routing call
 
 // One workgroup: routing of every token row, then the route tables (small
 // batches whose logits already exist).

@@ -3,12 +3,14 @@
 // Y[m][n] = s_w[n] * sum_k W[n][k] * x[m][k] for the token rows m of a task,
 // with W in the container's q8 (int8) or q4 (nibble) packing, used as exact
 // int8 operands of v_mfma_i32_32x32x32_i8.  Activations are quantised per
-// token row into two int8 limbs, x ~= s_x * (256 * hi + lo) with
-// |256 * hi + lo| <= 2^14 (15 significant bits against the row's max), and
-// both limbs are multiplied by the same weight fragment; the int32 sums are
-// combined in fp32 in the epilogue.  The per-element rounding of x is at most
-// amax / 2^15, so outputs stay within ~1e-4 relative of the fp32 matmul of
-// moonlight_kernels.metal:62-130 while every product and sum is exact.
+// token row into three int8 limbs, x ~= s_x * (65536 * hi + 256 * mid + lo)
+// with |65536 * hi + 256 * mid + lo| <= 2^22 (23 significant bits against the
+// row's max, the precision of an fp32 operand), and every limb is multiplied
+// by the same weight fragment; the int32 sums are combined in fp32 in the
+// epilogue.  The per-element rounding of x is at most amax / 2^23, so a row
+// whose max is 100x its rms still sees ~4e-6 relative error: outputs match the
+// fp32 matmul of moonlight_kernels.metal:62-130 to fp32 rounding while every
+// product and sum is exact.
 //
 // A launch covers a table of independent tasks (one per active routed expert
 // plus the shared expert, or one dense matrix).  Tiles are 128 token rows x
@@ -34,7 +36,8 @@ struct GemmTask {
     const uint8_t *w = nullptr, *w2 = nullptr;  // [n_out][k] packed (w2: up rows, SwiGLU)
     const float *s = nullptr, *s2 = nullptr;    // per weight row scales
     int rows = 0, n_out = 0, k = 0;
-    const int8_t *a_hi = nullptr, *a_lo = nullptr;  // quantised activations, row stride a_stride
+    // quantised activations (limbs hi, mid, lo), row stride a_stride
+    const int8_t *a_hi = nullptr, *a_mid = nullptr, *a_lo = nullptr;
     const float *a_scale = nullptr;
     long a_stride = 0;
     const int *a_rows = nullptr;  // optional: activation row of token row m
@@ -54,9 +57,10 @@ struct QGemmLaunch {
 
 // Per-row activation quantisation (optionally RMSNorm'ed first,
 // moonlight_kernels.metal:23-41): rows of `x` (stride x_stride floats) ->
-// hi/lo limbs (row stride `width` bytes) and scales.
+// hi/mid/lo limbs (row stride `width` bytes) and scales.
 int quantize_activations(const float *x, long x_stride, int rows, int width, const float *norm_w,
-                         float eps, int8_t *hi, int8_t *lo, float *scale, hipStream_t stream);
+                         float eps, int8_t *hi, int8_t *mid, int8_t *lo, float *scale,
+                         hipStream_t stream);
 
 // One dense task, e.g. a prefill projection.  Epilogue: plain or residual
 // (task.resid) or SwiGLU pair (dual, task.w2 = up).
@@ -81,11 +85,11 @@ struct MoeGemmParams {
     const float *norm_w = nullptr;
     float eps = 1e-5f;
     // scratch
-    int8_t *xq_hi = nullptr, *xq_lo = nullptr;  // [rows, hidden]
+    int8_t *xq_hi = nullptr, *xq_mid = nullptr, *xq_lo = nullptr;  // [rows, hidden]
     float *xq_scale = nullptr;                   // [rows]
-    int8_t *hq_hi = nullptr, *hq_lo = nullptr;  // [rows*top_k, inter]
+    int8_t *hq_hi = nullptr, *hq_mid = nullptr, *hq_lo = nullptr;  // [rows*top_k, inter]
     float *hq_scale = nullptr;                   // [rows*top_k]
-    int8_t *sq_hi = nullptr, *sq_lo = nullptr;  // [rows, shared_width]
+    int8_t *sq_hi = nullptr, *sq_mid = nullptr, *sq_lo = nullptr;  // [rows, shared_width]
     float *sq_scale = nullptr;                   // [rows]
     GemmTask *tasks = nullptr;                   // [2][kQgMaxTasks]
     int *tile_start = nullptr;                   // [2][kQgMaxTasks + 1]

@@ -1,14 +1,15 @@
 // qgemm.hip -- grouped int8-MFMA GEMM for prefill (see qgemm.h for the
 // numerics).  gfx950: v_mfma_i32_32x32x32_i8, wave64.
 //
-// Workgroup: 4 waves in a 2 x 2 arrangement over a 128 (token rows) x 256
-// (weight rows) tile; each wave owns 64 x 128 = 2 x 4 MFMA blocks per limb.
-// Pipeline: q8 has four LDS stages of 64-wide k slices copied straight into
-// LDS by global_load_lds, three in flight while one is multiplied; q4 has two
-// stages, 64-wide slices unpacked in registers on the way.  One barrier per
-// slice.  MFMA operand layout (measured on gfx950): lane l supplies row
-// (l % 32) and the 16-byte k chunk (l / 32) of a 32-wide k step, for A rows and
-// for B columns alike; result register r of lane l is
+// Workgroup: 8 waves in a 4 x 2 arrangement over a 128 (token rows) x 256
+// (weight rows) tile; each wave owns 32 x 128 = 1 x 4 MFMA blocks per limb
+// (three limbs: 192 int32 accumulators, two waves per SIMD).  Pipeline: q8
+// has three LDS stages of 64-wide k slices copied straight into LDS by
+// global_load_lds, two in flight while one is multiplied; q4 has two stages,
+// 64-wide slices unpacked in registers on the way.  One barrier per slice.
+// MFMA operand layout (measured on gfx950): lane l supplies row (l % 32) and
+// the 16-byte k chunk (l / 32) of a 32-wide k step, for A rows and for B
+// columns alike; result register r of lane l is
 // C[(r / 4) * 8 + (l / 32) * 4 + r % 4][l % 32].
 #include "qgemm.h"
 
@@ -19,7 +20,8 @@ namespace mlh {
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 typedef int i32x16 __attribute__((ext_vector_type(16)));
 
-constexpr int kQuantMax = 16384;     // |256 * hi + lo| bound
+constexpr int kLimbs = 3;
+constexpr float kQuantMax = 4194304.0f;  // 2^22: |65536 * hi + 256 * mid + lo| bound
 
 bool qgemm_shape_ok(int fmt, int k) {
     return (fmt == kQ8 || fmt == kQ4) && k > 0 && k % kQgBK == 0;
@@ -29,12 +31,21 @@ bool qgemm_shape_ok(int fmt, int k) {
 // activation quantisation: one wave per row
 // ---------------------------------------------------------------------------
 
-__device__ __forceinline__ void quant_pair(float v, float inv, int &h, int &l) {
+// v * inv rounded to an integer q, |q| <= 2^22, as q = 65536 h + 256 m + l
+// with m, l in [-128, 127] and h in [-64, 64]
+__device__ __forceinline__ void quant_limbs(float v, float inv, int &h, int &m, int &l) {
     float q = rintf(v * inv);
-    q = fminf(fmaxf(q, -(float)kQuantMax), (float)kQuantMax);
+    q = fminf(fmaxf(q, -kQuantMax), kQuantMax);
     const int qi = (int)q;
-    h = (qi + 128) >> 8;  // floor: lo lands in [-128, 127]
-    l = qi - h * 256;
+    const int t = (qi + 128) >> 8;  // floor: l lands in [-128, 127]
+    l = qi - t * 256;
+    h = (t + 128) >> 8;
+    m = t - h * 256;
+}
+
+__device__ __forceinline__ unsigned pack_bytes(int a, int b, int c, int d) {
+    return (unsigned)(a & 0xFF) | ((unsigned)(b & 0xFF) << 8) | ((unsigned)(c & 0xFF) << 16) |
+           ((unsigned)(d & 0xFF) << 24);
 }
 
 // Rows of up to kQuantRegChunks * 256 values stay in registers (one read of
@@ -42,14 +53,15 @@ __device__ __forceinline__ void quant_pair(float v, float inv, int &h, int &l) {
 constexpr int kQuantRegChunks = 16;
 
 // One set of rows to quantise: x (row stride x_stride, optionally
-// RMSNorm'ed with norm_w) -> hi / lo limbs (row stride width) and scales.
+// RMSNorm'ed with norm_w) -> hi / mid / lo limbs (row stride width) and
+// scales.
 struct QuantSeg {
     const float *x = nullptr;
     long x_stride = 0;
     int rows = 0, width = 0;
     const float *norm_w = nullptr;
     float eps = 0.0f;
-    int8_t *hi = nullptr, *lo = nullptr;
+    int8_t *hi = nullptr, *mid = nullptr, *lo = nullptr;
     float *scale = nullptr;
 };
 
@@ -59,7 +71,7 @@ __device__ __forceinline__ void quantize_row(const QuantSeg &s, int row) {
     const float *x = s.x, *norm_w = s.norm_w;
     const int width = s.width;
     const float eps = s.eps;
-    int8_t *hi = s.hi, *lo = s.lo;
+    int8_t *hi = s.hi, *mid = s.mid, *lo = s.lo;
     float *scale = s.scale;
     const int lane = threadIdx.x & (kWave - 1);
     const float *xr = x + (long)row * s.x_stride;
@@ -106,25 +118,23 @@ __device__ __forceinline__ void quantize_row(const QuantSeg &s, int row) {
         amax = fmaxf(amax, fmaxf(fmaxf(fabsf(t.x), fabsf(t.y)), fmaxf(fabsf(t.z), fabsf(t.w))));
     }
     amax = wave_max(amax);
-    const float inv = amax > 0.0f ? (float)kQuantMax / amax : 0.0f;
-    if (lane == 0) scale[row] = amax / (float)kQuantMax;
+    const float inv = amax > 0.0f ? kQuantMax / amax : 0.0f;
+    if (lane == 0) scale[row] = amax / kQuantMax;
     int8_t *hr = hi + (long)row * width;
+    int8_t *mr = mid + (long)row * width;
     int8_t *lr = lo + (long)row * width;
     for (int c = 0; c < nc; ++c) {
         const int i = (c * kWave + lane) * 4;
         if (i >= width) continue;
         const f32x4 t = normed(c);
-        int h0, h1, h2, h3, l0, l1, l2, l3;
-        quant_pair(t.x, inv, h0, l0);
-        quant_pair(t.y, inv, h1, l1);
-        quant_pair(t.z, inv, h2, l2);
-        quant_pair(t.w, inv, h3, l3);
-        const unsigned hp = (h0 & 0xFF) | ((h1 & 0xFF) << 8) | ((h2 & 0xFF) << 16) |
-                            ((unsigned)(h3 & 0xFF) << 24);
-        const unsigned lp = (l0 & 0xFF) | ((l1 & 0xFF) << 8) | ((l2 & 0xFF) << 16) |
-                            ((unsigned)(l3 & 0xFF) << 24);
-        *reinterpret_cast<unsigned *>(hr + i) = hp;
-        *reinterpret_cast<unsigned *>(lr + i) = lp;
+        int h0, h1, h2, h3, m0, m1, m2, m3, l0, l1, l2, l3;
+        quant_limbs(t.x, inv, h0, m0, l0);
+        quant_limbs(t.y, inv, h1, m1, l1);
+        quant_limbs(t.z, inv, h2, m2, l2);
+        quant_limbs(t.w, inv, h3, m3, l3);
+        *reinterpret_cast<unsigned *>(hr + i) = pack_bytes(h0, h1, h2, h3);
+        *reinterpret_cast<unsigned *>(mr + i) = pack_bytes(m0, m1, m2, m3);
+        *reinterpret_cast<unsigned *>(lr + i) = pack_bytes(l0, l1, l2, l3);
     }
 }
 
@@ -140,7 +150,7 @@ __global__ __launch_bounds__(256) void quantize_act_kernel(QuantSeg a, QuantSeg 
 }
 
 static bool quant_seg_ok(const QuantSeg &s) {
-    return s.rows == 0 || (s.x && s.hi && s.lo && s.scale && s.rows > 0 && s.width > 0 &&
+    return s.rows == 0 || (s.x && s.hi && s.mid && s.lo && s.scale && s.rows > 0 && s.width > 0 &&
                            s.width % 4 == 0 && s.x_stride % 4 == 0);
 }
 
@@ -159,8 +169,9 @@ static int quantize_segments(const QuantSeg &a, const QuantSeg &b, hipStream_t s
 }
 
 int quantize_activations(const float *x, long x_stride, int rows, int width, const float *norm_w,
-                         float eps, int8_t *hi, int8_t *lo, float *scale, hipStream_t stream) {
-    if (!x || !hi || !lo || !scale || rows <= 0 || width <= 0) return kErrArgs;
+                         float eps, int8_t *hi, int8_t *mid, int8_t *lo, float *scale,
+                         hipStream_t stream) {
+    if (!x || !hi || !mid || !lo || !scale || rows <= 0 || width <= 0) return kErrArgs;
     QuantSeg a;
     a.x = x;
     a.x_stride = x_stride;
@@ -169,6 +180,7 @@ int quantize_activations(const float *x, long x_stride, int rows, int width, con
     a.norm_w = norm_w;
     a.eps = eps;
     a.hi = hi;
+    a.mid = mid;
     a.lo = lo;
     a.scale = scale;
     return quantize_segments(a, QuantSeg{}, stream);
@@ -231,19 +243,39 @@ __device__ __forceinline__ int lds_off(int row, int chunk) {
     else return row * 128 + ((chunk ^ ((row ^ (row >> 3)) & 7)) << 4);
 }
 
-// Tile shape of a BM-row tile (BM = 128 or kQgBMSmall = 32): MI x NF blocks
-// of 32 x 32 per wave and limb, LDS stages, DMA instructions per wave and
-// slice (q8).
+// Tile shape of a BM-row tile (BM = 128 or kQgBMSmall = 32).  BM = 128: 8
+// waves (two per SIMD) in a 4 (token rows) x 2 (weight rows) grid, each wave
+// 32 x 128 = 1 x 4 blocks of 32 x 32 per limb (192 int32 accumulators);
+// BM = 32: 4 waves side by side, each 32 x 64 = 1 x 2 blocks.  A stage holds
+// the three limb tiles of A and the weight tile.  q8 DMA: A blocks of 16
+// rows, wave w taking blocks w, w + kWaves, ... (BM = 32 has 6 A blocks, so
+// waves 0-1 issue one more than waves 2-3), B blocks likewise.
 template <int FMT, int BM> struct QgShape {
     static constexpr int kRB = QgCfg<FMT>::kRB;
-    static constexpr int kStages = FMT == kQ8 ? (BM == 128 ? 4 : 3) : 2;
-    static constexpr int kMI = BM == 128 ? 2 : 1;
-    static constexpr int kNF = BM == 128 ? 4 : 2;
-    static constexpr int kLdsA = 2 * BM * kRB;
-    static constexpr int kStage = (2 * BM + kQgBW) * kRB;
+    static constexpr int kWaves = BM == 128 ? 8 : 4;
+    static constexpr int kThreads = kWaves * kWave;
+    static constexpr int kWM = BM / 32;            // waves along the token rows
+    static constexpr int kWN = kWaves / kWM;       // waves along the weight rows
+    static constexpr int kMI = 1;
+    static constexpr int kNF = kQgBW / 32 / kWN;   // 32-row weight blocks per wave
+    static constexpr int kStages = FMT == kQ8 ? 3 : 2;
+    static constexpr int kLdsA = kLimbs * BM * kRB;
+    static constexpr int kStage = (kLimbs * BM + kQgBW) * kRB;
     static constexpr int kLds = kStages * kStage + BM * 8;  // + scales and row map
-    static constexpr int kDmaPerSlice = (2 * BM / 16 + kQgBW / 16) / 4;
+    static constexpr int kRowBlocks = BM / 16;
+    static constexpr int kABlocks = kLimbs * kRowBlocks;
+    static constexpr int kBBlocks = kQgBW / 16;
+    static constexpr int kBPer = kBBlocks / kWaves;
+    static constexpr int kAMax = (kABlocks + kWaves - 1) / kWaves, kAMin = kABlocks / kWaves;
+    static constexpr int kDmaMax = kAMax + kBPer, kDmaMin = kAMin + kBPer;
+    // register path (q4): 16-byte A chunks and packed B chunks per thread and slice
+    static constexpr int kNA = (kLimbs * BM * 4 + kThreads - 1) / kThreads;
+    static constexpr int kNB = kQgBW * 2 / kThreads;
+    static_assert(kWaves % kRowBlocks == 0 || kRowBlocks % kWaves == 0, "A row block per wave");
+    static_assert(kBBlocks % kWaves == 0 && (kQgBW * 2) % kThreads == 0, "B split");
 };
+static_assert(QgShape<kQ8, kQgBM>::kLds <= 160 * 1024, "q8 128-row tile exceeds the LDS");
+static_assert(2 * QgShape<kQ8, kQgBMSmall>::kLds <= 160 * 1024, "two 32-row tiles per CU");
 
 // s_waitcnt on the vector-memory counter only (gfx9 encoding: vmcnt in bits
 // 3:0 and 15:14, expcnt 6:4 and lgkmcnt 11:8 left at their no-wait maxima).
@@ -251,14 +283,12 @@ template <int N> __device__ __forceinline__ void wait_vmcnt() {
     __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
-// Workgroup over a BM x 256 tile.  BM = 128: 4 waves in a 2 (rows) x 2
-// (weight rows) arrangement, a wave owning 64 token rows x 128 weight rows =
-// 2 x 4 blocks of 32 x 32 per limb (256 int32 accumulators, in AGPRs).  BM =
-// 32 (batches whose experts hold few rows each): the 4 waves side by side, a
-// wave owning 32 x 64 = 1 x 2 blocks, so the MFMA work per weight byte is a
-// quarter and the tile is bound by the weight stream instead of by padding.
+// Workgroup over a BM x 256 tile (QgShape).  The 32-row tile serves
+// batches whose experts hold few rows each: the MFMA work per weight byte is
+// a quarter, so the tile is bound by the weight stream instead of by padding.
 template <int FMT, bool DUAL, int BM>
-__global__ __launch_bounds__(256, BM == 128 ? 1 : 2) void qgemm_kernel(QGemmLaunch L) {
+__global__ __launch_bounds__((QgShape<FMT, BM>::kThreads), BM == 128 ? 1 : 2) void qgemm_kernel(
+    QGemmLaunch L) {
     extern __shared__ __attribute__((aligned(16))) int8_t qg_lds[];
     using Sh = QgShape<FMT, BM>;
     constexpr int kRB = Sh::kRB;
@@ -308,10 +338,11 @@ __global__ __launch_bounds__(256, BM == 128 ? 1 : 2) void qgemm_kernel(QGemmLaun
     const int m0 = (grp * kQgGroup + rem % gsize) * BM;
     const int n0 = (rem / gsize) * outw;
 
+    constexpr int kThreads = Sh::kThreads;
     const int tid = threadIdx.x;
     const int lane = tid & (kWave - 1);
     const int wave = tid >> 6;
-    const int wm = BM == 128 ? (wave & 1) : 0, wn = BM == 128 ? (wave >> 1) : wave;
+    const int wm = wave % Sh::kWM, wn = wave / Sh::kWM;
 
     if (tid < BM) {
         const int m = m0 + tid;
@@ -332,91 +363,90 @@ __global__ __launch_bounds__(256, BM == 128 ? 1 : 2) void qgemm_kernel(QGemmLaun
     const uint8_t *const w_gate = tk.w;
     const uint8_t *const w_up = tk.w2;
     // output / weight row held by LDS B row j: SwiGLU tiles give each wave
-    // its gate blocks and then the matching up blocks (BM = 128: blocks
-    // f = 0, 1 gate, 2, 3 up of a 128-row wave half; BM = 32: block 0 gate,
-    // 1 up of a 64-row wave quarter)
+    // its kNF / 2 gate blocks and then the matching up blocks (kNF = 4:
+    // blocks f = 0, 1 gate, 2, 3 up of a 128-row wave half; kNF = 2: block 0
+    // gate, 1 up of a 64-row wave quarter)
     auto b_out = [&](int j, bool &up) -> int {
         if (!DUAL) {
             up = false;
             return n0 + j;
         }
-        if (BM == 128) {
-            const int f = (j >> 5) & 3;
-            up = f >= 2;
-            return n0 + (j >> 7) * 64 + (f & 1) * 32 + (j & 31);
-        }
-        up = ((j >> 5) & 1) != 0;
-        return n0 + (j >> 6) * 32 + (j & 31);
+        constexpr int kHalf = kNF / 2;
+        const int f = (j >> 5) % kNF;
+        up = f >= kHalf;
+        return n0 + (j / (kNF * 32)) * (kHalf * 32) + (f % kHalf) * 32 + (j & 31);
     };
     auto b_row_src = [&](int j) -> const uint8_t * {
         bool up;
         const int out = b_out(j, up);
         return (up ? w_up : w_gate) + (long)(out < tk.n_out ? out : 0) * w_row_bytes;
     };
+    auto limb_base = [&](int limb) -> const int8_t * {
+        return limb == 0 ? tk.a_hi : (limb == 1 ? tk.a_mid : tk.a_lo);
+    };
     auto a_row_src = [&](int limb, int r) -> const int8_t * {
         const int arow = lds_arow[r] >= 0 ? lds_arow[r] : lds_arow[0];
-        return (limb ? tk.a_lo : tk.a_hi) + (long)arow * tk.a_stride;
+        return limb_base(limb) + (long)arow * tk.a_stride;
     };
 
-    // DMA path (q8, 64-byte rows), blocks of 16 rows = 1 KB: wave w issues
-    // the A blocks (BM = 128: limb h / 2, rows (w + 4 (h % 2)) * 16 + l / 4 for
-    // h = 0..3; BM = 32: limb w / 2, rows (w % 2) * 16 + l / 4) and the B
-    // blocks (rows (w + 4 q) * 16 + l / 4) for q = 0..3; lane l fills LDS row
-    // (block row 0 + l / 4), physical chunk l % 4, so it loads the logical
-    // chunk (l % 4) ^ g(row).  Both limbs share a lane's A rows.
+    // DMA path (q8, 64-byte rows), blocks of 16 rows = 1 KB: A block b holds
+    // limb b / kRowBlocks, rows (b % kRowBlocks) * 16 + l / 4; wave w issues A
+    // blocks w, w + kWaves, ..., all in row block w % kRowBlocks, and B
+    // blocks (rows (w + kWaves q) * 16 + l / 4); lane l fills LDS row (block
+    // row 0 + l / 4), physical chunk l % 4, so it loads the logical chunk
+    // (l % 4) ^ g(row).  The limbs share a lane's A rows.
     const int lr = lane >> 2, lc = lane & 3;
-    unsigned a_off[2] = {0u, 0u};  // byte offsets of this lane's A rows
-    // register path (q4, 64-byte rows): BM / 32 A chunks and 2 packed B chunks
-    constexpr int kNA = BM / 32;
+    unsigned a_off = 0u;  // byte offset of this lane's A row
+    // register path (q4, 64-byte rows): kNA A chunks and kNB packed B chunks
+    constexpr int kNA = Sh::kNA, kNB = Sh::kNB;
     const int8_t *a_src[kNA];
     int a_dst[kNA];
-    const uint8_t *b_src[2];
-    int b_dst[2];
-    u32x4 ra[kNA], rb[2];
+    const uint8_t *b_src[kNB];
+    int b_dst[kNB];
+    u32x4 ra[kNA], rb[kNB];
     if constexpr (kDma) {
-#pragma unroll
-        for (int h = 0; h < (BM == 128 ? 2 : 1); ++h) {
-            const int r = (BM == 128 ? (wave + 4 * h) : (wave & 1)) * 16 + lr;
-            const int arow = lds_arow[r] >= 0 ? lds_arow[r] : lds_arow[0];
-            a_off[h] = (unsigned)(arow * tk.a_stride);
-        }
+        const int r = (wave % Sh::kRowBlocks) * 16 + lr;
+        const int arow = lds_arow[r] >= 0 ? lds_arow[r] : lds_arow[0];
+        a_off = (unsigned)(arow * tk.a_stride);
     } else {
 #pragma unroll
         for (int q = 0; q < kNA; ++q) {
-            const int c = tid + 256 * q;
+            const int c = min(tid + kThreads * q, kLimbs * BM * 4 - 1);
             const int limb = c / (4 * BM), r = (c >> 2) & (BM - 1), kc = c & 3;
             a_src[q] = a_row_src(limb, r) + kc * 16;
             a_dst[q] = limb * (BM * kRB) + lds_off<kRB>(r, kc);
         }
 #pragma unroll
-        for (int q = 0; q < 2; ++q) {
-            const int c = tid + 256 * q;
+        for (int q = 0; q < kNB; ++q) {
+            const int c = tid + kThreads * q;
             const int j = c >> 1, part = c & 1;  // 32 packed columns per part
             b_src[q] = b_row_src(j) + part * 16;
             b_dst[q] = (j << 1) | part;
         }
     }
 
-    // one k slice of 64 into LDS stage buf (8 DMA instructions per wave)
+    // one k slice of 64 into LDS stage buf (kDmaMin or kDmaMax DMA
+    // instructions per wave)
     auto issue_dma = [&](int k0, int buf) {
         __attribute__((address_space(3))) int8_t *stage =
             (__attribute__((address_space(3))) int8_t *)(qg_lds + buf * kStage);
+        constexpr int kRowBlocks = Sh::kRowBlocks;
 #pragma unroll
-        for (int h = 0; h < (BM == 128 ? 4 : 1); ++h) {
-            const int rb = BM == 128 ? wave + 4 * (h & 1) : (wave & 1);
-            const int limb = BM == 128 ? h >> 1 : wave >> 1;
+        for (int h = 0; h < Sh::kAMax; ++h) {
+            const int b = wave + Sh::kWaves * h;  // A block
+            if (h >= Sh::kAMin && b >= Sh::kABlocks) break;  // wave-uniform
+            const int limb = b / kRowBlocks, rb = b % kRowBlocks;
             const int r = rb * 16 + lr;  // A row of this lane
             const int ca = lc ^ (((r >> 1) ^ (r >> 3)) & 3);
             // uniform base + 32-bit lane offset: one VGPR per address
-            const int8_t *abase = limb ? tk.a_lo : tk.a_hi;
-            const unsigned aoff = a_off[h & 1] + (unsigned)(k0 + ca * 16);
+            const unsigned aoff = a_off + (unsigned)(k0 + ca * 16);
             __builtin_amdgcn_global_load_lds(
-                (const __attribute__((address_space(1))) void *)(abase + aoff),
-                stage + limb * (BM * kRB) + rb * 1024, 16, 0, 0);
+                (const __attribute__((address_space(1))) void *)(limb_base(limb) + aoff),
+                stage + b * 1024, 16, 0, 0);
         }
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const int bb = wave + 4 * q;
+        for (int q = 0; q < Sh::kBPer; ++q) {
+            const int bb = wave + Sh::kWaves * q;
             const int j = bb * 16 + lr;  // B row of this lane
             bool up;
             const int out = b_out(j, up);
@@ -433,7 +463,7 @@ __global__ __launch_bounds__(256, BM == 128 ? 1 : 2) void qgemm_kernel(QGemmLaun
 #pragma unroll
         for (int q = 0; q < kNA; ++q) ra[q] = load_global16(a_src[q] + k0);
 #pragma unroll
-        for (int q = 0; q < 2; ++q) rb[q] = load_global16(b_src[q] + k0 / 2);
+        for (int q = 0; q < kNB; ++q) rb[q] = load_global16(b_src[q] + k0 / 2);
     };
     auto stash = [&](int buf) {
         int8_t *a = qg_lds + buf * kStage;
@@ -441,7 +471,7 @@ __global__ __launch_bounds__(256, BM == 128 ? 1 : 2) void qgemm_kernel(QGemmLaun
         for (int q = 0; q < kNA; ++q) *reinterpret_cast<u32x4 *>(a + a_dst[q]) = ra[q];
         int8_t *b = a + kLdsA;
 #pragma unroll
-        for (int q = 0; q < 2; ++q) {
+        for (int q = 0; q < kNB; ++q) {
             const int j = b_dst[q] >> 1, part = b_dst[q] & 1;
             unsigned v[8];
             unpack_q4_word(rb[q].x, v[0], v[1]);
@@ -455,9 +485,9 @@ __global__ __launch_bounds__(256, BM == 128 ? 1 : 2) void qgemm_kernel(QGemmLaun
         }
     };
 
-    i32x16 acc[2][kMI][kNF];  // [limb][row block][weight-row block]
+    i32x16 acc[kLimbs][kMI][kNF];  // [limb][row block][weight-row block]
 #pragma unroll
-    for (int a = 0; a < 2; ++a)
+    for (int a = 0; a < kLimbs; ++a)
 #pragma unroll
         for (int i = 0; i < kMI; ++i)
 #pragma unroll
@@ -470,18 +500,19 @@ __global__ __launch_bounds__(256, BM == 128 ? 1 : 2) void qgemm_kernel(QGemmLaun
     // two 32-wide k steps: all fragments are read before the first MFMA so
     // the LDS latency overlaps the MFMAs
     auto compute_pair = [&](int buf, int ksub0) {
-        const int8_t *ah = qg_lds + buf * kStage;
-        const int8_t *al = ah + BM * kRB;
-        const int8_t *bb = ah + kLdsA;
-        i32x4 fa_h[2][kMI], fa_l[2][kMI], fb[2][kNF];
+        const int8_t *a0 = qg_lds + buf * kStage;
+        const int8_t *bb = a0 + kLdsA;
+        i32x4 fa[2][kLimbs][kMI], fb[2][kNF];
 #pragma unroll
         for (int s2 = 0; s2 < 2; ++s2) {
             const int chunk = (ksub0 + s2) * 2 + half;
 #pragma unroll
             for (int i = 0; i < kMI; ++i) {
                 const int row = wm * (kMI * 32) + i * 32 + frow;
-                fa_h[s2][i] = *reinterpret_cast<const i32x4 *>(ah + lds_off<kRB>(row, chunk));
-                fa_l[s2][i] = *reinterpret_cast<const i32x4 *>(al + lds_off<kRB>(row, chunk));
+#pragma unroll
+                for (int a = 0; a < kLimbs; ++a)
+                    fa[s2][a][i] = *reinterpret_cast<const i32x4 *>(a0 + a * (BM * kRB) +
+                                                                    lds_off<kRB>(row, chunk));
             }
 #pragma unroll
             for (int f = 0; f < kNF; ++f) {
@@ -494,32 +525,33 @@ __global__ __launch_bounds__(256, BM == 128 ? 1 : 2) void qgemm_kernel(QGemmLaun
 #pragma unroll
             for (int i = 0; i < kMI; ++i)
 #pragma unroll
-                for (int f = 0; f < kNF; ++f) {
-                    acc[0][i][f] = __builtin_amdgcn_mfma_i32_32x32x32_i8(
-                        fa_h[s2][i], fb[s2][f], acc[0][i][f], 0, 0, 0);
-                    acc[1][i][f] = __builtin_amdgcn_mfma_i32_32x32x32_i8(
-                        fa_l[s2][i], fb[s2][f], acc[1][i][f], 0, 0, 0);
-                }
+                for (int f = 0; f < kNF; ++f)
+#pragma unroll
+                    for (int a = 0; a < kLimbs; ++a)
+                        acc[a][i][f] = __builtin_amdgcn_mfma_i32_32x32x32_i8(
+                            fa[s2][a][i], fb[s2][f], acc[a][i][f], 0, 0, 0);
     };
 
     if constexpr (kDma) {
         // kStages stages: slices ks + 1 .. ks + kStages - 1 stream into LDS
-        // while slice ks is multiplied.  A wave's DMA completes in order,
-        // kDmaPerSlice instructions per slice, so slice ks has landed when at
-        // most that many per later slice in flight remain; the barrier after
-        // the wait makes every wave's part visible and frees the stage of
-        // slice ks - 1 for slice ks + kStages - 1.
-        constexpr int NPS = Sh::kDmaPerSlice;
+        // while slice ks is multiplied.  A wave's DMA completes in order, its
+        // kDmaMax or kDmaMin instructions per slice, so slice ks has landed
+        // when at most that many for the later slice in flight remain; the
+        // barrier after the wait makes every wave's part visible and frees
+        // the stage of slice ks - 1 for slice ks + kStages - 1.
+        static_assert(kStages == 3, "waits below assume one later slice in flight");
+        const bool more = Sh::kDmaMax == Sh::kDmaMin ||
+                          __builtin_amdgcn_readfirstlane(wave) + Sh::kWaves * Sh::kAMin <
+                              Sh::kABlocks;
         const int nk = tk.k / kRB;  // k % 64 == 0 (qgemm_shape_ok)
         for (int st = 0; st < kStages - 1 && st < nk; ++st) issue_dma(st * kRB, st);
         for (int ks = 0; ks < nk; ++ks) {
-            const int later = nk - 1 - ks;
-            if (kStages >= 4 && later >= 2)
-                wait_vmcnt<2 * NPS>();
-            else if (later >= 1)
-                wait_vmcnt<NPS>();
-            else
+            if (ks + 1 < nk) {
+                if (more) wait_vmcnt<Sh::kDmaMax>();
+                else wait_vmcnt<Sh::kDmaMin>();
+            } else {
                 wait_vmcnt<0>();
+            }
             // a bare barrier: __syncthreads() would also wait for the stores
             // and loads of the fence it implies
             __builtin_amdgcn_s_barrier();
@@ -567,6 +599,11 @@ __global__ __launch_bounds__(256, BM == 128 ? 1 : 2) void qgemm_kernel(QGemmLaun
     // complete the scale loads now: stores share the vector-memory counter,
     // so a wait placed after the first store would also wait for the stores
     __builtin_amdgcn_s_waitcnt(0);
+    // 65536 hi + 256 mid + lo of one result register (the int32 sums are exact)
+    auto limb_sum = [&](int i, int f, int r) -> float {
+        return (float)acc[0][i][f][r] * 65536.0f +
+               ((float)acc[1][i][f][r] * 256.0f + (float)acc[2][i][f][r]);
+    };
     // the residual and plain paths are separate instantiations, so the plain
     // path carries no wait for residual loads (which would drain the stores)
     auto epilogue = [&](auto with_resid) {
@@ -600,10 +637,8 @@ __global__ __launch_bounds__(256, BM == 128 ? 1 : 2) void qgemm_kernel(QGemmLaun
 #pragma unroll
                         for (int f = 0; f < kF; ++f) {
                             if (ncol[f] < tk.n_out) {
-                                const float g = ((float)acc[0][i][f][r] * 256.0f +
-                                                 (float)acc[1][i][f][r]) * sx * sw[f];
-                                const float u = ((float)acc[0][i][f + kF][r] * 256.0f +
-                                                 (float)acc[1][i][f + kF][r]) * sx * su[f];
+                                const float g = limb_sum(i, f, r) * sx * sw[f];
+                                const float u = limb_sum(i, f + kF, r) * sx * su[f];
                                 store_global(yrow + ncol[f], silu(g) * u);
                             }
                         }
@@ -611,8 +646,7 @@ __global__ __launch_bounds__(256, BM == 128 ? 1 : 2) void qgemm_kernel(QGemmLaun
 #pragma unroll
                         for (int f = 0; f < kF; ++f) {
                             if (ncol[f] < tk.n_out) {
-                                float v = ((float)acc[0][i][f][r] * 256.0f +
-                                           (float)acc[1][i][f][r]) * sx * sw[f];
+                                float v = limb_sum(i, f, r) * sx * sw[f];
                                 if (kResid) v = res[r - rg][f] + v;
                                 store_global(yrow + ncol[f], v);
                             }
@@ -635,8 +669,8 @@ static void launch_qgemm(const QGemmLaunch &L, int grid, hipStream_t stream) {
                                    kLds) == hipSuccess;
     }();
     (void)attr;
-    hipLaunchKernelGGL((qgemm_kernel<FMT, DUAL, BM>), dim3((unsigned)grid), dim3(256), kLds,
-                       stream, L);
+    hipLaunchKernelGGL((qgemm_kernel<FMT, DUAL, BM>), dim3((unsigned)grid),
+                       dim3(QgShape<FMT, BM>::kThreads), kLds, stream, L);
 }
 
 template <int BM>
@@ -668,7 +702,7 @@ static int host_tiles(bool dual, int rows, int n_out, int bm) {
 
 int qgemm_single(int fmt, bool dual, const GemmTask &task, hipStream_t stream) {
     if (!qgemm_shape_ok(fmt, task.k) || task.rows <= 0 || task.n_out <= 0 || !task.w ||
-        !task.s || !task.a_hi || !task.a_lo || !task.a_scale || !task.y ||
+        !task.s || !task.a_hi || !task.a_mid || !task.a_lo || !task.a_scale || !task.y ||
         (dual && (!task.w2 || !task.s2)) || task.a_stride % 16)
         return kErrArgs;
     QGemmLaunch L;
@@ -708,6 +742,7 @@ __device__ __forceinline__ void moe_schedule_body(const MoeScheduleParams &sp) {
         a.n_out = p.inter;
         a.k = p.hidden;
         a.a_hi = p.xq_hi;
+        a.a_mid = p.xq_mid;
         a.a_lo = p.xq_lo;
         a.a_scale = p.xq_scale;
         a.a_stride = p.hidden;
@@ -724,6 +759,7 @@ __device__ __forceinline__ void moe_schedule_body(const MoeScheduleParams &sp) {
         b.n_out = p.hidden;
         b.k = p.inter;
         b.a_hi = p.hq_hi + (long)off * p.inter;
+        b.a_mid = p.hq_mid + (long)off * p.inter;
         b.a_lo = p.hq_lo + (long)off * p.inter;
         b.a_scale = p.hq_scale + off;
         b.a_stride = p.inter;
@@ -746,6 +782,7 @@ __device__ __forceinline__ void moe_schedule_body(const MoeScheduleParams &sp) {
             a.n_out = p.shared_width;
             a.k = p.hidden;
             a.a_hi = p.xq_hi;
+            a.a_mid = p.xq_mid;
             a.a_lo = p.xq_lo;
             a.a_scale = p.xq_scale;
             a.a_stride = p.hidden;
@@ -761,6 +798,7 @@ __device__ __forceinline__ void moe_schedule_body(const MoeScheduleParams &sp) {
             b.n_out = p.hidden;
             b.k = p.shared_width;
             b.a_hi = p.sq_hi;
+            b.a_mid = p.sq_mid;
             b.a_lo = p.sq_lo;
             b.a_scale = p.sq_scale;
             b.a_stride = p.shared_width;
@@ -834,9 +872,11 @@ int moe_gemm(const MoeGemmParams &p, hipStream_t stream) {
     xs.norm_w = p.norm_w;
     xs.eps = p.eps;
     xs.hi = p.xq_hi;
+    xs.mid = p.xq_mid;
     xs.lo = p.xq_lo;
     xs.scale = p.xq_scale;
-    if (!p.x || !p.xq_hi || !p.xq_lo || !p.xq_scale || !quant_seg_ok(xs)) return kErrArgs;
+    if (!p.x || !p.xq_hi || !p.xq_mid || !p.xq_lo || !p.xq_scale || !quant_seg_ok(xs))
+        return kErrArgs;
     if (p.route_in_prep &&
         (p.route.rows != p.rows || p.rows > kRouteOneGroupRows || !p.route.logits ||
          p.route.experts != p.experts || p.route.top_k != p.top_k || p.top_k > kMaxTopK ||
@@ -888,6 +928,7 @@ int moe_gemm(const MoeGemmParams &p, hipStream_t stream) {
             hs.rows = entries;
             hs.width = p.inter;
             hs.hi = p.hq_hi;
+            hs.mid = p.hq_mid;
             hs.lo = p.hq_lo;
             hs.scale = p.hq_scale;
             if (p.has_shared) {
@@ -896,6 +937,7 @@ int moe_gemm(const MoeGemmParams &p, hipStream_t stream) {
                 ss.rows = p.rows;
                 ss.width = p.shared_width;
                 ss.hi = p.sq_hi;
+                ss.mid = p.sq_mid;
                 ss.lo = p.sq_lo;
                 ss.scale = p.sq_scale;
             }

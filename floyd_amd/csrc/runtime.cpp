@@ -126,13 +126,18 @@ struct MoonlightSession {
     float *shared_hidden = nullptr, *shared_out = nullptr, *dense_hidden = nullptr;
     float *moe_routed = nullptr;  // routed part of moonlight_test_moe
     // MFMA path for batches of >= kMoeGemmMinRows token rows (prefill)
-    int8_t *aq_hi = nullptr, *aq_lo = nullptr;  // quantised activations [max_batch][aq_width]
+    // quantised activations (three limbs) [max_batch][aq_width]
+    int8_t *aq_hi = nullptr, *aq_mid = nullptr, *aq_lo = nullptr;
     float *aq_scale = nullptr;
     int aq_width = 0;
-    int8_t *hq_hi = nullptr, *hq_lo = nullptr;  // quantised expert hidden [max_batch*K][inter]
+    // quantised expert hidden (three limbs) [max_batch*K][inter]
+    int8_t *hq_hi = nullptr, *hq_mid = nullptr, *hq_lo = nullptr;
     float *hq_scale = nullptr;
     GemmTask *gemm_tasks = nullptr;
     int *gemm_tile_start = nullptr;
+    // router logits of every MoE layer of the last forward [L][max_batch][E]
+    // (moonlight_session_trace_router; nullptr: not kept)
+    float *router_trace = nullptr;
     // caller-given expert ids for the MoE test / timing hooks
     int *fixed_ids = nullptr;
     int fixed_rows = 0;
@@ -145,7 +150,9 @@ struct MoonlightSession {
     mlh::SampleWork sample;        // device sampler buffers (allocated on first use)
     int *host_sample = nullptr;    // pinned: sampler flag and token
     // one-row decode step (embed .. lm_head) as a graph: captured on the
-    // second decode of the session, replayed at every later position
+    // second decode of the session, replayed at every later position; the
+    // captured graph lives as long as its executable
+    hipGraph_t decode_graph = nullptr;
     hipGraphExec_t decode_exec = nullptr;
     int eager_decodes = 0;
     bool decode_graph_failed = false, decode_graph_off = false;
@@ -391,7 +398,9 @@ bool place_tensors(MoonlightModel *m, std::string *error) {
 // buffer at its arena offsets (padding bytes are don't-care) and moves to HBM
 // in one copy.  A pool of reader threads preads a stage's pieces (at most
 // 4 MiB each) in parallel while the other buffer's copy runs.
-// MLH_LOAD_THREADS overrides the reader count (default: up to 8).
+// MLH_LOAD_THREADS overrides the reader count (default: up to 8);
+// MLH_LOAD_STAGE_BYTES and MLH_LOAD_PIECE_BYTES override the stage and piece
+// sizes (read at every model open; a piece is at most a stage).
 static int load_threads() {
     const char *env = getenv("MLH_LOAD_THREADS");
     int n = env ? atoi(env) : 0;
@@ -402,9 +411,15 @@ static int load_threads() {
     return std::max(1, std::min(n, 64));
 }
 
+static size_t load_size(const char *name, size_t fallback) {
+    const char *env = getenv(name);
+    const long long v = env ? atoll(env) : 0;
+    return v > 0 ? (size_t)v : fallback;
+}
+
 bool upload_container(MoonlightModel *m, const Container &ct, std::string *error) {
-    constexpr size_t kStage = 64u << 20;
-    constexpr size_t kPiece = 4u << 20;
+    const size_t kStage = load_size("MLH_LOAD_STAGE_BYTES", 64u << 20);
+    const size_t kPiece = std::min(kStage, load_size("MLH_LOAD_PIECE_BYTES", 4u << 20));
     struct Piece {
         int tensor;
         int64_t offset;  // within the tensor
@@ -836,6 +851,8 @@ void free_session(MoonlightSession *s) {
     if (!s) return;
     for (void *p : s->allocations) (void)hipFree(p);
     if (s->decode_exec) (void)hipGraphExecDestroy(s->decode_exec);
+    if (s->decode_graph) (void)hipGraphDestroy(s->decode_graph);
+    if (s->router_trace) (void)hipFree(s->router_trace);
     if (s->host_step) (void)hipHostFree(s->host_step);
     if (s->host_logits) (void)hipHostFree(s->host_logits);
     if (s->host_flag) (void)hipHostFree(s->host_flag);
@@ -880,7 +897,7 @@ int gemm_rows(MoonlightSession *s, const Matrix &m, const Matrix *up, const floa
               int in_w, int out_w, float *y, const float *norm_w, const float *resid) {
     hipStream_t st = stream_of(s);
     if (int e = quantize_activations(x, in_w, rows, in_w, norm_w, s->model->cfg.rms_norm_epsilon,
-                                     s->aq_hi, s->aq_lo, s->aq_scale, st))
+                                     s->aq_hi, s->aq_mid, s->aq_lo, s->aq_scale, st))
         return e;
     GemmTask t;
     t.w = m.w;
@@ -893,6 +910,7 @@ int gemm_rows(MoonlightSession *s, const Matrix &m, const Matrix *up, const floa
     t.n_out = out_w;
     t.k = in_w;
     t.a_hi = s->aq_hi;
+    t.a_mid = s->aq_mid;
     t.a_lo = s->aq_lo;
     t.a_scale = s->aq_scale;
     t.a_stride = in_w;
@@ -1214,9 +1232,11 @@ int experts(MoonlightSession *s, int layer, const float *x, int rows, const floa
         // the token-row quantisation is consumed by stage 0 before the shared
         // hidden is quantised into the same buffer
         g.xq_hi = g.sq_hi = s->aq_hi;
+        g.xq_mid = g.sq_mid = s->aq_mid;
         g.xq_lo = g.sq_lo = s->aq_lo;
         g.xq_scale = g.sq_scale = s->aq_scale;
         g.hq_hi = s->hq_hi;
+        g.hq_mid = s->hq_mid;
         g.hq_lo = s->hq_lo;
         g.hq_scale = s->hq_scale;
         g.tasks = s->gemm_tasks;
@@ -1277,7 +1297,15 @@ bool enqueue_forward(MoonlightSession *s, int count, int start, float *layer_out
         } else if (ok) {
             int *trace = s->route_trace + (size_t)l * s->options.max_batch * c.experts_per_token;
             RouteParams inline_r;
-            ok = route(s, l, s->h, count, lp.post_norm, trace, false, &inline_r) == kOk &&
+            ok = route(s, l, s->h, count, lp.post_norm, trace, false, &inline_r) == kOk;
+            // the router logits exist once route() returns (selection may
+            // still be pending in the first expert launch)
+            if (ok && s->router_trace)
+                ok = hipMemcpyAsync(s->router_trace +
+                                        (size_t)l * s->options.max_batch * c.expert_count,
+                                    s->router_logits, (size_t)count * c.expert_count * 4,
+                                    hipMemcpyDeviceToDevice, st) == hipSuccess;
+            ok = ok &&
                  experts(s, l, s->h, count, lp.post_norm, s->h, s->h, nullptr, &inline_r) == kOk;
         }
         if (ok && layer_outputs)
@@ -1298,7 +1326,8 @@ static bool decode_graph_enabled() {
 }
 
 // Captures the one-row decode kernels into s->decode_exec.  The capture runs
-// nothing; a failure leaves the session on the eager path.
+// nothing; a failure leaves the session on the eager path.  The graph is kept
+// until the executable is destroyed (drop_decode_graph / free_session).
 bool capture_decode(MoonlightSession *s, int start) {
     hipStream_t st = stream_of(s);
     if (hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal) != hipSuccess) return false;
@@ -1308,9 +1337,12 @@ bool capture_decode(MoonlightSession *s, int start) {
     hipGraphExec_t exec = nullptr;
     const bool built = ok && ended && graph &&
                        hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0) == hipSuccess;
-    if (graph) (void)hipGraphDestroy(graph);
     (void)hipGetLastError();
-    if (!built) return false;
+    if (!built) {
+        if (graph) (void)hipGraphDestroy(graph);
+        return false;
+    }
+    s->decode_graph = graph;
     s->decode_exec = exec;
     return true;
 }
@@ -1318,7 +1350,9 @@ bool capture_decode(MoonlightSession *s, int start) {
 // Drops the captured decode graph (its launches baked in state that changed).
 void drop_decode_graph(MoonlightSession *s) {
     if (s->decode_exec) (void)hipGraphExecDestroy(s->decode_exec);
+    if (s->decode_graph) (void)hipGraphDestroy(s->decode_graph);
     s->decode_exec = nullptr;
+    s->decode_graph = nullptr;
 }
 
 // A next-token choice made on the device after the forward (choose_token,
@@ -1400,15 +1434,17 @@ int forward(MoonlightSession *s, const int *ids, int count, int start, float *la
     for (int l = 0; l < c.layer_count; ++l) s->kv_lengths[l] = start + count;
     if (last_logits) memcpy(last_logits, s->host_logits, (size_t)c.vocab_size * sizeof(float));
     if (*s->host_flag) return set_error(error, error_size, "Moonlight fast route table failed");
+    // the forward is committed: a failed token choice below leaves the
+    // session at the new position, ready for the next decode
+    float ms = 0.0f;
+    if (hipEventElapsedTime(&ms, s->ev_start, s->ev_stop) == hipSuccess) s->last_device_ms = ms;
+    s->position = start + count;
+    s->last_forward_rows = count;
     if (pick) {
         if (s->host_sample[0])
             return set_error(error, error_size, "Moonlight sampler: logits are not finite");
         *pick->token = s->host_sample[1];
     }
-    float ms = 0.0f;
-    if (hipEventElapsedTime(&ms, s->ev_start, s->ev_stop) == hipSuccess) s->last_device_ms = ms;
-    s->position = start + count;
-    s->last_forward_rows = count;
     return 1;
 }
 
@@ -1432,6 +1468,12 @@ extern "C" int moonlight_session_create(MoonlightSession **out, MoonlightModel *
         return set_error(error, error_size, "unsupported Moonlight MLA dimensions");
     if (c.q_lora_rank)
         return set_error(error, error_size, "unsupported Moonlight MLA dimensions");
+    // the device routing of one forward covers max_batch * top_k positions
+    if ((int64_t)options->max_batch * c.experts_per_token > kRouteMaxPositions)
+        return set_error(error, error_size,
+                         "Moonlight max_batch %d exceeds the device routing limit of %d rows",
+                         options->max_batch,
+                         kRouteMaxPositions / (c.experts_per_token > 0 ? c.experts_per_token : 1));
     MoonlightSession *s = new MoonlightSession();
     s->model = model;
     s->options = *options;
@@ -1522,9 +1564,12 @@ extern "C" int moonlight_session_create(MoonlightSession **out, MoonlightModel *
         for (int w : widths) aw = w > aw ? w : aw;
         s->aq_width = aw;
         gemm_ok = session_alloc(s, &s->aq_hi, mb * (size_t)aw, error, error_size) &&
+                  session_alloc(s, &s->aq_mid, mb * (size_t)aw, error, error_size) &&
                   session_alloc(s, &s->aq_lo, mb * (size_t)aw, error, error_size) &&
                   session_alloc(s, &s->aq_scale, mb, error, error_size) &&
                   session_alloc(s, &s->hq_hi, mb * K * (size_t)c.moe_intermediate_size, error,
+                                error_size) &&
+                  session_alloc(s, &s->hq_mid, mb * K * (size_t)c.moe_intermediate_size, error,
                                 error_size) &&
                   session_alloc(s, &s->hq_lo, mb * K * (size_t)c.moe_intermediate_size, error,
                                 error_size) &&
@@ -1650,10 +1695,16 @@ extern "C" int moonlight_session_decode_sample(MoonlightSession *s, int token, f
     pick.u = temperature > 0.0f ? random_unit(&state) : 0.0;
     pick.token = next_token;
     const double t0 = monotonic_seconds();
-    if (!forward(s, &token, 1, s->position, nullptr, nullptr, error, error_size, &pick)) return 0;
-    if (temperature > 0.0f) *rng_state = state;
+    const int before = s->position;
+    const bool chosen =
+        forward(s, &token, 1, s->position, nullptr, nullptr, error, error_size, &pick) != 0;
+    if (s->position == before) return 0;  // the forward itself failed
+    // the step is decoded (KV appended, position advanced) even when the
+    // token choice failed; the caller's state advances only with a token
     s->stats.decode_tokens++;
     s->stats.decode_ms += (monotonic_seconds() - t0) * 1000.0;
+    if (!chosen) return 0;
+    if (temperature > 0.0f) *rng_state = state;
     return 1;
 }
 
@@ -1929,6 +1980,64 @@ extern "C" int moonlight_session_decode_graph(MoonlightSession *s, int enable) {
         s->decode_graph_off = false;
     }
     return s->decode_exec ? 1 : 0;
+}
+
+extern "C" int moonlight_session_copy_route_tables(const MoonlightSession *s, int rows,
+                                                   int *n_unique, int *unique, int *counts,
+                                                   int *offsets, int *list_rows,
+                                                   int *list_slots, int *list_pos) {
+    if (!s || rows <= 0 || rows > s->options.max_batch) return 0;
+    const ModelConfig &c = s->model->cfg;
+    const size_t E = (size_t)c.expert_count, n = (size_t)rows * c.experts_per_token;
+    hipStream_t st = context()->stream;
+    bool ok = true;
+    auto copy = [&](int *dst, const int *src, size_t count) {
+        if (ok && dst)
+            ok = hipMemcpyAsync(dst, src, count * sizeof(int), hipMemcpyDeviceToHost, st) ==
+                 hipSuccess;
+    };
+    copy(n_unique, s->n_unique, 1);
+    copy(unique, s->unique, E);
+    copy(counts, s->counts, E);
+    copy(offsets, s->offsets, E);
+    copy(list_rows, s->list_rows, n);
+    copy(list_slots, s->list_slots, n);
+    copy(list_pos, s->list_pos, n);
+    return ok && hipStreamSynchronize(st) == hipSuccess ? 1 : 0;
+}
+
+extern "C" int moonlight_session_trace_router(MoonlightSession *s, int enable) {
+    if (!s) return 0;
+    drop_decode_graph(s);
+    if (!enable) {
+        if (s->router_trace) (void)hipFree(s->router_trace);
+        s->router_trace = nullptr;
+        return 1;
+    }
+    if (s->router_trace) return 1;
+    const ModelConfig &c = s->model->cfg;
+    const size_t n = (size_t)c.layer_count * s->options.max_batch * (size_t)c.expert_count;
+    void *p = nullptr;
+    if (hipMalloc(&p, n * sizeof(float)) != hipSuccess) return 0;
+    s->router_trace = static_cast<float *>(p);
+    return 1;
+}
+
+extern "C" int moonlight_session_copy_router_trace(const MoonlightSession *s, int layer,
+                                                   float *logits, int capacity_rows) {
+    if (!s || !logits || !s->router_trace || capacity_rows < s->last_forward_rows) return 0;
+    const ModelConfig &c = s->model->cfg;
+    if (layer < c.first_dense_layer_count || layer >= c.layer_count ||
+        s->model->layers[layer].dense)
+        return 0;
+    hipStream_t st = context()->stream;
+    const size_t E = (size_t)c.expert_count;
+    return hipMemcpyAsync(logits, s->router_trace + (size_t)layer * s->options.max_batch * E,
+                          (size_t)s->last_forward_rows * E * sizeof(float),
+                          hipMemcpyDeviceToHost, st) == hipSuccess &&
+                   hipStreamSynchronize(st) == hipSuccess
+               ? 1
+               : 0;
 }
 
 extern "C" int moonlight_session_device_time(MoonlightSession *s, double *ms) {

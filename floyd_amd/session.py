@@ -92,6 +92,10 @@ SIGNATURES = {
                                                   C.POINTER(C.c_uint64), C.POINTER(C.c_int),
                                                   _cp, _sz]),
     "moonlight_session_fix_routes": (C.c_int, [_vp, _vp, C.c_int]),
+    "moonlight_session_copy_route_tables": (C.c_int, [_vp, C.c_int, _vp, _vp, _vp, _vp, _vp,
+                                                      _vp, _vp]),
+    "moonlight_session_trace_router": (C.c_int, [_vp, C.c_int]),
+    "moonlight_session_copy_router_trace": (C.c_int, [_vp, C.c_int, _vp, C.c_int]),
     "moonlight_session_time_moe": (C.c_int, [_vp, C.c_int, C.c_int, C.c_uint64, C.c_int,
                                              C.c_int, C.POINTER(C.c_double),
                                              C.POINTER(C.c_int)]),
@@ -303,6 +307,32 @@ class Session:
             ok = lib().moonlight_session_fix_routes(self.handle, p, ids.shape[0])
         if not ok:
             raise SessionError("fix_routes failed")
+
+    def route_tables(self, rows):
+        """Device route tables of the last routing of `rows` token rows:
+        dict(n_unique, unique, counts, offsets, list_rows, list_slots, list_pos)."""
+        e, k = self.info["expert_count"], self.info["experts_per_token"]
+        n = np.zeros(1, np.int32)
+        t = {name: np.full(e, -7, np.int32) for name in ("unique", "counts", "offsets")}
+        t.update({name: np.full(rows * k, -7, np.int32)
+                  for name in ("list_rows", "list_slots", "list_pos")})
+        ok = lib().moonlight_session_copy_route_tables(
+            self.handle, rows, n.ctypes.data, t["unique"].ctypes.data, t["counts"].ctypes.data,
+            t["offsets"].ctypes.data, t["list_rows"].ctypes.data, t["list_slots"].ctypes.data,
+            t["list_pos"].ctypes.data)
+        if not ok:
+            raise SessionError("copy_route_tables failed")
+        t["n_unique"] = int(n[0])
+        return t
+
+    def trace_router(self, enable=True):
+        if not lib().moonlight_session_trace_router(self.handle, int(bool(enable))):
+            raise SessionError("trace_router failed")
+
+    def router_trace(self, layer, rows):
+        out = np.empty((rows, self.info["expert_count"]), np.float32)
+        ok = lib().moonlight_session_copy_router_trace(self.handle, layer, out.ctypes.data, rows)
+        return out if ok else None
 
     def time_moe(self, layer, rows, seed=7, warmup=5, iters=50):
         us, uniq = C.c_double(), C.c_int()

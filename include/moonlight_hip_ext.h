@@ -126,6 +126,34 @@ int moonlight_session_decode_sample(MoonlightSession *session, int token,
                                     uint64_t *rng_state, int *next_token,
                                     char *error, size_t error_size);
 
+/* Device route tables of the session's last routing (moonlight_test_moe,
+ * moonlight_session_time_moe or a forward's last MoE layer), for `rows`
+ * token rows: the number of distinct experts, the experts in first-appearance
+ * order over (row, slot) (unique, [expert_count], first *n_unique valid),
+ * entries per expert (counts, [expert_count]), the start of each active
+ * expert's compact list (offsets, [expert_count], valid where counts > 0),
+ * and per list entry its token row and slot (list_rows / list_slots,
+ * [rows * top_k]); list_pos[r * top_k + k] is the list entry of (r, k).
+ * Expert e's j-th entry, list_rows[offsets[e] + j], is the reference's
+ * rows[e * max_batch + j] of prepare_route_tables (moonlight_metal.m:525-559).
+ * Any output may be NULL.  Returns 1, or 0 for rows outside [1, max_batch]. */
+int moonlight_session_copy_route_tables(const MoonlightSession *session, int rows,
+                                        int *n_unique, int *unique, int *counts,
+                                        int *offsets, int *list_rows, int *list_slots,
+                                        int *list_pos);
+
+/* enable != 0: every later forward also keeps the router logits of each MoE
+ * layer ([layer][row][expert_count], f32, before the sigmoid) in a session
+ * buffer allocated here; 0 frees it.  A captured decode graph is dropped
+ * either way (its launches differ).  Returns 1 on success. */
+int moonlight_session_trace_router(MoonlightSession *session, int enable);
+
+/* Copies the router logits of `layer` of the last forward ([rows]
+ * [expert_count] floats; rows = that forward's row count) into `logits`.
+ * Returns 1, or 0 without an enabled trace or for a dense layer. */
+int moonlight_session_copy_router_trace(const MoonlightSession *session, int layer,
+                                        float *logits, int capacity_rows);
+
 #ifdef __cplusplus
 }
 #endif

@@ -502,9 +502,6 @@ int orc_attention(OrcModel *m, int layer, const float *x, int rows,
     float *q = malloc((size_t)rows * qw * sizeof(float));
     float *comp = malloc((size_t)rows * cw * sizeof(float));
     float *ctx = malloc((size_t)rows * ctxw * sizeof(float));
-    float *qa = malloc((size_t)lw * sizeof(float));
-    float *lc = malloc((size_t)lw * sizeof(float));
-    float *scores = malloc((size_t)(position + rows) * sizeof(float));
     float rope_buf[512];
     mm(&qm, x, q, rows, c->hidden_size, qw);
     mm(&kvam, x, comp, rows, c->hidden_size, cw);
@@ -525,6 +522,18 @@ int orc_attention(OrcModel *m, int layer, const float *x, int rows,
     }
 
     float attention_scale = 1.0f / sqrtf((float)(nope + rope));
+    /* rows are independent once every cache row is written: threads split
+     * the rows, each (row, head) computed exactly as in the serial order */
+#ifdef _OPENMP
+    #pragma omp parallel num_threads(g_threads)
+#endif
+    {
+    float *qa = malloc((size_t)lw * sizeof(float));
+    float *lc = malloc((size_t)lw * sizeof(float));
+    float *scores = malloc((size_t)(position + rows) * sizeof(float));
+#ifdef _OPENMP
+    #pragma omp for schedule(dynamic, 1)
+#endif
     for (int r = 0; r < rows; ++r) {
         int keys = position + r + 1;
         for (int h = 0; h < heads; ++h) {
@@ -565,15 +574,16 @@ int orc_attention(OrcModel *m, int layer, const float *x, int rows,
             }
         }
     }
+    free(qa);
+    free(lc);
+    free(scores);
+    }
     mm(&om, ctx, out, rows, ctxw, c->hidden_size);
     m->kv_lengths[layer] = position + rows;
     if (m->position < position + rows) m->position = position + rows;
     free(q);
     free(comp);
     free(ctx);
-    free(qa);
-    free(lc);
-    free(scores);
     return 1;
 }
 

@@ -13,8 +13,17 @@ when rows * top_k > 1024.
                              routes fixed per token (moe_route_fixed), q8 and q4,
                              T = 64 (32-row tiles), 512 and the full T = 2048
 
-Tolerance: rel-L2 <= 1e-3 against the fp32 oracle (BASELINE.json north_star);
-the limb quantisation keeps the measured error near 1e-4.
+  test_gemm_outliers         dense projections (q_proj, kv_a, o_proj, the
+                             11264-wide down projection) and the MoE layer at
+                             Moonlight shape with outlier-heavy activations (a
+                             few dims at 100-300x the row rms)
+  test_moonlight_prefill_attention  prefill MLA at 16 heads / latent 512 over
+                             511 and 512 rows (odd and even row pairs)
+  test_moonlight_dense_mlp   the 11264-wide dense SwiGLU block at T = 512
+
+Tolerance: rel-L2 <= 1e-3 against the fp32 oracle
+is the contract; the three-limb activation split (23 bits against each row's
+max) keeps the measured error near fp32 rounding, so most gates are 1e-4.
 """
 import numpy as np
 import pytest
@@ -23,7 +32,7 @@ import container_util as CU
 import oracle_lib as O
 from conftest import rel_l2
 from floyd_amd import session as S
-from test_moonlight_scale_gpu import MOON, moe_layer_names, oracle_with
+from test_moonlight_scale_gpu import MOON, attention_names, moe_layer_names, oracle_with
 
 pytestmark = pytest.mark.gpu
 
@@ -65,7 +74,7 @@ def test_tiny_moe_gemm(tiny, rows):
     errs = {k: rel_l2(got[k], e[k]) for k in e}
     print(f"[gpu] rel-L2 {errs}", flush=True)
     for k, v in errs.items():
-        assert v < 1e-3, k
+        assert v < 1e-4, k
     sess.close()
     orc.close()
 
@@ -82,38 +91,35 @@ def test_tiny_prefill_gemm(tiny):
     assert O.lib().orc_forward(orc.handle, O.iptr(ids), 40, 0, O.fptr(e_layers),
                                O.iptr(e_trace), O.fptr(e_logits))
     sess = S.Session(model, 64, 64)
+    sess.trace_router(True)
     layers, logits = sess.prefill_layers(ids)
-    # The device's routes per layer.  Its selection is bit-exact on its own
-    # router logits (test_tiny_moe_gemm); against the oracle's own top-k a row
-    # can differ where two experts tie within the ~1e-4 drift of the limb
-    # GEMM, so the layer outputs are compared with the oracle forced onto the
-    # device's routes, and route mismatches must stay rare.
-    trace = np.full((L, 40, 6), -1, np.int32)
+    # routes: in slot order, equal to the oracle's selection on the device's
+    # router logits of the layer and to the oracle's own forward, with no
+    # mismatched row (tests/test_moonlight_metal_runtime.c:205-213)
     for l in range(cfg["first_dense_layer_count"], L):
-        trace[l] = sess.test_copy_routes(l, 40)
-        diff = [r for r in range(40) if set(trace[l, r]) != set(e_trace[l, r])]
+        routes = sess.test_copy_routes(l, 40)
+        want, _ = O.route(sess.router_trace(l, 40),
+                          tensors[f"model.layers.{l}.mlp.gate.e_score_correction_bias"], 6, 1,
+                          2.446)
+        assert np.array_equal(routes, want), l
+        diff = [r for r in range(40) if list(routes[r]) != list(e_trace[l, r])]
         print(f"[gpu] layer {l} rows routed unlike the oracle's own top-k: {diff}", flush=True)
-        assert len(diff) <= 2, (l, diff)
-    f_layers = np.empty_like(e_layers)
-    f_logits = np.empty_like(e_logits)
-    forced = CU.oracle_model(cfg, tensors, 64)
-    assert O.lib().orc_forward_routes(forced.handle, O.iptr(ids), 40, 0, O.iptr(trace),
-                                      O.fptr(f_layers), O.fptr(f_logits))
+        assert not diff, (l, diff)
     for l in range(L):
-        err = rel_l2(layers[l], f_layers[l])
-        print(f"[gpu] layer {l} rel-L2 {err:.2e}", flush=True)
-        assert err < 1e-3, l
-    assert rel_l2(logits, f_logits) < 1e-3
-    assert int(np.argmax(logits)) == int(np.argmax(f_logits))
-    # decode after a GEMM prefill continues from the same caches (the forced
-    # oracle holds the caches of the device's routes)
-    greedy = int(np.argmax(f_logits))
+        err = rel_l2(layers[l], e_layers[l])
+        print(f"[gpu] layer {l} rel-L2 {err:.2e} max-abs "
+              f"{np.max(np.abs(layers[l] - e_layers[l])):.2e}", flush=True)
+        assert err < 1e-4 and np.max(np.abs(layers[l] - e_layers[l])) < 2e-3, l
+    # the reference's logits gate (test_moonlight_metal_runtime.c:216)
+    assert np.max(np.abs(logits - e_logits)) < 3e-4 and rel_l2(logits, e_logits) < 1e-4
+    assert int(np.argmax(logits)) == int(np.argmax(e_logits))
+    # decode after a GEMM prefill continues from the same caches
+    greedy = int(np.argmax(e_logits))
     dec = sess.decode(greedy)
     e_dec = np.empty_like(e_logits)
-    assert O.lib().orc_forward(forced.handle, O.iptr(np.array([greedy], np.int32)), 1, 40, None,
+    assert O.lib().orc_forward(orc.handle, O.iptr(np.array([greedy], np.int32)), 1, 40, None,
                                None, O.fptr(e_dec))
-    assert rel_l2(dec, e_dec) < 1e-3
-    forced.close()
+    assert rel_l2(dec, e_dec) < 1e-4 and np.max(np.abs(dec - e_dec)) < 3e-4
     sess.close()
     orc.close()
 
@@ -150,7 +156,125 @@ def test_moonlight_moe_fixed(moon, rows):
                                        O.fptr(e_w), O.fptr(expect))
     err = rel_l2(got["out"], expect)
     print(f"[gpu] T={rows} out rel-L2 {err:.2e}", flush=True)
-    assert err < 1e-3
+    assert err < 1e-4
     sess.fix_routes(None)
+    sess.close()
+    orc.close()
+
+
+def outlier_rows(rows, width, seed, dims=4):
+    """x ~ N(0, 1) with `dims` fixed feature columns set to +-100..300 in every
+    row: a few dimensions at 100-300x the rms of the others, as the hidden
+    states of DeepSeek-V3-family models carry (a single column cannot exceed
+    sqrt(width) times the rms of its own row)."""
+    x = O.fill_normal(rows * width, seed).reshape(rows, width)
+    rng = np.random.default_rng(seed)
+    cols = rng.choice(width, dims, replace=False)
+    x[:, cols] = (rng.uniform(100, 300, (rows, dims)) *
+                  rng.choice([-1.0, 1.0], (rows, dims))).astype(np.float32)
+    return x
+
+
+# (weight, input width, output width, rows): the dense prefill projections
+# at Moonlight shape; the down projection's 11264-wide rows limit the batch
+# to what the session's input buffer holds (rows * 11264 <= 512 * 2048)
+DENSE = [("model.layers.3.self_attn.q_proj.weight", 2048, 3072, 512),
+         ("model.layers.3.self_attn.kv_a_proj_with_mqa.weight", 2048, 576, 511),
+         ("model.layers.3.self_attn.o_proj.weight", 2048, 2048, 512),
+         ("model.layers.0.mlp.down_proj.weight", 11264, 2048, 90)]
+
+
+@pytest.mark.parametrize("name,width,out,rows", DENSE, ids=lambda v: str(v).split(".")[-2]
+                         if isinstance(v, str) else str(v))
+def test_gemm_outliers_dense(moon, name, width, out, rows):
+    print(f"[gpu] dense GEMM {name} T={rows} with outlier columns", flush=True)
+    sess = S.Session(moon, 512, 512)
+    orc = oracle_with(moon, [name], 8)
+    for kind, x in (("normal", O.fill_normal(rows * width, 500 + rows).reshape(rows, width)),
+                    ("outliers", outlier_rows(rows, width, 600 + rows))):
+        got = sess.test_matmul(name, x, out)
+        assert got is not None
+        expect = np.empty((rows, out), np.float32)
+        assert O.lib().orc_named_matmul(orc.handle, name.encode(), O.fptr(x), rows, width, out,
+                                        O.fptr(expect))
+        err = rel_l2(got, expect)
+        print(f"[gpu] {kind}: rel-L2 {err:.2e}", flush=True)
+        assert err < 1e-4, kind
+    sess.close()
+    orc.close()
+
+
+def test_gemm_outliers_moe(moon):
+    rows = 512
+    print(f"[gpu] Moonlight MoE layer T={rows} with outlier columns", flush=True)
+    ids = O.zipf_routes(rows, 64, 6, seed=4100)
+    x = outlier_rows(rows, 2048, 4200)
+    sess = S.Session(moon, rows, rows)
+    sess.fix_routes(ids)
+    got = sess.test_moe(1, x)
+    assert got is not None and np.array_equal(got["ids"], ids)
+    orc = oracle_with(moon, moe_layer_names(1), 8)
+    expect = np.empty_like(x)
+    e_w = np.empty((rows, 6), np.float32)
+    assert O.lib().orc_moe_layer_fixed(orc.handle, 1, O.fptr(x), rows, O.iptr(ids), O.fptr(e_w),
+                                       O.fptr(expect))
+    # the layer output includes no residual here: compare the routed + shared sum
+    err = rel_l2(got["out"], expect)
+    print(f"[gpu] out rel-L2 {err:.2e}", flush=True)
+    assert err < 1e-4
+    sess.fix_routes(None)
+    sess.close()
+    orc.close()
+
+
+@pytest.mark.parametrize("rows", [511, 512])
+def test_moonlight_prefill_attention(moon, rows):
+    """Prefill MLA (flash form over 16-key tiles, two query rows per
+    workgroup) at 16 heads / latent 512 / rope 64 against orc_attention
+    (moonlight_kernels.metal:218-375 with key_count = pos + r + 1); then
+    prefill(n - 1) + decode(1) equals prefill(n) on the last row
+    (tests/test_moonlight_metal_mla.c:219-238)."""
+    layer = 2
+    print(f"[gpu] Moonlight prefill attention, {rows} rows", flush=True)
+    x = O.fill_normal(rows * 2048, 700 + rows).reshape(rows, 2048)
+    sess = S.Session(moon, 1024, 512)
+    got = sess.test_attention(layer, x, 0)
+    assert got is not None
+    orc = oracle_with(moon, attention_names(layer), 1024)
+    expect = np.empty_like(x)
+    assert O.lib().orc_attention(orc.handle, layer, O.fptr(x), rows, 0, O.fptr(expect))
+    err = rel_l2(got, expect)
+    print(f"[gpu] rel-L2 {err:.2e} max-abs {np.max(np.abs(got - expect)):.2e}", flush=True)
+    assert err < 1e-4
+    lat, rope = sess.test_copy_kv(layer, rows)
+    elat = np.empty((rows, 512), np.float32)
+    erope = np.empty((rows, 64), np.float32)
+    assert O.lib().orc_model_copy_kv(orc.handle, layer, O.fptr(elat), O.fptr(erope), rows)
+    assert rel_l2(lat, elat) < 1e-5 and rel_l2(rope, erope) < 1e-5
+    split = S.Session(moon, 1024, 512)
+    assert split.test_attention(layer, x[:rows - 1], 0) is not None
+    last = split.test_attention(layer, x[rows - 1:], rows - 1)
+    assert last is not None
+    assert np.max(np.abs(last[0] - got[rows - 1])) < 3e-4
+    assert rel_l2(last[0], expect[rows - 1]) < 1e-4
+    split.close()
+    sess.close()
+    orc.close()
+
+
+def test_moonlight_dense_mlp(moon):
+    rows = 512
+    print(f"[gpu] Moonlight dense SwiGLU block T={rows}", flush=True)
+    names = [f"model.layers.0.mlp.{m}_proj.weight" for m in ("gate", "up", "down")]
+    x = O.fill_normal(rows * 2048, 800).reshape(rows, 2048)
+    sess = S.Session(moon, 512, 512)
+    got = sess.test_dense_mlp(0, x)
+    assert got is not None
+    orc = oracle_with(moon, names, 8)
+    expect = np.empty_like(x)
+    assert O.lib().orc_dense_mlp(orc.handle, 0, O.fptr(x), rows, O.fptr(expect))
+    err = rel_l2(got, expect)
+    print(f"[gpu] rel-L2 {err:.2e}", flush=True)
+    assert err < 1e-4
     sess.close()
     orc.close()
