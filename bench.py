@@ -108,13 +108,13 @@ def prefill_moe_ops(ids, rows, experts=64):
     """(algorithmic FLOP, int8 MFMA ops executed) of one MoE prefill layer with
     the given routes: routed 2*(3*1408*2048) FLOP per (token, expert), shared
     2*(3*2816*2048) per token, router 2*64*2048 per token; the MFMA path runs
-    128-row tiles with two int8 limbs."""
+    128-row tiles with three int8 activation limbs."""
     import numpy as np
     counts = np.bincount(np.asarray(ids).ravel(), minlength=experts)
     flop = counts.sum() * 2 * 3 * 1408 * 2048 + rows * (2 * 3 * 2816 * 2048 + 2 * 64 * 2048)
     padded = sum(-(-int(c) // 128) * 128 for c in counts if c)
     shared_pad = -(-rows // 128) * 128
-    ops = 2 * 2 * (padded * 3 * 1408 * 2048 + shared_pad * 3 * 2816 * 2048)
+    ops = 3 * 2 * (padded * 3 * 1408 * 2048 + shared_pad * 3 * 2816 * 2048)
     return int(flop), int(ops)
 
 
@@ -238,8 +238,17 @@ def moonlight_extras(native, extra, decode_tokens):
         if ctx == 4096:
             extra["sampler_vocab163840"] = sampler_timing(sess, logits)
         sess.close()
-    # full-model prefill of 2048 tokens (27 layers + lm_head of the last row)
-    rows = 2048
+    full_prefill(model, extra)
+    model.close()
+    model = S.Model.synthetic(expert_bits=4, dense_bits=4)
+    prefill_moe(model, 4, extra)
+    model.close()
+
+
+def full_prefill(model, extra, rows=2048):
+    """Full-model prefill of `rows` tokens (27 layers + lm_head of the last
+    row), device time of the middle of three runs."""
+    from floyd_amd import session as S
     sess = S.Session(model, rows + 16, rows)
     ids = [(7919 * i + 17) % 163840 for i in range(rows)]
     dev = []
@@ -256,10 +265,21 @@ def moonlight_extras(native, extra, decode_tokens):
     print(f"[bench] prefill T={rows}: {dev_ms:.2f} ms device ({rows / (dev_ms * 1e-3):.0f} tok/s)",
           file=sys.stderr, flush=True)
     sess.close()
+
+
+def prefill_only():
+    """Config 3 (MoE prefill layer, q8 and q4) and the 2048-token full-model
+    prefill, one JSON line (profiler runs and quick checks)."""
+    from floyd_amd import session as S
+    extra = {}
+    model = S.Model.synthetic()
+    prefill_moe(model, 8, extra)
+    full_prefill(model, extra)
     model.close()
     model = S.Model.synthetic(expert_bits=4, dense_bits=4)
     prefill_moe(model, 4, extra)
     model.close()
+    print(json.dumps(extra), flush=True)
 
 
 def measured_traffic(kernel):
@@ -408,6 +428,8 @@ def main():
     parser.add_argument("--load-only", type=int, default=0, metavar="LAYERS",
                         help="only time moonlight_model_open on a Moonlight-shaped q8 "
                              "container of LAYERS layers written under $TMPDIR")
+    parser.add_argument("--prefill-only", action="store_true",
+                        help="only config 3 (MoE prefill q8 / q4) and the 2048-token prefill")
     parser.add_argument("--decode-only", type=int, default=0, metavar="CTX",
                         help="only greedy decode steps of the synthetic model at context "
                              "CTX, printed per token (profiler runs)")
@@ -426,6 +448,9 @@ def main():
         return
     if args.decode_only:
         decode_only(args.decode_only, args.decode_tokens)
+        return
+    if args.prefill_only:
+        prefill_only()
         return
 
     # headline: benchmark config 1, q4 [11264 x 2048], batch 1
