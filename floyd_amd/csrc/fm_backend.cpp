@@ -110,9 +110,14 @@ void run(int fmt, float *y, const float *x, const void *w, size_t w_bytes, const
 
 }  // namespace
 
+namespace mlh {
+bool fm_static_setup();  // fm_static.hip
+}
+
 extern "C" {
 
-int fm_init(void) { return mlh::context() ? 1 : 0; }
+// Also looks up the device address of fm_matmul_static's static scratch.
+int fm_init(void) { return mlh::context() && mlh::fm_static_setup() ? 1 : 0; }
 
 const char *fm_device_name(void) {
     mlh::DeviceContext *ctx = mlh::context();

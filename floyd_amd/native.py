@@ -60,6 +60,8 @@ SIGNATURES = {
                                              _c.c_int, _c.c_int]),
     "fm_matmul_deepseek_v4_fp4": (_c.c_int, [_vp, _vp, _vp, _vp, _c.c_int, _c.c_int,
                                              _c.c_int]),
+    "fm_matmul_static": (_c.c_int, [_c.c_int, _vp, _vp, _vp, _vp, _c.c_int, _c.c_int,
+                                    _c.c_int]),
 }
 
 _lib = None

@@ -37,6 +37,23 @@ int fm_matmul_deepseek_v4_fp8(float *y, const float *x, const uint8_t *w,
 int fm_matmul_deepseek_v4_fp4(float *y, const float *x, const uint8_t *w,
                               const uint8_t *s, int O, int I, int S);
 
+/* No counterpart in the reference.  For callers that cannot allocate device
+ * memory (serving loops and harnesses that forbid hipMalloc): fm_matmul_q8
+ * (bits = 8) or fm_matmul_q4 (bits = 4) with cache = 0, the same kernels and
+ * results, but x, y, w and s are staged in a static device array of
+ * FM_STATIC_SCRATCH_BYTES per GPU (held from load to process end) instead of
+ * library-allocated memory; the call allocates nothing.  Limit: the staging,
+ * 256-byte aligned S*I*4 + S*O*4 + weight bytes, plus O*4, must fit the array
+ * (e.g. a q8 [11264 x 2048] matrix with S <= 32).  Returns 1, or 0 with y
+ * filled with NaN and the reason in mlk_last_error() (bad arguments, sizes
+ * beyond the limit, device failure).  Synchronous.  The array keeps the last
+ * call's contents; every byte a call reads is written by that call first.
+ * Calls on one GPU share the array, so overlapping calls would race: calls of
+ * one process are serialised by a lock. */
+#define FM_STATIC_SCRATCH_BYTES (32u << 20)
+int fm_matmul_static(int bits, float *y, const float *x, const void *w,
+                     const float *s, int O, int I, int S);
+
 #ifdef __cplusplus
 }
 #endif
