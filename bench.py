@@ -77,6 +77,29 @@ class GemvCase:
                                    self.rows, warmup, iters, use_graph)
         return us, self.bytes / (us * 1e-6) / 1e9
 
+    def time_median(self, windows=11, per_window=100):
+        """Median (and spread) of the per-launch average over `windows`
+        graph replays of `per_window` launches each (BASELINE.md section 5's
+        median over >= 100 launches)."""
+        us = sorted(self.native.time_gemv(self.fmt, self.w, self.s, self.x, self.y, self.O,
+                                          self.I, self.rows, 2, per_window, True)
+                    for _ in range(windows))
+        return {"median_us": round(us[len(us) // 2], 3), "min_us": round(us[0], 3),
+                "max_us": round(us[-1], 3), "launches": windows * per_window}
+
+    def read_ceiling(self, warmup=5, iters=100):
+        """Same-run ceiling of a GEMV of this shape: the fastest plain
+        read-only stream of the same weight bytes, rotating over the same
+        copies, over a few grid sizes (launch ramp and tail included)."""
+        best = None
+        scratch = self.native.DeviceBuffer(4096 * 4 * 4)
+        for blocks in (256, 512, 1024, 2048, 4096):
+            us = self.native.time_read(self.w, self.wbytes, blocks, scratch, warmup, iters)
+            if best is None or us < best[0]:
+                best = (us, blocks)
+        scratch.close()
+        return best
+
     def host_inputs(self):
         import numpy as np
         q = self.w[0].download(np.uint8 if self.fmt else np.float32)
@@ -320,11 +343,23 @@ def cpu_baseline(case, budget_s=10.0):
         if elapsed >= budget_s or reps >= 20000:
             break
     per = elapsed / reps
+    # the reference tests' serial semantics: one thread
+    reps1, t0 = 0, time.perf_counter()
+    while True:
+        oracle_lib.matmul(case.fmt, q, s, x, case.O, case.I, threads=1)
+        reps1 += 1
+        elapsed1 = time.perf_counter() - t0
+        if elapsed1 >= budget_s / 4 or reps1 >= 2000:
+            break
+    per1 = elapsed1 / reps1
     return {"value": round(case.bytes / per / 1e9, 3), "unit": "GB/s", "cores": threads,
             "kind": "port",
             "sample": f"{reps} oracle GEMVs of the same workload, {elapsed:.1f} s "
                       f"(OpenMP over output rows, gcc -O3 -march=x86-64-v3)",
-            "ms_per_step": round(per * 1e3, 4), "parity_rel_l2": err}
+            "ms_per_step": round(per * 1e3, 4), "parity_rel_l2": err,
+            "one_thread": {"value": round(case.bytes / per1 / 1e9, 3), "unit": "GB/s",
+                           "ms_per_step": round(per1 * 1e3, 3),
+                           "sample": f"{reps1} GEMVs, {elapsed1:.1f} s"}}
 
 
 def decode_only(ctx, tokens):
@@ -467,12 +502,28 @@ def main():
             "cfg1_q4_2048x11264_b1": (2, 2048, 11264, 1),
             "q8_2048x11264_b1": (1, 2048, 11264, 1),
             "f32_lmhead_163840x2048_b1": (0, 163840, 2048, 1)}
+    def with_ceiling(case, us):
+        """The GEMV time against the same-run read-only ceiling of its weights."""
+        c_us, c_blocks = case.read_ceiling()
+        return {"read_ceiling_us": round(c_us, 3), "read_ceiling_blocks": c_blocks,
+                "read_ceiling_GB/s": round(case.wbytes / (c_us * 1e-6) / 1e9, 1),
+                "gemv_over_ceiling": round(c_us / us, 4)}
+
+    head_median = head.time_median()
+    head_ceiling = with_ceiling(head, head_us)
+    print(f"[bench] headline median {head_median['median_us']} us; read ceiling "
+          f"{head_ceiling['read_ceiling_us']} us ({head_ceiling['gemv_over_ceiling']:.0%} of it)",
+          file=sys.stderr, flush=True)
     for index, (name, (fmt, o, i, rows)) in enumerate(extra_cases.items()):
         case = GemvCase(native, fmt, o, i, rows, seed=1000 + index)
         us, gbs = case.time(args.warmup, max(50, args.steps // 2))
         extra[name] = {"us": round(us, 3), "GB/s": round(gbs, 1),
                        "frac": round(gbs / HBM_PEAK_GBS, 4), "bytes": case.bytes}
-        print(f"[bench] {name}: {us:.2f} us {gbs:.0f} GB/s", file=sys.stderr, flush=True)
+        extra[name].update(case.time_median())
+        extra[name].update(with_ceiling(case, us))
+        print(f"[bench] {name}: {us:.2f} us {gbs:.0f} GB/s (median "
+              f"{extra[name]['median_us']} us, read ceiling {extra[name]['read_ceiling_us']} us)",
+              file=sys.stderr, flush=True)
         case.close()
 
     # copy yardstick: 256 MiB per launch, two buffer pairs
@@ -519,6 +570,8 @@ def main():
         "extra": extra,
     }
     line["extra"]["headline_stream_launch_us"] = round(head_us_stream, 3)
+    line["extra"]["headline_median"] = head_median
+    line["extra"]["headline_read_ceiling"] = head_ceiling
     head.close()
     print(json.dumps(line), flush=True)
 

@@ -7,18 +7,20 @@
 // nibble and 2j+1 in the high nibble of byte j, stored as q+8
 // (tools/convert_moonlight.py:46-66).
 //
-// Work decomposition.  A workgroup is 4 wavefronts.  A row of W is cut into
-// 16-byte chunks; a group of LPR lanes covers a row, each lane owning the chunks
-// li, li+LPR, ... of every row it visits (k-tiles of KT chunks per lane).
+// Work decomposition.  A workgroup is 4 (or, for the quantised formats, 8)
+// wavefronts.  A row of W is cut into 16-byte chunks; a group of LPR lanes
+// covers a row, each lane owning the chunks li, li+LPR, ... of every row it
+// visits (k-tiles of KT chunks per lane).
 //   KS = 1: every wave owns R rows (per lane group);
-//   KS = 4: the 4 waves of a workgroup share the same R rows and split the
+//   KS > 1: the waves of a workgroup share the same R rows and split the
 //           k-tiles between them (wide rows: the 11264-long down projections),
 //           partial sums meet in LDS.
 // Per k-tile a lane issues its R*KT 16-byte non-temporal weight loads back to
-// back, then loads the matching x slice once and reuses it for the R rows.
-// int8 / nibbles become floats with v_cvt_f32_ubyteN on byte-biased values (q+128
-// resp. the stored nibble) and the bias is removed once per row:
-//      sum x*q = sum x*(q+bias) - bias*sum x.
+// back, then uses them against the matching slice of x for the R rows.
+//   f32 weights (lm_head, router): fp32 FMAs against x read from L1 / L2
+//           (gemv_block).
+//   q8 / q4 weights: int8-limb dot products against x split once per
+//           workgroup into LDS (limb_block; the numerics are described there).
 // R*B partial sums are reduced over the lane group with a transposed butterfly.
 // Prologue: optional RMSNorm of x (moonlight_kernels.metal:23-41).  Epilogues:
 // plain, residual add, and SwiGLU of a gate/up pair (moonlight_kernels.metal:533-541).
@@ -34,45 +36,13 @@ template <> struct FmtTraits<kF32> { static constexpr int kElemsPerChunk = 4; };
 template <> struct FmtTraits<kQ8> { static constexpr int kElemsPerChunk = 16; };
 template <> struct FmtTraits<kQ4> { static constexpr int kElemsPerChunk = 32; };
 
-template <int FMT>
-__device__ __forceinline__ float chunk_dot(u32x4 w, const float *x, float acc) {
-    if constexpr (FMT == kF32) {
-        acc = fmaf(__uint_as_float(w.x), x[0], acc);
-        acc = fmaf(__uint_as_float(w.y), x[1], acc);
-        acc = fmaf(__uint_as_float(w.z), x[2], acc);
-        acc = fmaf(__uint_as_float(w.w), x[3], acc);
-    } else if constexpr (FMT == kQ8) {
-        unsigned int d[4] = {w.x ^ 0x80808080u, w.y ^ 0x80808080u, w.z ^ 0x80808080u,
-                             w.w ^ 0x80808080u};
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            acc = fmaf((float)(d[j] & 0xFFu), x[4 * j + 0], acc);
-            acc = fmaf((float)((d[j] >> 8) & 0xFFu), x[4 * j + 1], acc);
-            acc = fmaf((float)((d[j] >> 16) & 0xFFu), x[4 * j + 2], acc);
-            acc = fmaf((float)(d[j] >> 24), x[4 * j + 3], acc);
-        }
-    } else {
-        unsigned int d[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            unsigned int lo = d[j] & 0x0F0F0F0Fu;
-            unsigned int hi = (d[j] >> 4) & 0x0F0F0F0Fu;
-            const float *xs = x + 8 * j;
-            acc = fmaf((float)(lo & 0xFFu), xs[0], acc);
-            acc = fmaf((float)(hi & 0xFFu), xs[1], acc);
-            acc = fmaf((float)((lo >> 8) & 0xFFu), xs[2], acc);
-            acc = fmaf((float)((hi >> 8) & 0xFFu), xs[3], acc);
-            acc = fmaf((float)((lo >> 16) & 0xFFu), xs[4], acc);
-            acc = fmaf((float)((hi >> 16) & 0xFFu), xs[5], acc);
-            acc = fmaf((float)(lo >> 24), xs[6], acc);
-            acc = fmaf((float)(hi >> 24), xs[7], acc);
-        }
-    }
+// One 16-byte chunk of f32 weights (4 values) against 4 values of x.
+__device__ __forceinline__ float chunk_dot_f32(u32x4 w, const float *x, float acc) {
+    acc = fmaf(__uint_as_float(w.x), x[0], acc);
+    acc = fmaf(__uint_as_float(w.y), x[1], acc);
+    acc = fmaf(__uint_as_float(w.z), x[2], acc);
+    acc = fmaf(__uint_as_float(w.w), x[3], acc);
     return acc;
-}
-
-template <int FMT> __device__ __forceinline__ constexpr float byte_bias() {
-    return FMT == kQ8 ? 128.0f : (FMT == kQ4 ? 8.0f : 0.0f);
 }
 
 __host__ __device__ constexpr int row_bytes_of(int fmt, int width) {
@@ -109,6 +79,7 @@ __host__ __device__ constexpr int rows_per_block(bool dual) {
 
 template <int FMT, int B, int KT, int LPR, int R, int KS>
 __device__ __forceinline__ void gemv_block(const GemvJob<B> job) {
+    static_assert(FMT == kF32, "q8 / q4 take limb_block");
     constexpr int EPC = FmtTraits<FMT>::kElemsPerChunk;
     constexpr int GPW = kWave / LPR;
     constexpr int NV = R * B;
@@ -168,9 +139,6 @@ __device__ __forceinline__ void gemv_block(const GemvJob<B> job) {
     float acc[NV];
 #pragma unroll
     for (int v = 0; v < NV; ++v) acc[v] = 0.0f;
-    float sumx[B];
-#pragma unroll
-    for (int b = 0; b < B; ++b) sumx[b] = 0.0f;
 
     for (int kt0 = kpart * KT * LPR; kt0 < nc; kt0 += KS * KT * LPR) {
         u32x4 wv[R][KT];
@@ -214,7 +182,6 @@ __device__ __forceinline__ void gemv_block(const GemvJob<B> job) {
                     xr[b][k][e + 1] = v.y;
                     xr[b][k][e + 2] = v.z;
                     xr[b][k][e + 3] = v.w;
-                    sumx[b] += (v.x + v.y) + (v.z + v.w);
                 }
             }
         }
@@ -224,14 +191,7 @@ __device__ __forceinline__ void gemv_block(const GemvJob<B> job) {
             for (int k = 0; k < KT; ++k)
 #pragma unroll
                 for (int b = 0; b < B; ++b)
-                    acc[r * B + b] = chunk_dot<FMT>(wv[r][k], xr[b][k], acc[r * B + b]);
-    }
-
-    if constexpr (FMT != kF32) {
-#pragma unroll
-        for (int r = 0; r < R; ++r)
-#pragma unroll
-            for (int b = 0; b < B; ++b) acc[r * B + b] -= byte_bias<FMT>() * sumx[b];
+                    acc[r * B + b] = chunk_dot_f32(wv[r][k], xr[b][k], acc[r * B + b]);
     }
 
     butterfly_reduce<NV, LPR>(acc, lane);

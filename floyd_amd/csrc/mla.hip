@@ -157,152 +157,6 @@ __global__ __launch_bounds__(256) void mla_prep_kernel(MlaParams p, int chunks) 
     }
 }
 
-// Latent slice of a lane: LPL values per lane, float4 groups at 4*lane and
-// 256 + 4*lane for the 512-wide cache (coalesced 1 KB per wave load).
-template <int LPL>
-__device__ __forceinline__ int lat_index(int lane, int i) {
-    if constexpr (LPL >= 4) return (i / 4) * 256 + 4 * lane + (i % 4);
-    else if constexpr (LPL == 2) return 2 * lane + i;
-    else return lane;
-}
-
-template <int LPL>
-__device__ __forceinline__ void load_lat(const float *row, int lane, float (&v)[LPL]) {
-    if constexpr (LPL >= 4) {
-#pragma unroll
-        for (int g = 0; g < LPL / 4; ++g) {
-            const f32x4 a = load_f4(row + g * 256 + 4 * lane);
-            v[4 * g + 0] = a.x; v[4 * g + 1] = a.y; v[4 * g + 2] = a.z; v[4 * g + 3] = a.w;
-        }
-    } else {
-#pragma unroll
-        for (int i = 0; i < LPL; ++i) v[i] = row[lat_index<LPL>(lane, i)];
-    }
-}
-
-// One workgroup per (split of KS keys, token row).  Wave w takes keys
-// 8w .. 8w + 7 of the split and scores them against all heads (two passes of
-// 8 heads, transposed butterfly over 64 (key, head) sums); the latent rows it
-// loads (one batch of loads per wave) also go to LDS, where the context pass
-// reads them back: thread t accumulates latent dims t, t + 256 of every head.
-constexpr int kAttendLdsBytes = kMlaKeysPerSplit * kMlaMaxLatent * 4;
-template <int LPL>
-__global__ __launch_bounds__(256) void mla_attend_kernel(MlaParams p) {
-    constexpr int H = kMlaMaxHeads;
-    constexpr int KS = kMlaKeysPerSplit;
-    constexpr int KB = KS / 4;  // keys per wave
-    constexpr int HP = 8;       // heads per scoring pass
-    extern __shared__ __attribute__((aligned(16))) float lat_s[];  // [KS][latent]
-    __shared__ float prob[KS][H];  // scores, then probabilities, key-major
-    __shared__ float smax[H], ssum[H];
-    const int split = blockIdx.x;
-    const int r = blockIdx.y;
-    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-    const int keys = mla_position(p) + r + 1;
-    const int k0 = split * KS;
-    const int nk = keys - k0 < KS ? keys - k0 : KS;
-    const long part = ((long)r * p.max_splits + split) * H;
-    if (nk <= 0) {
-        if (t < H) {
-            p.part_max[part + t] = -INFINITY;
-            p.part_sum[part + t] = 0.0f;
-        }
-        return;
-    }
-    float lv[KB][LPL];
-    float rv[KB];
-#pragma unroll
-    for (int b = 0; b < KB; ++b) {
-        const int j = wave * KB + b < nk ? wave * KB + b : nk - 1;  // clamp: not written
-        const long k = k0 + j;
-        load_lat<LPL>(p.latent_cache + k * p.latent, lane, lv[b]);
-        rv[b] = lane < p.rope ? p.rope_cache[k * p.rope + lane] : 0.0f;
-    }
-#pragma unroll
-    for (int b = 0; b < KB; ++b)
-#pragma unroll
-        for (int e = 0; e < LPL; ++e)
-            lat_s[(wave * KB + b) * p.latent + lat_index<LPL>(lane, e)] = lv[b][e];
-#pragma unroll
-    for (int hp = 0; hp < H; hp += HP) {
-        float qa[HP][LPL];
-        float qr[HP];
-#pragma unroll
-        for (int i = 0; i < HP; ++i) {
-            const int h = hp + i;
-            const bool hv = h < p.heads;
-            if (hv) {
-                load_lat<LPL>(p.query_absorbed + ((long)r * p.heads + h) * p.latent, lane, qa[i]);
-            } else {
-#pragma unroll
-                for (int e = 0; e < LPL; ++e) qa[i][e] = 0.0f;
-            }
-            qr[i] = (hv && lane < p.rope)
-                        ? p.query_rope[((long)r * p.heads + h) * p.rope + lane]
-                        : 0.0f;
-        }
-        float sc[KB * HP];
-#pragma unroll
-        for (int b = 0; b < KB; ++b)
-#pragma unroll
-            for (int i = 0; i < HP; ++i) {
-                float a = qr[i] * rv[b];
-#pragma unroll
-                for (int e = 0; e < LPL; ++e) a = fmaf(qa[i][e], lv[b][e], a);
-                sc[b * HP + i] = a;
-            }
-        butterfly_reduce<KB * HP, 64>(sc, lane);
-        const int vi = butterfly_index<KB * HP, 64>(lane);
-        const int b = vi / HP, i = vi % HP;
-        if (butterfly_writer<KB * HP, 64>(lane) && wave * KB + b < nk)
-            prob[wave * KB + b][hp + i] = sc[0] * p.scale;
-    }
-    __syncthreads();
-    {  // local softmax statistics: 16 lanes per head
-        const int h = t >> 4, sub = t & 15;
-        float m = -INFINITY;
-        for (int j = sub; j < nk; j += 16) m = fmaxf(m, prob[j][h]);
-#pragma unroll
-        for (int o = 8; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
-        float sum = 0.0f;
-        for (int j = sub; j < nk; j += 16) {
-            const float e = expf(prob[j][h] - m);
-            prob[j][h] = e;
-            sum += e;
-        }
-#pragma unroll
-        for (int o = 8; o >= 1; o >>= 1) sum += __shfl_xor(sum, o, 64);
-        if (sub == 0) {
-            smax[h] = m;
-            ssum[h] = sum;
-        }
-    }
-    __syncthreads();
-    if (t < H) {
-        p.part_max[part + t] = smax[t];
-        p.part_sum[part + t] = ssum[t];
-    }
-    for (int l = t; l < p.latent; l += blockDim.x) {
-        float acc[H];
-#pragma unroll
-        for (int h = 0; h < H; ++h) acc[h] = 0.0f;
-        for (int j = 0; j < nk; ++j) {
-            const float v = lat_s[j * p.latent + l];
-            const f32x4 *pj = reinterpret_cast<const f32x4 *>(prob[j]);
-#pragma unroll
-            for (int g = 0; g < H / 4; ++g) {
-                const f32x4 w = pj[g];
-                acc[4 * g + 0] = fmaf(w.x, v, acc[4 * g + 0]);
-                acc[4 * g + 1] = fmaf(w.y, v, acc[4 * g + 1]);
-                acc[4 * g + 2] = fmaf(w.z, v, acc[4 * g + 2]);
-                acc[4 * g + 3] = fmaf(w.w, v, acc[4 * g + 3]);
-            }
-        }
-#pragma unroll
-        for (int h = 0; h < H; ++h)
-            if (h < p.heads) p.part_lc[(part + h) * p.latent + l] = acc[h];
-    }
-}
 
 // The same split of kMlaKeysPerSplit keys on fp32 matrix cores
 // (v_mfma_f32_16x16x4_f32: fp32 products and sums, like the VALU form, in
@@ -938,16 +792,6 @@ __global__ __launch_bounds__(256) void mla_value_kernel(MlaParams p) {
         p.context[((long)r * p.heads + h) * p.vdim + v0 + vi] = acc[0];
 }
 
-template <int LPL>
-static void launch_attend(dim3 grid, size_t lds, hipStream_t stream, const MlaParams &p) {
-    static const bool attr = [] {
-        return hipFuncSetAttribute(reinterpret_cast<const void *>(&mla_attend_kernel<LPL>),
-                                   hipFuncAttributeMaxDynamicSharedMemorySize,
-                                   kAttendLdsBytes) == hipSuccess;
-    }();
-    (void)attr;
-    hipLaunchKernelGGL(mla_attend_kernel<LPL>, grid, dim3(256), lds, stream, p);
-}
 
 int mla_attention_core(const MlaParams &p, hipStream_t stream) {
     if (p.heads <= 0 || p.heads > kMlaMaxHeads || p.latent <= 0 || p.latent % 64 ||
@@ -958,9 +802,9 @@ int mla_attention_core(const MlaParams &p, hipStream_t stream) {
         (p.position + p.rows + kMlaKeysPerSplit - 1) / kMlaKeysPerSplit > p.max_splits ||
         (p.grid_splits && (!p.position_dev || p.grid_splits > p.max_splits)))
         return kErrArgs;
-    const bool mfma = p.rope % 4 == 0 && (p.latent + p.rope) % 16 == 0 &&
-                      p.latent + p.rope <= kAttnDims;
-    if (mfma && p.rows > 1 && !p.grid_splits && p.nope % 16 == 0 && p.vdim % 16 == 0) {
+    // the fp32-MFMA score tiles take 16 dims per step (mla_session_shape_ok)
+    if (p.rope % 16 || p.latent + p.rope > kAttnDims) return kErrArgs;
+    if (p.rows > 1 && !p.grid_splits && p.nope % 16 == 0 && p.vdim % 16 == 0) {
         // prefill: cache append + query rope, the absorb as a per-head GEMM,
         // flash attention writing lc directly, the value as a per-head GEMM
         constexpr int RB = kPfRowsPerGroup;
@@ -985,22 +829,11 @@ int mla_attention_core(const MlaParams &p, hipStream_t stream) {
     const int splits = p.grid_splits ? p.grid_splits
                                      : (p.position + p.rows + kMlaKeysPerSplit - 1) / kMlaKeysPerSplit;
     const dim3 grid(splits, p.rows);
-    const size_t lds = (size_t)kMlaKeysPerSplit * p.latent * sizeof(float);
-    if (mfma) {
-        static const bool attr = hipFuncSetAttribute(
-            reinterpret_cast<const void *>(&mla_attend_mfma_kernel),
-            hipFuncAttributeMaxDynamicSharedMemorySize, (int)kAttnMfmaLds) == hipSuccess;
-        (void)attr;
-        hipLaunchKernelGGL(mla_attend_mfma_kernel, grid, dim3(512), kAttnMfmaLds, stream, p);
-    } else {
-        switch (p.latent / 64) {
-        case 1: launch_attend<1>(grid, lds, stream, p); break;
-        case 2: launch_attend<2>(grid, lds, stream, p); break;
-        case 4: launch_attend<4>(grid, lds, stream, p); break;
-        case 8: launch_attend<8>(grid, lds, stream, p); break;
-        default: return kErrArgs;
-        }
-    }
+    static const bool attr = hipFuncSetAttribute(
+        reinterpret_cast<const void *>(&mla_attend_mfma_kernel),
+        hipFuncAttributeMaxDynamicSharedMemorySize, (int)kAttnMfmaLds) == hipSuccess;
+    (void)attr;
+    hipLaunchKernelGGL(mla_attend_mfma_kernel, grid, dim3(512), kAttnMfmaLds, stream, p);
     hipLaunchKernelGGL(mla_merge_kernel, dim3(p.rows, p.heads, p.latent / kMergeDims), dim3(512),
                        0, stream, p);
     hipLaunchKernelGGL(mla_value_kernel, dim3(p.rows, p.heads, (p.vdim + 31) / 32), dim3(256), 0,

@@ -11,13 +11,6 @@ namespace mlh {
 constexpr int kRouteMaxPositions = 16384;
 int route_topk(const RouteParams &p, hipStream_t stream);
 
-// Router matvec (f32 router [experts][width], x RMSNorm'ed with norm_w) and
-// routing of at most kFusedRouteMaxRows token rows in one launch; `counter` is
-// a device word that is 0 between calls.
-constexpr int kFusedRouteMaxRows = 4;
-int router_route(const RouteParams &p, const float *x, const float *norm_w, float eps,
-                 const float *router, int width, unsigned *counter, hipStream_t stream);
-
 // f32 router logits of many token rows, x RMSNorm'ed with norm_w when it is
 // non-null: logits [rows, experts].
 int router_logits(const float *x, const float *norm_w, float eps, const float *w, int rows,

@@ -34,103 +34,6 @@ __global__ __launch_bounds__(256) void route_kernel(RouteParams p) {
     small_tables(p, L);
 }
 
-// Decode: the router matvec and the routing in one launch.  Workgroup g
-// computes the logits of experts 4g .. 4g + 3 for every row (a wave per
-// expert, x RMSNorm'ed on the fly, k order per lane then a wave sum); the
-// last workgroup to finish (device counter, fenced) routes the rows and builds
-// the tables, then re-arms the counter.
-__global__ __launch_bounds__(256) void router_route_kernel(RouteParams p, const float *x,
-                                                           const float *norm_w, float eps,
-                                                           const float *router, int width,
-                                                           unsigned *counter) {
-    __shared__ RouteLds L;
-    __shared__ float inv_rms[kFusedRouteMaxRows];
-    __shared__ bool last;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int e = blockIdx.x * 4 + wave;
-    float* logits = const_cast<float *>(p.logits);
-    // RMSNorm statistics of the rows (each workgroup computes them)
-    if (wave < p.rows) {
-        float ss = 0.0f;
-        if (norm_w) {
-            for (int i0 = lane * 4; i0 < width; i0 += 256 * 8) {
-                f32x4 v[8];
-#pragma unroll
-                for (int b = 0; b < 8; ++b) {
-                    const int i = i0 + 256 * b;
-                    v[b] = i < width ? load_f4(x + (long)wave * width + i)
-                                     : f32x4{0.f, 0.f, 0.f, 0.f};
-                }
-#pragma unroll
-                for (int b = 0; b < 8; ++b)
-                    ss += v[b].x * v[b].x + v[b].y * v[b].y + v[b].z * v[b].z + v[b].w * v[b].w;
-            }
-        }
-        ss = wave_sum(ss);
-        if (lane == 0) inv_rms[wave] = norm_w ? 1.0f / sqrtf(ss / (float)width + eps) : 1.0f;
-    }
-    __syncthreads();
-    if (e < p.experts) {
-        const float *wr = router + (long)e * width;
-        for (int r = 0; r < p.rows; ++r) {
-            const float *xr = x + (long)r * width;
-            float acc = 0.0f;
-            for (int i0 = lane * 4; i0 < width; i0 += 256 * 8) {
-                f32x4 wv[8], xv[8], nv[8];
-#pragma unroll
-                for (int b = 0; b < 8; ++b) {
-                    const int i = i0 + 256 * b;
-                    const bool ok = i < width;
-                    wv[b] = ok ? load_f4(wr + i) : f32x4{0.f, 0.f, 0.f, 0.f};
-                    xv[b] = ok ? load_f4(xr + i) : f32x4{0.f, 0.f, 0.f, 0.f};
-                    nv[b] = (ok && norm_w) ? load_f4(norm_w + i) : f32x4{1.f, 1.f, 1.f, 1.f};
-                }
-#pragma unroll
-                for (int b = 0; b < 8; ++b) {
-                    const float rs = inv_rms[r];
-                    acc = fmaf(xv[b].x * rs * nv[b].x, wv[b].x, acc);
-                    acc = fmaf(xv[b].y * rs * nv[b].y, wv[b].y, acc);
-                    acc = fmaf(xv[b].z * rs * nv[b].z, wv[b].z, acc);
-                    acc = fmaf(xv[b].w * rs * nv[b].w, wv[b].w, acc);
-                }
-            }
-            acc = wave_sum(acc);
-            if (lane == 0) logits[(long)r * p.experts + e] = acc;
-        }
-    }
-    // last workgroup: everything above is visible to it after the fences
-    __threadfence();
-    __syncthreads();
-    if (threadIdx.x == 0) last = atomicAdd(counter, 1u) == gridDim.x - 1;
-    __syncthreads();
-    if (!last) return;
-    __threadfence();
-    if (p.rows == 1 && p.experts <= 64) {
-        if (wave == 0) {
-            route_single_64(p, lane);
-            if (lane == 0) atomicExch(counter, 0u);
-        }
-        return;
-    }
-    for (int r = wave; r < p.rows; r += 4) route_any(p, r, lane, L.ids);
-    __syncthreads();
-    small_tables(p, L);
-    if (threadIdx.x == 0) atomicExch(counter, 0u);
-}
-
-int router_route(const RouteParams &p, const float *x, const float *norm_w, float eps,
-                 const float *router, int width, unsigned *counter, hipStream_t stream) {
-    if (!p.logits || !p.bias || !p.ids || !p.weights || p.rows <= 0 ||
-        p.rows > kFusedRouteMaxRows || p.experts <= 0 || p.experts > kMaxExperts ||
-        p.top_k <= 0 || p.top_k > kMaxTopK || p.top_k > p.experts || !p.n_unique ||
-        !p.unique || !p.counts || !p.offsets || !p.list_rows || !p.list_slots ||
-        !p.list_pos || !p.error || !x || !router || !counter || width <= 0 || width % 4)
-        return kErrArgs;
-    hipLaunchKernelGGL(router_route_kernel, dim3((p.experts + 3) / 4), dim3(256), 0, stream, p,
-                       x, norm_w, eps, router, width, counter);
-    return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
-}
-
 // Larger batches: one wave per token row over many workgroups; the tables
 // follow in route_lists_kernel.
 __global__ __launch_bounds__(256) void route_select_kernel(RouteParams p) {

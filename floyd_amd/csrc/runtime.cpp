@@ -121,7 +121,6 @@ struct MoonlightSession {
     // pre-split limb rows of the expert GEMV inputs (batches of 2+ rows)
     unsigned char *limb_x = nullptr, *limb_xs = nullptr, *limb_h = nullptr, *limb_sh = nullptr;
     long limb_x_stride = 0, limb_h_stride = 0, limb_sh_stride = 0;
-    unsigned *route_counter = nullptr;   // last-workgroup counter of the fused routing
     float *expert_hidden = nullptr, *expert_out = nullptr;
     float *shared_hidden = nullptr, *shared_out = nullptr, *dense_hidden = nullptr;
     float *moe_routed = nullptr;  // routed part of moonlight_test_moe
@@ -1038,17 +1037,6 @@ static int presplit_min_rows() {
     return v;
 }
 
-// Decode batches: router matvec and routing in one launch (last-workgroup
-// pattern) or as two launches (measured faster: the fused form pays a device
-// scope release per workgroup).  MLH_FUSED_ROUTE=1 selects one (read once).
-static bool fused_route_enabled() {
-    static const bool v = [] {
-        const char *env = getenv("MLH_FUSED_ROUTE");
-        return env && atoi(env) != 0;
-    }();
-    return v;
-}
-
 // The MFMA router (32 x 32 tiles, one workgroup per tile) has the
 // parallelism for prefill batches; fewer rows take the GEMV.
 constexpr int kRouterMfmaMinRows = 256;
@@ -1056,24 +1044,7 @@ constexpr int kRouterMfmaMinRows = 256;
 // fixed: the MoE test / timing hooks take the caller's expert ids when set
 // (moonlight_session_fix_routes); forward passes always route by top-k.
 // Single-row batches with at most 64 experts route inside the first expert
-// launch unless MLH_INLINE_ROUTE=0 (read once).
-// One-row MoE layers run the down projections and the combine as one launch
-// (MLH_FUSED_DOWN=0: the grouped down GEMV and a separate combine).
-static bool fused_down_enabled() {
-    static const bool v = [] {
-        const char *env = getenv("MLH_FUSED_DOWN");
-        return !env || atoi(env) != 0;
-    }();
-    return v;
-}
-
-static bool inline_route_enabled() {
-    static const bool v = [] {
-        const char *env = getenv("MLH_INLINE_ROUTE");
-        return !env || atoi(env) != 0;
-    }();
-    return v;
-}
+// launch, and their down projections and combine run as one launch.
 
 // With `inline_route`, a single-row batch with at most 64 experts gets only
 // its router logits here; the selection and the route tables are left to
@@ -1097,18 +1068,13 @@ int route(MoonlightSession *s, int layer, const float *x, int rows, const float 
     const LayerPlan &lp = s->model->layers[layer];
     const bool f32_router = lp.router.fmt == kF32;
     const float *router_w = reinterpret_cast<const float *>(lp.router.w);
-    // decode batches: router matvec and routing in one launch
-    const bool fused = fused_route_enabled() && f32_router && rows <= kFusedRouteMaxRows &&
-                       c.hidden_size % 4 == 0;
-    if (!fused) {
-        if (rows >= kRouterMfmaMinRows && f32_router && c.hidden_size % 16 == 0) {
-            if (router_logits(x, norm_w, c.rms_norm_epsilon, router_w, rows, c.expert_count,
-                              c.hidden_size, s->router_logits, stream_of(s)))
-                return kErrLaunch;
-        } else if (gemv_rows(s, lp.router, x, rows, c.hidden_size, c.expert_count,
-                             s->router_logits, norm_w)) {
+    if (rows >= kRouterMfmaMinRows && f32_router && c.hidden_size % 16 == 0) {
+        if (router_logits(x, norm_w, c.rms_norm_epsilon, router_w, rows, c.expert_count,
+                          c.hidden_size, s->router_logits, stream_of(s)))
             return kErrLaunch;
-        }
+    } else if (gemv_rows(s, lp.router, x, rows, c.hidden_size, c.expert_count,
+                         s->router_logits, norm_w)) {
+        return kErrLaunch;
     }
     RouteParams r;
     r.logits = s->router_logits;
@@ -1133,17 +1099,13 @@ int route(MoonlightSession *s, int layer, const float *x, int rows, const float 
     r.expert_table = lp.expert_table;
     r.tasks = s->expert_tasks;
     r.task_slots = rows * r.top_k < r.experts ? rows * r.top_k : r.experts;
-    if (fused)
-        return router_route(r, x, norm_w, c.rms_norm_epsilon, router_w, c.hidden_size,
-                            s->route_counter, stream_of(s));
     if (inline_route) *inline_route = RouteParams{};
-    if (inline_route && inline_route_enabled() && rows == 1 && c.expert_count <= 64 &&
-        rows < presplit_min_rows()) {
+    if (inline_route && rows == 1 && c.expert_count <= 64 && rows < presplit_min_rows()) {
         *inline_route = r;
         return kOk;
     }
     // a few rows on the GEMM path: the first GEMM launch routes them
-    if (inline_route && inline_route_enabled() && rows <= kRouteOneGroupRows &&
+    if (inline_route && rows <= kRouteOneGroupRows &&
         rows * r.top_k <= kRouteFusedMaxPositions && r.top_k <= kMaxTopK &&
         r.experts <= kMaxExperts && moe_uses_gemm(s, layer, rows)) {
         *inline_route = r;
@@ -1247,7 +1209,7 @@ int experts(MoonlightSession *s, int layer, const float *x, int rows, const floa
         g.shared_out = f.shared_out;
         if (int e = moe_gemm(g, stream_of(s))) return e;
     } else {
-        const bool fused_down = fused_down_enabled() && down_combine_ok(f);
+        const bool fused_down = down_combine_ok(f);
         if (fused_down) {
             f.combine_out = out;
             f.combine_resid = resid;
@@ -1463,7 +1425,10 @@ extern "C" int moonlight_session_create(MoonlightSession **out, MoonlightModel *
     if (c.kv_lora_rank > 512 || c.qk_rope_dim > 256 || (c.qk_rope_dim & 1) ||
         c.expert_count > 256 || c.experts_per_token > c.expert_count ||
         // limits of the HIP kernels (mla.h, moe.hip)
+        // (the attention's fp32-MFMA score tiles take the rope part 16 dims
+        // at a time)
         c.head_count > kMlaMaxHeads || c.kv_lora_rank % 64 || c.qk_rope_dim > 64 ||
+        c.qk_rope_dim % 16 ||
         c.qk_nope_dim > 256 || c.qk_nope_dim <= 0 || c.value_dim <= 0 || c.experts_per_token > 16)
         return set_error(error, error_size, "unsupported Moonlight MLA dimensions");
     if (c.q_lora_rank)
@@ -1534,8 +1499,6 @@ extern "C" int moonlight_session_create(MoonlightSession **out, MoonlightModel *
         session_alloc(s, &s->limb_xs, mb * s->limb_x_stride, error, error_size) &&
         session_alloc(s, &s->limb_h, mb * K * s->limb_h_stride, error, error_size) &&
         session_alloc(s, &s->limb_sh, mb * s->limb_sh_stride, error, error_size) &&
-        session_alloc(s, &s->route_counter, 1, error, error_size) &&
-        hipMemset(s->route_counter, 0, sizeof(unsigned)) == hipSuccess &&
         session_alloc(s, &s->route_trace, L * mb * K, error, error_size) &&
         session_alloc(s, &s->expert_hidden, mb * K * (size_t)c.moe_intermediate_size, error,
                       error_size) &&
