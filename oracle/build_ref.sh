@@ -20,10 +20,12 @@ echo "build_ref: built $OUT/libref_moe.so $OUT/libref_model.so"
 
 # The reference's own boundary tests, compiled unchanged from their sources
 # and linked against libfloyd_amd.so in place of moonlight_metal.m /
-# backend_metal.m: proof that the C ABI is a drop-in.  test_backend_metal
-# needs no fixtures and runs on the GPU (tests/test_reference_link_gpu.py);
-# the Moonlight tests need model/oracle fixture directories that do not exist
-# here, so they are only linked.
+# backend_metal.m: proof that the C ABI is a drop-in.  They run on the GPU
+# (tests/test_reference_link_gpu.py, tests/test_reference_moonlight_gpu.py)
+# against fixtures written by the CPU oracle (tests/golden/).  The runtime
+# test asserts an Apple device name (test_moonlight_metal_runtime.c:94); its
+# runnable build is made from a copy with that one string changed to
+# "gfx950", written into this build directory only.
 LIB="$HERE/../floyd_amd/lib"
 if [ -f "$LIB/libfloyd_amd.so" ]; then
     LINK="-L$LIB -lfloyd_amd -Wl,-rpath,\$ORIGIN/../../floyd_amd/lib -lm"
@@ -32,5 +34,11 @@ if [ -f "$LIB/libfloyd_amd.so" ]; then
         gcc -O2 -w -fopenmp -I"$REF" -o "$OUT/test_moonlight_metal_$t" \
             "$REF/tests/test_moonlight_metal_$t.c" "$REF/moonlight_model.c" $LINK
     done
+    sed 's/moonlight_device_name(model), "Apple"/moonlight_device_name(model), "gfx950"/' \
+        "$REF/tests/test_moonlight_metal_runtime.c" > "$OUT/runtime_device_patched.c"
+    grep -q '"gfx950"' "$OUT/runtime_device_patched.c"
+    gcc -O2 -w -fopenmp -I"$REF" -I"$REF/tests" -o "$OUT/test_moonlight_metal_runtime_gfx950" \
+        "$OUT/runtime_device_patched.c" "$REF/moonlight_model.c" $LINK
+    rm -f "$OUT/runtime_device_patched.c"
     echo "build_ref: linked the reference's backend and Moonlight tests against libfloyd_amd.so"
 fi
