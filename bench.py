@@ -290,6 +290,21 @@ def full_prefill(model, extra, rows=2048):
     sess.close()
 
 
+def moe_only():
+    """Config 2 only: the MoE layer at T = 1, 8, 64 (profiler runs)."""
+    from floyd_amd import session as S
+    model = S.Model.synthetic()
+    sess = S.Session(model, 128, 64)
+    out = {}
+    for rows in (1, 8, 64):
+        us, uniq = sess.time_moe(1, rows, seed=rows, warmup=5, iters=20)
+        out[f"T{rows}"] = {"us": round(us, 2), "unique_experts": uniq}
+        print(f"[bench] MoE layer T={rows}: {us:.1f} us, U={uniq}", file=sys.stderr, flush=True)
+    sess.close()
+    model.close()
+    print(json.dumps(out), flush=True)
+
+
 def prefill_only():
     """Config 3 (MoE prefill layer, q8 and q4) and the 2048-token full-model
     prefill, one JSON line (profiler runs and quick checks)."""
@@ -463,6 +478,8 @@ def main():
     parser.add_argument("--load-only", type=int, default=0, metavar="LAYERS",
                         help="only time moonlight_model_open on a Moonlight-shaped q8 "
                              "container of LAYERS layers written under $TMPDIR")
+    parser.add_argument("--moe-only", action="store_true",
+                        help="only config 2 (MoE decode layer at T = 1, 8, 64)")
     parser.add_argument("--prefill-only", action="store_true",
                         help="only config 3 (MoE prefill q8 / q4) and the 2048-token prefill")
     parser.add_argument("--decode-only", type=int, default=0, metavar="CTX",
@@ -486,6 +503,9 @@ def main():
         return
     if args.prefill_only:
         prefill_only()
+        return
+    if args.moe_only:
+        moe_only()
         return
 
     # headline: benchmark config 1, q4 [11264 x 2048], batch 1

@@ -36,8 +36,10 @@ struct GemmTask {
     const uint8_t *w = nullptr, *w2 = nullptr;  // [n_out][k] packed (w2: up rows, SwiGLU)
     const float *s = nullptr, *s2 = nullptr;    // per weight row scales
     int rows = 0, n_out = 0, k = 0;
-    // quantised activations (limbs hi, mid, lo), row stride a_stride
-    const int8_t *a_hi = nullptr, *a_mid = nullptr, *a_lo = nullptr;
+    // quantised activations: limb l (0 hi, 1 mid, 2 lo) of row r at
+    // a + l * a_plane + r * a_stride
+    const int8_t *a = nullptr;
+    long a_plane = 0;
     const float *a_scale = nullptr;
     long a_stride = 0;
     const int *a_rows = nullptr;  // optional: activation row of token row m
@@ -57,10 +59,10 @@ struct QGemmLaunch {
 
 // Per-row activation quantisation (optionally RMSNorm'ed first,
 // moonlight_kernels.metal:23-41): rows of `x` (stride x_stride floats) ->
-// hi/mid/lo limbs (row stride `width` bytes) and scales.
+// limbs hi, mid, lo at q, q + plane, q + 2 plane (row stride `width` bytes)
+// and scales.
 int quantize_activations(const float *x, long x_stride, int rows, int width, const float *norm_w,
-                         float eps, int8_t *hi, int8_t *mid, int8_t *lo, float *scale,
-                         hipStream_t stream);
+                         float eps, int8_t *q, long plane, float *scale, hipStream_t stream);
 
 // One dense task, e.g. a prefill projection.  Epilogue: plain or residual
 // (task.resid) or SwiGLU pair (dual, task.w2 = up).
@@ -85,12 +87,16 @@ struct MoeGemmParams {
     const float *norm_w = nullptr;
     float eps = 1e-5f;
     // scratch
-    int8_t *xq_hi = nullptr, *xq_mid = nullptr, *xq_lo = nullptr;  // [rows, hidden]
-    float *xq_scale = nullptr;                   // [rows]
-    int8_t *hq_hi = nullptr, *hq_mid = nullptr, *hq_lo = nullptr;  // [rows*top_k, inter]
-    float *hq_scale = nullptr;                   // [rows*top_k]
-    int8_t *sq_hi = nullptr, *sq_mid = nullptr, *sq_lo = nullptr;  // [rows, shared_width]
-    float *sq_scale = nullptr;                   // [rows]
+    // three limb planes each (limb l at base + l * plane)
+    int8_t *xq = nullptr;  // [3][rows, hidden]
+    long xq_plane = 0;
+    float *xq_scale = nullptr;  // [rows]
+    int8_t *hq = nullptr;  // [3][rows*top_k, inter]
+    long hq_plane = 0;
+    float *hq_scale = nullptr;  // [rows*top_k]
+    int8_t *sq = nullptr;  // [3][rows, shared_width]
+    long sq_plane = 0;
+    float *sq_scale = nullptr;  // [rows]
     GemmTask *tasks = nullptr;                   // [2][kQgMaxTasks]
     int *tile_start = nullptr;                   // [2][kQgMaxTasks + 1]
     // outputs (same layouts as the GEMV expert path)

@@ -53,15 +53,16 @@ __device__ __forceinline__ unsigned pack_bytes(int a, int b, int c, int d) {
 constexpr int kQuantRegChunks = 16;
 
 // One set of rows to quantise: x (row stride x_stride, optionally
-// RMSNorm'ed with norm_w) -> hi / mid / lo limbs (row stride width) and
-// scales.
+// RMSNorm'ed with norm_w) -> limbs hi, mid, lo at q, q + plane, q + 2 plane
+// (row stride width) and scales.
 struct QuantSeg {
     const float *x = nullptr;
     long x_stride = 0;
     int rows = 0, width = 0;
     const float *norm_w = nullptr;
     float eps = 0.0f;
-    int8_t *hi = nullptr, *mid = nullptr, *lo = nullptr;
+    int8_t *q = nullptr;
+    long plane = 0;
     float *scale = nullptr;
 };
 
@@ -71,7 +72,7 @@ __device__ __forceinline__ void quantize_row(const QuantSeg &s, int row) {
     const float *x = s.x, *norm_w = s.norm_w;
     const int width = s.width;
     const float eps = s.eps;
-    int8_t *hi = s.hi, *mid = s.mid, *lo = s.lo;
+    int8_t *hi = s.q, *mid = s.q + s.plane, *lo = s.q + 2 * s.plane;
     float *scale = s.scale;
     const int lane = threadIdx.x & (kWave - 1);
     const float *xr = x + (long)row * s.x_stride;
@@ -150,7 +151,8 @@ __global__ __launch_bounds__(256) void quantize_act_kernel(QuantSeg a, QuantSeg 
 }
 
 static bool quant_seg_ok(const QuantSeg &s) {
-    return s.rows == 0 || (s.x && s.hi && s.mid && s.lo && s.scale && s.rows > 0 && s.width > 0 &&
+    return s.rows == 0 || (s.x && s.q && s.plane >= (long)s.rows * s.width && s.scale &&
+                           s.rows > 0 && s.width > 0 &&
                            s.width % 4 == 0 && s.x_stride % 4 == 0);
 }
 
@@ -169,9 +171,8 @@ static int quantize_segments(const QuantSeg &a, const QuantSeg &b, hipStream_t s
 }
 
 int quantize_activations(const float *x, long x_stride, int rows, int width, const float *norm_w,
-                         float eps, int8_t *hi, int8_t *mid, int8_t *lo, float *scale,
-                         hipStream_t stream) {
-    if (!x || !hi || !mid || !lo || !scale || rows <= 0 || width <= 0) return kErrArgs;
+                         float eps, int8_t *q, long plane, float *scale, hipStream_t stream) {
+    if (!x || !q || !scale || rows <= 0 || width <= 0) return kErrArgs;
     QuantSeg a;
     a.x = x;
     a.x_stride = x_stride;
@@ -179,9 +180,8 @@ int quantize_activations(const float *x, long x_stride, int rows, int width, con
     a.width = width;
     a.norm_w = norm_w;
     a.eps = eps;
-    a.hi = hi;
-    a.mid = mid;
-    a.lo = lo;
+    a.q = q;
+    a.plane = plane;
     a.scale = scale;
     return quantize_segments(a, QuantSeg{}, stream);
 }
@@ -381,8 +381,12 @@ __global__ __launch_bounds__((QgShape<FMT, BM>::kThreads), BM == 128 ? 1 : 2) vo
         const int out = b_out(j, up);
         return (up ? w_up : w_gate) + (long)(out < tk.n_out ? out : 0) * w_row_bytes;
     };
-    auto limb_base = [&](int limb) -> const int8_t * {
-        return limb == 0 ? tk.a_hi : (limb == 1 ? tk.a_mid : tk.a_lo);
+    // limb planes at a fixed distance: the limb of an address is arithmetic,
+    // not a choice between pointers (which would put them in scratch memory)
+    const int8_t *const a_base = tk.a;
+    const long a_plane = tk.a_plane;
+    auto limb_base = [a_base, a_plane](int limb) -> const int8_t * {
+        return a_base + limb * a_plane;
     };
     auto a_row_src = [&](int limb, int r) -> const int8_t * {
         const int arow = lds_arow[r] >= 0 ? lds_arow[r] : lds_arow[0];
@@ -702,7 +706,8 @@ static int host_tiles(bool dual, int rows, int n_out, int bm) {
 
 int qgemm_single(int fmt, bool dual, const GemmTask &task, hipStream_t stream) {
     if (!qgemm_shape_ok(fmt, task.k) || task.rows <= 0 || task.n_out <= 0 || !task.w ||
-        !task.s || !task.a_hi || !task.a_mid || !task.a_lo || !task.a_scale || !task.y ||
+        !task.s || !task.a || task.a_plane < (long)task.rows * task.a_stride || !task.a_scale ||
+        !task.y ||
         (dual && (!task.w2 || !task.s2)) || task.a_stride % 16)
         return kErrArgs;
     QGemmLaunch L;
@@ -741,9 +746,8 @@ __device__ __forceinline__ void moe_schedule_body(const MoeScheduleParams &sp) {
         a.rows = cnt;
         a.n_out = p.inter;
         a.k = p.hidden;
-        a.a_hi = p.xq_hi;
-        a.a_mid = p.xq_mid;
-        a.a_lo = p.xq_lo;
+        a.a = p.xq;
+        a.a_plane = p.xq_plane;
         a.a_scale = p.xq_scale;
         a.a_stride = p.hidden;
         a.a_rows = p.list_rows + off;
@@ -758,9 +762,8 @@ __device__ __forceinline__ void moe_schedule_body(const MoeScheduleParams &sp) {
         b.rows = cnt;
         b.n_out = p.hidden;
         b.k = p.inter;
-        b.a_hi = p.hq_hi + (long)off * p.inter;
-        b.a_mid = p.hq_mid + (long)off * p.inter;
-        b.a_lo = p.hq_lo + (long)off * p.inter;
+        b.a = p.hq + (long)off * p.inter;
+        b.a_plane = p.hq_plane;
         b.a_scale = p.hq_scale + off;
         b.a_stride = p.inter;
         b.y = p.expert_out + (long)off * p.hidden;
@@ -781,9 +784,8 @@ __device__ __forceinline__ void moe_schedule_body(const MoeScheduleParams &sp) {
             a.rows = p.rows;
             a.n_out = p.shared_width;
             a.k = p.hidden;
-            a.a_hi = p.xq_hi;
-            a.a_mid = p.xq_mid;
-            a.a_lo = p.xq_lo;
+            a.a = p.xq;
+            a.a_plane = p.xq_plane;
             a.a_scale = p.xq_scale;
             a.a_stride = p.hidden;
             a.y = p.shared_hidden;
@@ -797,9 +799,8 @@ __device__ __forceinline__ void moe_schedule_body(const MoeScheduleParams &sp) {
             b.rows = p.rows;
             b.n_out = p.hidden;
             b.k = p.shared_width;
-            b.a_hi = p.sq_hi;
-            b.a_mid = p.sq_mid;
-            b.a_lo = p.sq_lo;
+            b.a = p.sq;
+            b.a_plane = p.sq_plane;
             b.a_scale = p.sq_scale;
             b.a_stride = p.shared_width;
             b.y = p.shared_out;
@@ -871,11 +872,10 @@ int moe_gemm(const MoeGemmParams &p, hipStream_t stream) {
     xs.width = p.hidden;
     xs.norm_w = p.norm_w;
     xs.eps = p.eps;
-    xs.hi = p.xq_hi;
-    xs.mid = p.xq_mid;
-    xs.lo = p.xq_lo;
+    xs.q = p.xq;
+    xs.plane = p.xq_plane;
     xs.scale = p.xq_scale;
-    if (!p.x || !p.xq_hi || !p.xq_mid || !p.xq_lo || !p.xq_scale || !quant_seg_ok(xs))
+    if (!p.x || !p.xq || !p.xq_scale || !quant_seg_ok(xs))
         return kErrArgs;
     if (p.route_in_prep &&
         (p.route.rows != p.rows || p.rows > kRouteOneGroupRows || !p.route.logits ||
@@ -927,18 +927,16 @@ int moe_gemm(const MoeGemmParams &p, hipStream_t stream) {
             hs.x_stride = p.inter;
             hs.rows = entries;
             hs.width = p.inter;
-            hs.hi = p.hq_hi;
-            hs.mid = p.hq_mid;
-            hs.lo = p.hq_lo;
+            hs.q = p.hq;
+            hs.plane = p.hq_plane;
             hs.scale = p.hq_scale;
             if (p.has_shared) {
                 ss.x = p.shared_hidden;
                 ss.x_stride = p.shared_width;
                 ss.rows = p.rows;
                 ss.width = p.shared_width;
-                ss.hi = p.sq_hi;
-                ss.mid = p.sq_mid;
-                ss.lo = p.sq_lo;
+                ss.q = p.sq;
+                ss.plane = p.sq_plane;
                 ss.scale = p.sq_scale;
             }
             st = quantize_segments(hs, ss, stream);

@@ -125,12 +125,14 @@ struct MoonlightSession {
     float *shared_hidden = nullptr, *shared_out = nullptr, *dense_hidden = nullptr;
     float *moe_routed = nullptr;  // routed part of moonlight_test_moe
     // MFMA path for batches of >= kMoeGemmMinRows token rows (prefill)
-    // quantised activations (three limbs) [max_batch][aq_width]
-    int8_t *aq_hi = nullptr, *aq_mid = nullptr, *aq_lo = nullptr;
+    // quantised activations: three limb planes [3][max_batch][aq_width]
+    int8_t *aq = nullptr;
+    long aq_plane = 0;
     float *aq_scale = nullptr;
     int aq_width = 0;
-    // quantised expert hidden (three limbs) [max_batch*K][inter]
-    int8_t *hq_hi = nullptr, *hq_mid = nullptr, *hq_lo = nullptr;
+    // quantised expert hidden: three limb planes [3][max_batch*K][inter]
+    int8_t *hq = nullptr;
+    long hq_plane = 0;
     float *hq_scale = nullptr;
     GemmTask *gemm_tasks = nullptr;
     int *gemm_tile_start = nullptr;
@@ -889,14 +891,14 @@ constexpr int kGemmMinRows = 16;
 constexpr int kMoeGemmMinRows = 5;
 
 bool use_gemm(const MoonlightSession *s, int fmt, int rows, int in_w) {
-    return rows >= kGemmMinRows && s->aq_hi && in_w <= s->aq_width && qgemm_shape_ok(fmt, in_w);
+    return rows >= kGemmMinRows && s->aq && in_w <= s->aq_width && qgemm_shape_ok(fmt, in_w);
 }
 
 int gemm_rows(MoonlightSession *s, const Matrix &m, const Matrix *up, const float *x, int rows,
               int in_w, int out_w, float *y, const float *norm_w, const float *resid) {
     hipStream_t st = stream_of(s);
     if (int e = quantize_activations(x, in_w, rows, in_w, norm_w, s->model->cfg.rms_norm_epsilon,
-                                     s->aq_hi, s->aq_mid, s->aq_lo, s->aq_scale, st))
+                                     s->aq, s->aq_plane, s->aq_scale, st))
         return e;
     GemmTask t;
     t.w = m.w;
@@ -908,9 +910,8 @@ int gemm_rows(MoonlightSession *s, const Matrix &m, const Matrix *up, const floa
     t.rows = rows;
     t.n_out = out_w;
     t.k = in_w;
-    t.a_hi = s->aq_hi;
-    t.a_mid = s->aq_mid;
-    t.a_lo = s->aq_lo;
+    t.a = s->aq;
+    t.a_plane = s->aq_plane;
     t.a_scale = s->aq_scale;
     t.a_stride = in_w;
     t.y = y;
@@ -1056,7 +1057,7 @@ static bool moe_uses_gemm(const MoonlightSession *s, int layer, int rows) {
     const ModelConfig &c = s->model->cfg;
     const LayerPlan &lp = s->model->layers[layer];
     const int sw = c.moe_intermediate_size * c.shared_expert_count;
-    return rows >= kMoeGemmMinRows && s->hq_hi && qgemm_shape_ok(lp.expert_fmt, c.hidden_size) &&
+    return rows >= kMoeGemmMinRows && s->hq && qgemm_shape_ok(lp.expert_fmt, c.hidden_size) &&
            qgemm_shape_ok(lp.expert_fmt, c.moe_intermediate_size) &&
            qgemm_shape_ok(lp.sh_gate.fmt, c.hidden_size) && qgemm_shape_ok(lp.sh_gate.fmt, sw) &&
            c.hidden_size <= s->aq_width && sw <= s->aq_width;
@@ -1193,13 +1194,11 @@ int experts(MoonlightSession *s, int layer, const float *x, int rows, const floa
         g.eps = f.eps;
         // the token-row quantisation is consumed by stage 0 before the shared
         // hidden is quantised into the same buffer
-        g.xq_hi = g.sq_hi = s->aq_hi;
-        g.xq_mid = g.sq_mid = s->aq_mid;
-        g.xq_lo = g.sq_lo = s->aq_lo;
+        g.xq = g.sq = s->aq;
+        g.xq_plane = g.sq_plane = s->aq_plane;
         g.xq_scale = g.sq_scale = s->aq_scale;
-        g.hq_hi = s->hq_hi;
-        g.hq_mid = s->hq_mid;
-        g.hq_lo = s->hq_lo;
+        g.hq = s->hq;
+        g.hq_plane = s->hq_plane;
         g.hq_scale = s->hq_scale;
         g.tasks = s->gemm_tasks;
         g.tile_start = s->gemm_tile_start;
@@ -1526,16 +1525,11 @@ extern "C" int moonlight_session_create(MoonlightSession **out, MoonlightModel *
         int aw = 0;
         for (int w : widths) aw = w > aw ? w : aw;
         s->aq_width = aw;
-        gemm_ok = session_alloc(s, &s->aq_hi, mb * (size_t)aw, error, error_size) &&
-                  session_alloc(s, &s->aq_mid, mb * (size_t)aw, error, error_size) &&
-                  session_alloc(s, &s->aq_lo, mb * (size_t)aw, error, error_size) &&
+        s->aq_plane = (long)(mb * (size_t)aw);
+        s->hq_plane = (long)(mb * K * (size_t)c.moe_intermediate_size);
+        gemm_ok = session_alloc(s, &s->aq, 3 * (size_t)s->aq_plane, error, error_size) &&
                   session_alloc(s, &s->aq_scale, mb, error, error_size) &&
-                  session_alloc(s, &s->hq_hi, mb * K * (size_t)c.moe_intermediate_size, error,
-                                error_size) &&
-                  session_alloc(s, &s->hq_mid, mb * K * (size_t)c.moe_intermediate_size, error,
-                                error_size) &&
-                  session_alloc(s, &s->hq_lo, mb * K * (size_t)c.moe_intermediate_size, error,
-                                error_size) &&
+                  session_alloc(s, &s->hq, 3 * (size_t)s->hq_plane, error, error_size) &&
                   session_alloc(s, &s->hq_scale, mb * K, error, error_size) &&
                   session_alloc(s, &s->gemm_tasks, 2 * (size_t)kQgMaxTasks, error, error_size) &&
                   session_alloc(s, &s->gemm_tile_start, 2 * (size_t)(kQgMaxTasks + 1), error,
