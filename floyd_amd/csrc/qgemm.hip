@@ -13,6 +13,7 @@
 // C[(r / 4) * 8 + (l / 32) * 4 + r % 4][l % 32].
 #include "qgemm.h"
 
+#include <cstdlib>
 #include <type_traits>
 
 namespace mlh {
@@ -219,6 +220,53 @@ __host__ __device__ __forceinline__ int tiles_of(int rows, int n_out) {
     return ((rows + BM - 1) / BM) * ((n_out + outw - 1) / outw);
 }
 
+// Tile blockIdx.x of a launch -> its task record and the first token row m0
+// and output n0 of its BM x 256 tile; false for workgroups past the tiles.
+// Tiles run in XCD-contiguous order (workgroup i goes to XCD i % 8): each XCD
+// takes a contiguous range of tiles, and within a task groups of kQgGroup row
+// tiles share one column tile, so neighbouring workgroups of an XCD reuse
+// weight tiles from its L2.
+template <bool DUAL, int BM>
+__device__ __forceinline__ bool map_tile(const QGemmLaunch &L, GemmTask &tk, int &m0, int &n0) {
+    int local;
+    {
+        int begin = 0, end;
+        int n_tasks = 1;
+        if (L.tasks) {
+            const int nr = *L.n_routed;
+            n_tasks = nr + 1;
+            end = L.range == 1 ? L.tile_start[nr] : L.tile_start[nr + 1];
+            if (L.range == 2) begin = L.tile_start[nr];
+        } else {
+            end = tiles_of<DUAL, BM>(L.single.rows, L.single.n_out);
+        }
+        const int total = end - begin;
+        const int per = (total + 7) >> 3;
+        const int slot = blockIdx.x >> 3;
+        if (slot >= per) return false;
+        const int tile = begin + (blockIdx.x & 7) * per + slot;
+        if (tile >= end) return false;
+        if (L.tasks) {
+            const int t = find_task(L.tile_start, n_tasks, tile);
+            tk = L.tasks[t];
+            local = tile - L.tile_start[t];
+        } else {
+            tk = L.single;
+            local = tile;
+        }
+    }
+    constexpr int outw = DUAL ? kQgBW / 2 : kQgBW;
+    const int n_tiles = (tk.n_out + outw - 1) / outw;
+    const int m_tiles = (tk.rows + BM - 1) / BM;
+    const int per_group = kQgGroup * n_tiles;
+    const int grp = local / per_group;
+    const int gsize = min(kQgGroup, m_tiles - grp * kQgGroup);
+    const int rem = local - grp * per_group;
+    m0 = (grp * kQgGroup + rem % gsize) * BM;
+    n0 = (rem / gsize) * outw;
+    return true;
+}
+
 // LDS tiles hold one k slice per stage as rows of RB bytes (RB / 16 chunks of
 // 16 bytes): q8 slices are 128 wide and go straight from global memory into
 // LDS (global_load_lds_dwordx4, full 128-byte lines per row); q4 slices are
@@ -299,44 +347,9 @@ __global__ __launch_bounds__((QgShape<FMT, BM>::kThreads), BM == 128 ? 1 : 2) vo
     constexpr bool kDma = FMT == kQ8;
     float *lds_scale = reinterpret_cast<float *>(qg_lds + kStages * kStage);
     int *lds_arow = reinterpret_cast<int *>(qg_lds + kStages * kStage + BM * 4);
-    // ---- tile -> (task, row tile, column tile), XCD-contiguous order
     GemmTask tk;
-    int local;
-    {
-        int begin = 0, end;
-        int n_tasks = 1;
-        if (L.tasks) {
-            const int nr = *L.n_routed;
-            n_tasks = nr + 1;
-            end = L.range == 1 ? L.tile_start[nr] : L.tile_start[nr + 1];
-            if (L.range == 2) begin = L.tile_start[nr];
-        } else {
-            end = tiles_of<DUAL, BM>(L.single.rows, L.single.n_out);
-        }
-        const int total = end - begin;
-        const int per = (total + 7) >> 3;
-        const int slot = blockIdx.x >> 3;
-        if (slot >= per) return;
-        const int tile = begin + (blockIdx.x & 7) * per + slot;
-        if (tile >= end) return;
-        if (L.tasks) {
-            const int t = find_task(L.tile_start, n_tasks, tile);
-            tk = L.tasks[t];
-            local = tile - L.tile_start[t];
-        } else {
-            tk = L.single;
-            local = tile;
-        }
-    }
-    constexpr int outw = DUAL ? kQgBW / 2 : kQgBW;
-    const int n_tiles = (tk.n_out + outw - 1) / outw;
-    const int m_tiles = (tk.rows + BM - 1) / BM;
-    const int per_group = kQgGroup * n_tiles;
-    const int grp = local / per_group;
-    const int gsize = min(kQgGroup, m_tiles - grp * kQgGroup);
-    const int rem = local - grp * per_group;
-    const int m0 = (grp * kQgGroup + rem % gsize) * BM;
-    const int n0 = (rem / gsize) * outw;
+    int m0, n0;
+    if (!map_tile<DUAL, BM>(L, tk, m0, n0)) return;
 
     constexpr int kThreads = Sh::kThreads;
     const int tid = threadIdx.x;
@@ -664,6 +677,227 @@ __global__ __launch_bounds__((QgShape<FMT, BM>::kThreads), BM == 128 ? 1 : 2) vo
     else epilogue(std::false_type{});
 }
 
+// ---------------------------------------------------------------------------
+// Weight-streaming tile (launches whose tasks hold few token rows, e.g. the
+// MoE layer of a decode batch): BM = 16 * MB token rows x 256 weight rows per
+// workgroup, each of its 4 waves owning 64 weight rows (4 blocks of 16) for
+// all BM rows, with no barrier.  Weights, read once, are the stream: a wave
+// copies its rows into a private LDS ring by DMA, 128 contiguous bytes of a
+// row per lane group (a DMA instruction covers 8 rows x 128 bytes: on MI355X
+// a plain read of such runs moves ~6 TB/s, of the 64-byte pieces an MFMA
+// fragment holds ~4.2 TB/s), kStages steps of 128 k ahead; the activation
+// limbs of the BM rows (L2-resident, shared by every tile of the task) load
+// straight into registers.  Products on v_mfma_i32_16x16x64_i8: lane l
+// supplies row / column l % 16 and the 16 k values 16 (l / 16) .. + 15 of a
+// 64-wide step, for activations (A) and weights (B) alike; result register r
+// of lane l is C[4 (l / 16) + r][l % 16].
+// ---------------------------------------------------------------------------
+
+template <int FMT, int MB> struct QsShape {
+    static constexpr int kBM = 16 * MB;
+    static constexpr int kStages = 2;                  // 128-k steps in flight
+    static constexpr int kRowBytes = FMT == kQ8 ? 128 : 64;  // weight bytes per row and step
+    static constexpr int kWaveStage = 64 * kRowBytes;        // one wave's rows per step
+    static constexpr int kLds = 4 * kStages * kWaveStage;
+    // per lane and step: weight DMA (64 rows of kRowBytes, 1 KB per
+    // instruction) + activation loads (2 slices x 3 limbs x MB row blocks)
+    static constexpr int kDma = kWaveStage / 1024;
+    static constexpr int kLoads = kDma + 2 * kLimbs * MB;
+    static_assert((kStages - 1) * kLoads <= 63, "vmcnt range");
+};
+
+typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+
+template <int FMT, bool DUAL, int MB>
+__global__ __launch_bounds__(256, 2) void qgemm_stream_kernel(QGemmLaunch L) {
+    using Sh = QsShape<FMT, MB>;
+    constexpr int BM = Sh::kBM;
+    constexpr int S = Sh::kStages;
+    constexpr int NL = Sh::kLoads;
+    constexpr int RB = Sh::kRowBytes;
+    extern __shared__ __attribute__((aligned(16))) unsigned char qs_lds[];
+    GemmTask tk;
+    int m0, n0;
+    if (!map_tile<DUAL, BM>(L, tk, m0, n0)) return;
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = threadIdx.x >> 6;
+    const int l16 = lane & 15, kq = lane >> 4;
+    unsigned char *my_lds = qs_lds + wave * S * Sh::kWaveStage;
+
+    // activation rows of this lane (A row l16 of each row block); rows past
+    // the task's end read its first row (their results are never stored)
+    const int8_t *a_src[MB];
+#pragma unroll
+    for (int i = 0; i < MB; ++i) {
+        const int m = m0 + 16 * i + l16;
+        const int mm = m < tk.rows ? m : m0;
+        const int arow = tk.a_rows ? tk.a_rows[mm] : mm;
+        a_src[i] = tk.a + (long)arow * tk.a_stride + 16 * kq;
+    }
+    // weight row of LDS row j (0..63) of this wave: SwiGLU tiles give a wave
+    // 32 gate rows (LDS rows 0..31) and the matching 32 up rows (32..63)
+    const long w_row_bytes = FMT == kQ8 ? tk.k : tk.k / 2;
+    auto w_row = [&](int j, int &n) -> const uint8_t * {
+        const uint8_t *base = tk.w;
+        if (DUAL) {
+            n = n0 + wave * 32 + (j & 31);
+            if (j >= 32) base = tk.w2;
+        } else {
+            n = n0 + wave * 64 + j;
+        }
+        const int nn = n < tk.n_out ? n : 0;
+        return base + (long)nn * w_row_bytes;
+    };
+    // DMA lane roles: instruction d covers LDS rows 8 d .. 8 d + 7 (q8) or
+    // 16 d .. 16 d + 15 (q4), lane l row (l / (RB / 16)), physical 16-byte
+    // chunk l % (RB / 16), which holds the row's logical chunk
+    // (l % (RB / 16)) ^ (row & 7) (q8; q4 rows of 4 chunks XOR row & 3)
+    constexpr int kChunks = RB / 16;
+    constexpr int kRowsPerDma = 64 / kChunks;
+    const uint8_t *dma_src[Sh::kDma];
+#pragma unroll
+    for (int d = 0; d < Sh::kDma; ++d) {
+        const int j = d * kRowsPerDma + lane / kChunks;
+        int n;
+        const uint8_t *row = w_row(j, n);
+        const int logical = (lane % kChunks) ^ (j & (kChunks - 1));
+        dma_src[d] = row + logical * 16;
+    }
+    const int nsteps = tk.k / 128;  // k % 64 == 0; an odd last half-step is handled below
+    const int nk = tk.k / 64;
+    i32x4 ra[S][2][kLimbs][MB];
+    auto issue = [&](int step, int st) {
+        __attribute__((address_space(3))) unsigned char *dst =
+            (__attribute__((address_space(3))) unsigned char *)(my_lds + st * Sh::kWaveStage);
+        const long koff = (long)step * RB;
+#pragma unroll
+        for (int d = 0; d < Sh::kDma; ++d)
+            __builtin_amdgcn_global_load_lds(
+                (const __attribute__((address_space(1))) void *)(dma_src[d] + koff),
+                dst + d * 1024, 16, 0, 0);
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int slice = min(2 * step + h, nk - 1);
+#pragma unroll
+            for (int a = 0; a < kLimbs; ++a)
+#pragma unroll
+                for (int i = 0; i < MB; ++i) {
+                    const u32x4 v =
+                        load_global16(a_src[i] + a * tk.a_plane + (long)slice * 64);
+                    ra[st][h][a][i] = i32x4{(int)v.x, (int)v.y, (int)v.z, (int)v.w};
+                }
+        }
+    };
+    i32x4 acc[kLimbs][MB][4];
+#pragma unroll
+    for (int a = 0; a < kLimbs; ++a)
+#pragma unroll
+        for (int i = 0; i < MB; ++i)
+#pragma unroll
+            for (int f = 0; f < 4; ++f) acc[a][i][f] = i32x4{0, 0, 0, 0};
+    // the two 64-wide slices of a step (nh = 1: only the first exists)
+    auto compute = [&](int st, int nh) {
+        const unsigned char *stage = my_lds + st * Sh::kWaveStage;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            if (h >= nh) break;  // uniform
+            i32x4 bw[4];
+#pragma unroll
+            for (int f = 0; f < 4; ++f) {
+                const int j = f * 16 + l16;
+                if constexpr (FMT == kQ8) {
+                    const int phys = (h * 4 + kq) ^ (j & 7);
+                    const u32x4 v = *reinterpret_cast<const u32x4 *>(stage + j * RB + phys * 16);
+                    bw[f] = i32x4{(int)v.x, (int)v.y, (int)v.z, (int)v.w};
+                } else {
+                    // 8 packed bytes = the 16 k values of this lane
+                    const int phys = (h * 2 + (kq >> 1)) ^ (j & 3);
+                    const u32x2 v = *reinterpret_cast<const u32x2 *>(stage + j * RB + phys * 16 +
+                                                                    (kq & 1) * 8);
+                    unsigned o0, o1, o2, o3;
+                    unpack_q4_word(v.x, o0, o1);
+                    unpack_q4_word(v.y, o2, o3);
+                    bw[f] = i32x4{(int)o0, (int)o1, (int)o2, (int)o3};
+                }
+            }
+#pragma unroll
+            for (int f = 0; f < 4; ++f)
+#pragma unroll
+                for (int i = 0; i < MB; ++i)
+#pragma unroll
+                    for (int a = 0; a < kLimbs; ++a)
+                        acc[a][i][f] = __builtin_amdgcn_mfma_i32_16x16x64_i8(
+                            ra[st][h][a][i], bw[f], acc[a][i][f], 0, 0, 0);
+        }
+    };
+    const int steps = (nk + 1) / 2;  // the last step may hold one slice
+    (void)nsteps;
+#pragma unroll
+    for (int j = 0; j < S; ++j)
+        if (j < steps) issue(j, j);
+    for (int t0 = 0; t0 < steps; t0 += S) {
+#pragma unroll
+        for (int j = 0; j < S; ++j) {
+            const int t = t0 + j;
+            if (t < steps) {  // uniform
+                if (t + S - 1 < steps) wait_vmcnt<(S - 1) * NL>();
+                else wait_vmcnt<0>();
+                compute(j, min(2, nk - 2 * t));
+                if (t + S < steps) issue(t + S, j);
+            }
+        }
+    }
+
+    // ---- epilogue: lane l holds C[4 (l / 16) + r][l % 16] of each block
+    constexpr int kF = DUAL ? 2 : 4;
+    int ncol[kF];
+    float sw[kF], su[kF];
+#pragma unroll
+    for (int f = 0; f < kF; ++f) {
+        w_row(f * 16 + l16, ncol[f]);
+        const bool ok = ncol[f] < tk.n_out;
+        sw[f] = ok ? load_global_f32(tk.s + ncol[f]) : 0.0f;
+        su[f] = (DUAL && ok) ? load_global_f32(tk.s2 + ncol[f]) : 0.0f;
+    }
+    float sx[MB][4];
+#pragma unroll
+    for (int i = 0; i < MB; ++i)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int m = m0 + 16 * i + 4 * kq + r;
+            const int mm = m < tk.rows ? m : m0;
+            sx[i][r] = load_global_f32(tk.a_scale + (tk.a_rows ? tk.a_rows[mm] : mm));
+        }
+    __builtin_amdgcn_s_waitcnt(0);
+    auto limb_sum = [&](int i, int f, int r) -> float {
+        return (float)acc[0][i][f][r] * 65536.0f +
+               ((float)acc[1][i][f][r] * 256.0f + (float)acc[2][i][f][r]);
+    };
+    const bool resid = !DUAL && tk.resid;
+#pragma unroll
+    for (int i = 0; i < MB; ++i)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int m = m0 + 16 * i + 4 * kq + r;
+            if (m >= tk.rows) continue;
+            float *yrow = tk.y + (long)m * tk.y_stride;
+#pragma unroll
+            for (int f = 0; f < kF; ++f) {
+                if (ncol[f] >= tk.n_out) continue;
+                if (DUAL) {
+                    const float g = limb_sum(i, f, r) * sx[i][r] * sw[f];
+                    const float u = limb_sum(i, f + 2, r) * sx[i][r] * su[f];
+                    store_global(yrow + ncol[f], silu(g) * u);
+                } else {
+                    float v = limb_sum(i, f, r) * sx[i][r] * sw[f];
+                    if (resid)
+                        v = load_global_f32(tk.resid + (long)m * tk.resid_stride + ncol[f]) + v;
+                    store_global(yrow + ncol[f], v);
+                }
+            }
+        }
+}
+
 template <int FMT, bool DUAL, int BM>
 static void launch_qgemm(const QGemmLaunch &L, int grid, hipStream_t stream) {
     constexpr int kLds = QgShape<FMT, BM>::kLds;
@@ -689,13 +923,66 @@ static void launch_qgemm_bm(int fmt, bool dual, const QGemmLaunch &L, int grid,
     }
 }
 
-static int launch_qgemm_fmt(int fmt, bool dual, int bm, const QGemmLaunch &L, int tiles_bound,
+template <int FMT, bool DUAL, int MB>
+static void launch_stream(const QGemmLaunch &L, int grid, hipStream_t stream) {
+    constexpr int kLds = QsShape<FMT, MB>::kLds;
+    static const bool attr = [] {
+        return hipFuncSetAttribute(
+                   reinterpret_cast<const void *>(&qgemm_stream_kernel<FMT, DUAL, MB>),
+                   hipFuncAttributeMaxDynamicSharedMemorySize, kLds) == hipSuccess;
+    }();
+    (void)attr;
+    hipLaunchKernelGGL((qgemm_stream_kernel<FMT, DUAL, MB>), dim3((unsigned)grid), dim3(256),
+                       kLds, stream, L);
+}
+
+template <int MB>
+static void launch_stream_mb(int fmt, bool dual, const QGemmLaunch &L, int grid,
+                             hipStream_t stream) {
+    if (fmt == kQ8) {
+        if (dual) launch_stream<kQ8, true, MB>(L, grid, stream);
+        else launch_stream<kQ8, false, MB>(L, grid, stream);
+    } else {
+        if (dual) launch_stream<kQ4, true, MB>(L, grid, stream);
+        else launch_stream<kQ4, false, MB>(L, grid, stream);
+    }
+}
+
+// Tile kinds: the weight-streaming tile with 16 token rows, the LDS tiles
+// with 32 or 128.
+enum TileKind { kTileStream16 = 0, kTileLds32 = 1, kTileLds128 = 2 };
+
+static int tile_bm(int kind) {
+    return kind == kTileStream16 ? 16 : (kind == kTileLds128 ? kQgBM : kQgBMSmall);
+}
+
+// Tile choices, measured on MI355X.  A batch of at most 16 token rows streams
+// the weights (every task fits one row tile); the streaming tile copies 128 k
+// per step, so its reductions must be whole multiples of 128 (`stream_ok`).
+// MoE layer: 16-row streaming tile up to 16 rows (T = 8: 99 against 108 us
+// on the 32-row LDS tile), the 32-row LDS tile up to 80 rows per expert on
+// average (T = 64: 170 against 180 us streaming), 128 rows above.  Dense
+// projections: the 32-row tile up to 64 rows.
+static int moe_tile(int rows, double rows_per_expert, bool stream_ok) {
+    if (stream_ok && rows <= 16) return kTileStream16;
+    return rows_per_expert <= 80.0 ? kTileLds32 : kTileLds128;
+}
+static int dense_tile(int rows, bool stream_ok) {
+    if (stream_ok && rows <= 16) return kTileStream16;
+    return rows <= 2 * kQgBMSmall ? kTileLds32 : kTileLds128;
+}
+
+static int launch_qgemm_fmt(int fmt, bool dual, int kind, const QGemmLaunch &L, int tiles_bound,
                             hipStream_t stream) {
     if (tiles_bound <= 0) return kOk;
-    if ((fmt != kQ8 && fmt != kQ4) || (bm != kQgBM && bm != kQgBMSmall)) return kErrArgs;
+    if (fmt != kQ8 && fmt != kQ4) return kErrArgs;
     const int grid = ((tiles_bound + 7) / 8) * 8;
-    if (bm == kQgBM) launch_qgemm_bm<kQgBM>(fmt, dual, L, grid, stream);
-    else launch_qgemm_bm<kQgBMSmall>(fmt, dual, L, grid, stream);
+    switch (kind) {
+    case kTileStream16: launch_stream_mb<1>(fmt, dual, L, grid, stream); break;
+    case kTileLds32: launch_qgemm_bm<kQgBMSmall>(fmt, dual, L, grid, stream); break;
+    case kTileLds128: launch_qgemm_bm<kQgBM>(fmt, dual, L, grid, stream); break;
+    default: return kErrArgs;
+    }
     return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
 }
 
@@ -712,10 +999,9 @@ int qgemm_single(int fmt, bool dual, const GemmTask &task, hipStream_t stream) {
         return kErrArgs;
     QGemmLaunch L;
     L.single = task;
-    // few rows: the 32-row tile spends a quarter of the MFMA work per weight byte
-    const int bm = task.rows <= 2 * kQgBMSmall ? kQgBMSmall : kQgBM;
-    return launch_qgemm_fmt(fmt, dual, bm, L, host_tiles(dual, task.rows, task.n_out, bm),
-                            stream);
+    const int kind = dense_tile(task.rows, task.k % 128 == 0);
+    return launch_qgemm_fmt(fmt, dual, kind, L,
+                            host_tiles(dual, task.rows, task.n_out, tile_bm(kind)), stream);
 }
 
 // ---------------------------------------------------------------------------
@@ -729,7 +1015,11 @@ struct MoeScheduleParams {
 
 __device__ __forceinline__ void moe_schedule_body(const MoeScheduleParams &sp) {
     const MoeGemmParams &p = sp.p;
-    const bool small = sp.bm == kQgBMSmall;
+    const int bm = sp.bm;
+    auto tiles_rt = [bm](bool dual, int rows, int n_out) {
+        const int outw = dual ? kQgBW / 2 : kQgBW;
+        return ((rows + bm - 1) / bm) * ((n_out + outw - 1) / outw);
+    };
     __shared__ int tiles[2][kQgMaxTasks];
     const int nr = *p.n_unique;
     GemmTask *t0 = p.tasks;
@@ -754,8 +1044,7 @@ __device__ __forceinline__ void moe_schedule_body(const MoeScheduleParams &sp) {
         a.y = p.expert_hidden + (long)off * p.inter;
         a.y_stride = p.inter;
         t0[u] = a;
-        tiles[0][u] = small ? tiles_of<true, kQgBMSmall>(cnt, p.inter)
-                            : tiles_of<true, kQgBM>(cnt, p.inter);
+        tiles[0][u] = tiles_rt(true, cnt, p.inter);
         GemmTask b;
         b.w = ew.down;
         b.s = ew.down_s;
@@ -769,8 +1058,7 @@ __device__ __forceinline__ void moe_schedule_body(const MoeScheduleParams &sp) {
         b.y = p.expert_out + (long)off * p.hidden;
         b.y_stride = p.hidden;
         t1[u] = b;
-        tiles[1][u] = small ? tiles_of<false, kQgBMSmall>(cnt, p.hidden)
-                            : tiles_of<false, kQgBM>(cnt, p.hidden);
+        tiles[1][u] = tiles_rt(false, cnt, p.hidden);
     }
     if (threadIdx.x == 0) {
         tiles[0][nr] = 0;
@@ -791,8 +1079,7 @@ __device__ __forceinline__ void moe_schedule_body(const MoeScheduleParams &sp) {
             a.y = p.shared_hidden;
             a.y_stride = p.shared_width;
             t0[nr] = a;
-            tiles[0][nr] = small ? tiles_of<true, kQgBMSmall>(p.rows, p.shared_width)
-                                 : tiles_of<true, kQgBM>(p.rows, p.shared_width);
+            tiles[0][nr] = tiles_rt(true, p.rows, p.shared_width);
             GemmTask b;
             b.w = p.shared_down;
             b.s = p.shared_down_s;
@@ -806,8 +1093,7 @@ __device__ __forceinline__ void moe_schedule_body(const MoeScheduleParams &sp) {
             b.y = p.shared_out;
             b.y_stride = p.hidden;
             t1[nr] = b;
-            tiles[1][nr] = small ? tiles_of<false, kQgBMSmall>(p.rows, p.hidden)
-                                 : tiles_of<false, kQgBM>(p.rows, p.hidden);
+            tiles[1][nr] = tiles_rt(false, p.rows, p.hidden);
         }
     }
     __syncthreads();
@@ -856,10 +1142,11 @@ int moe_gemm(const MoeGemmParams &p, hipStream_t stream) {
         return kErrArgs;
     const int entries = p.rows * p.top_k;
     const int max_tasks = entries < p.experts ? entries : p.experts;
-    // experts holding at most 80 rows on average take 32-row tiles: measured
-    // on the Moonlight MoE layer, 32-row tiles win up to 72 rows per expert
-    // (369 against 390 us at T = 768) and lose from 96 (420 against 411 us)
-    const int bm = entries <= 80 * p.experts ? kQgBMSmall : kQgBM;
+    // one tile kind for the whole layer, from the average rows per expert
+    const bool stream_ok = p.hidden % 128 == 0 && p.inter % 128 == 0 &&
+                           (!p.has_shared || p.shared_width % 128 == 0);
+    const int kind = moe_tile(p.rows, (double)entries / p.experts, stream_ok);
+    const int bm = tile_bm(kind);
     MoeScheduleParams sp;
     sp.p = p;
     sp.bm = bm;
@@ -909,14 +1196,14 @@ int moe_gemm(const MoeGemmParams &p, hipStream_t stream) {
             p.has_shared ? host_tiles(dual, p.rows, dual ? p.shared_width : p.hidden, bm) : 0;
         if (same) {
             L.range = 0;
-            st = launch_qgemm_fmt(p.expert_fmt, dual, bm, L, routed_mt * routed_nt + shared_t,
+            st = launch_qgemm_fmt(p.expert_fmt, dual, kind, L, routed_mt * routed_nt + shared_t,
                                   stream);
         } else {
             L.range = 1;
-            st = launch_qgemm_fmt(p.expert_fmt, dual, bm, L, routed_mt * routed_nt, stream);
+            st = launch_qgemm_fmt(p.expert_fmt, dual, kind, L, routed_mt * routed_nt, stream);
             if (!st) {
                 L.range = 2;
-                st = launch_qgemm_fmt(p.shared_fmt, dual, bm, L, shared_t, stream);
+                st = launch_qgemm_fmt(p.shared_fmt, dual, kind, L, shared_t, stream);
             }
         }
         if (st) return st;

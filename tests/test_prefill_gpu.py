@@ -181,11 +181,15 @@ def outlier_rows(rows, width, seed, dims=4):
 DENSE = [("model.layers.3.self_attn.q_proj.weight", 2048, 3072, 512),
          ("model.layers.3.self_attn.kv_a_proj_with_mqa.weight", 2048, 576, 511),
          ("model.layers.3.self_attn.o_proj.weight", 2048, 2048, 512),
-         ("model.layers.0.mlp.down_proj.weight", 11264, 2048, 90)]
+         ("model.layers.0.mlp.down_proj.weight", 11264, 2048, 90),
+         # few rows: the weight-streaming tiles (16 and 32 token rows)
+         ("model.layers.3.self_attn.q_proj.weight", 2048, 3072, 16),
+         ("model.layers.3.self_attn.kv_a_proj_with_mqa.weight", 2048, 576, 27),
+         ("model.layers.0.mlp.down_proj.weight", 11264, 2048, 31)]
 
 
-@pytest.mark.parametrize("name,width,out,rows", DENSE, ids=lambda v: str(v).split(".")[-2]
-                         if isinstance(v, str) else str(v))
+@pytest.mark.parametrize("name,width,out,rows", DENSE,
+                         ids=[f"{d[0].split('.')[-2]}-{d[3]}" for d in DENSE])
 def test_gemm_outliers_dense(moon, name, width, out, rows):
     print(f"[gpu] dense GEMM {name} T={rows} with outlier columns", flush=True)
     sess = S.Session(moon, 512, 512)
