@@ -277,12 +277,12 @@ __device__ __forceinline__ bool map_tile(const QGemmLaunch &L, GemmTask &tk, int
 // so that the MFMA fragment reads (32 consecutive rows, one chunk) and the
 // tile writes hit distinct banks whether the LDS serves 8 or 16 lanes of a
 // 128-bit access per cycle.
-template <int FMT> struct QgCfg;
-template <> struct QgCfg<kQ8> {
-    static constexpr int kRB = 64;
-};
-template <> struct QgCfg<kQ4> {
-    static constexpr int kRB = 64;
+// Stage width: q8 32-row tiles (weight-stream bound) copy 128-k slices, so a
+// DMA instruction covers 8 rows x 128 contiguous bytes (on MI355X runs of
+// 128 bytes stream ~6 TB/s, runs of 64 bytes ~4.2 TB/s); the 128-row tile
+// (MFMA bound) keeps 64-k slices to fit more stages.
+template <int FMT, int BM> struct QgCfg {
+    static constexpr int kRB = (FMT == kQ8 && BM == 32) ? 128 : 64;
 };
 
 template <int RB>
@@ -295,11 +295,13 @@ __device__ __forceinline__ int lds_off(int row, int chunk) {
 // waves (two per SIMD) in a 4 (token rows) x 2 (weight rows) grid, each wave
 // 32 x 128 = 1 x 4 blocks of 32 x 32 per limb (192 int32 accumulators);
 // BM = 32: 4 waves side by side, each 32 x 64 = 1 x 2 blocks.  A stage holds
-// the three limb tiles of A and the weight tile.  q8 DMA: A blocks of 16
-// rows, wave w taking blocks w, w + kWaves, ... (BM = 32 has 6 A blocks, so
-// waves 0-1 issue one more than waves 2-3), B blocks likewise.
+// the three limb tiles of A and the weight tile.  q8 DMA: blocks of 1 KB
+// (1024 / kRB rows), wave w taking A blocks w, w + kWaves, ... (waves may
+// issue one more than others when the count does not divide), B blocks
+// likewise.
 template <int FMT, int BM> struct QgShape {
-    static constexpr int kRB = QgCfg<FMT>::kRB;
+    static constexpr int kRB = QgCfg<FMT, BM>::kRB;
+    static constexpr int kRowsDma = 1024 / kRB;    // rows per DMA block
     static constexpr int kWaves = BM == 128 ? 8 : 4;
     static constexpr int kThreads = kWaves * kWave;
     static constexpr int kWM = BM / 32;            // waves along the token rows
@@ -310,9 +312,9 @@ template <int FMT, int BM> struct QgShape {
     static constexpr int kLdsA = kLimbs * BM * kRB;
     static constexpr int kStage = (kLimbs * BM + kQgBW) * kRB;
     static constexpr int kLds = kStages * kStage + BM * 8;  // + scales and row map
-    static constexpr int kRowBlocks = BM / 16;
+    static constexpr int kRowBlocks = BM / kRowsDma;
     static constexpr int kABlocks = kLimbs * kRowBlocks;
-    static constexpr int kBBlocks = kQgBW / 16;
+    static constexpr int kBBlocks = kQgBW / kRowsDma;
     static constexpr int kBPer = kBBlocks / kWaves;
     static constexpr int kAMax = (kABlocks + kWaves - 1) / kWaves, kAMin = kABlocks / kWaves;
     static constexpr int kDmaMax = kAMax + kBPer, kDmaMin = kAMin + kBPer;
@@ -323,7 +325,8 @@ template <int FMT, int BM> struct QgShape {
     static_assert(kBBlocks % kWaves == 0 && (kQgBW * 2) % kThreads == 0, "B split");
 };
 static_assert(QgShape<kQ8, kQgBM>::kLds <= 160 * 1024, "q8 128-row tile exceeds the LDS");
-static_assert(2 * QgShape<kQ8, kQgBMSmall>::kLds <= 160 * 1024, "two 32-row tiles per CU");
+static_assert(QgShape<kQ8, kQgBMSmall>::kLds <= 160 * 1024, "q8 32-row tile exceeds the LDS");
+static_assert(2 * QgShape<kQ4, kQgBMSmall>::kLds <= 160 * 1024, "two q4 32-row tiles per CU");
 
 // s_waitcnt on the vector-memory counter only (gfx9 encoding: vmcnt in bits
 // 3:0 and 15:14, expcnt 6:4 and lgkmcnt 11:8 left at their no-wait maxima).
@@ -335,7 +338,8 @@ template <int N> __device__ __forceinline__ void wait_vmcnt() {
 // batches whose experts hold few rows each: the MFMA work per weight byte is
 // a quarter, so the tile is bound by the weight stream instead of by padding.
 template <int FMT, bool DUAL, int BM>
-__global__ __launch_bounds__((QgShape<FMT, BM>::kThreads), BM == 128 ? 1 : 2) void qgemm_kernel(
+__global__ __launch_bounds__((QgShape<FMT, BM>::kThreads),
+                             (BM == 128 || QgShape<FMT, BM>::kRB == 128) ? 1 : 2) void qgemm_kernel(
     QGemmLaunch L) {
     extern __shared__ __attribute__((aligned(16))) int8_t qg_lds[];
     using Sh = QgShape<FMT, BM>;
@@ -406,13 +410,16 @@ __global__ __launch_bounds__((QgShape<FMT, BM>::kThreads), BM == 128 ? 1 : 2) vo
         return limb_base(limb) + (long)arow * tk.a_stride;
     };
 
-    // DMA path (q8, 64-byte rows), blocks of 16 rows = 1 KB: A block b holds
-    // limb b / kRowBlocks, rows (b % kRowBlocks) * 16 + l / 4; wave w issues A
-    // blocks w, w + kWaves, ..., all in row block w % kRowBlocks, and B
-    // blocks (rows (w + kWaves q) * 16 + l / 4); lane l fills LDS row (block
-    // row 0 + l / 4), physical chunk l % 4, so it loads the logical chunk
-    // (l % 4) ^ g(row).  The limbs share a lane's A rows.
-    const int lr = lane >> 2, lc = lane & 3;
+    // DMA path (q8), blocks of R = 1024 / kRB rows = 1 KB: A block b holds
+    // limb b / kRowBlocks, rows (b % kRowBlocks) * R + l / (kRB / 16); wave w
+    // issues A blocks w, w + kWaves, ..., all in row block w % kRowBlocks,
+    // and B blocks (rows (w + kWaves q) * R + l / (kRB / 16)); lane l fills
+    // LDS row (block row 0 + l / (kRB / 16)), physical chunk l % (kRB / 16),
+    // so it loads the logical chunk (l % (kRB / 16)) ^ g(row).  The limbs
+    // share a lane's A rows.
+    constexpr int kCh = kRB / 16;
+    const int lr = lane / kCh, lc = lane % kCh;
+    auto swz = [](int r) { return kRB == 64 ? (((r >> 1) ^ (r >> 3)) & 3) : ((r ^ (r >> 3)) & 7); };
     unsigned a_off = 0u;  // byte offset of this lane's A row
     // register path (q4, 64-byte rows): kNA A chunks and kNB packed B chunks
     constexpr int kNA = Sh::kNA, kNB = Sh::kNB;
@@ -422,7 +429,7 @@ __global__ __launch_bounds__((QgShape<FMT, BM>::kThreads), BM == 128 ? 1 : 2) vo
     int b_dst[kNB];
     u32x4 ra[kNA], rb[kNB];
     if constexpr (kDma) {
-        const int r = (wave % Sh::kRowBlocks) * 16 + lr;
+        const int r = (wave % Sh::kRowBlocks) * Sh::kRowsDma + lr;
         const int arow = lds_arow[r] >= 0 ? lds_arow[r] : lds_arow[0];
         a_off = (unsigned)(arow * tk.a_stride);
     } else {
@@ -453,8 +460,8 @@ __global__ __launch_bounds__((QgShape<FMT, BM>::kThreads), BM == 128 ? 1 : 2) vo
             const int b = wave + Sh::kWaves * h;  // A block
             if (h >= Sh::kAMin && b >= Sh::kABlocks) break;  // wave-uniform
             const int limb = b / kRowBlocks, rb = b % kRowBlocks;
-            const int r = rb * 16 + lr;  // A row of this lane
-            const int ca = lc ^ (((r >> 1) ^ (r >> 3)) & 3);
+            const int r = rb * Sh::kRowsDma + lr;  // A row of this lane
+            const int ca = lc ^ swz(r);
             // uniform base + 32-bit lane offset: one VGPR per address
             const unsigned aoff = a_off + (unsigned)(k0 + ca * 16);
             __builtin_amdgcn_global_load_lds(
@@ -464,11 +471,11 @@ __global__ __launch_bounds__((QgShape<FMT, BM>::kThreads), BM == 128 ? 1 : 2) vo
 #pragma unroll
         for (int q = 0; q < Sh::kBPer; ++q) {
             const int bb = wave + Sh::kWaves * q;
-            const int j = bb * 16 + lr;  // B row of this lane
+            const int j = bb * Sh::kRowsDma + lr;  // B row of this lane
             bool up;
             const int out = b_out(j, up);
             const uint8_t *bbase = up ? w_up : w_gate;
-            const int cb = lc ^ (((j >> 1) ^ (j >> 3)) & 3);
+            const int cb = lc ^ swz(j);
             const unsigned boff =
                 (unsigned)((out < tk.n_out ? out : 0) * tk.k) + (unsigned)(k0 + cb * 16);
             __builtin_amdgcn_global_load_lds(
@@ -560,7 +567,7 @@ __global__ __launch_bounds__((QgShape<FMT, BM>::kThreads), BM == 128 ? 1 : 2) vo
         const bool more = Sh::kDmaMax == Sh::kDmaMin ||
                           __builtin_amdgcn_readfirstlane(wave) + Sh::kWaves * Sh::kAMin <
                               Sh::kABlocks;
-        const int nk = tk.k / kRB;  // k % 64 == 0 (qgemm_shape_ok)
+        const int nk = tk.k / kRB;  // k % kRB == 0 (qgemm_shape_ok, and the tile pickers for kRB = 128)
         for (int st = 0; st < kStages - 1 && st < nk; ++st) issue_dma(st * kRB, st);
         for (int ks = 0; ks < nk; ++ks) {
             if (ks + 1 < nk) {
@@ -573,7 +580,8 @@ __global__ __launch_bounds__((QgShape<FMT, BM>::kThreads), BM == 128 ? 1 : 2) vo
             // and loads of the fence it implies
             __builtin_amdgcn_s_barrier();
             if (ks + kStages - 1 < nk) issue_dma((ks + kStages - 1) * kRB, (ks + kStages - 1) % kStages);
-            compute_pair(ks % kStages, 0);
+#pragma unroll
+            for (int kp = 0; kp < kRB / 32; kp += 2) compute_pair(ks % kStages, kp);
         }
     } else {
         // two buffers: slice ks + 2 is in registers while slice ks is multiplied
@@ -957,19 +965,22 @@ static int tile_bm(int kind) {
 }
 
 // Tile choices, measured on MI355X.  A batch of at most 16 token rows streams
-// the weights (every task fits one row tile); the streaming tile copies 128 k
-// per step, so its reductions must be whole multiples of 128 (`stream_ok`).
+// the weights (every task fits one row tile); the streaming tile and the q8
+// 32-row tile copy 128 k per step, so they need reductions that are whole
+// multiples of 128 (`k128`; otherwise the 128-row tile runs).
 // MoE layer: 16-row streaming tile up to 16 rows (T = 8: 99 against 108 us
 // on the 32-row LDS tile), the 32-row LDS tile up to 80 rows per expert on
 // average (T = 64: 170 against 180 us streaming), 128 rows above.  Dense
 // projections: the 32-row tile up to 64 rows.
-static int moe_tile(int rows, double rows_per_expert, bool stream_ok) {
-    if (stream_ok && rows <= 16) return kTileStream16;
-    return rows_per_expert <= 80.0 ? kTileLds32 : kTileLds128;
+static int moe_tile(int fmt, int rows, double rows_per_expert, bool k128) {
+    if (k128 && rows <= 16) return kTileStream16;
+    const bool small_ok = fmt == kQ4 || k128;  // the q8 32-row tile steps 128 k
+    return small_ok && rows_per_expert <= 80.0 ? kTileLds32 : kTileLds128;
 }
-static int dense_tile(int rows, bool stream_ok) {
-    if (stream_ok && rows <= 16) return kTileStream16;
-    return rows <= 2 * kQgBMSmall ? kTileLds32 : kTileLds128;
+static int dense_tile(int fmt, int rows, bool k128) {
+    if (k128 && rows <= 16) return kTileStream16;
+    const bool small_ok = fmt == kQ4 || k128;
+    return small_ok && rows <= 2 * kQgBMSmall ? kTileLds32 : kTileLds128;
 }
 
 static int launch_qgemm_fmt(int fmt, bool dual, int kind, const QGemmLaunch &L, int tiles_bound,
@@ -999,7 +1010,7 @@ int qgemm_single(int fmt, bool dual, const GemmTask &task, hipStream_t stream) {
         return kErrArgs;
     QGemmLaunch L;
     L.single = task;
-    const int kind = dense_tile(task.rows, task.k % 128 == 0);
+    const int kind = dense_tile(fmt, task.rows, task.k % 128 == 0);
     return launch_qgemm_fmt(fmt, dual, kind, L,
                             host_tiles(dual, task.rows, task.n_out, tile_bm(kind)), stream);
 }
@@ -1143,9 +1154,10 @@ int moe_gemm(const MoeGemmParams &p, hipStream_t stream) {
     const int entries = p.rows * p.top_k;
     const int max_tasks = entries < p.experts ? entries : p.experts;
     // one tile kind for the whole layer, from the average rows per expert
-    const bool stream_ok = p.hidden % 128 == 0 && p.inter % 128 == 0 &&
-                           (!p.has_shared || p.shared_width % 128 == 0);
-    const int kind = moe_tile(p.rows, (double)entries / p.experts, stream_ok);
+    const bool k128 = p.hidden % 128 == 0 && p.inter % 128 == 0 &&
+                      (!p.has_shared || p.shared_width % 128 == 0);
+    const bool any_q8 = p.expert_fmt == kQ8 || (p.has_shared && p.shared_fmt == kQ8);
+    const int kind = moe_tile(any_q8 ? kQ8 : kQ4, p.rows, (double)entries / p.experts, k128);
     const int bm = tile_bm(kind);
     MoeScheduleParams sp;
     sp.p = p;
