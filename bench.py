@@ -305,6 +305,23 @@ def moe_only():
     print(json.dumps(out), flush=True)
 
 
+def attn_only():
+    """One decode attention block ([q | kv_a] GEMV, MLA chain, o_proj) at
+    ctx 4096 and 16384, stream launches (profiler runs and quick checks)."""
+    from floyd_amd import session as S
+    model = S.Model.synthetic()
+    out = {}
+    for ctx in (4096, 16384):
+        sess = S.Session(model, ctx + 8, 1)
+        sess.fill_kv(ctx, seed=ctx, layer=1)
+        us = sess.time_attention(1, 1, ctx, warmup=5, iters=50)
+        out[f"ctx{ctx}"] = {"us": round(us, 2)}
+        print(f"[bench] attention block ctx={ctx}: {us:.1f} us", file=sys.stderr, flush=True)
+        sess.close()
+    model.close()
+    print(json.dumps(out), flush=True)
+
+
 def prefill_only():
     """Config 3 (MoE prefill layer, q8 and q4) and the 2048-token full-model
     prefill, one JSON line (profiler runs and quick checks)."""
@@ -482,6 +499,8 @@ def main():
                         help="only config 2 (MoE decode layer at T = 1, 8, 64)")
     parser.add_argument("--prefill-only", action="store_true",
                         help="only config 3 (MoE prefill q8 / q4) and the 2048-token prefill")
+    parser.add_argument("--attn-only", action="store_true",
+                        help="only the decode attention block at ctx 4096 and 16384")
     parser.add_argument("--decode-only", type=int, default=0, metavar="CTX",
                         help="only greedy decode steps of the synthetic model at context "
                              "CTX, printed per token (profiler runs)")
@@ -506,6 +525,9 @@ def main():
         return
     if args.moe_only:
         moe_only()
+        return
+    if args.attn_only:
+        attn_only()
         return
 
     # headline: benchmark config 1, q4 [11264 x 2048], batch 1

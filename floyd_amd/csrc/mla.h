@@ -8,6 +8,9 @@ namespace mlh {
 constexpr int kMlaMaxHeads = 16;        // Moonlight: 16 heads
 constexpr int kMlaKeysPerSplit = 32;    // keys per workgroup in mla_attend
 constexpr int kMlaMaxLatent = 512;      // kv_lora_rank limit (moonlight_metal.m:1041)
+constexpr int kMlaDecodeRows = 16;      // token rows per decode-path launch group
+constexpr int kMlaValueDims = 32;       // latent dims per merge + value workgroup
+constexpr int kMlaCountStride = 32;     // ints between arrival counters (one per 128 bytes)
 
 // A weight matrix in one of the container formats (f32 / int8 / packed int4)
 // with its per-row scales.
@@ -46,10 +49,15 @@ struct MlaParams {
     float *part_lc = nullptr;           // [rows, max_splits, kMlaMaxHeads, latent]
     float *latent_context = nullptr;    // scratch [rows, heads, latent] merged lc
     float *context = nullptr;           // out [rows, heads, vdim]
+    // decode path (at most kMlaDecodeRows rows per launch group):
+    float *value_part = nullptr;   // [rows][heads][latent / kMlaValueDims][vdim] value partials
+    int *merge_count = nullptr;    // [rows][heads] x kMlaCountStride arrival counters, zero between launches
 };
 
-// Cache append + query RoPE + absorb, split-K attention, merge, value
-// projection (four launches).  o_proj is a plain GEMV on `context`.
+// Prefill: cache append + query RoPE, absorb GEMM, flash attention, value
+// GEMM.  Decode: cache append + query RoPE + absorb, split-K
+// attention, merge + value projection (three launches per group of
+// kMlaDecodeRows rows).  o_proj is a plain GEMV on `context`.
 int mla_attention_core(const MlaParams &p, hipStream_t stream);
 
 }  // namespace mlh

@@ -9,18 +9,22 @@
 //   value          moonlight_attention_decode_value (moonlight_kernels.metal:345-375)
 //   orchestration  encode_attention_buffer  (moonlight_metal.m:287-440)
 //
-// Launches per attention call:
-//   mla_prep    (row, cache-append | head): RMSNorm + RoPE into the caches,
-//               RoPE of the query's rope part, and the absorbed query
-//               qa_h = W_UK_h^T q_nope_h with each wave streaming whole kv_b
-//               rows (coalesced 8-column lane slices).
+// Launches per decode attention call (groups of up to kMlaDecodeRows rows):
+//   mla_prep    (row, cache-append | head x 128 latent columns): RMSNorm +
+//               RoPE into the caches, RoPE of the query's rope part, and the
+//               absorbed query qa_h = W_UK_h^T q_nope_h, each wave reading
+//               128-column runs of 4 kv_b rows per instruction.
 //   mla_attend  (key split of kMlaKeysPerSplit keys, row): every latent row
 //               read once scores ALL heads (the reference re-reads the cache
 //               per head); per split a local max / exp-sum and the partial
 //               latent context of every head, from the split's rows in LDS.
-//   mla_merge   (row, head, 32-wide latent chunk): one-pass log-sum-exp
-//               merge of the splits into lc_h.
-//   mla_value   (row, head, 32 value rows): ctx_h = W_UV_h lc_h.
+//   mla_merge_value (row, head, kMlaValueDims latent dims): one-pass
+//               log-sum-exp merge of the splits into that slice of lc_h,
+//               its share of ctx_h = W_UV_h lc_h, and the sum of the shares
+//               by the head's last workgroup.
+// Prefill (more than one row, outside a captured graph) runs mla_prep for
+// the cache and the query rope, the absorb and value as per-head MFMA GEMMs
+// and a flash-attention kernel (mla_prefill_attend).
 #include "mla.h"
 
 #include "mlh_device.h"
@@ -33,51 +37,72 @@ __device__ __forceinline__ int mla_position(const MlaParams &p) {
     return p.position_dev ? *p.position_dev : p.position;
 }
 
-// Eight consecutive dequantised kv_b values w[row, col..col+7] (col % 8 == 0),
-// moonlight_weight_value (moonlight_kernels.metal:202-216) applied per element.
-__device__ __forceinline__ void kvb_load8(const MatrixRef &m, int row, int col, int width,
-                                          float (&out)[8]) {
-    if (m.fmt == kF32) {
+// Eight consecutive dequantised kv_b values w[row, col..col+7] (col % 8 ==
+// 0), moonlight_weight_value (moonlight_kernels.metal:202-216) per element,
+// in two steps for a format known at compile time: kvb_fetch8 issues the
+// loads, kvb_decode8 dequantises, so a thread can have many rows in flight
+// before it decodes the first (a run-time format switch would make every
+// load wait before the next is issued).
+template <int FMT> struct Kvb8 {
+    f32x4 a, b;   // kF32
+    uint2 q8;     // kQ8
+    unsigned q4;  // kQ4
+    float s;
+};
+template <int FMT>
+__device__ __forceinline__ void kvb_fetch8(const MatrixRef &m, int row, int col, int width,
+                                           Kvb8<FMT> &r) {
+    if constexpr (FMT == kF32) {
         const float *p = reinterpret_cast<const float *>(m.w) + (long)row * width + col;
-        const f32x4 a = load_f4(p), b = load_f4(p + 4);
-        out[0] = a.x; out[1] = a.y; out[2] = a.z; out[3] = a.w;
-        out[4] = b.x; out[5] = b.y; out[6] = b.z; out[7] = b.w;
-        return;
+        r.a = load_f4(p);
+        r.b = load_f4(p + 4);
+    } else if constexpr (FMT == kQ8) {
+        r.s = m.s[row];
+        r.q8 = *reinterpret_cast<const uint2 *>(m.w + (long)row * width + col);
+    } else {
+        r.s = m.s[row];
+        r.q4 = *reinterpret_cast<const unsigned *>(m.w + (long)row * ((width + 1) / 2) + col / 2);
     }
-    const float s = m.s[row];
-    if (m.fmt == kQ8) {
-        const uint2 v = *reinterpret_cast<const uint2 *>(m.w + (long)row * width + col);
+}
+template <int FMT>
+__device__ __forceinline__ void kvb_decode8(const Kvb8<FMT> &r, float (&out)[8]) {
+    if constexpr (FMT == kF32) {
+        out[0] = r.a.x; out[1] = r.a.y; out[2] = r.a.z; out[3] = r.a.w;
+        out[4] = r.b.x; out[5] = r.b.y; out[6] = r.b.z; out[7] = r.b.w;
+    } else if constexpr (FMT == kQ8) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            out[i] = (float)(int8_t)((v.x >> (8 * i)) & 0xFF) * s;
-            out[4 + i] = (float)(int8_t)((v.y >> (8 * i)) & 0xFF) * s;
+            out[i] = (float)(int8_t)((r.q8.x >> (8 * i)) & 0xFF) * r.s;
+            out[4 + i] = (float)(int8_t)((r.q8.y >> (8 * i)) & 0xFF) * r.s;
         }
-        return;
-    }
-    const unsigned v =
-        *reinterpret_cast<const unsigned *>(m.w + (long)row * ((width + 1) / 2) + col / 2);
+    } else {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        out[2 * i] = (float)((int)((v >> (8 * i)) & 15) - 8) * s;
-        out[2 * i + 1] = (float)((int)((v >> (8 * i + 4)) & 15) - 8) * s;
+        for (int i = 0; i < 4; ++i) {
+            out[2 * i] = (float)((int)((r.q4 >> (8 * i)) & 15) - 8) * r.s;
+            out[2 * i + 1] = (float)((int)((r.q4 >> (8 * i + 4)) & 15) - 8) * r.s;
+        }
     }
 }
 
-// grid (rows, 1 + heads * chunks), chunks = latent / 64 (or 0: grid
+// grid (rows, 1 + heads * chunks), chunks = ceil(latent / 128) (or 0: grid
 // (rows, 1 + heads), the query rope only): role 0 appends the cache rows; role
-// 1 + h * chunks + c ropes head h's query (c == 0) and absorbs it into the 64
-// latent columns c * 64 .. + 63: thread (i = t / 8, j = t % 8) takes kv_b
-// rows i, i + 32, ... of the head's nope part and columns 8 j .. 8 j + 7, all
-// loads of a thread issued before its FMAs; the 32 row groups meet in LDS.
-constexpr int kMlaAbsorbCols = 64;
+// 1 + h * chunks + c ropes head h's query (c == 0) and absorbs it into the
+// latent columns 128 c .. 128 c + 127: qa_h[l] = sum_i q_nope[i] kv_b[h
+// (nope + v) + i][l].  A wave instruction covers 4 nope rows x 128 columns
+// (16 lanes per row, 8 columns per lane: contiguous row runs), wave w rows
+// 4 (w + 4 j) .. + 3 for j = 0, 1, ...; a lane issues the loads of 8 rows
+// before decoding any; the 4 lanes of a column set and the 4 waves meet by
+// shuffles and LDS.
+constexpr int kMlaAbsorbCols = 128;
+template <int FMT>
 __global__ __launch_bounds__(256) void mla_prep_kernel(MlaParams p, int chunks) {
     const int r = blockIdx.x;
     const int role = blockIdx.y;
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-    const int pos = mla_position(p) + r;
     const int hw = p.nope + p.rope;
     const int half = p.rope / 2;
     if (role == 0) {
+        const int pos = mla_position(p) + r;
         __shared__ float part[4];
         const float *c = p.compressed + (long)r * p.compressed_stride;
         float cv[kMlaMaxLatent / 256];
@@ -112,9 +137,10 @@ __global__ __launch_bounds__(256) void mla_prep_kernel(MlaParams p, int chunks) 
     }
     // chunks == 0: the query rope only (prefill absorbs with mla_head_gemm)
     const int h = chunks ? (role - 1) / chunks : role - 1;
-    const int col0 = chunks ? ((role - 1) % chunks) * kMlaAbsorbCols : 0;
+    const int cc = chunks ? (role - 1) % chunks : 0;
     const float *q = p.query + (long)r * p.query_stride + (long)h * hw;
-    if (col0 == 0 && t < half) {
+    if (cc == 0 && t < half) {
+        const int pos = mla_position(p) + r;
         const float angle = (float)pos * p.inv_freq[t];
         const float cs = cosf(angle), sn = sinf(angle);
         const float first = q[p.nope + 2 * t], second = q[p.nope + 2 * t + 1];
@@ -123,64 +149,78 @@ __global__ __launch_bounds__(256) void mla_prep_kernel(MlaParams p, int chunks) 
         qr[half + t] = second * cs + first * sn;
     }
     if (!chunks) return;
-    // qa[l] = sum_c q_nope[c] * kv_b[h*(nope+v) + c, l]
-    constexpr int kRowsPerThread = 256 / 32;  // nope <= 256
-    __shared__ float red[32][kMlaAbsorbCols + 1];
-    const int i = t >> 3, j = t & 7;
-    const int col = col0 + 8 * j;
+    constexpr int kBatch = 8;  // wave instructions (4 rows each) in flight per lane
+    __shared__ float red[4][kMlaAbsorbCols];
+    const int sub = lane >> 4;                              // row within an instruction
+    const int col = cc * kMlaAbsorbCols + 8 * (lane & 15);  // first of the lane's 8 columns
+    const bool col_ok = col < p.latent;
     const int wrow = h * (p.nope + p.vdim);
-    float wv[kRowsPerThread][8];
-    float qc[kRowsPerThread];
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    const int steps = (p.nope + 15) / 16;  // instructions per wave
+    for (int j0 = 0; j0 < steps; j0 += kBatch) {
+        Kvb8<FMT> raw[kBatch];
+        float qc[kBatch];
 #pragma unroll
-    for (int u = 0; u < kRowsPerThread; ++u) {
-        const int c = i + 32 * u;
-        qc[u] = c < p.nope ? q[c] : 0.0f;
-        if (c < p.nope) {
-            kvb_load8(p.kv_b, wrow + c, col, p.latent, wv[u]);
-        } else {
+        for (int j = 0; j < kBatch; ++j) {
+            const int i = 4 * (wave + 4 * (j0 + j)) + sub;  // nope row
+            const bool ok = j0 + j < steps && i < p.nope;
+            qc[j] = ok ? q[i] : 0.0f;
+            kvb_fetch8<FMT>(p.kv_b, wrow + (ok ? i : 0), col_ok ? col : 0, p.latent, raw[j]);
+        }
 #pragma unroll
-            for (int e = 0; e < 8; ++e) wv[u][e] = 0.0f;
+        for (int j = 0; j < kBatch; ++j) {
+            float w[8];
+            kvb_decode8<FMT>(raw[j], w);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) acc[e] = fmaf(qc[j], w[e], acc[e]);
         }
     }
-    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int u = 0; u < kRowsPerThread; ++u)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) acc[e] = fmaf(qc[u], wv[u][e], acc[e]);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) red[i][8 * j + e] = acc[e];
-    __syncthreads();
-    if (t < kMlaAbsorbCols) {
-        float v = 0.0f;
-        for (int g = 0; g < 32; ++g) v += red[g][t];
-        p.query_absorbed[((long)r * p.heads + h) * p.latent + col0 + t] = v;
+    for (int e = 0; e < 8; ++e) {
+        acc[e] += __shfl_xor(acc[e], 16, 64);
+        acc[e] += __shfl_xor(acc[e], 32, 64);
     }
+    if (sub == 0) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) red[wave][8 * (lane & 15) + e] = acc[e];
+    }
+    __syncthreads();
+    if (t < kMlaAbsorbCols && cc * kMlaAbsorbCols + t < p.latent)
+        p.query_absorbed[((long)r * p.heads + h) * p.latent + cc * kMlaAbsorbCols + t] =
+            (red[0][t] + red[1][t]) + (red[2][t] + red[3][t]);
 }
 
 
-// The same split of kMlaKeysPerSplit keys on fp32 matrix cores
-// (v_mfma_f32_16x16x4_f32: fp32 products and sums, like the VALU form, in
-// another order).  Operand layout (measured on gfx950): lane l supplies
-// A[l % 16][l / 16] and B[l / 16][l % 16]; result register i of lane l is
-// D[4 (l / 16) + i][l % 16].  Four MFMAs consume one 16-byte operand read:
-// in step j lane group g = l / 16 takes k index 4 g + j.
+// One split of kMlaKeysPerSplit keys (the reference's scores + softmax +
+// latent context, per split) on fp32 matrix cores (v_mfma_f32_16x16x4_f32:
+// fp32 products and sums, in another order than the reference).  Operand
+// layout (measured on gfx950): lane l supplies A[l % 16][l / 16] and
+// B[l / 16][l % 16]; result register i of lane l is D[4 (l / 16) + i][l % 16].
+// Four MFMAs consume one 16-byte operand read: in step j lane group g = l / 16
+// takes k index 4 g + j.  The splits cover the keys before the row's own
+// position; mla_merge_value adds the row's own (new) key, so a cache of
+// exactly 32 n keys takes n splits.  All 8 waves (two per SIMD, so one
+// wave's LDS latency hides under the other's MFMAs) copy key rows and
+// compute:
 //   scores  S[key][head] = [lat | rope][key] . [qa | q_rope][head] over the
-//           latent + rope dims; the 4 compute waves split those dims (each
-//           holds its query slices in registers, read once from L2) and meet
-//           in LDS (sums in wave order).
-//   context LC[head][d] = sum_key P[head][key] lat[key][d]; the 4 compute
-//           waves split the 16-wide d tiles.
-// 512 threads: waves 4..7 only share the DMA of the split's key rows into
-// LDS (the load is per-CU issue bound), then leave.  LDS holds the key rows
-// (latent + rope, stride kAttnRowStride floats: 16-byte aligned,
-// bank-spread) and P; the cross-wave score partials reuse the rope columns
-// once every wave is done with them.  77.5 KB: two workgroups per CU.
+//           latent + rope dims: wave w takes the 16-dim steps w, w + 8, ...
+//           for both key tiles (query slices in registers, read once from
+//           L2); the 8 partials meet in LDS in two rounds (waves 4..7 store,
+//           waves 0..3 add theirs; sums in wave order).
+//   context LC[head][d] = sum_key P[head][key] lat[key][d]: wave w takes the
+//           16-wide d tiles w, w + 8, w + 16, w + 24.
+// Loops have compile-time trip counts and no branches (steps past the
+// latent + rope width multiply a zero query slice), so every LDS read of a
+// phase is issued ahead of its MFMAs.  LDS holds the key rows (latent +
+// rope, stride kAttnRowStride floats: 16-byte aligned, bank-spread) and P;
+// the cross-wave score partials reuse the rope columns once every wave is
+// done with them.  76.5 KB: two workgroups per CU.
 constexpr int kAttnDims = kMlaMaxLatent + 64;       // latent + rope
 constexpr int kAttnRowStride = kAttnDims + 4;       // floats
 constexpr int kAttnPStride = kMlaKeysPerSplit + 4;  // floats, P[head][key]
 constexpr size_t kAttnMfmaLds =
-    sizeof(float) * ((size_t)kMlaKeysPerSplit * kAttnRowStride + kMlaMaxHeads * kAttnPStride) +
-    1024;  // + the prefetch sink
+    sizeof(float) * ((size_t)kMlaKeysPerSplit * kAttnRowStride + kMlaMaxHeads * kAttnPStride);
+static_assert(kMlaKeysPerSplit == 32, "two 16-key tiles per split");
 static_assert(4 * kMlaKeysPerSplit * kMlaMaxHeads <= kMlaKeysPerSplit * 64,
               "score partials fit the rope columns");
 
@@ -189,47 +229,49 @@ typedef float f32x4v __attribute__((ext_vector_type(4)));
 __global__ __launch_bounds__(512) void mla_attend_mfma_kernel(MlaParams p) {
     constexpr int H = kMlaMaxHeads;
     constexpr int KS = kMlaKeysPerSplit;
-    constexpr int NJ = kAttnDims / 64;  // 16-dim steps per compute wave
+    constexpr int NS = (kAttnDims / 16 + 7) / 8;  // 16-dim score steps per wave
+    constexpr int NT = kMlaMaxLatent / 16 / 8;  // 16-wide context tiles per wave
     extern __shared__ __attribute__((aligned(16))) float attn_lds[];
     float *lat_s = attn_lds;                   // [KS][stride]
     float *p_s = lat_s + KS * kAttnRowStride;  // [H][KS + 4]
     __shared__ float smax[H], ssum[H];
     const int split = blockIdx.x;
     const int r = blockIdx.y;
-    const int t = threadIdx.x & 255, lane = t & 63, wave = t >> 6;
-    const bool loader = threadIdx.x >= 256;  // waves 4..7: DMA only
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const int g = lane >> 4, m16 = lane & 15;
-    const int keys = mla_position(p) + r + 1;
+    const int D = p.latent, R = p.rope;
+    const int KD = D + R;  // a multiple of 16 (launch condition)
+    // the position first (memory reads complete in issue order)
+    const int keys = mla_position(p) + r;  // the keys before row r's own
+    // ---- this wave's query slices: dims 16 (w + 8 j) + 4 g .. + 3 of head
+    // m16; absent heads read head 0 (their outputs are unused), dims past KD
+    // are zero
+    f32x4 qv[NS];
+    {
+        const long qh = (long)r * p.heads + (m16 < p.heads ? m16 : 0);
+        const float *qa = p.query_absorbed + qh * D;
+        const float *qr = p.query_rope + qh * R;
+#pragma unroll
+        for (int j = 0; j < NS; ++j) {
+            const int d = 16 * (wave + 8 * j) + 4 * g;
+            qv[j] = d < D ? load_f4(qa + d) : d < KD ? load_f4(qr + (d - D)) : f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+    }
     const int k0 = split * KS;
     const int nk = keys - k0 < KS ? keys - k0 : KS;
     const long part = ((long)r * p.max_splits + split) * H;
     if (nk <= 0) {
-        if (threadIdx.x < H) {
+        if (t < H) {
             p.part_max[part + t] = -INFINITY;
             p.part_sum[part + t] = 0.0f;
         }
         return;
     }
-    const int D = p.latent, R = p.rope;
-    const int KD = D + R;  // a multiple of 16 (launch condition)
-    // ---- this compute wave's query slices: dims wave * 16 + 64 j + 4 g ..
-    // + 3 of head m16 (absent heads read head 0; their outputs are unused)
-    f32x4 qv[NJ];
-    if (!loader) {
-        const long qh = (long)r * p.heads + (m16 < p.heads ? m16 : 0);
-        const float *qa = p.query_absorbed + qh * D;
-        const float *qr = p.query_rope + qh * R;
-#pragma unroll
-        for (int j = 0; j < NJ; ++j) {
-            const int d = wave * 16 + 64 * j + 4 * g;
-            if (d < KD) qv[j] = d < D ? load_f4(qa + d) : load_f4(qr + (d - D));
-        }
-    }
     // ---- the split's latent + rope rows into LDS by DMA (global_load_lds:
     // 16 bytes per lane into M0 + 16 * lane), 8 waves on rows w, w + 8, ...;
     // keys past the causal end copy the last valid row (finite values, zero
     // probability)
-    for (int row = threadIdx.x >> 6; row < KS; row += 8) {
+    for (int row = wave; row < KS; row += 8) {
         const long k = k0 + (row < nk ? row : nk - 1);
         const float *lsrc = p.latent_cache + k * D;
         const float *rsrc = p.rope_cache + k * R;
@@ -248,69 +290,54 @@ __global__ __launch_bounds__(512) void mla_attend_mfma_kernel(MlaParams p) {
     }
     __builtin_amdgcn_s_waitcnt(0);  // this wave's transfers have landed
     __syncthreads();
-    if (loader) {
-        // Prefetch of the value rows of kv_b (W_UV, which mla_value reads two
-        // launches later) into L2 / the last-level cache while the compute
-        // waves work: this split's share, by DMA into a scratch LDS block
-        // nobody reads.  Bare barriers (no wait for the prefetch) match the
-        // three the compute waves still pass; the wait comes before exit.
-        if (r == 0) {
-            const long row_bytes = p.kv_b.fmt == kF32   ? (long)D * 4
-                                   : p.kv_b.fmt == kQ4 ? (long)(D + 1) / 2
-                                                        : (long)D;
-            const long per_head = (long)p.vdim * row_bytes;  // contiguous value rows
-            const long total = (long)p.heads * per_head;
-            const long share = ((total + gridDim.x - 1) / gridDim.x + 15) & ~15L;
-            const long begin = (long)split * share;
-            const long end = begin + share < total ? begin + share : total;
-            __attribute__((address_space(3))) void *sink =
-                (__attribute__((address_space(3))) void *)(p_s + H * kAttnPStride);
-            for (long o = begin + 16L * t; o + 16 <= end; o += 16L * 256) {
-                const long hh = o / per_head, within = o - hh * per_head;
-                const uint8_t *src = p.kv_b.w + (hh * (p.nope + p.vdim) + p.nope) * row_bytes + within;
-                if (within + 16 <= per_head)
-                    __builtin_amdgcn_global_load_lds(
-                        (const __attribute__((address_space(1))) void *)src, sink, 16, 0, 0);
-            }
+    // ---- scores: 16-dim steps w + 8 j of both key tiles; one chain per key
+    // tile.  Steps past KD read row columns 0.. (finite) against a zero
+    // query slice.
+    f32x4v acc[KS / 16];
+#pragma unroll
+    for (int kt = 0; kt < KS / 16; ++kt) acc[kt] = f32x4v{0.f, 0.f, 0.f, 0.f};
+    {
+        f32x4 av[NS][KS / 16];
+#pragma unroll
+        for (int j = 0; j < NS; ++j) {
+            const int d0 = 16 * (wave + 8 * j);
+#pragma unroll
+            for (int kt = 0; kt < KS / 16; ++kt)
+                av[j][kt] = *reinterpret_cast<const f32x4 *>(
+                    lat_s + (16 * kt + m16) * kAttnRowStride + (d0 < KD ? d0 : 0) + 4 * g);
         }
-        __builtin_amdgcn_s_barrier();
-        __builtin_amdgcn_s_barrier();
-        __builtin_amdgcn_s_barrier();
-        __builtin_amdgcn_s_waitcnt(0);
-        return;
-    }
-    // ---- scores: compute wave w takes the 16-dim steps w, w + 4, ...; two
-    // accumulators per key tile keep two independent chains in flight
-    f32x4v acc[KS / 16][2];
 #pragma unroll
-    for (int kt = 0; kt < KS / 16; ++kt) acc[kt][0] = acc[kt][1] = f32x4v{0.f, 0.f, 0.f, 0.f};
+        for (int j = 0; j < NS; ++j)
 #pragma unroll
-    for (int j = 0; j < NJ; ++j) {
-        const int d0 = wave * 16 + 64 * j;
-        if (d0 < KD) {
+            for (int e = 0; e < 4; ++e)
 #pragma unroll
-            for (int kt = 0; kt < KS / 16; ++kt) {
-                const f32x4 av = *reinterpret_cast<const f32x4 *>(
-                    lat_s + (16 * kt + m16) * kAttnRowStride + d0 + 4 * g);
-                acc[kt][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(av.x, qv[j].x, acc[kt][0], 0, 0, 0);
-                acc[kt][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(av.y, qv[j].y, acc[kt][1], 0, 0, 0);
-                acc[kt][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(av.z, qv[j].z, acc[kt][0], 0, 0, 0);
-                acc[kt][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(av.w, qv[j].w, acc[kt][1], 0, 0, 0);
-            }
-        }
+                for (int kt = 0; kt < KS / 16; ++kt)
+                    acc[kt] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[j][kt][e], qv[j][e], acc[kt],
+                                                                   0, 0, 0);
     }
     __syncthreads();  // every wave is done with the rope columns
-    // score partial (wave, key j, head h) at i = (wave * KS + j) * H + h, in
-    // row i / 64, column D + i % 64 (the rope part; D + 64 <= the row stride)
+    // score partial (wave w % 4, key j, head h) at i = ((w % 4) * KS + j) * H
+    // + h, in row i / 64, column D + i % 64 (the rope part; D + 64 <= the row
+    // stride): waves 4..7 store theirs, waves 0..3 add theirs to them
     auto sc_at = [&](int i) -> float & { return lat_s[(i >> 6) * kAttnRowStride + D + (i & 63)]; };
+    if (wave >= 4) {
 #pragma unroll
-    for (int kt = 0; kt < KS / 16; ++kt)
+        for (int kt = 0; kt < KS / 16; ++kt)
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-            sc_at((wave * KS + 16 * kt + 4 * g + i) * H + m16) = acc[kt][0][i] + acc[kt][1][i];
+            for (int i = 0; i < 4; ++i)
+                sc_at(((wave - 4) * KS + 16 * kt + 4 * g + i) * H + m16) = acc[kt][i];
+    }
+    __syncthreads();
+    if (wave < 4) {
+#pragma unroll
+        for (int kt = 0; kt < KS / 16; ++kt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                sc_at((wave * KS + 16 * kt + 4 * g + i) * H + m16) += acc[kt][i];
+    }
     __syncthreads();
     // ---- local softmax statistics: 16 lanes per head, keys sub, sub + 16
-    {
+    if (t < 256) {
         const int h = t >> 4, sub = t & 15;
         float sv[KS / 16];
         float mx = -INFINITY;
@@ -344,34 +371,43 @@ __global__ __launch_bounds__(512) void mla_attend_mfma_kernel(MlaParams p) {
         p.part_max[part + t] = smax[t];
         p.part_sum[part + t] = ssum[t];
     }
-    // ---- context: compute wave w takes the 16-wide d tiles w, w + 4, ...
-    // (P rows are read once per pair of tiles; the two tiles' chains interleave)
+    // ---- context: wave w takes the 16-wide d tiles w + 8 i (tiles past D
+    // read tile 0 and store nothing); P rows once per wave, all B reads of
+    // the wave issued before its MFMAs, two tiles' chains interleaved
     f32x4 pv[KS / 16];
 #pragma unroll
     for (int u = 0; u < KS / 16; ++u)
         pv[u] = *reinterpret_cast<const f32x4 *>(p_s + m16 * kAttnPStride + 16 * u + 4 * g);
-    for (int dt = wave; dt < D / 16; dt += 8) {
-        const bool two = dt + 4 < D / 16;
-        f32x4v cacc[2] = {f32x4v{0.f, 0.f, 0.f, 0.f}, f32x4v{0.f, 0.f, 0.f, 0.f}};
+    float bv[NT][KS / 16][4];
 #pragma unroll
-        for (int u = 0; u < KS / 16; ++u) {
-            const float *lb = lat_s + (16 * u + 4 * g) * kAttnRowStride + dt * 16 + m16;
-            const float *lb2 = two ? lb + 64 : lb;
-            const float pj[4] = {pv[u].x, pv[u].y, pv[u].z, pv[u].w};
+    for (int i = 0; i < NT; ++i) {
+        const int dt = wave + 8 * i;
+        const int col = (dt < D / 16 ? dt : 0) * 16 + m16;
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                cacc[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(pj[j], lb[j * kAttnRowStride],
-                                                              cacc[0], 0, 0, 0);
-                cacc[1] = __builtin_amdgcn_mfma_f32_16x16x4f32(pj[j], lb2[j * kAttnRowStride],
-                                                              cacc[1], 0, 0, 0);
-            }
-        }
+        for (int u = 0; u < KS / 16; ++u)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int h = 4 * g + i;
-            if (h < p.heads) {
-                p.part_lc[(part + h) * D + dt * 16 + m16] = cacc[0][i];
-                if (two) p.part_lc[(part + h) * D + (dt + 4) * 16 + m16] = cacc[1][i];
+            for (int j = 0; j < 4; ++j) bv[i][u][j] = lat_s[(16 * u + 4 * g + j) * kAttnRowStride + col];
+    }
+    f32x4v cacc[NT];
+#pragma unroll
+    for (int i = 0; i < NT; ++i) cacc[i] = f32x4v{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int u = 0; u < KS / 16; ++u) {
+        const float pj[4] = {pv[u].x, pv[u].y, pv[u].z, pv[u].w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int i = 0; i < NT; ++i)
+                cacc[i] = __builtin_amdgcn_mfma_f32_16x16x4f32(pj[j], bv[i][u][j], cacc[i], 0, 0, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < NT; ++i) {
+        const int dt = wave + 8 * i;
+        if (dt < D / 16) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int h = 4 * g + q;
+                if (h < p.heads) p.part_lc[(part + h) * D + dt * 16 + m16] = cacc[i][q];
             }
         }
     }
@@ -693,52 +729,93 @@ __global__ __launch_bounds__(256, 2) void mla_prefill_attend_kernel(MlaParams p)
     }
 }
 
-// lc_h = sum_s e^{m_s - M} lc_s / sum_s e^{m_s - M} l_s over the key splits,
-// in one pass.  Workgroup (row, head, kMergeDims latent dims), 8 waves; a
-// wave's lanes form 64 / kMergeDims groups, so 16 lane groups take the splits
-// g, g + 16, ... with a running max (rescaling on a new max), loading
-// kMergeBatch splits before using them; the groups meet in LDS.
-constexpr int kMergeDims = 32;
-constexpr int kMergeBatch = 8;
-__global__ __launch_bounds__(512) void mla_merge_kernel(MlaParams p) {
+// Merge of the key splits and the value projection, one launch.  Workgroup
+// (row, head h, chunk c of kMlaValueDims latent dims), 8 waves:
+//   merge  lc_h[d] = sum_s e^{m_s - M} lc_s[d] / sum_s e^{m_s - M} l_s for
+//          the chunk's dims in one pass: the wave's lanes form 64 /
+//          kMlaValueDims groups, so 16 lane groups take the splits g, g + 16,
+//          ... with a running max (rescaling on a new max), loading
+//          kMergeBatch splits before using them; the groups meet in LDS.
+//          The row's own key (not in any split) joins as one more term: its
+//          score [qa | q_rope] . [lat | rope] over the whole workgroup, its
+//          weight 1 and its latent row.
+//   value  y_c[v] = W_UV_h[v, chunk] . lc_h[chunk] for every value row v:
+//          thread t takes row t / 4 (+ 128 per pass), dims 8 (t % 4) .. + 7;
+//          the first pass's weights are loaded before the merge starts.
+//   sum    ctx_h[v] = sum_c y_c[v] in chunk order, by the chunk workgroup
+//          that arrives last (merge_count; it resets the counter).  The
+//          shares travel as device-coherent (agent-scope) stores and loads,
+//          which on gfx950 bypass the per-XCD L2 copies: each workgroup
+//          waits for its stores to complete before its arrival increment, so
+//          the workgroup that counts last finds every share in memory, with
+//          no L2 write-back fence.
+constexpr int kMergeBatch = 16;
+template <int FMT>
+__global__ __launch_bounds__(512) void mla_merge_value_kernel(MlaParams p) {
     constexpr int H = kMlaMaxHeads;
     constexpr int KS = kMlaKeysPerSplit;
-    constexpr int DL = kMergeDims, NB = kMergeBatch;
+    constexpr int DL = kMlaValueDims, NB = kMergeBatch;
     constexpr int NG = 8 * (64 / DL);  // lane groups
     __shared__ float gm[NG], gl[NG];
     __shared__ float gacc[NG][DL];
-    const int r = blockIdx.x, h = blockIdx.y;
+    __shared__ float lcs[DL];
+    __shared__ float ownp[8];
+    __shared__ int last;
+    const int r = blockIdx.x, h = blockIdx.y, c = blockIdx.z;
+    const int nchunks = gridDim.z;
     const int t = threadIdx.x, lane = t & 63;
     const int dl = lane % DL, grp = (t >> 6) * (64 / DL) + lane / DL;
-    const int keys = mla_position(p) + r + 1;
+    // the position first: memory reads complete in issue order, so a wait
+    // for it does not also wait for the weight fetch below
+    const int pos = mla_position(p) + r;  // row r's own key; the splits hold keys 0 .. pos - 1
+    const int keys = pos;
+    // value rows of this thread: v = t / 4 + 128 i; dims c * DL + 8 (t % 4) ..
+    const int vq = t & 3, vr = t >> 2;
+    const int wrow0 = h * (p.nope + p.vdim) + p.nope;
+    const int vcol = c * DL + 8 * vq;
+    Kvb8<FMT> wraw;
+    kvb_fetch8<FMT>(p.kv_b, wrow0 + (vr < p.vdim ? vr : 0), vcol, p.latent, wraw);
+
+    // the own key's score terms (thread t: latent dim t, rope dim t) and
+    // its latent value in this chunk
+    const float *qa = p.query_absorbed + ((long)r * p.heads + h) * p.latent;
+    const float *qr = p.query_rope + ((long)r * p.heads + h) * p.rope;
+    const float *lnew = p.latent_cache + (long)pos * p.latent;
+    const float *rnew = p.rope_cache + (long)pos * p.rope;
+    float own = t < p.latent ? qa[t] * lnew[t] : 0.0f;
+    if (t < p.rope) own = fmaf(qr[t], rnew[t], own);
+    const float own_v = t < DL ? lnew[c * DL + t] : 0.0f;
+
     const int ns = (keys + KS - 1) / KS;
     const long base = (long)r * p.max_splits * H + h;
-    const float *lc = p.part_lc + base * p.latent + blockIdx.z * DL + dl;
+    const float *lc = p.part_lc + base * p.latent + c * DL + dl;
     const long lc_step = (long)H * p.latent;
     float M = -INFINITY, L = 0.0f, acc = 0.0f;
+    // branch-free batches (selects, no ifs), so that the compiler keeps all
+    // of a batch's loads ahead of their first use
     for (int s0 = grp; s0 < ns; s0 += NG * NB) {
         float mv[NB], lv[NB], v[NB];
+        bool ok[NB];
 #pragma unroll
         for (int i = 0; i < NB; ++i) {
-            const int s = s0 + NG * i < ns ? s0 + NG * i : s0;  // clamped: loaded, unused
+            ok[i] = s0 + NG * i < ns;
+            const int s = ok[i] ? s0 + NG * i : s0;  // clamped: loaded, unused
             mv[i] = p.part_max[base + (long)s * H];
             lv[i] = p.part_sum[base + (long)s * H];
             v[i] = lc[(long)s * lc_step];
         }
         float mn = M;
 #pragma unroll
-        for (int i = 0; i < NB; ++i)
-            if (s0 + NG * i < ns) mn = fmaxf(mn, mv[i]);
-        const float sc = expf(M - mn);  // 0 while M is -inf
+        for (int i = 0; i < NB; ++i) mn = fmaxf(mn, ok[i] ? mv[i] : -INFINITY);
+        // split s0 is valid, so mn is finite; the rescale is 0 while M is -inf
+        const float sc = expf(M - mn);
         acc *= sc;
         L *= sc;
 #pragma unroll
         for (int i = 0; i < NB; ++i) {
-            if (s0 + NG * i < ns) {
-                const float e = expf(mv[i] - mn);
-                acc = fmaf(e, v[i], acc);
-                L = fmaf(e, lv[i], L);
-            }
+            const float e = ok[i] ? expf(mv[i] - mn) : 0.0f;
+            acc = fmaf(e, v[i], acc);
+            L = fmaf(e, lv[i], L);
         }
         M = mn;
     }
@@ -747,49 +824,65 @@ __global__ __launch_bounds__(512) void mla_merge_kernel(MlaParams p) {
         gl[grp] = L;
     }
     gacc[grp][dl] = acc;
+    own = wave_sum(own);
+    if (lane == 0) ownp[t >> 6] = own;
     __syncthreads();
     if (t < DL) {
-        float mt = gm[0];  // group 0 holds split 0: finite
-        for (int i = 1; i < NG; ++i) mt = fmaxf(mt, gm[i]);
+        const float snew =
+            (((ownp[0] + ownp[1]) + (ownp[2] + ownp[3])) + ((ownp[4] + ownp[5]) + (ownp[6] + ownp[7]))) *
+            p.scale;
+        float mt = snew;  // groups without a split hold -inf
+        for (int i = 0; i < NG; ++i) mt = fmaxf(mt, gm[i]);
         float a = 0.0f, l = 0.0f;
         for (int i = 0; i < NG; ++i) {
             const float e = gm[i] == -INFINITY ? 0.0f : expf(gm[i] - mt);
             a = fmaf(e, gacc[i][t], a);
             l = fmaf(e, gl[i], l);
         }
-        p.latent_context[((long)r * p.heads + h) * p.latent + blockIdx.z * DL + t] = a / l;
+        const float en = expf(snew - mt);
+        a = fmaf(en, own_v, a);
+        l += en;
+        lcs[t] = a / l;
     }
-}
-
-// ctx_h[v] = W_UV_h[v, :] . lc_h: one wave per 8 value rows, lanes over
-// 8-column slices, transposed-butterfly reduction of the 8 rows.
-__global__ __launch_bounds__(256) void mla_value_kernel(MlaParams p) {
-    const int r = blockIdx.x, h = blockIdx.y;
-    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-    const int v0 = blockIdx.z * 32 + wave * 8;
-    const float *lc = p.latent_context + ((long)r * p.heads + h) * p.latent;
-    const int wrow0 = h * (p.nope + p.vdim) + p.nope;
-    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    for (int col = 8 * lane; col < p.latent; col += 512) {
-        float x[8];
-        const f32x4 a = load_f4(lc + col), b = load_f4(lc + col + 4);
-        x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w;
-        x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
-        float wv[8][8];
+    __syncthreads();
+    float *part = p.value_part + (((long)r * p.heads + h) * nchunks + c) * p.vdim;
+    for (int v0 = 0; v0 < p.vdim; v0 += 128) {
+        const int v = v0 + vr;
+        if (v0 > 0) kvb_fetch8<FMT>(p.kv_b, wrow0 + (v < p.vdim ? v : 0), vcol, p.latent, wraw);
+        float wv[8];
+        kvb_decode8<FMT>(wraw, wv);
+        float y = 0.0f;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const int row = wrow0 + (v0 + i < p.vdim ? v0 + i : v0);
-            kvb_load8(p.kv_b, row, col, p.latent, wv[i]);
-        }
-#pragma unroll
-        for (int i = 0; i < 8; ++i)
-#pragma unroll
-            for (int e = 0; e < 8; ++e) acc[i] = fmaf(x[e], wv[i][e], acc[i]);
+        for (int e = 0; e < 8; ++e) y = fmaf(wv[e], lcs[8 * vq + e], y);
+        y += __shfl_xor(y, 1, 64);
+        y += __shfl_xor(y, 2, 64);
+        if (vq == 0 && v < p.vdim)
+            __hip_atomic_store(part + v, y, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
-    butterfly_reduce<8, 64>(acc, lane);
-    const int vi = butterfly_index<8, 64>(lane);
-    if (butterfly_writer<8, 64>(lane) && v0 + vi < p.vdim)
-        p.context[((long)r * p.heads + h) * p.vdim + v0 + vi] = acc[0];
+    // the last of the head's chunk workgroups sums the shares
+    __builtin_amdgcn_s_waitcnt(0);  // this thread's share stores have completed
+    __syncthreads();
+    int *count = p.merge_count + (r * p.heads + h) * kMlaCountStride;
+    if (t == 0)
+        last = __hip_atomic_fetch_add(count, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+               nchunks - 1;
+    __syncthreads();
+    if (!last) return;
+    constexpr int kMaxChunks = kMlaMaxLatent / kMlaValueDims;
+    const float *parts = p.value_part + ((long)r * p.heads + h) * nchunks * p.vdim;
+    for (int v = t; v < p.vdim; v += 512) {
+        float sh[kMaxChunks];  // all shares in flight before the first add
+#pragma unroll
+        for (int i = 0; i < kMaxChunks; ++i)
+            sh[i] = i < nchunks ? __hip_atomic_load(parts + (long)i * p.vdim + v,
+                                                    __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                                : 0.0f;
+        float y = 0.0f;
+#pragma unroll
+        for (int i = 0; i < kMaxChunks; ++i) y += sh[i];
+        p.context[((long)r * p.heads + h) * p.vdim + v] = y;
+    }
+    if (t == 0) __hip_atomic_store(count, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 
@@ -813,7 +906,8 @@ int mla_attention_core(const MlaParams &p, hipStream_t stream) {
             hipFuncAttributeMaxDynamicSharedMemorySize, (int)pf_lds_bytes<RB>()) == hipSuccess;
         (void)attr;
         const unsigned mt = (unsigned)((p.rows + 63) / 64);
-        hipLaunchKernelGGL(mla_prep_kernel, dim3(p.rows, 1 + p.heads), dim3(256), 0, stream, p, 0);
+        hipLaunchKernelGGL(mla_prep_kernel<kF32>, dim3(p.rows, 1 + p.heads), dim3(256), 0, stream,
+                           p, 0);
         hipLaunchKernelGGL(mla_head_gemm_kernel<true>,
                            dim3(mt, (unsigned)((p.latent + 63) / 64), (unsigned)p.heads), dim3(256),
                            0, stream, p);
@@ -824,20 +918,44 @@ int mla_attention_core(const MlaParams &p, hipStream_t stream) {
                            0, stream, p);
         return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
     }
-    hipLaunchKernelGGL(mla_prep_kernel, dim3(p.rows, 1 + p.heads * (p.latent / kMlaAbsorbCols)),
-                       dim3(256), 0, stream, p, p.latent / kMlaAbsorbCols);
-    const int splits = p.grid_splits ? p.grid_splits
-                                     : (p.position + p.rows + kMlaKeysPerSplit - 1) / kMlaKeysPerSplit;
-    const dim3 grid(splits, p.rows);
+    // decode: groups of at most kMlaDecodeRows rows (the partial buffers'
+    // capacity), three launches each
+    if (!p.value_part || !p.merge_count || p.latent % kMlaValueDims ||
+        (p.position_dev && p.rows > kMlaDecodeRows) ||
+        (p.kv_b.fmt != kF32 && p.kv_b.fmt != kQ8 && p.kv_b.fmt != kQ4))
+        return kErrArgs;
     static const bool attr = hipFuncSetAttribute(
         reinterpret_cast<const void *>(&mla_attend_mfma_kernel),
         hipFuncAttributeMaxDynamicSharedMemorySize, (int)kAttnMfmaLds) == hipSuccess;
     (void)attr;
-    hipLaunchKernelGGL(mla_attend_mfma_kernel, grid, dim3(512), kAttnMfmaLds, stream, p);
-    hipLaunchKernelGGL(mla_merge_kernel, dim3(p.rows, p.heads, p.latent / kMergeDims), dim3(512),
-                       0, stream, p);
-    hipLaunchKernelGGL(mla_value_kernel, dim3(p.rows, p.heads, (p.vdim + 31) / 32), dim3(256), 0,
-                       stream, p);
+    for (int r0 = 0; r0 < p.rows; r0 += kMlaDecodeRows) {
+        MlaParams q = p;
+        q.rows = p.rows - r0 < kMlaDecodeRows ? p.rows - r0 : kMlaDecodeRows;
+        q.position = p.position + r0;
+        q.query = p.query + (long)r0 * p.query_stride;
+        q.compressed = p.compressed + (long)r0 * p.compressed_stride;
+        q.context = p.context + (long)r0 * p.heads * p.vdim;
+        const int chunks = (q.latent + kMlaAbsorbCols - 1) / kMlaAbsorbCols;
+        const dim3 pgrid(q.rows, 1 + q.heads * chunks);
+        const dim3 mgrid(q.rows, q.heads, q.latent / kMlaValueDims);
+        switch (q.kv_b.fmt) {
+        case kF32: hipLaunchKernelGGL(mla_prep_kernel<kF32>, pgrid, dim3(256), 0, stream, q, chunks); break;
+        case kQ8: hipLaunchKernelGGL(mla_prep_kernel<kQ8>, pgrid, dim3(256), 0, stream, q, chunks); break;
+        default: hipLaunchKernelGGL(mla_prep_kernel<kQ4>, pgrid, dim3(256), 0, stream, q, chunks); break;
+        }
+        // row r's splits hold keys 0 .. position + r - 1 (its own key joins
+        // in the merge)
+        const int last_keys = q.position + q.rows - 1;
+        const int needed = (last_keys + kMlaKeysPerSplit - 1) / kMlaKeysPerSplit;
+        const int splits = q.grid_splits ? q.grid_splits : (needed > 0 ? needed : 1);
+        hipLaunchKernelGGL(mla_attend_mfma_kernel, dim3(splits, q.rows), dim3(512), kAttnMfmaLds,
+                           stream, q);
+        switch (q.kv_b.fmt) {
+        case kF32: hipLaunchKernelGGL(mla_merge_value_kernel<kF32>, mgrid, dim3(512), 0, stream, q); break;
+        case kQ8: hipLaunchKernelGGL(mla_merge_value_kernel<kQ8>, mgrid, dim3(512), 0, stream, q); break;
+        default: hipLaunchKernelGGL(mla_merge_value_kernel<kQ4>, mgrid, dim3(512), 0, stream, q); break;
+        }
+    }
     return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
 }
 

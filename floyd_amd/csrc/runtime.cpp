@@ -112,6 +112,8 @@ struct MoonlightSession {
     float *h = nullptr, *tmp = nullptr, *query = nullptr, *compressed = nullptr;
     float *query_rope = nullptr, *query_absorbed = nullptr, *context = nullptr;
     float *part_max = nullptr, *part_sum = nullptr, *part_lc = nullptr, *latent_ctx = nullptr;
+    float *value_part = nullptr;  // decode MLA value shares
+    int *merge_count = nullptr;                             // zeroed at creation
     float *latent_kv = nullptr, *rope_kv = nullptr, *logits = nullptr;
     float *router_logits = nullptr, *route_weights = nullptr;
     int *route_ids = nullptr, *n_unique = nullptr, *unique = nullptr, *counts = nullptr;
@@ -1022,6 +1024,8 @@ int attention(MoonlightSession *s, int layer, const float *x, int rows, int posi
     p.part_lc = s->part_lc;
     p.latent_context = s->latent_ctx;
     p.context = s->context;
+    p.value_part = s->value_part;
+    p.merge_count = s->merge_count;
     if (int e = mla_attention_core(p, stream_of(s))) return e;
     return gemv_rows(s, lp.o, s->context, rows, c.head_count * c.value_dim, c.hidden_size, out,
                      nullptr, resid);
@@ -1448,11 +1452,13 @@ extern "C" int moonlight_session_create(MoonlightSession **out, MoonlightModel *
     const size_t heads = (size_t)c.head_count;
     s->max_splits = (int)((ctx + kMlaKeysPerSplit - 1) / kMlaKeysPerSplit);
     const size_t splits = (size_t)s->max_splits;
+    // the split-attention (decode) path runs at most kMlaDecodeRows rows per launch group
+    const size_t dr = mb < (size_t)kMlaDecodeRows ? mb : (size_t)kMlaDecodeRows;
     const size_t sw = (size_t)c.moe_intermediate_size * c.shared_expert_count;
     size_t lat_elems, rope_elems, lc_elems, logit_elems;
     if (!mul_ok(L * ctx, (size_t)c.kv_lora_rank, &lat_elems) ||
         !mul_ok(L * ctx, (size_t)c.qk_rope_dim, &rope_elems) ||
-        !mul_ok(mb * splits * kMlaMaxHeads, (size_t)c.kv_lora_rank, &lc_elems) ||
+        !mul_ok(dr * splits * kMlaMaxHeads, (size_t)c.kv_lora_rank, &lc_elems) ||
         !mul_ok(mb, (size_t)c.vocab_size, &logit_elems)) {
         delete s;
         return set_error(error, error_size, "Moonlight session size overflow");
@@ -1474,9 +1480,14 @@ extern "C" int moonlight_session_create(MoonlightSession **out, MoonlightModel *
         session_alloc(s, &s->context, mb * heads * c.value_dim, error, error_size) &&
         session_alloc(s, &s->query_rope, mb * heads * c.qk_rope_dim, error, error_size) &&
         session_alloc(s, &s->query_absorbed, mb * heads * c.kv_lora_rank, error, error_size) &&
-        session_alloc(s, &s->part_max, mb * splits * kMlaMaxHeads, error, error_size) &&
-        session_alloc(s, &s->part_sum, mb * splits * kMlaMaxHeads, error, error_size) &&
+        session_alloc(s, &s->part_max, dr * splits * kMlaMaxHeads, error, error_size) &&
+        session_alloc(s, &s->part_sum, dr * splits * kMlaMaxHeads, error, error_size) &&
         session_alloc(s, &s->part_lc, lc_elems, error, error_size) &&
+        session_alloc(s, &s->value_part,
+                      dr * heads * (c.kv_lora_rank / kMlaValueDims) * (size_t)c.value_dim, error,
+                      error_size) &&
+        session_alloc(s, &s->merge_count, dr * heads * kMlaCountStride, error, error_size) &&
+        hipMemset(s->merge_count, 0, dr * heads * kMlaCountStride * sizeof(int)) == hipSuccess &&
         session_alloc(s, &s->latent_ctx, mb * heads * c.kv_lora_rank, error, error_size) &&
         session_alloc(s, &s->router_logits, mb * E, error, error_size) &&
         session_alloc(s, &s->route_ids, mb * K, error, error_size) &&
@@ -1898,6 +1909,35 @@ extern "C" int moonlight_session_time_moe(MoonlightSession *s, int layer, int ro
     if (hipEventElapsedTime(&ms, s->ev_start, s->ev_stop) != hipSuccess) return 0;
     *avg_us = (double)ms * 1000.0 / iters;
     if (unique_experts) *unique_experts = s->host_ids[0];
+    return 1;
+}
+
+extern "C" int moonlight_session_time_attention(MoonlightSession *s, int layer, int rows,
+                                                int position, uint64_t seed, int warmup,
+                                                int iters, double *avg_us) {
+    if (!s || !avg_us || rows <= 0 || rows > s->options.max_batch || iters <= 0 || warmup < 0 ||
+        position < 0 || position + rows > s->options.context_size)
+        return 0;
+    const ModelConfig &c = s->model->cfg;
+    if (layer < 0 || layer >= c.layer_count || c.q_lora_rank ||
+        !s->model->layers[layer].error.empty())
+        return 0;
+    const LayerPlan &lp = s->model->layers[layer];
+    hipStream_t st = stream_of(s);
+    if (fill_normal(s->tmp, (int64_t)rows * c.hidden_size, seed, 0.0f, 1.0f, 0, st) != kOk)
+        return 0;
+    auto pass = [&]() {
+        return attention(s, layer, s->tmp, rows, position, s->h, lp.input_norm, s->tmp) == kOk;
+    };
+    bool ok = true;
+    for (int i = 0; ok && i < warmup; ++i) ok = pass();
+    ok = ok && hipEventRecord(s->ev_start, st) == hipSuccess;
+    for (int i = 0; ok && i < iters; ++i) ok = pass();
+    ok = ok && hipEventRecord(s->ev_stop, st) == hipSuccess;
+    if (!finish(s) || !ok) return 0;
+    float ms = 0.0f;
+    if (hipEventElapsedTime(&ms, s->ev_start, s->ev_stop) != hipSuccess) return 0;
+    *avg_us = (double)ms * 1000.0 / iters;
     return 1;
 }
 

@@ -99,6 +99,8 @@ SIGNATURES = {
     "moonlight_session_time_moe": (C.c_int, [_vp, C.c_int, C.c_int, C.c_uint64, C.c_int,
                                              C.c_int, C.POINTER(C.c_double),
                                              C.POINTER(C.c_int)]),
+    "moonlight_session_time_attention": (C.c_int, [_vp, C.c_int, C.c_int, C.c_int, C.c_uint64,
+                                                   C.c_int, C.c_int, C.POINTER(C.c_double)]),
 }
 
 _bound = False
@@ -340,6 +342,13 @@ class Session:
                                                 C.byref(us), C.byref(uniq)):
             raise SessionError("time_moe failed")
         return us.value, uniq.value
+
+    def time_attention(self, layer, rows, position, seed=7, warmup=5, iters=50):
+        us = C.c_double()
+        if not lib().moonlight_session_time_attention(self.handle, layer, rows, position, seed,
+                                                      warmup, iters, C.byref(us)):
+            raise SessionError("time_attention failed")
+        return us.value
 
     # ---- test hooks (0 = failure, no message) ----
     def test_embed(self, ids):

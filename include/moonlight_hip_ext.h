@@ -80,6 +80,19 @@ int moonlight_session_time_moe(MoonlightSession *session, int layer, int rows,
                                uint64_t seed, int warmup, int iters,
                                double *avg_us, int *unique_experts);
 
+/* Times `iters` back-to-back device passes of one attention block exactly as
+ * a decode runs it (the [q | kv_a] GEMV with the input RMSNorm, cache
+ * append, query RoPE and absorb, split attention over the `position` cached
+ * keys plus the new rows, merge, value and o_proj with the residual) on
+ * `rows` token rows drawn ~N(0, 1) from `seed`, at cache position
+ * `position` (0 <= position, position + rows <= context_size; the cache rows
+ * at position .. position + rows - 1 are rewritten by every pass and the
+ * session's cache lengths are left unchanged).  avg_us: HIP-event time per
+ * pass. */
+int moonlight_session_time_attention(MoonlightSession *session, int layer, int rows,
+                                     int position, uint64_t seed, int warmup, int iters,
+                                     double *avg_us);
+
 /* Fixes the routed experts of the next moonlight_test_moe /
  * moonlight_session_time_moe calls: token row r uses expert_ids[r * top_k ..]
  * (moe_route_fixed semantics, moe_route.h:76-87: weights are the router's
