@@ -311,6 +311,8 @@ std::string gemv_kernel_name(int fmt, int O, int I, int rows, bool dual) {
 
 static bool aligned16(const void *ptr) { return ((uintptr_t)ptr & 15u) == 0; }
 
+bool gemv_mfma(const GemvParams &p, hipStream_t stream);  // gemv_mfma.hip
+
 int gemv(const GemvParams &p_in, hipStream_t stream) {
     if (!p_in.w || !p_in.x || !p_in.y || p_in.O <= 0 || p_in.I <= 0 || p_in.rows <= 0)
         return kErrArgs;
@@ -318,6 +320,9 @@ int gemv(const GemvParams &p_in, hipStream_t stream) {
     if (p_in.epilogue == kEpiSiluDual && (!p_in.w2 || (p_in.fmt != kF32 && !p_in.s2)))
         return kErrArgs;
     if (p_in.epilogue == kEpiResidual && !p_in.resid) return kErrArgs;
+    // q8 / q4 with up to 4 token rows: the matrix-core kernel when it takes the shape
+    if (gemv_mfma(p_in, stream))
+        return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
     const long row_bytes = row_bytes_of(p_in.fmt, p_in.I);
     const bool vector_ok =
         row_bytes % 16 == 0 && (p_in.fmt != kQ4 || p_in.I % 2 == 0) &&

@@ -1,0 +1,438 @@
+// gemv_mfma.hip -- q8 / q4 dequant GEMV for 1..4 token rows on int8 matrix
+// cores (gfx950: v_mfma_i32_16x16x64_i8).
+//
+// Semantics are those of gemv() (moonlight_kernels.metal:43-130 and the
+// RMSNorm / residual / SwiGLU variants, :23-41, :533-541):
+//     y[b, o] = s[o] * sum_i W[o, i] * x'[b, i],  x' = RMSNorm(x) or x.
+//
+// Numerics.  Each wave splits its quarter of the k range of every token row
+// b into four int8 limbs against a power-of-two step 2^-e (chosen so that
+// the wave's largest |x| maps below 2^30):
+//     x ~= 2^-e * q,  q = rint(x * 2^e) = 2^24 L0 + 2^16 L1 + 2^8 L2 + L3,
+// L0 in [-64, 64], L1..L3 in [-128, 127].  x * 2^e is exact in fp32, so the
+// only rounding is rint's (at most half a step, and never more than fp32's
+// own rounding of x for the wave's larger elements).  The products of the
+// stored weights with each limb are exact int32 sums on the matrix cores;
+// the limbs are combined and scaled in fp32 once per wave, the four waves'
+// shares added in fp32 and multiplied by the row scale.  q4 weights enter as
+// the stored nibbles u = q + 8 (0..15); 8 * (sum of the limbs) comes off
+// with one extra MFMA against a ones operand.  With RMSNorm the limbs are
+// taken of x * norm_w and the 1 / rms factor is applied to the sum.
+//
+// Work decomposition.  A workgroup (4 waves) owns 16 output rows (16 gate +
+// 16 up rows for SwiGLU); wave w takes the k quarter [w I / 4, (w + 1) I /
+// 4).  A wave copies its weight rows of the quarter into its own LDS region
+// by DMA (global_load_lds, 1 KB per instruction, contiguous row runs: 256
+// bytes and more per row), loads and splits its x quarter meanwhile, then
+// runs one MFMA per 64-k step: A = the x limbs (MFMA row 4 L + b), B = the
+// 16 weight rows.  Only the final cross-wave sum meets in LDS (one
+// barrier).  LDS rows of weights are XOR-swizzled in 16-byte chunks so the
+// 16 rows an operand read touches hit distinct banks.
+#include "mlh_device.h"
+#include "mlh_host.h"
+
+namespace mlh {
+
+namespace {
+
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+
+// 16-byte global load the compiler does not track.  The compiler treats LDS
+// DMA and register loads as one out-of-order counter and would wait for the
+// whole DMA before the first use of a register loaded ahead of it; these
+// loads instead complete in issue order before the DMA (memory reads return
+// in order) and are waited for explicitly with wait_loaded<N>.
+__device__ __forceinline__ f32x4 load16_untracked(const float *p) {
+    f32x4 v;
+    asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(v) : "v"(p) : "memory");
+    return v;
+}
+// s_waitcnt vmcnt(N), tying v to it: uses of v cannot move above the wait.
+template <int N>
+__device__ __forceinline__ void wait_loaded(f32x4 &v) {
+    asm volatile("s_waitcnt vmcnt(%1)" : "+v"(v) : "n"(N));
+}
+
+// Wave reductions on DPP only (no LDS instruction: with an LDS DMA in flight
+// the compiler would wait for it before any LDS instruction, ds_bpermute
+// included).  Lane 63 ends with the total; every lane gets it by readlane.
+#define MLH_DPP(v, ctrl, rmask) \
+    __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), ctrl, rmask, 0xF, false))
+__device__ __forceinline__ float dpp_wave_sum(float v) {
+    v += MLH_DPP(v, 0xB1, 0xF);   // quad_perm [1,0,3,2]
+    v += MLH_DPP(v, 0x4E, 0xF);   // quad_perm [2,3,0,1]
+    v += MLH_DPP(v, 0x141, 0xF);  // row_half_mirror
+    v += MLH_DPP(v, 0x140, 0xF);  // row_mirror
+    // row_bcast15 / row_bcast31 write only the masked rows: the others add
+    // their own value, so they are not read below
+    const float b15 = MLH_DPP(v, 0x142, 0xA);
+    v = (threadIdx.x & 16) ? v + b15 : v;
+    const float b31 = MLH_DPP(v, 0x143, 0xC);
+    v = (threadIdx.x & 32) ? v + b31 : v;
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+__device__ __forceinline__ float dpp_wave_max(float v) {
+    v = fmaxf(v, MLH_DPP(v, 0xB1, 0xF));
+    v = fmaxf(v, MLH_DPP(v, 0x4E, 0xF));
+    v = fmaxf(v, MLH_DPP(v, 0x141, 0xF));
+    v = fmaxf(v, MLH_DPP(v, 0x140, 0xF));
+    v = fmaxf(v, MLH_DPP(v, 0x142, 0xA));
+    v = fmaxf(v, MLH_DPP(v, 0x143, 0xC));
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+#undef MLH_DPP
+
+constexpr int kRows = 16;         // output rows per workgroup
+constexpr int kXPad = 64;         // bytes of padding per LDS limb row (bank spread)
+
+// Byte position of element e (0..15) of a 16-element k slice in the limb
+// rows: q4 nibble unpacking yields elements 0,2,4,6 | 1,3,5,7 | 8,10,12,14 |
+// 9,11,13,15, and the limbs are stored in that order.
+template <int FMT>
+__device__ __forceinline__ int slice_pos(int e) {
+    if constexpr (FMT == kQ4) return (e & 8) + ((e & 1) << 2) + ((e & 7) >> 1);
+    return e;
+}
+
+struct MfmaGemvArgs {
+    GemvParams p;
+    int ndma;  // DMA instructions per wave (selects the instantiation)
+};
+
+// ND: DMA instructions per wave (a compile-time count, so that the wait for
+// the x loads issued before them is exact)
+template <int FMT, int B, bool DUAL, int ND>
+struct MgShape {
+    static constexpr int kNr = DUAL ? 2 * kRows : kRows;      // weight rows
+    static constexpr int kKqb = ND * 1024 / kNr;              // weight bytes per row and wave
+    static constexpr int kKq = FMT == kQ8 ? kKqb : 2 * kKqb;  // k elements per wave
+    static constexpr int kI = 4 * kKq;
+    static constexpr int kPass = (kKq + 511) / 512;          // x passes of 8 elements per lane
+    static constexpr int kXrow = kKq + kXPad;
+    static constexpr int kWaveLds = 4 * B * kXrow + kNr * kKqb;
+    static constexpr int kNch = kKqb / 16;
+    static constexpr int kSwz = kNch % 16 == 0 ? 15 : kNch % 8 == 0 ? 7 : kNch % 4 == 0 ? 3 : 0;
+};
+
+template <int FMT, int B, bool DUAL, int ND>
+__global__ __launch_bounds__(256) void gemv_mfma_kernel(MfmaGemvArgs a) {
+    using Sh = MgShape<FMT, B, DUAL, ND>;
+    const GemvParams &p = a.p;
+    extern __shared__ __attribute__((aligned(16))) unsigned char gm_lds[];
+    __shared__ float red[4][2][B][kRows];
+    __shared__ float red_ss[4][B];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int row0 = blockIdx.x * kRows;
+    constexpr int row_bytes = FMT == kQ8 ? Sh::kI : Sh::kI / 2;
+    constexpr int kq = Sh::kKq, kqb = Sh::kKqb, xrow = Sh::kXrow, swz = Sh::kSwz;
+    const int k0 = wave * kq;
+    unsigned char *xl = gm_lds + wave * Sh::kWaveLds;  // [4 limbs][B][xrow]
+    unsigned char *wl = xl + 4 * B * xrow;              // [nr][kqb], 16-byte chunks swizzled
+
+    // ---- 1. x of this wave's quarter (and norm_w): 8 elements per lane and
+    // pass, all loads unconditional (norm_w absent: x itself, unused), issued
+    // before the weight DMA so that the wait for them leaves the DMA in flight
+    constexpr int kMaxPass = Sh::kPass;
+    const bool has_norm = p.norm_w != nullptr;
+    const float *nw = has_norm ? p.norm_w : p.x;
+    f32x4 xv[kMaxPass][B][2];
+    f32x4 nv[kMaxPass][2];
+#pragma unroll
+    for (int j = 0; j < kMaxPass; ++j) {
+        const int e = j * 512 + lane * 8;
+        const int ec = e < kq ? e : 0;
+#pragma unroll
+        for (int b = 0; b < B; ++b) {
+            const float *xb = p.x + (long)b * p.x_stride + k0 + ec;
+            xv[j][b][0] = load16_untracked(xb);
+            xv[j][b][1] = load16_untracked(xb + 4);
+        }
+        nv[j][0] = load16_untracked(nw + k0 + ec);
+        nv[j][1] = load16_untracked(nw + k0 + ec + 4);
+    }
+    // ---- 2. the weight rows of the quarter into LDS: instruction d writes
+    // bytes [1024 d, 1024 d + 1024) of the region; lane i the 16 bytes of row
+    // r = (1024 d + 16 i) / kqb, physical chunk c, which holds the row's
+    // logical chunk c ^ (r & swz) (rows past O repeat row O - 1)
+#pragma unroll
+    for (int d = 0; d < ND; ++d) {
+        const int f = 1024 * d + 16 * lane;
+        const int r = f / kqb, c = (f % kqb) >> 4;
+        const int logical = c ^ (r & swz);
+        int orow = row0 + (DUAL ? (r & 15) : r);
+        orow = orow < p.O ? orow : p.O - 1;
+        const uint8_t *base = (DUAL && r >= kRows) ? p.w2 : p.w;
+        const uint8_t *src = base + (long)orow * row_bytes + (FMT == kQ8 ? k0 : k0 / 2) + logical * 16;
+        __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void *)src,
+                                         (__attribute__((address_space(3))) void *)(wl + 1024 * d),
+                                         16, 0, 0);
+    }
+    // the x loads have landed once at most the ND DMA instructions are in flight
+#pragma unroll
+    for (int j = 0; j < kMaxPass; ++j) {
+#pragma unroll
+        for (int b = 0; b < B; ++b) {
+            wait_loaded<ND>(xv[j][b][0]);
+            wait_loaded<ND>(xv[j][b][1]);
+        }
+        wait_loaded<ND>(nv[j][0]);
+        wait_loaded<ND>(nv[j][1]);
+    }
+    // ---- 3. split x into limbs in registers while the DMA is in flight (an
+    // LDS store would wait for the DMA: the compiler cannot tell the regions
+    // apart)
+    float ss[B], amax[B];
+#pragma unroll
+    for (int b = 0; b < B; ++b) {
+        ss[b] = 0.0f;
+        amax[b] = 0.0f;
+    }
+#pragma unroll
+    for (int j = 0; j < kMaxPass; ++j) {
+        if (j * 512 + lane * 8 < kq) {
+#pragma unroll
+            for (int b = 0; b < B; ++b) {
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    f32x4 v = xv[j][b][h];
+                    ss[b] += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+                    if (has_norm) {
+                        v.x *= nv[j][h].x;
+                        v.y *= nv[j][h].y;
+                        v.z *= nv[j][h].z;
+                        v.w *= nv[j][h].w;
+                    }
+                    xv[j][b][h] = v;
+                    amax[b] = fmaxf(amax[b], fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)),
+                                                   fmaxf(fabsf(v.z), fabsf(v.w))));
+                }
+            }
+        }
+    }
+    float step_inv[B], step[B];
+#pragma unroll
+    for (int b = 0; b < B; ++b) {
+        amax[b] = dpp_wave_max(amax[b]);
+        ss[b] = dpp_wave_sum(ss[b]);
+        // 2^e with amax * 2^e < 2^30 (amax = 0: any e; the limbs are 0)
+        int e2 = 0;
+        (void)frexpf(amax[b], &e2);  // amax < 2^e2
+        const int ex = amax[b] > 0.0f ? 30 - e2 : 0;
+        step_inv[b] = ldexpf(1.0f, ex);
+        step[b] = ldexpf(1.0f, -ex);
+    }
+    // the 8 elements of a pass fill bytes e .. e + 7 of each limb row (q4: in
+    // the slice order, elements 0,2,4,6 then 1,3,5,7 of the 8)
+    unsigned lw[kMaxPass][B][4][2];
+#pragma unroll
+    for (int j = 0; j < kMaxPass; ++j) {
+#pragma unroll
+        for (int b = 0; b < B; ++b) {
+            const float v8[8] = {xv[j][b][0].x, xv[j][b][0].y, xv[j][b][0].z, xv[j][b][0].w,
+                                 xv[j][b][1].x, xv[j][b][1].y, xv[j][b][1].z, xv[j][b][1].w};
+#pragma unroll
+            for (int L = 0; L < 4; ++L) lw[j][b][L][0] = lw[j][b][L][1] = 0u;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const int q = (int)rintf(v8[i] * step_inv[b]);
+                // balanced base-256 digits: q = 2^24 L0 + 2^16 L1 + 2^8 L2 + L3
+                const int l3 = (int)(signed char)(q & 255);
+                int r = (q - l3) >> 8;
+                const int l2 = (int)(signed char)(r & 255);
+                r = (r - l2) >> 8;
+                const int l1 = (int)(signed char)(r & 255);
+                const int l0 = (r - l1) >> 8;
+                const int pos = slice_pos<FMT>(i);  // 0..7 within the 8 bytes
+                const int wd = pos >> 2, sh = 8 * (pos & 3);
+                lw[j][b][0][wd] |= (unsigned)(l0 & 255) << sh;
+                lw[j][b][1][wd] |= (unsigned)(l1 & 255) << sh;
+                lw[j][b][2][wd] |= (unsigned)(l2 & 255) << sh;
+                lw[j][b][3][wd] |= (unsigned)(l3 & 255) << sh;
+            }
+        }
+    }
+    // this wave's DMA has landed; no LDS access may be scheduled above the
+    // wait (the compiler would wait for the DMA at the first one instead)
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_waitcnt(0);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int j = 0; j < kMaxPass; ++j) {
+        const int e = j * 512 + lane * 8;
+        if (e < kq) {
+#pragma unroll
+            for (int b = 0; b < B; ++b)
+#pragma unroll
+                for (int L = 0; L < 4; ++L)
+                    *reinterpret_cast<uint2 *>(xl + (L * B + b) * xrow + e) =
+                        uint2{lw[j][b][L][0], lw[j][b][L][1]};
+        }
+    }
+    // (a wave reads only its own LDS region: its LDS stores complete in order
+    // before its reads below)
+
+    // ---- 4. MFMA over the 64-k steps: A row m = 4 L + b (lane m = l % 16
+    // supplies it), B column n = weight row l % 16; lane group g = l / 16
+    // supplies k bytes 16 g .. 16 g + 15 of the step
+    const int m = lane & 15, g = lane >> 4;
+    const int limb = m >> 2, tb = m & 3;
+    const bool a_ok = tb < B;
+    const unsigned char *arow = xl + (limb * B + (a_ok ? tb : 0)) * xrow;
+    const int n = lane & 15;
+    const unsigned char *wrow = wl + n * kqb;
+    const unsigned char *wrow2 = wl + (kRows + n) * kqb;
+    i32x4 acc = {0, 0, 0, 0}, acc2 = {0, 0, 0, 0}, acc1 = {0, 0, 0, 0};
+    constexpr int nsteps = kq / 64;
+    const i32x4 ones = {0x01010101, 0x01010101, 0x01010101, 0x01010101};
+    for (int s = 0; s < nsteps; ++s) {
+        const u32x4 av = *reinterpret_cast<const u32x4 *>(arow + 64 * s + 16 * g);
+        const i32x4 A = a_ok ? i32x4{(int)av.x, (int)av.y, (int)av.z, (int)av.w}
+                             : i32x4{0, 0, 0, 0};
+        i32x4 Bw, Bu;
+        if constexpr (FMT == kQ8) {
+            const int lc = 4 * s + g;  // logical chunk
+            const u32x4 w = *reinterpret_cast<const u32x4 *>(wrow + 16 * (lc ^ (n & swz)));
+            Bw = i32x4{(int)w.x, (int)w.y, (int)w.z, (int)w.w};
+            if constexpr (DUAL) {
+                const u32x4 u = *reinterpret_cast<const u32x4 *>(wrow2 + 16 * (lc ^ (n & swz)));
+                Bu = i32x4{(int)u.x, (int)u.y, (int)u.z, (int)u.w};
+            }
+        } else {
+            const int lc = 2 * s + (g >> 1);  // logical chunk; 8-byte half g & 1
+            const uint2 w = *reinterpret_cast<const uint2 *>(wrow + 16 * (lc ^ (n & swz)) + 8 * (g & 1));
+            Bw = i32x4{(int)(w.x & 0x0F0F0F0Fu), (int)((w.x >> 4) & 0x0F0F0F0Fu),
+                       (int)(w.y & 0x0F0F0F0Fu), (int)((w.y >> 4) & 0x0F0F0F0Fu)};
+            if constexpr (DUAL) {
+                const uint2 u = *reinterpret_cast<const uint2 *>(wrow2 + 16 * (lc ^ (n & swz)) + 8 * (g & 1));
+                Bu = i32x4{(int)(u.x & 0x0F0F0F0Fu), (int)((u.x >> 4) & 0x0F0F0F0Fu),
+                           (int)(u.y & 0x0F0F0F0Fu), (int)((u.y >> 4) & 0x0F0F0F0Fu)};
+            }
+            acc1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A, ones, acc1, 0, 0, 0);
+        }
+        acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(A, Bw, acc, 0, 0, 0);
+        if constexpr (DUAL) acc2 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A, Bu, acc2, 0, 0, 0);
+    }
+    // ---- 5. lane (g, n) holds limb g of token rows b = 0..3 (registers) for
+    // weight row n: combine the limbs across the lane groups, scale
+    const float limb_w = g == 0 ? 16777216.0f : g == 1 ? 65536.0f : g == 2 ? 256.0f : 1.0f;
+#pragma unroll
+    for (int b = 0; b < B; ++b) {
+        int c = acc[b], c2 = DUAL ? acc2[b] : 0;
+        if constexpr (FMT == kQ4) {
+            c -= 8 * acc1[b];
+            if (DUAL) c2 -= 8 * acc1[b];
+        }
+        float v = (float)c * limb_w, v2 = (float)c2 * limb_w;
+        v += __shfl_xor(v, 16, 64);
+        v += __shfl_xor(v, 32, 64);
+        if (DUAL) {
+            v2 += __shfl_xor(v2, 16, 64);
+            v2 += __shfl_xor(v2, 32, 64);
+        }
+        if (g == 0) {
+            red[wave][0][b][n] = v * step[b];
+            if (DUAL) red[wave][1][b][n] = v2 * step[b];
+        }
+        if (lane == 0) red_ss[wave][b] = ss[b];
+    }
+    __syncthreads();
+    // ---- 6. the four waves' shares (in wave order) and the epilogue
+    if (wave != 0 || g >= B) return;
+    const int b = g;  // lanes 16 b + n, b < B
+    const int row = row0 + n;
+    if (row >= p.O) return;
+    float inv_rms = 1.0f;
+    if (p.norm_w) {
+        const float tot = (red_ss[0][b] + red_ss[1][b]) + (red_ss[2][b] + red_ss[3][b]);
+        inv_rms = 1.0f / sqrtf(tot / (float)Sh::kI + p.eps);
+    }
+    const float sum = ((red[0][0][b][n] + red[1][0][b][n]) + (red[2][0][b][n] + red[3][0][b][n])) * inv_rms;
+    float *yb = p.y + (long)b * p.y_stride;
+    if (DUAL) {
+        const float sum2 = ((red[0][1][b][n] + red[1][1][b][n]) + (red[2][1][b][n] + red[3][1][b][n])) * inv_rms;
+        yb[row] = silu(sum * p.s[row]) * (sum2 * p.s2[row]);
+        return;
+    }
+    float out = sum * p.s[row];
+    if (p.epilogue == kEpiResidual) out = p.resid[(long)b * p.resid_stride + row] + out;
+    yb[row] = out;
+}
+
+template <int FMT, int B, bool DUAL, int ND>
+bool launch_one(const MfmaGemvArgs &a, hipStream_t stream) {
+    using Sh = MgShape<FMT, B, DUAL, ND>;
+    // shapes whose x passes exceed the register budget are not instantiated
+    // (the dynamic LDS plus the static reduction arrays within the 160 KB)
+    if constexpr (Sh::kPass > (B == 1 ? 6 : B == 2 ? 3 : 2) || 4 * Sh::kWaveLds > 150 * 1024) {
+        return false;
+    } else {
+    if (Sh::kI != a.p.I) return false;
+    constexpr int lds = 4 * Sh::kWaveLds;
+    static const bool attr = [] {
+        if (lds <= 64 * 1024) return true;
+        if (hipFuncSetAttribute(reinterpret_cast<const void *>(&gemv_mfma_kernel<FMT, B, DUAL, ND>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, lds) == hipSuccess)
+            return true;
+        (void)hipGetLastError();  // not sticky: the caller falls back
+        return false;
+    }();
+    if (!attr) return false;
+    hipLaunchKernelGGL((gemv_mfma_kernel<FMT, B, DUAL, ND>), dim3((a.p.O + kRows - 1) / kRows),
+                       dim3(256), lds, stream, a);
+    return true;
+    }
+}
+
+// DMA counts of the Moonlight shapes: 16 or 32 rows x (I / 4) weight bytes
+// per wave, I = 2048 or 11264
+template <int FMT, int B, bool DUAL>
+bool launch_nd(const MfmaGemvArgs &a, hipStream_t stream) {
+    switch (a.ndma) {
+    case 4: return launch_one<FMT, B, DUAL, 4>(a, stream);
+    case 8: return launch_one<FMT, B, DUAL, 8>(a, stream);
+    case 16: return launch_one<FMT, B, DUAL, 16>(a, stream);
+    case 22: return launch_one<FMT, B, DUAL, 22>(a, stream);
+    case 44: return launch_one<FMT, B, DUAL, 44>(a, stream);
+    default: return false;
+    }
+}
+
+template <int FMT, bool DUAL>
+bool launch_b(const MfmaGemvArgs &a, hipStream_t stream) {
+    switch (a.p.rows) {
+    case 1: return launch_nd<FMT, 1, DUAL>(a, stream);
+    case 2: return launch_nd<FMT, 2, DUAL>(a, stream);
+    case 4: return launch_nd<FMT, 4, DUAL>(a, stream);
+    default: return false;
+    }
+}
+
+}  // namespace
+
+// The matrix-core GEMV for the shapes it covers (q8 / q4, 1, 2 or 4 token
+// rows, I a multiple of 256 (q8) or 512 (q4), aligned operands, no pre-split
+// x); returns false, launching nothing, otherwise.  Measured on MI355X
+// against the vector kernel (gemv_impl.h), graph replays: q4 11264 x 2048
+// 5.27 against 5.95 us, q8 3648 x 2048 4.16 against 4.72 us, q8 11264 x 2048
+// at 4 rows 9.9 against 12.7 us; wide-k matrices with few rows (2048 x
+// 11264: 128 workgroups) stay on the vector kernel.
+bool gemv_mfma(const GemvParams &p, hipStream_t stream) {
+    if ((p.fmt != kQ8 && p.fmt != kQ4) || p.rows < 1 || p.rows > 4 || p.rows == 3 || p.limbs)
+        return false;
+    if (p.O < 4096 && p.I > 4096) return false;
+    const bool dual = p.epilogue == kEpiSiluDual;
+    const int max_pass = p.rows == 1 ? 6 : p.rows == 2 ? 3 : 2;
+    if (p.I % (p.fmt == kQ8 ? 256 : 512) || p.I / 4 > max_pass * 512) return false;
+    auto al = [](const void *q) { return ((uintptr_t)q & 15u) == 0; };
+    if (!al(p.w) || (dual && !al(p.w2)) || !al(p.x) || p.x_stride % 4 ||
+        (p.norm_w && !al(p.norm_w)))
+        return false;
+    MfmaGemvArgs a;
+    a.p = p;
+    const int kqb = p.fmt == kQ8 ? p.I / 4 : p.I / 8;  // weight bytes per row and wave
+    a.ndma = (dual ? 2 * kRows : kRows) * kqb / 1024;
+    return dual ? (p.fmt == kQ8 ? launch_b<kQ8, true>(a, stream) : launch_b<kQ4, true>(a, stream))
+                : (p.fmt == kQ8 ? launch_b<kQ8, false>(a, stream) : launch_b<kQ4, false>(a, stream));
+}
+
+}  // namespace mlh
