@@ -41,7 +41,9 @@ typedef int i32x4 __attribute__((ext_vector_type(4)));
 // DMA and register loads as one out-of-order counter and would wait for the
 // whole DMA before the first use of a register loaded ahead of it; these
 // loads instead complete in issue order before the DMA (memory reads return
-// in order) and are waited for explicitly with wait_loaded<N>.
+// in order) and are waited for explicitly with wait_loaded<N>.  Nothing may
+// touch their registers before that wait; tests/test_gemv_mfma_isa.py checks
+// the compiled code for it.
 __device__ __forceinline__ f32x4 load16_untracked(const float *p) {
     f32x4 v;
     asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(v) : "v"(p) : "memory");
