@@ -21,9 +21,11 @@ struct CombineParams {
     const float *weights = nullptr;     // [rows, top_k]
     const int *list_pos = nullptr;      // [rows, top_k]
     const float *expert_out = nullptr;  // [list, hidden]
-    const float *shared_out = nullptr;  // [rows, hidden]
+    float *shared_out = nullptr;        // [rows, hidden]
+    const float *shared_out2 = nullptr; // optional second part of the shared output
     const float *resid = nullptr;       // optional [rows, hidden]
-    float *routed_copy = nullptr;       // optional [rows, hidden]
+    float *routed_copy = nullptr;       // optional [rows, hidden] (test hook: shared_out
+                                        // then holds the summed shared output)
     float *out = nullptr;               // [rows, hidden]
 };
 int moe_combine(const CombineParams &p, hipStream_t stream);

@@ -263,8 +263,12 @@ __global__ __launch_bounds__(256) void combine_kernel(CombineParams p) {
             const int pos = p.list_pos[q];
             if (pos >= 0) routed += p.weights[q] * p.expert_out[(long)pos * p.hidden + d];
         }
-        const float shared = p.shared_out[(long)r * p.hidden + d];
-        if (p.routed_copy) p.routed_copy[(long)r * p.hidden + d] = routed;
+        float shared = p.shared_out[(long)r * p.hidden + d];
+        if (p.shared_out2) shared += p.shared_out2[(long)r * p.hidden + d];
+        if (p.routed_copy) {
+            p.routed_copy[(long)r * p.hidden + d] = routed;
+            p.shared_out[(long)r * p.hidden + d] = shared;
+        }
         float out = routed + shared;
         if (p.resid) out = p.resid[(long)r * p.hidden + d] + out;
         p.out[(long)r * p.hidden + d] = out;

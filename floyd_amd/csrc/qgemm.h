@@ -36,6 +36,7 @@ struct GemmTask {
     const uint8_t *w = nullptr, *w2 = nullptr;  // [n_out][k] packed (w2: up rows, SwiGLU)
     const float *s = nullptr, *s2 = nullptr;    // per weight row scales
     int rows = 0, n_out = 0, k = 0;
+    int w_ld = 0;  // weight row length in elements (0: k); a k slice of longer rows
     // quantised activations: limb l (0 hi, 1 mid, 2 lo) of row r at
     // a + l * a_plane + r * a_stride
     const int8_t *a = nullptr;
@@ -52,7 +53,8 @@ struct GemmTask {
 struct QGemmLaunch {
     const GemmTask *tasks = nullptr;  // device table (MoE); nullptr: `single`
     const int *tile_start = nullptr;  // device [tasks + 1] tile prefix sums
-    const int *n_routed = nullptr;    // device: routed task count (shared task follows)
+    const int *n_routed = nullptr;    // device: routed task count (shared tasks follow)
+    int n_shared = 1;                 // shared-expert tasks after the routed ones
     int range = 0;                    // 0 all tasks, 1 routed only, 2 shared only
     GemmTask single;
 };
@@ -104,6 +106,9 @@ struct MoeGemmParams {
     float *expert_out = nullptr;     // [rows*top_k, hidden]
     float *shared_hidden = nullptr;  // [rows, shared_width]
     float *shared_out = nullptr;     // [rows, hidden]
+    // optional [rows, hidden]: the shared down projection runs as two k
+    // halves (shared_out + shared_out2) when its width is twice inter
+    float *shared_out2 = nullptr;
 };
 int moe_gemm(const MoeGemmParams &p, hipStream_t stream);
 

@@ -234,8 +234,8 @@ __device__ __forceinline__ bool map_tile(const QGemmLaunch &L, GemmTask &tk, int
         int n_tasks = 1;
         if (L.tasks) {
             const int nr = *L.n_routed;
-            n_tasks = nr + 1;
-            end = L.range == 1 ? L.tile_start[nr] : L.tile_start[nr + 1];
+            n_tasks = nr + L.n_shared;
+            end = L.range == 1 ? L.tile_start[nr] : L.tile_start[nr + L.n_shared];
             if (L.range == 2) begin = L.tile_start[nr];
         } else {
             end = tiles_of<DUAL, BM>(L.single.rows, L.single.n_out);
@@ -376,7 +376,8 @@ __global__ __launch_bounds__((QgShape<FMT, BM>::kThreads),
 
     // ---- per-thread global sources (fixed over k).  Rows past the task's end
     // read row m0 (A) or weight row 0 (B): their outputs are never stored.
-    const long w_row_bytes = FMT == kQ8 ? tk.k : tk.k / 2;
+    const int w_ld = tk.w_ld ? tk.w_ld : tk.k;
+    const long w_row_bytes = FMT == kQ8 ? w_ld : w_ld / 2;
     const uint8_t *const w_gate = tk.w;
     const uint8_t *const w_up = tk.w2;
     // output / weight row held by LDS B row j: SwiGLU tiles give each wave
@@ -477,7 +478,7 @@ __global__ __launch_bounds__((QgShape<FMT, BM>::kThreads),
             const uint8_t *bbase = up ? w_up : w_gate;
             const int cb = lc ^ swz(j);
             const unsigned boff =
-                (unsigned)((out < tk.n_out ? out : 0) * tk.k) + (unsigned)(k0 + cb * 16);
+                (unsigned)((out < tk.n_out ? out : 0) * w_row_bytes) + (unsigned)(k0 + cb * 16);
             __builtin_amdgcn_global_load_lds(
                 (const __attribute__((address_space(1))) void *)(bbase + boff),
                 stage + kLdsA + bb * 1024, 16, 0, 0);
@@ -744,7 +745,8 @@ __global__ __launch_bounds__(256, 2) void qgemm_stream_kernel(QGemmLaunch L) {
     }
     // weight row of LDS row j (0..63) of this wave: SwiGLU tiles give a wave
     // 32 gate rows (LDS rows 0..31) and the matching 32 up rows (32..63)
-    const long w_row_bytes = FMT == kQ8 ? tk.k : tk.k / 2;
+    const int w_ld = tk.w_ld ? tk.w_ld : tk.k;
+    const long w_row_bytes = FMT == kQ8 ? w_ld : w_ld / 2;
     auto w_row = [&](int j, int &n) -> const uint8_t * {
         const uint8_t *base = tk.w;
         if (DUAL) {
@@ -1024,6 +1026,12 @@ struct MoeScheduleParams {
     int bm;  // token rows per tile of the launches that read the tables
 };
 
+// Tasks of the shared down projection: 2 k halves when its width is twice
+// inter and a second output exists, else 1.
+__host__ __device__ inline int moe_shared_down_parts(const MoeGemmParams &p) {
+    return p.has_shared && p.shared_out2 && p.shared_width == 2 * p.inter ? 2 : 1;
+}
+
 __device__ __forceinline__ void moe_schedule_body(const MoeScheduleParams &sp) {
     const MoeGemmParams &p = sp.p;
     const int bm = sp.bm;
@@ -1071,9 +1079,10 @@ __device__ __forceinline__ void moe_schedule_body(const MoeScheduleParams &sp) {
         t1[u] = b;
         tiles[1][u] = tiles_rt(false, cnt, p.hidden);
     }
+    const int nsd = moe_shared_down_parts(p);  // shared down tasks (k parts)
     if (threadIdx.x == 0) {
         tiles[0][nr] = 0;
-        tiles[1][nr] = 0;
+        for (int i = 0; i < nsd; ++i) tiles[1][nr + i] = 0;
         if (p.has_shared) {
             GemmTask a;
             a.w = p.shared_gate;
@@ -1091,32 +1100,41 @@ __device__ __forceinline__ void moe_schedule_body(const MoeScheduleParams &sp) {
             a.y_stride = p.shared_width;
             t0[nr] = a;
             tiles[0][nr] = tiles_rt(true, p.rows, p.shared_width);
-            GemmTask b;
-            b.w = p.shared_down;
-            b.s = p.shared_down_s;
-            b.rows = p.rows;
-            b.n_out = p.hidden;
-            b.k = p.shared_width;
-            b.a = p.sq;
-            b.a_plane = p.sq_plane;
-            b.a_scale = p.sq_scale;
-            b.a_stride = p.shared_width;
-            b.y = p.shared_out;
-            b.y_stride = p.hidden;
-            t1[nr] = b;
-            tiles[1][nr] = tiles_rt(false, p.rows, p.hidden);
+            // the shared down projection as nsd k parts of `inter` columns
+            // (its tiles then last as long as the routed ones'), part i into
+            // shared_out (i = 0) or shared_out2 (i = 1)
+            const int kpart = p.shared_width / nsd;
+            for (int i = 0; i < nsd; ++i) {
+                GemmTask b;
+                const long col = (long)i * kpart;
+                b.w = p.shared_down + (p.shared_fmt == kQ8 ? col : col / 2);
+                b.s = p.shared_down_s;
+                b.rows = p.rows;
+                b.n_out = p.hidden;
+                b.k = kpart;
+                b.w_ld = p.shared_width;
+                b.a = p.sq + col;
+                b.a_plane = p.sq_plane;
+                b.a_scale = p.sq_scale;
+                b.a_stride = p.shared_width;
+                b.y = i == 0 ? p.shared_out : p.shared_out2;
+                b.y_stride = p.hidden;
+                t1[nr + i] = b;
+                tiles[1][nr + i] = tiles_rt(false, p.rows, p.hidden);
+            }
         }
     }
     __syncthreads();
     if (threadIdx.x < 2) {
         const int s = threadIdx.x;
+        const int extra = s == 0 ? 1 : nsd;
         int *start = p.tile_start + s * (kQgMaxTasks + 1);
         int acc = 0;
-        for (int u = 0; u <= nr; ++u) {
+        for (int u = 0; u < nr + extra; ++u) {
             start[u] = acc;
             acc += tiles[s][u];
         }
-        start[nr + 1] = acc;
+        start[nr + extra] = acc;
     }
 }
 
@@ -1146,7 +1164,7 @@ __global__ __launch_bounds__(256) void moe_prep_kernel(QuantSeg a, MoeSchedulePa
 
 
 int moe_gemm(const MoeGemmParams &p, hipStream_t stream) {
-    if (p.rows <= 0 || p.experts <= 0 || p.experts + 1 > kQgMaxTasks || p.top_k <= 0 ||
+    if (p.rows <= 0 || p.experts <= 0 || p.experts + 2 > kQgMaxTasks || p.top_k <= 0 ||
         !qgemm_shape_ok(p.expert_fmt, p.hidden) || !qgemm_shape_ok(p.expert_fmt, p.inter) ||
         (p.has_shared && (!qgemm_shape_ok(p.shared_fmt, p.hidden) ||
                           !qgemm_shape_ok(p.shared_fmt, p.shared_width))))
@@ -1201,11 +1219,13 @@ int moe_gemm(const MoeGemmParams &p, hipStream_t stream) {
         L.tasks = p.tasks + stage * kQgMaxTasks;
         L.tile_start = p.tile_start + stage * (kQgMaxTasks + 1);
         L.n_routed = p.n_unique;
+        L.n_shared = dual ? 1 : moe_shared_down_parts(p);
         // upper bounds of the tile counts: sum_e ceil(n_e / BM) <= entries / BM + tasks
         const int routed_mt = entries / bm + max_tasks;
         const int routed_nt = host_tiles(dual, 1, dual ? p.inter : p.hidden, bm);
         const int shared_t =
-            p.has_shared ? host_tiles(dual, p.rows, dual ? p.shared_width : p.hidden, bm) : 0;
+            p.has_shared ? L.n_shared * host_tiles(dual, p.rows, dual ? p.shared_width : p.hidden, bm)
+                         : 0;
         if (same) {
             L.range = 0;
             st = launch_qgemm_fmt(p.expert_fmt, dual, kind, L, routed_mt * routed_nt + shared_t,

@@ -125,6 +125,7 @@ struct MoonlightSession {
     long limb_x_stride = 0, limb_h_stride = 0, limb_sh_stride = 0;
     float *expert_hidden = nullptr, *expert_out = nullptr;
     float *shared_hidden = nullptr, *shared_out = nullptr, *dense_hidden = nullptr;
+    float *shared_out2 = nullptr;  // second k half of the GEMM path's shared down
     float *moe_routed = nullptr;  // routed part of moonlight_test_moe
     // MFMA path for batches of >= kMoeGemmMinRows token rows (prefill)
     // quantised activations: three limb planes [3][max_batch][aq_width]
@@ -1166,6 +1167,9 @@ int experts(MoonlightSession *s, int layer, const float *x, int rows, const floa
     f.shared_hidden = s->shared_hidden;
     f.shared_out = s->shared_out;
     const bool gemm = moe_uses_gemm(s, layer, rows);
+    // the GEMM path runs a shared down projection twice inter wide as two k
+    // halves into shared_out and shared_out2 (moe_shared_down_parts)
+    const bool split_shared = gemm && f.shared_width == 2 * f.inter;
     if (gemm) {
         MoeGemmParams g;
         g.rows = f.rows;
@@ -1210,6 +1214,7 @@ int experts(MoonlightSession *s, int layer, const float *x, int rows, const floa
         g.expert_out = f.expert_out;
         g.shared_hidden = f.shared_hidden;
         g.shared_out = f.shared_out;
+        g.shared_out2 = split_shared ? s->shared_out2 : nullptr;
         if (int e = moe_gemm(g, stream_of(s))) return e;
     } else {
         const bool fused_down = down_combine_ok(f);
@@ -1232,6 +1237,7 @@ int experts(MoonlightSession *s, int layer, const float *x, int rows, const floa
     cb.list_pos = s->list_pos;
     cb.expert_out = s->expert_out;
     cb.shared_out = s->shared_out;
+    cb.shared_out2 = split_shared ? s->shared_out2 : nullptr;
     cb.resid = resid;
     cb.routed_copy = routed_copy;
     cb.out = out;
@@ -1515,6 +1521,7 @@ extern "C" int moonlight_session_create(MoonlightSession **out, MoonlightModel *
         session_alloc(s, &s->expert_out, mb * K * H, error, error_size) &&
         session_alloc(s, &s->shared_hidden, mb * (sw ? sw : 1), error, error_size) &&
         session_alloc(s, &s->shared_out, mb * H, error, error_size) &&
+        session_alloc(s, &s->shared_out2, mb * H, error, error_size) &&
         session_alloc(s, &s->moe_routed, mb * H, error, error_size) &&
         session_alloc(s, &s->dense_hidden,
                       mb * (size_t)(c.dense_intermediate_size > 0 ? c.dense_intermediate_size : 1),
