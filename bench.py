@@ -290,13 +290,14 @@ def full_prefill(model, extra, rows=2048):
     sess.close()
 
 
-def moe_only():
-    """Config 2 only: the MoE layer at T = 1, 8, 64 (profiler runs)."""
+def moe_only(sizes=None):
+    """Config 2 only: the MoE layer at T = 1, 8, 64, or at the row counts in
+    `sizes` (profiler runs)."""
     from floyd_amd import session as S
     model = S.Model.synthetic()
     sess = S.Session(model, 128, 64)
     out = {}
-    for rows in (1, 8, 64):
+    for rows in sizes or (1, 8, 64):
         us, uniq = sess.time_moe(1, rows, seed=rows, warmup=5, iters=20)
         out[f"T{rows}"] = {"us": round(us, 2), "unique_experts": uniq}
         print(f"[bench] MoE layer T={rows}: {us:.1f} us, U={uniq}", file=sys.stderr, flush=True)
@@ -305,13 +306,14 @@ def moe_only():
     print(json.dumps(out), flush=True)
 
 
-def attn_only():
+def attn_only(sizes=None):
     """One decode attention block ([q | kv_a] GEMV, MLA chain, o_proj) at
-    ctx 4096 and 16384, stream launches (profiler runs and quick checks)."""
+    ctx 4096 and 16384, or at the contexts in `sizes`, stream launches
+    (profiler runs and quick checks)."""
     from floyd_amd import session as S
     model = S.Model.synthetic()
     out = {}
-    for ctx in (4096, 16384):
+    for ctx in sizes or (4096, 16384):
         sess = S.Session(model, ctx + 8, 1)
         sess.fill_kv(ctx, seed=ctx, layer=1)
         us = sess.time_attention(1, 1, ctx, warmup=5, iters=50)
@@ -501,6 +503,9 @@ def main():
                         help="only config 3 (MoE prefill q8 / q4) and the 2048-token prefill")
     parser.add_argument("--attn-only", action="store_true",
                         help="only the decode attention block at ctx 4096 and 16384")
+    parser.add_argument("--sizes", type=str, default="",
+                        help="comma-separated MoE row counts (--moe-only) or contexts "
+                             "(--attn-only) in place of the defaults")
     parser.add_argument("--decode-only", type=int, default=0, metavar="CTX",
                         help="only greedy decode steps of the synthetic model at context "
                              "CTX, printed per token (profiler runs)")
@@ -523,11 +528,12 @@ def main():
     if args.prefill_only:
         prefill_only()
         return
+    sizes = [int(v) for v in args.sizes.split(",") if v]
     if args.moe_only:
-        moe_only()
+        moe_only(sizes)
         return
     if args.attn_only:
-        attn_only()
+        attn_only(sizes)
         return
 
     # headline: benchmark config 1, q4 [11264 x 2048], batch 1

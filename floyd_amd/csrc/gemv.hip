@@ -300,8 +300,19 @@ int gemv_rows_per_block(const GemvPlan &plan, bool dual) {
     return out * (64 / plan.lpr) * (plan.ks == 1 ? plan.waves : 1);
 }
 
-// Template name of the kernel gemv() launches for this shape (vector path).
+bool gemv_mfma(const GemvParams &p, hipStream_t stream, std::string *name = nullptr);  // gemv_mfma.hip
+
+// Template name of the kernel gemv() launches for this shape (aligned
+// operands, no pre-split x).
 std::string gemv_kernel_name(int fmt, int O, int I, int rows, bool dual) {
+    GemvParams q;
+    q.fmt = fmt;
+    q.O = O;
+    q.I = I;
+    q.rows = rows;
+    q.epilogue = dual ? kEpiSiluDual : q.epilogue;
+    std::string mfma;
+    if (gemv_mfma(q, nullptr, &mfma)) return mfma;
     const GemvPlan pl = plan_gemv(fmt, O, I, rows < kMaxGemvRows ? rows : kMaxGemvRows, dual);
     char buf[96];
     snprintf(buf, sizeof(buf), "mlh::gemv_kernel<0, %d, %d, %d, %d, %d, %d, %d>", fmt, pl.b,
@@ -310,8 +321,6 @@ std::string gemv_kernel_name(int fmt, int O, int I, int rows, bool dual) {
 }
 
 static bool aligned16(const void *ptr) { return ((uintptr_t)ptr & 15u) == 0; }
-
-bool gemv_mfma(const GemvParams &p, hipStream_t stream);  // gemv_mfma.hip
 
 int gemv(const GemvParams &p_in, hipStream_t stream) {
     if (!p_in.w || !p_in.x || !p_in.y || p_in.O <= 0 || p_in.I <= 0 || p_in.rows <= 0)

@@ -360,8 +360,9 @@ __global__ __launch_bounds__(256) void gemv_mfma_kernel(MfmaGemvArgs a) {
     yb[row] = out;
 }
 
+// With `name` set nothing is launched: the kernel's template name is stored.
 template <int FMT, int B, bool DUAL, int ND>
-bool launch_one(const MfmaGemvArgs &a, hipStream_t stream) {
+bool launch_one(const MfmaGemvArgs &a, hipStream_t stream, std::string *name) {
     using Sh = MgShape<FMT, B, DUAL, ND>;
     // shapes whose x passes exceed the register budget are not instantiated
     // (the dynamic LDS plus the static reduction arrays within the 160 KB)
@@ -369,6 +370,13 @@ bool launch_one(const MfmaGemvArgs &a, hipStream_t stream) {
         return false;
     } else {
     if (Sh::kI != a.p.I) return false;
+    if (name) {
+        char buf[96];
+        snprintf(buf, sizeof(buf), "mlh::(anonymous namespace)::gemv_mfma_kernel<%d, %d, %s, %d>",
+                 FMT, B, DUAL ? "true" : "false", ND);
+        *name = buf;
+        return true;
+    }
     constexpr int lds = 4 * Sh::kWaveLds;
     static const bool attr = [] {
         if (lds <= 64 * 1024) return true;
@@ -388,23 +396,23 @@ bool launch_one(const MfmaGemvArgs &a, hipStream_t stream) {
 // DMA counts of the Moonlight shapes: 16 or 32 rows x (I / 4) weight bytes
 // per wave, I = 2048 or 11264
 template <int FMT, int B, bool DUAL>
-bool launch_nd(const MfmaGemvArgs &a, hipStream_t stream) {
+bool launch_nd(const MfmaGemvArgs &a, hipStream_t stream, std::string *name) {
     switch (a.ndma) {
-    case 4: return launch_one<FMT, B, DUAL, 4>(a, stream);
-    case 8: return launch_one<FMT, B, DUAL, 8>(a, stream);
-    case 16: return launch_one<FMT, B, DUAL, 16>(a, stream);
-    case 22: return launch_one<FMT, B, DUAL, 22>(a, stream);
-    case 44: return launch_one<FMT, B, DUAL, 44>(a, stream);
+    case 4: return launch_one<FMT, B, DUAL, 4>(a, stream, name);
+    case 8: return launch_one<FMT, B, DUAL, 8>(a, stream, name);
+    case 16: return launch_one<FMT, B, DUAL, 16>(a, stream, name);
+    case 22: return launch_one<FMT, B, DUAL, 22>(a, stream, name);
+    case 44: return launch_one<FMT, B, DUAL, 44>(a, stream, name);
     default: return false;
     }
 }
 
 template <int FMT, bool DUAL>
-bool launch_b(const MfmaGemvArgs &a, hipStream_t stream) {
+bool launch_b(const MfmaGemvArgs &a, hipStream_t stream, std::string *name) {
     switch (a.p.rows) {
-    case 1: return launch_nd<FMT, 1, DUAL>(a, stream);
-    case 2: return launch_nd<FMT, 2, DUAL>(a, stream);
-    case 4: return launch_nd<FMT, 4, DUAL>(a, stream);
+    case 1: return launch_nd<FMT, 1, DUAL>(a, stream, name);
+    case 2: return launch_nd<FMT, 2, DUAL>(a, stream, name);
+    case 4: return launch_nd<FMT, 4, DUAL>(a, stream, name);
     default: return false;
     }
 }
@@ -417,8 +425,10 @@ bool launch_b(const MfmaGemvArgs &a, hipStream_t stream) {
 // against the vector kernel (gemv_impl.h), graph replays: q4 11264 x 2048
 // 5.27 against 5.95 us, q8 3648 x 2048 4.16 against 4.72 us, q8 11264 x 2048
 // at 4 rows 9.9 against 12.7 us; wide-k matrices with few rows (2048 x
-// 11264: 128 workgroups) stay on the vector kernel.
-bool gemv_mfma(const GemvParams &p, hipStream_t stream) {
+// 11264: 128 workgroups) stay on the vector kernel.  With `name` set it
+// launches nothing and stores the template name of the kernel it would
+// launch (operand alignment not checked).
+bool gemv_mfma(const GemvParams &p, hipStream_t stream, std::string *name) {
     if ((p.fmt != kQ8 && p.fmt != kQ4) || p.rows < 1 || p.rows > 4 || p.rows == 3 || p.limbs)
         return false;
     if (p.O < 4096 && p.I > 4096) return false;
@@ -426,15 +436,17 @@ bool gemv_mfma(const GemvParams &p, hipStream_t stream) {
     const int max_pass = p.rows == 1 ? 6 : p.rows == 2 ? 3 : 2;
     if (p.I % (p.fmt == kQ8 ? 256 : 512) || p.I / 4 > max_pass * 512) return false;
     auto al = [](const void *q) { return ((uintptr_t)q & 15u) == 0; };
-    if (!al(p.w) || (dual && !al(p.w2)) || !al(p.x) || p.x_stride % 4 ||
-        (p.norm_w && !al(p.norm_w)))
+    if (!name && (!al(p.w) || (dual && !al(p.w2)) || !al(p.x) || p.x_stride % 4 ||
+                  (p.norm_w && !al(p.norm_w))))
         return false;
     MfmaGemvArgs a;
     a.p = p;
     const int kqb = p.fmt == kQ8 ? p.I / 4 : p.I / 8;  // weight bytes per row and wave
     a.ndma = (dual ? 2 * kRows : kRows) * kqb / 1024;
-    return dual ? (p.fmt == kQ8 ? launch_b<kQ8, true>(a, stream) : launch_b<kQ4, true>(a, stream))
-                : (p.fmt == kQ8 ? launch_b<kQ8, false>(a, stream) : launch_b<kQ4, false>(a, stream));
+    return dual ? (p.fmt == kQ8 ? launch_b<kQ8, true>(a, stream, name)
+                                : launch_b<kQ4, true>(a, stream, name))
+                : (p.fmt == kQ8 ? launch_b<kQ8, false>(a, stream, name)
+                                : launch_b<kQ4, false>(a, stream, name));
 }
 
 }  // namespace mlh

@@ -6,7 +6,8 @@
 namespace mlh {
 
 constexpr int kMlaMaxHeads = 16;        // Moonlight: 16 heads
-constexpr int kMlaKeysPerSplit = 32;    // keys per workgroup in mla_attend
+constexpr int kMlaTileKeys = 16;        // keys per mla_attend tile
+constexpr int kMlaAttendGroups = 256;   // mla_attend workgroups per launch group (all rows)
 constexpr int kMlaMaxLatent = 512;      // kv_lora_rank limit (moonlight_metal.m:1041)
 constexpr int kMlaDecodeRows = 16;      // token rows per decode-path launch group
 constexpr int kMlaValueDims = 32;       // latent dims per merge + value workgroup
@@ -26,10 +27,10 @@ struct MlaParams {
     int rows = 0, position = 0, heads = 0;
     // When set, the kernels read the position from this device int instead
     // of `position` (a captured decode graph replays at every position), and
-    // the attend grid is grid_splits key splits (splits past the causal end
-    // exit at once).
+    // the attend grid is grid_splits workgroups per row whatever the position.
     const int *position_dev = nullptr;
     int grid_splits = 0;
+    int splits = 0;  // attend workgroups per row of a launch group (set by mla_attention_core)
     int nope = 0, rope = 0, vdim = 0, latent = 0;
     float eps = 1e-5f, scale = 1.0f;
     const float *query = nullptr;       // [rows][heads * (nope + rope)] (q_proj output)
@@ -44,9 +45,9 @@ struct MlaParams {
     float *query_rope = nullptr;        // scratch [rows, heads, rope]
     float *query_absorbed = nullptr;    // scratch [rows, heads, latent]
     int max_splits = 0;                 // split capacity of the partial buffers
-    float *part_max = nullptr;          // [rows, max_splits, kMlaMaxHeads]
-    float *part_sum = nullptr;          // [rows, max_splits, kMlaMaxHeads]
-    float *part_lc = nullptr;           // [rows, max_splits, kMlaMaxHeads, latent]
+    float *part_max = nullptr;          // [rows, kMlaMaxHeads, max_splits]
+    float *part_sum = nullptr;          // [rows, kMlaMaxHeads, max_splits]
+    float *part_lc = nullptr;           // [rows, kMlaMaxHeads, latent / kMlaValueDims, max_splits, kMlaValueDims]
     float *latent_context = nullptr;    // scratch [rows, heads, latent] merged lc
     float *context = nullptr;           // out [rows, heads, vdim]
     // decode path (at most kMlaDecodeRows rows per launch group):

@@ -14,10 +14,10 @@
 //               RoPE into the caches, RoPE of the query's rope part, and the
 //               absorbed query qa_h = W_UK_h^T q_nope_h, each wave reading
 //               128-column runs of 4 kv_b rows per instruction.
-//   mla_attend  (key split of kMlaKeysPerSplit keys, row): every latent row
-//               read once scores ALL heads (the reference re-reads the cache
-//               per head); per split a local max / exp-sum and the partial
-//               latent context of every head, from the split's rows in LDS.
+//   mla_attend  (split, row): a run of kMlaTileKeys-key tiles per workgroup;
+//               every latent row read once scores ALL heads (the reference
+//               re-reads the cache per head); per split a running max /
+//               exp-sum and the partial latent context of every head.
 //   mla_merge_value (row, head, kMlaValueDims latent dims): one-pass
 //               log-sum-exp merge of the splits into that slice of lc_h,
 //               its share of ctx_h = W_UV_h lc_h, and the sum of the shares
@@ -191,58 +191,128 @@ __global__ __launch_bounds__(256) void mla_prep_kernel(MlaParams p, int chunks) 
 }
 
 
-// One split of kMlaKeysPerSplit keys (the reference's scores + softmax +
-// latent context, per split) on fp32 matrix cores (v_mfma_f32_16x16x4_f32:
-// fp32 products and sums, in another order than the reference).  Operand
-// layout (measured on gfx950): lane l supplies A[l % 16][l / 16] and
-// B[l / 16][l % 16]; result register i of lane l is D[4 (l / 16) + i][l % 16].
-// Four MFMAs consume one 16-byte operand read: in step j lane group g = l / 16
-// takes k index 4 g + j.  The splits cover the keys before the row's own
-// position; mla_merge_value adds the row's own (new) key, so a cache of
-// exactly 32 n keys takes n splits.  All 8 waves (two per SIMD, so one
-// wave's LDS latency hides under the other's MFMAs) copy key rows and
-// compute:
-//   scores  S[key][head] = [lat | rope][key] . [qa | q_rope][head] over the
-//           latent + rope dims: wave w takes the 16-dim steps w, w + 8, ...
-//           for both key tiles (query slices in registers, read once from
-//           L2); the 8 partials meet in LDS in two rounds (waves 4..7 store,
-//           waves 0..3 add theirs; sums in wave order).
-//   context LC[head][d] = sum_key P[head][key] lat[key][d]: wave w takes the
-//           16-wide d tiles w, w + 8, w + 16, w + 24.
-// Loops have compile-time trip counts and no branches (steps past the
-// latent + rope width multiply a zero query slice), so every LDS read of a
-// phase is issued ahead of its MFMAs.  LDS holds the key rows (latent +
-// rope, stride kAttnRowStride floats: 16-byte aligned, bank-spread) and P;
-// the cross-wave score partials reuse the rope columns once every wave is
-// done with them.  76.5 KB: two workgroups per CU.
+// The keys before a row's own position in tiles of kMlaTileKeys, spread over
+// `splits` workgroups per row (the reference's scores + softmax + latent
+// context, moonlight_kernels.metal:247-343, per workgroup): with at most
+// `splits` tiles workgroup b takes tile b, else tiles b * tiles / splits ..
+// (b + 1) * tiles / splits - 1, so the merge finds min(tiles, splits)
+// partials.  A workgroup keeps a running max / exp-sum per head across its
+// tiles and writes one partial (max, sum, latent context of every head).
+// fp32 matrix cores (v_mfma_f32_16x16x4_f32: fp32 products and sums, in
+// another order than the reference).  Operand layout (measured on gfx950):
+// lane l supplies A[l % 16][l / 16] and B[l / 16][l % 16]; result register i
+// of lane l is D[4 (l / 16) + i][l % 16].  Four MFMAs consume one 16-byte
+// operand read: in step j lane group g = l / 16 takes k index 4 g + j.  The
+// row's own (new) key joins in mla_merge_value.  Per tile, all 8 waves:
+//   scores  S[key][head] = [lat | rope][key] . [qa | q_rope][head]: wave w
+//           takes the 16-dim steps w, w + 8, ... (query slices in registers,
+//           read once); the 8 partials meet in LDS.
+//   softmax 16 lanes per head: tile max, running max, P = exp(S - max), the
+//           rescale of the running sum and context.
+//   context LC[head][d] += P[head][key] lat[key][d]: wave w takes the 16-wide
+//           d tiles w, w + 8, w + 16, w + 24.
+// The rows of the next two tiles are in flight in registers (coalesced
+// 16-byte loads) while a tile is in use, and go into LDS (two buffers) at
+// the top of their step: three barriers per tile.  Loops have
+// compile-time trip counts (steps past the latent + rope width multiply a
+// zero query slice), so every LDS read of a phase is issued ahead of its
+// MFMAs.
 constexpr int kAttnDims = kMlaMaxLatent + 64;       // latent + rope
-constexpr int kAttnRowStride = kAttnDims + 4;       // floats
-constexpr int kAttnPStride = kMlaKeysPerSplit + 4;  // floats, P[head][key]
+constexpr int kAttnRowStride = kAttnDims + 4;       // floats (16-byte aligned rows, banks spread)
+constexpr int kAttnPStride = kMlaTileKeys + 4;      // floats, P[head][key]
+constexpr int kAttnTileFloats = kMlaTileKeys * kAttnRowStride;
 constexpr size_t kAttnMfmaLds =
-    sizeof(float) * ((size_t)kMlaKeysPerSplit * kAttnRowStride + kMlaMaxHeads * kAttnPStride);
-static_assert(kMlaKeysPerSplit == 32, "two 16-key tiles per split");
-static_assert(4 * kMlaKeysPerSplit * kMlaMaxHeads <= kMlaKeysPerSplit * 64,
-              "score partials fit the rope columns");
+    sizeof(float) * (2 * (size_t)kAttnTileFloats + 8 * kMlaTileKeys * kMlaMaxHeads +
+                     kMlaMaxHeads * kAttnPStride);
+static_assert(kMlaTileKeys == 16, "one 16-key MFMA tile per key tile");
+static_assert(kMlaMaxLatent / 4 * kMlaTileKeys <= 4 * 512 && 64 / 4 * kMlaTileKeys <= 512,
+              "a tile is at most 4 latent and 1 rope 16-byte loads per thread");
 
 typedef float f32x4v __attribute__((ext_vector_type(4)));
 
+// Sum / max over the 16 lanes of a DPP row, every lane receiving it (pairs
+// exchanged symmetrically, so all lanes add in the same order).
+#define MLH_DPP(v, ctrl) \
+    __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), ctrl, 0xF, 0xF, false))
+__device__ __forceinline__ float row16_sum(float v) {
+    v += MLH_DPP(v, 0xB1);   // quad_perm [1,0,3,2]
+    v += MLH_DPP(v, 0x4E);   // quad_perm [2,3,0,1]
+    v += MLH_DPP(v, 0x141);  // row_half_mirror
+    return v + MLH_DPP(v, 0x140);  // row_mirror
+}
+__device__ __forceinline__ float row16_max(float v) {
+    v = fmaxf(v, MLH_DPP(v, 0xB1));
+    v = fmaxf(v, MLH_DPP(v, 0x4E));
+    v = fmaxf(v, MLH_DPP(v, 0x141));
+    return fmaxf(v, MLH_DPP(v, 0x140));
+}
+#undef MLH_DPP
+
 __global__ __launch_bounds__(512) void mla_attend_mfma_kernel(MlaParams p) {
     constexpr int H = kMlaMaxHeads;
-    constexpr int KS = kMlaKeysPerSplit;
+    constexpr int TK = kMlaTileKeys;
     constexpr int NS = (kAttnDims / 16 + 7) / 8;  // 16-dim score steps per wave
-    constexpr int NT = kMlaMaxLatent / 16 / 8;  // 16-wide context tiles per wave
+    constexpr int NT = kMlaMaxLatent / 16 / 8;    // 16-wide context tiles per wave
+    constexpr int DL = kMlaValueDims;
     extern __shared__ __attribute__((aligned(16))) float attn_lds[];
-    float *lat_s = attn_lds;                   // [KS][stride]
-    float *p_s = lat_s + KS * kAttnRowStride;  // [H][KS + 4]
+    float *const buf0 = attn_lds;
+    float *const buf1 = attn_lds + kAttnTileFloats;
+    float *const sp = attn_lds + 2 * kAttnTileFloats;  // score partials [wave][key][head]
+    float *const p_s = sp + 8 * TK * H;                // P [head][key]
     __shared__ float smax[H], ssum[H];
-    const int split = blockIdx.x;
-    const int r = blockIdx.y;
+    __shared__ __attribute__((aligned(16))) float sscale[H];
+    const int b = blockIdx.x, r = blockIdx.y;
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const int g = lane >> 4, m16 = lane & 15;
     const int D = p.latent, R = p.rope;
     const int KD = D + R;  // a multiple of 16 (launch condition)
     // the position first (memory reads complete in issue order)
     const int keys = mla_position(p) + r;  // the keys before row r's own
+    const int tiles = (keys + TK - 1) / TK;
+    const int G = p.splits;
+    int t_begin = b, t_end = b < tiles ? b + 1 : b;
+    if (tiles > G) {  // 32-bit products: b * tiles < 2^31 for any cache that fits in HBM
+        t_begin = (int)((unsigned)(b * tiles) / (unsigned)G);
+        t_end = (int)((unsigned)((b + 1) * tiles) / (unsigned)G);
+    }
+    if (t_begin >= t_end) return;  // no partial: the merge reads min(tiles, splits)
+    if (t < H) {
+        smax[t] = -INFINITY;
+        ssum[t] = 0.0f;
+    }
+    // ---- tile rows through registers: 16-byte piece f = t + 512 u of the
+    // latent part (key f / (D / 4)), piece t of the rope part (key t / (R /
+    // 4)); pieces past the tile repeat a piece of the tile (the same value
+    // stored twice), so loads and stores need no branches; keys past the
+    // causal end load the last valid row (finite values, zero probability)
+    const int D4 = D >> 2, R4 = R >> 2;
+    int lkey[4], lcol[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        const int f = (t + 512 * u) % (TK * D4);
+        lkey[u] = f / D4;
+        lcol[u] = 4 * (f % D4);
+    }
+    const int rkey = (t % (TK * R4)) / R4, rcol = 4 * (t % R4);
+    f32x4 la[4], ra, lb[4], rb;
+    // a tile past the run loads the cache's first 16 bytes into every lane
+    // (offsets masked, no branches: every path has the same loads in flight)
+    auto load_tile = [&](int tile, f32x4 (&lr)[4], f32x4 &rr) {
+        const long live = -(long)(tile < t_end);
+        const int k0 = tile * TK, last = (keys - k0 < TK ? keys - k0 : TK) - 1;
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+            lr[u] = load_f4(p.latent_cache +
+                            (((long)(k0 + (lkey[u] < last ? lkey[u] : last)) * D + lcol[u]) & live));
+        rr = load_f4(p.rope_cache + (((long)(k0 + (rkey < last ? rkey : last)) * R + rcol) & live));
+    };
+    auto store_tile = [&](float *buf, const f32x4 (&lr)[4], const f32x4 &rr) {
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+            *reinterpret_cast<f32x4 *>(buf + lkey[u] * kAttnRowStride + lcol[u]) = lr[u];
+        *reinterpret_cast<f32x4 *>(buf + rkey * kAttnRowStride + D + rcol) = rr;
+    };
+    load_tile(t_begin, la, ra);
     // ---- this wave's query slices: dims 16 (w + 8 j) + 4 g .. + 3 of head
     // m16; absent heads read head 0 (their outputs are unused), dims past KD
     // are zero
@@ -253,161 +323,135 @@ __global__ __launch_bounds__(512) void mla_attend_mfma_kernel(MlaParams p) {
         const float *qr = p.query_rope + qh * R;
 #pragma unroll
         for (int j = 0; j < NS; ++j) {
+            // branch-free: every slice loads (dims past KD reload dim 0)
             const int d = 16 * (wave + 8 * j) + 4 * g;
-            qv[j] = d < D ? load_f4(qa + d) : d < KD ? load_f4(qr + (d - D)) : f32x4{0.f, 0.f, 0.f, 0.f};
+            const f32x4 v = load_f4(d < D ? qa + d : d < KD ? qr + (d - D) : qa);
+            const bool in = d < KD;
+            qv[j] = f32x4{in ? v.x : 0.f, in ? v.y : 0.f, in ? v.z : 0.f, in ? v.w : 0.f};
         }
     }
-    const int k0 = split * KS;
-    const int nk = keys - k0 < KS ? keys - k0 : KS;
-    const long part = ((long)r * p.max_splits + split) * H;
-    if (nk <= 0) {
-        if (t < H) {
-            p.part_max[part + t] = -INFINITY;
-            p.part_sum[part + t] = 0.0f;
-        }
-        return;
-    }
-    // ---- the split's latent + rope rows into LDS by DMA (global_load_lds:
-    // 16 bytes per lane into M0 + 16 * lane), 8 waves on rows w, w + 8, ...;
-    // keys past the causal end copy the last valid row (finite values, zero
-    // probability)
-    for (int row = wave; row < KS; row += 8) {
-        const long k = k0 + (row < nk ? row : nk - 1);
-        const float *lsrc = p.latent_cache + k * D;
-        const float *rsrc = p.rope_cache + k * R;
-        __attribute__((address_space(3))) float *dst =
-            (__attribute__((address_space(3))) float *)(lat_s + row * kAttnRowStride);
-        for (int c0 = 0; c0 < D; c0 += 256) {  // 64 lanes x 4 floats
-            if (c0 + 4 * lane < D)
-                __builtin_amdgcn_global_load_lds(
-                    (const __attribute__((address_space(1))) void *)(lsrc + c0 + 4 * lane),
-                    dst + c0, 16, 0, 0);
-        }
-        if (4 * lane < R)
-            __builtin_amdgcn_global_load_lds(
-                (const __attribute__((address_space(1))) void *)(rsrc + 4 * lane), dst + D, 16, 0,
-                0);
-    }
-    __builtin_amdgcn_s_waitcnt(0);  // this wave's transfers have landed
-    __syncthreads();
-    // ---- scores: 16-dim steps w + 8 j of both key tiles; one chain per key
-    // tile.  Steps past KD read row columns 0.. (finite) against a zero
-    // query slice.
-    f32x4v acc[KS / 16];
-#pragma unroll
-    for (int kt = 0; kt < KS / 16; ++kt) acc[kt] = f32x4v{0.f, 0.f, 0.f, 0.f};
-    {
-        f32x4 av[NS][KS / 16];
-#pragma unroll
-        for (int j = 0; j < NS; ++j) {
-            const int d0 = 16 * (wave + 8 * j);
-#pragma unroll
-            for (int kt = 0; kt < KS / 16; ++kt)
-                av[j][kt] = *reinterpret_cast<const f32x4 *>(
-                    lat_s + (16 * kt + m16) * kAttnRowStride + (d0 < KD ? d0 : 0) + 4 * g);
-        }
-#pragma unroll
-        for (int j = 0; j < NS; ++j)
-#pragma unroll
-            for (int e = 0; e < 4; ++e)
-#pragma unroll
-                for (int kt = 0; kt < KS / 16; ++kt)
-                    acc[kt] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[j][kt][e], qv[j][e], acc[kt],
-                                                                   0, 0, 0);
-    }
-    __syncthreads();  // every wave is done with the rope columns
-    // score partial (wave w % 4, key j, head h) at i = ((w % 4) * KS + j) * H
-    // + h, in row i / 64, column D + i % 64 (the rope part; D + 64 <= the row
-    // stride): waves 4..7 store theirs, waves 0..3 add theirs to them
-    auto sc_at = [&](int i) -> float & { return lat_s[(i >> 6) * kAttnRowStride + D + (i & 63)]; };
-    if (wave >= 4) {
-#pragma unroll
-        for (int kt = 0; kt < KS / 16; ++kt)
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-                sc_at(((wave - 4) * KS + 16 * kt + 4 * g + i) * H + m16) = acc[kt][i];
-    }
-    __syncthreads();
-    if (wave < 4) {
-#pragma unroll
-        for (int kt = 0; kt < KS / 16; ++kt)
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-                sc_at((wave * KS + 16 * kt + 4 * g + i) * H + m16) += acc[kt][i];
-    }
-    __syncthreads();
-    // ---- local softmax statistics: 16 lanes per head, keys sub, sub + 16
-    if (t < 256) {
-        const int h = t >> 4, sub = t & 15;
-        float sv[KS / 16];
-        float mx = -INFINITY;
-#pragma unroll
-        for (int u = 0; u < KS / 16; ++u) {
-            const int j = sub + 16 * u;
-            const float sum = (sc_at((0 * KS + j) * H + h) + sc_at((1 * KS + j) * H + h)) +
-                              (sc_at((2 * KS + j) * H + h) + sc_at((3 * KS + j) * H + h));
-            sv[u] = j < nk ? sum * p.scale : -INFINITY;
-            mx = fmaxf(mx, sv[u]);
-        }
-#pragma unroll
-        for (int o = 8; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
-        float sum = 0.0f;
-#pragma unroll
-        for (int u = 0; u < KS / 16; ++u) {
-            const int j = sub + 16 * u;
-            const float e = j < nk ? expf(sv[u] - mx) : 0.0f;
-            p_s[h * kAttnPStride + j] = e;
-            sum += e;
-        }
-#pragma unroll
-        for (int o = 8; o >= 1; o >>= 1) sum += __shfl_xor(sum, o, 64);
-        if (sub == 0) {
-            smax[h] = mx;
-            ssum[h] = sum;
-        }
-    }
-    __syncthreads();
-    if (t < H) {
-        p.part_max[part + t] = smax[t];
-        p.part_sum[part + t] = ssum[t];
-    }
-    // ---- context: wave w takes the 16-wide d tiles w + 8 i (tiles past D
-    // read tile 0 and store nothing); P rows once per wave, all B reads of
-    // the wave issued before its MFMAs, two tiles' chains interleaved
-    f32x4 pv[KS / 16];
-#pragma unroll
-    for (int u = 0; u < KS / 16; ++u)
-        pv[u] = *reinterpret_cast<const f32x4 *>(p_s + m16 * kAttnPStride + 16 * u + 4 * g);
-    float bv[NT][KS / 16][4];
-#pragma unroll
-    for (int i = 0; i < NT; ++i) {
-        const int dt = wave + 8 * i;
-        const int col = (dt < D / 16 ? dt : 0) * 16 + m16;
-#pragma unroll
-        for (int u = 0; u < KS / 16; ++u)
-#pragma unroll
-            for (int j = 0; j < 4; ++j) bv[i][u][j] = lat_s[(16 * u + 4 * g + j) * kAttnRowStride + col];
-    }
+    // every load so far (query slices included) has landed: inside the tile
+    // loop only prefetched rows are in flight, waited for at their store
+    __builtin_amdgcn_s_waitcnt(0);
     f32x4v cacc[NT];
 #pragma unroll
     for (int i = 0; i < NT; ++i) cacc[i] = f32x4v{0.f, 0.f, 0.f, 0.f};
+    // one tile from its LDS buffer: scores, softmax, context
+    auto process = [&](const float *cur, int tile) {
+        const int nk = keys - tile * TK < TK ? keys - tile * TK : TK;
+        // ---- scores: 16-dim steps w + 8 j, two chains (even / odd k steps);
+        // steps past KD read row columns 0.. (finite) against a zero query slice
+        {
+            f32x4 av[NS];
 #pragma unroll
-    for (int u = 0; u < KS / 16; ++u) {
-        const float pj[4] = {pv[u].x, pv[u].y, pv[u].z, pv[u].w};
+            for (int j = 0; j < NS; ++j) {
+                const int d0 = 16 * (wave + 8 * j);
+                av[j] = *reinterpret_cast<const f32x4 *>(cur + m16 * kAttnRowStride +
+                                                         (d0 < KD ? d0 : 0) + 4 * g);
+            }
+            __builtin_amdgcn_sched_barrier(0);  // all row reads issued before the products
+            f32x4v a0 = f32x4v{0.f, 0.f, 0.f, 0.f}, a1 = a0;
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
+            for (int j = 0; j < NS; ++j) {
+                a0 = __builtin_amdgcn_mfma_f32_16x16x4f32(av[j].x, qv[j].x, a0, 0, 0, 0);
+                a1 = __builtin_amdgcn_mfma_f32_16x16x4f32(av[j].y, qv[j].y, a1, 0, 0, 0);
+                a0 = __builtin_amdgcn_mfma_f32_16x16x4f32(av[j].z, qv[j].z, a0, 0, 0, 0);
+                a1 = __builtin_amdgcn_mfma_f32_16x16x4f32(av[j].w, qv[j].w, a1, 0, 0, 0);
+            }
 #pragma unroll
-            for (int i = 0; i < NT; ++i)
-                cacc[i] = __builtin_amdgcn_mfma_f32_16x16x4f32(pj[j], bv[i][u][j], cacc[i], 0, 0, 0);
+            for (int i = 0; i < 4; ++i) sp[(wave * TK + 4 * g + i) * H + m16] = a0[i] + a1[i];
+        }
+        __syncthreads();
+        // ---- softmax: 16 lanes (one DPP row) per head, one key each
+        if (t < 256) {
+            const int h = t >> 4, j = t & 15;
+            const float *q = sp + j * H + h;
+            const float s8 = ((q[0 * TK * H] + q[1 * TK * H]) + (q[2 * TK * H] + q[3 * TK * H])) +
+                             ((q[4 * TK * H] + q[5 * TK * H]) + (q[6 * TK * H] + q[7 * TK * H]));
+            const float s = j < nk ? s8 * p.scale : -INFINITY;
+            const float mo = smax[h];
+            const float mn = fmaxf(mo, row16_max(s));  // finite: key 0 of the tile is valid
+            const float e = j < nk ? expf(s - mn) : 0.0f;
+            p_s[h * kAttnPStride + j] = e;
+            const float sum = row16_sum(e);
+            if (j == 0) {
+                const float f = expf(mo - mn);  // 0 on the first tile
+                sscale[h] = f;
+                ssum[h] = ssum[h] * f + sum;
+                smax[h] = mn;
+            }
+        }
+        __syncthreads();
+        // ---- context: rescale, then P x lat for the wave's d tiles (tiles
+        // past D read tile 0 and store nothing)
+        {
+            const f32x4 f = *reinterpret_cast<const f32x4 *>(sscale + 4 * g);
+            const f32x4 pv = *reinterpret_cast<const f32x4 *>(p_s + m16 * kAttnPStride + 4 * g);
+            float bv[NT][4];
+#pragma unroll
+            for (int i = 0; i < NT; ++i) {
+                const int dt = wave + 8 * i;
+                const int col = (dt < D / 16 ? dt : 0) * 16 + m16;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) bv[i][j] = cur[(4 * g + j) * kAttnRowStride + col];
+            }
+#pragma unroll
+            for (int i = 0; i < NT; ++i) {
+                cacc[i][0] *= f.x;
+                cacc[i][1] *= f.y;
+                cacc[i][2] *= f.z;
+                cacc[i][3] *= f.w;
+            }
+            const float pj[4] = {pv.x, pv.y, pv.z, pv.w};
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+#pragma unroll
+                for (int i = 0; i < NT; ++i)
+                    cacc[i] = __builtin_amdgcn_mfma_f32_16x16x4f32(pj[j], bv[i][j], cacc[i], 0, 0, 0);
+        }
+    };
+    // two tiles in flight: register set A holds the even tiles of the run,
+    // B the odd ones; a tile's rows go into its buffer at the top of its
+    // step (the buffer was last read two steps before, ahead of this step's
+    // first barrier), then the set loads the tile two ahead
+    // (pairs of steps in a loop without a mid exit, an odd last tile after
+    // it, so that the compiler sees the same loads in flight on every path)
+    load_tile(t_begin + 1, lb, rb);
+    int tile = t_begin;
+    for (; tile + 1 < t_end; tile += 2) {
+        store_tile(buf0, la, ra);
+        __syncthreads();
+        load_tile(tile + 2, la, ra);
+        process(buf0, tile);
+        store_tile(buf1, lb, rb);
+        __syncthreads();
+        load_tile(tile + 3, lb, rb);
+        process(buf1, tile + 1);
+    }
+    if (tile < t_end) {
+        store_tile(buf0, la, ra);
+        __syncthreads();
+        process(buf0, tile);
+    }
+    // ---- the partial: max / sum at [row][head][split], the latent context
+    // at [row][head][chunk of DL dims][split][DL]
+    const int nc = D / DL;
+    if (t < H) {
+        const long at = ((long)r * H + t) * p.max_splits + b;
+        p.part_max[at] = smax[t];
+        p.part_sum[at] = ssum[t];
     }
 #pragma unroll
     for (int i = 0; i < NT; ++i) {
         const int dt = wave + 8 * i;
         if (dt < D / 16) {
+            const int d = dt * 16 + m16;
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 const int h = 4 * g + q;
-                if (h < p.heads) p.part_lc[(part + h) * D + dt * 16 + m16] = cacc[i][q];
+                if (h < p.heads)
+                    p.part_lc[((((long)r * H + h) * nc + d / DL) * p.max_splits + b) * DL + d % DL] =
+                        cacc[i][q];
             }
         }
     }
@@ -732,13 +776,13 @@ __global__ __launch_bounds__(256, 2) void mla_prefill_attend_kernel(MlaParams p)
 // Merge of the key splits and the value projection, one launch.  Workgroup
 // (row, head h, chunk c of kMlaValueDims latent dims), 8 waves:
 //   merge  lc_h[d] = sum_s e^{m_s - M} lc_s[d] / sum_s e^{m_s - M} l_s for
-//          the chunk's dims in one pass: the wave's lanes form 64 /
-//          kMlaValueDims groups, so 16 lane groups take the splits g, g + 16,
-//          ... with a running max (rescaling on a new max), loading
-//          kMergeBatch splits before using them; the groups meet in LDS.
-//          The row's own key (not in any split) joins as one more term: its
-//          score [qa | q_rope] . [lat | rope] over the whole workgroup, its
-//          weight 1 and its latent row.
+//          the chunk's dims in one pass over its contiguous partials: thread
+//          t takes dims 4 (t % 8) .. + 3 of the splits t / 8, t / 8 + 64, ...
+//          with a running max (rescaling on a new max), loading kMergeBatch
+//          splits before using them; the 8 slots of a wave meet by
+//          shuffles, the 8 waves in LDS.  The row's own key (not in any
+//          split) joins as one more term: its score [qa | q_rope] . [lat |
+//          rope] over the whole workgroup, its weight 1 and its latent row.
 //   value  y_c[v] = W_UV_h[v, chunk] . lc_h[chunk] for every value row v:
 //          thread t takes row t / 4 (+ 128 per pass), dims 8 (t % 4) .. + 7;
 //          the first pass's weights are loaded before the merge starts.
@@ -749,22 +793,22 @@ __global__ __launch_bounds__(256, 2) void mla_prefill_attend_kernel(MlaParams p)
 //          waits for its stores to complete before its arrival increment, so
 //          the workgroup that counts last finds every share in memory, with
 //          no L2 write-back fence.
-constexpr int kMergeBatch = 16;
+constexpr int kMergeBatch = 4;
 template <int FMT>
 __global__ __launch_bounds__(512) void mla_merge_value_kernel(MlaParams p) {
     constexpr int H = kMlaMaxHeads;
-    constexpr int KS = kMlaKeysPerSplit;
+    constexpr int TK = kMlaTileKeys;
     constexpr int DL = kMlaValueDims, NB = kMergeBatch;
-    constexpr int NG = 8 * (64 / DL);  // lane groups
+    constexpr int NG = 8;  // waves
+    static_assert(DL == 32, "8 threads of 4 dims per split");
     __shared__ float gm[NG], gl[NG];
-    __shared__ float gacc[NG][DL];
+    __shared__ __attribute__((aligned(16))) float gacc[NG][DL];
     __shared__ float lcs[DL];
     __shared__ float ownp[8];
     __shared__ int last;
     const int r = blockIdx.x, h = blockIdx.y, c = blockIdx.z;
     const int nchunks = gridDim.z;
-    const int t = threadIdx.x, lane = t & 63;
-    const int dl = lane % DL, grp = (t >> 6) * (64 / DL) + lane / DL;
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     // the position first: memory reads complete in issue order, so a wait
     // for it does not also wait for the weight fetch below
     const int pos = mla_position(p) + r;  // row r's own key; the splits hold keys 0 .. pos - 1
@@ -786,44 +830,71 @@ __global__ __launch_bounds__(512) void mla_merge_value_kernel(MlaParams p) {
     if (t < p.rope) own = fmaf(qr[t], rnew[t], own);
     const float own_v = t < DL ? lnew[c * DL + t] : 0.0f;
 
-    const int ns = (keys + KS - 1) / KS;
-    const long base = (long)r * p.max_splits * H + h;
-    const float *lc = p.part_lc + base * p.latent + c * DL + dl;
-    const long lc_step = (long)H * p.latent;
-    float M = -INFINITY, L = 0.0f, acc = 0.0f;
+    const int tiles = (keys + TK - 1) / TK;
+    const int ns = tiles < p.splits ? tiles : p.splits;  // partials of this row
+    const long mbase = ((long)r * H + h) * p.max_splits;
+    const int dq = t & 7, slot = t >> 3;
+    const float *lc = p.part_lc + (((long)r * H + h) * nchunks + c) * p.max_splits * DL + 4 * dq;
+    float M = -INFINITY, L = 0.0f;
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
     // branch-free batches (selects, no ifs), so that the compiler keeps all
     // of a batch's loads ahead of their first use
-    for (int s0 = grp; s0 < ns; s0 += NG * NB) {
-        float mv[NB], lv[NB], v[NB];
+    for (int s0 = slot; s0 < ns; s0 += 64 * NB) {
+        float mv[NB], lv[NB];
+        f32x4 v[NB];
         bool ok[NB];
 #pragma unroll
         for (int i = 0; i < NB; ++i) {
-            ok[i] = s0 + NG * i < ns;
-            const int s = ok[i] ? s0 + NG * i : s0;  // clamped: loaded, unused
-            mv[i] = p.part_max[base + (long)s * H];
-            lv[i] = p.part_sum[base + (long)s * H];
-            v[i] = lc[(long)s * lc_step];
+            ok[i] = s0 + 64 * i < ns;
+            const int s = ok[i] ? s0 + 64 * i : s0;  // clamped: loaded, unused
+            mv[i] = p.part_max[mbase + s];
+            lv[i] = p.part_sum[mbase + s];
+            v[i] = load_f4(lc + (long)s * DL);
         }
         float mn = M;
 #pragma unroll
         for (int i = 0; i < NB; ++i) mn = fmaxf(mn, ok[i] ? mv[i] : -INFINITY);
         // split s0 is valid, so mn is finite; the rescale is 0 while M is -inf
         const float sc = expf(M - mn);
-        acc *= sc;
+        acc.x *= sc;
+        acc.y *= sc;
+        acc.z *= sc;
+        acc.w *= sc;
         L *= sc;
 #pragma unroll
         for (int i = 0; i < NB; ++i) {
             const float e = ok[i] ? expf(mv[i] - mn) : 0.0f;
-            acc = fmaf(e, v[i], acc);
+            acc.x = fmaf(e, v[i].x, acc.x);
+            acc.y = fmaf(e, v[i].y, acc.y);
+            acc.z = fmaf(e, v[i].z, acc.z);
+            acc.w = fmaf(e, v[i].w, acc.w);
             L = fmaf(e, lv[i], L);
         }
         M = mn;
     }
-    if (dl == 0) {
-        gm[grp] = M;
-        gl[grp] = L;
+    // the 8 slots of the wave (lanes 8 apart), then the waves in LDS
+#pragma unroll
+    for (int o = 8; o <= 32; o <<= 1) {
+        const float M2 = __shfl_xor(M, o, 64), L2 = __shfl_xor(L, o, 64);
+        const f32x4 a2 = {__shfl_xor(acc.x, o, 64), __shfl_xor(acc.y, o, 64),
+                          __shfl_xor(acc.z, o, 64), __shfl_xor(acc.w, o, 64)};
+        const float mn = fmaxf(M, M2);
+        const float e1 = M == -INFINITY ? 0.0f : expf(M - mn);
+        const float e2 = M2 == -INFINITY ? 0.0f : expf(M2 - mn);
+        acc.x = acc.x * e1 + a2.x * e2;
+        acc.y = acc.y * e1 + a2.y * e2;
+        acc.z = acc.z * e1 + a2.z * e2;
+        acc.w = acc.w * e1 + a2.w * e2;
+        L = L * e1 + L2 * e2;
+        M = mn;
     }
-    gacc[grp][dl] = acc;
+    if (lane < 8) {
+        if (lane == 0) {
+            gm[wave] = M;
+            gl[wave] = L;
+        }
+        *reinterpret_cast<f32x4 *>(&gacc[wave][4 * dq]) = acc;
+    }
     own = wave_sum(own);
     if (lane == 0) ownp[t >> 6] = own;
     __syncthreads();
@@ -892,7 +963,6 @@ int mla_attention_core(const MlaParams &p, hipStream_t stream) {
         p.nope <= 0 || p.nope > 256 || p.vdim <= 0 || p.rows <= 0 || p.max_splits <= 0 ||
         !p.latent_context || p.position < 0 || p.query_stride < (long)p.heads * (p.nope + p.rope) ||
         p.compressed_stride < p.latent + p.rope ||
-        (p.position + p.rows + kMlaKeysPerSplit - 1) / kMlaKeysPerSplit > p.max_splits ||
         (p.grid_splits && (!p.position_dev || p.grid_splits > p.max_splits)))
         return kErrArgs;
     // the fp32-MFMA score tiles take 16 dims per step (mla_session_shape_ok)
@@ -944,11 +1014,15 @@ int mla_attention_core(const MlaParams &p, hipStream_t stream) {
         default: hipLaunchKernelGGL(mla_prep_kernel<kQ4>, pgrid, dim3(256), 0, stream, q, chunks); break;
         }
         // row r's splits hold keys 0 .. position + r - 1 (its own key joins
-        // in the merge)
-        const int last_keys = q.position + q.rows - 1;
-        const int needed = (last_keys + kMlaKeysPerSplit - 1) / kMlaKeysPerSplit;
-        const int splits = q.grid_splits ? q.grid_splits : (needed > 0 ? needed : 1);
-        hipLaunchKernelGGL(mla_attend_mfma_kernel, dim3(splits, q.rows), dim3(512), kAttnMfmaLds,
+        // in the merge): kMlaAttendGroups workgroups over the group's rows,
+        // at most one per key tile of the last row
+        const int tiles = (q.position + q.rows - 1 + kMlaTileKeys - 1) / kMlaTileKeys;
+        int splits = (kMlaAttendGroups + q.rows - 1) / q.rows;
+        if (splits > tiles) splits = tiles;
+        if (splits > q.max_splits) splits = q.max_splits;
+        if (splits < 1) splits = 1;
+        q.splits = q.grid_splits ? q.grid_splits : splits;
+        hipLaunchKernelGGL(mla_attend_mfma_kernel, dim3(q.splits, q.rows), dim3(512), kAttnMfmaLds,
                            stream, q);
         switch (q.kv_b.fmt) {
         case kF32: hipLaunchKernelGGL(mla_merge_value_kernel<kF32>, mgrid, dim3(512), 0, stream, q); break;

@@ -1456,7 +1456,9 @@ extern "C" int moonlight_session_create(MoonlightSession **out, MoonlightModel *
     const size_t H = (size_t)c.hidden_size, L = (size_t)c.layer_count, E = (size_t)c.expert_count;
     const size_t K = (size_t)c.experts_per_token;
     const size_t heads = (size_t)c.head_count;
-    s->max_splits = (int)((ctx + kMlaKeysPerSplit - 1) / kMlaKeysPerSplit);
+    // attend partials per row: one per workgroup, at most one per key tile
+    s->max_splits = (int)std::min<size_t>((ctx + kMlaTileKeys - 1) / kMlaTileKeys,
+                                          (size_t)kMlaAttendGroups);
     const size_t splits = (size_t)s->max_splits;
     // the split-attention (decode) path runs at most kMlaDecodeRows rows per launch group
     const size_t dr = mb < (size_t)kMlaDecodeRows ? mb : (size_t)kMlaDecodeRows;

@@ -97,7 +97,9 @@ def attention_names(layer):
                             "o_proj.weight", "kv_a_layernorm.weight")]
 
 
-@pytest.mark.parametrize("pos", [4096, 16383])
+# 4096: one key tile per attend workgroup; 5000: one or two (uneven split);
+# 16383: four
+@pytest.mark.parametrize("pos", [4096, 5000, 16383])
 def test_mla_decode(moon, pos):
     print(f"[gpu] moonlight MLA decode at position {pos}", flush=True)
     ctx, layer = pos + 1, 2
