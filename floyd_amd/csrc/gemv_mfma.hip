@@ -31,6 +31,8 @@
 #include "mlh_device.h"
 #include "mlh_host.h"
 
+#include <type_traits>
+
 namespace mlh {
 
 namespace {
@@ -121,7 +123,7 @@ __global__ __launch_bounds__(256) void gemv_mfma_kernel(MfmaGemvArgs a) {
     using Sh = MgShape<FMT, B, DUAL, ND>;
     const GemvParams &p = a.p;
     extern __shared__ __attribute__((aligned(16))) unsigned char gm_lds[];
-    __shared__ float red[4][2][B][kRows];
+    __shared__ float red[4][4][2][B][kRows];  // [wave][limb][gate / up][token row][row]
     __shared__ float red_ss[4][B];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int row0 = blockIdx.x * kRows;
@@ -258,6 +260,17 @@ __global__ __launch_bounds__(256) void gemv_mfma_kernel(MfmaGemvArgs a) {
     __builtin_amdgcn_sched_barrier(0);
     __builtin_amdgcn_s_waitcnt(0);
     __builtin_amdgcn_sched_barrier(0);
+    // the epilogue's operands of lane 16 b + n (row row0 + n, token row b),
+    // in flight during the products and the reduction
+    const int er = row0 + (lane & 15), eb = lane >> 4 < B ? lane >> 4 : 0;
+    const int erc = er < p.O ? er : p.O - 1;
+    const bool has_res = p.epilogue == kEpiResidual;
+    float e_s = 0.0f, e_s2 = 0.0f, e_res = 0.0f;
+    if (wave == 0) {
+        e_s = p.s[erc];
+        if (DUAL) e_s2 = p.s2[erc];
+        if (has_res) e_res = p.resid[(long)eb * p.resid_stride + erc];
+    }
 #pragma unroll
     for (int j = 0; j < kMaxPass; ++j) {
         const int e = j * 512 + lane * 8;
@@ -285,35 +298,55 @@ __global__ __launch_bounds__(256) void gemv_mfma_kernel(MfmaGemvArgs a) {
     const unsigned char *wrow2 = wl + (kRows + n) * kqb;
     i32x4 acc = {0, 0, 0, 0}, acc2 = {0, 0, 0, 0}, acc1 = {0, 0, 0, 0};
     constexpr int nsteps = kq / 64;
+    // steps in groups of 8 (and one group of the rest): the group's LDS
+    // reads issued before its products
+    using WRaw = typename std::conditional<FMT == kQ8, u32x4, uint2>::type;
     const i32x4 ones = {0x01010101, 0x01010101, 0x01010101, 0x01010101};
-    for (int s = 0; s < nsteps; ++s) {
-        const u32x4 av = *reinterpret_cast<const u32x4 *>(arow + 64 * s + 16 * g);
-        const i32x4 A = a_ok ? i32x4{(int)av.x, (int)av.y, (int)av.z, (int)av.w}
-                             : i32x4{0, 0, 0, 0};
-        i32x4 Bw, Bu;
-        if constexpr (FMT == kQ8) {
-            const int lc = 4 * s + g;  // logical chunk
-            const u32x4 w = *reinterpret_cast<const u32x4 *>(wrow + 16 * (lc ^ (n & swz)));
-            Bw = i32x4{(int)w.x, (int)w.y, (int)w.z, (int)w.w};
-            if constexpr (DUAL) {
-                const u32x4 u = *reinterpret_cast<const u32x4 *>(wrow2 + 16 * (lc ^ (n & swz)));
-                Bu = i32x4{(int)u.x, (int)u.y, (int)u.z, (int)u.w};
+    auto group = [&](int s0, auto count) {
+        constexpr int U = decltype(count)::value;
+        u32x4 av[U];
+        WRaw wv[U], uv[U];
+#pragma unroll
+        for (int i = 0; i < U; ++i) {
+            const int s = s0 + i;
+            av[i] = *reinterpret_cast<const u32x4 *>(arow + 64 * s + 16 * g);
+            if constexpr (FMT == kQ8) {
+                const int lc = 4 * s + g;  // logical chunk
+                wv[i] = *reinterpret_cast<const u32x4 *>(wrow + 16 * (lc ^ (n & swz)));
+                if constexpr (DUAL) uv[i] = *reinterpret_cast<const u32x4 *>(wrow2 + 16 * (lc ^ (n & swz)));
+            } else {
+                const int lc = 2 * s + (g >> 1);  // logical chunk; 8-byte half g & 1
+                wv[i] = *reinterpret_cast<const uint2 *>(wrow + 16 * (lc ^ (n & swz)) + 8 * (g & 1));
+                if constexpr (DUAL)
+                    uv[i] = *reinterpret_cast<const uint2 *>(wrow2 + 16 * (lc ^ (n & swz)) + 8 * (g & 1));
             }
-        } else {
-            const int lc = 2 * s + (g >> 1);  // logical chunk; 8-byte half g & 1
-            const uint2 w = *reinterpret_cast<const uint2 *>(wrow + 16 * (lc ^ (n & swz)) + 8 * (g & 1));
-            Bw = i32x4{(int)(w.x & 0x0F0F0F0Fu), (int)((w.x >> 4) & 0x0F0F0F0Fu),
-                       (int)(w.y & 0x0F0F0F0Fu), (int)((w.y >> 4) & 0x0F0F0F0Fu)};
-            if constexpr (DUAL) {
-                const uint2 u = *reinterpret_cast<const uint2 *>(wrow2 + 16 * (lc ^ (n & swz)) + 8 * (g & 1));
-                Bu = i32x4{(int)(u.x & 0x0F0F0F0Fu), (int)((u.x >> 4) & 0x0F0F0F0Fu),
-                           (int)(u.y & 0x0F0F0F0Fu), (int)((u.y >> 4) & 0x0F0F0F0Fu)};
-            }
-            acc1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A, ones, acc1, 0, 0, 0);
         }
-        acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(A, Bw, acc, 0, 0, 0);
-        if constexpr (DUAL) acc2 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A, Bu, acc2, 0, 0, 0);
-    }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int i = 0; i < U; ++i) {
+            const i32x4 A = a_ok ? i32x4{(int)av[i].x, (int)av[i].y, (int)av[i].z, (int)av[i].w}
+                                 : i32x4{0, 0, 0, 0};
+            i32x4 Bw, Bu;
+            if constexpr (FMT == kQ8) {
+                Bw = i32x4{(int)wv[i].x, (int)wv[i].y, (int)wv[i].z, (int)wv[i].w};
+                if constexpr (DUAL) Bu = i32x4{(int)uv[i].x, (int)uv[i].y, (int)uv[i].z, (int)uv[i].w};
+            } else {
+                const uint2 w = wv[i];
+                Bw = i32x4{(int)(w.x & 0x0F0F0F0Fu), (int)((w.x >> 4) & 0x0F0F0F0Fu),
+                           (int)(w.y & 0x0F0F0F0Fu), (int)((w.y >> 4) & 0x0F0F0F0Fu)};
+                if constexpr (DUAL) {
+                    const uint2 u = uv[i];
+                    Bu = i32x4{(int)(u.x & 0x0F0F0F0Fu), (int)((u.x >> 4) & 0x0F0F0F0Fu),
+                               (int)(u.y & 0x0F0F0F0Fu), (int)((u.y >> 4) & 0x0F0F0F0Fu)};
+                }
+                acc1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A, ones, acc1, 0, 0, 0);
+            }
+            acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(A, Bw, acc, 0, 0, 0);
+            if constexpr (DUAL) acc2 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A, Bu, acc2, 0, 0, 0);
+        }
+    };
+    for (int s0 = 0; s0 + 8 <= nsteps; s0 += 8) group(s0, std::integral_constant<int, 8>{});
+    if constexpr (nsteps % 8 != 0) group(nsteps - nsteps % 8, std::integral_constant<int, nsteps % 8>{});
     // ---- 5. lane (g, n) holds limb g of token rows b = 0..3 (registers) for
     // weight row n: combine the limbs across the lane groups, scale
     const float limb_w = g == 0 ? 16777216.0f : g == 1 ? 65536.0f : g == 2 ? 256.0f : 1.0f;
@@ -324,21 +357,13 @@ __global__ __launch_bounds__(256) void gemv_mfma_kernel(MfmaGemvArgs a) {
             c -= 8 * acc1[b];
             if (DUAL) c2 -= 8 * acc1[b];
         }
-        float v = (float)c * limb_w, v2 = (float)c2 * limb_w;
-        v += __shfl_xor(v, 16, 64);
-        v += __shfl_xor(v, 32, 64);
-        if (DUAL) {
-            v2 += __shfl_xor(v2, 16, 64);
-            v2 += __shfl_xor(v2, 32, 64);
-        }
-        if (g == 0) {
-            red[wave][0][b][n] = v * step[b];
-            if (DUAL) red[wave][1][b][n] = v2 * step[b];
-        }
+        red[wave][g][0][b][n] = (float)c * limb_w * step[b];
+        if (DUAL) red[wave][g][1][b][n] = (float)c2 * limb_w * step[b];
         if (lane == 0) red_ss[wave][b] = ss[b];
     }
     __syncthreads();
-    // ---- 6. the four waves' shares (in wave order) and the epilogue
+    // ---- 6. the shares of the four limbs and four waves (limbs, then waves,
+    // in order) and the epilogue
     if (wave != 0 || g >= B) return;
     const int b = g;  // lanes 16 b + n, b < B
     const int row = row0 + n;
@@ -348,15 +373,21 @@ __global__ __launch_bounds__(256) void gemv_mfma_kernel(MfmaGemvArgs a) {
         const float tot = (red_ss[0][b] + red_ss[1][b]) + (red_ss[2][b] + red_ss[3][b]);
         inv_rms = 1.0f / sqrtf(tot / (float)Sh::kI + p.eps);
     }
-    const float sum = ((red[0][0][b][n] + red[1][0][b][n]) + (red[2][0][b][n] + red[3][0][b][n])) * inv_rms;
+    auto total = [&](int u) {
+        float w4[4];
+#pragma unroll
+        for (int w = 0; w < 4; ++w)
+            w4[w] = (red[w][0][u][b][n] + red[w][1][u][b][n]) + (red[w][2][u][b][n] + red[w][3][u][b][n]);
+        return ((w4[0] + w4[1]) + (w4[2] + w4[3])) * inv_rms;
+    };
+    const float sum = total(0);
     float *yb = p.y + (long)b * p.y_stride;
     if (DUAL) {
-        const float sum2 = ((red[0][1][b][n] + red[1][1][b][n]) + (red[2][1][b][n] + red[3][1][b][n])) * inv_rms;
-        yb[row] = silu(sum * p.s[row]) * (sum2 * p.s2[row]);
+        yb[row] = silu(sum * e_s) * (total(1) * e_s2);
         return;
     }
-    float out = sum * p.s[row];
-    if (p.epilogue == kEpiResidual) out = p.resid[(long)b * p.resid_stride + row] + out;
+    float out = sum * e_s;
+    if (has_res) out = e_res + out;
     yb[row] = out;
 }
 
