@@ -204,14 +204,21 @@ __device__ __forceinline__ void unpack_q4_word(unsigned w, unsigned &out0, unsig
 }
 
 __device__ __forceinline__ int find_task(const int *tile_start, int n, int tile) {
-    // last t in [0, n) with tile_start[t] <= tile
-    int lo = 0, hi = n - 1;
-    while (lo < hi) {
-        const int mid = (lo + hi + 1) >> 1;
-        if (tile_start[mid] <= tile) lo = mid;
-        else hi = mid - 1;
+    // last t in [0, n) with tile_start[t] <= tile (tile_start non-decreasing,
+    // tile_start[0] = 0): every lane of the wave tests entries lane, lane +
+    // 64, ... and the ballots count them -- one round of loads for the first
+    // 128 tasks instead of a chain of dependent ones
+    const int lane = threadIdx.x & 63;
+    const int i0 = lane, i1 = lane + 64;
+    const int v0 = tile_start[i0 < n ? i0 : 0];
+    const int v1 = tile_start[i1 < n ? i1 : 0];
+    int count = __popcll(__ballot(i0 < n && v0 <= tile)) + __popcll(__ballot(i1 < n && v1 <= tile));
+    for (int c0 = 128; c0 < n; c0 += 64) {
+        const int i = c0 + lane;
+        const int v = tile_start[i < n ? i : 0];
+        count += __popcll(__ballot(i < n && v <= tile));
     }
-    return lo;
+    return count - 1;
 }
 
 template <bool DUAL, int BM>
@@ -1032,7 +1039,11 @@ __host__ __device__ inline int moe_shared_down_parts(const MoeGemmParams &p) {
     return p.has_shared && p.shared_out2 && p.shared_width == 2 * p.inter ? 2 : 1;
 }
 
-__device__ __forceinline__ void moe_schedule_body(const MoeScheduleParams &sp) {
+// With L (routing in the same workgroup) the route tables and the expert
+// table (ew_lds, [experts]) come from LDS instead of global memory.
+__device__ __forceinline__ void moe_schedule_body(const MoeScheduleParams &sp,
+                                                  const RouteLds *L = nullptr,
+                                                  const ExpertWeights *ew_lds = nullptr) {
     const MoeGemmParams &p = sp.p;
     const int bm = sp.bm;
     auto tiles_rt = [bm](bool dual, int rows, int n_out) {
@@ -1040,13 +1051,13 @@ __device__ __forceinline__ void moe_schedule_body(const MoeScheduleParams &sp) {
         return ((rows + bm - 1) / bm) * ((n_out + outw - 1) / outw);
     };
     __shared__ int tiles[2][kQgMaxTasks];
-    const int nr = *p.n_unique;
+    const int nr = L ? L->unique_total : *p.n_unique;
     GemmTask *t0 = p.tasks;
     GemmTask *t1 = p.tasks + kQgMaxTasks;
     for (int u = threadIdx.x; u < nr; u += blockDim.x) {
-        const int e = p.unique[u];
-        const int cnt = p.counts[e], off = p.offsets[e];
-        const ExpertWeights ew = p.expert_table[e];
+        const int e = L ? L->unique[u] : p.unique[u];
+        const int cnt = L ? L->counts[e] : p.counts[e], off = L ? L->offsets[e] : p.offsets[e];
+        const ExpertWeights ew = ew_lds ? ew_lds[e] : p.expert_table[e];
         GemmTask a;
         a.w = ew.gate;
         a.w2 = ew.up;
@@ -1124,40 +1135,47 @@ __device__ __forceinline__ void moe_schedule_body(const MoeScheduleParams &sp) {
             }
         }
     }
-    __syncthreads();
-    if (threadIdx.x < 2) {
-        const int s = threadIdx.x;
-        const int extra = s == 0 ? 1 : nsd;
-        int *start = p.tile_start + s * (kQgMaxTasks + 1);
+    lds_barrier();  // the tables are read by the next launch
+    // tile prefix sums: entry u of stage s by its own thread (independent
+    // LDS reads rather than one thread's dependent chain)
+    for (int idx = threadIdx.x; idx < 2 * (kQgMaxTasks + 1); idx += blockDim.x) {
+        const int s = idx / (kQgMaxTasks + 1), u = idx % (kQgMaxTasks + 1);
+        const int n = nr + (s == 0 ? 1 : nsd);
+        if (u > n) continue;
         int acc = 0;
-        for (int u = 0; u < nr + extra; ++u) {
-            start[u] = acc;
-            acc += tiles[s][u];
-        }
-        start[nr + extra] = acc;
+        for (int v = 0; v < u; ++v) acc += tiles[s][v];
+        p.tile_start[s * (kQgMaxTasks + 1) + u] = acc;
     }
 }
 
 // The token-row quantisation of the MoE input (RMSNorm'ed) and, in the last
-// workgroup, the GEMM task and tile tables: one launch before stage 0.
+// workgroup, the GEMM task and tile tables: one launch before stage 0.  Eight
+// waves: a row each to quantise, or to route (the routing workgroup).
+constexpr int kPrepWaves = 8;
 template <bool REG>
-__global__ __launch_bounds__(256) void moe_prep_kernel(QuantSeg a, MoeScheduleParams sp,
-                                                       int blocks_a) {
+__global__ __launch_bounds__(64 * kPrepWaves) void moe_prep_kernel(QuantSeg a, MoeScheduleParams sp,
+                                                                   int blocks_a) {
     if ((int)blockIdx.x == blocks_a) {
         if (sp.p.route_in_prep) {
-            // route_kernel's work: selection per row, then the route tables
-            // (read back below after the barrier, as the next launch would)
+            // route_kernel's work: selection (wave w: row w), the route tables
+            // kept in LDS for the schedule, the expert table staged in LDS
+            // meanwhile
             __shared__ RouteLds L;
+            __shared__ ExpertWeights ew[64];
+            const RouteParams &rp = sp.p.route;  // rows <= kPrepWaves, experts <= 64
             const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-            for (int r = wave; r < sp.p.route.rows; r += 4) route_any(sp.p.route, r, lane, L.ids);
-            __syncthreads();
-            small_tables(sp.p.route, L);
-            __syncthreads();
+            if (wave == 0 && lane < rp.experts) ew[lane] = sp.p.expert_table[lane];
+            if (wave < rp.rows) (void)select_row_64(rp, wave, lane, L.ids);
+            lds_barrier();
+            small_tables(rp, L);
+            lds_barrier();
+            moe_schedule_body(sp, &L, ew);
+            return;
         }
         moe_schedule_body(sp);
         return;
     }
-    const int row = (int)blockIdx.x * 4 + (int)(threadIdx.x >> 6);
+    const int row = (int)blockIdx.x * kPrepWaves + (int)(threadIdx.x >> 6);
     if (row >= a.rows) return;
     quantize_row<REG>(a, row);
 }
@@ -1197,18 +1215,19 @@ int moe_gemm(const MoeGemmParams &p, hipStream_t stream) {
     if (p.route_in_prep &&
         (p.route.rows != p.rows || p.rows > kRouteOneGroupRows || !p.route.logits ||
          p.route.experts != p.experts || p.route.top_k != p.top_k || p.top_k > kMaxTopK ||
-         p.experts > kMaxExperts || p.rows * p.top_k > kRouteFusedMaxPositions ||
+         p.experts > 64 || p.rows * p.top_k > kRouteFusedMaxPositions ||
          !p.route.ids || !p.route.weights || !p.route.n_unique || !p.route.unique ||
          !p.route.counts || !p.route.offsets || !p.route.list_rows || !p.route.list_slots ||
          !p.route.list_pos || !p.route.error))
         return kErrArgs;
-    const int blocks_x = (p.rows + 3) / 4;
+    static_assert(kRouteOneGroupRows <= kPrepWaves, "a wave per routed row");
+    const int blocks_x = (p.rows + kPrepWaves - 1) / kPrepWaves;
     if (p.hidden <= kQuantRegChunks * kWave * 4)
-        hipLaunchKernelGGL(moe_prep_kernel<true>, dim3(blocks_x + 1), dim3(256), 0, stream, xs,
-                           sp, blocks_x);
+        hipLaunchKernelGGL(moe_prep_kernel<true>, dim3(blocks_x + 1), dim3(64 * kPrepWaves), 0,
+                           stream, xs, sp, blocks_x);
     else
-        hipLaunchKernelGGL(moe_prep_kernel<false>, dim3(blocks_x + 1), dim3(256), 0, stream, xs,
-                           sp, blocks_x);
+        hipLaunchKernelGGL(moe_prep_kernel<false>, dim3(blocks_x + 1), dim3(64 * kPrepWaves), 0,
+                           stream, xs, sp, blocks_x);
     if (hipGetLastError() != hipSuccess) return kErrLaunch;
     int st = kOk;
 

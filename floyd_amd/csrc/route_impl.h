@@ -52,12 +52,21 @@ struct RowSelection {
 };
 
 template <bool WRITE = true>
+__device__ __forceinline__ RowSelection select_row_64_v(const RouteParams &p, int r, int lane,
+                                                       int *lds_ids, float logit, float bias);
+template <bool WRITE = true>
 __device__ __forceinline__ RowSelection select_row_64(const RouteParams &p, int r, int lane,
                                                      int *lds_ids) {
+    const bool have = lane < p.experts;
+    return select_row_64_v<WRITE>(p, r, lane, lds_ids, have ? p.logits[(long)r * p.experts + lane] : 0.0f,
+                                  have ? p.bias[lane] : 0.0f);
+}
+// The same with this lane's logit and bias already loaded.
+template <bool WRITE>
+__device__ __forceinline__ RowSelection select_row_64_v(const RouteParams &p, int r, int lane,
+                                                       int *lds_ids, float logit, float bias) {
     const int E = p.experts, K = p.top_k;
     const bool have = lane < E;
-    const float logit = have ? p.logits[(long)r * E + lane] : 0.0f;
-    const float bias = have ? p.bias[lane] : 0.0f;
     const float score = have ? sigmoid_exact(logit) : 0.0f;
     const float sel = have ? score + bias : -INFINITY;
     RowSelection rs{-1, 0ull};
@@ -285,6 +294,7 @@ constexpr int kRouteOneGroupRows = 8;
 constexpr int kRouteFusedMaxPositions = 1024;
 struct RouteLds {
     int first_pos[kMaxExperts], counts[kMaxExperts], offsets[kMaxExperts];
+    int unique[kMaxExperts];  // experts in first-appearance order
     int ids[kRouteFusedMaxPositions];
     unsigned long long first_mask[kRouteFusedMaxPositions / 64];
     int word_prefix[kRouteFusedMaxPositions / 64];
@@ -306,6 +316,14 @@ __device__ inline void write_tasks(const RouteParams &p, const int *counts, cons
         store_task(p.tasks + u, ExpertWeights{}, 0, 0);
 }
 
+// A barrier for LDS data: the wave's LDS accesses complete, then the
+// workgroup meets.  Global stores are not waited for (__syncthreads would
+// wait for them): nothing in the workgroup reads them back.
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+    __builtin_amdgcn_s_barrier();
+}
+
 __device__ inline void small_tables(const RouteParams &p, RouteLds &L) {
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -316,7 +334,7 @@ __device__ inline void small_tables(const RouteParams &p, RouteLds &L) {
         L.first_pos[e] = INT_MAX;
         L.counts[e] = 0;
     }
-    __syncthreads();
+    lds_barrier();
     // first appearance and count per expert (order-independent LDS atomics)
     for (int q = tid; q < n_pos; q += blockDim.x) {
         const int e = L.ids[q];
@@ -328,11 +346,12 @@ __device__ inline void small_tables(const RouteParams &p, RouteLds &L) {
         atomicMin(&L.first_pos[e], q);
         atomicAdd(&L.counts[e], 1);
     }
-    __syncthreads();
+    lds_barrier();
     // first-appearance ranks: a bit per list position that is the first
     // occurrence of its expert; the rank of e counts those bits before it
     const int nwords = (n_pos + 63) / 64;
-    for (int w = wave; w < nwords; w += 4) {
+    const int nwaves = (int)blockDim.x >> 6;
+    for (int w = wave; w < nwords; w += nwaves) {
         const int q = w * 64 + lane;
         bool first = false;
         if (q < n_pos) {
@@ -342,7 +361,7 @@ __device__ inline void small_tables(const RouteParams &p, RouteLds &L) {
         const unsigned long long m = __ballot(first);
         if (lane == 0) L.first_mask[w] = m;
     }
-    __syncthreads();
+    lds_barrier();
     if (wave == 0) {  // word prefix (<= 16 words) by a wave scan
         const int cnt = lane < nwords ? __popcll(L.first_mask[lane]) : 0;
         int incl = cnt;
@@ -358,7 +377,7 @@ __device__ inline void small_tables(const RouteParams &p, RouteLds &L) {
             *p.n_unique = total;
         }
     }
-    __syncthreads();
+    lds_barrier();
     for (int e = tid; e < E; e += blockDim.x) {
         L.rank_of[e] = -1;
         if (L.counts[e] > 0) {
@@ -367,11 +386,12 @@ __device__ inline void small_tables(const RouteParams &p, RouteLds &L) {
                              __popcll(L.first_mask[q / 64] & ((1ull << (q % 64)) - 1ull));
             L.rank_of[e] = rank;
             L.count_by_rank[rank] = L.counts[e];
+            L.unique[rank] = e;
             p.unique[rank] = e;
         }
         p.counts[e] = L.counts[e];
     }
-    __syncthreads();
+    lds_barrier();
     if (wave == 0) {  // exclusive scan of the counts in rank order (<= 256 ranks)
         int c4[4], local = 0;
         const int n_unique = L.unique_total;
@@ -395,17 +415,17 @@ __device__ inline void small_tables(const RouteParams &p, RouteLds &L) {
             run += c4[i];
         }
     }
-    __syncthreads();
+    lds_barrier();
     for (int e = tid; e < E; e += blockDim.x) {
         if (L.rank_of[e] >= 0) {
             L.offsets[e] = L.offset_by_rank[L.rank_of[e]];
             p.offsets[e] = L.offsets[e];
         }
     }
-    __syncthreads();
+    lds_barrier();
     write_tasks(p, L.counts, L.offsets, L.rank_of, L.unique_total);
     // compact lists: entries of expert e in (row, slot) order
-    for (int e = wave; e < E; e += 4) {
+    for (int e = wave; e < E; e += nwaves) {
         if (L.counts[e] == 0) continue;
         int running = 0;
         const int base = L.offsets[e];

@@ -1112,9 +1112,10 @@ int route(MoonlightSession *s, int layer, const float *x, int rows, const float 
     }
     // a few rows on the GEMM path: the first GEMM launch routes them
     if (inline_route && rows <= kRouteOneGroupRows &&
-        rows * r.top_k <= kRouteFusedMaxPositions && r.top_k <= kMaxTopK &&
-        r.experts <= kMaxExperts && moe_uses_gemm(s, layer, rows)) {
+        rows * r.top_k <= kRouteFusedMaxPositions && r.top_k <= kMaxTopK && r.experts <= 64 &&
+        moe_uses_gemm(s, layer, rows)) {
         *inline_route = r;
+        inline_route->tasks = nullptr;  // the GEMM path builds its own task tables
         return kOk;
     }
     return route_topk(r, stream_of(s));
