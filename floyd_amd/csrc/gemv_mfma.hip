@@ -101,13 +101,16 @@ __device__ __forceinline__ int slice_pos(int e) {
 struct MfmaGemvArgs {
     GemvParams p;
     int ndma;  // DMA instructions per wave (selects the instantiation)
+    int rw;    // output rows per workgroup
 };
 
 // ND: DMA instructions per wave (a compile-time count, so that the wait for
-// the x loads issued before them is exact)
-template <int FMT, int B, bool DUAL, int ND>
+// the x loads issued before them is exact); RW: output rows per workgroup
+// (16, or 8 for wide-k matrices with few rows: twice the workgroups, the
+// MFMA's weight columns 8..15 repeat 0..7 and are not stored)
+template <int FMT, int B, bool DUAL, int ND, int RW = kRows>
 struct MgShape {
-    static constexpr int kNr = DUAL ? 2 * kRows : kRows;      // weight rows
+    static constexpr int kNr = DUAL ? 2 * RW : RW;            // weight rows
     static constexpr int kKqb = ND * 1024 / kNr;              // weight bytes per row and wave
     static constexpr int kKq = FMT == kQ8 ? kKqb : 2 * kKqb;  // k elements per wave
     static constexpr int kI = 4 * kKq;
@@ -118,15 +121,15 @@ struct MgShape {
     static constexpr int kSwz = kNch % 16 == 0 ? 15 : kNch % 8 == 0 ? 7 : kNch % 4 == 0 ? 3 : 0;
 };
 
-template <int FMT, int B, bool DUAL, int ND>
+template <int FMT, int B, bool DUAL, int ND, int RW>
 __global__ __launch_bounds__(256) void gemv_mfma_kernel(MfmaGemvArgs a) {
-    using Sh = MgShape<FMT, B, DUAL, ND>;
+    using Sh = MgShape<FMT, B, DUAL, ND, RW>;
     const GemvParams &p = a.p;
     extern __shared__ __attribute__((aligned(16))) unsigned char gm_lds[];
-    __shared__ float red[4][4][2][B][kRows];  // [wave][limb][gate / up][token row][row]
+    __shared__ float red[4][4][2][B][RW];  // [wave][limb][gate / up][token row][row]
     __shared__ float red_ss[4][B];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int row0 = blockIdx.x * kRows;
+    const int row0 = blockIdx.x * RW;
     constexpr int row_bytes = FMT == kQ8 ? Sh::kI : Sh::kI / 2;
     constexpr int kq = Sh::kKq, kqb = Sh::kKqb, xrow = Sh::kXrow, swz = Sh::kSwz;
     const int k0 = wave * kq;
@@ -163,9 +166,9 @@ __global__ __launch_bounds__(256) void gemv_mfma_kernel(MfmaGemvArgs a) {
         const int f = 1024 * d + 16 * lane;
         const int r = f / kqb, c = (f % kqb) >> 4;
         const int logical = c ^ (r & swz);
-        int orow = row0 + (DUAL ? (r & 15) : r);
+        int orow = row0 + (DUAL ? (r & (RW - 1)) : r);
         orow = orow < p.O ? orow : p.O - 1;
-        const uint8_t *base = (DUAL && r >= kRows) ? p.w2 : p.w;
+        const uint8_t *base = (DUAL && r >= RW) ? p.w2 : p.w;
         const uint8_t *src = base + (long)orow * row_bytes + (FMT == kQ8 ? k0 : k0 / 2) + logical * 16;
         __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void *)src,
                                          (__attribute__((address_space(3))) void *)(wl + 1024 * d),
@@ -294,8 +297,9 @@ __global__ __launch_bounds__(256) void gemv_mfma_kernel(MfmaGemvArgs a) {
     const bool a_ok = tb < B;
     const unsigned char *arow = xl + (limb * B + (a_ok ? tb : 0)) * xrow;
     const int n = lane & 15;
-    const unsigned char *wrow = wl + n * kqb;
-    const unsigned char *wrow2 = wl + (kRows + n) * kqb;
+    const int wn = n & (RW - 1);  // weight row of MFMA column n
+    const unsigned char *wrow = wl + wn * kqb;
+    const unsigned char *wrow2 = wl + (RW + wn) * kqb;
     i32x4 acc = {0, 0, 0, 0}, acc2 = {0, 0, 0, 0}, acc1 = {0, 0, 0, 0};
     constexpr int nsteps = kq / 64;
     // steps in groups of 8 (and one group of the rest): the group's LDS
@@ -312,13 +316,13 @@ __global__ __launch_bounds__(256) void gemv_mfma_kernel(MfmaGemvArgs a) {
             av[i] = *reinterpret_cast<const u32x4 *>(arow + 64 * s + 16 * g);
             if constexpr (FMT == kQ8) {
                 const int lc = 4 * s + g;  // logical chunk
-                wv[i] = *reinterpret_cast<const u32x4 *>(wrow + 16 * (lc ^ (n & swz)));
-                if constexpr (DUAL) uv[i] = *reinterpret_cast<const u32x4 *>(wrow2 + 16 * (lc ^ (n & swz)));
+                wv[i] = *reinterpret_cast<const u32x4 *>(wrow + 16 * (lc ^ (wn & swz)));
+                if constexpr (DUAL) uv[i] = *reinterpret_cast<const u32x4 *>(wrow2 + 16 * (lc ^ (wn & swz)));
             } else {
                 const int lc = 2 * s + (g >> 1);  // logical chunk; 8-byte half g & 1
-                wv[i] = *reinterpret_cast<const uint2 *>(wrow + 16 * (lc ^ (n & swz)) + 8 * (g & 1));
+                wv[i] = *reinterpret_cast<const uint2 *>(wrow + 16 * (lc ^ (wn & swz)) + 8 * (g & 1));
                 if constexpr (DUAL)
-                    uv[i] = *reinterpret_cast<const uint2 *>(wrow2 + 16 * (lc ^ (n & swz)) + 8 * (g & 1));
+                    uv[i] = *reinterpret_cast<const uint2 *>(wrow2 + 16 * (lc ^ (wn & swz)) + 8 * (g & 1));
             }
         }
         __builtin_amdgcn_sched_barrier(0);
@@ -357,8 +361,10 @@ __global__ __launch_bounds__(256) void gemv_mfma_kernel(MfmaGemvArgs a) {
             c -= 8 * acc1[b];
             if (DUAL) c2 -= 8 * acc1[b];
         }
-        red[wave][g][0][b][n] = (float)c * limb_w * step[b];
-        if (DUAL) red[wave][g][1][b][n] = (float)c2 * limb_w * step[b];
+        if (n < RW) {
+            red[wave][g][0][b][n] = (float)c * limb_w * step[b];
+            if (DUAL) red[wave][g][1][b][n] = (float)c2 * limb_w * step[b];
+        }
         if (lane == 0) red_ss[wave][b] = ss[b];
     }
     __syncthreads();
@@ -367,7 +373,7 @@ __global__ __launch_bounds__(256) void gemv_mfma_kernel(MfmaGemvArgs a) {
     if (wave != 0 || g >= B) return;
     const int b = g;  // lanes 16 b + n, b < B
     const int row = row0 + n;
-    if (row >= p.O) return;
+    if (n >= RW || row >= p.O) return;
     float inv_rms = 1.0f;
     if (p.norm_w) {
         const float tot = (red_ss[0][b] + red_ss[1][b]) + (red_ss[2][b] + red_ss[3][b]);
@@ -392,9 +398,9 @@ __global__ __launch_bounds__(256) void gemv_mfma_kernel(MfmaGemvArgs a) {
 }
 
 // With `name` set nothing is launched: the kernel's template name is stored.
-template <int FMT, int B, bool DUAL, int ND>
+template <int FMT, int B, bool DUAL, int ND, int RW>
 bool launch_one(const MfmaGemvArgs &a, hipStream_t stream, std::string *name) {
-    using Sh = MgShape<FMT, B, DUAL, ND>;
+    using Sh = MgShape<FMT, B, DUAL, ND, RW>;
     // shapes whose x passes exceed the register budget are not instantiated
     // (the dynamic LDS plus the static reduction arrays within the 160 KB)
     if constexpr (Sh::kPass > (B == 1 ? 6 : B == 2 ? 3 : 2) || 4 * Sh::kWaveLds > 150 * 1024) {
@@ -403,37 +409,48 @@ bool launch_one(const MfmaGemvArgs &a, hipStream_t stream, std::string *name) {
     if (Sh::kI != a.p.I) return false;
     if (name) {
         char buf[96];
-        snprintf(buf, sizeof(buf), "mlh::(anonymous namespace)::gemv_mfma_kernel<%d, %d, %s, %d>",
-                 FMT, B, DUAL ? "true" : "false", ND);
+        snprintf(buf, sizeof(buf), "mlh::(anonymous namespace)::gemv_mfma_kernel<%d, %d, %s, %d, %d>",
+                 FMT, B, DUAL ? "true" : "false", ND, RW);
         *name = buf;
         return true;
     }
     constexpr int lds = 4 * Sh::kWaveLds;
     static const bool attr = [] {
         if (lds <= 64 * 1024) return true;
-        if (hipFuncSetAttribute(reinterpret_cast<const void *>(&gemv_mfma_kernel<FMT, B, DUAL, ND>),
+        if (hipFuncSetAttribute(reinterpret_cast<const void *>(&gemv_mfma_kernel<FMT, B, DUAL, ND, RW>),
                                 hipFuncAttributeMaxDynamicSharedMemorySize, lds) == hipSuccess)
             return true;
         (void)hipGetLastError();  // not sticky: the caller falls back
         return false;
     }();
     if (!attr) return false;
-    hipLaunchKernelGGL((gemv_mfma_kernel<FMT, B, DUAL, ND>), dim3((a.p.O + kRows - 1) / kRows),
+    hipLaunchKernelGGL((gemv_mfma_kernel<FMT, B, DUAL, ND, RW>), dim3((a.p.O + RW - 1) / RW),
                        dim3(256), lds, stream, a);
     return true;
     }
 }
 
 // DMA counts of the Moonlight shapes: 16 or 32 rows x (I / 4) weight bytes
-// per wave, I = 2048 or 11264
+// per wave, I = 2048 or 11264; 8 rows at I = 11264
 template <int FMT, int B, bool DUAL>
 bool launch_nd(const MfmaGemvArgs &a, hipStream_t stream, std::string *name) {
+    if (a.rw == 8) {
+        if constexpr (DUAL || B != 1) {
+            return false;
+        } else {
+            switch (a.ndma) {
+            case 11: return launch_one<FMT, B, DUAL, 11, 8>(a, stream, name);
+            case 22: return launch_one<FMT, B, DUAL, 22, 8>(a, stream, name);
+            default: return false;
+            }
+        }
+    }
     switch (a.ndma) {
-    case 4: return launch_one<FMT, B, DUAL, 4>(a, stream, name);
-    case 8: return launch_one<FMT, B, DUAL, 8>(a, stream, name);
-    case 16: return launch_one<FMT, B, DUAL, 16>(a, stream, name);
-    case 22: return launch_one<FMT, B, DUAL, 22>(a, stream, name);
-    case 44: return launch_one<FMT, B, DUAL, 44>(a, stream, name);
+    case 4: return launch_one<FMT, B, DUAL, 4, kRows>(a, stream, name);
+    case 8: return launch_one<FMT, B, DUAL, 8, kRows>(a, stream, name);
+    case 16: return launch_one<FMT, B, DUAL, 16, kRows>(a, stream, name);
+    case 22: return launch_one<FMT, B, DUAL, 22, kRows>(a, stream, name);
+    case 44: return launch_one<FMT, B, DUAL, 44, kRows>(a, stream, name);
     default: return false;
     }
 }
@@ -455,15 +472,17 @@ bool launch_b(const MfmaGemvArgs &a, hipStream_t stream, std::string *name) {
 // x); returns false, launching nothing, otherwise.  Measured on MI355X
 // against the vector kernel (gemv_impl.h), graph replays: q4 11264 x 2048
 // 5.27 against 5.95 us, q8 3648 x 2048 4.16 against 4.72 us, q8 11264 x 2048
-// at 4 rows 9.9 against 12.7 us; wide-k matrices with few rows (2048 x
-// 11264: 128 workgroups) stay on the vector kernel.  With `name` set it
+// at 4 rows 9.9 against 12.7 us.  Wide-k matrices with few rows (2048 x
+// 11264) take 8-row workgroups at one token row (256 workgroups rather than
+// 128), else the vector kernel.  With `name` set it
 // launches nothing and stores the template name of the kernel it would
 // launch (operand alignment not checked).
 bool gemv_mfma(const GemvParams &p, hipStream_t stream, std::string *name) {
     if ((p.fmt != kQ8 && p.fmt != kQ4) || p.rows < 1 || p.rows > 4 || p.rows == 3 || p.limbs)
         return false;
-    if (p.O < 4096 && p.I > 4096) return false;
     const bool dual = p.epilogue == kEpiSiluDual;
+    const int rw = p.O < 4096 && p.I > 4096 ? 8 : kRows;
+    if (rw == 8 && (dual || p.rows != 1)) return false;
     const int max_pass = p.rows == 1 ? 6 : p.rows == 2 ? 3 : 2;
     if (p.I % (p.fmt == kQ8 ? 256 : 512) || p.I / 4 > max_pass * 512) return false;
     auto al = [](const void *q) { return ((uintptr_t)q & 15u) == 0; };
@@ -473,7 +492,8 @@ bool gemv_mfma(const GemvParams &p, hipStream_t stream, std::string *name) {
     MfmaGemvArgs a;
     a.p = p;
     const int kqb = p.fmt == kQ8 ? p.I / 4 : p.I / 8;  // weight bytes per row and wave
-    a.ndma = (dual ? 2 * kRows : kRows) * kqb / 1024;
+    a.rw = rw;
+    a.ndma = (dual ? 2 * rw : rw) * kqb / 1024;
     return dual ? (p.fmt == kQ8 ? launch_b<kQ8, true>(a, stream, name)
                                 : launch_b<kQ4, true>(a, stream, name))
                 : (p.fmt == kQ8 ? launch_b<kQ8, false>(a, stream, name)
