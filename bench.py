@@ -295,9 +295,10 @@ def moe_only(sizes=None):
     `sizes` (profiler runs)."""
     from floyd_amd import session as S
     model = S.Model.synthetic()
-    sess = S.Session(model, 128, 64)
+    rows_list = sizes or (1, 8, 64)
+    sess = S.Session(model, max(128, max(rows_list)), max(64, max(rows_list)))
     out = {}
-    for rows in sizes or (1, 8, 64):
+    for rows in rows_list:
         us, uniq = sess.time_moe(1, rows, seed=rows, warmup=5, iters=20)
         out[f"T{rows}"] = {"us": round(us, 2), "unique_experts": uniq}
         print(f"[bench] MoE layer T={rows}: {us:.1f} us, U={uniq}", file=sys.stderr, flush=True)
