@@ -397,6 +397,241 @@ __global__ __launch_bounds__(256) void gemv_mfma_kernel(MfmaGemvArgs a) {
     yb[row] = out;
 }
 
+
+// Weights straight into registers in the MFMA B layout, for matrices whose
+// wave k quarter (KQ elements) fits in registers: no LDS copy of the weights
+// (the LDS traffic of the DMA kernel's product phase is shared by every
+// workgroup of a CU), and no LDS DMA, so every load is an ordinary one the
+// compiler waits for where its registers are used.  Lane (g, n) loads weight
+// row row0 + n in 16-byte pieces: q8 piece s = k bytes 64 s + 16 g (MFMA
+// step s), q4 piece j = bytes 64 j + 16 g (steps 2 j and 2 j + 1, one 8-byte
+// half each), so a wave instruction reads 64 contiguous bytes of each of 16
+// rows; the limb rows are read at the same k positions.
+template <int FMT, int B, bool DUAL, int KQ>
+__global__ __launch_bounds__(256) void gemv_mfma_direct_kernel(GemvParams p) {
+    constexpr int S = KQ / 64;                  // MFMA steps per wave
+    constexpr int NW = FMT == kQ8 ? S : S / 2;  // 16-byte weight pieces per lane and matrix
+    constexpr int kPass = (KQ + 511) / 512;
+    constexpr int xrow = KQ + kXPad;
+    __shared__ __attribute__((aligned(16))) unsigned char xl_all[4][4 * B * xrow];
+    __shared__ float red[4][4][2][B][kRows];  // [wave][limb][gate / up][token row][row]
+    __shared__ float red_ss[4][B];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int row0 = blockIdx.x * kRows;
+    const int k0 = wave * KQ;
+    const long row_bytes = FMT == kQ8 ? p.I : p.I / 2;
+    unsigned char *xl = xl_all[wave];
+    const int n = lane & 15, g = lane >> 4;
+
+    // ---- x of this wave's quarter (and norm_w), then the weights, then
+    // the epilogue's operands: in-order completion lets the split start
+    // while the weights are still in flight
+    const bool has_norm = p.norm_w != nullptr;
+    const float *nw = has_norm ? p.norm_w : p.x;
+    f32x4 xv[kPass][B][2];
+    f32x4 nv[kPass][2];
+#pragma unroll
+    for (int j = 0; j < kPass; ++j) {
+        const int e = j * 512 + lane * 8;
+        const int ec = e < KQ ? e : 0;
+#pragma unroll
+        for (int b = 0; b < B; ++b) {
+            const float *xb = p.x + (long)b * p.x_stride + k0 + ec;
+            xv[j][b][0] = load_f4(xb);
+            xv[j][b][1] = load_f4(xb + 4);
+        }
+        nv[j][0] = load_f4(nw + k0 + ec);
+        nv[j][1] = load_f4(nw + k0 + ec + 4);
+    }
+    const int wr_row = row0 + n < p.O ? row0 + n : p.O - 1;
+    const long w_off = (long)wr_row * row_bytes + (FMT == kQ8 ? k0 : k0 / 2) + 16 * g;
+    u32x4 wv[NW], uv[DUAL ? NW : 1];
+#pragma unroll
+    for (int i = 0; i < NW; ++i) {
+        wv[i] = load_global16(p.w + w_off + 64 * i);
+        if constexpr (DUAL) uv[i] = load_global16(p.w2 + w_off + 64 * i);
+    }
+    const int eb = g < B ? g : 0;
+    const bool has_res = p.epilogue == kEpiResidual;
+    const float e_s = p.s[wr_row];
+    const float e_s2 = DUAL ? p.s2[wr_row] : 0.0f;
+    const float e_res = has_res ? p.resid[(long)eb * p.resid_stride + wr_row] : 0.0f;
+
+    // ---- split x into limbs (as gemv_mfma_kernel) and store the limb rows
+    float ss[B], amax[B];
+#pragma unroll
+    for (int b = 0; b < B; ++b) {
+        ss[b] = 0.0f;
+        amax[b] = 0.0f;
+    }
+#pragma unroll
+    for (int j = 0; j < kPass; ++j) {
+        if (j * 512 + lane * 8 < KQ) {
+#pragma unroll
+            for (int b = 0; b < B; ++b) {
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    f32x4 v = xv[j][b][h];
+                    ss[b] += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+                    if (has_norm) {
+                        v.x *= nv[j][h].x;
+                        v.y *= nv[j][h].y;
+                        v.z *= nv[j][h].z;
+                        v.w *= nv[j][h].w;
+                    }
+                    xv[j][b][h] = v;
+                    amax[b] = fmaxf(amax[b], fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)),
+                                                   fmaxf(fabsf(v.z), fabsf(v.w))));
+                }
+            }
+        }
+    }
+    float step_inv[B], step[B];
+#pragma unroll
+    for (int b = 0; b < B; ++b) {
+        amax[b] = dpp_wave_max(amax[b]);
+        ss[b] = dpp_wave_sum(ss[b]);
+        int e2 = 0;
+        (void)frexpf(amax[b], &e2);  // amax < 2^e2
+        const int ex = amax[b] > 0.0f ? 30 - e2 : 0;
+        step_inv[b] = ldexpf(1.0f, ex);
+        step[b] = ldexpf(1.0f, -ex);
+    }
+#pragma unroll
+    for (int j = 0; j < kPass; ++j) {
+        const int e = j * 512 + lane * 8;
+        if (e < KQ) {
+#pragma unroll
+            for (int b = 0; b < B; ++b) {
+                const float v8[8] = {xv[j][b][0].x, xv[j][b][0].y, xv[j][b][0].z, xv[j][b][0].w,
+                                     xv[j][b][1].x, xv[j][b][1].y, xv[j][b][1].z, xv[j][b][1].w};
+                unsigned lw[4][2] = {{0u, 0u}, {0u, 0u}, {0u, 0u}, {0u, 0u}};
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    const int q = (int)rintf(v8[i] * step_inv[b]);
+                    const int l3 = (int)(signed char)(q & 255);
+                    int r = (q - l3) >> 8;
+                    const int l2 = (int)(signed char)(r & 255);
+                    r = (r - l2) >> 8;
+                    const int l1 = (int)(signed char)(r & 255);
+                    const int l0 = (r - l1) >> 8;
+                    const int pos = slice_pos<FMT>(i);
+                    const int wd = pos >> 2, sh = 8 * (pos & 3);
+                    lw[0][wd] |= (unsigned)(l0 & 255) << sh;
+                    lw[1][wd] |= (unsigned)(l1 & 255) << sh;
+                    lw[2][wd] |= (unsigned)(l2 & 255) << sh;
+                    lw[3][wd] |= (unsigned)(l3 & 255) << sh;
+                }
+#pragma unroll
+                for (int L = 0; L < 4; ++L)
+                    *reinterpret_cast<uint2 *>(xl + (L * B + b) * xrow + e) = uint2{lw[L][0], lw[L][1]};
+            }
+        }
+    }
+    // (a wave reads only its own limb rows: its LDS stores complete in order
+    // before its reads below)
+
+    // ---- MFMA steps: A row m = 4 L + b from LDS, B column n from registers
+    const int m = lane & 15;
+    const int limb = m >> 2, tb = m & 3;
+    const bool a_ok = tb < B;
+    const unsigned char *arow = xl + (limb * B + (a_ok ? tb : 0)) * xrow;
+    i32x4 acc = {0, 0, 0, 0}, acc2 = {0, 0, 0, 0}, acc1 = {0, 0, 0, 0};
+    const i32x4 ones = {0x01010101, 0x01010101, 0x01010101, 0x01010101};
+    u32x4 av[S];
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+        const int aoff = FMT == kQ8 ? 64 * s + 16 * g : 128 * (s >> 1) + 32 * g + 16 * (s & 1);
+        av[s] = *reinterpret_cast<const u32x4 *>(arow + aoff);
+    }
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+        const i32x4 A = a_ok ? i32x4{(int)av[s].x, (int)av[s].y, (int)av[s].z, (int)av[s].w}
+                             : i32x4{0, 0, 0, 0};
+        i32x4 Bw, Bu;
+        if constexpr (FMT == kQ8) {
+            Bw = i32x4{(int)wv[s].x, (int)wv[s].y, (int)wv[s].z, (int)wv[s].w};
+            if constexpr (DUAL) Bu = i32x4{(int)uv[s].x, (int)uv[s].y, (int)uv[s].z, (int)uv[s].w};
+        } else {
+            const u32x4 w4 = wv[s >> 1];
+            const unsigned wx = (s & 1) ? w4.z : w4.x, wy = (s & 1) ? w4.w : w4.y;
+            Bw = i32x4{(int)(wx & 0x0F0F0F0Fu), (int)((wx >> 4) & 0x0F0F0F0Fu),
+                       (int)(wy & 0x0F0F0F0Fu), (int)((wy >> 4) & 0x0F0F0F0Fu)};
+            if constexpr (DUAL) {
+                const u32x4 u4 = uv[s >> 1];
+                const unsigned ux = (s & 1) ? u4.z : u4.x, uy = (s & 1) ? u4.w : u4.y;
+                Bu = i32x4{(int)(ux & 0x0F0F0F0Fu), (int)((ux >> 4) & 0x0F0F0F0Fu),
+                           (int)(uy & 0x0F0F0F0Fu), (int)((uy >> 4) & 0x0F0F0F0Fu)};
+            }
+            acc1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A, ones, acc1, 0, 0, 0);
+        }
+        acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(A, Bw, acc, 0, 0, 0);
+        if constexpr (DUAL) acc2 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A, Bu, acc2, 0, 0, 0);
+    }
+    // ---- limbs combined, the four waves' shares in LDS, the epilogue
+    const float limb_w = g == 0 ? 16777216.0f : g == 1 ? 65536.0f : g == 2 ? 256.0f : 1.0f;
+#pragma unroll
+    for (int b = 0; b < B; ++b) {
+        int c = acc[b], c2 = DUAL ? acc2[b] : 0;
+        if constexpr (FMT == kQ4) {
+            c -= 8 * acc1[b];
+            if (DUAL) c2 -= 8 * acc1[b];
+        }
+        red[wave][g][0][b][n] = (float)c * limb_w * step[b];
+        if (DUAL) red[wave][g][1][b][n] = (float)c2 * limb_w * step[b];
+        if (lane == 0) red_ss[wave][b] = ss[b];
+    }
+    __syncthreads();
+    if (wave != 0 || g >= B) return;
+    const int b = g;
+    const int row = row0 + n;
+    if (row >= p.O) return;
+    float inv_rms = 1.0f;
+    if (p.norm_w) {
+        const float tot = (red_ss[0][b] + red_ss[1][b]) + (red_ss[2][b] + red_ss[3][b]);
+        inv_rms = 1.0f / sqrtf(tot / (float)p.I + p.eps);
+    }
+    auto total = [&](int u) {
+        float w4[4];
+#pragma unroll
+        for (int w = 0; w < 4; ++w)
+            w4[w] = (red[w][0][u][b][n] + red[w][1][u][b][n]) + (red[w][2][u][b][n] + red[w][3][u][b][n]);
+        return ((w4[0] + w4[1]) + (w4[2] + w4[3])) * inv_rms;
+    };
+    const float sum = total(0);
+    float *yb = p.y + (long)b * p.y_stride;
+    if (DUAL) {
+        yb[row] = silu(sum * e_s) * (total(1) * e_s2);
+        return;
+    }
+    float out = sum * e_s;
+    if (has_res) out = e_res + out;
+    yb[row] = out;
+}
+
+template <int FMT, int B, bool DUAL, int KQ>
+bool launch_direct(const GemvParams &p, hipStream_t stream, std::string *name) {
+    if (name) {
+        char buf[96];
+        snprintf(buf, sizeof(buf), "mlh::(anonymous namespace)::gemv_mfma_direct_kernel<%d, %d, %s, %d>",
+                 FMT, B, DUAL ? "true" : "false", KQ);
+        *name = buf;
+        return true;
+    }
+    hipLaunchKernelGGL((gemv_mfma_direct_kernel<FMT, B, DUAL, KQ>), dim3((p.O + kRows - 1) / kRows),
+                       dim3(256), 0, stream, p);
+    return true;
+}
+template <int FMT, bool DUAL>
+bool launch_direct_b(const GemvParams &p, hipStream_t stream, std::string *name) {
+    switch (p.rows) {
+    case 1: return launch_direct<FMT, 1, DUAL, 512>(p, stream, name);
+    case 2: return launch_direct<FMT, 2, DUAL, 512>(p, stream, name);
+    case 4: return launch_direct<FMT, 4, DUAL, 512>(p, stream, name);
+    default: return false;
+    }
+}
+
 // With `name` set nothing is launched: the kernel's template name is stored.
 template <int FMT, int B, bool DUAL, int ND, int RW>
 bool launch_one(const MfmaGemvArgs &a, hipStream_t stream, std::string *name) {
@@ -489,6 +724,15 @@ bool gemv_mfma(const GemvParams &p, hipStream_t stream, std::string *name) {
     if (!name && (!al(p.w) || (dual && !al(p.w2)) || !al(p.x) || p.x_stride % 4 ||
                   (p.norm_w && !al(p.norm_w))))
         return false;
+    // k quarters of 512: weights straight into registers, except q8 at one
+    // token row (measured on MI355X, graph replays: q4 11264 x 2048 5.27 ->
+    // 5.21 us, q8 at 4 rows 9.3 -> 8.6 us median, q8 at one row 6.43 -> 6.60
+    // us, so that stays on the DMA kernel)
+    if (p.I == 2048 && rw == kRows && !(p.fmt == kQ8 && p.rows == 1))
+        return dual ? (p.fmt == kQ8 ? launch_direct_b<kQ8, true>(p, stream, name)
+                                    : launch_direct_b<kQ4, true>(p, stream, name))
+                    : (p.fmt == kQ8 ? launch_direct_b<kQ8, false>(p, stream, name)
+                                    : launch_direct_b<kQ4, false>(p, stream, name));
     MfmaGemvArgs a;
     a.p = p;
     const int kqb = p.fmt == kQ8 ? p.I / 4 : p.I / 8;  // weight bytes per row and wave
