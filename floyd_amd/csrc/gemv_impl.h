@@ -865,6 +865,7 @@ __global__ __launch_bounds__(W * 64) void gemv_kernel(GemvLaunch L) {
         run_job<MODE, FMT, B, KT, LPR, R, KS, W>(job, gemv_lds);
     } else {
         const ExpertGemvParams &p = L.expert;
+        __shared__ __align__(16) unsigned long long route_keys[W][64];
         // flat grid: routed task t owns workgroups t * routed_blocks ..,
         // the shared expert the ones after them (no idle workgroups)
         const int routed_wgs = p.routed_tasks * p.routed_blocks;
@@ -886,9 +887,10 @@ __global__ __launch_bounds__(W * 64) void gemv_kernel(GemvLaunch L) {
             if (p.route.logits) {
                 // one token row: the tables for the later launches, then this
                 // workgroup's own selection (every wave, no barrier)
-                if (blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x < 64)
-                    route_single_64(p.route, threadIdx.x);
-                if (inline_task_expert(p.route, task, &ew) < 0) return;
+                const int wave = threadIdx.x >> 6;
+                if (blockIdx.x == 0 && blockIdx.y == 0 && wave == 0)
+                    route_single_64(p.route, threadIdx.x, route_keys[0]);
+                if (inline_task_expert(p.route, task, &ew, route_keys[wave]) < 0) return;
                 n = 1;
                 off = task;
             } else if (p.tasks) {

@@ -3,6 +3,7 @@
 #include "device_context.h"
 #include "mlh_host.h"
 #include "../../include/moonlight_kernels.h"
+#include "moe.h"
 
 #include <mutex>
 #include <vector>
@@ -307,6 +308,42 @@ int mlk_time_read(void *const *src, int n_buffers, size_t bytes, int blocks, uns
     if (sync) return sync;
     *avg_us = (double)ms * 1000.0 / iters;
     return kOk;
+}
+
+int mlk_route_topk(const float *logits, const float *bias, int rows, int experts, int top_k,
+                   int normalize, float routed_scale, int *ids, float *weights) {
+    hipStream_t st = lib_stream();
+    if (!st) return kErrDevice;
+    if (!logits || !bias || !ids || !weights || rows <= 0 || experts <= 0 || top_k <= 0)
+        return finish(kErrArgs, "mlk_route_topk");
+    // the route tables the kernels also write, in one scratch allocation
+    const size_t pos = (size_t)rows * top_k;
+    const size_t n_int = 2 + 3 * (size_t)experts + 3 * pos;
+    int *tab = nullptr;
+    if (int e = check_hip(hipMalloc(&tab, n_int * sizeof(int)), "mlk_route_topk")) return e;
+    RouteParams p;
+    p.logits = logits;
+    p.bias = bias;
+    p.rows = rows;
+    p.experts = experts;
+    p.top_k = top_k;
+    p.normalize = normalize;
+    p.routed_scale = routed_scale;
+    p.ids = ids;
+    p.weights = weights;
+    p.n_unique = tab;
+    p.error = tab + 1;
+    p.unique = tab + 2;
+    p.counts = p.unique + experts;
+    p.offsets = p.counts + experts;
+    p.list_rows = p.offsets + experts;
+    p.list_slots = p.list_rows + pos;
+    p.list_pos = p.list_slots + pos;
+    int status = check_hip(hipMemsetAsync(tab, 0, n_int * sizeof(int), st), "mlk_route_topk");
+    if (status == kOk) status = finish(route_topk(p, st), "mlk_route_topk");
+    const int sync = check_hip(hipStreamSynchronize(st), "mlk_route_topk");
+    (void)hipFree(tab);
+    return status != kOk ? status : sync;
 }
 
 int mlk_quantize(int bits, const float *w, int rows, int cols, uint8_t *q, float *s) {

@@ -24,12 +24,13 @@ constexpr int kRouteLdsIds = 4096;
 // batches whose logits already exist).
 __global__ __launch_bounds__(256) void route_kernel(RouteParams p) {
     __shared__ RouteLds L;
+    __shared__ __align__(16) unsigned long long keys[4][64];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     if (p.rows == 1 && p.experts <= 64) {
-        if (wave == 0) route_single_64(p, lane);
+        if (wave == 0) route_single_64(p, lane, keys[0]);
         return;
     }
-    for (int r = wave; r < p.rows; r += 4) route_any(p, r, lane, L.ids);
+    for (int r = wave; r < p.rows; r += 4) route_any(p, r, lane, L.ids, keys[wave]);
     __syncthreads();
     small_tables(p, L);
 }
@@ -37,8 +38,9 @@ __global__ __launch_bounds__(256) void route_kernel(RouteParams p) {
 // Larger batches: one wave per token row over many workgroups; the tables
 // follow in route_lists_kernel.
 __global__ __launch_bounds__(256) void route_select_kernel(RouteParams p) {
+    __shared__ __align__(16) unsigned long long keys[4][64];
     const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (r < p.rows) route_any(p, r, threadIdx.x & 63, nullptr);
+    if (r < p.rows) route_any(p, r, threadIdx.x & 63, nullptr, keys[threadIdx.x >> 6]);
 }
 
 // Route tables of a batch of more than a few rows (prepare_route_tables,

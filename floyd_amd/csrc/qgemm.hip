@@ -1162,10 +1162,11 @@ __global__ __launch_bounds__(64 * kPrepWaves) void moe_prep_kernel(QuantSeg a, M
             // meanwhile
             __shared__ RouteLds L;
             __shared__ ExpertWeights ew[64];
+            __shared__ __align__(16) unsigned long long keys[kPrepWaves][64];
             const RouteParams &rp = sp.p.route;  // rows <= kPrepWaves, experts <= 64
             const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
             if (wave == 0 && lane < rp.experts) ew[lane] = sp.p.expert_table[lane];
-            if (wave < rp.rows) (void)select_row_64(rp, wave, lane, L.ids);
+            if (wave < rp.rows) (void)select_row_64(rp, wave, lane, L.ids, keys[wave]);
             lds_barrier();
             small_tables(rp, L);
             lds_barrier();

@@ -45,26 +45,59 @@ __device__ __forceinline__ void store_task(ExpertTask *t, const ExpertWeights &w
 // experts with sel > -inf can be taken (NaN never compares greater), as in
 // the arg-max.  With WRITE, writes ids / weights / trace (and lds_ids);
 // returns the slot of this lane's expert (-1: not taken) and the mask of
-// filled slots.
+// filled slots.  `keys` is the calling wave's own 64-entry LDS scratch
+// (16-byte aligned).
 struct RowSelection {
     int slot;
     unsigned long long filled;  // bit k: slot k holds a valid expert
 };
 
+// The rank above for every lane of a wave at once.  Each lane publishes a
+// 64-bit key that is unique in the wave: the order-preserving bit pattern of
+// its selection score (sign flipped for positive scores, all bits inverted
+// for negative ones, so unsigned order is float order) above 63 - lane, so
+// that of two equal scores the lower lane has the larger key.  rank(e) is
+// then the number of keys above e's: 64 compares against keys read back as
+// LDS broadcasts.  A lane that cannot be taken (score -inf or NaN) publishes
+// 0, below every live key, so it outranks no lane.
+__device__ __forceinline__ int wave_rank_desc(float sel, bool live, int lane,
+                                              unsigned long long *keys) {
+    const unsigned u = __float_as_uint(sel);
+    const unsigned ord = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    const unsigned long long key =
+        live ? ((unsigned long long)ord << 32) | (unsigned)(63 - lane) : 0ull;
+    keys[lane] = key;
+    // the wave's own LDS accesses complete in issue order: the loads below
+    // see every lane's store
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    int ra = 0, rb = 0;
+#pragma unroll
+    for (int o = 0; o < 64; o += 4) {
+        const ulonglong2 k0 = *reinterpret_cast<const ulonglong2 *>(keys + o);
+        const ulonglong2 k1 = *reinterpret_cast<const ulonglong2 *>(keys + o + 2);
+        ra += (k0.x > key) + (k0.y > key);
+        rb += (k1.x > key) + (k1.y > key);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    return ra + rb;
+}
+
 template <bool WRITE = true>
 __device__ __forceinline__ RowSelection select_row_64_v(const RouteParams &p, int r, int lane,
-                                                       int *lds_ids, float logit, float bias);
+                                                       int *lds_ids, float logit, float bias,
+                                                       unsigned long long *keys);
 template <bool WRITE = true>
 __device__ __forceinline__ RowSelection select_row_64(const RouteParams &p, int r, int lane,
-                                                     int *lds_ids) {
+                                                     int *lds_ids, unsigned long long *keys) {
     const bool have = lane < p.experts;
     return select_row_64_v<WRITE>(p, r, lane, lds_ids, have ? p.logits[(long)r * p.experts + lane] : 0.0f,
-                                  have ? p.bias[lane] : 0.0f);
+                                  have ? p.bias[lane] : 0.0f, keys);
 }
 // The same with this lane's logit and bias already loaded.
 template <bool WRITE>
 __device__ __forceinline__ RowSelection select_row_64_v(const RouteParams &p, int r, int lane,
-                                                       int *lds_ids, float logit, float bias) {
+                                                       int *lds_ids, float logit, float bias,
+                                                       unsigned long long *keys) {
     const int E = p.experts, K = p.top_k;
     const bool have = lane < E;
     const float score = have ? sigmoid_exact(logit) : 0.0f;
@@ -73,15 +106,10 @@ __device__ __forceinline__ RowSelection select_row_64_v(const RouteParams &p, in
     if (p.fixed_ids) {
         for (int k = 0; k < K; ++k)
             if (p.fixed_ids[(long)r * K + k] == lane) rs.slot = k;
-    } else if (sel > -INFINITY) {
-        const int sel_bits = __float_as_int(sel);
-        int rank = 0;
-#pragma unroll 8
-        for (int o = 0; o < 64; ++o) {
-            const float so = __int_as_float(__builtin_amdgcn_readlane(sel_bits, o));
-            rank += (so > sel) || (so == sel && o < lane);
-        }
-        if (rank < K) rs.slot = rank;
+    } else {
+        const bool live = sel > -INFINITY;
+        const int rank = wave_rank_desc(sel, live, lane, keys);
+        if (live && rank < K) rs.slot = rank;
     }
     // slot k -> expert; weights summed in slot order (moe_route_finalize)
     int my_id = -1;
@@ -119,12 +147,13 @@ __device__ __forceinline__ RowSelection select_row_64_v(const RouteParams &p, in
 // With one row and distinct experts the tables are direct: expert e in slot k
 // is the u-th taken expert (u = k unless a fixed id was invalid), with one
 // list entry at offset u.
-__device__ __forceinline__ void route_single_64(const RouteParams &p, int lane) {
+__device__ __forceinline__ void route_single_64(const RouteParams &p, int lane,
+                                                unsigned long long *keys) {
     const int E = p.experts, K = p.top_k;
     const bool have = lane < E;
     ExpertWeights ew{};
     if (p.tasks && have) ew = p.expert_table[lane];  // in flight with the logits
-    const RowSelection rs = select_row_64(p, 0, lane, nullptr);
+    const RowSelection rs = select_row_64(p, 0, lane, nullptr, keys);
     const int slot = rs.slot;
     if (lane < K && !((rs.filled >> lane) & 1ull)) {
         p.list_pos[lane] = -1;
@@ -153,11 +182,11 @@ __device__ __forceinline__ void route_single_64(const RouteParams &p, int lane) 
 // Every lane loads its expert's table entry alongside the logits, so the
 // weights need no dependent load.  Called by whole waves.
 __device__ __forceinline__ int inline_task_expert(const RouteParams &p, int task,
-                                                  ExpertWeights *ew) {
+                                                  ExpertWeights *ew, unsigned long long *keys) {
     const int lane = threadIdx.x & 63;
     ExpertWeights mine{};
     if (lane < p.experts) mine = p.expert_table[lane];
-    const RowSelection rs = select_row_64<false>(p, 0, lane, nullptr);
+    const RowSelection rs = select_row_64<false>(p, 0, lane, nullptr, keys);
     const int u = rs.slot >= 0 ? __popcll(rs.filled & ((1ull << rs.slot) - 1ull)) : -1;
     const unsigned long long m = __ballot(u == task);
     if (!m) return -1;
@@ -278,9 +307,10 @@ __device__ inline void route_row(const RouteParams &p, int r, int lane, int *lds
 }
 
 // Any expert count: the rank form for up to 64 experts, else the arg-max scan.
-__device__ inline void route_any(const RouteParams &p, int r, int lane, int *lds_ids) {
+__device__ inline void route_any(const RouteParams &p, int r, int lane, int *lds_ids,
+                                 unsigned long long *keys) {
     if (p.experts <= 64)
-        (void)select_row_64(p, r, lane, lds_ids);
+        (void)select_row_64(p, r, lane, lds_ids, keys);
     else
         route_row(p, r, lane, lds_ids);
 }

@@ -127,7 +127,7 @@ struct MoonlightSession {
     float *shared_hidden = nullptr, *shared_out = nullptr, *dense_hidden = nullptr;
     float *shared_out2 = nullptr;  // second k half of the GEMM path's shared down
     float *moe_routed = nullptr;  // routed part of moonlight_test_moe
-    // MFMA path for batches of >= kMoeGemmMinRows token rows (prefill)
+    // MFMA path for batches of >= moe_gemm_min_rows() token rows
     // quantised activations: three limb planes [3][max_batch][aq_width]
     int8_t *aq = nullptr;
     long aq_plane = 0;
@@ -885,13 +885,22 @@ bool to_host(MoonlightSession *s, void *dst, const void *src, size_t bytes) {
 
 // Batches of at least this many token rows take the int8-MFMA GEMM (weights
 // read once per 32 or 128 rows) instead of the GEMV (once per 4 rows).  The
-// MoE layer switches earlier: its GEMV reads each active expert once per 4
-// of that expert's rows in separate launches per stage, while the grouped
-// GEMM covers all experts in one launch per stage (measured on MI355X at
-// T = 4 .. 7: equal at 4, 96 against 112 us at 5, 106 against 129 us at 7).
-// The dense projections keep the GEMV up to 16 rows.
+// MoE layer switches at 3 rows: the grouped GEMM streams each active
+// expert once for all its rows in one launch per stage, with the routing in
+// its first launch, while the grouped GEMV runs a routing launch, two stage
+// launches and a combine (measured on MI355X, whole layer: equal at T = 2,
+// 53.5 us; 58 against 74 us at T = 3, 64 against 92 us at T = 4).  The
+// dense projections keep the GEMV up to 16 rows.
 constexpr int kGemmMinRows = 16;
-constexpr int kMoeGemmMinRows = 5;
+// MLH_MOE_GEMM_MIN_ROWS overrides the MoE switch (read once, at least 2).
+static int moe_gemm_min_rows() {
+    static const int v = [] {
+        const char *env = getenv("MLH_MOE_GEMM_MIN_ROWS");
+        const int n = env ? atoi(env) : 3;
+        return n < 2 ? 2 : n;
+    }();
+    return v;
+}
 
 bool use_gemm(const MoonlightSession *s, int fmt, int rows, int in_w) {
     return rows >= kGemmMinRows && s->aq && in_w <= s->aq_width && qgemm_shape_ok(fmt, in_w);
@@ -1062,7 +1071,7 @@ static bool moe_uses_gemm(const MoonlightSession *s, int layer, int rows) {
     const ModelConfig &c = s->model->cfg;
     const LayerPlan &lp = s->model->layers[layer];
     const int sw = c.moe_intermediate_size * c.shared_expert_count;
-    return rows >= kMoeGemmMinRows && s->hq && qgemm_shape_ok(lp.expert_fmt, c.hidden_size) &&
+    return rows >= moe_gemm_min_rows() && s->hq && qgemm_shape_ok(lp.expert_fmt, c.hidden_size) &&
            qgemm_shape_ok(lp.expert_fmt, c.moe_intermediate_size) &&
            qgemm_shape_ok(lp.sh_gate.fmt, c.hidden_size) && qgemm_shape_ok(lp.sh_gate.fmt, sw) &&
            c.hidden_size <= s->aq_width && sw <= s->aq_width;
@@ -1538,7 +1547,7 @@ extern "C" int moonlight_session_create(MoonlightSession **out, MoonlightModel *
                       hipHostMallocDefault) == hipSuccess &&
         hipEventCreate(&s->ev_start) == hipSuccess && hipEventCreate(&s->ev_stop) == hipSuccess;
     bool gemm_ok = ok;
-    if (ok && options->max_batch >= kMoeGemmMinRows) {
+    if (ok && options->max_batch >= moe_gemm_min_rows()) {
         // MFMA prefill scratch: quantised activations of the widest matmul
         // input, quantised expert hidden rows, per-stage task tables
         const int widths[] = {c.hidden_size, c.head_count * c.value_dim,

@@ -48,6 +48,8 @@ SIGNATURES = {
                                  _c.c_int, _c.c_int, _c.POINTER(_c.c_double)]),
     "mlk_time_read": (_c.c_int, [_c.POINTER(_vp), _c.c_int, _c.c_size_t, _c.c_int, _vp,
                                  _c.c_int, _c.c_int, _c.POINTER(_c.c_double)]),
+    "mlk_route_topk": (_c.c_int, [_vp, _vp, _c.c_int, _c.c_int, _c.c_int, _c.c_int,
+                                  _c.c_float, _vp, _vp]),
     "mlk_quantize": (_c.c_int, [_c.c_int, _vp, _c.c_int, _c.c_int, _vp, _vp]),
     "mlk_fill_normal": (_c.c_int, [_vp, _c.c_int64, _c.c_uint64, _c.c_float, _c.c_float,
                                    _c.c_int]),
@@ -207,6 +209,11 @@ def time_read(src_list, nbytes, blocks, scratch, warmup, iters):
     check(load().mlk_time_read(sa, n, nbytes, blocks, _ptr(scratch), warmup, iters,
                                _c.byref(out)), "mlk_time_read")
     return out.value
+
+
+def route_topk(logits, bias, rows, experts, top_k, normalize, routed_scale, ids, weights):
+    check(load().mlk_route_topk(_ptr(logits), _ptr(bias), rows, experts, top_k, normalize,
+                                routed_scale, _ptr(ids), _ptr(weights)), "mlk_route_topk")
 
 
 def quantize(bits, w, rows, cols, q, s):

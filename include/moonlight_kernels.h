@@ -14,6 +14,8 @@
  *                      encode_matmul_at (moonlight_metal.m:164-197)
  *   mlk_gemv_swiglu    gate + up matmuls + moonlight_silu_multiply
  *                      (moonlight_metal.m:459-472, moonlight_kernels.metal:533-541)
+ *   mlk_route_topk     moonlight_route_sigmoid_topk (moonlight_kernels.metal:469-512)
+ *                      = moe_route_select + moe_route_finalize (moe_route.h:47-99)
  *   mlk_quantize       quant_int8 / quant_int4 (tools/convert_moonlight.py:46-66)
  */
 #ifndef MOONLIGHT_KERNELS_H
@@ -79,6 +81,16 @@ int mlk_time_copy(void *const *src, void *const *dst, int n_buffers,
  * that many bytes can reach, launch ramp and tail included. */
 int mlk_time_read(void *const *src, int n_buffers, size_t bytes, int blocks,
                   unsigned *scratch, int warmup, int iters, double *avg_us);
+
+/* ---- routing --------------------------------------------------------------
+ * Sigmoid top-k of rows x experts router logits: ids[r, k] is the expert with
+ * the k-th largest sigmoid(logit) + bias (lower index on ties; NaN and -inf
+ * never taken, -1 when fewer than top_k can be), weights[r, k] its sigmoid
+ * score, divided by the row's sum (+ 1e-20) when normalize, times
+ * routed_scale.  Runs the decode path's routing kernels and waits for them. */
+int mlk_route_topk(const float *logits, const float *bias, int rows, int experts,
+                   int top_k, int normalize, float routed_scale, int *ids,
+                   float *weights);
 
 /* ---- packing / synthetic weights ---------------------------------------- */
 int mlk_quantize(int bits, const float *w, int rows, int cols, uint8_t *q,

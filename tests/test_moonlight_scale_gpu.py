@@ -2,7 +2,8 @@
 synthetic q8 model generated in HBM (moonlight_model_create_synthetic): the
 oracle reads the very same packed weights back from the device.
 
-  test_moe_decode         config 2: one MoE layer, T = 1, 8, 64 token rows
+  test_moe_decode         config 2: one MoE layer, T = 1, 2, 4, 8, 64 token
+                          rows (one-row path, grouped GEMV, grouped GEMM)
   test_mla_decode         config 4 attention: one layer at position 4096 and
                           16383 (128 / 512 key splits) over a latent cache
                           pre-filled ~N(0, 1)
@@ -59,7 +60,7 @@ def moe_layer_names(layer):
     return names
 
 
-@pytest.mark.parametrize("rows", [1, 8, 64])
+@pytest.mark.parametrize("rows", [1, 2, 4, 8, 64])
 def test_moe_decode(moon, rows):
     print(f"[gpu] moonlight MoE layer rows={rows}", flush=True)
     sess = S.Session(moon, 128, 64)

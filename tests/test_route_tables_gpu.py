@@ -6,8 +6,8 @@ order, bit for bit.  Every builder of the tables is covered:
 
   1 row     forward pass: routing inside the first expert launch
             (route_single_64)
-  4 rows    forward pass: route_kernel (one workgroup, small_tables)
-  5, 8      forward pass on the MoE GEMM path: routing inside the GEMM prep
+  2 rows    forward pass: route_kernel (one workgroup, small_tables)
+  4, 5, 8   forward pass on the MoE GEMM path: routing inside the GEMM prep
             launch (small_tables)
   64, 2048  forward pass: route_select_kernel + route_lists_kernel
   fixed     caller-given ids (moe_route_fixed semantics) through
@@ -58,7 +58,7 @@ def check_tables(sess, ids):
     return n
 
 
-@pytest.mark.parametrize("rows", [1, 4, 5, 8, 64, 2048])
+@pytest.mark.parametrize("rows", [1, 2, 4, 5, 8, 64, 2048])
 def test_forward_tables(tiny, rows):
     cfg, tensors, model = tiny
     print(f"[gpu] route tables of a {rows}-row forward", flush=True)

@@ -132,10 +132,10 @@ def test_mla(tiny):
     orc.close()
 
 
-# rows = 1: routing inline in the gate/up launch; rows = 4: the routing
-# launches and the grouped GEMV (from 5 rows the layer takes the int8-MFMA
-# GEMM, tested in test_prefill_gpu.py)
-@pytest.mark.parametrize("rows", [1, 4])
+# rows = 1: routing inline in the gate/up launch; rows = 2: the routing
+# launch and the grouped GEMV; rows = 4: the int8-MFMA grouped GEMM (from 3
+# rows, when the shapes allow it; more rows in test_prefill_gpu.py)
+@pytest.mark.parametrize("rows", [1, 2, 4])
 def test_moe(tiny, rows):
     cfg, tensors, model = tiny
     rng = np.random.default_rng(3)
