@@ -329,9 +329,16 @@ int gemv(const GemvParams &p_in, hipStream_t stream) {
     if (p_in.epilogue == kEpiSiluDual && (!p_in.w2 || (p_in.fmt != kF32 && !p_in.s2)))
         return kErrArgs;
     if (p_in.epilogue == kEpiResidual && !p_in.resid) return kErrArgs;
+    // router partials: only the matrix-core kernels write them
+    if (p_in.router_parts &&
+        (!p_in.router_w || !p_in.router_nw || p_in.router_experts <= 0 ||
+         p_in.router_experts > 64 || p_in.O % 4 || ((uintptr_t)p_in.router_w & 15u) ||
+         !gemv_router_ok(p_in)))
+        return kErrArgs;
     // q8 / q4 with up to 4 token rows: the matrix-core kernel when it takes the shape
     if (gemv_mfma(p_in, stream))
         return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
+    if (p_in.router_parts) return kErrArgs;
     const long row_bytes = row_bytes_of(p_in.fmt, p_in.I);
     const bool vector_ok =
         row_bytes % 16 == 0 && (p_in.fmt != kQ4 || p_in.I % 2 == 0) &&

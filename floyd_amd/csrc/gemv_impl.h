@@ -774,6 +774,17 @@ struct RouteParams {
     const ExpertWeights *expert_table = nullptr;  // device [experts]
     ExpertTask *tasks = nullptr;                  // out [task_slots]
     int task_slots = 0;
+    // optional, one token row routed inside the first expert launch: the
+    // logits come as partials of the GEMV that wrote the row (GemvParams
+    // router_parts, n_parts per expert, then n_parts partial sums of
+    // squares of the row's `width` values): logit[e] = sum_j
+    // logit_parts[e * n_parts + j] / sqrt(sum_j logit_parts[experts *
+    // n_parts + j] / width + eps), the sums in one fixed order; the launch's
+    // workgroup 0 also stores them in logits_out
+    const float *logit_parts = nullptr;
+    float *logits_out = nullptr;
+    int n_parts = 0, width = 0;
+    float eps = 0.0f;
 };
 struct ExpertGemvParams {
     int stage = 0;  // 0: gate/up + SwiGLU, 1: down
@@ -885,12 +896,20 @@ __global__ __launch_bounds__(W * 64) void gemv_kernel(GemvLaunch L) {
         } else {
             ExpertWeights ew;
             if (p.route.logits) {
-                // one token row: the tables for the later launches, then this
-                // workgroup's own selection (every wave, no barrier)
+                // one token row: the logits (from partials: the whole
+                // workgroup, one barrier), the tables for the later launches,
+                // then this workgroup's own selection (every wave)
+                __shared__ float route_logits[kMaxExperts + 1];
                 const int wave = threadIdx.x >> 6;
+                const float *lds_logits = nullptr;
+                if (p.route.logit_parts) {
+                    logits_from_parts(p.route, route_logits);
+                    lds_logits = route_logits;
+                }
                 if (blockIdx.x == 0 && blockIdx.y == 0 && wave == 0)
-                    route_single_64(p.route, threadIdx.x, route_keys[0]);
-                if (inline_task_expert(p.route, task, &ew, route_keys[wave]) < 0) return;
+                    route_single_64(p.route, threadIdx.x, route_keys[0], lds_logits);
+                if (inline_task_expert(p.route, task, &ew, route_keys[wave], lds_logits) < 0)
+                    return;
                 n = 1;
                 off = task;
             } else if (p.tasks) {

@@ -104,6 +104,59 @@ struct MfmaGemvArgs {
     int rw;    // output rows per workgroup
 };
 
+// Router operands of wave 0 (one token row, p.router_parts set): lane e's
+// router weights over the workgroup's RW output rows and the RMSNorm weight
+// of lane n's row (loaded with the epilogue operands, used after the
+// products).
+template <int RW>
+struct RouterOperands {
+    f32x4 w[RW / 4];
+    float nw;
+};
+template <int RW>
+__device__ __forceinline__ RouterOperands<RW> load_router(const GemvParams &p, int lane, int row0,
+                                                          int erc) {
+    RouterOperands<RW> r;
+    const int e = lane < p.router_experts ? lane : 0;
+    const float *src = p.router_w + (long)e * p.O + row0;
+#pragma unroll
+    for (int i = 0; i < RW / 4; ++i) r.w[i] = load_f4(src + 4 * i);
+    r.nw = p.router_nw[erc];
+    return r;
+}
+// Wave 0 after the epilogue: lane n < RW holds output y of row row0 + n (0
+// past O).  Writes this workgroup's router logit partials (sum over its rows
+// of w[e, o] * y[o] * nw[o], in row order) and its sum of y^2 (row order).
+// hw: LDS [2 * RW] of wave 0.
+template <int RW>
+__device__ __forceinline__ void store_router_parts(const GemvParams &p, int lane, float y,
+                                                   const RouterOperands<RW> &r, float *hw) {
+    if (lane < RW) {
+        hw[lane] = y * r.nw;
+        hw[RW + lane] = y * y;
+    }
+    // a wave's LDS accesses complete in issue order: the reads below see
+    // every lane's store
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    float part = 0.0f;
+#pragma unroll
+    for (int i = 0; i < RW / 4; ++i) {
+        const f32x4 h = *reinterpret_cast<const f32x4 *>(hw + 4 * i);
+        part = fmaf(r.w[i].x, h.x, part);
+        part = fmaf(r.w[i].y, h.y, part);
+        part = fmaf(r.w[i].z, h.z, part);
+        part = fmaf(r.w[i].w, h.w, part);
+    }
+    const long n = gridDim.x;
+    if (lane < p.router_experts) p.router_parts[(long)lane * n + blockIdx.x] = part;
+    if (lane == 0) {
+        float ss = 0.0f;
+#pragma unroll
+        for (int i = 0; i < RW; ++i) ss += hw[RW + i];
+        p.router_parts[(long)p.router_experts * n + blockIdx.x] = ss;
+    }
+}
+
 // ND: DMA instructions per wave (a compile-time count, so that the wait for
 // the x loads issued before them is exact); RW: output rows per workgroup
 // (16, or 8 for wide-k matrices with few rows: twice the workgroups, the
@@ -128,6 +181,7 @@ __global__ __launch_bounds__(256) void gemv_mfma_kernel(MfmaGemvArgs a) {
     extern __shared__ __attribute__((aligned(16))) unsigned char gm_lds[];
     __shared__ float red[4][4][2][B][RW];  // [wave][limb][gate / up][token row][row]
     __shared__ float red_ss[4][B];
+    __shared__ __attribute__((aligned(16))) float router_hw[2 * RW];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int row0 = blockIdx.x * RW;
     constexpr int row_bytes = FMT == kQ8 ? Sh::kI : Sh::kI / 2;
@@ -269,10 +323,13 @@ __global__ __launch_bounds__(256) void gemv_mfma_kernel(MfmaGemvArgs a) {
     const int erc = er < p.O ? er : p.O - 1;
     const bool has_res = p.epilogue == kEpiResidual;
     float e_s = 0.0f, e_s2 = 0.0f, e_res = 0.0f;
+    const bool router = !DUAL && B == 1 && p.router_parts != nullptr;
+    RouterOperands<RW> ro{};
     if (wave == 0) {
         e_s = p.s[erc];
         if (DUAL) e_s2 = p.s2[erc];
         if (has_res) e_res = p.resid[(long)eb * p.resid_stride + erc];
+        if (router) ro = load_router<RW>(p, lane, row0, erc);
     }
 #pragma unroll
     for (int j = 0; j < kMaxPass; ++j) {
@@ -370,31 +427,36 @@ __global__ __launch_bounds__(256) void gemv_mfma_kernel(MfmaGemvArgs a) {
     __syncthreads();
     // ---- 6. the shares of the four limbs and four waves (limbs, then waves,
     // in order) and the epilogue
-    if (wave != 0 || g >= B) return;
+    if (wave != 0) return;
     const int b = g;  // lanes 16 b + n, b < B
     const int row = row0 + n;
-    if (n >= RW || row >= p.O) return;
-    float inv_rms = 1.0f;
-    if (p.norm_w) {
-        const float tot = (red_ss[0][b] + red_ss[1][b]) + (red_ss[2][b] + red_ss[3][b]);
-        inv_rms = 1.0f / sqrtf(tot / (float)Sh::kI + p.eps);
-    }
-    auto total = [&](int u) {
-        float w4[4];
+    float y_out = 0.0f;  // this lane's output, for the router partials
+    if (g < B && n < RW && row < p.O) {
+        float inv_rms = 1.0f;
+        if (p.norm_w) {
+            const float tot = (red_ss[0][b] + red_ss[1][b]) + (red_ss[2][b] + red_ss[3][b]);
+            inv_rms = 1.0f / sqrtf(tot / (float)Sh::kI + p.eps);
+        }
+        auto total = [&](int u) {
+            float w4[4];
 #pragma unroll
-        for (int w = 0; w < 4; ++w)
-            w4[w] = (red[w][0][u][b][n] + red[w][1][u][b][n]) + (red[w][2][u][b][n] + red[w][3][u][b][n]);
-        return ((w4[0] + w4[1]) + (w4[2] + w4[3])) * inv_rms;
-    };
-    const float sum = total(0);
-    float *yb = p.y + (long)b * p.y_stride;
-    if (DUAL) {
-        yb[row] = silu(sum * e_s) * (total(1) * e_s2);
-        return;
+            for (int w = 0; w < 4; ++w)
+                w4[w] = (red[w][0][u][b][n] + red[w][1][u][b][n]) + (red[w][2][u][b][n] + red[w][3][u][b][n]);
+            return ((w4[0] + w4[1]) + (w4[2] + w4[3])) * inv_rms;
+        };
+        const float sum = total(0);
+        float *yb = p.y + (long)b * p.y_stride;
+        if (DUAL) {
+            yb[row] = silu(sum * e_s) * (total(1) * e_s2);
+        } else {
+            float out = sum * e_s;
+            if (has_res) out = e_res + out;
+            yb[row] = out;
+            y_out = out;
+        }
     }
-    float out = sum * e_s;
-    if (has_res) out = e_res + out;
-    yb[row] = out;
+    // the whole of wave 0, converged: the partials read every lane's output
+    if (router) store_router_parts<RW>(p, lane, y_out, ro, router_hw);
 }
 
 
@@ -416,6 +478,7 @@ __global__ __launch_bounds__(256) void gemv_mfma_direct_kernel(GemvParams p) {
     __shared__ __attribute__((aligned(16))) unsigned char xl_all[4][4 * B * xrow];
     __shared__ float red[4][4][2][B][kRows];  // [wave][limb][gate / up][token row][row]
     __shared__ float red_ss[4][B];
+    __shared__ __attribute__((aligned(16))) float router_hw[2 * kRows];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int row0 = blockIdx.x * kRows;
     const int k0 = wave * KQ;
@@ -456,6 +519,9 @@ __global__ __launch_bounds__(256) void gemv_mfma_direct_kernel(GemvParams p) {
     const float e_s = p.s[wr_row];
     const float e_s2 = DUAL ? p.s2[wr_row] : 0.0f;
     const float e_res = has_res ? p.resid[(long)eb * p.resid_stride + wr_row] : 0.0f;
+    const bool router = !DUAL && B == 1 && p.router_parts != nullptr;
+    RouterOperands<kRows> ro{};
+    if (router && wave == 0) ro = load_router<kRows>(p, lane, row0, wr_row);
 
     // ---- split x into limbs (as gemv_mfma_kernel) and store the limb rows
     float ss[B], amax[B];
@@ -582,31 +648,36 @@ __global__ __launch_bounds__(256) void gemv_mfma_direct_kernel(GemvParams p) {
         if (lane == 0) red_ss[wave][b] = ss[b];
     }
     __syncthreads();
-    if (wave != 0 || g >= B) return;
+    if (wave != 0) return;
     const int b = g;
     const int row = row0 + n;
-    if (row >= p.O) return;
-    float inv_rms = 1.0f;
-    if (p.norm_w) {
-        const float tot = (red_ss[0][b] + red_ss[1][b]) + (red_ss[2][b] + red_ss[3][b]);
-        inv_rms = 1.0f / sqrtf(tot / (float)p.I + p.eps);
-    }
-    auto total = [&](int u) {
-        float w4[4];
+    float y_out = 0.0f;  // this lane's output, for the router partials
+    if (g < B && row < p.O) {
+        float inv_rms = 1.0f;
+        if (p.norm_w) {
+            const float tot = (red_ss[0][b] + red_ss[1][b]) + (red_ss[2][b] + red_ss[3][b]);
+            inv_rms = 1.0f / sqrtf(tot / (float)p.I + p.eps);
+        }
+        auto total = [&](int u) {
+            float w4[4];
 #pragma unroll
-        for (int w = 0; w < 4; ++w)
-            w4[w] = (red[w][0][u][b][n] + red[w][1][u][b][n]) + (red[w][2][u][b][n] + red[w][3][u][b][n]);
-        return ((w4[0] + w4[1]) + (w4[2] + w4[3])) * inv_rms;
-    };
-    const float sum = total(0);
-    float *yb = p.y + (long)b * p.y_stride;
-    if (DUAL) {
-        yb[row] = silu(sum * e_s) * (total(1) * e_s2);
-        return;
+            for (int w = 0; w < 4; ++w)
+                w4[w] = (red[w][0][u][b][n] + red[w][1][u][b][n]) + (red[w][2][u][b][n] + red[w][3][u][b][n]);
+            return ((w4[0] + w4[1]) + (w4[2] + w4[3])) * inv_rms;
+        };
+        const float sum = total(0);
+        float *yb = p.y + (long)b * p.y_stride;
+        if (DUAL) {
+            yb[row] = silu(sum * e_s) * (total(1) * e_s2);
+        } else {
+            float out = sum * e_s;
+            if (has_res) out = e_res + out;
+            yb[row] = out;
+            y_out = out;
+        }
     }
-    float out = sum * e_s;
-    if (has_res) out = e_res + out;
-    yb[row] = out;
+    // the whole of wave 0, converged: the partials read every lane's output
+    if (router) store_router_parts<kRows>(p, lane, y_out, ro, router_hw);
 }
 
 template <int FMT, int B, bool DUAL, int KQ>
@@ -712,18 +783,38 @@ bool launch_b(const MfmaGemvArgs &a, hipStream_t stream, std::string *name) {
 // 128), else the vector kernel.  With `name` set it
 // launches nothing and stores the template name of the kernel it would
 // launch (operand alignment not checked).
-bool gemv_mfma(const GemvParams &p, hipStream_t stream, std::string *name) {
+// Output rows per workgroup when the matrix-core kernels take p (operand
+// alignment checked when `aligned`), else 0.
+static int mfma_rows(const GemvParams &p, bool aligned) {
     if ((p.fmt != kQ8 && p.fmt != kQ4) || p.rows < 1 || p.rows > 4 || p.rows == 3 || p.limbs)
-        return false;
+        return 0;
     const bool dual = p.epilogue == kEpiSiluDual;
     const int rw = p.O < 4096 && p.I > 4096 ? 8 : kRows;
-    if (rw == 8 && (dual || p.rows != 1)) return false;
+    if (rw == 8 && (dual || p.rows != 1)) return 0;
     const int max_pass = p.rows == 1 ? 6 : p.rows == 2 ? 3 : 2;
-    if (p.I % (p.fmt == kQ8 ? 256 : 512) || p.I / 4 > max_pass * 512) return false;
+    if (p.I % (p.fmt == kQ8 ? 256 : 512) || p.I / 4 > max_pass * 512) return 0;
     auto al = [](const void *q) { return ((uintptr_t)q & 15u) == 0; };
-    if (!name && (!al(p.w) || (dual && !al(p.w2)) || !al(p.x) || p.x_stride % 4 ||
-                  (p.norm_w && !al(p.norm_w))))
-        return false;
+    if (aligned && (!al(p.w) || (dual && !al(p.w2)) || !al(p.x) || p.x_stride % 4 ||
+                    (p.norm_w && !al(p.norm_w))))
+        return 0;
+    return rw;
+}
+
+bool gemv_router_ok(const GemvParams &p) {
+    const int rw = mfma_rows(p, true);
+    return rw > 0 && p.rows == 1 && p.epilogue != kEpiSiluDual && p.O % rw == 0;
+}
+
+int gemv_router_parts(const GemvParams &p) {
+    const int rw = mfma_rows(p, false);
+    return rw > 0 ? p.O / rw : 0;
+}
+
+bool gemv_mfma(const GemvParams &p, hipStream_t stream, std::string *name) {
+    const int rw = mfma_rows(p, !name);
+    if (!rw) return false;
+    const bool dual = p.epilogue == kEpiSiluDual;
+    if (p.router_parts && !gemv_router_ok(p)) return false;
     // k quarters of 512: weights straight into registers, except q8 at one
     // token row (measured on MI355X, graph replays: q4 11264 x 2048 5.27 ->
     // 5.21 us, q8 at 4 rows 9.3 -> 8.6 us median, q8 at one row 6.43 -> 6.60

@@ -40,9 +40,24 @@ struct GemvParams {
     // already applied
     const unsigned char *limbs = nullptr;
     long limb_stride = 0;
+    // optional, one token row of a plain or residual epilogue on the int8
+    // matrix-core kernels (gemv_router_ok): router logit partials of the
+    // output row y for the next MoE layer's router.  Workgroup j of the
+    // launch writes router_parts[e * n + j] = sum over its output rows o of
+    // router_w[e, o] * (y[o] * router_nw[o]) for e < router_experts and
+    // router_parts[router_experts * n + j] = sum of y[o]^2 (n = the launch's
+    // workgroups, gemv_router_parts)
+    const float *router_w = nullptr;   // [router_experts, O] f32
+    const float *router_nw = nullptr;  // [O] the router input's RMSNorm weight
+    float *router_parts = nullptr;
+    int router_experts = 0;
 };
 
 int gemv(const GemvParams &p, hipStream_t stream);
+// Whether gemv() can write router logit partials for p (router fields
+// aside), and how many partials per expert it then writes.
+bool gemv_router_ok(const GemvParams &p);
+int gemv_router_parts(const GemvParams &p);
 
 struct GemvPlan;
 // Launch geometry the planner picks for a GEMV shape (exposed for the grouped

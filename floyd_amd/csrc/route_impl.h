@@ -143,17 +143,56 @@ __device__ __forceinline__ RowSelection select_row_64_v(const RouteParams &p, in
     return rs;
 }
 
+// The router logits of one token row from the GEMV partials described at
+// RouteParams::logit_parts, by the whole workgroup (one barrier; every
+// thread must call it).  All experts + 1 rows (expert rows, then the
+// sum-of-squares row) are summed in one pass, so the workgroup waits for one
+// round of loads: tpr threads per row (4, or 2 when 4 do not fit the
+// workgroup), thread t summing part t % tpr of row t / tpr left to right;
+// the parts meet as (p0 + p1) + (p2 + p3), so every workgroup gets the same
+// bits.  lds [experts + 1] receives them scaled; workgroup 0 also stores the
+// logits (logits_out).
+__device__ inline void logits_from_parts(const RouteParams &p, float *lds) {
+    const int t = threadIdx.x, E = p.experts, np = p.n_parts;
+    const int tpr = (E + 1) * 4 <= (int)blockDim.x ? 4 : 2;  // E <= 64, 256 threads
+    const int row = t / tpr, q = t % tpr;
+    const int per = np / tpr;  // np % 16 == 0: whole 16-byte loads per part
+    if (row <= E) {
+        const float *src = p.logit_parts + (long)row * np + q * per;
+        float sum = 0.0f;
+        for (int j = 0; j < per; j += 4) {
+            const f32x4 v = load_f4(src + j);
+            sum = (((sum + v.x) + v.y) + v.z) + v.w;
+        }
+        sum += __shfl_xor(sum, 1, 64);
+        if (tpr == 4) sum += __shfl_xor(sum, 2, 64);
+        if (q == 0) lds[row] = sum;
+    }
+    __syncthreads();
+    const float inv_rms = 1.0f / sqrtf(lds[E] / (float)p.width + p.eps);
+    if (t < E) {
+        const float lg = lds[t] * inv_rms;
+        lds[t] = lg;
+        if (blockIdx.x == 0 && blockIdx.y == 0 && p.logits_out) p.logits_out[t] = lg;
+    }
+    __syncthreads();
+}
+
 // One token row: routing and route tables by a single wave with no barrier.
 // With one row and distinct experts the tables are direct: expert e in slot k
 // is the u-th taken expert (u = k unless a fixed id was invalid), with one
 // list entry at offset u.
 __device__ __forceinline__ void route_single_64(const RouteParams &p, int lane,
-                                                unsigned long long *keys) {
+                                                unsigned long long *keys,
+                                                const float *lds_logits = nullptr) {
     const int E = p.experts, K = p.top_k;
     const bool have = lane < E;
     ExpertWeights ew{};
     if (p.tasks && have) ew = p.expert_table[lane];  // in flight with the logits
-    const RowSelection rs = select_row_64(p, 0, lane, nullptr, keys);
+    const RowSelection rs =
+        lds_logits ? select_row_64_v<true>(p, 0, lane, nullptr, have ? lds_logits[lane] : 0.0f,
+                                           have ? p.bias[lane] : 0.0f, keys)
+                   : select_row_64(p, 0, lane, nullptr, keys);
     const int slot = rs.slot;
     if (lane < K && !((rs.filled >> lane) & 1ull)) {
         p.list_pos[lane] = -1;
@@ -182,11 +221,16 @@ __device__ __forceinline__ void route_single_64(const RouteParams &p, int lane,
 // Every lane loads its expert's table entry alongside the logits, so the
 // weights need no dependent load.  Called by whole waves.
 __device__ __forceinline__ int inline_task_expert(const RouteParams &p, int task,
-                                                  ExpertWeights *ew, unsigned long long *keys) {
+                                                  ExpertWeights *ew, unsigned long long *keys,
+                                                  const float *lds_logits = nullptr) {
     const int lane = threadIdx.x & 63;
+    const bool have = lane < p.experts;
     ExpertWeights mine{};
-    if (lane < p.experts) mine = p.expert_table[lane];
-    const RowSelection rs = select_row_64<false>(p, 0, lane, nullptr, keys);
+    if (have) mine = p.expert_table[lane];
+    const RowSelection rs =
+        lds_logits ? select_row_64_v<false>(p, 0, lane, nullptr, have ? lds_logits[lane] : 0.0f,
+                                            have ? p.bias[lane] : 0.0f, keys)
+                   : select_row_64<false>(p, 0, lane, nullptr, keys);
     const int u = rs.slot >= 0 ? __popcll(rs.filled & ((1ull << rs.slot) - 1ull)) : -1;
     const unsigned long long m = __ballot(u == task);
     if (!m) return -1;

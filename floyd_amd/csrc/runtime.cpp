@@ -116,6 +116,9 @@ struct MoonlightSession {
     int *merge_count = nullptr;                             // zeroed at creation
     float *latent_kv = nullptr, *rope_kv = nullptr, *logits = nullptr;
     float *router_logits = nullptr, *route_weights = nullptr;
+    // router logit partials of one token row written by o_proj for the MoE
+    // layer after it ([experts + 1][hidden / 8], GemvParams router_parts)
+    float *router_parts = nullptr;
     int *route_ids = nullptr, *n_unique = nullptr, *unique = nullptr, *counts = nullptr;
     int *offsets = nullptr, *list_rows = nullptr, *list_slots = nullptr, *list_pos = nullptr;
     int *route_error = nullptr, *route_trace = nullptr, *ids = nullptr;
@@ -933,9 +936,18 @@ int gemm_rows(MoonlightSession *s, const Matrix &m, const Matrix *up, const floa
     return qgemm_single(m.fmt, up != nullptr, t, st);
 }
 
+// Router partials of a one-row GEMV's output for the next MoE layer (see
+// GemvParams router_parts).
+struct RouterFuse {
+    const float *w = nullptr, *nw = nullptr;
+    float *parts = nullptr;
+    int experts = 0;
+};
+
 int gemv_rows(MoonlightSession *s, const Matrix &m, const float *x, int rows, int in_w,
-              int out_w, float *y, const float *norm_w = nullptr, const float *resid = nullptr) {
-    if (use_gemm(s, m.fmt, rows, in_w))
+              int out_w, float *y, const float *norm_w = nullptr, const float *resid = nullptr,
+              const RouterFuse *rf = nullptr) {
+    if (!rf && use_gemm(s, m.fmt, rows, in_w))
         return gemm_rows(s, m, nullptr, x, rows, in_w, out_w, y, norm_w, resid);
     GemvParams p;
     p.fmt = m.fmt;
@@ -953,6 +965,12 @@ int gemv_rows(MoonlightSession *s, const Matrix &m, const float *x, int rows, in
     p.resid = resid;
     p.resid_stride = out_w;
     p.epilogue = resid ? kEpiResidual : kEpiPlain;
+    if (rf) {
+        p.router_w = rf->w;
+        p.router_nw = rf->nw;
+        p.router_parts = rf->parts;
+        p.router_experts = rf->experts;
+    }
     return gemv(p, stream_of(s));
 }
 
@@ -985,7 +1003,8 @@ int swiglu_rows(MoonlightSession *s, const Matrix &g, const Matrix &u, const flo
 // the attend grid is fixed (decode graph capture).
 int attention(MoonlightSession *s, int layer, const float *x, int rows, int position,
               float *out, const float *norm_w, const float *resid,
-              const int *position_dev = nullptr, int grid_splits = 0) {
+              const int *position_dev = nullptr, int grid_splits = 0,
+              const RouterFuse *rf = nullptr) {
     const ModelConfig &c = s->model->cfg;
     const LayerPlan &lp = s->model->layers[layer];
     const int qw = c.head_count * (c.qk_nope_dim + c.qk_rope_dim);
@@ -1038,7 +1057,7 @@ int attention(MoonlightSession *s, int layer, const float *x, int rows, int posi
     p.merge_count = s->merge_count;
     if (int e = mla_attention_core(p, stream_of(s))) return e;
     return gemv_rows(s, lp.o, s->context, rows, c.head_count * c.value_dim, c.hidden_size, out,
-                     nullptr, resid);
+                     nullptr, resid, rf);
 }
 
 // Expert GEMV batches of at least this many token rows split their inputs
@@ -1077,13 +1096,44 @@ static bool moe_uses_gemm(const MoonlightSession *s, int layer, int rows) {
            c.hidden_size <= s->aq_width && sw <= s->aq_width;
 }
 
+// Partials per expert that o_proj of `layer` writes for the router of the
+// same layer when one token row can take the fused router (the layer is an
+// MoE layer routed inside its first expert launch, f32 router, o_proj on the
+// int8 matrix-core GEMV), else 0.
+int router_fuse_parts(const MoonlightSession *s, int layer) {
+    const ModelConfig &c = s->model->cfg;
+    const LayerPlan &lp = s->model->layers[layer];
+    if (lp.dense || lp.router.fmt != kF32 || c.expert_count > 64 || c.experts_per_token > 64 ||
+        presplit_min_rows() <= 1 || !lp.post_norm || ((uintptr_t)lp.router.w & 15u) ||
+        c.hidden_size % 4)
+        return 0;
+    GemvParams p;
+    p.fmt = lp.o.fmt;
+    p.w = lp.o.w;
+    p.O = c.hidden_size;
+    p.I = c.head_count * c.value_dim;
+    p.rows = 1;
+    p.x = s->context;
+    p.x_stride = p.I;
+    p.epilogue = kEpiResidual;
+    if (!gemv_router_ok(p)) return 0;
+    const int n = gemv_router_parts(p);
+    return n > 0 && n % 16 == 0 && n <= c.hidden_size / 8 + 1 ? n : 0;
+}
+
+// fused_parts > 0 (one token row, router_fuse_parts): o_proj has written
+// the router logit partials; no router launch, the first expert launch
+// derives the logits (and stores them in router_logits).
 int route(MoonlightSession *s, int layer, const float *x, int rows, const float *norm_w,
-          int *trace, bool fixed = false, RouteParams *inline_route = nullptr) {
+          int *trace, bool fixed = false, RouteParams *inline_route = nullptr,
+          int fused_parts = 0) {
     const ModelConfig &c = s->model->cfg;
     const LayerPlan &lp = s->model->layers[layer];
     const bool f32_router = lp.router.fmt == kF32;
     const float *router_w = reinterpret_cast<const float *>(lp.router.w);
-    if (rows >= kRouterMfmaMinRows && f32_router && c.hidden_size % 16 == 0) {
+    if (fused_parts > 0) {
+        if (rows != 1 || !inline_route || fixed) return kErrArgs;
+    } else if (rows >= kRouterMfmaMinRows && f32_router && c.hidden_size % 16 == 0) {
         if (router_logits(x, norm_w, c.rms_norm_epsilon, router_w, rows, c.expert_count,
                           c.hidden_size, s->router_logits, stream_of(s)))
             return kErrLaunch;
@@ -1115,6 +1165,15 @@ int route(MoonlightSession *s, int layer, const float *x, int rows, const float 
     r.tasks = s->expert_tasks;
     r.task_slots = rows * r.top_k < r.experts ? rows * r.top_k : r.experts;
     if (inline_route) *inline_route = RouteParams{};
+    if (fused_parts > 0) {
+        r.logit_parts = s->router_parts;
+        r.logits_out = s->router_logits;
+        r.n_parts = fused_parts;
+        r.width = c.hidden_size;
+        r.eps = c.rms_norm_epsilon;
+        *inline_route = r;
+        return kOk;
+    }
     if (inline_route && rows == 1 && c.expert_count <= 64 && rows < presplit_min_rows()) {
         *inline_route = r;
         return kOk;
@@ -1268,8 +1327,18 @@ bool enqueue_forward(MoonlightSession *s, int count, int start, float *layer_out
                          s->route_error, st) == kOk;
     for (int l = 0; ok && l < c.layer_count; ++l) {
         const LayerPlan &lp = m->layers[l];
+        // one row: o_proj also writes the router logit partials of the MoE
+        // layer's router (no router launch)
+        const int fused = count == 1 ? router_fuse_parts(s, l) : 0;
+        RouterFuse rf;
+        if (fused) {
+            rf.w = reinterpret_cast<const float *>(lp.router.w);
+            rf.nw = lp.post_norm;
+            rf.parts = s->router_parts;
+            rf.experts = c.expert_count;
+        }
         ok = attention(s, l, s->h, count, start, s->h, lp.input_norm, s->h, s->pos_dev,
-                       grid_splits) == kOk;
+                       grid_splits, fused ? &rf : nullptr) == kOk;
         if (ok && lp.dense) {
             ok = swiglu_rows(s, lp.gate, lp.up, s->h, count, c.hidden_size,
                              c.dense_intermediate_size, s->dense_hidden, lp.post_norm) == kOk &&
@@ -1278,16 +1347,16 @@ bool enqueue_forward(MoonlightSession *s, int count, int start, float *layer_out
         } else if (ok) {
             int *trace = s->route_trace + (size_t)l * s->options.max_batch * c.experts_per_token;
             RouteParams inline_r;
-            ok = route(s, l, s->h, count, lp.post_norm, trace, false, &inline_r) == kOk;
-            // the router logits exist once route() returns (selection may
-            // still be pending in the first expert launch)
+            ok = route(s, l, s->h, count, lp.post_norm, trace, false, &inline_r, fused) == kOk;
+            ok = ok &&
+                 experts(s, l, s->h, count, lp.post_norm, s->h, s->h, nullptr, &inline_r) == kOk;
+            // the router logits exist once the first expert launch has run
+            // (they come from o_proj's partials there when fused)
             if (ok && s->router_trace)
                 ok = hipMemcpyAsync(s->router_trace +
                                         (size_t)l * s->options.max_batch * c.expert_count,
                                     s->router_logits, (size_t)count * c.expert_count * 4,
                                     hipMemcpyDeviceToDevice, st) == hipSuccess;
-            ok = ok &&
-                 experts(s, l, s->h, count, lp.post_norm, s->h, s->h, nullptr, &inline_r) == kOk;
         }
         if (ok && layer_outputs)
             ok = to_host(s, layer_outputs + (size_t)l * count * H, s->h, (size_t)count * H * 4);
@@ -1508,6 +1577,8 @@ extern "C" int moonlight_session_create(MoonlightSession **out, MoonlightModel *
         hipMemset(s->merge_count, 0, dr * heads * kMlaCountStride * sizeof(int)) == hipSuccess &&
         session_alloc(s, &s->latent_ctx, mb * heads * c.kv_lora_rank, error, error_size) &&
         session_alloc(s, &s->router_logits, mb * E, error, error_size) &&
+        session_alloc(s, &s->router_parts, (size_t)(E + 1) * (c.hidden_size / 8 + 1), error,
+                      error_size) &&
         session_alloc(s, &s->route_ids, mb * K, error, error_size) &&
         session_alloc(s, &s->route_weights, mb * K, error, error_size) &&
         session_alloc(s, &s->n_unique, 1, error, error_size) &&
