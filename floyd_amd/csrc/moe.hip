@@ -332,11 +332,19 @@ __global__ __launch_bounds__(1024) void moe_down_combine_kernel(DownCombineParam
     long stride;
     bool active = true;
     if (u < p.top_k) {
+        // a slot without an expert (e.g. NaN logits: nothing is taken, and
+        // the task table may hold no weights at all) reads the shared down
+        // rows instead, in bounds at the routed stride, and contributes 0
         const int pos = p.list_pos[u];
         active = pos >= 0;
-        const ExpertTask tk = p.tasks[active ? pos : 0];
-        w = tk.w.down;
-        s = tk.w.down_s;
+        if (active) {
+            const ExpertTask tk = p.tasks[pos];
+            w = tk.w.down;
+            s = tk.w.down_s;
+        } else {
+            w = p.shared_down;
+            s = p.shared_down_s;
+        }
         stride = row_bytes_of(FMT, I);
         x = p.expert_hidden + (long)(active ? pos : 0) * I;
     } else {

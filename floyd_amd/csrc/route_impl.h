@@ -14,6 +14,9 @@
 
 namespace mlh {
 
+// experts of a one-row batch whose logits come as GEMV partials
+constexpr int kMaxRouteFused = 64;
+
 // Router score 1 / (1 + e^-x) (moe_route.h:12-14) with e^-x correctly
 // rounded to f32: exp is evaluated in double and rounded once.  Host glibc
 // expf, which the reference's CPU twin calls, misrounds ~0.06 % of inputs by
@@ -144,29 +147,43 @@ __device__ __forceinline__ RowSelection select_row_64_v(const RouteParams &p, in
 }
 
 // The router logits of one token row from the GEMV partials described at
-// RouteParams::logit_parts, by the whole workgroup (one barrier; every
-// thread must call it).  All experts + 1 rows (expert rows, then the
-// sum-of-squares row) are summed in one pass, so the workgroup waits for one
-// round of loads: tpr threads per row (4, or 2 when 4 do not fit the
-// workgroup), thread t summing part t % tpr of row t / tpr left to right;
-// the parts meet as (p0 + p1) + (p2 + p3), so every workgroup gets the same
-// bits.  lds [experts + 1] receives them scaled; workgroup 0 also stores the
-// logits (logits_out).
-__device__ inline void logits_from_parts(const RouteParams &p, float *lds) {
-    const int t = threadIdx.x, E = p.experts, np = p.n_parts;
-    const int tpr = (E + 1) * 4 <= (int)blockDim.x ? 4 : 2;  // E <= 64, 256 threads
-    const int row = t / tpr, q = t % tpr;
-    const int per = np / tpr;  // np % 16 == 0: whole 16-byte loads per part
-    if (row <= E) {
-        const float *src = p.logit_parts + (long)row * np + q * per;
-        float sum = 0.0f;
-        for (int j = 0; j < per; j += 4) {
-            const f32x4 v = load_f4(src + j);
-            sum = (((sum + v.x) + v.y) + v.z) + v.w;
-        }
-        sum += __shfl_xor(sum, 1, 64);
-        if (tpr == 4) sum += __shfl_xor(sum, 2, 64);
-        if (q == 0) lds[row] = sum;
+// RouteParams::logit_parts, by the whole workgroup of 256 threads (one
+// barrier; every thread must call it).  The experts + 1 rows (expert rows,
+// then the sum-of-squares row) of NP floats are read coalesced: a row's
+// NP / 4 lanes each take one 16-byte piece, a wave instruction covers
+// 64 / (NP / 4) rows, and every load is unconditional (rows clamped, the
+// count fixed at compile time), so the workgroup waits for one round of
+// loads.  A row's lanes meet by an xor-shuffle tree, the same in every
+// workgroup, so every workgroup gets the same bits.  lds [experts + 1]
+// receives them scaled; workgroup 0 also stores the logits (logits_out).
+template <int NP>
+__device__ inline void logits_from_parts_np(const RouteParams &p, float *lds) {
+    constexpr int kLpr = NP / 4;                        // lanes per row
+    constexpr int kRpi = 64 / kLpr;                     // rows per wave instruction
+    constexpr int kStride = 4 * kRpi;                   // rows per round of the 4 waves
+    constexpr int kIter = (kMaxRouteFused + kStride) / kStride;  // covers 64 + 1 rows
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int E = p.experts;
+    const int sub = lane / kLpr, piece = lane % kLpr;
+    float sum[kIter];
+#pragma unroll
+    for (int i = 0; i < kIter; ++i) {
+        const int row = wave * kRpi + i * kStride + sub;
+        const int rc = row <= E ? row : E;  // clamped: loaded, unused
+        const f32x4 v = load_f4(p.logit_parts + (long)rc * NP + 4 * piece);
+        sum[i] = (v.x + v.y) + (v.z + v.w);
+    }
+    // the rows' trees step by step across all rows, so that the shuffles of
+    // one step are independent and overlap
+#pragma unroll
+    for (int o = 1; o < kLpr; o <<= 1) {
+#pragma unroll
+        for (int i = 0; i < kIter; ++i) sum[i] += __shfl_xor(sum[i], o, 64);
+    }
+#pragma unroll
+    for (int i = 0; i < kIter; ++i) {
+        const int row = wave * kRpi + i * kStride + sub;
+        if (piece == 0 && row <= E) lds[row] = sum[i];
     }
     __syncthreads();
     const float inv_rms = 1.0f / sqrtf(lds[E] / (float)p.width + p.eps);
@@ -176,6 +193,16 @@ __device__ inline void logits_from_parts(const RouteParams &p, float *lds) {
         if (blockIdx.x == 0 && blockIdx.y == 0 && p.logits_out) p.logits_out[t] = lg;
     }
     __syncthreads();
+}
+// n_parts: a power of two from 16 to 256; experts <= kMaxRouteFused.
+__device__ inline void logits_from_parts(const RouteParams &p, float *lds) {
+    switch (p.n_parts) {
+    case 16: logits_from_parts_np<16>(p, lds); break;
+    case 32: logits_from_parts_np<32>(p, lds); break;
+    case 64: logits_from_parts_np<64>(p, lds); break;
+    case 128: logits_from_parts_np<128>(p, lds); break;
+    default: logits_from_parts_np<256>(p, lds); break;
+    }
 }
 
 // One token row: routing and route tables by a single wave with no barrier.

@@ -1118,7 +1118,8 @@ int router_fuse_parts(const MoonlightSession *s, int layer) {
     p.epilogue = kEpiResidual;
     if (!gemv_router_ok(p)) return 0;
     const int n = gemv_router_parts(p);
-    return n > 0 && n % 16 == 0 && n <= c.hidden_size / 8 + 1 ? n : 0;
+    // logits_from_parts: a power of two from 16 to 256
+    return n >= 16 && n <= 256 && (n & (n - 1)) == 0 && n <= c.hidden_size / 8 + 1 ? n : 0;
 }
 
 // fused_parts > 0 (one token row, router_fuse_parts): o_proj has written

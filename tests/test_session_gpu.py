@@ -172,6 +172,31 @@ def test_moe(tiny, rows):
     orc.close()
 
 
+def test_decode_nan_row_reports_route_error(tmp_path, device):
+    """A token whose embedding row is NaN makes every router logit NaN, so no
+    expert is taken in any MoE layer (NaN never compares greater, as in the
+    reference's arg-max).  The one-row decode path (routing inside the first
+    expert launch, down projections and combine in one launch) must report
+    the route error (prepare_route_tables rejects such ids,
+    moonlight_metal.m:545) without touching the empty expert slots' weights,
+    and a reset session decodes normally afterwards."""
+    print("[gpu] decode of a NaN embedding row (no expert taken)", flush=True)
+    cfg = dict(CU.TINY)
+    tensors = CU.build_tensors(cfg, ebits=8, dbits=8, seed=4321)
+    tensors["model.embed_tokens.weight"][5] = np.nan
+    model = S.Model.open(CU.write_container(str(tmp_path), cfg, tensors))
+    sess = S.Session(model, 32, 4)
+    sess.prefill([1, 2, 3])
+    with pytest.raises(S.SessionError, match="route"):
+        sess.decode(5)
+    sess.reset()
+    sess.prefill([1, 2, 3])
+    logits = sess.decode(4)
+    assert np.all(np.isfinite(logits))
+    sess.close()
+    model.close()
+
+
 def test_dense_mlp(tiny):
     cfg, tensors, model = tiny
     rng = np.random.default_rng(4)
