@@ -354,7 +354,20 @@ __global__ __launch_bounds__(1024) void moe_down_combine_kernel(DownCombineParam
         stride = row_bytes_of(FMT, p.shared_width);
         x = p.shared_hidden + (long)j * I;
     }
-    // ---- weights first (clamped addresses, zero past the row end)
+    // ---- the input vector first, every pass unconditional (clamped), then
+    // the weights (clamped addresses, zero past the row end): in-order
+    // completion lets the limb split below wait for the input alone while
+    // the weights stream
+    constexpr int kXPass = (LPR * NJ * (FMT == kQ8 ? 16 : 32) + 511) / 512;  // inter <= this
+    f32x4 xa[kXPass], xb[kXPass];
+#pragma unroll
+    for (int i = 0; i < kXPass; ++i) {
+        const int e0 = lane * 8 + 512 * i;
+        const int ec = e0 < I ? e0 : 0;
+        xa[i] = load_f4(x + ec);
+        xb[i] = load_f4(x + ec + 4);
+    }
+    __builtin_amdgcn_sched_barrier(0);  // keep the input loads ahead of the weights
     u32x4 wv[NJ];
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
@@ -363,12 +376,15 @@ __global__ __launch_bounds__(1024) void moe_down_combine_kernel(DownCombineParam
         wv[j] = c < nc ? v : u32x4{0u, 0u, 0u, 0u};
     }
     const float sw = load_global_f32(s + row);
+    __builtin_amdgcn_sched_barrier(0);  // the split below waits for the input loads only
     // ---- this wave's input vector into limbs
     unsigned char *my = dc_lds + u * limb_row_lds(FMT, I);
-    for (int e0 = lane * 8; e0 - lane * 8 < I; e0 += 64 * 8) {
+#pragma unroll
+    for (int i = 0; i < kXPass; ++i) {
+        if (512 * i >= I) break;  // uniform: no loads past here
+        const int e0 = lane * 8 + 512 * i;
         const bool in = e0 < I;
-        const int ec = in ? e0 : 0;
-        const f32x4 a = load_f4(x + ec), b = load_f4(x + ec + 4);
+        const f32x4 a = xa[i], b = xb[i];
         const float v[8] = {in ? a.x : 0.f, in ? a.y : 0.f, in ? a.z : 0.f, in ? a.w : 0.f,
                             in ? b.x : 0.f, in ? b.y : 0.f, in ? b.z : 0.f, in ? b.w : 0.f};
         limb_quantise<FMT>(v, in, e0, my, I, nc);
