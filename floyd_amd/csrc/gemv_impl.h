@@ -900,16 +900,20 @@ __global__ __launch_bounds__(W * 64) void gemv_kernel(GemvLaunch L) {
                 // workgroup, one barrier), the tables for the later launches,
                 // then this workgroup's own selection (every wave)
                 __shared__ float route_logits[kMaxExperts + 1];
-                const int wave = threadIdx.x >> 6;
-                const float *lds_logits = nullptr;
+                const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+                // the bias and the expert table entries are in flight while
+                // the logits are summed
+                LaneRoute lr;
                 if (p.route.logit_parts) {
+                    lr = lane_route_load<false>(p.route, lane);
                     logits_from_parts(p.route, route_logits);
-                    lds_logits = route_logits;
+                    lr.logit = lane < p.route.experts ? route_logits[lane] : 0.0f;
+                } else {
+                    lr = lane_route_load<true>(p.route, lane);
                 }
                 if (blockIdx.x == 0 && blockIdx.y == 0 && wave == 0)
-                    route_single_64(p.route, threadIdx.x, route_keys[0], lds_logits);
-                if (inline_task_expert(p.route, task, &ew, route_keys[wave], lds_logits) < 0)
-                    return;
+                    route_single_64(p.route, lane, route_keys[0], lr);
+                if (inline_task_expert(p.route, task, &ew, route_keys[wave], lr) < 0) return;
                 n = 1;
                 off = task;
             } else if (p.tasks) {

@@ -209,17 +209,36 @@ __device__ inline void logits_from_parts(const RouteParams &p, float *lds) {
 // With one row and distinct experts the tables are direct: expert e in slot k
 // is the u-th taken expert (u = k unless a fixed id was invalid), with one
 // list entry at offset u.
+// A lane's routing operands for a one-row batch (lane = expert): its router
+// logit (LOGIT), its selection bias and its expert table entry (zero past
+// the experts).  Loaded unconditionally (index clamped; p.logits and
+// p.expert_table set), so the loads stay in flight together.
+struct LaneRoute {
+    float logit, bias;
+    ExpertWeights w;
+};
+template <bool LOGIT>
+__device__ __forceinline__ LaneRoute lane_route_load(const RouteParams &p, int lane) {
+    const bool have = lane < p.experts;
+    const int e = have ? lane : 0;
+    LaneRoute r;
+    r.w = p.expert_table[e];
+    const float b = p.bias[e];
+    r.bias = have ? b : 0.0f;
+    r.logit = 0.0f;
+    if constexpr (LOGIT) {
+        const float lg = p.logits[e];
+        r.logit = have ? lg : 0.0f;
+    }
+    return r;
+}
+
 __device__ __forceinline__ void route_single_64(const RouteParams &p, int lane,
-                                                unsigned long long *keys,
-                                                const float *lds_logits = nullptr) {
+                                                unsigned long long *keys, const LaneRoute &lr) {
     const int E = p.experts, K = p.top_k;
     const bool have = lane < E;
-    ExpertWeights ew{};
-    if (p.tasks && have) ew = p.expert_table[lane];  // in flight with the logits
-    const RowSelection rs =
-        lds_logits ? select_row_64_v<true>(p, 0, lane, nullptr, have ? lds_logits[lane] : 0.0f,
-                                           have ? p.bias[lane] : 0.0f, keys)
-                   : select_row_64(p, 0, lane, nullptr, keys);
+    const RowSelection rs = select_row_64_v<true>(p, 0, lane, nullptr, lr.logit, lr.bias, keys);
+    const ExpertWeights &ew = lr.w;
     const int slot = rs.slot;
     if (lane < K && !((rs.filled >> lane) & 1ull)) {
         p.list_pos[lane] = -1;
@@ -240,24 +259,28 @@ __device__ __forceinline__ void route_single_64(const RouteParams &p, int lane,
     if (p.tasks && lane >= n_unique && lane < p.task_slots)
         store_task(p.tasks + lane, ExpertWeights{}, 0, 0);
 }
+// The same from memory (route_kernel; the expert table may be absent when
+// no task table is written).
+__device__ __forceinline__ void route_single_64(const RouteParams &p, int lane,
+                                                unsigned long long *keys) {
+    const bool have = lane < p.experts;
+    LaneRoute lr{have ? p.logits[lane] : 0.0f, have ? p.bias[lane] : 0.0f, ExpertWeights{}};
+    if (p.expert_table && have) lr.w = p.expert_table[lane];
+    route_single_64(p, lane, keys, lr);
+}
 
 
 // The expert of routed task `task` (the task-th taken expert in slot order)
 // of a one-row batch, selected from the router logits exactly as
 // route_single_64 selects it, and its weights; -1 when the task is empty.
-// Every lane loads its expert's table entry alongside the logits, so the
-// weights need no dependent load.  Called by whole waves.
+// Every lane holds its expert's table entry (LaneRoute), so the weights need
+// no dependent load.  Called by whole waves.
 __device__ __forceinline__ int inline_task_expert(const RouteParams &p, int task,
                                                   ExpertWeights *ew, unsigned long long *keys,
-                                                  const float *lds_logits = nullptr) {
+                                                  const LaneRoute &lr) {
     const int lane = threadIdx.x & 63;
-    const bool have = lane < p.experts;
-    ExpertWeights mine{};
-    if (have) mine = p.expert_table[lane];
-    const RowSelection rs =
-        lds_logits ? select_row_64_v<false>(p, 0, lane, nullptr, have ? lds_logits[lane] : 0.0f,
-                                            have ? p.bias[lane] : 0.0f, keys)
-                   : select_row_64<false>(p, 0, lane, nullptr, keys);
+    const ExpertWeights &mine = lr.w;
+    const RowSelection rs = select_row_64_v<false>(p, 0, lane, nullptr, lr.logit, lr.bias, keys);
     const int u = rs.slot >= 0 ? __popcll(rs.filled & ((1ull << rs.slot) - 1ull)) : -1;
     const unsigned long long m = __ballot(u == task);
     if (!m) return -1;
