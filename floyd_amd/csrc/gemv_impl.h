@@ -911,9 +911,24 @@ __global__ __launch_bounds__(W * 64) void gemv_kernel(GemvLaunch L) {
                 } else {
                     lr = lane_route_load<true>(p.route, lane);
                 }
-                if (blockIdx.x == 0 && blockIdx.y == 0 && wave == 0)
-                    route_single_64(p.route, lane, route_keys[0], lr);
-                if (inline_task_expert(p.route, task, &ew, route_keys[wave], lr) < 0) return;
+                // wave 0 selects this workgroup's expert (one wave per
+                // workgroup: fewer waves per SIMD compete for the issue
+                // slots), wave 1 of workgroup 0 writes the route tables
+                __shared__ ExpertWeights sel_ew;
+                __shared__ int sel_ok;
+                if (wave == 0) {
+                    ExpertWeights e;
+                    const int src = inline_task_expert(p.route, task, &e, route_keys[0], lr);
+                    if (lane == 0) {
+                        sel_ok = src >= 0;
+                        sel_ew = e;
+                    }
+                } else if (wave == 1 && blockIdx.x == 0 && blockIdx.y == 0) {
+                    route_single_64(p.route, lane, route_keys[1], lr);
+                }
+                __syncthreads();
+                if (!sel_ok) return;
+                ew = sel_ew;
                 n = 1;
                 off = task;
             } else if (p.tasks) {
