@@ -811,53 +811,62 @@ __global__ __launch_bounds__(512) void mla_merge_value_kernel(MlaParams p) {
     const int r = blockIdx.x, h = blockIdx.y, c = blockIdx.z;
     const int nchunks = gridDim.z;
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-    // the position first: memory reads complete in issue order, so a wait
-    // for it does not also wait for the weight fetch below
-    const int pos = mla_position(p) + r;  // row r's own key; the splits hold keys 0 .. pos - 1
-    const int keys = pos;
+    // ---- loads, in this order and all unconditional (indices clamped; no
+    // load under a branch, whose join would wait for every load before it):
+    // the split partials (a row has at most kMlaAttendGroups <= 64 NB
+    // splits: one batch of NB per thread, masked once the position is
+    // known), the first value-weight rows, the position, the own key's
+    // score terms and latent value
+    static_assert(64 * NB >= kMlaAttendGroups, "one batch covers every split");
+    const long mbase = ((long)r * H + h) * p.max_splits;
+    const int dq = t & 7, slot = t >> 3;
+    const float *lc = p.part_lc + (((long)r * H + h) * nchunks + c) * p.max_splits * DL + 4 * dq;
+    float mv[NB], lv[NB];
+    f32x4 v[NB];
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+        const int s = slot + 64 * i < p.max_splits ? slot + 64 * i : p.max_splits - 1;
+        mv[i] = p.part_max[mbase + s];
+        lv[i] = p.part_sum[mbase + s];
+        v[i] = load_f4(lc + (long)s * DL);
+    }
     // value rows of this thread: v = t / 4 + 128 i; dims c * DL + 8 (t % 4) ..
     const int vq = t & 3, vr = t >> 2;
     const int wrow0 = h * (p.nope + p.vdim) + p.nope;
     const int vcol = c * DL + 8 * vq;
     Kvb8<FMT> wraw;
     kvb_fetch8<FMT>(p.kv_b, wrow0 + (vr < p.vdim ? vr : 0), vcol, p.latent, wraw);
-
-    // the own key's score terms (thread t: latent dim t, rope dim t) and
-    // its latent value in this chunk
+    const int pos = mla_position(p) + r;  // row r's own key; the splits hold keys 0 .. pos - 1
+    const int keys = pos;
+    // thread t: latent dim t, rope dim t of the own key's score, latent
+    // value t of this chunk
     const float *qa = p.query_absorbed + ((long)r * p.heads + h) * p.latent;
     const float *qr = p.query_rope + ((long)r * p.heads + h) * p.rope;
     const float *lnew = p.latent_cache + (long)pos * p.latent;
     const float *rnew = p.rope_cache + (long)pos * p.rope;
-    float own = t < p.latent ? qa[t] * lnew[t] : 0.0f;
-    if (t < p.rope) own = fmaf(qr[t], rnew[t], own);
-    const float own_v = t < DL ? lnew[c * DL + t] : 0.0f;
+    const int tl = t < p.latent ? t : 0, tr = t < p.rope ? t : 0, tv = t < DL ? t : 0;
+    const float qa_t = qa[tl], ln_t = lnew[tl], qr_t = qr[tr], rn_t = rnew[tr];
+    const float lv_t = lnew[c * DL + tv];
+    // (selects, not branches: a load the compiler sinks into a branch is
+    // waited for at the join)
+    float own = (t < p.latent ? qa_t : 0.0f) * ln_t;
+    own = fmaf(t < p.rope ? qr_t : 0.0f, rn_t, own);
+    const float own_v = t < DL ? lv_t : 0.0f;
 
     const int tiles = (keys + TK - 1) / TK;
     const int ns = tiles < p.splits ? tiles : p.splits;  // partials of this row
-    const long mbase = ((long)r * H + h) * p.max_splits;
-    const int dq = t & 7, slot = t >> 3;
-    const float *lc = p.part_lc + (((long)r * H + h) * nchunks + c) * p.max_splits * DL + 4 * dq;
     float M = -INFINITY, L = 0.0f;
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-    // branch-free batches (selects, no ifs), so that the compiler keeps all
-    // of a batch's loads ahead of their first use
-    for (int s0 = slot; s0 < ns; s0 += 64 * NB) {
-        float mv[NB], lv[NB];
-        f32x4 v[NB];
+    {
         bool ok[NB];
 #pragma unroll
-        for (int i = 0; i < NB; ++i) {
-            ok[i] = s0 + 64 * i < ns;
-            const int s = ok[i] ? s0 + 64 * i : s0;  // clamped: loaded, unused
-            mv[i] = p.part_max[mbase + s];
-            lv[i] = p.part_sum[mbase + s];
-            v[i] = load_f4(lc + (long)s * DL);
-        }
+        for (int i = 0; i < NB; ++i) ok[i] = slot + 64 * i < ns;
         float mn = M;
 #pragma unroll
         for (int i = 0; i < NB; ++i) mn = fmaxf(mn, ok[i] ? mv[i] : -INFINITY);
-        // split s0 is valid, so mn is finite; the rescale is 0 while M is -inf
-        const float sc = expf(M - mn);
+        // no valid split for this thread: mn is -inf and nothing changes
+        // (M - mn would be NaN); else the rescale is 0 while M is -inf
+        const float sc = mn == -INFINITY ? 1.0f : expf(M - mn);
         acc.x *= sc;
         acc.y *= sc;
         acc.z *= sc;
@@ -865,12 +874,15 @@ __global__ __launch_bounds__(512) void mla_merge_value_kernel(MlaParams p) {
         L *= sc;
 #pragma unroll
         for (int i = 0; i < NB; ++i) {
+            // masked slots hold stale memory (possibly NaN): zero their
+            // values, not only their weight
             const float e = ok[i] ? expf(mv[i] - mn) : 0.0f;
-            acc.x = fmaf(e, v[i].x, acc.x);
-            acc.y = fmaf(e, v[i].y, acc.y);
-            acc.z = fmaf(e, v[i].z, acc.z);
-            acc.w = fmaf(e, v[i].w, acc.w);
-            L = fmaf(e, lv[i], L);
+            const f32x4 vi = ok[i] ? v[i] : f32x4{0.f, 0.f, 0.f, 0.f};
+            acc.x = fmaf(e, vi.x, acc.x);
+            acc.y = fmaf(e, vi.y, acc.y);
+            acc.z = fmaf(e, vi.z, acc.z);
+            acc.w = fmaf(e, vi.w, acc.w);
+            L = fmaf(e, ok[i] ? lv[i] : 0.0f, L);
         }
         M = mn;
     }
