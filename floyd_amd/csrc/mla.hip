@@ -102,15 +102,31 @@ __global__ __launch_bounds__(256) void mla_prep_kernel(MlaParams p, int chunks) 
     const int hw = p.nope + p.rope;
     const int half = p.rope / 2;
     if (role == 0) {
-        const int pos = mla_position(p) + r;
         __shared__ float part[4];
         const float *c = p.compressed + (long)r * p.compressed_stride;
+        // loads first, unconditional (clamped): the compressed row, and with
+        // the absorb (chunks > 0) the rope halves of every head's query,
+        // pairs t and t + 256 of heads x rope / 2
         float cv[kMlaMaxLatent / 256];
 #pragma unroll
         for (int u = 0; u < kMlaMaxLatent / 256; ++u) {
             const int i = t + 256 * u;
-            cv[u] = i < p.latent ? c[i] : 0.0f;
+            const float v = c[i < p.latent ? i : 0];
+            cv[u] = i < p.latent ? v : 0.0f;
         }
+        constexpr int kQPairs = 2;
+        static_assert(kMlaMaxHeads * 64 / 2 <= 256 * kQPairs, "rope pairs of every head");
+        const int npair = chunks ? p.heads * half : 0;
+        float q1[kQPairs], q2[kQPairs], fq[kQPairs];
+#pragma unroll
+        for (int k = 0; k < kQPairs; ++k) {
+            const int j = t + 256 * k, jc = j < npair ? j : 0;
+            const float *qh = p.query + (long)r * p.query_stride + (long)(jc / half) * hw + p.nope;
+            q1[k] = qh[2 * (jc % half)];
+            q2[k] = qh[2 * (jc % half) + 1];
+            fq[k] = p.inv_freq[jc % half];
+        }
+        const int pos = mla_position(p) + r;
         float ss = 0.0f;
 #pragma unroll
         for (int u = 0; u < kMlaMaxLatent / 256; ++u) ss += cv[u] * cv[u];
@@ -133,13 +149,27 @@ __global__ __launch_bounds__(256) void mla_prep_kernel(MlaParams p, int chunks) 
             rp[t] = first * cs - second * sn;
             rp[half + t] = second * cs + first * sn;
         }
+        // the query rope of every head (same angles as the key's)
+#pragma unroll
+        for (int k = 0; k < kQPairs; ++k) {
+            const int j = t + 256 * k;
+            if (j < npair) {
+                const int hh = j / half, i = j % half;
+                const float angle = (float)pos * fq[k];
+                const float cs = cosf(angle), sn = sinf(angle);
+                float *qr = p.query_rope + ((long)r * p.heads + hh) * p.rope;
+                qr[i] = q1[k] * cs - q2[k] * sn;
+                qr[half + i] = q2[k] * cs + q1[k] * sn;
+            }
+        }
         return;
     }
-    // chunks == 0: the query rope only (prefill absorbs with mla_head_gemm)
+    // chunks == 0: the query rope only (prefill absorbs with mla_head_gemm);
+    // with the absorb the query rope is role 0's
     const int h = chunks ? (role - 1) / chunks : role - 1;
     const int cc = chunks ? (role - 1) % chunks : 0;
     const float *q = p.query + (long)r * p.query_stride + (long)h * hw;
-    if (cc == 0 && t < half) {
+    if (!chunks && t < half) {
         const int pos = mla_position(p) + r;
         const float angle = (float)pos * p.inv_freq[t];
         const float cs = cosf(angle), sn = sinf(angle);
