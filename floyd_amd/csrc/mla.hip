@@ -228,19 +228,20 @@ __global__ __launch_bounds__(256) void mla_prep_kernel(MlaParams p, int chunks) 
 // (b + 1) * tiles / splits - 1, so the merge finds min(tiles, splits)
 // partials.  A workgroup keeps a running max / exp-sum per head across its
 // tiles and writes one partial (max, sum, latent context of every head).
-// fp32 matrix cores (v_mfma_f32_16x16x4_f32: fp32 products and sums, in
-// another order than the reference).  Operand layout (measured on gfx950):
-// lane l supplies A[l % 16][l / 16] and B[l / 16][l % 16]; result register i
-// of lane l is D[4 (l / 16) + i][l % 16].  Four MFMAs consume one 16-byte
-// operand read: in step j lane group g = l / 16 takes k index 4 g + j.  The
+// The products run on the f16 matrix cores as split-f16 triples (split_f16:
+// ~22-bit operands, fp32 accumulation, another order than the reference;
+// measured against the oracle: the same rel-L2, 1.7-2.7e-6, as the former
+// fp32 16x16x4 products), with fp32 operands in LDS and registers.  The
 // row's own (new) key joins in mla_merge_value.  Per tile, all 8 waves:
 //   scores  S[key][head] = [lat | rope][key] . [qa | q_rope][head]: wave w
-//           takes the 16-dim steps w, w + 8, ... (query slices in registers,
-//           read once); the 8 partials meet in LDS.
+//           takes the 32-dim steps w, w + 8, w + 16
+//           (v_mfma_f32_16x16x32_f16; query slices split once, in
+//           registers); the 8 partials meet in LDS.
 //   softmax 16 lanes per head: tile max, running max, P = exp(S - max), the
 //           rescale of the running sum and context.
 //   context LC[head][d] += P[head][key] lat[key][d]: wave w takes the 16-wide
-//           d tiles w, w + 8, w + 16, w + 24.
+//           d tiles w, w + 8, w + 16, w + 24 (v_mfma_f32_16x16x16_f16 over
+//           the tile's 16 keys).
 // The rows of the next two tiles are in flight in registers (coalesced
 // 16-byte loads) while a tile is in use, and go into LDS (two buffers) at
 // the top of their step: three barriers per tile.  Loops have
@@ -278,10 +279,32 @@ __device__ __forceinline__ float row16_max(float v) {
 }
 #undef MLH_DPP
 
+// fp32 products on the f16 matrix cores: x = hi + lo with hi = f16(x) and
+// lo = f16(x - hi) (22 significant bits), and a.b ~ hi_a.hi_b + hi_a.lo_b +
+// lo_a.hi_b in fp32 accumulation (the dropped lo_a.lo_b and the rounding of
+// lo are ~2^-22 relative).  Values must lie inside the f16 range (|x| <
+// 65504; a larger one turns the products to inf / NaN, not to a wrong finite
+// value).  gfx950 operand layouts (measured): v_mfma_f32_16x16x32_f16 lane l
+// supplies A[l % 16][8 (l / 16) .. + 7] and B[8 (l / 16) .. + 7][l % 16];
+// v_mfma_f32_16x16x16_f16 A[l % 16][4 (l / 16) .. + 3] and B[4 (l / 16) ..
+// + 3][l % 16]; both return D[4 (l / 16) + i][l % 16] in register i, as the
+// fp32 16x16x4 instruction does.
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+template <int N, typename V>
+__device__ __forceinline__ void split_f16(const float (&x)[N], V &hi, V &lo) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+        const _Float16 h = (_Float16)x[i];
+        hi[i] = h;
+        lo[i] = (_Float16)(x[i] - (float)h);
+    }
+}
+
 __global__ __launch_bounds__(512) void mla_attend_mfma_kernel(MlaParams p) {
     constexpr int H = kMlaMaxHeads;
     constexpr int TK = kMlaTileKeys;
-    constexpr int NS = (kAttnDims / 16 + 7) / 8;  // 16-dim score steps per wave
+    constexpr int NS = (kAttnDims / 32 + 7) / 8;  // 32-dim score steps per wave
     constexpr int NT = kMlaMaxLatent / 16 / 8;    // 16-wide context tiles per wave
     constexpr int DL = kMlaValueDims;
     extern __shared__ __attribute__((aligned(16))) float attn_lds[];
@@ -343,10 +366,11 @@ __global__ __launch_bounds__(512) void mla_attend_mfma_kernel(MlaParams p) {
         *reinterpret_cast<f32x4 *>(buf + rkey * kAttnRowStride + D + rcol) = rr;
     };
     load_tile(t_begin, la, ra);
-    // ---- this wave's query slices: dims 16 (w + 8 j) + 4 g .. + 3 of head
-    // m16; absent heads read head 0 (their outputs are unused), dims past KD
-    // are zero
-    f32x4 qv[NS];
+    // ---- this wave's query slices, split into f16 halves: dims 32 (w + 8 j)
+    // + 8 g .. + 7 of head m16 (D and KD are multiples of 16, so the 8 dims
+    // lie in one part and wholly inside or past KD); absent heads read head
+    // 0 (their outputs are unused), dims past KD are zero
+    half8 qh8[NS], ql8[NS];
     {
         const long qh = (long)r * p.heads + (m16 < p.heads ? m16 : 0);
         const float *qa = p.query_absorbed + qh * D;
@@ -354,10 +378,13 @@ __global__ __launch_bounds__(512) void mla_attend_mfma_kernel(MlaParams p) {
 #pragma unroll
         for (int j = 0; j < NS; ++j) {
             // branch-free: every slice loads (dims past KD reload dim 0)
-            const int d = 16 * (wave + 8 * j) + 4 * g;
-            const f32x4 v = load_f4(d < D ? qa + d : d < KD ? qr + (d - D) : qa);
+            const int d = 32 * (wave + 8 * j) + 8 * g;
+            const float *src = d < D ? qa + d : d < KD ? qr + (d - D) : qa;
+            const f32x4 v0 = load_f4(src), v1 = load_f4(src + 4);
             const bool in = d < KD;
-            qv[j] = f32x4{in ? v.x : 0.f, in ? v.y : 0.f, in ? v.z : 0.f, in ? v.w : 0.f};
+            const float x[8] = {in ? v0.x : 0.f, in ? v0.y : 0.f, in ? v0.z : 0.f, in ? v0.w : 0.f,
+                                in ? v1.x : 0.f, in ? v1.y : 0.f, in ? v1.z : 0.f, in ? v1.w : 0.f};
+            split_f16<8>(x, qh8[j], ql8[j]);
         }
     }
     // every load so far (query slices included) has landed: inside the tile
@@ -369,24 +396,29 @@ __global__ __launch_bounds__(512) void mla_attend_mfma_kernel(MlaParams p) {
     // one tile from its LDS buffer: scores, softmax, context
     auto process = [&](const float *cur, int tile) {
         const int nk = keys - tile * TK < TK ? keys - tile * TK : TK;
-        // ---- scores: 16-dim steps w + 8 j, two chains (even / odd k steps);
-        // steps past KD read row columns 0.. (finite) against a zero query slice
+        // ---- scores: 32-dim steps w + 8 j on the f16 matrix cores (three
+        // products each, two accumulator chains); a lane's 8 dims past KD
+        // read row columns 0.. (finite) against a zero query slice
         {
-            f32x4 av[NS];
+            f32x4 av[NS][2];
 #pragma unroll
             for (int j = 0; j < NS; ++j) {
-                const int d0 = 16 * (wave + 8 * j);
-                av[j] = *reinterpret_cast<const f32x4 *>(cur + m16 * kAttnRowStride +
-                                                         (d0 < KD ? d0 : 0) + 4 * g);
+                const int d = 32 * (wave + 8 * j) + 8 * g;
+                const float *row = cur + m16 * kAttnRowStride + (d < KD ? d : 0);
+                av[j][0] = *reinterpret_cast<const f32x4 *>(row);
+                av[j][1] = *reinterpret_cast<const f32x4 *>(row + 4);
             }
             __builtin_amdgcn_sched_barrier(0);  // all row reads issued before the products
             f32x4v a0 = f32x4v{0.f, 0.f, 0.f, 0.f}, a1 = a0;
 #pragma unroll
             for (int j = 0; j < NS; ++j) {
-                a0 = __builtin_amdgcn_mfma_f32_16x16x4f32(av[j].x, qv[j].x, a0, 0, 0, 0);
-                a1 = __builtin_amdgcn_mfma_f32_16x16x4f32(av[j].y, qv[j].y, a1, 0, 0, 0);
-                a0 = __builtin_amdgcn_mfma_f32_16x16x4f32(av[j].z, qv[j].z, a0, 0, 0, 0);
-                a1 = __builtin_amdgcn_mfma_f32_16x16x4f32(av[j].w, qv[j].w, a1, 0, 0, 0);
+                const float x[8] = {av[j][0].x, av[j][0].y, av[j][0].z, av[j][0].w,
+                                    av[j][1].x, av[j][1].y, av[j][1].z, av[j][1].w};
+                half8 kh, kl;
+                split_f16<8>(x, kh, kl);
+                a0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, qh8[j], a0, 0, 0, 0);
+                a1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, ql8[j], a1, 0, 0, 0);
+                a0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(kl, qh8[j], a0, 0, 0, 0);
             }
 #pragma unroll
             for (int i = 0; i < 4; ++i) sp[(wave * TK + 4 * g + i) * H + m16] = a0[i] + a1[i];
@@ -432,12 +464,19 @@ __global__ __launch_bounds__(512) void mla_attend_mfma_kernel(MlaParams p) {
                 cacc[i][2] *= f.z;
                 cacc[i][3] *= f.w;
             }
+            // P [head][keys 4 g ..] against lat [keys 4 g ..][d] on the f16
+            // matrix cores (the same operands as four fp32 16x16x4 steps)
             const float pj[4] = {pv.x, pv.y, pv.z, pv.w};
+            half4 ph, pl;
+            split_f16<4>(pj, ph, pl);
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
-#pragma unroll
-                for (int i = 0; i < NT; ++i)
-                    cacc[i] = __builtin_amdgcn_mfma_f32_16x16x4f32(pj[j], bv[i][j], cacc[i], 0, 0, 0);
+            for (int i = 0; i < NT; ++i) {
+                half4 bh, bl;
+                split_f16<4>(bv[i], bh, bl);
+                cacc[i] = __builtin_amdgcn_mfma_f32_16x16x16f16(ph, bh, cacc[i], 0, 0, 0);
+                cacc[i] = __builtin_amdgcn_mfma_f32_16x16x16f16(ph, bl, cacc[i], 0, 0, 0);
+                cacc[i] = __builtin_amdgcn_mfma_f32_16x16x16f16(pl, bh, cacc[i], 0, 0, 0);
+            }
         }
     };
     // two tiles in flight: register set A holds the even tiles of the run,
