@@ -632,9 +632,10 @@ __global__ __launch_bounds__(256) void mla_head_gemm_kernel(MlaParams p) {
 // key_count = position + row + 1), flash form: a workgroup takes RB query
 // rows and every head, and streams key tiles of kPfKeys cache rows
 // through two LDS buffers (DMA of tile t + 1 in flight while tile t is
-// used).  Per tile and row, on fp32 MFMA with the operand layouts of
-// mla_attend_mfma_kernel: scores S[key][head] (the 4 waves split the latent +
-// rope dims; partials summed in LDS in wave order), the causal mask, an
+// used).  Per tile and row, on the f16 matrix cores as split-f16 triples
+// (split_f16) with the operand layouts of mla_attend_mfma_kernel: scores
+// S[key][head] (the 4 waves split the latent + rope dims in 32-dim steps;
+// partials summed in LDS in wave order), the causal mask, an
 // online softmax (running max and sum per row and head; the context is
 // rescaled when the max grows), and the context LC[head][d] += P . lat (the
 // waves split the 16-wide d tiles).  The normalised lc goes straight to
@@ -666,8 +667,8 @@ __device__ __forceinline__ void lds_barrier() {
 template <int RB>
 __global__ __launch_bounds__(256, 2) void mla_prefill_attend_kernel(MlaParams p) {
     constexpr int H = kMlaMaxHeads, KS = kPfKeys;
-    constexpr int NJ = kAttnDims / 64;         // 16-dim score steps per wave
-    constexpr int NQ = kMlaMaxLatent / 64;     // d tiles per wave
+    constexpr int NJ = (kAttnDims / 32 + 3) / 4;  // 32-dim score steps per wave
+    constexpr int NQ = kMlaMaxLatent / 64;        // d tiles per wave
     constexpr int PS = KS + 4;                 // P row stride
     extern __shared__ __attribute__((aligned(16))) float pf_lds[];
     float *kbuf = pf_lds;                            // [2][KS][kPfRowStride]
@@ -684,8 +685,10 @@ __global__ __launch_bounds__(256, 2) void mla_prefill_attend_kernel(MlaParams p)
     const int keys = pos0 + nrow;
     const int ntiles = (keys + KS - 1) / KS;
     const int D = p.latent, R = p.rope, KD = D + R;  // KD a multiple of 16 (launch condition)
-    // ---- queries of the rows (absent rows repeat row r0, absent heads head 0)
-    f32x4 qv[RB][NJ];
+    // ---- queries of the rows split into f16 halves (split_f16): dims
+    // 32 (w + 4 j) + 8 g .. + 7 of head m16 (absent rows repeat row r0,
+    // absent heads head 0, dims past KD are zero)
+    half8 qh8[RB][NJ], ql8[RB][NJ];
 #pragma unroll
     for (int b = 0; b < RB; ++b) {
         const long qh = (long)(r0 + (b < nrow ? b : 0)) * p.heads + (m16 < p.heads ? m16 : 0);
@@ -693,8 +696,13 @@ __global__ __launch_bounds__(256, 2) void mla_prefill_attend_kernel(MlaParams p)
         const float *qr = p.query_rope + qh * R;
 #pragma unroll
         for (int j = 0; j < NJ; ++j) {
-            const int d = wave * 16 + 64 * j + 4 * g;
-            if (d < KD) qv[b][j] = d < D ? load_f4(qa + d) : load_f4(qr + (d - D));
+            const int d = 32 * (wave + 4 * j) + 8 * g;
+            const float *src = d < D ? qa + d : d < KD ? qr + (d - D) : qa;
+            const f32x4 v0 = load_f4(src), v1 = load_f4(src + 4);
+            const bool in = d < KD;
+            const float x[8] = {in ? v0.x : 0.f, in ? v0.y : 0.f, in ? v0.z : 0.f, in ? v0.w : 0.f,
+                                in ? v1.x : 0.f, in ? v1.y : 0.f, in ? v1.z : 0.f, in ? v1.w : 0.f};
+            split_f16<8>(x, qh8[b][j], ql8[b][j]);
         }
     }
     for (int i = t; i < RB * H; i += blockDim.x) {
@@ -702,11 +710,14 @@ __global__ __launch_bounds__(256, 2) void mla_prefill_attend_kernel(MlaParams p)
         l_s[i] = 0.0f;
     }
     // ---- latent rows of a key tile -> LDS buffer by DMA (16 bytes per lane
-    // into M0 + 16 lane); the rope part goes to registers: a wave's one rope
-    // step (dims D + 16 w ..) of key m16 as a float4 per lane.  Rows past the
-    // last key copy the last key (finite, masked).
-    const bool has_rope = 16 * wave < R;  // D % 64 == 0: step j = D / 64
-    auto issue = [&](int tile, int buf, f32x4 &rope_next) {
+    // into M0 + 16 lane); the rope part goes to registers: 32-dim step st =
+    // D / 32 + s (dims D + 32 s ..) belongs to wave st % 4, which holds dims
+    // D + 32 s + 8 g .. + 7 of key m16 (rope dims past R read dim 0 against a
+    // zero query).  Rows past the last key copy the last key (finite, masked).
+    const int rope_s = ((wave - D / 32) % 4 + 4) % 4;  // this wave's rope step
+    const bool has_rope = 32 * rope_s < R;
+    const int rope_col = 32 * rope_s + 8 * g < R ? 32 * rope_s + 8 * g : 0;
+    auto issue = [&](int tile, int buf, f32x4 (&rope_next)[2]) {
         float *kb = kbuf + buf * KS * kPfRowStride;
         for (int row = wave; row < KS; row += 4) {
             const int k = tile * KS + row < keys ? tile * KS + row : keys - 1;
@@ -721,7 +732,8 @@ __global__ __launch_bounds__(256, 2) void mla_prefill_attend_kernel(MlaParams p)
         }
         if (has_rope) {
             const int k = tile * KS + m16 < keys ? tile * KS + m16 : keys - 1;
-            rope_next = load_f4(p.rope_cache + (long)k * R + 16 * wave + 4 * g);
+            rope_next[0] = load_f4(p.rope_cache + (long)k * R + rope_col);
+            rope_next[1] = load_f4(p.rope_cache + (long)k * R + rope_col + 4);
         }
     };
     f32x4v acc[RB][NQ];
@@ -729,34 +741,43 @@ __global__ __launch_bounds__(256, 2) void mla_prefill_attend_kernel(MlaParams p)
     for (int b = 0; b < RB; ++b)
 #pragma unroll
         for (int q = 0; q < NQ; ++q) acc[b][q] = f32x4v{0.f, 0.f, 0.f, 0.f};
-    f32x4 rope_cur = {0.f, 0.f, 0.f, 0.f}, rope_next = {0.f, 0.f, 0.f, 0.f};
+    f32x4 rope_cur[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+    f32x4 rope_next[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
     issue(0, 0, rope_next);
     for (int kt = 0; kt < ntiles; ++kt) {
         __builtin_amdgcn_s_waitcnt(0);  // this wave's part of tile kt has landed
         __syncthreads();                // every part visible; tile kt - 1 and P free
-        rope_cur = rope_next;
+        rope_cur[0] = rope_next[0];
+        rope_cur[1] = rope_next[1];
         if (kt + 1 < ntiles) issue(kt + 1, (kt + 1) & 1, rope_next);
         const float *kb = kbuf + (kt & 1) * KS * kPfRowStride;
-        // ---- scores of the tile: wave w takes the 16-dim steps w, w + 4, ...
+        // ---- scores of the tile: wave w takes the 32-dim steps w, w + 4, ...
+        // (v_mfma_f32_16x16x32_f16, split-f16 triples, two accumulator chains)
         {
             f32x4v sacc[RB][2];
 #pragma unroll
             for (int b = 0; b < RB; ++b) sacc[b][0] = sacc[b][1] = f32x4v{0.f, 0.f, 0.f, 0.f};
-            // two accumulators per row (even / odd MFMA of a step); grouping
-            // all rows' MFMAs of one component measured slower
 #pragma unroll
             for (int j = 0; j < NJ; ++j) {
-                const int d0 = wave * 16 + 64 * j;
+                const int d0 = 32 * (wave + 4 * j);
                 if (d0 < KD) {
-                    const f32x4 av = d0 < D ? *reinterpret_cast<const f32x4 *>(
-                                                  kb + m16 * kPfRowStride + d0 + 4 * g)
-                                            : rope_cur;
+                    f32x4 a0, a1;
+                    if (d0 < D) {
+                        const float *row = kb + m16 * kPfRowStride + d0 + 8 * g;
+                        a0 = *reinterpret_cast<const f32x4 *>(row);
+                        a1 = *reinterpret_cast<const f32x4 *>(row + 4);
+                    } else {
+                        a0 = rope_cur[0];
+                        a1 = rope_cur[1];
+                    }
+                    const float x[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+                    half8 kh, kl;
+                    split_f16<8>(x, kh, kl);
 #pragma unroll
                     for (int b = 0; b < RB; ++b) {
-                        sacc[b][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(av.x, qv[b][j].x, sacc[b][0], 0, 0, 0);
-                        sacc[b][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(av.y, qv[b][j].y, sacc[b][1], 0, 0, 0);
-                        sacc[b][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(av.z, qv[b][j].z, sacc[b][0], 0, 0, 0);
-                        sacc[b][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(av.w, qv[b][j].w, sacc[b][1], 0, 0, 0);
+                        sacc[b][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, qh8[b][j], sacc[b][0], 0, 0, 0);
+                        sacc[b][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, ql8[b][j], sacc[b][1], 0, 0, 0);
+                        sacc[b][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kl, qh8[b][j], sacc[b][0], 0, 0, 0);
                     }
                 }
             }
@@ -811,15 +832,20 @@ __global__ __launch_bounds__(256, 2) void mla_prefill_attend_kernel(MlaParams p)
 #pragma unroll
                     for (int i = 0; i < 4; ++i) acc[b][q][i] *= scl[i];
             }
+            half4 ph, pl;
+            split_f16<4>(pj, ph, pl);
 #pragma unroll
             for (int q = 0; q < NQ; ++q) {
                 const int dt = wave + 4 * q;
                 if (dt < D / 16) {
                     const float *lb = kb + (4 * g) * kPfRowStride + dt * 16 + m16;
-#pragma unroll
-                    for (int j = 0; j < 4; ++j)
-                        acc[b][q] = __builtin_amdgcn_mfma_f32_16x16x4f32(pj[j], lb[j * kPfRowStride],
-                                                                        acc[b][q], 0, 0, 0);
+                    const float bx[4] = {lb[0], lb[kPfRowStride], lb[2 * kPfRowStride],
+                                         lb[3 * kPfRowStride]};
+                    half4 bh, bl;
+                    split_f16<4>(bx, bh, bl);
+                    acc[b][q] = __builtin_amdgcn_mfma_f32_16x16x16f16(ph, bh, acc[b][q], 0, 0, 0);
+                    acc[b][q] = __builtin_amdgcn_mfma_f32_16x16x16f16(ph, bl, acc[b][q], 0, 0, 0);
+                    acc[b][q] = __builtin_amdgcn_mfma_f32_16x16x16f16(pl, bh, acc[b][q], 0, 0, 0);
                 }
             }
         }
