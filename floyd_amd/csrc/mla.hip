@@ -796,15 +796,12 @@ __global__ __launch_bounds__(256, 2) void mla_prefill_attend_kernel(MlaParams p)
             const int key = kt * KS + k;
             const bool valid = b < nrow && key <= pos0 + b;
             const float sv = valid ? sum * p.scale : -INFINITY;
-            float mt = sv;
-#pragma unroll
-            for (int o = 8; o >= 1; o >>= 1) mt = fmaxf(mt, __shfl_xor(mt, o, 64));
+            // the 16 keys of (b, h) are the 16 lanes of one DPP row
+            const float mt = row16_max(sv);
             const float mo = m_s[b * H + h];
             const float mn = mt > mo + kPfLazyMax ? mt : mo;  // -inf mo: the tile max
             const float e = valid ? __expf(sv - mn) : 0.0f;
-            float es = e;
-#pragma unroll
-            for (int o = 8; o >= 1; o >>= 1) es += __shfl_xor(es, o, 64);
+            const float es = row16_sum(e);
             p_s[(b * H + h) * PS + k] = e;
             if (k == 0) {
                 const float sc = mn == mo ? 1.0f : __expf(mo - mn);  // 0 while mo is -inf
