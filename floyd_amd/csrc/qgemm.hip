@@ -1040,7 +1040,8 @@ __host__ __device__ inline int moe_shared_down_parts(const MoeGemmParams &p) {
 }
 
 // With L (routing in the same workgroup) the route tables and the expert
-// table (ew_lds, [experts]) come from LDS instead of global memory.
+// table (ew_lds, [experts]) come from LDS instead of global memory.  Called
+// by whole workgroups of at least two waves.
 __device__ __forceinline__ void moe_schedule_body(const MoeScheduleParams &sp,
                                                   const RouteLds *L = nullptr,
                                                   const ExpertWeights *ew_lds = nullptr) {
@@ -1136,15 +1137,36 @@ __device__ __forceinline__ void moe_schedule_body(const MoeScheduleParams &sp,
         }
     }
     lds_barrier();  // the tables are read by the next launch
-    // tile prefix sums: entry u of stage s by its own thread (independent
-    // LDS reads rather than one thread's dependent chain)
-    for (int idx = threadIdx.x; idx < 2 * (kQgMaxTasks + 1); idx += blockDim.x) {
-        const int s = idx / (kQgMaxTasks + 1), u = idx % (kQgMaxTasks + 1);
-        const int n = nr + (s == 0 ? 1 : nsd);
-        if (u > n) continue;
-        int acc = 0;
-        for (int v = 0; v < u; ++v) acc += tiles[s][v];
-        p.tile_start[s * (kQgMaxTasks + 1) + u] = acc;
+    // tile prefix sums tile_start[u] = sum of tiles[s][v < u], u = 0..n: wave
+    // s scans stage s, kPer consecutive entries per lane (one round of
+    // independent LDS reads) and a wave scan over the lanes' sums (a loop of
+    // dependent LDS reads per entry waited for each read in turn)
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    if (wave < 2) {
+        const int s = wave;
+        const int n = nr + (s == 0 ? 1 : nsd);  // tiles[s][0 .. n - 1] are set
+        constexpr int kPer = (kQgMaxTasks + 1 + 63) / 64;
+        int v[kPer], local = 0;
+#pragma unroll
+        for (int i = 0; i < kPer; ++i) {
+            const int u = lane * kPer + i;
+            v[i] = tiles[s][u < n ? u : 0];
+            v[i] = u < n ? v[i] : 0;
+            local += v[i];
+        }
+        int incl = local;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const int up = __shfl_up(incl, o, 64);
+            if (lane >= o) incl += up;
+        }
+        int run = incl - local;
+#pragma unroll
+        for (int i = 0; i < kPer; ++i) {
+            const int u = lane * kPer + i;
+            if (u <= n) p.tile_start[s * (kQgMaxTasks + 1) + u] = run;
+            run += v[i];
+        }
     }
 }
 
@@ -1152,6 +1174,7 @@ __device__ __forceinline__ void moe_schedule_body(const MoeScheduleParams &sp,
 // workgroup, the GEMM task and tile tables: one launch before stage 0.  Eight
 // waves: a row each to quantise, or to route (the routing workgroup).
 constexpr int kPrepWaves = 8;
+static_assert(kPrepWaves >= 2, "moe_schedule_body scans with two waves");
 template <bool REG>
 __global__ __launch_bounds__(64 * kPrepWaves) void moe_prep_kernel(QuantSeg a, MoeScheduleParams sp,
                                                                    int blocks_a) {
