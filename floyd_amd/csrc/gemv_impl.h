@@ -437,20 +437,165 @@ constexpr int limb_pre_passes() {
     return B == 1 ? (passes < 6 ? passes : 6) : 1;
 }
 
+// A job's token rows (RMSNorm'ed with job.norm_w) split into limbs in the
+// LDS row layout, in two steps so that the loads can be issued well before
+// the split: issue() loads the first passes of x (and norm_w) into
+// registers; quantise() takes the RMSNorm statistics (one workgroup barrier)
+// and stores the limb rows, loading any further passes on the way.  Every
+// thread of the workgroup calls both; with `presplit` (limb rows copied in
+// by DMA instead) both do nothing but the barrier.
+template <int FMT, int B, int KT, int KS, int W>
+struct LimbRowsX {
+    static constexpr int NJP = limb_pre_passes<FMT, B, KT, KS, W>();
+    static constexpr int EPT = 8;                 // x elements per thread per pass
+    static constexpr int XV = EPT / 4;            // float4 loads per thread per pass and row
+    static constexpr int PASS = W * kWave * EPT;  // x elements split per workgroup pass
+    f32x4 xv[NJP][B][XV];
+    f32x4 nv[NJP][XV];
+
+    __device__ __forceinline__ void issue(const GemvJob<B> &job, bool presplit) {
+        const int tid = threadIdx.x;
+        const int I = job.I;
+        const int npass = (I + PASS - 1) / PASS;
+#pragma unroll
+        for (int j = 0; j < NJP; ++j) {
+            if (!presplit && j < npass) {
+                const int e0 = tid * EPT + j * PASS;
+                const int ec = e0 < I ? e0 : 0;
+#pragma unroll
+                for (int b = 0; b < B; ++b) {
+                    if (b < job.rows) {  // uniform: absent token rows cost nothing
+#pragma unroll
+                        for (int h = 0; h < XV; ++h) xv[j][b][h] = load_f4(job.x[b] + ec + 4 * h);
+                    }
+                }
+                if (job.norm_w) {
+#pragma unroll
+                    for (int h = 0; h < XV; ++h) nv[j][h] = load_f4(job.norm_w + ec + 4 * h);
+                }
+            }
+        }
+    }
+
+    __device__ __forceinline__ void quantise(const GemvJob<B> &job, unsigned char *lds,
+                                             bool presplit) {
+        __shared__ float ss_red[W][B];
+        const int tid = threadIdx.x;
+        const int lane = tid & (kWave - 1);
+        const int wave = tid / kWave;
+        const int I = job.I;
+        const int nc = row_bytes_of(FMT, I) / 16;
+        const int lds_row = limb_row_lds(FMT, I);
+        const int npass = (I + PASS - 1) / PASS;
+        // RMSNorm statistics (workgroup reduction)
+        float inv_rms[B];
+#pragma unroll
+        for (int b = 0; b < B; ++b) inv_rms[b] = 1.0f;
+        if (job.norm_w && !presplit) {
+            float ss[B];
+#pragma unroll
+            for (int b = 0; b < B; ++b) ss[b] = 0.0f;
+#pragma unroll
+            for (int j = 0; j < NJP; ++j) {
+                if (j < npass && tid * EPT + j * PASS < I) {
+#pragma unroll
+                    for (int b = 0; b < B; ++b)
+                        if (b < job.rows)
+#pragma unroll
+                        for (int h = 0; h < XV; ++h)
+                            ss[b] += xv[j][b][h].x * xv[j][b][h].x + xv[j][b][h].y * xv[j][b][h].y +
+                                     xv[j][b][h].z * xv[j][b][h].z + xv[j][b][h].w * xv[j][b][h].w;
+                }
+            }
+            for (int j = NJP; j < npass; ++j) {
+                const int e0 = tid * EPT + j * PASS;
+                if (e0 < I) {
+#pragma unroll
+                    for (int b = 0; b < B; ++b)
+                        if (b < job.rows)
+#pragma unroll
+                        for (int h = 0; h < XV; ++h) {
+                            const f32x4 t = load_f4(job.x[b] + e0 + 4 * h);
+                            ss[b] += t.x * t.x + t.y * t.y + t.z * t.z + t.w * t.w;
+                        }
+                }
+            }
+#pragma unroll
+            for (int b = 0; b < B; ++b) {
+                const float w_ss = wave_sum(ss[b]);
+                if (lane == 0) ss_red[wave][b] = w_ss;
+            }
+            __syncthreads();
+#pragma unroll
+            for (int b = 0; b < B; ++b) {
+                float tot = (ss_red[0][b] + ss_red[1][b]) + (ss_red[2][b] + ss_red[3][b]);
+#pragma unroll
+                for (int w = 4; w < W; w += 4)
+                    tot += (ss_red[w][b] + ss_red[w + 1][b]) + (ss_red[w + 2][b] + ss_red[w + 3][b]);
+                inv_rms[b] = 1.0f / sqrtf(tot / (float)I + job.eps);
+            }
+        }
+        // quantise x into LDS
+        auto quantise_pass = [&](const f32x4 (&xp)[XV], const f32x4 (&np)[XV], int b, int e0) {
+            float v[EPT];
+#pragma unroll
+            for (int h = 0; h < XV; ++h) {
+                v[4 * h + 0] = xp[h].x;
+                v[4 * h + 1] = xp[h].y;
+                v[4 * h + 2] = xp[h].z;
+                v[4 * h + 3] = xp[h].w;
+            }
+            if (job.norm_w) {
+#pragma unroll
+                for (int h = 0; h < XV; ++h) {
+                    v[4 * h + 0] = v[4 * h + 0] * inv_rms[b] * np[h].x;
+                    v[4 * h + 1] = v[4 * h + 1] * inv_rms[b] * np[h].y;
+                    v[4 * h + 2] = v[4 * h + 2] * inv_rms[b] * np[h].z;
+                    v[4 * h + 3] = v[4 * h + 3] * inv_rms[b] * np[h].w;
+                }
+            }
+            limb_quantise<FMT>(v, e0 < I && b < job.rows, e0, lds + b * lds_row, I, nc);
+        };
+#pragma unroll
+        for (int j = 0; j < NJP; ++j) {
+            if (!presplit && j < npass) {
+                const int e0 = tid * EPT + j * PASS;
+#pragma unroll
+                for (int b = 0; b < B; ++b)
+                    if (b < job.rows) quantise_pass(xv[j][b], nv[j], b, e0);
+            }
+        }
+        for (int j = presplit ? npass : NJP; j < npass; ++j) {
+            const int e0 = tid * EPT + j * PASS;
+            const int ec = e0 < I ? e0 : 0;
+            f32x4 np[XV];
+#pragma unroll
+            for (int h = 0; h < XV; ++h)
+                np[h] = job.norm_w ? load_f4(job.norm_w + ec + 4 * h) : f32x4{1.f, 1.f, 1.f, 1.f};
+#pragma unroll
+            for (int b = 0; b < B; ++b) {
+                if (b < job.rows) {
+                    f32x4 xp[XV];
+#pragma unroll
+                    for (int h = 0; h < XV; ++h) xp[h] = load_f4(job.x[b] + ec + 4 * h);
+                    quantise_pass(xp, np, b, e0);
+                }
+            }
+        }
+    }
+};
+
 // One job: the token rows of job.x against row block job.row_block of the
 // weights.  W waves per workgroup (4 or 8); with KS > 1 the W waves split k.
-template <int FMT, int B, int KT, int LPR, int R, int KS, int W = 4>
+// XR: the caller has already stored the job's limb rows in LDS (LimbRowsX)
+// and passed a workgroup barrier since.
+template <int FMT, int B, int KT, int LPR, int R, int KS, int W = 4, bool XR = false>
 __device__ __forceinline__ void limb_block(const GemvJob<B> job, unsigned char *lds) {
     constexpr int GPW = kWave / LPR;
     constexpr int NV = R * B;
-    constexpr int NJP = limb_pre_passes<FMT, B, KT, KS, W>();
-    constexpr int EPT = 8;                 // x elements per thread per pass
-    constexpr int XV = EPT / 4;            // float4 loads per thread per pass and row
-    constexpr int PASS = W * kWave * EPT;  // x elements split per workgroup pass
     static_assert(NV <= LPR, "partial sums exceed the lane group");
     static_assert(KS == 1 || (LPR == kWave && KS == W), "k-split needs whole-wave row groups");
     __shared__ float red[W][NV];
-    __shared__ float ss_red[W][B];
 
     const int tid = threadIdx.x;
     const int lane = tid & (kWave - 1);
@@ -471,9 +616,8 @@ __device__ __forceinline__ void limb_block(const GemvJob<B> job, unsigned char *
     const int row_bytes = row_bytes_of(FMT, I);
     const int nc = row_bytes / 16;
     const int lds_row = limb_row_lds(FMT, I);
-    const int npass = (I + PASS - 1) / PASS;
 
-    const bool presplit = job.limbs[0] != nullptr;
+    const bool presplit = !XR && job.limbs[0] != nullptr;
     if (presplit) {
         // ---- 1'. pre-split rows: 1 KB blocks straight into LDS (DMA)
         const int nblk = lds_row / 1024;
@@ -491,26 +635,8 @@ __device__ __forceinline__ void limb_block(const GemvJob<B> job, unsigned char *
         }
     }
     // ---- 1. x (and norm_w) of the first passes
-    f32x4 xv[NJP][B][XV];
-    f32x4 nv[NJP][XV];
-#pragma unroll
-    for (int j = 0; j < NJP; ++j) {
-        if (!presplit && j < npass) {
-            const int e0 = tid * EPT + j * PASS;
-            const int ec = e0 < I ? e0 : 0;
-#pragma unroll
-            for (int b = 0; b < B; ++b) {
-                if (b < job.rows) {  // uniform: absent token rows cost nothing
-#pragma unroll
-                    for (int h = 0; h < XV; ++h) xv[j][b][h] = load_f4(job.x[b] + ec + 4 * h);
-                }
-            }
-            if (job.norm_w) {
-#pragma unroll
-                for (int h = 0; h < XV; ++h) nv[j][h] = load_f4(job.norm_w + ec + 4 * h);
-            }
-        }
-    }
+    LimbRowsX<FMT, B, KT, KS, W> xr;
+    if constexpr (!XR) xr.issue(job, presplit);
     // ---- 2. the value this lane writes, and its epilogue operands
     const int vi = butterfly_index<NV, LPR>(lane);
     const int vr = vi / B, vb = vi % B;
@@ -571,104 +697,10 @@ __device__ __forceinline__ void limb_block(const GemvJob<B> job, unsigned char *
     u32x4 wa[R][KT];
     load_tile(wa, kpart * KT * LPR, out0);
 
-    // ---- 4. RMSNorm statistics (workgroup reduction)
-    float inv_rms[B];
-#pragma unroll
-    for (int b = 0; b < B; ++b) inv_rms[b] = 1.0f;
-    if (job.norm_w && !presplit) {
-        float ss[B];
-#pragma unroll
-        for (int b = 0; b < B; ++b) ss[b] = 0.0f;
-#pragma unroll
-        for (int j = 0; j < NJP; ++j) {
-            if (j < npass && tid * EPT + j * PASS < I) {
-#pragma unroll
-                for (int b = 0; b < B; ++b)
-                    if (b < job.rows)
-#pragma unroll
-                    for (int h = 0; h < XV; ++h)
-                        ss[b] += xv[j][b][h].x * xv[j][b][h].x + xv[j][b][h].y * xv[j][b][h].y +
-                                 xv[j][b][h].z * xv[j][b][h].z + xv[j][b][h].w * xv[j][b][h].w;
-            }
-        }
-        for (int j = NJP; j < npass; ++j) {
-            const int e0 = tid * EPT + j * PASS;
-            if (e0 < I) {
-#pragma unroll
-                for (int b = 0; b < B; ++b)
-                    if (b < job.rows)
-#pragma unroll
-                    for (int h = 0; h < XV; ++h) {
-                        const f32x4 t = load_f4(job.x[b] + e0 + 4 * h);
-                        ss[b] += t.x * t.x + t.y * t.y + t.z * t.z + t.w * t.w;
-                    }
-            }
-        }
-#pragma unroll
-        for (int b = 0; b < B; ++b) {
-            const float w_ss = wave_sum(ss[b]);
-            if (lane == 0) ss_red[wave][b] = w_ss;
-        }
-        __syncthreads();
-#pragma unroll
-        for (int b = 0; b < B; ++b) {
-            float tot = (ss_red[0][b] + ss_red[1][b]) + (ss_red[2][b] + ss_red[3][b]);
-#pragma unroll
-            for (int w = 4; w < W; w += 4)
-                tot += (ss_red[w][b] + ss_red[w + 1][b]) + (ss_red[w + 2][b] + ss_red[w + 3][b]);
-            inv_rms[b] = 1.0f / sqrtf(tot / (float)I + job.eps);
-        }
-    }
-
-    // ---- 5. quantise x into LDS
-    auto quantise_pass = [&](const f32x4 (&xp)[XV], const f32x4 (&np)[XV], int b, int e0) {
-        float v[EPT];
-#pragma unroll
-        for (int h = 0; h < XV; ++h) {
-            v[4 * h + 0] = xp[h].x;
-            v[4 * h + 1] = xp[h].y;
-            v[4 * h + 2] = xp[h].z;
-            v[4 * h + 3] = xp[h].w;
-        }
-        if (job.norm_w) {
-#pragma unroll
-            for (int h = 0; h < XV; ++h) {
-                v[4 * h + 0] = v[4 * h + 0] * inv_rms[b] * np[h].x;
-                v[4 * h + 1] = v[4 * h + 1] * inv_rms[b] * np[h].y;
-                v[4 * h + 2] = v[4 * h + 2] * inv_rms[b] * np[h].z;
-                v[4 * h + 3] = v[4 * h + 3] * inv_rms[b] * np[h].w;
-            }
-        }
-        limb_quantise<FMT>(v, e0 < I && b < job.rows, e0, lds + b * lds_row, I, nc);
-    };
-#pragma unroll
-    for (int j = 0; j < NJP; ++j) {
-        if (!presplit && j < npass) {
-            const int e0 = tid * EPT + j * PASS;
-#pragma unroll
-            for (int b = 0; b < B; ++b)
-                if (b < job.rows) quantise_pass(xv[j][b], nv[j], b, e0);
-        }
-    }
-    for (int j = presplit ? npass : NJP; j < npass; ++j) {
-        const int e0 = tid * EPT + j * PASS;
-        const int ec = e0 < I ? e0 : 0;
-        f32x4 np[XV];
-#pragma unroll
-        for (int h = 0; h < XV; ++h)
-            np[h] = job.norm_w ? load_f4(job.norm_w + ec + 4 * h) : f32x4{1.f, 1.f, 1.f, 1.f};
-#pragma unroll
-        for (int b = 0; b < B; ++b) {
-            if (b < job.rows) {
-                f32x4 xp[XV];
-#pragma unroll
-                for (int h = 0; h < XV; ++h) xp[h] = load_f4(job.x[b] + ec + 4 * h);
-                quantise_pass(xp, np, b, e0);
-            }
-        }
-    }
+    // ---- 4, 5. RMSNorm statistics, x quantised into LDS
+    if constexpr (!XR) xr.quantise(job, lds, presplit);
     if (presplit) __builtin_amdgcn_s_waitcnt(0);  // this wave's DMA blocks have landed
-    __syncthreads();
+    if constexpr (!XR) __syncthreads();
 
     // ---- 6. dot products of one k tile into acc
     auto dot_tile = [&](const u32x4 (&wv)[R][KT], int kt0, float (&acc)[NV]) {
@@ -885,6 +917,11 @@ __global__ __launch_bounds__(W * 64) void gemv_kernel(GemvLaunch L) {
         job.row_block = shared ? (int)blockIdx.x - routed_wgs : (int)blockIdx.x % p.routed_blocks;
         int n, off = 0;
         const int *list = nullptr;
+        // one routed token row of q8 / q4 experts: the row is split into
+        // limbs while the routing runs (its loads issued with the router
+        // operands'), so that only the weight stream follows the selection
+        constexpr bool kLimbX = FMT != kF32 && B == 1;
+        bool x_ready = false;
         if (shared) {
             n = p.shared_rows;
             job.w = p.sh_w;  // stage 0: shared gate (sh_w2 = up); stage 1: shared down
@@ -901,6 +938,17 @@ __global__ __launch_bounds__(W * 64) void gemv_kernel(GemvLaunch L) {
                 // then this workgroup's own selection (every wave)
                 __shared__ float route_logits[kMaxExperts + 1];
                 const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+                GemvJob<B> xjob;
+                LimbRowsX<FMT, B, KT, KS, W> xr;
+                if constexpr (kLimbX) {
+                    xjob.I = p.hidden;
+                    xjob.rows = 1;
+                    xjob.x[0] = p.x;  // token row 0
+                    xjob.limbs[0] = nullptr;
+                    xjob.norm_w = p.norm_w;  // inline routing: stage 0 only
+                    xjob.eps = p.eps;
+                    xr.issue(xjob, false);
+                }
                 // the bias and the expert table entries are in flight while
                 // the logits are summed
                 LaneRoute lr;
@@ -910,6 +958,11 @@ __global__ __launch_bounds__(W * 64) void gemv_kernel(GemvLaunch L) {
                     lr.logit = lane < p.route.experts ? route_logits[lane] : 0.0f;
                 } else {
                     lr = lane_route_load<true>(p.route, lane);
+                }
+                if constexpr (kLimbX) {
+                    // the limb rows, published by the barrier below
+                    xr.quantise(xjob, gemv_lds, false);
+                    x_ready = true;
                 }
                 // wave 0 selects this workgroup's expert (one wave per
                 // workgroup: fewer waves per SIMD compete for the issue
@@ -979,6 +1032,12 @@ __global__ __launch_bounds__(W * 64) void gemv_kernel(GemvLaunch L) {
                 const long lrow = p.stage == 0 ? token : (shared ? j : off + j);
                 job.limbs[b] = shared ? (p.sh_limbs ? p.sh_limbs + lrow * p.sh_limb_stride : nullptr)
                                       : (p.limbs ? p.limbs + lrow * p.limb_stride : nullptr);
+            }
+            if constexpr (kLimbX) {
+                if (x_ready) {
+                    limb_block<FMT, B, KT, LPR, R, KS, W, true>(job, gemv_lds);
+                    return;
+                }
             }
             run_job<MODE, FMT, B, KT, LPR, R, KS, W>(job, gemv_lds);
         }
