@@ -18,18 +18,25 @@ struct CachedWeight {
     float *s = nullptr;
 };
 
-std::mutex g_mutex;  // guards the cache and the scratch buffers
-std::unordered_map<const void *, CachedWeight> g_cache;
-void *g_scratch = nullptr;
-size_t g_scratch_bytes = 0;
+std::mutex g_mutex;  // guards every device's cache and staging buffer
 
-bool ensure_scratch(size_t bytes) {
-    if (bytes <= g_scratch_bytes) return true;
-    if (g_scratch) (void)hipFree(g_scratch);
-    g_scratch = nullptr;
-    g_scratch_bytes = 0;
-    if (hipMalloc(&g_scratch, bytes) != hipSuccess) return false;
-    g_scratch_bytes = bytes;
+// Per device: the weights cached by host pointer and the staging buffer of
+// x, y and transient weights.
+struct DeviceState {
+    std::unordered_map<const void *, CachedWeight> cache;
+    void *scratch = nullptr;
+    size_t scratch_bytes = 0;
+};
+constexpr int kMaxDevices = 64;
+DeviceState g_state[kMaxDevices];
+
+bool ensure_scratch(DeviceState &d, size_t bytes) {
+    if (bytes <= d.scratch_bytes) return true;
+    if (d.scratch) (void)hipFree(d.scratch);
+    d.scratch = nullptr;
+    d.scratch_bytes = 0;
+    if (hipMalloc(&d.scratch, bytes) != hipSuccess) return false;
+    d.scratch_bytes = bytes;
     return true;
 }
 
@@ -51,7 +58,13 @@ void run(int fmt, float *y, const float *x, const void *w, size_t w_bytes, const
         fill_nan(y, (long)O * S);
         return;
     }
+    if (ctx->device >= kMaxDevices) {
+        mlh::set_last_error("fm_matmul: device index out of range");
+        fill_nan(y, (long)O * S);
+        return;
+    }
     std::lock_guard<std::mutex> lock(g_mutex);
+    DeviceState &d = g_state[ctx->device];
     hipStream_t st = ctx->stream;
     const size_t x_bytes = (size_t)S * I * sizeof(float);
     const size_t y_bytes = (size_t)S * O * sizeof(float);
@@ -59,16 +72,16 @@ void run(int fmt, float *y, const float *x, const void *w, size_t w_bytes, const
     CachedWeight dev;
     bool transient = true;
     if (cache) {
-        auto it = g_cache.find(w);
-        if (it != g_cache.end()) {
+        auto it = d.cache.find(w);
+        if (it != d.cache.end()) {
             dev = it->second;  // a hit ignores sizes: one stable pointer per tensor
             transient = false;
         }
     }
     size_t need = align(x_bytes) + align(y_bytes);
     if (transient && !cache) need += align(w_bytes) + align((size_t)O * sizeof(float));
-    bool ok = ensure_scratch(need);
-    char *base = static_cast<char *>(g_scratch);
+    bool ok = ensure_scratch(d, need);
+    char *base = static_cast<char *>(d.scratch);
     if (ok && transient) {
         if (cache) {
             ok = hipMalloc(&dev.w, w_bytes) == hipSuccess &&
@@ -81,7 +94,7 @@ void run(int fmt, float *y, const float *x, const void *w, size_t w_bytes, const
         ok = ok && hipMemcpyAsync(dev.w, w, w_bytes, hipMemcpyHostToDevice, st) == hipSuccess &&
              hipMemcpyAsync(dev.s, s, (size_t)O * sizeof(float), hipMemcpyHostToDevice, st) ==
                  hipSuccess;
-        if (ok && cache) g_cache[w] = dev;
+        if (ok && cache) d.cache[w] = dev;
     }
     float *dx = reinterpret_cast<float *>(base);
     float *dy = reinterpret_cast<float *>(base + align(x_bytes));

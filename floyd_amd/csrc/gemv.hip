@@ -130,26 +130,8 @@ int limb_quantise_rows(const LimbRowsParams &a, const LimbRowsParams &b, hipStre
 
 // Waves the planner tries to keep in flight: with ~8 waves per CU the HBM
 // latency (~1-2 us under load) is hidden without relying on deep per-wave
-// queues.  MLH_GEMV_PLAN="kt,r,ks" (read once) overrides the choice for
-// tuning sweeps.
+// queues.
 static constexpr long kTargetWaves = 2048;
-
-static bool plan_override(GemvPlan *plan) {
-    static int parsed = 0, kt = 0, r = 0, ks = 0, waves = 4;
-    if (!parsed) {
-        const char *env = getenv("MLH_GEMV_PLAN");
-        const int n = env ? sscanf(env, "%d,%d,%d,%d", &kt, &r, &ks, &waves) : 0;
-        if (n < 3) kt = 0;
-        if (n < 4) waves = 4;
-        parsed = 1;
-    }
-    if (!kt) return false;
-    plan->kt = kt;
-    plan->r = r;
-    plan->ks = ks;
-    plan->waves = waves;
-    return true;
-}
 
 // Plans measured best on MI355X for the Moonlight decode shapes (batch 1):
 // sweeps over kt x r x ks of back-to-back launches, 400+ MB weight rotation.
@@ -180,12 +162,6 @@ GemvPlan plan_gemv(int fmt, int O, int I, int rows, bool dual) {
         return plan;
     }
     plan.lpr = 64;
-    if (plan_override(&plan)) {
-        if (plan.r * plan.b > 16) plan.r = 16 / plan.b;
-        if (dual && plan.r < 2) plan.r = 2;
-        if (fmt == kF32 || plan.ks != 1) plan.waves = 4;
-        return plan;
-    }
     if (plan.b == 1) {
         for (const PlanEntry &e : kMeasuredPlans) {
             if (e.fmt == fmt && e.O == O && e.I == I && e.dual == (int)dual) {
@@ -240,30 +216,12 @@ GemvPlan plan_gemv(int fmt, int O, int I, int rows, bool dual) {
 // launch (I = max_I, KT up to 3 columns of 64 chunks), 8 rows per wave when
 // the registers allow (the x prologue of every workgroup is amortised over
 // more rows; measured best for the Moonlight expert shapes).
-// MLH_EXPERT_PLAN="kt,r,ks;kt,r,ks" (stage 0; stage 1, read once) overrides.
-static bool expert_plan_override(bool dual, GemvPlan *plan) {
-    static int parsed = 0, v[2][3] = {{0, 0, 0}, {0, 0, 0}};
-    if (!parsed) {
-        const char *env = getenv("MLH_EXPERT_PLAN");
-        if (!env || sscanf(env, "%d,%d,%d;%d,%d,%d", &v[0][0], &v[0][1], &v[0][2], &v[1][0],
-                           &v[1][1], &v[1][2]) != 6)
-            v[0][0] = v[1][0] = 0;
-        parsed = 1;
-    }
-    const int *e = v[dual ? 0 : 1];
-    if (!e[0]) return false;
-    plan->kt = e[0];
-    plan->r = e[1];
-    plan->ks = e[2];
-    return true;
-}
-
 GemvPlan plan_expert_gemv(int fmt, int O, int I, int rows, bool dual, int tasks, int max_I) {
     GemvPlan plan = plan_gemv(fmt, O, max_I, rows, dual);
     plan.waves = 4;  // grouped launches use 4-wave workgroups
     if (plan.lpr < 64) return plan;
     if (fmt != kF32) {
-        if (!expert_plan_override(dual, &plan)) {
+        {
             const int nc = row_bytes_of(fmt, max_I) / 16;
             if (nc <= 192) {
                 plan.ks = 1;

@@ -798,7 +798,8 @@ struct RouteParams {
     int *list_rows = nullptr;  // [rows*top_k] token row per list entry
     int *list_slots = nullptr; // [rows*top_k] slot per list entry
     int *list_pos = nullptr;   // [rows*top_k] list entry of (row, slot), -1 if invalid
-    int *error = nullptr;      // [1] set to 1 when an id is out of range
+    int *error = nullptr;      // [1] set to error_code when an id is out of range (if still 0)
+    int error_code = 1;        // the forward passes layer + 1, so the first failing layer is kept
     // optional [rows, top_k] expert ids given by the caller: weights come from
     // their scores (moe_route_fixed, moe_route.h:76-87) instead of a top-k
     const int *fixed_ids = nullptr;

@@ -800,9 +800,18 @@ static int mfma_rows(const GemvParams &p, bool aligned) {
     return rw;
 }
 
+bool gemv_mfma(const GemvParams &p, hipStream_t stream, std::string *name);
+
 bool gemv_router_ok(const GemvParams &p) {
     const int rw = mfma_rows(p, true);
-    return rw > 0 && p.rows == 1 && p.epilogue != kEpiSiluDual && p.O % rw == 0;
+    if (!(rw > 0 && p.rows == 1 && p.epilogue != kEpiSiluDual && p.O % rw == 0)) return false;
+    // a kernel of the dispatch below exists for the shape (instantiated DMA
+    // counts, register and LDS budgets): asked in name-only mode, which
+    // launches nothing
+    GemvParams q = p;
+    q.router_parts = nullptr;
+    std::string name;
+    return gemv_mfma(q, nullptr, &name);
 }
 
 int gemv_router_parts(const GemvParams &p) {

@@ -11,7 +11,8 @@
 namespace mlh {
 
 static std::mutex g_context_mutex;
-static DeviceContext g_context;
+static constexpr int kMaxDevices = 64;
+static DeviceContext g_contexts[kMaxDevices];
 static thread_local std::string g_last_error;
 
 void set_last_error(const std::string &message) { g_last_error = message; }
@@ -24,37 +25,54 @@ int check_hip(hipError_t status, const char *what) {
 }
 
 DeviceContext *context() {
+    int device = 0;
+    if (hipGetDevice(&device) != hipSuccess) {
+        set_last_error("no HIP device is available");
+        return nullptr;
+    }
+    return context_of(device);
+}
+
+DeviceContext *context_of(int device) {
     std::lock_guard<std::mutex> lock(g_context_mutex);
-    if (g_context.ready) return &g_context;
+    if (device < 0 || device >= kMaxDevices) {
+        set_last_error("HIP device index out of range");
+        return nullptr;
+    }
+    DeviceContext &ctx = g_contexts[device];
+    if (ctx.ready) return &ctx;
     int count = 0;
-    if (hipGetDeviceCount(&count) != hipSuccess || count <= 0) {
+    if (hipGetDeviceCount(&count) != hipSuccess || count <= device) {
         set_last_error("no HIP device is available");
         return nullptr;
     }
     hipDeviceProp_t prop;
-    if (hipGetDeviceProperties(&prop, 0) != hipSuccess) {
-        set_last_error("cannot query HIP device 0");
+    if (hipGetDeviceProperties(&prop, device) != hipSuccess) {
+        set_last_error("cannot query HIP device " + std::to_string(device));
         return nullptr;
     }
     std::string arch = prop.gcnArchName;
     if (arch.rfind("gfx950", 0) != 0) {
-        set_last_error("device 0 is " + arch + "; this library is built for gfx950 (MI355X)");
+        set_last_error("device " + std::to_string(device) + " is " + arch +
+                       "; this library is built for gfx950 (MI355X)");
         return nullptr;
     }
-    if (hipSetDevice(0) != hipSuccess ||
-        hipStreamCreateWithFlags(&g_context.stream, hipStreamNonBlocking) != hipSuccess) {
-        set_last_error("cannot create the HIP stream");
-        return nullptr;
+    {
+        DeviceScope scope(device);
+        if (hipStreamCreateWithFlags(&ctx.stream, hipStreamNonBlocking) != hipSuccess) {
+            set_last_error("cannot create the HIP stream");
+            return nullptr;
+        }
     }
-    g_context.device = 0;
+    ctx.device = device;
     // Marketing names can be empty inside containers; the architecture is
     // always appended so callers can tell the device class.
-    g_context.name = std::string(prop.name[0] ? prop.name : "AMD Instinct GPU") + " [" +
-                     arch.substr(0, arch.find(':')) + "]";
-    g_context.arch = arch;
-    g_context.cu_count = prop.multiProcessorCount;
-    g_context.ready = true;
-    return &g_context;
+    ctx.name = std::string(prop.name[0] ? prop.name : "AMD Instinct GPU") + " [" +
+               arch.substr(0, arch.find(':')) + "]";
+    ctx.arch = arch;
+    ctx.cu_count = prop.multiProcessorCount;
+    ctx.ready = true;
+    return &ctx;
 }
 
 }  // namespace mlh

@@ -660,8 +660,14 @@ constexpr size_t pf_lds_bytes() {
 // operations, not for its loads in flight (__syncthreads() would also wait
 // for the next key tile's DMA and serialise the double buffering).
 __device__ __forceinline__ void lds_barrier() {
+    // The empty asm statements clobber memory, so the compiler keeps every
+    // memory access on its side of the barrier (s_barrier alone is no memory
+    // operation to it).  An LDS release fence would do the same but also wait
+    // for the key tile's LDS DMA in flight (vmcnt(0)).
+    asm volatile("" ::: "memory");
     __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0); vmcnt, expcnt not waited
     __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
 }
 
 template <int RB>
@@ -883,10 +889,9 @@ __global__ __launch_bounds__(256, 2) void mla_prefill_attend_kernel(MlaParams p)
 //   sum    ctx_h[v] = sum_c y_c[v] in chunk order, by the chunk workgroup
 //          that arrives last (merge_count; it resets the counter).  The
 //          shares travel as device-coherent (agent-scope) stores and loads,
-//          which on gfx950 bypass the per-XCD L2 copies: each workgroup
-//          waits for its stores to complete before its arrival increment, so
-//          the workgroup that counts last finds every share in memory, with
-//          no L2 write-back fence.
+//          which on gfx950 bypass the per-XCD L2 copies; the arrival
+//          increment is an agent-scope acquire-release, so the workgroup
+//          that counts last is ordered after every share store.
 constexpr int kMergeBatch = 4;
 template <int FMT>
 __global__ __launch_bounds__(512) void mla_merge_value_kernel(MlaParams p) {
@@ -1036,12 +1041,18 @@ __global__ __launch_bounds__(512) void mla_merge_value_kernel(MlaParams p) {
         if (vq == 0 && v < p.vdim)
             __hip_atomic_store(part + v, y, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
-    // the last of the head's chunk workgroups sums the shares
-    __builtin_amdgcn_s_waitcnt(0);  // this thread's share stores have completed
+    // the last of the head's chunk workgroups sums the shares.  Ordering:
+    // every thread's share stores happen before thread 0's increment (the
+    // workgroup barrier), which releases them at agent scope; the increment
+    // that counts last acquires every earlier one (they form one release
+    // sequence on the counter), and the barrier after it passes that on to
+    // the workgroup's loads.  The explicit wait for the stores before the
+    // barrier is the same order at the hardware level.
+    __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     int *count = p.merge_count + (r * p.heads + h) * kMlaCountStride;
     if (t == 0)
-        last = __hip_atomic_fetch_add(count, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+        last = __hip_atomic_fetch_add(count, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT) ==
                nchunks - 1;
     __syncthreads();
     if (!last) return;

@@ -74,7 +74,7 @@ __global__ __launch_bounds__(1024) void route_lists_kernel(RouteParams p) {
             atomicMin(&first_pos[id], q);
         } else if (e == 0) {
             p.list_pos[q] = -1;
-            *p.error = 1;  // prepare_route_tables rejects such ids (moonlight_metal.m:545)
+            if (*p.error == 0) *p.error = p.error_code;  // prepare_route_tables rejects such ids (moonlight_metal.m:545)
         }
     }
     __syncthreads();

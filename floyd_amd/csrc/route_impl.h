@@ -242,7 +242,7 @@ __device__ __forceinline__ void route_single_64(const RouteParams &p, int lane,
     const int slot = rs.slot;
     if (lane < K && !((rs.filled >> lane) & 1ull)) {
         p.list_pos[lane] = -1;
-        *p.error = 1;  // prepare_route_tables rejects such ids (moonlight_metal.m:545)
+        if (*p.error == 0) *p.error = p.error_code;  // prepare_route_tables rejects such ids (moonlight_metal.m:545)
     }
     const int n_unique = __popcll(rs.filled);
     if (lane == 0) *p.n_unique = n_unique;
@@ -444,8 +444,12 @@ __device__ inline void write_tasks(const RouteParams &p, const int *counts, cons
 // workgroup meets.  Global stores are not waited for (__syncthreads would
 // wait for them): nothing in the workgroup reads them back.
 __device__ __forceinline__ void lds_barrier() {
-    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+    // LDS-only release / acquire around the barrier: the compiler keeps every
+    // LDS access on its side of it (a plain s_barrier is no memory operation
+    // to it) and waits only for LDS operations (lgkmcnt), not for loads
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
     __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
 __device__ inline void small_tables(const RouteParams &p, RouteLds &L) {
@@ -464,7 +468,7 @@ __device__ inline void small_tables(const RouteParams &p, RouteLds &L) {
         const int e = L.ids[q];
         if (e < 0 || e >= E) {
             p.list_pos[q] = -1;
-            *p.error = 1;  // prepare_route_tables rejects such ids (moonlight_metal.m:545)
+            if (*p.error == 0) *p.error = p.error_code;  // prepare_route_tables rejects such ids (moonlight_metal.m:545)
             continue;
         }
         atomicMin(&L.first_pos[e], q);

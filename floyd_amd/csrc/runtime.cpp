@@ -85,6 +85,7 @@ struct LayerPlan {
 }  // namespace
 
 struct MoonlightModel {
+    DeviceContext *ctx = nullptr;  // the device the model lives on (current at open)
     ModelConfig cfg;
     std::vector<DeviceTensor> tensors;
     std::unordered_map<std::string, int> index;
@@ -130,7 +131,7 @@ struct MoonlightSession {
     float *shared_hidden = nullptr, *shared_out = nullptr, *dense_hidden = nullptr;
     float *shared_out2 = nullptr;  // second k half of the GEMM path's shared down
     float *moe_routed = nullptr;  // routed part of moonlight_test_moe
-    // MFMA path for batches of >= moe_gemm_min_rows() token rows
+    // MFMA path for batches of >= kMoeGemmMinRows token rows
     // quantised activations: three limb planes [3][max_batch][aq_width]
     int8_t *aq = nullptr;
     long aq_plane = 0;
@@ -169,6 +170,17 @@ struct MoonlightSession {
     hipEvent_t ev_start = nullptr, ev_stop = nullptr;
     double last_device_ms = 0.0;
 };
+
+namespace {
+
+// The model's device made current for the duration of an API call (the
+// caller's current device is restored afterwards).
+struct ApiScope : DeviceScope {
+    explicit ApiScope(const MoonlightModel *m) : DeviceScope(m && m->ctx ? m->ctx->device : -1) {}
+    explicit ApiScope(const MoonlightSession *s) : ApiScope(s ? s->model : nullptr) {}
+};
+
+}  // namespace
 
 namespace {
 
@@ -452,7 +464,7 @@ bool upload_container(MoonlightModel *m, const Container &ct, std::string *error
             stages.back().hi = a + n;
         }
     }
-    DeviceContext *ctx = context();
+    DeviceContext *ctx = m->ctx;
     void *stage[2] = {nullptr, nullptr};
     hipEvent_t done[2] = {nullptr, nullptr};
     bool ok = hipHostMalloc(&stage[0], kStage, hipHostMallocDefault) == hipSuccess &&
@@ -524,6 +536,7 @@ extern "C" int moonlight_model_open(MoonlightModel **out, const char *path, char
     std::string why;
     if (!ct.open(path, &why)) return set_error(error, error_size, "%s", why.c_str());
     MoonlightModel *m = new MoonlightModel();
+    m->ctx = ctx;
     m->cfg = ct.config();
     m->device_name = ctx->name;
     for (const TensorEntry &te : ct.tensors()) {
@@ -542,7 +555,10 @@ extern "C" int moonlight_model_open(MoonlightModel **out, const char *path, char
     return 1;
 }
 
-extern "C" void moonlight_model_close(MoonlightModel *model) { free_model(model); }
+extern "C" void moonlight_model_close(MoonlightModel *model) {
+    ApiScope api_scope(model);
+    free_model(model);
+}
 
 extern "C" const char *moonlight_device_name(const MoonlightModel *model) {
     return model ? model->device_name.c_str() : "(none)";
@@ -631,6 +647,7 @@ extern "C" int moonlight_model_create_synthetic(MoonlightModel **out,
         (sc->dense_bits != 8 && sc->dense_bits != 4))
         return set_error(error, error_size, "unsupported synthetic Moonlight config");
     MoonlightModel *m = new MoonlightModel();
+    m->ctx = ctx;
     ModelConfig &c = m->cfg;
     c.hidden_size = sc->hidden_size;
     c.layer_count = sc->layer_count;
@@ -804,7 +821,8 @@ extern "C" size_t moonlight_model_read_tensor(const MoonlightModel *model, const
     if (!model || !name || !dst) return 0;
     const DeviceTensor *t = find_tensor(model, name);
     if (!t || (size_t)t->nbytes > capacity) return 0;
-    DeviceContext *ctx = context();
+    ApiScope api_scope(model);
+    DeviceContext *ctx = model->ctx;
     if (!ctx || hipMemcpyAsync(dst, t->dev, (size_t)t->nbytes, hipMemcpyDeviceToHost,
                                ctx->stream) != hipSuccess ||
         hipStreamSynchronize(ctx->stream) != hipSuccess)
@@ -870,7 +888,7 @@ void free_session(MoonlightSession *s) {
     delete s;
 }
 
-hipStream_t stream_of(const MoonlightSession *) { return context()->stream; }
+hipStream_t stream_of(const MoonlightSession *s) { return s->model->ctx->stream; }
 
 // Synchronises the stream (one "command buffer" in the reference's sense).
 bool finish(MoonlightSession *s) {
@@ -895,15 +913,7 @@ bool to_host(MoonlightSession *s, void *dst, const void *src, size_t bytes) {
 // 53.5 us; 58 against 74 us at T = 3, 64 against 92 us at T = 4).  The
 // dense projections keep the GEMV up to 16 rows.
 constexpr int kGemmMinRows = 16;
-// MLH_MOE_GEMM_MIN_ROWS overrides the MoE switch (read once, at least 2).
-static int moe_gemm_min_rows() {
-    static const int v = [] {
-        const char *env = getenv("MLH_MOE_GEMM_MIN_ROWS");
-        const int n = env ? atoi(env) : 3;
-        return n < 2 ? 2 : n;
-    }();
-    return v;
-}
+constexpr int kMoeGemmMinRows = 3;
 
 bool use_gemm(const MoonlightSession *s, int fmt, int rows, int in_w) {
     return rows >= kGemmMinRows && s->aq && in_w <= s->aq_width && qgemm_shape_ok(fmt, in_w);
@@ -1062,14 +1072,8 @@ int attention(MoonlightSession *s, int layer, const float *x, int rows, int posi
 
 // Expert GEMV batches of at least this many token rows split their inputs
 // into limb rows once per stage (limb_quantise_rows) rather than in every
-// workgroup.  MLH_PRESPLIT_MIN_ROWS overrides (read once).
-static int presplit_min_rows() {
-    static const int v = [] {
-        const char *env = getenv("MLH_PRESPLIT_MIN_ROWS");
-        return env ? atoi(env) : 2;
-    }();
-    return v;
-}
+// workgroup.
+constexpr int kPresplitMinRows = 2;
 
 // The MFMA router (32 x 32 tiles, one workgroup per tile) has the
 // parallelism for prefill batches; fewer rows take the GEMV.
@@ -1090,7 +1094,7 @@ static bool moe_uses_gemm(const MoonlightSession *s, int layer, int rows) {
     const ModelConfig &c = s->model->cfg;
     const LayerPlan &lp = s->model->layers[layer];
     const int sw = c.moe_intermediate_size * c.shared_expert_count;
-    return rows >= moe_gemm_min_rows() && s->hq && qgemm_shape_ok(lp.expert_fmt, c.hidden_size) &&
+    return rows >= kMoeGemmMinRows && s->hq && qgemm_shape_ok(lp.expert_fmt, c.hidden_size) &&
            qgemm_shape_ok(lp.expert_fmt, c.moe_intermediate_size) &&
            qgemm_shape_ok(lp.sh_gate.fmt, c.hidden_size) && qgemm_shape_ok(lp.sh_gate.fmt, sw) &&
            c.hidden_size <= s->aq_width && sw <= s->aq_width;
@@ -1104,7 +1108,7 @@ int router_fuse_parts(const MoonlightSession *s, int layer) {
     const ModelConfig &c = s->model->cfg;
     const LayerPlan &lp = s->model->layers[layer];
     if (lp.dense || lp.router.fmt != kF32 || c.expert_count > 64 || c.experts_per_token > 64 ||
-        presplit_min_rows() <= 1 || !lp.post_norm || ((uintptr_t)lp.router.w & 15u) ||
+        !lp.post_norm || ((uintptr_t)lp.router.w & 15u) ||
         c.hidden_size % 4)
         return 0;
     GemvParams p;
@@ -1161,6 +1165,7 @@ int route(MoonlightSession *s, int layer, const float *x, int rows, const float 
     r.list_slots = s->list_slots;
     r.list_pos = s->list_pos;
     r.error = s->route_error;
+    r.error_code = layer + 1;
     r.fixed_ids = fixed && s->fixed_rows >= rows ? s->fixed_ids : nullptr;
     r.expert_table = lp.expert_table;
     r.tasks = s->expert_tasks;
@@ -1175,7 +1180,7 @@ int route(MoonlightSession *s, int layer, const float *x, int rows, const float 
         *inline_route = r;
         return kOk;
     }
-    if (inline_route && rows == 1 && c.expert_count <= 64 && rows < presplit_min_rows()) {
+    if (inline_route && rows == 1 && c.expert_count <= 64 && rows < kPresplitMinRows) {
         *inline_route = r;
         return kOk;
     }
@@ -1219,7 +1224,7 @@ int experts(MoonlightSession *s, int layer, const float *x, int rows, const floa
     f.list_rows = s->list_rows;
     f.tasks = s->expert_tasks;  // written by route() (or by stage 0 routing inline)
     if (inline_route && inline_route->logits) f.route = *inline_route;
-    if (rows >= presplit_min_rows() && c.hidden_size % 32 == 0 &&
+    if (rows >= kPresplitMinRows && c.hidden_size % 32 == 0 &&
         c.moe_intermediate_size % 32 == 0) {
         f.limb_x = s->limb_x;
         f.limb_xs = s->limb_xs;
@@ -1314,6 +1319,13 @@ int experts(MoonlightSession *s, int layer, const float *x, int rows, const floa
     return moe_combine(cb, stream_of(s));
 }
 
+// Token rows of one routing call: each routes at most kRouteMaxPositions
+// (row, slot) positions (the route-table kernels keep them in LDS).
+int moe_chunk_rows(const ModelConfig &c) {
+    const int k = c.experts_per_token > 0 ? c.experts_per_token : 1;
+    return kRouteMaxPositions / k;
+}
+
 // The kernels of one forward over `count` token rows at `start` (embed,
 // layers, final norm + lm_head), reading the ids and the position uploaded
 // to step_dev.  With `graph` the attend grids are sized for the whole
@@ -1346,34 +1358,32 @@ bool enqueue_forward(MoonlightSession *s, int count, int start, float *layer_out
                  gemv_rows(s, lp.down, s->dense_hidden, count, c.dense_intermediate_size,
                            c.hidden_size, s->h, nullptr, s->h) == kOk;
         } else if (ok) {
-            int *trace = s->route_trace + (size_t)l * s->options.max_batch * c.experts_per_token;
-            RouteParams inline_r;
-            ok = route(s, l, s->h, count, lp.post_norm, trace, false, &inline_r, fused) == kOk;
-            ok = ok &&
-                 experts(s, l, s->h, count, lp.post_norm, s->h, s->h, nullptr, &inline_r) == kOk;
-            // the router logits exist once the first expert launch has run
-            // (they come from o_proj's partials there when fused)
-            if (ok && s->router_trace)
-                ok = hipMemcpyAsync(s->router_trace +
-                                        (size_t)l * s->options.max_batch * c.expert_count,
-                                    s->router_logits, (size_t)count * c.expert_count * 4,
-                                    hipMemcpyDeviceToDevice, st) == hipSuccess;
+            // one routing call covers at most kRouteMaxPositions (row, slot)
+            // positions: larger batches run the MoE block in row chunks (a
+            // row's experts are summed in its slot order, so the chunks do
+            // not change any row's arithmetic)
+            const int chunk = moe_chunk_rows(c);
+            for (int r0 = 0; ok && r0 < count; r0 += chunk) {
+                const int n = std::min(chunk, count - r0);
+                float *hr = s->h + (size_t)r0 * H;
+                const size_t row_base = (size_t)l * s->options.max_batch + (size_t)r0;
+                int *trace = s->route_trace + row_base * c.experts_per_token;
+                RouteParams inline_r;
+                ok = route(s, l, hr, n, lp.post_norm, trace, false, &inline_r, fused) == kOk;
+                ok = ok && experts(s, l, hr, n, lp.post_norm, hr, hr, nullptr, &inline_r) == kOk;
+                // the router logits exist once the first expert launch has run
+                // (they come from o_proj's partials there when fused)
+                if (ok && s->router_trace)
+                    ok = hipMemcpyAsync(s->router_trace + row_base * c.expert_count,
+                                        s->router_logits, (size_t)n * c.expert_count * 4,
+                                        hipMemcpyDeviceToDevice, st) == hipSuccess;
+            }
         }
         if (ok && layer_outputs)
             ok = to_host(s, layer_outputs + (size_t)l * count * H, s->h, (size_t)count * H * 4);
     }
     return ok && gemv_rows(s, m->lm_head, s->h + (size_t)(count - 1) * H, 1, c.hidden_size,
                            c.vocab_size, s->logits, m->final_norm) == kOk;
-}
-
-// Decode steps replay one captured graph unless MLH_DECODE_GRAPH=0 (read
-// once).
-static bool decode_graph_enabled() {
-    static const bool v = [] {
-        const char *env = getenv("MLH_DECODE_GRAPH");
-        return !env || atoi(env) != 0;
-    }();
-    return v;
 }
 
 // Captures the one-row decode kernels into s->decode_exec.  The capture runs
@@ -1451,9 +1461,14 @@ int forward(MoonlightSession *s, const int *ids, int count, int start, float *la
     if (pick && !sampler_ready(s))
         return set_error(error, error_size, "Moonlight sampler allocation failed");
     hipStream_t st = stream_of(s);
+    // MOONLIGHT_PROFILE (moonlight_metal.m:1899, 1932-1937, 1972-1979): one
+    // line per submission on stderr; a forward here is one submission
+    const bool profile = getenv("MOONLIGHT_PROFILE") != nullptr;
+    const double command_start = profile ? monotonic_seconds() : 0.0;
+    double wait_start = 0.0;
     s->host_step[0] = start;
     memcpy(s->host_ids, ids, (size_t)count * sizeof(int));
-    const bool decode = count == 1 && !layer_outputs && decode_graph_enabled() &&
+    const bool decode = count == 1 && !layer_outputs &&
                         !s->decode_graph_off && !s->decode_graph_failed;
     // the first decode runs eagerly (lazy per-kernel set-up happens outside
     // any capture); the second captures
@@ -1475,6 +1490,7 @@ int forward(MoonlightSession *s, const int *ids, int count, int start, float *la
          (!last_logits ||
           to_host(s, s->host_logits, s->logits, (size_t)c.vocab_size * sizeof(float))) &&
          to_host(s, s->host_flag, s->route_error, sizeof(int));
+    if (profile) wait_start = monotonic_seconds();
     if (!finish(s) || !ok) {
         // the device state of a partial forward is unusable: invalidate the caches
         for (int l = 0; l < c.layer_count; ++l)
@@ -1482,13 +1498,23 @@ int forward(MoonlightSession *s, const int *ids, int count, int start, float *la
         return set_error(error, error_size, "Moonlight forward failed on the device: %s",
                          hipGetErrorString(hipGetLastError()));
     }
+    const double wait_end = profile ? monotonic_seconds() : 0.0;
     for (int l = 0; l < c.layer_count; ++l) s->kv_lengths[l] = start + count;
     if (last_logits) memcpy(last_logits, s->host_logits, (size_t)c.vocab_size * sizeof(float));
-    if (*s->host_flag) return set_error(error, error_size, "Moonlight fast route table failed");
+    if (*s->host_flag)
+        return set_error(error, error_size, "Moonlight fast route table failed at layer %d",
+                         *s->host_flag - 1);
     // the forward is committed: a failed token choice below leaves the
     // session at the new position, ready for the next decode
     float ms = 0.0f;
     if (hipEventElapsedTime(&ms, s->ev_start, s->ev_stop) == hipSuccess) s->last_device_ms = ms;
+    if (profile)
+        fprintf(stderr,
+                "moonlight profile rows=%d start=%d layers=%d graph=%d encode=%.3f wait=%.3f "
+                "gpu=%.3f ms\n",
+                count, start, c.layer_count, decode && s->decode_exec ? 1 : 0,
+                (wait_start - command_start) * 1000.0, (wait_end - wait_start) * 1000.0,
+                s->last_device_ms);
     s->position = start + count;
     s->last_forward_rows = count;
     if (pick) {
@@ -1504,6 +1530,7 @@ int forward(MoonlightSession *s, const int *ids, int count, int start, float *la
 extern "C" int moonlight_session_create(MoonlightSession **out, MoonlightModel *model,
                                         const MoonlightOptions *options, char *error,
                                         size_t error_size) {
+    ApiScope api_scope(model);
     if (!out || !model || !options)
         return set_error(error, error_size, "model and session options are required");
     *out = nullptr;
@@ -1522,12 +1549,6 @@ extern "C" int moonlight_session_create(MoonlightSession **out, MoonlightModel *
         return set_error(error, error_size, "unsupported Moonlight MLA dimensions");
     if (c.q_lora_rank)
         return set_error(error, error_size, "unsupported Moonlight MLA dimensions");
-    // the device routing of one forward covers max_batch * top_k positions
-    if ((int64_t)options->max_batch * c.experts_per_token > kRouteMaxPositions)
-        return set_error(error, error_size,
-                         "Moonlight max_batch %d exceeds the device routing limit of %d rows",
-                         options->max_batch,
-                         kRouteMaxPositions / (c.experts_per_token > 0 ? c.experts_per_token : 1));
     MoonlightSession *s = new MoonlightSession();
     s->model = model;
     s->options = *options;
@@ -1619,7 +1640,7 @@ extern "C" int moonlight_session_create(MoonlightSession **out, MoonlightModel *
                       hipHostMallocDefault) == hipSuccess &&
         hipEventCreate(&s->ev_start) == hipSuccess && hipEventCreate(&s->ev_stop) == hipSuccess;
     bool gemm_ok = ok;
-    if (ok && options->max_batch >= moe_gemm_min_rows()) {
+    if (ok && options->max_batch >= kMoeGemmMinRows) {
         // MFMA prefill scratch: quantised activations of the widest matmul
         // input, quantised expert hidden rows, per-stage task tables
         const int widths[] = {c.hidden_size, c.head_count * c.value_dim,
@@ -1647,9 +1668,13 @@ extern "C" int moonlight_session_create(MoonlightSession **out, MoonlightModel *
     return 1;
 }
 
-extern "C" void moonlight_session_destroy(MoonlightSession *session) { free_session(session); }
+extern "C" void moonlight_session_destroy(MoonlightSession *session) {
+    ApiScope api_scope(session);
+    free_session(session);
+}
 
 extern "C" void moonlight_session_reset(MoonlightSession *s) {
+    ApiScope api_scope(s);
     if (!s) return;
     s->position = 0;
     s->last_forward_rows = 0;
@@ -1674,6 +1699,7 @@ extern "C" MoonlightStats moonlight_session_stats(const MoonlightSession *s) {
 
 extern "C" int moonlight_session_prefill(MoonlightSession *s, const int *ids, int count,
                                          float *last_logits, char *error, size_t error_size) {
+    ApiScope api_scope(s);
     if (!s || !ids || !last_logits || count <= 0 || count > s->options.max_batch ||
         count > s->options.context_size)
         return set_error(error, error_size, "invalid Moonlight prefill request");
@@ -1688,6 +1714,7 @@ extern "C" int moonlight_session_prefill(MoonlightSession *s, const int *ids, in
 
 extern "C" int moonlight_session_append(MoonlightSession *s, const int *ids, int count,
                                         float *last_logits, char *error, size_t error_size) {
+    ApiScope api_scope(s);
     if (!s || !ids || !last_logits || count <= 0 || count > s->options.max_batch ||
         s->position <= 0 || s->position + count > s->options.context_size)
         return set_error(error, error_size, "invalid Moonlight append request");
@@ -1700,6 +1727,7 @@ extern "C" int moonlight_session_append(MoonlightSession *s, const int *ids, int
 
 extern "C" int moonlight_session_decode(MoonlightSession *s, int token, float *logits,
                                         char *error, size_t error_size) {
+    ApiScope api_scope(s);
     if (!s || !logits || s->position < 0 || s->position >= s->options.context_size)
         return set_error(error, error_size, "invalid Moonlight decode request");
     const double t0 = monotonic_seconds();
@@ -1723,6 +1751,7 @@ static double random_unit(uint64_t *state) {
 extern "C" int moonlight_session_sample(MoonlightSession *s, float temperature, float top_p,
                                         uint64_t *rng_state, int *token, char *error,
                                         size_t error_size) {
+    ApiScope api_scope(s);
     if (!s || !token || s->position <= 0 || (temperature > 0.0f && !rng_state))
         return set_error(error, error_size, "invalid Moonlight sample request");
     if (!sampler_ready(s)) return set_error(error, error_size, "Moonlight sampler allocation failed");
@@ -1744,6 +1773,7 @@ extern "C" int moonlight_session_sample(MoonlightSession *s, float temperature, 
 extern "C" int moonlight_session_decode_sample(MoonlightSession *s, int token, float temperature,
                                                float top_p, uint64_t *rng_state, int *next_token,
                                                char *error, size_t error_size) {
+    ApiScope api_scope(s);
     if (!s || !next_token || s->position < 0 || s->position >= s->options.context_size ||
         (temperature > 0.0f && !rng_state))
         return set_error(error, error_size, "invalid Moonlight decode request");
@@ -1770,6 +1800,7 @@ extern "C" int moonlight_session_decode_sample(MoonlightSession *s, int token, f
 extern "C" int moonlight_test_prefill_layers(MoonlightSession *s, const int *ids, int count,
                                              float *layer_outputs, float *last_logits,
                                              char *error, size_t error_size) {
+    ApiScope api_scope(s);
     if (!s || !ids || !layer_outputs || !last_logits || count <= 0 ||
         count > s->options.max_batch || s->position != 0)
         return set_error(error, error_size, "invalid Moonlight layer trace request");
@@ -1785,6 +1816,7 @@ extern "C" int moonlight_test_prefill_layers(MoonlightSession *s, const int *ids
 // ---------------------------------------------------------------------------
 
 extern "C" int moonlight_test_embed(MoonlightSession *s, const int *ids, int count, float *output) {
+    ApiScope api_scope(s);
     if (!s || !ids || !output || count <= 0 || count > s->options.max_batch) return 0;
     const ModelConfig &c = s->model->cfg;
     if (!s->model->embed) return 0;
@@ -1802,6 +1834,7 @@ extern "C" int moonlight_test_embed(MoonlightSession *s, const int *ids, int cou
 extern "C" int moonlight_test_rmsnorm(MoonlightSession *s, const float *input,
                                       const char *weight_name, int rows, int width,
                                       float *output) {
+    ApiScope api_scope(s);
     if (!s || !input || !weight_name || !output || rows <= 0 || width <= 0 ||
         rows > s->options.max_batch)
         return 0;
@@ -1820,6 +1853,7 @@ extern "C" int moonlight_test_rmsnorm(MoonlightSession *s, const float *input,
 extern "C" int moonlight_test_matmul(MoonlightSession *s, const char *weight_name,
                                      const float *input, int rows, int input_width,
                                      int output_width, float *output) {
+    ApiScope api_scope(s);
     if (!s || !weight_name || !input || !output || rows <= 0 || input_width <= 0 ||
         output_width <= 0 || rows > s->options.max_batch)
         return 0;
@@ -1839,6 +1873,7 @@ extern "C" int moonlight_test_matmul(MoonlightSession *s, const char *weight_nam
 
 extern "C" int moonlight_test_attention(MoonlightSession *s, int layer, const float *input,
                                         int rows, int position, float *output) {
+    ApiScope api_scope(s);
     if (!s || !input || !output || rows <= 0 || position < 0 || rows > s->options.max_batch)
         return 0;
     const ModelConfig &c = s->model->cfg;
@@ -1863,12 +1898,13 @@ extern "C" int moonlight_test_kv_length(const MoonlightSession *s, int layer) {
 
 extern "C" int moonlight_test_copy_kv(const MoonlightSession *s, int layer, float *latent,
                                       float *rope, int capacity) {
+    ApiScope api_scope(s);
     if (!s || !latent || !rope || capacity < 0) return 0;
     const ModelConfig &c = s->model->cfg;
     if (layer < 0 || layer >= c.layer_count || capacity < s->kv_lengths[layer]) return 0;
     const size_t n = (size_t)s->kv_lengths[layer];
     const size_t ctx = (size_t)s->options.context_size;
-    hipStream_t st = context()->stream;
+    hipStream_t st = s->model->ctx->stream;
     bool ok = hipMemcpyAsync(latent, s->latent_kv + (size_t)layer * ctx * c.kv_lora_rank,
                              n * c.kv_lora_rank * sizeof(float), hipMemcpyDeviceToHost,
                              st) == hipSuccess &&
@@ -1882,6 +1918,7 @@ extern "C" int moonlight_test_copy_kv(const MoonlightSession *s, int layer, floa
 extern "C" int moonlight_test_moe(MoonlightSession *s, int layer, const float *input, int rows,
                                   int *route_ids, float *route_weights, float *router_scores,
                                   float *routed_output, float *shared_output, float *output) {
+    ApiScope api_scope(s);
     if (!s || !input || !output || rows <= 0 || rows > s->options.max_batch) return 0;
     const ModelConfig &c = s->model->cfg;
     if (layer < c.first_dense_layer_count || layer >= c.layer_count || c.expert_count <= 0 ||
@@ -1889,29 +1926,42 @@ extern "C" int moonlight_test_moe(MoonlightSession *s, int layer, const float *i
         return 0;
     if (!s->model->layers[layer].error.empty()) return 0;
     const size_t hidden_bytes = (size_t)rows * c.hidden_size * sizeof(float);
-    const size_t route_bytes = (size_t)rows * c.experts_per_token * sizeof(float);
-    const size_t score_bytes = (size_t)rows * c.expert_count * sizeof(float);
     hipStream_t st = stream_of(s);
-    // submission 1: router + top-k (+ device route tables)
-    bool ok = to_device(s, s->tmp, input, hidden_bytes) &&
-              hipMemsetAsync(s->route_error, 0, sizeof(int), st) == hipSuccess &&
-              route(s, layer, s->tmp, rows, nullptr, nullptr, true) == kOk &&
-              to_host(s, s->host_flag, s->route_error, sizeof(int));
-    if (!finish(s) || !ok || *s->host_flag) return 0;
-    // submission 2: experts, shared expert, routed + shared (no residual)
-    ok = experts(s, layer, s->tmp, rows, nullptr, nullptr, s->h, s->moe_routed) == kOk;
-    const float *routed_dev = s->moe_routed;
-    if (ok && route_ids) ok = to_host(s, route_ids, s->route_ids, route_bytes);
-    if (ok && route_weights) ok = to_host(s, route_weights, s->route_weights, route_bytes);
-    if (ok && router_scores) ok = to_host(s, router_scores, s->router_logits, score_bytes);
-    if (ok && routed_output) ok = to_host(s, routed_output, routed_dev, hidden_bytes);
-    if (ok && shared_output) ok = to_host(s, shared_output, s->shared_out, hidden_bytes);
-    if (ok) ok = to_host(s, output, s->h, hidden_bytes);
-    return finish(s) && ok;
+    if (!to_device(s, s->tmp, input, hidden_bytes)) return 0;
+    // two submissions per routing chunk (moe_chunk_rows rows; one chunk up to
+    // 2730 Moonlight rows): router + top-k (+ device route tables), then the
+    // experts, the shared expert and routed + shared (no residual)
+    const int chunk = moe_chunk_rows(c);
+    const size_t H = (size_t)c.hidden_size, K = (size_t)c.experts_per_token;
+    const size_t E = (size_t)c.expert_count;
+    for (int r0 = 0; r0 < rows; r0 += chunk) {
+        const int n = std::min(chunk, rows - r0);
+        const float *x = s->tmp + (size_t)r0 * H;
+        bool ok = hipMemsetAsync(s->route_error, 0, sizeof(int), st) == hipSuccess &&
+                  route(s, layer, x, n, nullptr, nullptr, true) == kOk &&
+                  to_host(s, s->host_flag, s->route_error, sizeof(int));
+        if (!finish(s) || !ok || *s->host_flag) return 0;
+        float *out_dev = s->h + (size_t)r0 * H;
+        float *routed_dev = s->moe_routed + (size_t)r0 * H;
+        ok = experts(s, layer, x, n, nullptr, nullptr, out_dev, routed_dev) == kOk;
+        const size_t rb = (size_t)n * K * sizeof(float), hb = (size_t)n * H * sizeof(float);
+        if (ok && route_ids) ok = to_host(s, route_ids + r0 * K, s->route_ids, rb);
+        if (ok && route_weights) ok = to_host(s, route_weights + r0 * K, s->route_weights, rb);
+        if (ok && router_scores)
+            ok = to_host(s, router_scores + r0 * E, s->router_logits, (size_t)n * E * sizeof(float));
+        if (ok && shared_output) ok = to_host(s, shared_output + r0 * H, s->shared_out, hb);
+        if (r0 + n == rows) {
+            if (ok && routed_output) ok = to_host(s, routed_output, s->moe_routed, hidden_bytes);
+            if (ok) ok = to_host(s, output, s->h, hidden_bytes);
+        }
+        if (!finish(s) || !ok) return 0;
+    }
+    return 1;
 }
 
 extern "C" int moonlight_test_dense_mlp(MoonlightSession *s, int layer, const float *input,
                                         int rows, float *output) {
+    ApiScope api_scope(s);
     if (!s || !input || !output || rows <= 0 || rows > s->options.max_batch) return 0;
     const ModelConfig &c = s->model->cfg;
     if (layer < 0 || layer >= c.layer_count || !s->model->layers[layer].dense ||
@@ -1930,10 +1980,11 @@ extern "C" int moonlight_test_dense_mlp(MoonlightSession *s, int layer, const fl
 
 extern "C" int moonlight_test_copy_routes(const MoonlightSession *s, int layer, int *route_ids,
                                           int capacity) {
+    ApiScope api_scope(s);
     if (!s || !route_ids || capacity < s->last_forward_rows) return 0;
     const ModelConfig &c = s->model->cfg;
     if (layer < c.first_dense_layer_count || layer >= c.layer_count) return 0;
-    hipStream_t st = context()->stream;
+    hipStream_t st = s->model->ctx->stream;
     const size_t n = (size_t)s->last_forward_rows * c.experts_per_token;
     const int *src = s->route_trace + (size_t)layer * s->options.max_batch * c.experts_per_token;
     return hipMemcpyAsync(route_ids, src, n * sizeof(int), hipMemcpyDeviceToHost, st) ==
@@ -1949,6 +2000,7 @@ extern "C" int moonlight_test_copy_routes(const MoonlightSession *s, int layer, 
 
 extern "C" int moonlight_session_fill_kv(MoonlightSession *s, int layer, int length,
                                          uint64_t seed) {
+    ApiScope api_scope(s);
     if (!s || length < 0 || length > s->options.context_size) return 0;
     const ModelConfig &c = s->model->cfg;
     if (layer >= c.layer_count) return 0;
@@ -1969,71 +2021,136 @@ extern "C" int moonlight_session_fill_kv(MoonlightSession *s, int layer, int len
     return hipStreamSynchronize(st) == hipSuccess ? 1 : 0;
 }
 
+namespace {
+
+// Inputs of the timing hooks: `count` blocks of rows x hidden values ~N(0, 1),
+// block b drawn from seed + b (one block when count is 1).  Device memory of
+// the hook's own, released by the caller with hipFree.
+float *timing_inputs(MoonlightSession *s, int rows, int count, uint64_t seed) {
+    const ModelConfig &c = s->model->cfg;
+    const size_t block = (size_t)rows * c.hidden_size;
+    float *pool = nullptr;
+    if (hipMalloc(&pool, block * count * sizeof(float)) != hipSuccess) return nullptr;
+    for (int b = 0; b < count; ++b)
+        if (fill_normal(pool + block * b, (int64_t)block, seed + (uint64_t)b, 0.0f, 1.0f, 0,
+                        stream_of(s)) != kOk) {
+            (void)hipFree(pool);
+            return nullptr;
+        }
+    return pool;
+}
+
+// The layers a timing hook cycles through: `layer` alone, or with layer < 0
+// every usable layer of the kind (MoE layers when `moe`).
+std::vector<int> timing_layers(const MoonlightSession *s, int layer, bool moe) {
+    const ModelConfig &c = s->model->cfg;
+    std::vector<int> out;
+    for (int l = 0; l < c.layer_count; ++l) {
+        const LayerPlan &lp = s->model->layers[l];
+        if ((layer >= 0 && l != layer) || !lp.error.empty() ||
+            (moe && (l < c.first_dense_layer_count || lp.dense)))
+            continue;
+        out.push_back(l);
+    }
+    return out;
+}
+
+}  // namespace
+
 extern "C" int moonlight_session_time_moe(MoonlightSession *s, int layer, int rows, uint64_t seed,
                                           int warmup, int iters, double *avg_us,
                                           int *unique_experts) {
+    ApiScope api_scope(s);
     if (!s || !avg_us || rows <= 0 || rows > s->options.max_batch || iters <= 0 || warmup < 0)
         return 0;
     const ModelConfig &c = s->model->cfg;
-    if (layer < c.first_dense_layer_count || layer >= c.layer_count ||
-        !s->model->layers[layer].error.empty())
-        return 0;
-    const LayerPlan &lp = s->model->layers[layer];
+    if (layer >= c.layer_count || rows > moe_chunk_rows(c)) return 0;
+    const std::vector<int> layers = timing_layers(s, layer, true);
+    if (layers.empty() || (layer >= 0 && layers[0] != layer)) return 0;
     hipStream_t st = stream_of(s);
-    if (fill_normal(s->tmp, (int64_t)rows * c.hidden_size, seed, 0.0f, 1.0f, 0, st) != kOk)
-        return 0;
-    auto pass = [&]() {
+    // a fixed layer reads one input block; a rotation draws a fresh block for
+    // every pass (warm-up passes included)
+    const int passes = warmup + iters;
+    const int blocks = layer >= 0 ? 1 : passes;
+    const size_t block = (size_t)rows * c.hidden_size;
+    float *inputs = timing_inputs(s, rows, blocks, seed);
+    if (!inputs) return 0;
+    auto pass = [&](int i) {
+        const int l = layers[(size_t)i % layers.size()];
+        const LayerPlan &lp = s->model->layers[l];
+        const float *x = inputs + block * (size_t)(i % blocks);
         RouteParams inline_r;
-        return route(s, layer, s->tmp, rows, lp.post_norm, nullptr, true, &inline_r) == kOk &&
-               experts(s, layer, s->tmp, rows, lp.post_norm, s->tmp, s->h, nullptr, &inline_r) ==
-                   kOk;
+        return route(s, l, x, rows, lp.post_norm, nullptr, true, &inline_r) == kOk &&
+               experts(s, l, x, rows, lp.post_norm, x, s->h, nullptr, &inline_r) == kOk;
     };
     bool ok = hipMemsetAsync(s->route_error, 0, sizeof(int), st) == hipSuccess;
-    for (int i = 0; ok && i < warmup; ++i) ok = pass();
+    for (int i = 0; ok && i < warmup; ++i) ok = pass(i);
     ok = ok && hipEventRecord(s->ev_start, st) == hipSuccess;
-    for (int i = 0; ok && i < iters; ++i) ok = pass();
+    for (int i = warmup; ok && i < passes; ++i) ok = pass(i);
     ok = ok && hipEventRecord(s->ev_stop, st) == hipSuccess &&
-         to_host(s, s->host_flag, s->route_error, sizeof(int)) &&
-         to_host(s, s->host_ids, s->n_unique, sizeof(int));
-    if (!finish(s) || !ok || *s->host_flag) return 0;
+         to_host(s, s->host_flag, s->route_error, sizeof(int));
     float ms = 0.0f;
-    if (hipEventElapsedTime(&ms, s->ev_start, s->ev_stop) != hipSuccess) return 0;
+    ok = finish(s) && ok && !*s->host_flag &&
+         hipEventElapsedTime(&ms, s->ev_start, s->ev_stop) == hipSuccess;
+    // the distinct experts of every timed pass, from an untimed replay of the
+    // same passes (routing is deterministic)
+    int *counts = nullptr;
+    if (ok && unique_experts) {
+        ok = hipHostMalloc((void **)&counts, (size_t)iters * sizeof(int), hipHostMallocDefault) ==
+             hipSuccess;
+        for (int i = warmup; ok && i < passes; ++i)
+            ok = pass(i) && to_host(s, counts + (i - warmup), s->n_unique, sizeof(int));
+        ok = finish(s) && ok;
+        long total = 0;
+        for (int i = 0; ok && i < iters; ++i) total += counts[i];
+        if (ok) *unique_experts = (int)total;
+    }
+    if (counts) (void)hipHostFree(counts);
+    (void)hipFree(inputs);
+    if (!ok) return 0;
     *avg_us = (double)ms * 1000.0 / iters;
-    if (unique_experts) *unique_experts = s->host_ids[0];
     return 1;
 }
 
 extern "C" int moonlight_session_time_attention(MoonlightSession *s, int layer, int rows,
                                                 int position, uint64_t seed, int warmup,
                                                 int iters, double *avg_us) {
+    ApiScope api_scope(s);
     if (!s || !avg_us || rows <= 0 || rows > s->options.max_batch || iters <= 0 || warmup < 0 ||
         position < 0 || position + rows > s->options.context_size)
         return 0;
     const ModelConfig &c = s->model->cfg;
-    if (layer < 0 || layer >= c.layer_count || c.q_lora_rank ||
-        !s->model->layers[layer].error.empty())
-        return 0;
-    const LayerPlan &lp = s->model->layers[layer];
+    if (layer >= c.layer_count || c.q_lora_rank) return 0;
+    const std::vector<int> layers = timing_layers(s, layer, false);
+    if (layers.empty() || (layer >= 0 && layers[0] != layer)) return 0;
     hipStream_t st = stream_of(s);
-    if (fill_normal(s->tmp, (int64_t)rows * c.hidden_size, seed, 0.0f, 1.0f, 0, st) != kOk)
-        return 0;
-    auto pass = [&]() {
-        return attention(s, layer, s->tmp, rows, position, s->h, lp.input_norm, s->tmp) == kOk;
+    const int passes = warmup + iters;
+    const int blocks = layer >= 0 ? 1 : passes;
+    const size_t block = (size_t)rows * c.hidden_size;
+    float *inputs = timing_inputs(s, rows, blocks, seed);
+    if (!inputs) return 0;
+    auto pass = [&](int i) {
+        const int l = layers[(size_t)i % layers.size()];
+        const float *x = inputs + block * (size_t)(i % blocks);
+        return attention(s, l, x, rows, position, s->h, s->model->layers[l].input_norm, x) ==
+               kOk;
     };
     bool ok = true;
-    for (int i = 0; ok && i < warmup; ++i) ok = pass();
+    for (int i = 0; ok && i < warmup; ++i) ok = pass(i);
     ok = ok && hipEventRecord(s->ev_start, st) == hipSuccess;
-    for (int i = 0; ok && i < iters; ++i) ok = pass();
+    for (int i = warmup; ok && i < passes; ++i) ok = pass(i);
     ok = ok && hipEventRecord(s->ev_stop, st) == hipSuccess;
-    if (!finish(s) || !ok) return 0;
     float ms = 0.0f;
-    if (hipEventElapsedTime(&ms, s->ev_start, s->ev_stop) != hipSuccess) return 0;
+    ok = finish(s) && ok && hipEventElapsedTime(&ms, s->ev_start, s->ev_stop) == hipSuccess;
+    (void)hipFree(inputs);
+    if (!ok) return 0;
     *avg_us = (double)ms * 1000.0 / iters;
     return 1;
 }
 
 extern "C" int moonlight_session_fix_routes(MoonlightSession *s, const int *expert_ids,
                                             int rows) {
+    ApiScope api_scope(s);
     if (!s) return 0;
     const ModelConfig &c = s->model->cfg;
     if (!expert_ids || rows <= 0) {
@@ -2060,6 +2177,7 @@ extern "C" int moonlight_session_fix_routes(MoonlightSession *s, const int *expe
 }
 
 extern "C" int moonlight_session_decode_graph(MoonlightSession *s, int enable) {
+    ApiScope api_scope(s);
     if (!s) return 0;
     if (enable == 0) {
         s->decode_graph_off = true;
@@ -2074,10 +2192,11 @@ extern "C" int moonlight_session_copy_route_tables(const MoonlightSession *s, in
                                                    int *n_unique, int *unique, int *counts,
                                                    int *offsets, int *list_rows,
                                                    int *list_slots, int *list_pos) {
+    ApiScope api_scope(s);
     if (!s || rows <= 0 || rows > s->options.max_batch) return 0;
     const ModelConfig &c = s->model->cfg;
     const size_t E = (size_t)c.expert_count, n = (size_t)rows * c.experts_per_token;
-    hipStream_t st = context()->stream;
+    hipStream_t st = s->model->ctx->stream;
     bool ok = true;
     auto copy = [&](int *dst, const int *src, size_t count) {
         if (ok && dst)
@@ -2095,6 +2214,7 @@ extern "C" int moonlight_session_copy_route_tables(const MoonlightSession *s, in
 }
 
 extern "C" int moonlight_session_trace_router(MoonlightSession *s, int enable) {
+    ApiScope api_scope(s);
     if (!s) return 0;
     drop_decode_graph(s);
     if (!enable) {
@@ -2113,12 +2233,13 @@ extern "C" int moonlight_session_trace_router(MoonlightSession *s, int enable) {
 
 extern "C" int moonlight_session_copy_router_trace(const MoonlightSession *s, int layer,
                                                    float *logits, int capacity_rows) {
+    ApiScope api_scope(s);
     if (!s || !logits || !s->router_trace || capacity_rows < s->last_forward_rows) return 0;
     const ModelConfig &c = s->model->cfg;
     if (layer < c.first_dense_layer_count || layer >= c.layer_count ||
         s->model->layers[layer].dense)
         return 0;
-    hipStream_t st = context()->stream;
+    hipStream_t st = s->model->ctx->stream;
     const size_t E = (size_t)c.expert_count;
     return hipMemcpyAsync(logits, s->router_trace + (size_t)layer * s->options.max_batch * E,
                           (size_t)s->last_forward_rows * E * sizeof(float),

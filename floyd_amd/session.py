@@ -337,13 +337,17 @@ class Session:
         return out if ok else None
 
     def time_moe(self, layer, rows, seed=7, warmup=5, iters=50):
+        """(us per pass, mean distinct experts per timed pass); layer -1
+        cycles through every MoE layer with a fresh input per pass."""
         us, uniq = C.c_double(), C.c_int()
         if not lib().moonlight_session_time_moe(self.handle, layer, rows, seed, warmup, iters,
                                                 C.byref(us), C.byref(uniq)):
             raise SessionError("time_moe failed")
-        return us.value, uniq.value
+        return us.value, uniq.value / iters
 
     def time_attention(self, layer, rows, position, seed=7, warmup=5, iters=50):
+        """us per pass; layer -1 cycles through every layer (each layer's
+        cache filled up to `position`) with a fresh input per pass."""
         us = C.c_double()
         if not lib().moonlight_session_time_attention(self.handle, layer, rows, position, seed,
                                                       warmup, iters, C.byref(us)):

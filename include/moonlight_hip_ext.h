@@ -70,25 +70,31 @@ int moonlight_model_tensor_info(const MoonlightModel *model, const char *name,
 int moonlight_session_fill_kv(MoonlightSession *session, int layer,
                               int length, uint64_t seed);
 
-/* Times `iters` back-to-back device passes of one MoE layer exactly as a
- * forward runs it (router GEMV with the fused post-attention RMSNorm, top-k
- * and route tables, grouped gate/up + down expert launches, shared expert,
- * combine into the residual) on `rows` token rows drawn ~N(0, 1) from `seed`
- * and resident in HBM.  avg_us: HIP-event time per pass; unique_experts: the
- * number of distinct routed experts of the pass (for the byte count). */
+/* Times `iters` back-to-back device passes (after `warmup` untimed ones) of
+ * one MoE layer exactly as a forward runs it (router GEMV with the fused
+ * post-attention RMSNorm, top-k and route tables, grouped gate/up + down
+ * expert launches, shared expert, combine into the residual) on `rows` token
+ * rows drawn ~N(0, 1) and resident in HBM.  layer >= 0: that layer, one input
+ * drawn from `seed`; layer < 0: the passes cycle through every MoE layer and
+ * pass i reads its own input (seed + i), so the weights come from HBM rather
+ * than the 256 MB last-level cache.  avg_us: HIP-event time per pass;
+ * unique_experts: the distinct routed experts summed over the timed passes
+ * (for the byte count).  rows is at most one routing call (16384 / top_k). */
 int moonlight_session_time_moe(MoonlightSession *session, int layer, int rows,
                                uint64_t seed, int warmup, int iters,
                                double *avg_us, int *unique_experts);
 
-/* Times `iters` back-to-back device passes of one attention block exactly as
- * a decode runs it (the [q | kv_a] GEMV with the input RMSNorm, cache
- * append, query RoPE and absorb, split attention over the `position` cached
- * keys plus the new rows, merge, value and o_proj with the residual) on
- * `rows` token rows drawn ~N(0, 1) from `seed`, at cache position
+/* Times `iters` back-to-back device passes (after `warmup` untimed ones) of
+ * one attention block exactly as a decode runs it (the [q | kv_a] GEMV with
+ * the input RMSNorm, cache append, query RoPE and absorb, split attention
+ * over the `position` cached keys plus the new rows, merge, value and o_proj
+ * with the residual) on `rows` token rows drawn ~N(0, 1), at cache position
  * `position` (0 <= position, position + rows <= context_size; the cache rows
  * at position .. position + rows - 1 are rewritten by every pass and the
- * session's cache lengths are left unchanged).  avg_us: HIP-event time per
- * pass. */
+ * session's cache lengths are left unchanged).  layer >= 0: that layer, one
+ * input drawn from `seed`; layer < 0: the passes cycle through every layer
+ * (fill every layer's cache first) and pass i reads its own input
+ * (seed + i).  avg_us: HIP-event time per pass. */
 int moonlight_session_time_attention(MoonlightSession *session, int layer, int rows,
                                      int position, uint64_t seed, int warmup, int iters,
                                      double *avg_us);

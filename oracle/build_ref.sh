@@ -41,4 +41,13 @@ if [ -f "$LIB/libfloyd_amd.so" ]; then
         "$OUT/runtime_device_patched.c" "$REF/moonlight_model.c" $LINK
     rm -f "$OUT/runtime_device_patched.c"
     echo "build_ref: linked the reference's backend and Moonlight tests against libfloyd_amd.so"
+    # The real callers: floyd's CLI (floyd.c, moonlight_chat.c, moonlight_model.c
+    # and the HTTP layer it links) compiled unchanged with the reference's own
+    # flags (Makefile:26-29) and linked against the library in place of
+    # moonlight_metal.o / backend_metal.o; dsv4_stub.c stands in for the
+    # DeepSeek-V4 objects, which are not part of this path.
+    gcc -O3 -fopenmp -w -I"$REF" -o "$OUT/floyd" "$REF/floyd.c" "$REF/moonlight_chat.c" \
+        "$REF/moonlight_model.c" "$REF/openai_http.c" "$REF/openai_responses.c" \
+        "$HERE/dsv4_stub.c" $LINK -pthread
+    echo "build_ref: linked floyd (floyd.c + moonlight_chat.c, unchanged) against libfloyd_amd.so"
 fi

@@ -70,3 +70,32 @@ def test_reference_tests_link_against_library(exported, name):
     boundary = {s for s in used if s.startswith(("moonlight_", "fm_"))}
     assert boundary, "no boundary symbols used"
     assert boundary <= exported, sorted(boundary - exported)
+
+
+# The production entry points moonlight_chat.c calls (moonlight_chat.c:133-153,
+# :173-202, :255-297, :377-413).
+CHAT_SYMBOLS = {"moonlight_model_open", "moonlight_model_close", "moonlight_model_info",
+                "moonlight_device_name", "moonlight_session_create",
+                "moonlight_session_destroy", "moonlight_session_reset",
+                "moonlight_session_position", "moonlight_session_stats",
+                "moonlight_session_prefill", "moonlight_session_append",
+                "moonlight_session_decode"}
+
+
+def test_floyd_cli_links_against_library(exported):
+    """floyd's own CLI -- floyd.c, moonlight_chat.c, moonlight_model.c and the
+    HTTP layer, compiled unchanged by oracle/build_ref.sh with a DeepSeek-V4
+    stub -- takes every Moonlight session symbol it uses from libfloyd_amd.so
+    and runs (its usage text needs no GPU)."""
+    path = os.path.join(ROOT, "oracle", "_ref", "floyd")
+    if not os.path.exists(path):
+        pytest.skip("oracle/_ref not built (needs the reference tree)")
+    out = subprocess.run(["nm", "-D", "--undefined-only", path], capture_output=True,
+                         text=True, check=True).stdout
+    used = {line.split()[-1] for line in out.splitlines()}
+    boundary = {s for s in used if s.startswith(("moonlight_", "fm_"))}
+    assert boundary == CHAT_SYMBOLS, sorted(boundary ^ CHAT_SYMBOLS)
+    assert boundary <= exported
+    run = subprocess.run([path, "--help"], capture_output=True, text=True, timeout=60)
+    assert run.returncode == 0, run.stderr
+    assert "floyd run --model DIR --prompt TEXT" in run.stdout

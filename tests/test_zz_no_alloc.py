@@ -13,6 +13,7 @@ from floyd_amd import native
 pytestmark = pytest.mark.gpu
 
 SCRATCH = 32 << 20
+_CACHED = []  # host weights handed to fm_matmul_q8 with cache = 1
 
 
 @pytest.fixture(scope="module")
@@ -68,3 +69,53 @@ def test_static_refuses_oversize(fm):
     assert fm.fm_matmul_static(3, fptr(y), fptr(x), q.ctypes.data, fptr(s), 64, 2048, 1) == 0
     # the array still serves a valid call afterwards
     run_pair(fm, 8, 64, 2048, 1, 5)
+
+
+def hip_runtime():
+    """The HIP runtime instance libfloyd_amd.so runs on (the one already
+    mapped into this process)."""
+    import ctypes
+    with open("/proc/self/maps") as f:
+        paths = {line.split()[-1] for line in f if "libamdhip64" in line}
+    assert paths, "libamdhip64 is not loaded"
+    return ctypes.CDLL(sorted(paths)[0])
+
+
+def device_free_bytes(hip):
+    import ctypes
+    free, total = ctypes.c_size_t(), ctypes.c_size_t()
+    assert hip.hipMemGetInfo(ctypes.byref(free), ctypes.byref(total)) == 0
+    return free.value
+
+
+def test_static_calls_allocate_nothing(fm):
+    """Free device memory is the same before and after a series of
+    fm_matmul_static calls (each shape called once beforehand, so the HIP
+    runtime's own lazy loading of the kernels' code is not counted).  As a
+    control, fm_matmul_q8 with cache = 1 on a new weight (a device copy kept
+    by host pointer) shows up in the same measurement."""
+    print("[gpu] fm_matmul_static: device free bytes across calls", flush=True)
+    hip = hip_runtime()
+    shapes = [(8, 11264, 2048, 4, 91), (4, 11264, 2048, 1, 92), (8, 577, 1031, 3, 93)]
+    cases = [(bits, O_, I, S) + case(bits, O_, I, S, seed) for bits, O_, I, S, seed in shapes]
+    for bits, O_, I, S, q, s, x in cases:
+        y = np.empty((S, O_), np.float32)
+        assert fm.fm_matmul_static(bits, fptr(y), fptr(x), q.ctypes.data, fptr(s), O_, I, S) == 1
+    before = device_free_bytes(hip)
+    for _ in range(3):
+        for bits, O_, I, S, q, s, x in cases:
+            y = np.empty((S, O_), np.float32)
+            assert fm.fm_matmul_static(bits, fptr(y), fptr(x), q.ctypes.data, fptr(s), O_, I,
+                                       S) == 1
+            assert np.isfinite(y).all()
+    after = device_free_bytes(hip)
+    assert after == before, (before, after)
+    # control: a cached fm_matmul_q8 weight (11264 x 2048 q8, 22 MiB) is a
+    # device allocation the measurement sees
+    bits, O_, I, S, q, s, x = cases[0]
+    q_new = q.copy()
+    _CACHED.append(q_new)  # the cache is keyed by host pointer: keep it alive
+    y = np.empty((S, O_), np.float32)
+    fm.fm_matmul_q8(fptr(y), fptr(x), q_new.ctypes.data, fptr(s), O_, I, S, 1)
+    assert np.isfinite(y).all()
+    assert device_free_bytes(hip) <= after - q_new.nbytes
