@@ -122,6 +122,16 @@ def moe_layer_bytes(unique, rows):
     return unique * expert + shared + router + rows * 2048 * 4 * 2
 
 
+def attn_block_bytes(ctx, rows=1):
+    """Algorithmic bytes of one q8 decode attention block at `ctx` cached
+    keys: [q | kv_a] (3648 x 2048), kv_b (4096 x 512) and o_proj (2048 x 2048)
+    with their row scales, the two RMSNorm weights, the latent + rope cache
+    (ctx x 576 f32) and the token rows in and out."""
+    rows_w = 3072 + 576 + 4096 + 2048
+    weights = (3072 + 576) * 2048 + 4096 * 512 + 2048 * 2048 + rows_w * 4 + (2048 + 512) * 4
+    return weights + ctx * 576 * 4 + rows * 2048 * 4 * 2
+
+
 # Algorithmic bytes of one full q8 decode step: attention 13.8 MB x 27 layers,
 # dense FFN 69.3 MB, MoE 69.9 MB x 26, f32 lm_head 1.342 GB, KV cache reads.
 DECODE_STEP_BYTES = {4096: 3856274688, 16384: 4620686592}
@@ -204,19 +214,36 @@ def moonlight_extras(native, extra, decode_tokens):
           file=sys.stderr, flush=True)
     sess = S.Session(model, 128, 64)
     for rows in (1, 8, 64):
-        us, uniq = sess.time_moe(1, rows, seed=rows, warmup=5, iters=50)
-        nbytes = moe_layer_bytes(uniq, rows)
+        # cold: the passes cycle through the 26 MoE layers, a fresh input per
+        # pass (26 x 70 MB and more: the weights stream from HBM); warm, for
+        # contrast: layer 1 on one input, its experts served from the 256 MB
+        # last-level cache at T = 1
+        us, uniq = sess.time_moe(-1, rows, seed=rows, warmup=26, iters=104)
+        warm_us, _ = sess.time_moe(1, rows, seed=rows, warmup=5, iters=50)
+        nbytes = int(round(moe_layer_bytes(uniq, rows)))
         gbs = nbytes / (us * 1e-6) / 1e9
         extra[f"cfg2_moe_decode_q8_T{rows}"] = {
-            "us": round(us, 2), "unique_experts": uniq, "bytes": nbytes,
-            "GB/s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)}
-        print(f"[bench] MoE layer T={rows}: {us:.1f} us, U={uniq}, {gbs:.0f} GB/s",
-              file=sys.stderr, flush=True)
+            "us": round(us, 2), "unique_experts_mean": round(uniq, 2), "bytes": nbytes,
+            "GB/s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4),
+            "layers": "26-layer rotation, fresh input per pass", "warm_us_layer1": round(warm_us, 2)}
+        print(f"[bench] MoE layer T={rows}: {us:.1f} us cold (26-layer rotation), U={uniq:.1f}, "
+              f"{gbs:.0f} GB/s; {warm_us:.1f} us warm (one layer)", file=sys.stderr, flush=True)
     sess.close()
     prefill_moe(model, 8, extra)
     for ctx in (4096, 16384):
         sess = S.Session(model, ctx + 2 * decode_tokens + 8, 1)
         sess.fill_kv(ctx, seed=ctx)
+        # one attention block, cold: cycling through the 27 layers' weights
+        # and caches, a fresh input per pass (the cache row at ctx is
+        # rewritten; the decodes below rewrite it again)
+        us = sess.time_attention(-1, 1, ctx, seed=ctx, warmup=27, iters=108)
+        nbytes = attn_block_bytes(ctx)
+        gbs = nbytes / (us * 1e-6) / 1e9
+        extra[f"attn_block_ctx{ctx}"] = {
+            "us": round(us, 2), "bytes": nbytes, "GB/s": round(gbs, 1),
+            "frac": round(gbs / HBM_PEAK_GBS, 4), "layers": "27-layer rotation, fresh input per pass"}
+        print(f"[bench] attention block ctx {ctx}: {us:.1f} us cold, {gbs:.0f} GB/s",
+              file=sys.stderr, flush=True)
         token = 1
         import numpy as np
         logits = np.empty(163840, np.float32)  # reused output buffer
@@ -299,9 +326,10 @@ def moe_only(sizes=None):
     sess = S.Session(model, max(128, max(rows_list)), max(64, max(rows_list)))
     out = {}
     for rows in rows_list:
-        us, uniq = sess.time_moe(1, rows, seed=rows, warmup=5, iters=20)
-        out[f"T{rows}"] = {"us": round(us, 2), "unique_experts": uniq}
-        print(f"[bench] MoE layer T={rows}: {us:.1f} us, U={uniq}", file=sys.stderr, flush=True)
+        us, uniq = sess.time_moe(-1, rows, seed=rows, warmup=26, iters=52)
+        out[f"T{rows}"] = {"us": round(us, 2), "unique_experts_mean": round(uniq, 2)}
+        print(f"[bench] MoE layer T={rows}: {us:.1f} us (26-layer rotation), U={uniq:.1f}",
+              file=sys.stderr, flush=True)
     sess.close()
     model.close()
     print(json.dumps(out), flush=True)
@@ -316,10 +344,11 @@ def attn_only(sizes=None):
     out = {}
     for ctx in sizes or (4096, 16384):
         sess = S.Session(model, ctx + 8, 1)
-        sess.fill_kv(ctx, seed=ctx, layer=1)
-        us = sess.time_attention(1, 1, ctx, warmup=5, iters=50)
+        sess.fill_kv(ctx, seed=ctx)
+        us = sess.time_attention(-1, 1, ctx, warmup=27, iters=54)
         out[f"ctx{ctx}"] = {"us": round(us, 2)}
-        print(f"[bench] attention block ctx={ctx}: {us:.1f} us", file=sys.stderr, flush=True)
+        print(f"[bench] attention block ctx={ctx}: {us:.1f} us (27-layer rotation)",
+              file=sys.stderr, flush=True)
         sess.close()
     model.close()
     print(json.dumps(out), flush=True)
