@@ -461,7 +461,7 @@ __global__ __launch_bounds__(256) void gemv_mfma_kernel(MfmaGemvArgs a) {
 
 
 // Weights straight into registers in the MFMA B layout, for matrices whose
-// wave k quarter (KQ elements) fits in registers: no LDS copy of the weights
+// wave k range (KQ elements) fits in registers: no LDS copy of the weights
 // (the LDS traffic of the DMA kernel's product phase is shared by every
 // workgroup of a CU), and no LDS DMA, so every load is an ordinary one the
 // compiler waits for where its registers are used.  Lane (g, n) loads weight
@@ -470,23 +470,33 @@ __global__ __launch_bounds__(256) void gemv_mfma_kernel(MfmaGemvArgs a) {
 // half each), so a wave instruction reads 64 contiguous bytes of each of 16
 // rows; the limb rows are read at the same k positions.
 template <int FMT, int B, bool DUAL, int KQ>
-__global__ __launch_bounds__(256) void gemv_mfma_direct_kernel(GemvParams p) {
+struct DirectLds {
+    static constexpr int kXrow = KQ + kXPad;
+    unsigned char xl[4][4 * B * kXrow];  // per wave: [4 limbs][B][xrow]
+    float red[4][4][2][B][kRows];        // [wave][limb][gate / up][token row][row]
+    float red_ss[4][B];
+};
+
+// One wave's share of a register-direct workgroup: the k range [k0, k0 +
+// KQ) of the workgroup's 16 output rows.  Issues the x (and norm_w) loads,
+// then the weight loads, then `epilogue_loads()` (the caller's operands, in
+// flight during the split and the products); splits x into limbs; leaves the
+// wave's limb-combined shares in L.red[wave] and its sum of squares of x in
+// L.red_ss[wave].
+template <int FMT, int B, bool DUAL, int KQ, typename EpilogueLoads>
+__device__ __forceinline__ void direct_wave(const GemvParams &p, int row0, int k0,
+                                            DirectLds<FMT, B, DUAL, KQ> &L,
+                                            EpilogueLoads &&epilogue_loads) {
     constexpr int S = KQ / 64;                  // MFMA steps per wave
     constexpr int NW = FMT == kQ8 ? S : S / 2;  // 16-byte weight pieces per lane and matrix
     constexpr int kPass = (KQ + 511) / 512;
     constexpr int xrow = KQ + kXPad;
-    __shared__ __attribute__((aligned(16))) unsigned char xl_all[4][4 * B * xrow];
-    __shared__ float red[4][4][2][B][kRows];  // [wave][limb][gate / up][token row][row]
-    __shared__ float red_ss[4][B];
-    __shared__ __attribute__((aligned(16))) float router_hw[2 * kRows];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int row0 = blockIdx.x * kRows;
-    const int k0 = wave * KQ;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const long row_bytes = FMT == kQ8 ? p.I : p.I / 2;
-    unsigned char *xl = xl_all[wave];
+    unsigned char *xl = L.xl[wave];
     const int n = lane & 15, g = lane >> 4;
 
-    // ---- x of this wave's quarter (and norm_w), then the weights, then
+    // ---- x of this wave's k range (and norm_w), then the weights, then
     // the epilogue's operands: in-order completion lets the split start
     // while the weights are still in flight
     const bool has_norm = p.norm_w != nullptr;
@@ -514,14 +524,7 @@ __global__ __launch_bounds__(256) void gemv_mfma_direct_kernel(GemvParams p) {
         wv[i] = load_global16(p.w + w_off + 64 * i);
         if constexpr (DUAL) uv[i] = load_global16(p.w2 + w_off + 64 * i);
     }
-    const int eb = g < B ? g : 0;
-    const bool has_res = p.epilogue == kEpiResidual;
-    const float e_s = p.s[wr_row];
-    const float e_s2 = DUAL ? p.s2[wr_row] : 0.0f;
-    const float e_res = has_res ? p.resid[(long)eb * p.resid_stride + wr_row] : 0.0f;
-    const bool router = !DUAL && B == 1 && p.router_parts != nullptr;
-    RouterOperands<kRows> ro{};
-    if (router && wave == 0) ro = load_router<kRows>(p, lane, row0, wr_row);
+    epilogue_loads();
 
     // ---- split x into limbs (as gemv_mfma_kernel) and store the limb rows
     float ss[B], amax[B];
@@ -589,8 +592,9 @@ __global__ __launch_bounds__(256) void gemv_mfma_direct_kernel(GemvParams p) {
                     lw[3][wd] |= (unsigned)(l3 & 255) << sh;
                 }
 #pragma unroll
-                for (int L = 0; L < 4; ++L)
-                    *reinterpret_cast<uint2 *>(xl + (L * B + b) * xrow + e) = uint2{lw[L][0], lw[L][1]};
+                for (int Lb = 0; Lb < 4; ++Lb)
+                    *reinterpret_cast<uint2 *>(xl + (Lb * B + b) * xrow + e) =
+                        uint2{lw[Lb][0], lw[Lb][1]};
             }
         }
     }
@@ -634,7 +638,7 @@ __global__ __launch_bounds__(256) void gemv_mfma_direct_kernel(GemvParams p) {
         acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(A, Bw, acc, 0, 0, 0);
         if constexpr (DUAL) acc2 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A, Bu, acc2, 0, 0, 0);
     }
-    // ---- limbs combined, the four waves' shares in LDS, the epilogue
+    // ---- limbs combined into the wave's shares
     const float limb_w = g == 0 ? 16777216.0f : g == 1 ? 65536.0f : g == 2 ? 256.0f : 1.0f;
 #pragma unroll
     for (int b = 0; b < B; ++b) {
@@ -643,10 +647,44 @@ __global__ __launch_bounds__(256) void gemv_mfma_direct_kernel(GemvParams p) {
             c -= 8 * acc1[b];
             if (DUAL) c2 -= 8 * acc1[b];
         }
-        red[wave][g][0][b][n] = (float)c * limb_w * step[b];
-        if (DUAL) red[wave][g][1][b][n] = (float)c2 * limb_w * step[b];
-        if (lane == 0) red_ss[wave][b] = ss[b];
+        L.red[wave][g][0][b][n] = (float)c * limb_w * step[b];
+        if (DUAL) L.red[wave][g][1][b][n] = (float)c2 * limb_w * step[b];
+        if (lane == 0) L.red_ss[wave][b] = ss[b];
     }
+}
+
+// Sum of the shares of the four limbs and four waves (limbs, then waves, in
+// order) for output row n, token row b, matrix u (0, or 1 = up).
+template <int FMT, int B, bool DUAL, int KQ>
+__device__ __forceinline__ float direct_total(const DirectLds<FMT, B, DUAL, KQ> &L, int u, int b,
+                                              int n) {
+    float w4[4];
+#pragma unroll
+    for (int w = 0; w < 4; ++w)
+        w4[w] = (L.red[w][0][u][b][n] + L.red[w][1][u][b][n]) +
+                (L.red[w][2][u][b][n] + L.red[w][3][u][b][n]);
+    return (w4[0] + w4[1]) + (w4[2] + w4[3]);
+}
+
+template <int FMT, int B, bool DUAL, int KQ>
+__global__ __launch_bounds__(256) void gemv_mfma_direct_kernel(GemvParams p) {
+    __shared__ __attribute__((aligned(16))) DirectLds<FMT, B, DUAL, KQ> L;
+    __shared__ __attribute__((aligned(16))) float router_hw[2 * kRows];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int row0 = blockIdx.x * kRows;
+    const int n = lane & 15, g = lane >> 4;
+    const int wr_row = row0 + n < p.O ? row0 + n : p.O - 1;
+    const int eb = g < B ? g : 0;
+    const bool has_res = p.epilogue == kEpiResidual;
+    const bool router = !DUAL && B == 1 && p.router_parts != nullptr;
+    float e_s = 0.0f, e_s2 = 0.0f, e_res = 0.0f;
+    RouterOperands<kRows> ro{};
+    direct_wave<FMT, B, DUAL, KQ>(p, row0, wave * KQ, L, [&] {
+        e_s = p.s[wr_row];
+        e_s2 = DUAL ? p.s2[wr_row] : 0.0f;
+        e_res = has_res ? p.resid[(long)eb * p.resid_stride + wr_row] : 0.0f;
+        if (router && wave == 0) ro = load_router<kRows>(p, lane, row0, wr_row);
+    });
     __syncthreads();
     if (wave != 0) return;
     const int b = g;
@@ -655,20 +693,13 @@ __global__ __launch_bounds__(256) void gemv_mfma_direct_kernel(GemvParams p) {
     if (g < B && row < p.O) {
         float inv_rms = 1.0f;
         if (p.norm_w) {
-            const float tot = (red_ss[0][b] + red_ss[1][b]) + (red_ss[2][b] + red_ss[3][b]);
+            const float tot = (L.red_ss[0][b] + L.red_ss[1][b]) + (L.red_ss[2][b] + L.red_ss[3][b]);
             inv_rms = 1.0f / sqrtf(tot / (float)p.I + p.eps);
         }
-        auto total = [&](int u) {
-            float w4[4];
-#pragma unroll
-            for (int w = 0; w < 4; ++w)
-                w4[w] = (red[w][0][u][b][n] + red[w][1][u][b][n]) + (red[w][2][u][b][n] + red[w][3][u][b][n]);
-            return ((w4[0] + w4[1]) + (w4[2] + w4[3])) * inv_rms;
-        };
-        const float sum = total(0);
+        const float sum = direct_total(L, 0, b, n) * inv_rms;
         float *yb = p.y + (long)b * p.y_stride;
         if (DUAL) {
-            yb[row] = silu(sum * e_s) * (total(1) * e_s2);
+            yb[row] = silu(sum * e_s) * ((direct_total(L, 1, b, n) * inv_rms) * e_s2);
         } else {
             float out = sum * e_s;
             if (has_res) out = e_res + out;
@@ -678,6 +709,85 @@ __global__ __launch_bounds__(256) void gemv_mfma_direct_kernel(GemvParams p) {
     }
     // the whole of wave 0, converged: the partials read every lane's output
     if (router) store_router_parts<kRows>(p, lane, y_out, ro, router_hw);
+}
+
+// Split-k form for wide-k matrices with few rows (2048 x 11264): workgroup
+// (row block, split) takes 16 output rows and the k chunk [split * 4 KQ,
+// (split + 1) * 4 KQ) (one KQ range per wave as in the direct kernel; waves
+// past I contribute nothing), so every workgroup streams as many weight
+// bytes as a 2048-wide direct workgroup and splits a quarter of x per wave
+// instead of all of it.  Each workgroup stores its share of every output
+// (and its sum of squares of x) in sk_part / sk_ss; the workgroup of a row
+// block that arrives last (sk_count, agent_handoff_arrive; it resets the
+// counter to zero) adds the shares of the splits in split order and
+// applies the epilogue, so the result does not depend on arrival order.
+// The partial arrays are the library's own device memory (static, per
+// GPU): launches on one GPU must not overlap (the library issues all its
+// work on one stream per device).
+constexpr int kSkMaxSplits = 16;
+constexpr int kSkMaxRowBlocks = 256;  // O <= 4096
+constexpr int kSkCountStride = 32;    // ints between counters (one per 128 bytes)
+__device__ float sk_part[kSkMaxRowBlocks * kSkMaxSplits * kMaxGemvRows * kRows];
+__device__ float sk_ss[kSkMaxRowBlocks * kSkMaxSplits * kMaxGemvRows];
+__device__ int sk_count[kSkMaxRowBlocks * kSkCountStride];  // zero between launches
+
+template <int FMT, int B, int KQ>
+__global__ __launch_bounds__(256) void gemv_mfma_splitk_kernel(GemvParams p) {
+    __shared__ __attribute__((aligned(16))) DirectLds<FMT, B, false, KQ> L;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int rb = blockIdx.x, split = blockIdx.y, splits = gridDim.y;
+    const int row0 = rb * kRows;
+    const int n = lane & 15, g = lane >> 4;
+    const int wr_row = row0 + n < p.O ? row0 + n : p.O - 1;
+    const int eb = g < B ? g : 0;
+    const bool has_res = p.epilogue == kEpiResidual;
+    const int k0 = (split * 4 + wave) * KQ;
+    float e_s = 0.0f, e_res = 0.0f;
+    if (k0 < p.I) {
+        direct_wave<FMT, B, false, KQ>(p, row0, k0, L, [&] {
+            e_s = p.s[wr_row];
+            e_res = has_res ? p.resid[(long)eb * p.resid_stride + wr_row] : 0.0f;
+        });
+    } else {
+#pragma unroll
+        for (int b = 0; b < B; ++b) {
+            L.red[wave][g][0][b][n] = 0.0f;
+            if (lane == 0) L.red_ss[wave][b] = 0.0f;
+        }
+        e_s = p.s[wr_row];
+        e_res = has_res ? p.resid[(long)eb * p.resid_stride + wr_row] : 0.0f;
+    }
+    __syncthreads();
+    // this workgroup's shares: lane (b, n) of wave 0
+    const long pbase = ((long)rb * kSkMaxSplits + split) * B;
+    if (wave == 0 && g < B) {
+        __hip_atomic_store(&sk_part[(pbase + g) * kRows + n], direct_total(L, 0, g, n),
+                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (n == 0)
+            __hip_atomic_store(&sk_ss[pbase + g],
+                               (L.red_ss[0][g] + L.red_ss[1][g]) + (L.red_ss[2][g] + L.red_ss[3][g]),
+                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    int *count = sk_count + rb * kSkCountStride;
+    if (!agent_handoff_arrive(count, splits) || wave != 0) return;
+    const int b = g;
+    const int row = row0 + n;
+    if (g < B) {
+        float sum = 0.0f, tot = 0.0f;
+        for (int k = 0; k < splits; ++k) {
+            const long pb = ((long)rb * kSkMaxSplits + k) * B + b;
+            sum += __hip_atomic_load(&sk_part[pb * kRows + n], __ATOMIC_RELAXED,
+                                     __HIP_MEMORY_SCOPE_AGENT);
+            tot += __hip_atomic_load(&sk_ss[pb], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        if (row < p.O) {
+            const float inv_rms = p.norm_w ? 1.0f / sqrtf(tot / (float)p.I + p.eps) : 1.0f;
+            float out = sum * inv_rms * e_s;
+            if (has_res) out = e_res + out;
+            p.y[(long)b * p.y_stride + row] = out;
+        }
+    }
+    if (lane == 0) __hip_atomic_store(count, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 template <int FMT, int B, bool DUAL, int KQ>
@@ -699,6 +809,41 @@ bool launch_direct_b(const GemvParams &p, hipStream_t stream, std::string *name)
     case 1: return launch_direct<FMT, 1, DUAL, 512>(p, stream, name);
     case 2: return launch_direct<FMT, 2, DUAL, 512>(p, stream, name);
     case 4: return launch_direct<FMT, 4, DUAL, 512>(p, stream, name);
+    default: return false;
+    }
+}
+
+// Splits of 4 x 512 k per workgroup for the split-k kernel, or 0 when it
+// does not take the shape.
+constexpr int kSkQuarter = 512;
+int splitk_splits(const GemvParams &p) {
+    const int chunk = 4 * kSkQuarter;
+    const int splits = (p.I + chunk - 1) / chunk;
+    if ((p.fmt != kQ8 && p.fmt != kQ4) || p.epilogue == kEpiSiluDual || p.rows < 1 ||
+        p.rows > 4 || p.rows == 3 || p.limbs || p.router_parts || p.I <= 4096 || p.O > 4096 ||
+        p.I % kSkQuarter || splits > kSkMaxSplits || (p.O + kRows - 1) / kRows > kSkMaxRowBlocks)
+        return 0;
+    return splits;
+}
+template <int FMT, int B>
+bool launch_splitk(const GemvParams &p, int splits, hipStream_t stream, std::string *name) {
+    if (name) {
+        char buf[96];
+        snprintf(buf, sizeof(buf), "mlh::(anonymous namespace)::gemv_mfma_splitk_kernel<%d, %d, %d>",
+                 FMT, B, kSkQuarter);
+        *name = buf;
+        return true;
+    }
+    hipLaunchKernelGGL((gemv_mfma_splitk_kernel<FMT, B, kSkQuarter>),
+                       dim3((p.O + kRows - 1) / kRows, splits), dim3(256), 0, stream, p);
+    return true;
+}
+template <int FMT>
+bool launch_splitk_b(const GemvParams &p, int splits, hipStream_t stream, std::string *name) {
+    switch (p.rows) {
+    case 1: return launch_splitk<FMT, 1>(p, splits, stream, name);
+    case 2: return launch_splitk<FMT, 2>(p, splits, stream, name);
+    case 4: return launch_splitk<FMT, 4>(p, splits, stream, name);
     default: return false;
     }
 }
@@ -811,7 +956,7 @@ bool gemv_router_ok(const GemvParams &p) {
     GemvParams q = p;
     q.router_parts = nullptr;
     std::string name;
-    return gemv_mfma(q, nullptr, &name);
+    return splitk_splits(q) == 0 && gemv_mfma(q, nullptr, &name);
 }
 
 int gemv_router_parts(const GemvParams &p) {
@@ -820,6 +965,14 @@ int gemv_router_parts(const GemvParams &p) {
 }
 
 bool gemv_mfma(const GemvParams &p, hipStream_t stream, std::string *name) {
+    // wide-k matrices with few rows: the split-k kernel
+    if (const int splits = splitk_splits(p)) {
+        auto al = [](const void *q) { return ((uintptr_t)q & 15u) == 0; };
+        if (!name && (!al(p.w) || !al(p.x) || p.x_stride % 4 || (p.norm_w && !al(p.norm_w))))
+            return false;
+        return p.fmt == kQ8 ? launch_splitk_b<kQ8>(p, splits, stream, name)
+                            : launch_splitk_b<kQ4>(p, splits, stream, name);
+    }
     const int rw = mfma_rows(p, !name);
     if (!rw) return false;
     const bool dual = p.epilogue == kEpiSiluDual;

@@ -889,9 +889,8 @@ __global__ __launch_bounds__(256, 2) void mla_prefill_attend_kernel(MlaParams p)
 //   sum    ctx_h[v] = sum_c y_c[v] in chunk order, by the chunk workgroup
 //          that arrives last (merge_count; it resets the counter).  The
 //          shares travel as device-coherent (agent-scope) stores and loads,
-//          which on gfx950 bypass the per-XCD L2 copies; the arrival
-//          increment is an agent-scope acquire-release, so the workgroup
-//          that counts last is ordered after every share store.
+//          which on gfx950 bypass the per-XCD L2 copies
+//          (agent_handoff_arrive, mlh_device.h).
 constexpr int kMergeBatch = 4;
 template <int FMT>
 __global__ __launch_bounds__(512) void mla_merge_value_kernel(MlaParams p) {
@@ -904,7 +903,6 @@ __global__ __launch_bounds__(512) void mla_merge_value_kernel(MlaParams p) {
     __shared__ __attribute__((aligned(16))) float gacc[NG][DL];
     __shared__ float lcs[DL];
     __shared__ float ownp[8];
-    __shared__ int last;
     const int r = blockIdx.x, h = blockIdx.y, c = blockIdx.z;
     const int nchunks = gridDim.z;
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
@@ -1041,21 +1039,9 @@ __global__ __launch_bounds__(512) void mla_merge_value_kernel(MlaParams p) {
         if (vq == 0 && v < p.vdim)
             __hip_atomic_store(part + v, y, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
-    // the last of the head's chunk workgroups sums the shares.  Ordering:
-    // every thread's share stores happen before thread 0's increment (the
-    // workgroup barrier), which releases them at agent scope; the increment
-    // that counts last acquires every earlier one (they form one release
-    // sequence on the counter), and the barrier after it passes that on to
-    // the workgroup's loads.  The explicit wait for the stores before the
-    // barrier is the same order at the hardware level.
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
+    // the last of the head's chunk workgroups sums the shares
     int *count = p.merge_count + (r * p.heads + h) * kMlaCountStride;
-    if (t == 0)
-        last = __hip_atomic_fetch_add(count, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT) ==
-               nchunks - 1;
-    __syncthreads();
-    if (!last) return;
+    if (!agent_handoff_arrive(count, nchunks)) return;
     constexpr int kMaxChunks = kMlaMaxLatent / kMlaValueDims;
     const float *parts = p.value_part + ((long)r * p.heads + h) * nchunks * p.vdim;
     for (int v = t; v < p.vdim; v += 512) {

@@ -119,4 +119,36 @@ __device__ __forceinline__ bool butterfly_writer(int lane) {
 
 __device__ __forceinline__ float silu(float g) { return g / (1.0f + expf(-g)); }
 
+// Hand-off between the workgroups of one launch: every workgroup stores its
+// shares with agent-scope atomic stores, arrives at a counter, and the
+// workgroup that arrives last reads all the shares with agent-scope atomic
+// loads (and resets the counter for the next launch).  On gfx950 agent-scope
+// stores and loads act at the device-coherent level (they bypass the
+// non-coherent state of the per-XCD L2 caches), so once a store has
+// completed, an agent-scope load from any XCD returns it.  The order is kept
+// at both levels:
+//  - hardware: every thread waits for its own stores (s_waitcnt) before the
+//    workgroup barrier that precedes the counter increment;
+//  - compiler: the empty asm statements clobber memory, so no load or store
+//    moves across the wait, the barriers or the increment.
+// An agent-scope release / acquire on the counter states the same order in
+// the HIP memory model, but on gfx950 each one writes back or invalidates
+// the XCD's L2 (buffer_wbl2 / buffer_inv sc1) in every workgroup; measured
+// on a 768-workgroup split-k GEMV: 17.4 us against 6.1 us with this form.
+// Every thread of the workgroup calls it; returns whether this workgroup
+// arrived last (the same value in every thread).
+__device__ __forceinline__ bool agent_handoff_arrive(int *count, int total) {
+    __shared__ int arrived_last;
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0);
+    asm volatile("" ::: "memory");
+    __syncthreads();
+    if (threadIdx.x == 0)
+        arrived_last = __hip_atomic_fetch_add(count, 1, __ATOMIC_RELAXED,
+                                              __HIP_MEMORY_SCOPE_AGENT) == total - 1;
+    __syncthreads();
+    asm volatile("" ::: "memory");
+    return arrived_last != 0;
+}
+
 }  // namespace mlh

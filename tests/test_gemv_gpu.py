@@ -36,6 +36,11 @@ SHAPES = [
     # tiny-fixture widths (hidden 256, expert 64) and odd shapes (generic path)
     (1, 192, 256, 5), (2, 80, 256, 3), (1, 256, 64, 2), (2, 256, 64, 1),
     (1, 128, 257, 4), (2, 128, 257, 4), (0, 7, 33, 2), (1, 33, 48, 9),
+    # split-k kernel (I > 4096, O <= 4096): 2 and 4 token rows, a last k
+    # chunk with only 1 or 2 of its 4 wave ranges (5120, 11264), row blocks
+    # past O (1000, 2040)
+    (1, 2048, 11264, 4), (2, 2048, 11264, 2), (1, 512, 5120, 1), (2, 1000, 6144, 4),
+    (1, 2040, 8192, 2),
 ]
 
 
@@ -58,7 +63,9 @@ def test_gemv_matches_oracle(device, fmt, out_width, in_width, rows):
     (1, 3072, 2048, 1), (2, 3648, 2048, 2), (0, 64, 2048, 3), (1, 192, 256, 4),
     (0, 163840 // 16, 2048, 1),
     # narrow rows with a partially filled last wave (lane groups past O)
-    (1, 80, 256, 2), (2, 80, 256, 1), (1, 40, 128, 3), (2, 72, 256, 2), (1, 20, 64, 1)])
+    (1, 80, 256, 2), (2, 80, 256, 1), (1, 40, 128, 3), (2, 72, 256, 2), (1, 20, 64, 1),
+    # split-k: the sum of squares adds up over the k chunks
+    (1, 2048, 11264, 1), (2, 1024, 5120, 4)])
 def test_gemv_rmsnorm_prologue(device, fmt, out_width, in_width, rows):
     print(f"[gpu] gemv+norm fmt={fmt} O={out_width} I={in_width} rows={rows}", flush=True)
     q, s = make_weights(fmt, out_width, in_width, seed=5 + out_width)
@@ -173,3 +180,27 @@ def test_fm_backend_reference_kernel_gate(device):
         assert maxrel(y, dense4) <= 1e-3
         x[:] = rng.uniform(-1, 1, S_ * I_)
     assert lib.fm_matmul_deepseek_v4_fp8(None, None, None, None, 128, 128, 1, 128) == 0
+
+
+@pytest.mark.parametrize("fmt,rows", [(1, 1), (2, 4)])
+def test_splitk_repeat_deterministic(device, fmt, rows):
+    """The split-k kernel's arrival counters reset themselves: back-to-back
+    launches (with a different shape in between) return the same bits, the
+    splits added in a fixed order whatever order the workgroups finish in."""
+    q, s = make_weights(fmt, 2048, 11264, seed=123)
+    x = O.fill_normal(rows * 11264, 77).reshape(rows, 11264)
+    dw, dx, ds = DeviceBuffer.from_array(q), DeviceBuffer.from_array(x), DeviceBuffer.from_array(s)
+    q2, s2 = make_weights(fmt, 1000, 6144, seed=9)
+    x2 = O.fill_normal(6144, 78).reshape(1, 6144)
+    dw2, dx2, ds2 = (DeviceBuffer.from_array(a) for a in (q2, x2, s2))
+    dy, dy2 = DeviceBuffer(rows * 2048 * 4), DeviceBuffer(1000 * 4)
+    first = None
+    for _ in range(4):
+        native.gemv(fmt, dw, ds, dx, dy, 2048, 11264, rows)
+        got = dy.download(np.float32)
+        if first is None:
+            first = got
+            assert rel_l2(got, O.matmul(fmt, q, s, x, 2048, 11264).ravel()) < TOL
+        assert np.array_equal(got.view(np.uint32), first.view(np.uint32))
+        native.gemv(fmt, dw2, ds2, dx2, dy2, 1000, 6144, 1)
+        assert rel_l2(dy2.download(np.float32), O.matmul(fmt, q2, s2, x2, 1000, 6144).ravel()) < TOL
