@@ -98,6 +98,16 @@ __device__ __forceinline__ int slice_pos(int e) {
     return e;
 }
 
+// A token row whose x holds a NaN or an infinity (its sum of squares of x is
+// not finite) cannot go through the limb split, which carries neither: its
+// outputs are NaN.  The reference's fp32 dot (moonlight_kernels.metal:62-130)
+// gives NaN there too, except where one sign of infinity meets only nonzero
+// weights, which gives that infinity: never a finite value.  (A finite x
+// whose squares overflow fp32, |x| > 1.8e19, is treated the same way.)
+__device__ __forceinline__ float nonfinite_guard(float tss, float v) {
+    return isfinite(tss) ? v : __builtin_nanf("");
+}
+
 struct MfmaGemvArgs {
     GemvParams p;
     int ndma;  // DMA instructions per wave (selects the instantiation)
@@ -444,12 +454,14 @@ __global__ __launch_bounds__(256) void gemv_mfma_kernel(MfmaGemvArgs a) {
                 w4[w] = (red[w][0][u][b][n] + red[w][1][u][b][n]) + (red[w][2][u][b][n] + red[w][3][u][b][n]);
             return ((w4[0] + w4[1]) + (w4[2] + w4[3])) * inv_rms;
         };
-        const float sum = total(0);
+        const float tss = (red_ss[0][b] + red_ss[1][b]) + (red_ss[2][b] + red_ss[3][b]);
+        const float sum = nonfinite_guard(tss, total(0) * e_s);
+        const float sum2 = DUAL ? total(1) * e_s2 : 0.0f;
         float *yb = p.y + (long)b * p.y_stride;
         if (DUAL) {
-            yb[row] = silu(sum * e_s) * (total(1) * e_s2);
+            yb[row] = silu(sum) * sum2;
         } else {
-            float out = sum * e_s;
+            float out = sum;
             if (has_res) out = e_res + out;
             yb[row] = out;
             y_out = out;
@@ -696,12 +708,14 @@ __global__ __launch_bounds__(256) void gemv_mfma_direct_kernel(GemvParams p) {
             const float tot = (L.red_ss[0][b] + L.red_ss[1][b]) + (L.red_ss[2][b] + L.red_ss[3][b]);
             inv_rms = 1.0f / sqrtf(tot / (float)p.I + p.eps);
         }
-        const float sum = direct_total(L, 0, b, n) * inv_rms;
+        const float tss = (L.red_ss[0][b] + L.red_ss[1][b]) + (L.red_ss[2][b] + L.red_ss[3][b]);
+        const float sum = nonfinite_guard(tss, (direct_total(L, 0, b, n) * inv_rms) * e_s);
+        const float sum2 = DUAL ? (direct_total(L, 1, b, n) * inv_rms) * e_s2 : 0.0f;
         float *yb = p.y + (long)b * p.y_stride;
         if (DUAL) {
-            yb[row] = silu(sum * e_s) * ((direct_total(L, 1, b, n) * inv_rms) * e_s2);
+            yb[row] = silu(sum) * sum2;
         } else {
-            float out = sum * e_s;
+            float out = sum;
             if (has_res) out = e_res + out;
             yb[row] = out;
             y_out = out;
@@ -782,7 +796,7 @@ __global__ __launch_bounds__(256) void gemv_mfma_splitk_kernel(GemvParams p) {
         }
         if (row < p.O) {
             const float inv_rms = p.norm_w ? 1.0f / sqrtf(tot / (float)p.I + p.eps) : 1.0f;
-            float out = sum * inv_rms * e_s;
+            float out = nonfinite_guard(tot, sum * inv_rms * e_s);
             if (has_res) out = e_res + out;
             p.y[(long)b * p.y_stride + row] = out;
         }

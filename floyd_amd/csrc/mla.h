@@ -53,6 +53,11 @@ struct MlaParams {
     // decode path (at most kMlaDecodeRows rows per launch group):
     float *value_part = nullptr;   // [rows][heads][latent / kMlaValueDims][vdim] value partials
     int *merge_count = nullptr;    // [rows][heads] x kMlaCountStride arrival counters, zero between launches
+    // optional: set to range_code (if still 0) when a query or key value
+    // written for the attention products is finite but outside the f16
+    // range of their split-f16 operands (|v| >= 65504)
+    int *range_error = nullptr;
+    int range_code = 0;
 };
 
 // Prefill: cache append + query RoPE, absorb GEMM, flash attention, value

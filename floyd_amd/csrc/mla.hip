@@ -37,6 +37,21 @@ __device__ __forceinline__ int mla_position(const MlaParams &p) {
     return p.position_dev ? *p.position_dev : p.position;
 }
 
+// The attention products take their fp32 operands as split-f16 pairs
+// (split_f16), which need |v| < 65504; the reference's fp32 products have no
+// such limit.  The kernels that write the operands (the cache rows, the
+// query rope, the absorbed query) check every value and report a finite one
+// outside the range through p.range_error instead of letting the products
+// turn it into inf / NaN.  NaN and inf inputs propagate as in fp32.
+constexpr float kSplitF16Max = 65504.0f;
+__device__ __forceinline__ bool outside_f16(float v) {
+    const float a = fabsf(v);
+    return a >= kSplitF16Max && a < INFINITY;
+}
+__device__ __forceinline__ void report_range(const MlaParams &p, bool bad) {
+    if (bad && p.range_error && *p.range_error == 0) *p.range_error = p.range_code;
+}
+
 // Eight consecutive dequantised kv_b values w[row, col..col+7] (col % 8 ==
 // 0), moonlight_weight_value (moonlight_kernels.metal:202-216) per element,
 // in two steps for a format known at compile time: kvb_fetch8 issues the
@@ -136,18 +151,25 @@ __global__ __launch_bounds__(256) void mla_prep_kernel(MlaParams p, int chunks) 
         const float total = (part[0] + part[1]) + (part[2] + part[3]);
         const float inv = 1.0f / sqrtf(total / (float)p.latent + p.eps);
         float *lat = p.latent_cache + (long)pos * p.latent;
+        bool bad = false;
 #pragma unroll
         for (int u = 0; u < kMlaMaxLatent / 256; ++u) {
             const int i = t + 256 * u;
-            if (i < p.latent) lat[i] = cv[u] * inv * p.kv_norm[i];
+            if (i < p.latent) {
+                const float v = cv[u] * inv * p.kv_norm[i];
+                lat[i] = v;
+                bad |= outside_f16(v);
+            }
         }
         float *rp = p.rope_cache + (long)pos * p.rope;
         if (t < half) {
             const float angle = (float)pos * p.inv_freq[t];
             const float cs = cosf(angle), sn = sinf(angle);
             const float first = c[p.latent + 2 * t], second = c[p.latent + 2 * t + 1];
-            rp[t] = first * cs - second * sn;
-            rp[half + t] = second * cs + first * sn;
+            const float a = first * cs - second * sn, b = second * cs + first * sn;
+            rp[t] = a;
+            rp[half + t] = b;
+            bad |= outside_f16(a) || outside_f16(b);
         }
         // the query rope of every head (same angles as the key's)
 #pragma unroll
@@ -158,10 +180,13 @@ __global__ __launch_bounds__(256) void mla_prep_kernel(MlaParams p, int chunks) 
                 const float angle = (float)pos * fq[k];
                 const float cs = cosf(angle), sn = sinf(angle);
                 float *qr = p.query_rope + ((long)r * p.heads + hh) * p.rope;
-                qr[i] = q1[k] * cs - q2[k] * sn;
-                qr[half + i] = q2[k] * cs + q1[k] * sn;
+                const float a = q1[k] * cs - q2[k] * sn, b = q2[k] * cs + q1[k] * sn;
+                qr[i] = a;
+                qr[half + i] = b;
+                bad |= outside_f16(a) || outside_f16(b);
             }
         }
+        report_range(p, bad);
         return;
     }
     // chunks == 0: the query rope only (prefill absorbs with mla_head_gemm);
@@ -175,8 +200,10 @@ __global__ __launch_bounds__(256) void mla_prep_kernel(MlaParams p, int chunks) 
         const float cs = cosf(angle), sn = sinf(angle);
         const float first = q[p.nope + 2 * t], second = q[p.nope + 2 * t + 1];
         float *qr = p.query_rope + ((long)r * p.heads + h) * p.rope;
-        qr[t] = first * cs - second * sn;
-        qr[half + t] = second * cs + first * sn;
+        const float a = first * cs - second * sn, b = second * cs + first * sn;
+        qr[t] = a;
+        qr[half + t] = b;
+        report_range(p, outside_f16(a) || outside_f16(b));
     }
     if (!chunks) return;
     constexpr int kBatch = 8;  // wave instructions (4 rows each) in flight per lane
@@ -215,9 +242,11 @@ __global__ __launch_bounds__(256) void mla_prep_kernel(MlaParams p, int chunks) 
         for (int e = 0; e < 8; ++e) red[wave][8 * (lane & 15) + e] = acc[e];
     }
     __syncthreads();
-    if (t < kMlaAbsorbCols && cc * kMlaAbsorbCols + t < p.latent)
-        p.query_absorbed[((long)r * p.heads + h) * p.latent + cc * kMlaAbsorbCols + t] =
-            (red[0][t] + red[1][t]) + (red[2][t] + red[3][t]);
+    if (t < kMlaAbsorbCols && cc * kMlaAbsorbCols + t < p.latent) {
+        const float v = (red[0][t] + red[1][t]) + (red[2][t] + red[3][t]);
+        p.query_absorbed[((long)r * p.heads + h) * p.latent + cc * kMlaAbsorbCols + t] = v;
+        report_range(p, outside_f16(v));
+    }
 }
 
 
@@ -619,9 +648,10 @@ __global__ __launch_bounds__(256) void mla_head_gemm_kernel(MlaParams p) {
         for (int i = 0; i < 4; ++i) {
             const long r = m0 + 16 * wave + 4 * g + i;
             if (r < p.rows && n < N) {
-                if constexpr (ABSORB)
+                if constexpr (ABSORB) {
                     p.query_absorbed[(r * p.heads + h) * p.latent + n] = acc[q][i];
-                else
+                    report_range(p, outside_f16(acc[q][i]));
+                } else
                     p.context[(r * p.heads + h) * p.vdim + n] = acc[q][i];
             }
         }

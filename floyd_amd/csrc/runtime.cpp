@@ -1065,6 +1065,8 @@ int attention(MoonlightSession *s, int layer, const float *x, int rows, int posi
     p.context = s->context;
     p.value_part = s->value_part;
     p.merge_count = s->merge_count;
+    p.range_error = s->route_error;  // the forward's error word (route errors: layer + 1)
+    p.range_code = -(layer + 1);
     if (int e = mla_attention_core(p, stream_of(s))) return e;
     return gemv_rows(s, lp.o, s->context, rows, c.head_count * c.value_dim, c.hidden_size, out,
                      nullptr, resid, rf);
@@ -1501,9 +1503,14 @@ int forward(MoonlightSession *s, const int *ids, int count, int start, float *la
     const double wait_end = profile ? monotonic_seconds() : 0.0;
     for (int l = 0; l < c.layer_count; ++l) s->kv_lengths[l] = start + count;
     if (last_logits) memcpy(last_logits, s->host_logits, (size_t)c.vocab_size * sizeof(float));
-    if (*s->host_flag)
+    if (*s->host_flag > 0)
         return set_error(error, error_size, "Moonlight fast route table failed at layer %d",
                          *s->host_flag - 1);
+    if (*s->host_flag < 0)
+        return set_error(error, error_size,
+                         "Moonlight attention failed at layer %d: a query or key value is "
+                         "outside the f16 range of the split-f16 attention products",
+                         -*s->host_flag - 1);
     // the forward is committed: a failed token choice below leaves the
     // session at the new position, ready for the next decode
     float ms = 0.0f;
@@ -1882,10 +1889,13 @@ extern "C" int moonlight_test_attention(MoonlightSession *s, int layer, const fl
         return 0;
     if (!s->model->layers[layer].error.empty()) return 0;
     const size_t bytes = (size_t)rows * c.hidden_size * sizeof(float);
+    hipStream_t st = stream_of(s);
     bool ok = to_device(s, s->tmp, input, bytes) &&
+              hipMemsetAsync(s->route_error, 0, sizeof(int), st) == hipSuccess &&
               attention(s, layer, s->tmp, rows, position, s->h, nullptr, nullptr) == kOk &&
-              to_host(s, output, s->h, bytes);
-    if (!finish(s) || !ok) return 0;
+              to_host(s, output, s->h, bytes) &&
+              to_host(s, s->host_flag, s->route_error, sizeof(int));
+    if (!finish(s) || !ok || *s->host_flag) return 0;
     s->kv_lengths[layer] = position + rows;
     if (s->position < position + rows) s->position = position + rows;
     return 1;

@@ -204,3 +204,51 @@ def test_splitk_repeat_deterministic(device, fmt, rows):
         assert np.array_equal(got.view(np.uint32), first.view(np.uint32))
         native.gemv(fmt, dw2, ds2, dx2, dy2, 1000, 6144, 1)
         assert rel_l2(dy2.download(np.float32), O.matmul(fmt, q2, s2, x2, 1000, 6144).ravel()) < TOL
+
+
+@pytest.mark.parametrize("fmt,out_width,in_width,rows,norm", [
+    (1, 2048, 2048, 1, False),   # LDS-DMA kernel (q8, one row): o_proj
+    (2, 11264, 2048, 1, False),  # register-direct kernel (q4)
+    (1, 3072, 2048, 2, False),   # register-direct kernel (q8, two rows)
+    (1, 2048, 11264, 1, False),  # split-k kernel
+    (2, 2048, 11264, 4, False),
+    (1, 3072, 2048, 2, True),    # RMSNorm: the normalised row is NaN
+])
+def test_gemv_nonfinite_inputs(device, fmt, out_width, in_width, rows, norm):
+    """A NaN or an infinity in x makes the token row's outputs NaN wherever
+    the reference's fp32 dot (x . q, then the scale) is NaN, and NaN or the
+    reference's infinity where that is infinite: never a finite value (the
+    limb split cannot carry them).  Rows without one are unaffected.  Row 0:
+    one +inf; row 1: a +inf and a -inf; row 2: a NaN; row 3: finite."""
+    print(f"[gpu] gemv non-finite x fmt={fmt} O={out_width} I={in_width} rows={rows}", flush=True)
+    q, s = make_weights(fmt, out_width, in_width, seed=4242)
+    x = O.fill_normal(rows * in_width, 17).reshape(rows, in_width)
+    x[0, 7] = np.inf
+    if rows > 1:
+        x[1, 100], x[1, in_width - 3] = np.inf, -np.inf
+    if rows > 2:
+        x[2, 555] = np.nan
+    dw, dx = DeviceBuffer.from_array(q), DeviceBuffer.from_array(x)
+    ds = DeviceBuffer.from_array(s)
+    dy = DeviceBuffer(rows * out_width * 4)
+    if norm:
+        nw = O.fill_normal(in_width, 4, mean=1.0, std=0.1)
+        dn = DeviceBuffer.from_array(nw)
+        native.gemv(fmt, dw, ds, dx, dy, out_width, in_width, rows, norm_w=dn, eps=1e-5)
+        xn = np.empty_like(x)
+        O.lib().orc_rmsnorm(O.fptr(x), O.fptr(nw), O.fptr(xn), rows, in_width, 1e-5)
+        expect = O.matmul(fmt, q, s, xn, out_width, in_width)
+    else:
+        native.gemv(fmt, dw, ds, dx, dy, out_width, in_width, rows)
+        with np.errstate(invalid="ignore", over="ignore"):
+            expect = O.matmul(fmt, q, s, x, out_width, in_width)
+    got = dy.download(np.float32).reshape(rows, out_width)
+    assert np.array_equal(np.isfinite(got), np.isfinite(expect))
+    assert np.isnan(got[np.isnan(expect)]).all()
+    inf = np.isinf(expect)
+    assert (np.isnan(got[inf]) | (got[inf] == expect[inf])).all()
+    assert not np.isfinite(expect[0]).all()  # the case is exercised
+    fin = np.isfinite(expect)
+    if rows > 3:
+        assert fin[3].all() and rel_l2(got[3], expect[3]) < TOL
+    assert rel_l2(got[fin], expect[fin]) < TOL
