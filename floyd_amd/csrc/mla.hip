@@ -847,7 +847,9 @@ __global__ __launch_bounds__(256, 2) void mla_prefill_attend_kernel(MlaParams p)
             }
         }
         lds_barrier();
-        // ---- context: wave w takes the d tiles w, w + 4, ...
+        // ---- context: wave w takes the d tiles w, w + 4, ...; each latent
+        // operand is split once and multiplies the P of every row
+        half4 ph[RB], pl[RB];
 #pragma unroll
         for (int b = 0; b < RB; ++b) {
             const f32x4 pv = *reinterpret_cast<const f32x4 *>(p_s + (b * H + m16) * PS + 4 * g);
@@ -865,20 +867,22 @@ __global__ __launch_bounds__(256, 2) void mla_prefill_attend_kernel(MlaParams p)
 #pragma unroll
                     for (int i = 0; i < 4; ++i) acc[b][q][i] *= scl[i];
             }
-            half4 ph, pl;
-            split_f16<4>(pj, ph, pl);
+            split_f16<4>(pj, ph[b], pl[b]);
+        }
 #pragma unroll
-            for (int q = 0; q < NQ; ++q) {
-                const int dt = wave + 4 * q;
-                if (dt < D / 16) {
-                    const float *lb = kb + (4 * g) * kPfRowStride + dt * 16 + m16;
-                    const float bx[4] = {lb[0], lb[kPfRowStride], lb[2 * kPfRowStride],
-                                         lb[3 * kPfRowStride]};
-                    half4 bh, bl;
-                    split_f16<4>(bx, bh, bl);
-                    acc[b][q] = __builtin_amdgcn_mfma_f32_16x16x16f16(ph, bh, acc[b][q], 0, 0, 0);
-                    acc[b][q] = __builtin_amdgcn_mfma_f32_16x16x16f16(ph, bl, acc[b][q], 0, 0, 0);
-                    acc[b][q] = __builtin_amdgcn_mfma_f32_16x16x16f16(pl, bh, acc[b][q], 0, 0, 0);
+        for (int q = 0; q < NQ; ++q) {
+            const int dt = wave + 4 * q;
+            if (dt < D / 16) {
+                const float *lb = kb + (4 * g) * kPfRowStride + dt * 16 + m16;
+                const float bx[4] = {lb[0], lb[kPfRowStride], lb[2 * kPfRowStride],
+                                     lb[3 * kPfRowStride]};
+                half4 bh, bl;
+                split_f16<4>(bx, bh, bl);
+#pragma unroll
+                for (int b = 0; b < RB; ++b) {
+                    acc[b][q] = __builtin_amdgcn_mfma_f32_16x16x16f16(ph[b], bh, acc[b][q], 0, 0, 0);
+                    acc[b][q] = __builtin_amdgcn_mfma_f32_16x16x16f16(ph[b], bl, acc[b][q], 0, 0, 0);
+                    acc[b][q] = __builtin_amdgcn_mfma_f32_16x16x16f16(pl[b], bh, acc[b][q], 0, 0, 0);
                 }
             }
         }
