@@ -308,11 +308,12 @@ __device__ __forceinline__ float row16_max(float v) {
 }
 #undef MLH_DPP
 
-// fp32 products on the f16 matrix cores: x = hi + lo with hi = f16(x) and
-// lo = f16(x - hi) (22 significant bits), and a.b ~ hi_a.hi_b + hi_a.lo_b +
-// lo_a.hi_b in fp32 accumulation (the dropped lo_a.lo_b and the rounding of
-// lo are ~2^-22 relative).  Values must lie inside the f16 range (|x| <
-// 65504; a larger one turns the products to inf / NaN, not to a wrong finite
+// fp32 products on the f16 matrix cores: x = hi + lo with hi = x truncated
+// to 11 significant bits and lo = f16(x - hi) (21 significant bits), and
+// a.b ~ hi_a.hi_b + hi_a.lo_b + lo_a.hi_b in fp32 accumulation (the dropped
+// lo_a.lo_b and the rounding of lo are ~2^-20 relative).  Values must lie
+// inside the f16 range (|x| < 65504; a larger one turns the products to
+// inf / NaN, not to a wrong finite
 // value).  gfx950 operand layouts (measured): v_mfma_f32_16x16x32_f16 lane l
 // supplies A[l % 16][8 (l / 16) .. + 7] and B[8 (l / 16) .. + 7][l % 16];
 // v_mfma_f32_16x16x16_f16 A[l % 16][4 (l / 16) .. + 3] and B[4 (l / 16) ..
@@ -320,13 +321,17 @@ __device__ __forceinline__ float row16_max(float v) {
 // fp32 16x16x4 instruction does.
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+// hi is x with its low 13 mantissa bits cleared (11 significant bits: exact
+// in f16 for |x| in [2^-14, 65504)), lo = x - hi is exact in fp32 and
+// rounded once to f16, so a split costs a mask, a subtraction and half of
+// each of two packed conversions per value.
 template <int N, typename V>
 __device__ __forceinline__ void split_f16(const float (&x)[N], V &hi, V &lo) {
 #pragma unroll
     for (int i = 0; i < N; ++i) {
-        const _Float16 h = (_Float16)x[i];
-        hi[i] = h;
-        lo[i] = (_Float16)(x[i] - (float)h);
+        const float h = __uint_as_float(__float_as_uint(x[i]) & 0xFFFFE000u);
+        hi[i] = (_Float16)h;
+        lo[i] = (_Float16)(x[i] - h);
     }
 }
 
