@@ -676,17 +676,23 @@ __global__ __launch_bounds__(256) void mla_head_gemm_kernel(MlaParams p) {
 // waves split the 16-wide d tiles).  The normalised lc goes straight to
 // latent_context: no split partials, no merge launch, and every key tile is
 // read once per RB rows instead of once per row.
-constexpr int kPfRowsPerGroup = 2;  // measured: 2 rows per workgroup beat 4
+// Query rows and waves per workgroup.  Measured on MI355X (2048-token
+// prefill): 2 rows on 4 waves 47.6 ms; 4 rows on 8 waves 48.4 ms (the key
+// tiles' f16 splits serve twice the rows, but the kernel is bound by its
+// per-tile barriers and latencies rather than by the vector work); 4 rows
+// on 4 waves exceed the register file.
+constexpr int kPfRowsPerGroup = 2;
+constexpr int kPfWaves = 4;
 constexpr int kPfKeys = 16;
 constexpr int kPfRowStride = kMlaMaxLatent + 4;  // latent rows in LDS (rope in registers)
 // The running max of a (row, head) moves only when a tile's max exceeds it
 // by more than this (e^8 ~ 3e3 keeps every exp term and sum far inside fp32);
 // the context rescale then runs on few tiles.
 constexpr float kPfLazyMax = 8.0f;
-template <int RB>
+template <int RB, int NW>
 constexpr size_t pf_lds_bytes() {
     return sizeof(float) * (2 * (size_t)kPfKeys * kPfRowStride +     // key tiles (latent)
-                            4 * RB * kPfKeys * kMlaMaxHeads +        // score partials
+                            NW * RB * kPfKeys * kMlaMaxHeads +       // score partials
                             RB * kMlaMaxHeads * (kPfKeys + 4) +      // P [row][head][key]
                             3 * RB * kMlaMaxHeads);                  // max, sum, rescale
 }
@@ -705,16 +711,19 @@ __device__ __forceinline__ void lds_barrier() {
     asm volatile("" ::: "memory");
 }
 
-template <int RB>
-__global__ __launch_bounds__(256, 2) void mla_prefill_attend_kernel(MlaParams p) {
+// RB query rows per workgroup of NW waves (4 or 8): wave w takes the 32-dim
+// score steps w, w + NW, ... and the 16-wide context d tiles w, w + NW, ...
+template <int RB, int NW>
+__global__ __launch_bounds__(64 * NW, 8 / NW) void mla_prefill_attend_kernel(MlaParams p) {
+    static_assert(NW == 4 || NW == 8, "4 or 8 waves");
     constexpr int H = kMlaMaxHeads, KS = kPfKeys;
-    constexpr int NJ = (kAttnDims / 32 + 3) / 4;  // 32-dim score steps per wave
-    constexpr int NQ = kMlaMaxLatent / 64;        // d tiles per wave
+    constexpr int NJ = (kAttnDims / 32 + NW - 1) / NW;  // 32-dim score steps per wave
+    constexpr int NQ = kMlaMaxLatent / 16 / NW;         // d tiles per wave
     constexpr int PS = KS + 4;                 // P row stride
     extern __shared__ __attribute__((aligned(16))) float pf_lds[];
     float *kbuf = pf_lds;                            // [2][KS][kPfRowStride]
-    float *part = kbuf + 2 * KS * kPfRowStride;      // [4 waves][RB][KS][H]
-    float *p_s = part + 4 * RB * KS * H;             // [RB][H][PS]
+    float *part = kbuf + 2 * KS * kPfRowStride;      // [NW waves][RB][KS][H]
+    float *p_s = part + NW * RB * KS * H;            // [RB][H][PS]
     float *m_s = p_s + RB * H * PS;                  // [RB][H]
     float *l_s = m_s + RB * H;
     float *sc_s = l_s + RB * H;
@@ -727,7 +736,7 @@ __global__ __launch_bounds__(256, 2) void mla_prefill_attend_kernel(MlaParams p)
     const int ntiles = (keys + KS - 1) / KS;
     const int D = p.latent, R = p.rope, KD = D + R;  // KD a multiple of 16 (launch condition)
     // ---- queries of the rows split into f16 halves (split_f16): dims
-    // 32 (w + 4 j) + 8 g .. + 7 of head m16 (absent rows repeat row r0,
+    // 32 (w + NW j) + 8 g .. + 7 of head m16 (absent rows repeat row r0,
     // absent heads head 0, dims past KD are zero)
     half8 qh8[RB][NJ], ql8[RB][NJ];
 #pragma unroll
@@ -737,7 +746,7 @@ __global__ __launch_bounds__(256, 2) void mla_prefill_attend_kernel(MlaParams p)
         const float *qr = p.query_rope + qh * R;
 #pragma unroll
         for (int j = 0; j < NJ; ++j) {
-            const int d = 32 * (wave + 4 * j) + 8 * g;
+            const int d = 32 * (wave + NW * j) + 8 * g;
             const float *src = d < D ? qa + d : d < KD ? qr + (d - D) : qa;
             const f32x4 v0 = load_f4(src), v1 = load_f4(src + 4);
             const bool in = d < KD;
@@ -752,15 +761,15 @@ __global__ __launch_bounds__(256, 2) void mla_prefill_attend_kernel(MlaParams p)
     }
     // ---- latent rows of a key tile -> LDS buffer by DMA (16 bytes per lane
     // into M0 + 16 lane); the rope part goes to registers: 32-dim step st =
-    // D / 32 + s (dims D + 32 s ..) belongs to wave st % 4, which holds dims
+    // D / 32 + s (dims D + 32 s ..) belongs to wave st % NW, which holds dims
     // D + 32 s + 8 g .. + 7 of key m16 (rope dims past R read dim 0 against a
     // zero query).  Rows past the last key copy the last key (finite, masked).
-    const int rope_s = ((wave - D / 32) % 4 + 4) % 4;  // this wave's rope step
+    const int rope_s = ((wave - D / 32) % NW + NW) % NW;  // this wave's rope step
     const bool has_rope = 32 * rope_s < R;
     const int rope_col = 32 * rope_s + 8 * g < R ? 32 * rope_s + 8 * g : 0;
     auto issue = [&](int tile, int buf, f32x4 (&rope_next)[2]) {
         float *kb = kbuf + buf * KS * kPfRowStride;
-        for (int row = wave; row < KS; row += 4) {
+        for (int row = wave; row < KS; row += NW) {
             const int k = tile * KS + row < keys ? tile * KS + row : keys - 1;
             const float *lsrc = p.latent_cache + (long)k * D;
             __attribute__((address_space(3))) float *dst =
@@ -792,7 +801,7 @@ __global__ __launch_bounds__(256, 2) void mla_prefill_attend_kernel(MlaParams p)
         rope_cur[1] = rope_next[1];
         if (kt + 1 < ntiles) issue(kt + 1, (kt + 1) & 1, rope_next);
         const float *kb = kbuf + (kt & 1) * KS * kPfRowStride;
-        // ---- scores of the tile: wave w takes the 32-dim steps w, w + 4, ...
+        // ---- scores of the tile: wave w takes the 32-dim steps w, w + NW, ...
         // (v_mfma_f32_16x16x32_f16, split-f16 triples, two accumulator chains)
         {
             f32x4v sacc[RB][2];
@@ -800,7 +809,7 @@ __global__ __launch_bounds__(256, 2) void mla_prefill_attend_kernel(MlaParams p)
             for (int b = 0; b < RB; ++b) sacc[b][0] = sacc[b][1] = f32x4v{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int j = 0; j < NJ; ++j) {
-                const int d0 = 32 * (wave + 4 * j);
+                const int d0 = 32 * (wave + NW * j);
                 if (d0 < KD) {
                     f32x4 a0, a1;
                     if (d0 < D) {
@@ -832,8 +841,9 @@ __global__ __launch_bounds__(256, 2) void mla_prefill_attend_kernel(MlaParams p)
         // ---- causal mask and online softmax: 16 lanes per (row, head), one key each
         for (int idx = t; idx < RB * H * KS; idx += blockDim.x) {
             const int b = idx / (H * KS), h = (idx / KS) % H, k = idx % KS;
-            const float sum = (part[((0 * RB + b) * KS + k) * H + h] + part[((1 * RB + b) * KS + k) * H + h]) +
-                              (part[((2 * RB + b) * KS + k) * H + h] + part[((3 * RB + b) * KS + k) * H + h]);
+            auto pw = [&](int w) { return part[((w * RB + b) * KS + k) * H + h]; };
+            float sum = (pw(0) + pw(1)) + (pw(2) + pw(3));
+            if constexpr (NW == 8) sum += (pw(4) + pw(5)) + (pw(6) + pw(7));
             const int key = kt * KS + k;
             const bool valid = b < nrow && key <= pos0 + b;
             const float sv = valid ? sum * p.scale : -INFINITY;
@@ -852,7 +862,7 @@ __global__ __launch_bounds__(256, 2) void mla_prefill_attend_kernel(MlaParams p)
             }
         }
         lds_barrier();
-        // ---- context: wave w takes the d tiles w, w + 4, ...; each latent
+        // ---- context: wave w takes the d tiles w, w + NW, ...; each latent
         // operand is split once and multiplies the P of every row
         half4 ph[RB], pl[RB];
 #pragma unroll
@@ -876,7 +886,7 @@ __global__ __launch_bounds__(256, 2) void mla_prefill_attend_kernel(MlaParams p)
         }
 #pragma unroll
         for (int q = 0; q < NQ; ++q) {
-            const int dt = wave + 4 * q;
+            const int dt = wave + NW * q;
             if (dt < D / 16) {
                 const float *lb = kb + (4 * g) * kPfRowStride + dt * 16 + m16;
                 const float bx[4] = {lb[0], lb[kPfRowStride], lb[2 * kPfRowStride],
@@ -899,7 +909,7 @@ __global__ __launch_bounds__(256, 2) void mla_prefill_attend_kernel(MlaParams p)
         if (b >= nrow) continue;
 #pragma unroll
         for (int q = 0; q < NQ; ++q) {
-            const int dt = wave + 4 * q;
+            const int dt = wave + NW * q;
             if (dt >= D / 16) continue;
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
@@ -1112,10 +1122,10 @@ int mla_attention_core(const MlaParams &p, hipStream_t stream) {
     if (p.rows > 1 && !p.grid_splits && p.nope % 16 == 0 && p.vdim % 16 == 0) {
         // prefill: cache append + query rope, the absorb as a per-head GEMM,
         // flash attention writing lc directly, the value as a per-head GEMM
-        constexpr int RB = kPfRowsPerGroup;
+        constexpr int RB = kPfRowsPerGroup, NW = kPfWaves;
         static const bool attr = hipFuncSetAttribute(
-            reinterpret_cast<const void *>(&mla_prefill_attend_kernel<RB>),
-            hipFuncAttributeMaxDynamicSharedMemorySize, (int)pf_lds_bytes<RB>()) == hipSuccess;
+            reinterpret_cast<const void *>(&mla_prefill_attend_kernel<RB, NW>),
+            hipFuncAttributeMaxDynamicSharedMemorySize, (int)pf_lds_bytes<RB, NW>()) == hipSuccess;
         (void)attr;
         const unsigned mt = (unsigned)((p.rows + 63) / 64);
         hipLaunchKernelGGL(mla_prep_kernel<kF32>, dim3(p.rows, 1 + p.heads), dim3(256), 0, stream,
@@ -1123,8 +1133,8 @@ int mla_attention_core(const MlaParams &p, hipStream_t stream) {
         hipLaunchKernelGGL(mla_head_gemm_kernel<true>,
                            dim3(mt, (unsigned)((p.latent + 63) / 64), (unsigned)p.heads), dim3(256),
                            0, stream, p);
-        hipLaunchKernelGGL(mla_prefill_attend_kernel<RB>, dim3((p.rows + RB - 1) / RB), dim3(256),
-                           pf_lds_bytes<RB>(), stream, p);
+        hipLaunchKernelGGL((mla_prefill_attend_kernel<RB, NW>), dim3((p.rows + RB - 1) / RB),
+                           dim3(64 * NW), (pf_lds_bytes<RB, NW>()), stream, p);
         hipLaunchKernelGGL(mla_head_gemm_kernel<false>,
                            dim3(mt, (unsigned)((p.vdim + 63) / 64), (unsigned)p.heads), dim3(256),
                            0, stream, p);
