@@ -536,6 +536,9 @@ def main():
     parser.add_argument("--sizes", type=str, default="",
                         help="comma-separated MoE row counts (--moe-only) or contexts "
                              "(--attn-only) in place of the defaults")
+    parser.add_argument("--gemv-only", type=str, default="", metavar="FMT,O,I,B",
+                        help="only one GEMV shape (fmt 0 f32, 1 q8, 2 q4), graph launches "
+                             "over rotated weight copies (profiler runs)")
     parser.add_argument("--decode-only", type=int, default=0, metavar="CTX",
                         help="only greedy decode steps of the synthetic model at context "
                              "CTX, printed per token (profiler runs)")
@@ -554,6 +557,17 @@ def main():
         return
     if args.decode_only:
         decode_only(args.decode_only, args.decode_tokens)
+        return
+    if args.gemv_only:
+        fmt, o, i, rows = (int(v) for v in args.gemv_only.split(","))
+        case = GemvCase(native, fmt, o, i, rows, seed=1000)
+        us, gbs = case.time(args.warmup, args.steps)
+        print(f"[bench] gemv fmt={fmt} {o}x{i} B={rows}: {us:.2f} us {gbs:.0f} GB/s "
+              f"({case.bytes} bytes, {native.gemv_kernel_name(fmt, o, i, rows)})",
+              file=sys.stderr, flush=True)
+        print(json.dumps({"fmt": fmt, "O": o, "I": i, "rows": rows, "us": round(us, 3),
+                          "GB/s": round(gbs, 1), "bytes": case.bytes}), flush=True)
+        case.close()
         return
     if args.prefill_only:
         prefill_only()
