@@ -28,6 +28,19 @@
 // 16 weight rows.  Only the final cross-wave sum meets in LDS (one
 // barrier).  LDS rows of weights are XOR-swizzled in 16-byte chunks so the
 // 16 rows an operand read touches hit distinct banks.
+//
+// Three kernels share that scheme:
+//   gemv_mfma_kernel         the LDS-DMA form above (any k, 8 or 16 rows);
+//   gemv_mfma_direct_kernel  k = 2048: a wave's 512-element quarter of each
+//                            weight row goes straight into registers in the
+//                            MFMA B layout (no LDS copy of the weights);
+//   gemv_mfma_splitk_kernel  k > 4096 with at most 4096 rows: workgroups of
+//                            (16-row block, 2048-wide k split); each stores
+//                            its share, and the block's last-arriving
+//                            workgroup adds the shares in split order and
+//                            applies the epilogue.
+// Every kernel also sums x^2 over its k range; a non-finite sum (a NaN or
+// infinite x, which the int8 limbs cannot carry) makes the row's output NaN.
 #include "mlh_device.h"
 #include "mlh_host.h"
 

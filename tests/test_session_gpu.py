@@ -64,6 +64,36 @@ def test_model_info_and_lifecycle(tiny):
         S.Session(model, 16, 32)
 
 
+PROFILE_LINE = (r"moonlight profile rows=(\d+) start=(\d+) layers=(\d+) graph=([01]) "
+                r"encode=([0-9.]+) wait=([0-9.]+) gpu=([0-9.]+) ms")
+
+
+def test_moonlight_profile_lines(tiny, capfd, monkeypatch):
+    """MOONLIGHT_PROFILE (moonlight_metal.m:1899, 1932-1937, 1972-1979): with
+    the variable set, every forward prints one timing line on stderr (a
+    forward is one submission here); the first decode runs eagerly and the
+    later ones replay the captured graph.  Without it nothing is printed."""
+    import re
+    cfg, tensors, model = tiny
+    sess = S.Session(model, 64, 8)
+    monkeypatch.setenv("MOONLIGHT_PROFILE", "1")
+    capfd.readouterr()
+    sess.prefill([1, 2, 3])
+    for tok in (4, 5, 6):
+        sess.decode(tok)
+    lines = [l for l in capfd.readouterr().err.splitlines() if l.startswith("moonlight profile")]
+    got = [re.fullmatch(PROFILE_LINE, l) for l in lines]
+    assert len(got) == 4 and all(got), lines
+    fields = [(int(m[1]), int(m[2]), int(m[3]), int(m[4])) for m in got]
+    assert fields == [(3, 0, cfg["layer_count"], 0), (1, 3, cfg["layer_count"], 0),
+                      (1, 4, cfg["layer_count"], 1), (1, 5, cfg["layer_count"], 1)]
+    assert all(float(m[7]) > 0.0 for m in got)
+    monkeypatch.delenv("MOONLIGHT_PROFILE")
+    sess.decode(7)
+    assert "moonlight profile" not in capfd.readouterr().err
+    sess.close()
+
+
 def test_primitives(tiny):
     cfg, tensors, model = tiny
     orc = CU.oracle_model(cfg, tensors, 64)
