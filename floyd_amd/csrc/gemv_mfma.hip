@@ -11,7 +11,8 @@
 //     x ~= 2^-e * q,  q = rint(x * 2^e) = 2^24 L0 + 2^16 L1 + 2^8 L2 + L3,
 // L0 in [-64, 64], L1..L3 in [-128, 127].  x * 2^e is exact in fp32, so the
 // only rounding is rint's (at most half a step, and never more than fp32's
-// own rounding of x for the wave's larger elements).  The products of the
+// own rounding of x for the wave's larger elements); the four limbs are the
+// bytes of (q + 0x808080) ^ 0x808080 (split_limbs8).  The products of the
 // stored weights with each limb are exact int32 sums on the matrix cores;
 // the limbs are combined and scaled in fp32 once per wave, the four waves'
 // shares added in fp32 and multiplied by the row scale.  q4 weights enter as
@@ -29,16 +30,20 @@
 // barrier).  LDS rows of weights are XOR-swizzled in 16-byte chunks so the
 // 16 rows an operand read touches hit distinct banks.
 //
-// Three kernels share that scheme:
+// Four kernels share that scheme:
 //   gemv_mfma_kernel         the LDS-DMA form above (any k, 8 or 16 rows);
 //   gemv_mfma_direct_kernel  k = 2048: a wave's 512-element quarter of each
 //                            weight row goes straight into registers in the
 //                            MFMA B layout (no LDS copy of the weights);
-//   gemv_mfma_splitk_kernel  k > 4096 with at most 4096 rows: workgroups of
-//                            (16-row block, 2048-wide k split); each stores
-//                            its share, and the block's last-arriving
-//                            workgroup adds the shares in split order and
-//                            applies the epilogue.
+//   gemv_mfma_wide_kernel    one token row, k a multiple of 1024 above 4096,
+//                            2048 or 4096 rows: k / 1024 waves per
+//                            workgroup of 8 rows, the MFMA's 16 columns
+//                            holding the 8 rows at two k slices;
+//   gemv_mfma_splitk_kernel  other k > 4096 with at most 4096 rows:
+//                            workgroups of (16-row block, 2048-wide k
+//                            split); each stores its share, and the block's
+//                            last-arriving workgroup adds the shares in
+//                            split order and applies the epilogue.
 // Every kernel also sums x^2 over its k range; a non-finite sum (a NaN or
 // infinite x, which the int8 limbs cannot carry) makes the row's output NaN.
 #include "mlh_device.h"
@@ -109,6 +114,40 @@ template <int FMT>
 __device__ __forceinline__ int slice_pos(int e) {
     if constexpr (FMT == kQ4) return (e & 8) + ((e & 1) << 2) + ((e & 7) >> 1);
     return e;
+}
+
+// The four limbs of 8 elements of x (already scaled by the step's inverse),
+// packed as the limb rows store them: lw[L][w] holds limb L of the elements
+// at byte positions 4 w .. 4 w + 3 (slice_pos order).  The balanced base-256
+// digits of q are the bytes of (q + 0x808080) ^ 0x808080: adding 128 to each
+// of the three low digits makes them the plain bytes of the sum (each in
+// 0..255), the xor takes the 128 off again in int8, and the top byte is L0.
+// So an element costs a rounding, a conversion, an add and an xor, and a 4 x
+// 4 byte transpose by v_perm_b32 gathers the limbs of 4 elements.
+__device__ __forceinline__ void limb_transpose(unsigned e0, unsigned e1, unsigned e2, unsigned e3,
+                                               unsigned &l0, unsigned &l1, unsigned &l2,
+                                               unsigned &l3) {
+    const unsigned a01 = __builtin_amdgcn_perm(e1, e0, 0x06020400u);  // e0.b0 e1.b0 e0.b2 e1.b2
+    const unsigned b01 = __builtin_amdgcn_perm(e1, e0, 0x07030501u);  // e0.b1 e1.b1 e0.b3 e1.b3
+    const unsigned a23 = __builtin_amdgcn_perm(e3, e2, 0x06020400u);
+    const unsigned b23 = __builtin_amdgcn_perm(e3, e2, 0x07030501u);
+    l3 = __builtin_amdgcn_perm(a23, a01, 0x05040100u);  // byte 0 of e0..e3
+    l2 = __builtin_amdgcn_perm(b23, b01, 0x05040100u);  // byte 1
+    l1 = __builtin_amdgcn_perm(a23, a01, 0x07060302u);  // byte 2
+    l0 = __builtin_amdgcn_perm(b23, b01, 0x07060302u);  // byte 3
+}
+template <int FMT>
+__device__ __forceinline__ void split_limbs8(const float (&v8)[8], float step_inv,
+                                             unsigned (&lw)[4][2]) {
+    unsigned e[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+        e[i] = (unsigned)((int)rintf(v8[i] * step_inv) + 0x808080) ^ 0x808080u;
+    // q8: bytes in element order; q4: elements 0,2,4,6 | 1,3,5,7 (slice_pos)
+    constexpr int i1 = FMT == kQ4 ? 2 : 1, i2 = FMT == kQ4 ? 4 : 2, i3 = FMT == kQ4 ? 6 : 3;
+    constexpr int j0 = FMT == kQ4 ? 1 : 4, j1 = FMT == kQ4 ? 3 : 5, j2 = FMT == kQ4 ? 5 : 6, j3 = 7;
+    limb_transpose(e[0], e[i1], e[i2], e[i3], lw[0][0], lw[1][0], lw[2][0], lw[3][0]);
+    limb_transpose(e[j0], e[j1], e[j2], e[j3], lw[0][1], lw[1][1], lw[2][1], lw[3][1]);
 }
 
 // A token row whose x holds a NaN or an infinity (its sum of squares of x is
@@ -314,25 +353,8 @@ __global__ __launch_bounds__(256) void gemv_mfma_kernel(MfmaGemvArgs a) {
         for (int b = 0; b < B; ++b) {
             const float v8[8] = {xv[j][b][0].x, xv[j][b][0].y, xv[j][b][0].z, xv[j][b][0].w,
                                  xv[j][b][1].x, xv[j][b][1].y, xv[j][b][1].z, xv[j][b][1].w};
-#pragma unroll
-            for (int L = 0; L < 4; ++L) lw[j][b][L][0] = lw[j][b][L][1] = 0u;
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const int q = (int)rintf(v8[i] * step_inv[b]);
-                // balanced base-256 digits: q = 2^24 L0 + 2^16 L1 + 2^8 L2 + L3
-                const int l3 = (int)(signed char)(q & 255);
-                int r = (q - l3) >> 8;
-                const int l2 = (int)(signed char)(r & 255);
-                r = (r - l2) >> 8;
-                const int l1 = (int)(signed char)(r & 255);
-                const int l0 = (r - l1) >> 8;
-                const int pos = slice_pos<FMT>(i);  // 0..7 within the 8 bytes
-                const int wd = pos >> 2, sh = 8 * (pos & 3);
-                lw[j][b][0][wd] |= (unsigned)(l0 & 255) << sh;
-                lw[j][b][1][wd] |= (unsigned)(l1 & 255) << sh;
-                lw[j][b][2][wd] |= (unsigned)(l2 & 255) << sh;
-                lw[j][b][3][wd] |= (unsigned)(l3 & 255) << sh;
-            }
+            // balanced base-256 digits: q = 2^24 L0 + 2^16 L1 + 2^8 L2 + L3
+            split_limbs8<FMT>(v8, step_inv[b], lw[j][b]);
         }
     }
     // this wave's DMA has landed; no LDS access may be scheduled above the
@@ -374,8 +396,8 @@ __global__ __launch_bounds__(256) void gemv_mfma_kernel(MfmaGemvArgs a) {
     // supplies k bytes 16 g .. 16 g + 15 of the step
     const int m = lane & 15, g = lane >> 4;
     const int limb = m >> 2, tb = m & 3;
-    const bool a_ok = tb < B;
-    const unsigned char *arow = xl + (limb * B + (a_ok ? tb : 0)) * xrow;
+    // (rows of b >= B repeat token row 0: their products are not used)
+    const unsigned char *arow = xl + (limb * B + (tb < B ? tb : 0)) * xrow;
     const int n = lane & 15;
     const int wn = n & (RW - 1);  // weight row of MFMA column n
     const unsigned char *wrow = wl + wn * kqb;
@@ -408,8 +430,7 @@ __global__ __launch_bounds__(256) void gemv_mfma_kernel(MfmaGemvArgs a) {
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int i = 0; i < U; ++i) {
-            const i32x4 A = a_ok ? i32x4{(int)av[i].x, (int)av[i].y, (int)av[i].z, (int)av[i].w}
-                                 : i32x4{0, 0, 0, 0};
+            const i32x4 A = i32x4{(int)av[i].x, (int)av[i].y, (int)av[i].z, (int)av[i].w};
             i32x4 Bw, Bu;
             if constexpr (FMT == kQ8) {
                 Bw = i32x4{(int)wv[i].x, (int)wv[i].y, (int)wv[i].z, (int)wv[i].w};
@@ -599,23 +620,8 @@ __device__ __forceinline__ void direct_wave(const GemvParams &p, int row0, int k
             for (int b = 0; b < B; ++b) {
                 const float v8[8] = {xv[j][b][0].x, xv[j][b][0].y, xv[j][b][0].z, xv[j][b][0].w,
                                      xv[j][b][1].x, xv[j][b][1].y, xv[j][b][1].z, xv[j][b][1].w};
-                unsigned lw[4][2] = {{0u, 0u}, {0u, 0u}, {0u, 0u}, {0u, 0u}};
-#pragma unroll
-                for (int i = 0; i < 8; ++i) {
-                    const int q = (int)rintf(v8[i] * step_inv[b]);
-                    const int l3 = (int)(signed char)(q & 255);
-                    int r = (q - l3) >> 8;
-                    const int l2 = (int)(signed char)(r & 255);
-                    r = (r - l2) >> 8;
-                    const int l1 = (int)(signed char)(r & 255);
-                    const int l0 = (r - l1) >> 8;
-                    const int pos = slice_pos<FMT>(i);
-                    const int wd = pos >> 2, sh = 8 * (pos & 3);
-                    lw[0][wd] |= (unsigned)(l0 & 255) << sh;
-                    lw[1][wd] |= (unsigned)(l1 & 255) << sh;
-                    lw[2][wd] |= (unsigned)(l2 & 255) << sh;
-                    lw[3][wd] |= (unsigned)(l3 & 255) << sh;
-                }
+                unsigned lw[4][2];
+                split_limbs8<FMT>(v8, step_inv[b], lw);
 #pragma unroll
                 for (int Lb = 0; Lb < 4; ++Lb)
                     *reinterpret_cast<uint2 *>(xl + (Lb * B + b) * xrow + e) =
@@ -626,11 +632,11 @@ __device__ __forceinline__ void direct_wave(const GemvParams &p, int row0, int k
     // (a wave reads only its own limb rows: its LDS stores complete in order
     // before its reads below)
 
-    // ---- MFMA steps: A row m = 4 L + b from LDS, B column n from registers
+    // ---- MFMA steps: A row m = 4 L + b from LDS (rows of b >= B repeat
+    // token row 0: their products are not used), B column n from registers
     const int m = lane & 15;
     const int limb = m >> 2, tb = m & 3;
-    const bool a_ok = tb < B;
-    const unsigned char *arow = xl + (limb * B + (a_ok ? tb : 0)) * xrow;
+    const unsigned char *arow = xl + (limb * B + (tb < B ? tb : 0)) * xrow;
     i32x4 acc = {0, 0, 0, 0}, acc2 = {0, 0, 0, 0}, acc1 = {0, 0, 0, 0};
     const i32x4 ones = {0x01010101, 0x01010101, 0x01010101, 0x01010101};
     u32x4 av[S];
@@ -641,8 +647,7 @@ __device__ __forceinline__ void direct_wave(const GemvParams &p, int row0, int k
     }
 #pragma unroll
     for (int s = 0; s < S; ++s) {
-        const i32x4 A = a_ok ? i32x4{(int)av[s].x, (int)av[s].y, (int)av[s].z, (int)av[s].w}
-                             : i32x4{0, 0, 0, 0};
+        const i32x4 A = i32x4{(int)av[s].x, (int)av[s].y, (int)av[s].z, (int)av[s].w};
         i32x4 Bw, Bu;
         if constexpr (FMT == kQ8) {
             Bw = i32x4{(int)wv[s].x, (int)wv[s].y, (int)wv[s].z, (int)wv[s].w};
@@ -817,6 +822,184 @@ __global__ __launch_bounds__(256) void gemv_mfma_splitk_kernel(GemvParams p) {
     if (lane == 0) __hip_atomic_store(count, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Wide-k form with no sum across workgroups, for one token row, k a multiple
+// of 1024 in (4096, 16384] and 2048 or 4096 rows (config 1's 2048 x 11264,
+// the dense down projection at decode).  A workgroup of k / 1024 waves owns
+// 8 output rows and the whole k range; wave w takes the columns [1024 w,
+// 1024 w + 1024) as two slices of 512.  The matrix-core B operand's 16
+// columns hold the 8 rows at both slices (column n: row n % 8, slice n / 8)
+// and A row 4 L + h holds limb L of x's slice h, so C[4 L + h][8 h + r] is
+// limb L's product of row r over slice h; the other products are not used.
+// A wave streams 8 rows x 1024 columns, as many weight bytes as a wave of
+// the direct kernel (16 rows x 512), and splits 1024 elements of x once
+// (one power-of-two step for both slices).  The waves' row totals meet in
+// LDS and wave 0 adds them in wave order.
+constexpr int kWideRows = 8;
+constexpr int kWideSlice = 512;
+constexpr int kWideMaxWaves = 16;
+
+struct WideLds {
+    static constexpr int kXrow = kWideSlice + kXPad;
+    unsigned char xl[kWideMaxWaves][4 * 2 * kXrow];  // per wave: [limb][slice][xrow]
+    float red[kWideMaxWaves][kWideRows];
+    float red_ss[kWideMaxWaves];
+};
+
+template <int FMT>
+__global__ __launch_bounds__(1024) void gemv_mfma_wide_kernel(GemvParams p) {
+    __shared__ __attribute__((aligned(16))) WideLds L;
+    constexpr int S = kWideSlice / 64;          // MFMA steps per slice
+    constexpr int NW = FMT == kQ8 ? S : S / 2;  // 16-byte weight pieces per lane
+    constexpr int xrow = WideLds::kXrow;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nwaves = blockDim.x >> 6;
+    const int row0 = blockIdx.x * kWideRows;
+    const int n = lane & 15, g = lane >> 4;
+    const int h = n >> 3;  // this lane's B column: row row0 + (n & 7) at slice h
+    const int wrow = row0 + (n & 7) < p.O ? row0 + (n & 7) : p.O - 1;
+    const int k0 = wave * 2 * kWideSlice;
+    const long row_bytes = FMT == kQ8 ? p.I : p.I / 2;
+    unsigned char *xl = L.xl[wave];
+
+    // ---- x (and norm_w) of both slices, then the weights, then the
+    // epilogue's operands: in-order completion lets the split start while
+    // the weights are in flight
+    const bool has_norm = p.norm_w != nullptr;
+    const float *nw = has_norm ? p.norm_w : p.x;
+    f32x4 xv[2][2], nv[2][2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const int e = k0 + j * kWideSlice + lane * 8;
+        xv[j][0] = load_f4(p.x + e);
+        xv[j][1] = load_f4(p.x + e + 4);
+        nv[j][0] = load_f4(nw + e);
+        nv[j][1] = load_f4(nw + e + 4);
+    }
+    const int kw = k0 + h * kWideSlice;
+    const long w_off = (long)wrow * row_bytes + (FMT == kQ8 ? kw : kw / 2) + 16 * g;
+    u32x4 wv[NW];
+#pragma unroll
+    for (int i = 0; i < NW; ++i) wv[i] = load_global16(p.w + w_off + 64 * i);
+    const bool has_res = p.epilogue == kEpiResidual;
+    float e_s = 0.0f, e_res = 0.0f;
+    if (wave == 0) {
+        e_s = p.s[wrow];
+        e_res = has_res ? p.resid[wrow] : 0.0f;
+    }
+
+    // ---- split x into four limbs against one step for the wave's range
+    float ss = 0.0f, amax = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+            f32x4 v = xv[j][q];
+            ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+            if (has_norm) {
+                v.x *= nv[j][q].x;
+                v.y *= nv[j][q].y;
+                v.z *= nv[j][q].z;
+                v.w *= nv[j][q].w;
+            }
+            xv[j][q] = v;
+            amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+        }
+    }
+    amax = dpp_wave_max(amax);
+    ss = dpp_wave_sum(ss);
+    int e2 = 0;
+    (void)frexpf(amax, &e2);  // amax < 2^e2
+    const int ex = amax > 0.0f ? 30 - e2 : 0;
+    const float step_inv = ldexpf(1.0f, ex), step = ldexpf(1.0f, -ex);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const float v8[8] = {xv[j][0].x, xv[j][0].y, xv[j][0].z, xv[j][0].w,
+                             xv[j][1].x, xv[j][1].y, xv[j][1].z, xv[j][1].w};
+        unsigned lw[4][2];
+        split_limbs8<FMT>(v8, step_inv, lw);
+#pragma unroll
+        for (int Lb = 0; Lb < 4; ++Lb)
+            *reinterpret_cast<uint2 *>(xl + (Lb * 2 + j) * xrow + lane * 8) = uint2{lw[Lb][0], lw[Lb][1]};
+    }
+    // (a wave reads only its own limb rows: its LDS stores complete in order
+    // before its reads below)
+
+    // ---- MFMA steps: A row m = 4 L + slice from LDS, B column n from
+    // registers (A rows 4 L + 2 and 4 L + 3 repeat slice 0 and 1: their
+    // products are not used)
+    const int m = lane & 15;
+    const unsigned char *arow = xl + ((m >> 2) * 2 + (m & 1)) * xrow;
+    i32x4 acc = {0, 0, 0, 0}, acc1 = {0, 0, 0, 0};
+    const i32x4 ones = {0x01010101, 0x01010101, 0x01010101, 0x01010101};
+    u32x4 av[S];
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+        const int aoff = FMT == kQ8 ? 64 * s + 16 * g : 128 * (s >> 1) + 32 * g + 16 * (s & 1);
+        av[s] = *reinterpret_cast<const u32x4 *>(arow + aoff);
+    }
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+        const i32x4 A = i32x4{(int)av[s].x, (int)av[s].y, (int)av[s].z, (int)av[s].w};
+        i32x4 Bw;
+        if constexpr (FMT == kQ8) {
+            Bw = i32x4{(int)wv[s].x, (int)wv[s].y, (int)wv[s].z, (int)wv[s].w};
+        } else {
+            const u32x4 w4 = wv[s >> 1];
+            const unsigned wx = (s & 1) ? w4.z : w4.x, wy = (s & 1) ? w4.w : w4.y;
+            Bw = i32x4{(int)(wx & 0x0F0F0F0Fu), (int)((wx >> 4) & 0x0F0F0F0Fu),
+                       (int)(wy & 0x0F0F0F0Fu), (int)((wy >> 4) & 0x0F0F0F0Fu)};
+            acc1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A, ones, acc1, 0, 0, 0);
+        }
+        acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(A, Bw, acc, 0, 0, 0);
+    }
+    // ---- lane (g, n) holds limb g of slices 0..1 (registers 0..1) for
+    // column n; its own product is slice h.  Limbs, then the two slices, are
+    // added across lanes (each sum is commutative, so every lane of a row
+    // ends with the same bits)
+    int c = h ? acc[1] : acc[0];
+    if constexpr (FMT == kQ4) c -= 8 * (h ? acc1[1] : acc1[0]);
+    const float limb_w = g == 0 ? 16777216.0f : g == 1 ? 65536.0f : g == 2 ? 256.0f : 1.0f;
+    float v = (float)c * limb_w * step;
+    v += __shfl_xor(v, 16);
+    v += __shfl_xor(v, 32);
+    v += __shfl_xor(v, 8);
+    if (lane < kWideRows) L.red[wave][lane] = v;
+    if (lane == 0) L.red_ss[wave] = ss;
+    __syncthreads();
+    if (wave != 0 || lane >= kWideRows || row0 + lane >= p.O) return;
+    float tot = 0.0f, tss = 0.0f;
+    for (int w = 0; w < nwaves; ++w) {
+        tot += L.red[w][lane];
+        tss += L.red_ss[w];
+    }
+    const float inv_rms = has_norm ? 1.0f / sqrtf(tss / (float)p.I + p.eps) : 1.0f;
+    const float sum = nonfinite_guard(tss, (tot * inv_rms) * e_s);
+    p.y[row0 + lane] = has_res ? e_res + sum : sum;
+}
+
+// The wide-k kernel takes p (one token row, k a multiple of 1024 in (4096,
+// 16384], 2048 or 4096 rows: one or two workgroups per CU).  Measured on
+// MI355X against the split-k kernel (same box, medians of graph replays):
+// q4 2048 x 11264 6.10 against 7.42 us, q8 2048 x 11264 7.74 against 8.80,
+// q4 2048 x 16384 7.13 against 8.69; q8 3000 x 7168 (375 workgroups, spread
+// unevenly over the CUs) 8.52 against 8.28, which stays on split-k.
+bool wide_ok(const GemvParams &p) {
+    return (p.fmt == kQ8 || p.fmt == kQ4) && p.rows == 1 && p.epilogue != kEpiSiluDual &&
+           !p.limbs && !p.router_parts && p.I > 4096 && p.I <= 1024 * kWideMaxWaves &&
+           p.I % 1024 == 0 && (p.O == 2048 || p.O == 4096);
+}
+template <int FMT>
+bool launch_wide(const GemvParams &p, hipStream_t stream, std::string *name) {
+    if (name) {
+        char buf[96];
+        snprintf(buf, sizeof(buf), "mlh::(anonymous namespace)::gemv_mfma_wide_kernel<%d>", FMT);
+        *name = buf;
+        return true;
+    }
+    hipLaunchKernelGGL((gemv_mfma_wide_kernel<FMT>), dim3((p.O + kWideRows - 1) / kWideRows),
+                       dim3(64 * (p.I / 1024)), 0, stream, p);
+    return true;
+}
+
 template <int FMT, int B, bool DUAL, int KQ>
 bool launch_direct(const GemvParams &p, hipStream_t stream, std::string *name) {
     if (name) {
@@ -983,7 +1166,7 @@ bool gemv_router_ok(const GemvParams &p) {
     GemvParams q = p;
     q.router_parts = nullptr;
     std::string name;
-    return splitk_splits(q) == 0 && gemv_mfma(q, nullptr, &name);
+    return splitk_splits(q) == 0 && !wide_ok(q) && gemv_mfma(q, nullptr, &name);
 }
 
 int gemv_router_parts(const GemvParams &p) {
@@ -992,9 +1175,14 @@ int gemv_router_parts(const GemvParams &p) {
 }
 
 bool gemv_mfma(const GemvParams &p, hipStream_t stream, std::string *name) {
-    // wide-k matrices with few rows: the split-k kernel
+    auto al = [](const void *q) { return ((uintptr_t)q & 15u) == 0; };
+    // wide-k matrices with few rows: at one token row and 2048 rows or more
+    // the wide kernel, else the split-k kernel
+    if (wide_ok(p)) {
+        if (!name && (!al(p.w) || !al(p.x) || (p.norm_w && !al(p.norm_w)))) return false;
+        return p.fmt == kQ8 ? launch_wide<kQ8>(p, stream, name) : launch_wide<kQ4>(p, stream, name);
+    }
     if (const int splits = splitk_splits(p)) {
-        auto al = [](const void *q) { return ((uintptr_t)q & 15u) == 0; };
         if (!name && (!al(p.w) || !al(p.x) || p.x_stride % 4 || (p.norm_w && !al(p.norm_w))))
             return false;
         return p.fmt == kQ8 ? launch_splitk_b<kQ8>(p, splits, stream, name)

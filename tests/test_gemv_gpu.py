@@ -41,6 +41,11 @@ SHAPES = [
     # past O (1000, 2040)
     (1, 2048, 11264, 4), (2, 2048, 11264, 2), (1, 512, 5120, 1), (2, 1000, 6144, 4),
     (1, 2040, 8192, 2),
+    # wide kernel (one row, I a multiple of 1024 in (4096, 16384], O 2048 or
+    # 4096; config 1's 2048 x 11264 above): 16 and 5 waves, O = 4096; O =
+    # 2053 and 3000 take split-k
+    (2, 2048, 16384, 1), (1, 2048, 5120, 1), (2, 4096, 11264, 1), (1, 3000, 7168, 1),
+    (1, 2053, 5120, 1),
 ]
 
 
@@ -64,8 +69,9 @@ def test_gemv_matches_oracle(device, fmt, out_width, in_width, rows):
     (0, 163840 // 16, 2048, 1),
     # narrow rows with a partially filled last wave (lane groups past O)
     (1, 80, 256, 2), (2, 80, 256, 1), (1, 40, 128, 3), (2, 72, 256, 2), (1, 20, 64, 1),
-    # split-k: the sum of squares adds up over the k chunks
-    (1, 2048, 11264, 1), (2, 1024, 5120, 4)])
+    # wide kernel: the sum of squares adds up over the waves; split-k: over
+    # the k chunks
+    (1, 2048, 11264, 1), (2, 2048, 5120, 1), (2, 1024, 5120, 4)])
 def test_gemv_rmsnorm_prologue(device, fmt, out_width, in_width, rows):
     print(f"[gpu] gemv+norm fmt={fmt} O={out_width} I={in_width} rows={rows}", flush=True)
     q, s = make_weights(fmt, out_width, in_width, seed=5 + out_width)
@@ -82,7 +88,8 @@ def test_gemv_rmsnorm_prologue(device, fmt, out_width, in_width, rows):
 
 
 @pytest.mark.parametrize("fmt,out_width,in_width,rows", [
-    (1, 2048, 2048, 1), (1, 2048, 11264, 2), (2, 2048, 1408, 1), (1, 256, 64, 3)])
+    (1, 2048, 2048, 1), (1, 2048, 11264, 2), (2, 2048, 1408, 1), (1, 256, 64, 3),
+    (1, 2048, 11264, 1)])
 def test_gemv_residual_epilogue(device, fmt, out_width, in_width, rows):
     q, s = make_weights(fmt, out_width, in_width, seed=17)
     x = O.fill_normal(rows * in_width, 8).reshape(rows, in_width)
@@ -186,7 +193,9 @@ def test_fm_backend_reference_kernel_gate(device):
 def test_splitk_repeat_deterministic(device, fmt, rows):
     """The split-k kernel's arrival counters reset themselves: back-to-back
     launches (with a different shape in between) return the same bits, the
-    splits added in a fixed order whatever order the workgroups finish in."""
+    splits added in a fixed order whatever order the workgroups finish in.
+    (At one row 2048 x 11264 takes the wide kernel, whose sums stay inside
+    a workgroup, and 1000 x 6144 the split-k kernel.)"""
     q, s = make_weights(fmt, 2048, 11264, seed=123)
     x = O.fill_normal(rows * 11264, 77).reshape(rows, 11264)
     dw, dx, ds = DeviceBuffer.from_array(q), DeviceBuffer.from_array(x), DeviceBuffer.from_array(s)
@@ -210,7 +219,8 @@ def test_splitk_repeat_deterministic(device, fmt, rows):
     (1, 2048, 2048, 1, False),   # LDS-DMA kernel (q8, one row): o_proj
     (2, 11264, 2048, 1, False),  # register-direct kernel (q4)
     (1, 3072, 2048, 2, False),   # register-direct kernel (q8, two rows)
-    (1, 2048, 11264, 1, False),  # split-k kernel
+    (1, 2048, 11264, 1, False),  # wide kernel
+    (1, 1000, 6144, 1, False),   # split-k kernel
     (2, 2048, 11264, 4, False),
     (1, 3072, 2048, 2, True),    # RMSNorm: the normalised row is NaN
 ])
