@@ -14,10 +14,12 @@ namespace mlh {
 // per session, on first use).
 struct SampleWork {
     int vocab = 0;
-    int blocks = 0;      // workgroups of the element-wise passes
-    int index_bits = 0;  // sort key = ((~bits(p) & 0x3fffffff) << index_bits) | token
+    int blocks = 0;  // workgroups of the element-wise passes
     float *probs = nullptr;
-    uint64_t *keys = nullptr, *sorted = nullptr;
+    // sort keys ~bits(p) & 0x3fffffff with their tokens, before and after the
+    // (stable) sort
+    uint32_t *keys = nullptr, *sorted = nullptr;
+    int *tokens = nullptr, *sorted_tokens = nullptr;
     double *scan = nullptr;
     float *part_v = nullptr;
     int *part_i = nullptr;

@@ -15,13 +15,14 @@
 //   prob_kernel   every workgroup folds the partials (the same total order), p in
 //                 fp32 from an exp in double rounded once, per-workgroup double sums
 //   key_kernel    every workgroup folds the sums in the same order, p /= (float)
-//                 total, sort key (~bits(p) << index_bits) | token over the 30 low
-//                 bits of p's pattern (0 <= p <= 1 keeps the top two at 0):
-//                 ascending keys
-//                 are descending p with equal p in token order, which is what the
-//                 reference's qsort yields (glibc 2.35 sorts arrays of this size
-//                 with a stable merge sort)
-//   rocPRIM radix sort of the keys and inclusive scan (double) of the sorted p
+//                 total, sort key ~bits(p) over the 30 low bits of p's pattern
+//                 (0 <= p <= 1 keeps the top two at 0): ascending keys are
+//                 descending p
+//   rocPRIM radix sort of the (key, token) pairs over the 30 key bits: the
+//                 sort is stable, so equal p stay in token order, which is
+//                 what the reference's qsort yields (glibc 2.35 sorts arrays
+//                 of this size with a stable merge sort); then an inclusive
+//                 scan (double) of the sorted p
 //   count_kernel  the first prefix sum >= top_p ends the nucleus (atomic min)
 //   pick_kernel   the first prefix sum >= u * kept inside the nucleus
 //   finish_kernel the token
@@ -167,15 +168,15 @@ __global__ __launch_bounds__(kThreads) void prob_kernel(const float *logits, int
 }
 
 __global__ __launch_bounds__(kThreads) void key_kernel(const float *probs, int V, const double *part_sum,
-                                                       int n, int index_bits, uint64_t *keys) {
+                                                       int n, uint32_t *keys, int *tokens) {
     const float total = (float)fold_sum(part_sum, n);
     const int base = blockIdx.x * kPerBlock + threadIdx.x * kPerThread;
 #pragma unroll
     for (int k = 0; k < kPerThread; ++k) {
         if (base + k < V) {
             const float p = probs[base + k] / total;
-            const uint64_t rank = (uint64_t)(~__float_as_uint(p) & kRankMask);
-            keys[base + k] = (rank << index_bits) | (uint64_t)(base + k);
+            keys[base + k] = ~__float_as_uint(p) & kRankMask;
+            tokens[base + k] = base + k;
         }
     }
 }
@@ -206,29 +207,24 @@ __global__ __launch_bounds__(kThreads) void search_kernel(const double *scan, in
     }
 }
 
-__global__ void finish_kernel(const uint64_t *sorted, int index_bits, int *ctl) {
-    if (threadIdx.x == 0) {
-        const int idx = min(ctl[1], ctl[0]);
-        ctl[3] = (int)(sorted[idx] & ((1ull << index_bits) - 1ull));
-    }
+__global__ void finish_kernel(const int *sorted_tokens, int *ctl) {
+    if (threadIdx.x == 0) ctl[3] = sorted_tokens[min(ctl[1], ctl[0])];
 }
 
 // p of a sort key, widened to double for the scan
 struct KeyProb {
-    int index_bits;
-    __host__ __device__ double operator()(uint64_t key) const {
-        const uint32_t bits = ~(uint32_t)(key >> index_bits) & kRankMask;
-        return (double)__builtin_bit_cast(float, bits);
+    __host__ __device__ double operator()(uint32_t key) const {
+        return (double)__builtin_bit_cast(float, ~key & kRankMask);
     }
 };
 
-using ProbIter = rocprim::transform_iterator<const uint64_t *, KeyProb, double>;
+using ProbIter = rocprim::transform_iterator<const uint32_t *, KeyProb, double>;
 
 }  // namespace
 
 void sample_free(SampleWork *w) {
-    void *bufs[] = {w->probs, w->keys, w->sorted, w->scan, w->part_v,
-                    w->part_i, w->part_sum, w->ctl, w->temp};
+    void *bufs[] = {w->probs, w->keys, w->sorted, w->tokens, w->sorted_tokens, w->scan,
+                    w->part_v, w->part_i, w->part_sum, w->ctl, w->temp};
     for (void *p : bufs)
         if (p) (void)hipFree(p);
     *w = SampleWork();
@@ -239,24 +235,23 @@ int sample_alloc(SampleWork *w, int vocab) {
     sample_free(w);
     w->vocab = vocab;
     w->blocks = (vocab + kPerBlock - 1) / kPerBlock;
-    int bits = 1;
-    while ((1ll << bits) < (long long)vocab) ++bits;
-    w->index_bits = bits;
     const size_t V = (size_t)vocab, nb = (size_t)w->blocks;
     size_t sort_bytes = 0, scan_bytes = 0;
     bool ok =
         hipMalloc((void **)&w->probs, V * sizeof(float)) == hipSuccess &&
-        hipMalloc((void **)&w->keys, V * sizeof(uint64_t)) == hipSuccess &&
-        hipMalloc((void **)&w->sorted, V * sizeof(uint64_t)) == hipSuccess &&
+        hipMalloc((void **)&w->keys, V * sizeof(uint32_t)) == hipSuccess &&
+        hipMalloc((void **)&w->sorted, V * sizeof(uint32_t)) == hipSuccess &&
+        hipMalloc((void **)&w->tokens, V * sizeof(int)) == hipSuccess &&
+        hipMalloc((void **)&w->sorted_tokens, V * sizeof(int)) == hipSuccess &&
         hipMalloc((void **)&w->scan, V * sizeof(double)) == hipSuccess &&
         hipMalloc((void **)&w->part_v, nb * sizeof(float)) == hipSuccess &&
         hipMalloc((void **)&w->part_i, nb * sizeof(int)) == hipSuccess &&
         hipMalloc((void **)&w->part_sum, nb * sizeof(double)) == hipSuccess &&
         hipMalloc((void **)&w->ctl, 4 * sizeof(int)) == hipSuccess &&
-        rocprim::radix_sort_keys(nullptr, sort_bytes, w->keys, w->sorted, (unsigned)V, 0,
-                                 kRankBits + bits) == hipSuccess &&
-        rocprim::inclusive_scan(nullptr, scan_bytes, ProbIter(w->sorted, KeyProb{bits}), w->scan,
-                                V, rocprim::plus<double>()) == hipSuccess;
+        rocprim::radix_sort_pairs(nullptr, sort_bytes, w->keys, w->sorted, w->tokens,
+                                  w->sorted_tokens, (unsigned)V, 0, kRankBits) == hipSuccess &&
+        rocprim::inclusive_scan(nullptr, scan_bytes, ProbIter(w->sorted, KeyProb{}), w->scan, V,
+                                rocprim::plus<double>()) == hipSuccess;
     if (ok) {
         w->temp_bytes = sort_bytes > scan_bytes ? sort_bytes : scan_bytes;
         ok = hipMalloc(&w->temp, w->temp_bytes ? w->temp_bytes : 16) == hipSuccess;
@@ -282,21 +277,20 @@ int sample_enqueue(SampleWork *w, const float *logits, float temperature, float 
     hipLaunchKernelGGL(prob_kernel, dim3(nb), dim3(kThreads), 0, stream, logits, V, temperature,
                        w->part_v, w->part_i, nb, w->probs, w->part_sum, w->ctl);
     hipLaunchKernelGGL(key_kernel, dim3(nb), dim3(kThreads), 0, stream, w->probs, V, w->part_sum,
-                       nb, w->index_bits, w->keys);
+                       nb, w->keys, w->tokens);
     size_t bytes = w->temp_bytes;
-    if (rocprim::radix_sort_keys(w->temp, bytes, w->keys, w->sorted, (unsigned)V, 0,
-                                 kRankBits + w->index_bits, stream) != hipSuccess)
+    if (rocprim::radix_sort_pairs(w->temp, bytes, w->keys, w->sorted, w->tokens, w->sorted_tokens,
+                                  (unsigned)V, 0, kRankBits, stream) != hipSuccess)
         return -2;
     bytes = w->temp_bytes;
-    if (rocprim::inclusive_scan(w->temp, bytes, ProbIter(w->sorted, KeyProb{w->index_bits}),
-                                w->scan, (size_t)V, rocprim::plus<double>(), stream) != hipSuccess)
+    if (rocprim::inclusive_scan(w->temp, bytes, ProbIter(w->sorted, KeyProb{}), w->scan,
+                                (size_t)V, rocprim::plus<double>(), stream) != hipSuccess)
         return -2;
     hipLaunchKernelGGL(search_kernel<false>, dim3(nb), dim3(kThreads), 0, stream, w->scan, V,
                        (double)top_p, u, w->ctl);
     hipLaunchKernelGGL(search_kernel<true>, dim3(nb), dim3(kThreads), 0, stream, w->scan, V,
                        (double)top_p, u, w->ctl);
-    hipLaunchKernelGGL(finish_kernel, dim3(1), dim3(64), 0, stream, w->sorted, w->index_bits,
-                       w->ctl);
+    hipLaunchKernelGGL(finish_kernel, dim3(1), dim3(64), 0, stream, w->sorted_tokens, w->ctl);
     return hipGetLastError() == hipSuccess ? 0 : -2;
 }
 
