@@ -41,6 +41,10 @@ struct MlaParams {
     const float *inv_freq = nullptr;    // [rope / 2] theta^(-2p/rope), host-computed
     MatrixRef kv_b;                     // [heads * (nope + vdim), latent]
     float *latent_cache = nullptr;      // this layer: [context, latent]
+    // this layer: [context][2][latent] f16 bit patterns, the halves hi, lo of
+    // every latent_cache value as the attention products split them
+    // (split_f16), written with the cache; the prefill attention reads them
+    uint16_t *latent_split = nullptr;
     float *rope_cache = nullptr;        // this layer: [context, rope]
     float *query_rope = nullptr;        // scratch [rows, heads, rope]
     float *query_absorbed = nullptr;    // scratch [rows, heads, latent]
@@ -65,5 +69,11 @@ struct MlaParams {
 // attention, merge + value projection (three launches per group of
 // kMlaDecodeRows rows).  o_proj is a plain GEMV on `context`.
 int mla_attention_core(const MlaParams &p, hipStream_t stream);
+
+// The f16 halves of `rows` rows of a latent cache (latent values each) into
+// its split copy, for caches filled by other means than the attention's own
+// cache append.
+int mla_split_cache(const float *latent, uint16_t *split, long rows, int width,
+                    hipStream_t stream);
 
 }  // namespace mlh

@@ -48,6 +48,14 @@ __device__ __forceinline__ bool outside_f16(float v) {
     const float a = fabsf(v);
     return a >= kSplitF16Max && a < INFINITY;
 }
+// The f16 halves of one cache value as split_f16 (below) makes them: hi =
+// x with its low 13 mantissa bits cleared, lo = f16(x - hi), as bits.
+__device__ __forceinline__ void split_f16_bits(float x, uint16_t &hi, uint16_t &lo) {
+    const float h = __uint_as_float(__float_as_uint(x) & 0xFFFFE000u);
+    hi = __builtin_bit_cast(uint16_t, (_Float16)h);
+    lo = __builtin_bit_cast(uint16_t, (_Float16)(x - h));
+}
+
 __device__ __forceinline__ void report_range(const MlaParams &p, bool bad) {
     if (bad && p.range_error && *p.range_error == 0) *p.range_error = p.range_code;
 }
@@ -151,6 +159,7 @@ __global__ __launch_bounds__(256) void mla_prep_kernel(MlaParams p, int chunks) 
         const float total = (part[0] + part[1]) + (part[2] + part[3]);
         const float inv = 1.0f / sqrtf(total / (float)p.latent + p.eps);
         float *lat = p.latent_cache + (long)pos * p.latent;
+        uint16_t *lsp = p.latent_split + (long)pos * 2 * p.latent;
         bool bad = false;
 #pragma unroll
         for (int u = 0; u < kMlaMaxLatent / 256; ++u) {
@@ -158,6 +167,10 @@ __global__ __launch_bounds__(256) void mla_prep_kernel(MlaParams p, int chunks) 
             if (i < p.latent) {
                 const float v = cv[u] * inv * p.kv_norm[i];
                 lat[i] = v;
+                uint16_t hi, lo;
+                split_f16_bits(v, hi, lo);
+                lsp[i] = hi;
+                lsp[p.latent + i] = lo;
                 bad |= outside_f16(v);
             }
         }
@@ -388,8 +401,8 @@ __global__ __launch_bounds__(512) void mla_attend_mfma_kernel(MlaParams p) {
         const long live = -(long)(tile < t_end);
         const int k0 = tile * TK, last = (keys - k0 < TK ? keys - k0 : TK) - 1;
 #pragma unroll
-        for (int u = 0; u < 4; ++u)
-            lr[u] = load_f4(p.latent_cache +
+        for (int u = 0; u < 4; ++u)  // the split row of a key: as many bytes as D floats
+            lr[u] = load_f4(reinterpret_cast<const float *>(p.latent_split) +
                             (((long)(k0 + (lkey[u] < last ? lkey[u] : last)) * D + lcol[u]) & live));
         rr = load_f4(p.rope_cache + (((long)(k0 + (rkey < last ? rkey : last)) * R + rcol) & live));
     };
@@ -434,25 +447,36 @@ __global__ __launch_bounds__(512) void mla_attend_mfma_kernel(MlaParams p) {
         // products each, two accumulator chains); a lane's 8 dims past KD
         // read row columns 0.. (finite) against a zero query slice
         {
+            // latent dims: the cached halves (hi at half d, lo at half D + d
+            // of the row); rope dims (d >= D, wave-uniform): fp32, split here
+            half8 kh[NS], kl[NS];
             f32x4 av[NS][2];
 #pragma unroll
             for (int j = 0; j < NS; ++j) {
                 const int d = 32 * (wave + 8 * j) + 8 * g;
-                const float *row = cur + m16 * kAttnRowStride + (d < KD ? d : 0);
-                av[j][0] = *reinterpret_cast<const f32x4 *>(row);
-                av[j][1] = *reinterpret_cast<const f32x4 *>(row + 4);
+                const float *row = cur + m16 * kAttnRowStride;
+                if (d < D) {
+                    const _Float16 *hr = reinterpret_cast<const _Float16 *>(row) + d;
+                    kh[j] = *reinterpret_cast<const half8 *>(hr);
+                    kl[j] = *reinterpret_cast<const half8 *>(hr + D);
+                } else {
+                    const float *rr = row + (d < KD ? d : D);
+                    av[j][0] = *reinterpret_cast<const f32x4 *>(rr);
+                    av[j][1] = *reinterpret_cast<const f32x4 *>(rr + 4);
+                }
             }
             __builtin_amdgcn_sched_barrier(0);  // all row reads issued before the products
             f32x4v a0 = f32x4v{0.f, 0.f, 0.f, 0.f}, a1 = a0;
 #pragma unroll
             for (int j = 0; j < NS; ++j) {
-                const float x[8] = {av[j][0].x, av[j][0].y, av[j][0].z, av[j][0].w,
-                                    av[j][1].x, av[j][1].y, av[j][1].z, av[j][1].w};
-                half8 kh, kl;
-                split_f16<8>(x, kh, kl);
-                a0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, qh8[j], a0, 0, 0, 0);
-                a1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, ql8[j], a1, 0, 0, 0);
-                a0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(kl, qh8[j], a0, 0, 0, 0);
+                if (32 * (wave + 8 * j) + 8 * g >= D) {
+                    const float x[8] = {av[j][0].x, av[j][0].y, av[j][0].z, av[j][0].w,
+                                        av[j][1].x, av[j][1].y, av[j][1].z, av[j][1].w};
+                    split_f16<8>(x, kh[j], kl[j]);
+                }
+                a0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh[j], qh8[j], a0, 0, 0, 0);
+                a1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh[j], ql8[j], a1, 0, 0, 0);
+                a0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(kl[j], qh8[j], a0, 0, 0, 0);
             }
 #pragma unroll
             for (int i = 0; i < 4; ++i) sp[(wave * TK + 4 * g + i) * H + m16] = a0[i] + a1[i];
@@ -483,13 +507,19 @@ __global__ __launch_bounds__(512) void mla_attend_mfma_kernel(MlaParams p) {
         {
             const f32x4 f = *reinterpret_cast<const f32x4 *>(sscale + 4 * g);
             const f32x4 pv = *reinterpret_cast<const f32x4 *>(p_s + m16 * kAttnPStride + 4 * g);
-            float bv[NT][4];
+            // keys 4 g .. 4 g + 3 of latent dim col: the cached halves
+            constexpr int RS = 2 * kAttnRowStride;  // halves per LDS row
+            half4 bh[NT], bl[NT];
 #pragma unroll
             for (int i = 0; i < NT; ++i) {
                 const int dt = wave + 8 * i;
                 const int col = (dt < D / 16 ? dt : 0) * 16 + m16;
+                const _Float16 *hb = reinterpret_cast<const _Float16 *>(cur) + (4 * g) * RS + col;
 #pragma unroll
-                for (int j = 0; j < 4; ++j) bv[i][j] = cur[(4 * g + j) * kAttnRowStride + col];
+                for (int j = 0; j < 4; ++j) {
+                    bh[i][j] = hb[j * RS];
+                    bl[i][j] = hb[j * RS + D];
+                }
             }
 #pragma unroll
             for (int i = 0; i < NT; ++i) {
@@ -505,11 +535,9 @@ __global__ __launch_bounds__(512) void mla_attend_mfma_kernel(MlaParams p) {
             split_f16<4>(pj, ph, pl);
 #pragma unroll
             for (int i = 0; i < NT; ++i) {
-                half4 bh, bl;
-                split_f16<4>(bv[i], bh, bl);
-                cacc[i] = __builtin_amdgcn_mfma_f32_16x16x16f16(ph, bh, cacc[i], 0, 0, 0);
-                cacc[i] = __builtin_amdgcn_mfma_f32_16x16x16f16(ph, bl, cacc[i], 0, 0, 0);
-                cacc[i] = __builtin_amdgcn_mfma_f32_16x16x16f16(pl, bh, cacc[i], 0, 0, 0);
+                cacc[i] = __builtin_amdgcn_mfma_f32_16x16x16f16(ph, bh[i], cacc[i], 0, 0, 0);
+                cacc[i] = __builtin_amdgcn_mfma_f32_16x16x16f16(ph, bl[i], cacc[i], 0, 0, 0);
+                cacc[i] = __builtin_amdgcn_mfma_f32_16x16x16f16(pl, bh[i], cacc[i], 0, 0, 0);
             }
         }
     };
@@ -771,7 +799,8 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void mla_prefill_attend_kernel(Mla
         float *kb = kbuf + buf * KS * kPfRowStride;
         for (int row = wave; row < KS; row += NW) {
             const int k = tile * KS + row < keys ? tile * KS + row : keys - 1;
-            const float *lsrc = p.latent_cache + (long)k * D;
+            // the key's f16 halves (2 D halves: as many bytes as D floats)
+            const float *lsrc = reinterpret_cast<const float *>(p.latent_split + (long)k * 2 * D);
             __attribute__((address_space(3))) float *dst =
                 (__attribute__((address_space(3))) float *)(kb + row * kPfRowStride);
             for (int c0 = 0; c0 < D; c0 += 256)
@@ -811,18 +840,18 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void mla_prefill_attend_kernel(Mla
             for (int j = 0; j < NJ; ++j) {
                 const int d0 = 32 * (wave + NW * j);
                 if (d0 < KD) {
-                    f32x4 a0, a1;
-                    if (d0 < D) {
-                        const float *row = kb + m16 * kPfRowStride + d0 + 8 * g;
-                        a0 = *reinterpret_cast<const f32x4 *>(row);
-                        a1 = *reinterpret_cast<const f32x4 *>(row + 4);
-                    } else {
-                        a0 = rope_cur[0];
-                        a1 = rope_cur[1];
-                    }
-                    const float x[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
                     half8 kh, kl;
-                    split_f16<8>(x, kh, kl);
+                    if (d0 < D) {  // the cached halves: hi at dims .., lo at D + dims
+                        const _Float16 *row =
+                            reinterpret_cast<const _Float16 *>(kb + m16 * kPfRowStride) + d0 + 8 * g;
+                        kh = *reinterpret_cast<const half8 *>(row);
+                        kl = *reinterpret_cast<const half8 *>(row + D);
+                    } else {
+                        const float x[8] = {rope_cur[0].x, rope_cur[0].y, rope_cur[0].z,
+                                            rope_cur[0].w, rope_cur[1].x, rope_cur[1].y,
+                                            rope_cur[1].z, rope_cur[1].w};
+                        split_f16<8>(x, kh, kl);
+                    }
 #pragma unroll
                     for (int b = 0; b < RB; ++b) {
                         sacc[b][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, qh8[b][j], sacc[b][0], 0, 0, 0);
@@ -888,11 +917,12 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void mla_prefill_attend_kernel(Mla
         for (int q = 0; q < NQ; ++q) {
             const int dt = wave + NW * q;
             if (dt < D / 16) {
-                const float *lb = kb + (4 * g) * kPfRowStride + dt * 16 + m16;
-                const float bx[4] = {lb[0], lb[kPfRowStride], lb[2 * kPfRowStride],
-                                     lb[3 * kPfRowStride]};
-                half4 bh, bl;
-                split_f16<4>(bx, bh, bl);
+                // keys 4 g .. 4 g + 3 of latent dim dt * 16 + m16, cached halves
+                constexpr int RS = 2 * kPfRowStride;  // halves per LDS row
+                const _Float16 *lb =
+                    reinterpret_cast<const _Float16 *>(kb + (4 * g) * kPfRowStride) + dt * 16 + m16;
+                const half4 bh = {lb[0], lb[RS], lb[2 * RS], lb[3 * RS]};
+                const half4 bl = {lb[D], lb[RS + D], lb[2 * RS + D], lb[3 * RS + D]};
 #pragma unroll
                 for (int b = 0; b < RB; ++b) {
                     acc[b][q] = __builtin_amdgcn_mfma_f32_16x16x16f16(ph[b], bh, acc[b][q], 0, 0, 0);
@@ -1108,6 +1138,31 @@ __global__ __launch_bounds__(512) void mla_merge_value_kernel(MlaParams p) {
     if (t == 0) __hip_atomic_store(count, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+
+__global__ __launch_bounds__(256) void split_cache_kernel(const float *latent, uint16_t *split,
+                                                          long rows, int width) {
+    const long n = rows * width;
+    for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (long)gridDim.x * blockDim.x) {
+        const long r = i / width;
+        const int c = (int)(i - r * width);
+        uint16_t hi, lo;
+        split_f16_bits(latent[i], hi, lo);
+        split[r * 2 * width + c] = hi;
+        split[r * 2 * width + width + c] = lo;
+    }
+}
+
+int mla_split_cache(const float *latent, uint16_t *split, long rows, int width,
+                    hipStream_t stream) {
+    if (rows < 0 || width <= 0 || (rows && (!latent || !split))) return kErrArgs;
+    if (rows == 0) return kOk;
+    const long n = rows * width;
+    const int blocks = (int)std::min<long>((n + 255) / 256, 4096);
+    hipLaunchKernelGGL(split_cache_kernel, dim3(blocks), dim3(256), 0, stream, latent, split,
+                       rows, width);
+    return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
+}
 
 int mla_attention_core(const MlaParams &p, hipStream_t stream) {
     if (p.heads <= 0 || p.heads > kMlaMaxHeads || p.latent <= 0 || p.latent % 64 ||

@@ -116,6 +116,8 @@ struct MoonlightSession {
     float *value_part = nullptr;  // decode MLA value shares
     int *merge_count = nullptr;                             // zeroed at creation
     float *latent_kv = nullptr, *rope_kv = nullptr, *logits = nullptr;
+    // the latent cache's f16 halves (hi, lo) per value: [L][ctx][2][latent]
+    uint16_t *latent_split = nullptr;
     float *router_logits = nullptr, *route_weights = nullptr;
     // router logit partials of one token row written by o_proj for the MoE
     // layer after it ([experts + 1][hidden / 8], GemvParams router_parts)
@@ -1054,6 +1056,8 @@ int attention(MoonlightSession *s, int layer, const float *x, int rows, int posi
     p.kv_b.w = lp.kv_b.w;
     p.kv_b.s = lp.kv_b.s;
     p.latent_cache = s->latent_kv + (size_t)layer * s->options.context_size * c.kv_lora_rank;
+    p.latent_split =
+        s->latent_split + (size_t)layer * s->options.context_size * 2 * c.kv_lora_rank;
     p.rope_cache = s->rope_kv + (size_t)layer * s->options.context_size * c.qk_rope_dim;
     p.query_rope = s->query_rope;
     p.query_absorbed = s->query_absorbed;
@@ -1583,6 +1587,7 @@ extern "C" int moonlight_session_create(MoonlightSession **out, MoonlightModel *
         session_alloc(s, &s->h, mb * H, error, error_size) &&
         session_alloc(s, &s->tmp, mb * H, error, error_size) &&
         session_alloc(s, &s->latent_kv, lat_elems, error, error_size) &&
+        session_alloc(s, &s->latent_split, 2 * lat_elems, error, error_size) &&
         session_alloc(s, &s->rope_kv, rope_elems, error, error_size) &&
         session_alloc(s, &s->step_dev, mb + 1, error, error_size) &&
         (s->pos_dev = s->step_dev, s->ids = s->step_dev + 1, true) &&
@@ -2022,6 +2027,9 @@ extern "C" int moonlight_session_fill_kv(MoonlightSession *s, int layer, int len
         if (length > 0 &&
             (fill_normal(s->latent_kv + (size_t)l * ctx * c.kv_lora_rank,
                          (int64_t)length * c.kv_lora_rank, sd, 0.0f, 1.0f, 0, st) != kOk ||
+             mla_split_cache(s->latent_kv + (size_t)l * ctx * c.kv_lora_rank,
+                             s->latent_split + (size_t)l * ctx * 2 * c.kv_lora_rank, length,
+                             c.kv_lora_rank, st) != kOk ||
              fill_normal(s->rope_kv + (size_t)l * ctx * c.qk_rope_dim,
                          (int64_t)length * c.qk_rope_dim, sd + 1, 0.0f, 1.0f, 0, st) != kOk))
             return 0;
