@@ -4,6 +4,7 @@
 #include "mlh_host.h"
 #include "../../include/moonlight_kernels.h"
 #include "moe.h"
+#include "sample.h"
 
 #include <mutex>
 #include <vector>
@@ -362,6 +363,33 @@ int mlk_route_topk(const float *logits, const float *bias, int rows, int experts
     const int sync = check_hip(hipStreamSynchronize(st), "mlk_route_topk");
     (void)hipFree(tab);
     return status != kOk ? status : sync;
+}
+
+int mlk_sample(const float *logits, int vocab, float temperature, float top_p, double u,
+               int *token) {
+    hipStream_t st = lib_stream();
+    if (!st) return kErrDevice;
+    if (!logits || !token || vocab <= 0 || !(u >= 0.0 && u < 1.0)) return finish(kErrArgs, "mlk_sample");
+    SampleWork w;
+    if (sample_alloc(&w, vocab) != 0) {
+        set_last_error("mlk_sample: device allocation failed");
+        return kErrDevice;
+    }
+    int out[2] = {0, -1};
+    int status = sample_enqueue(&w, logits, temperature, top_p, u, st) == 0 ? kOk : kErrLaunch;
+    if (status == kOk)
+        status = check_hip(hipMemcpyAsync(out, w.ctl + 2, sizeof(out), hipMemcpyDeviceToHost, st),
+                           "mlk_sample");
+    const int sync = check_hip(hipStreamSynchronize(st), "mlk_sample");
+    sample_free(&w);
+    if (status == kOk) status = sync;
+    if (status != kOk) return finish(status, "mlk_sample");
+    if (out[0] && temperature > 0.0f) {
+        set_last_error("mlk_sample: logits are not finite");
+        return kErrArgs;
+    }
+    *token = out[1];
+    return kOk;
 }
 
 int mlk_quantize(int bits, const float *w, int rows, int cols, uint8_t *q, float *s) {

@@ -16,19 +16,15 @@ struct SampleWork {
     int vocab = 0;
     int blocks = 0;  // workgroups of the element-wise passes
     float *probs = nullptr;
-    // sort keys ~bits(p) & 0x3fffffff with their tokens, before and after the
-    // (stable) sort
-    uint32_t *keys = nullptr, *sorted = nullptr;
-    int *tokens = nullptr, *sorted_tokens = nullptr;
-    double *scan = nullptr;
+    // rank keys ~bits(p) & 0x3fffffff: ascending key is descending p
+    uint32_t *keys = nullptr;
     float *part_v = nullptr;
     int *part_i = nullptr;
     double *part_sum = nullptr;
-    // ctl[0] nucleus end index, ctl[1] drawn index, ctl[2] non-finite flag,
-    // ctl[3] chosen token
+    // ctl[2] non-finite flag, ctl[3] chosen token (ctl[0..1] unused)
     int *ctl = nullptr;
-    void *temp = nullptr;
-    size_t temp_bytes = 0;
+    // selection scratch: histograms, candidate lists, round thresholds
+    void *select = nullptr;
 };
 
 int sample_alloc(SampleWork *w, int vocab);

@@ -50,6 +50,8 @@ SIGNATURES = {
                                  _c.c_int, _c.c_int, _c.POINTER(_c.c_double)]),
     "mlk_route_topk": (_c.c_int, [_vp, _vp, _c.c_int, _c.c_int, _c.c_int, _c.c_int,
                                   _c.c_float, _vp, _vp]),
+    "mlk_sample": (_c.c_int, [_vp, _c.c_int, _c.c_float, _c.c_float, _c.c_double,
+                              _c.POINTER(_c.c_int)]),
     "mlk_quantize": (_c.c_int, [_c.c_int, _vp, _c.c_int, _c.c_int, _vp, _vp]),
     "mlk_fill_normal": (_c.c_int, [_vp, _c.c_int64, _c.c_uint64, _c.c_float, _c.c_float,
                                    _c.c_int]),
@@ -214,6 +216,14 @@ def time_read(src_list, nbytes, blocks, scratch, warmup, iters):
 def route_topk(logits, bias, rows, experts, top_k, normalize, routed_scale, ids, weights):
     check(load().mlk_route_topk(_ptr(logits), _ptr(bias), rows, experts, top_k, normalize,
                                 routed_scale, _ptr(ids), _ptr(weights)), "mlk_route_topk")
+
+
+def sample(logits, vocab, temperature, top_p, u):
+    """The device sampler's token for `vocab` device logits (mlk_sample)."""
+    tok = _c.c_int(-1)
+    check(load().mlk_sample(_ptr(logits), vocab, temperature, top_p, u, _c.byref(tok)),
+          "mlk_sample")
+    return tok.value
 
 
 def quantize(bits, w, rows, cols, q, s):

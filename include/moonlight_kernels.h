@@ -17,6 +17,8 @@
  *   mlk_route_topk     moonlight_route_sigmoid_topk (moonlight_kernels.metal:469-512)
  *                      = moe_route_select + moe_route_finalize (moe_route.h:47-99)
  *   mlk_quantize       quant_int8 / quant_int4 (tools/convert_moonlight.py:46-66)
+ *   mlk_sample         choose_token (moonlight_chat.c:96-131), the caller-side
+ *                      sampler, on device logits
  */
 #ifndef MOONLIGHT_KERNELS_H
 #define MOONLIGHT_KERNELS_H
@@ -91,6 +93,16 @@ int mlk_time_read(void *const *src, int n_buffers, size_t bytes, int blocks,
 int mlk_route_topk(const float *logits, const float *bias, int rows, int experts,
                    int top_k, int normalize, float routed_scale, int *ids,
                    float *weights);
+
+/* ---- token choice ---------------------------------------------------------
+ * The token choose_token (moonlight_chat.c:96-131) picks from `vocab` device
+ * logits with the caller's draw u in [0, 1) (random_unit,
+ * moonlight_chat.c:89-94): the first index of the maximum when temperature
+ * <= 0, else the top-p draw.  The device sampler that
+ * moonlight_session_sample runs; writes *token (host memory) and waits.
+ * Non-finite logits under a top-p draw return -1 ("logits are not finite"). */
+int mlk_sample(const float *logits, int vocab, float temperature, float top_p,
+               double u, int *token);
 
 /* ---- packing / synthetic weights ---------------------------------------- */
 int mlk_quantize(int bits, const float *w, int rows, int cols, uint8_t *q,
