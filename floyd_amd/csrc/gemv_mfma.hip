@@ -253,8 +253,10 @@ __global__ __launch_bounds__(256) void gemv_mfma_kernel(MfmaGemvArgs a) {
     unsigned char *wl = xl + 4 * B * xrow;              // [nr][kqb], 16-byte chunks swizzled
 
     // ---- 1. x of this wave's quarter (and norm_w): 8 elements per lane and
-    // pass, all loads unconditional (norm_w absent: x itself, unused), issued
-    // before the weight DMA so that the wait for them leaves the DMA in flight
+    // pass, all loads unconditional (norm_w absent: x itself, unused; a
+    // conditional untracked load lets the register allocator copy its
+    // destination before the wait), issued before the weight DMA so that the
+    // wait for them leaves the DMA in flight
     constexpr int kMaxPass = Sh::kPass;
     const bool has_norm = p.norm_w != nullptr;
     const float *nw = has_norm ? p.norm_w : p.x;
@@ -546,9 +548,9 @@ __device__ __forceinline__ void direct_wave(const GemvParams &p, int row0, int k
     // the epilogue's operands: in-order completion lets the split start
     // while the weights are still in flight
     const bool has_norm = p.norm_w != nullptr;
-    const float *nw = has_norm ? p.norm_w : p.x;
+    const float *nw = p.norm_w;  // loaded only with a norm
     f32x4 xv[kPass][B][2];
-    f32x4 nv[kPass][2];
+    f32x4 nv[kPass][2] = {};
 #pragma unroll
     for (int j = 0; j < kPass; ++j) {
         const int e = j * 512 + lane * 8;
@@ -559,8 +561,10 @@ __device__ __forceinline__ void direct_wave(const GemvParams &p, int row0, int k
             xv[j][b][0] = load_f4(xb);
             xv[j][b][1] = load_f4(xb + 4);
         }
-        nv[j][0] = load_f4(nw + k0 + ec);
-        nv[j][1] = load_f4(nw + k0 + ec + 4);
+        if (has_norm) {
+            nv[j][0] = load_f4(nw + k0 + ec);
+            nv[j][1] = load_f4(nw + k0 + ec + 4);
+        }
     }
     const int wr_row = row0 + n < p.O ? row0 + n : p.O - 1;
     const long w_off = (long)wr_row * row_bytes + (FMT == kQ8 ? k0 : k0 / 2) + 16 * g;
@@ -864,15 +868,17 @@ __global__ __launch_bounds__(1024) void gemv_mfma_wide_kernel(GemvParams p) {
     // epilogue's operands: in-order completion lets the split start while
     // the weights are in flight
     const bool has_norm = p.norm_w != nullptr;
-    const float *nw = has_norm ? p.norm_w : p.x;
-    f32x4 xv[2][2], nv[2][2];
+    const float *nw = p.norm_w;  // loaded only with a norm
+    f32x4 xv[2][2], nv[2][2] = {};
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
         const int e = k0 + j * kWideSlice + lane * 8;
         xv[j][0] = load_f4(p.x + e);
         xv[j][1] = load_f4(p.x + e + 4);
-        nv[j][0] = load_f4(nw + e);
-        nv[j][1] = load_f4(nw + e + 4);
+        if (has_norm) {
+            nv[j][0] = load_f4(nw + e);
+            nv[j][1] = load_f4(nw + e + 4);
+        }
     }
     const int kw = k0 + h * kWideSlice;
     const long w_off = (long)wrow * row_bytes + (FMT == kQ8 ? kw : kw / 2) + 16 * g;
