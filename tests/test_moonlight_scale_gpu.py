@@ -4,6 +4,13 @@ oracle reads the very same packed weights back from the device.
 
   test_moe_decode         config 2: one MoE layer, T = 1, 2, 4, 8, 64 token
                           rows (one-row path, grouped GEMV, grouped GEMM)
+  test_moe_decode_q4      the same layer on a model packed at 4 bits
+                          (--ebits 4 --dbits 4): the q4 forms of the same
+                          decode kernels
+  test_decode_step_q4     two 27-layer decode steps of that model at ctx 4096
+                          (eager, then captured and replayed): q4 GEMVs for
+                          the attention and dense projections, q4 kv_b in
+                          the MLA launches, q4 experts
   test_mla_decode         config 4 attention: one layer at position 4096 and
                           16383 (128 / 512 key splits) over a latent cache
                           pre-filled ~N(0, 1)
@@ -67,9 +74,28 @@ def moe_layer_names(layer):
     return names
 
 
+@pytest.fixture(scope="module")
+def moon_q4(device):
+    print("[gpu] building the synthetic Moonlight model with q4 experts in HBM", flush=True)
+    model = S.Model.synthetic(expert_bits=4, dense_bits=4)
+    O.lib().orc_set_threads(16)
+    yield model
+    model.close()
+
+
 @pytest.mark.parametrize("rows", [1, 2, 4, 8, 64])
 def test_moe_decode(moon, rows):
     print(f"[gpu] moonlight MoE layer rows={rows}", flush=True)
+    check_moe_decode(moon, rows)
+
+
+@pytest.mark.parametrize("rows", [1, 2, 4, 8, 64])
+def test_moe_decode_q4(moon_q4, rows):
+    print(f"[gpu] moonlight MoE layer, q4 experts, rows={rows}", flush=True)
+    check_moe_decode(moon_q4, rows)
+
+
+def check_moe_decode(moon, rows):
     sess = S.Session(moon, 128, 64)
     x = O.fill_normal(rows * 2048, 40 + rows).reshape(rows, 2048)
     got = sess.test_moe(1, x)
@@ -238,6 +264,32 @@ def test_decode_step(moon, moon_oracle, kv):
                 compared += 1
     assert compared >= 12
     sess.close()
+
+
+def test_decode_step_q4(moon_q4):
+    kv = 4096
+    print(f"[gpu] moonlight q4 full decode steps at ctx {kv}", flush=True)
+    sess = S.Session(moon_q4, kv + 4, 1)
+    sess.fill_kv(kv, seed=77)
+    orc = oracle_with(moon_q4, all_names(moon_q4), kv + 4)
+    for l in range(27):
+        lat, rope = sess.test_copy_kv(l, kv)
+        assert O.lib().orc_model_set_kv(orc.handle, l, O.fptr(lat), O.fptr(rope), kv)
+    token = 4242
+    sess.trace_router(True)
+    for step in range(2):
+        logits = sess.decode(token)
+        trace, e_logits = oracle_step(orc, [token], kv + step)
+        err = rel_l2(logits, e_logits)
+        print(f"[gpu] q4 decode step {step} (graph {sess.decode_graph()}) logits rel-L2 "
+              f"{err:.3e}", flush=True)
+        assert err < 1e-3, step
+        assert int(np.argmax(logits)) == int(np.argmax(e_logits)), step
+        check_routes(sess, 1, trace, f"q4 step {step}")
+        token = int(np.argmax(e_logits))
+    assert sess.decode_graph()
+    sess.close()
+    orc.close()
 
 
 def test_prefill_append(moon, moon_oracle):
