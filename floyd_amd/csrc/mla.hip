@@ -691,6 +691,191 @@ __global__ __launch_bounds__(256) void mla_head_gemm_kernel(MlaParams p) {
     }
 }
 
+// The same products on the f16 matrix cores for q8 / q4 kv_b.  The stored
+// integers are exact in f16, so an fp32 activation x costs two products
+// instead of one fp32 MFMA at a sixteenth of the rate: hi = x with its low
+// 13 mantissa bits cleared (exact in f16) and lo' = f16((x - hi) 2^11) go
+// into two accumulators, combined as acc_hi + 2^-11 acc_lo (lo' scaled up
+// keeps lo out of f16's subnormal range, where it would lose its bits for
+// small x).  kv_b's per-row scale goes with the activation in the absorb
+// (its rows are the contraction index), divided by the head's largest scale
+// so that the activation stays near the magnitude of q (that scale multiplies
+// the result), and onto the sum in the value projection (its rows are the
+// outputs):
+//   ABSORB: qa[r][h][n] = smax sum_k (q_nope[r][h][k] s[h (nope + v) + k] / smax) w[h (nope + v) + k][n]
+//   value:  ctx[r][h][n] = s[h (nope + v) + nope + n] sum_k lc[r][h][k] w[h (nope + v) + nope + n][k]
+// Workgroup: 64 token rows x 64 outputs of one head (grid z); wave w: rows
+// 16 w .. + 15 against four 16-output tiles, KS steps of 32 k on
+// v_mfma_f32_16x16x32_f16 (lane (m16, g) supplies A[m16][8 g .. + 7] and
+// B[8 g .. + 7][m16]; D[4 g + i][m16] in register i).  A wave reads its own
+// activation rows from global memory; the value weights too (a lane's 8 k of
+// one output row are consecutive bytes).  The loops are unrolled with D
+// steps' loads in flight: the absorb (K = nope, a few steps) issues every
+// step at once and its weights (8 k of one output column lie in 8 rows) go
+// through LDS transposed, one barrier; the value projection (K = latent)
+// keeps D = 4 steps in flight.
+template <bool ABSORB, int FMT, int KS>
+__global__ __launch_bounds__(256) void mla_head_gemm_f16_kernel(MlaParams p) {
+    constexpr int BK = 32, K = KS * BK;
+    constexpr int D = ABSORB ? KS : (KS < 4 ? KS : 4);  // steps in flight
+    constexpr int WS = K + 8;                            // halves per transposed row
+    __shared__ __attribute__((aligned(16))) _Float16 wt[ABSORB ? 64 : 1][ABSORB ? WS : 8];
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int g = lane >> 4, m16 = lane & 15;
+    const int m0 = blockIdx.x * 64, n0 = blockIdx.y * 64, h = blockIdx.z;
+    const int N = ABSORB ? p.latent : p.vdim;
+    const long wrow0 = (long)h * (p.nope + p.vdim) + (ABSORB ? 0 : p.nope);
+    const long rbytes = FMT == kQ8 ? p.latent : p.latent / 2;  // bytes per kv_b row
+    // this lane's activation row (rows past the end load the last, unused)
+    const long r = m0 + 16 * wave + m16 < p.rows ? m0 + 16 * wave + m16 : p.rows - 1;
+    const float *xrow = ABSORB ? p.query + r * p.query_stride + (long)h * (p.nope + p.rope)
+                               : p.latent_context + (r * p.heads + h) * p.latent;
+    struct Step {
+        f32x4 x0, x1, s0, s1;
+        uint2 w[4];  // value: tile q's 8 k (q8: 8 bytes; q4: 4 bytes in .x)
+    };
+    Step st[KS];
+    auto load = [&](int j) {
+        const int k0 = j * BK + 8 * g;
+        st[j].x0 = load_f4(xrow + k0);
+        st[j].x1 = load_f4(xrow + k0 + 4);
+        if constexpr (ABSORB) {
+            st[j].s0 = load_f4(p.kv_b.s + wrow0 + k0);
+            st[j].s1 = load_f4(p.kv_b.s + wrow0 + k0 + 4);
+        } else {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int n = n0 + 16 * q + m16 < N ? n0 + 16 * q + m16 : N - 1;
+                const uint8_t *src = p.kv_b.w + (wrow0 + n) * rbytes;
+                if constexpr (FMT == kQ8)
+                    st[j].w[q] = *reinterpret_cast<const uint2 *>(src + k0);
+                else
+                    st[j].w[q] = uint2{*reinterpret_cast<const unsigned *>(src + k0 / 2), 0u};
+            }
+        }
+    };
+    // the 8 stored integers of a uint2 / 4-byte nibble run as f16
+    auto to_half8 = [](uint2 v) {
+        half8 o;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            if constexpr (FMT == kQ8)
+                o[i] = (_Float16)(int8_t)(((i < 4 ? v.x : v.y) >> (8 * (i & 3))) & 0xFF);
+            else
+                o[i] = (_Float16)((int)((v.x >> (4 * i)) & 15) - 8);
+        }
+        return o;
+    };
+#pragma unroll
+    for (int j = 0; j < D; ++j) load(j);
+    // absorb: the weight block [K k][64 n] into LDS transposed; thread t
+    // takes rows k = t / 8 + 32 u, columns n0 + 8 (t % 8) .. + 7
+    float smax = 1.0f, sinv = 1.0f;
+    if constexpr (ABSORB) {
+        const int sk = t >> 3, sn = 8 * (t & 7);
+        uint2 wv[KS];
+#pragma unroll
+        for (int u = 0; u < KS; ++u) {
+            const uint8_t *src = p.kv_b.w + (wrow0 + sk + 32 * u) * rbytes;
+            if constexpr (FMT == kQ8)
+                wv[u] = *reinterpret_cast<const uint2 *>(src + n0 + sn);
+            else
+                wv[u] = uint2{*reinterpret_cast<const unsigned *>(src + (n0 + sn) / 2), 0u};
+        }
+        // the head's largest absorb-row scale (every wave)
+        float m = 0.0f;
+        for (int k = lane; k < K; k += 64) m = fmaxf(m, fabsf(p.kv_b.s[wrow0 + k]));
+        m = wave_max(m);
+        smax = m;
+        sinv = m > 0.0f ? 1.0f / m : 0.0f;
+#pragma unroll
+        for (int u = 0; u < KS; ++u) {
+            const half8 v = to_half8(wv[u]);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) wt[sn + i][sk + 32 * u] = v[i];
+        }
+        __syncthreads();
+    }
+    f32x4v acc[4], accl[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) acc[q] = accl[q] = f32x4v{0.f, 0.f, 0.f, 0.f};
+    bool bad = false;
+#pragma unroll
+    for (int j = 0; j < KS; ++j) {
+        if (j + D < KS) load(j + D);
+        float x[8] = {st[j].x0.x, st[j].x0.y, st[j].x0.z, st[j].x0.w,
+                      st[j].x1.x, st[j].x1.y, st[j].x1.z, st[j].x1.w};
+        if constexpr (ABSORB) {
+            const float sc[8] = {st[j].s0.x, st[j].s0.y, st[j].s0.z, st[j].s0.w,
+                                 st[j].s1.x, st[j].s1.y, st[j].s1.z, st[j].s1.w};
+#pragma unroll
+            for (int i = 0; i < 8; ++i) x[i] *= sc[i] * sinv;
+        }
+        half8 ah, al;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            bad |= outside_f16(2.0f * x[i]);  // lo' below is at most 2 |x|
+            const float hv = __uint_as_float(__float_as_uint(x[i]) & 0xFFFFE000u);
+            ah[i] = (_Float16)hv;
+            al[i] = (_Float16)((x[i] - hv) * 2048.0f);
+        }
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            half8 b;
+            if constexpr (ABSORB)
+                b = *reinterpret_cast<const half8 *>(&wt[16 * q + m16][j * BK + 8 * g]);
+            else
+                b = to_half8(st[j].w[q]);
+            acc[q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, b, acc[q], 0, 0, 0);
+            accl[q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, b, accl[q], 0, 0, 0);
+        }
+    }
+    report_range(p, bad);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const int n = n0 + 16 * q + m16;
+        const float sv = ABSORB ? smax : n < N ? p.kv_b.s[wrow0 + n] : 1.0f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const long rr = m0 + 16 * wave + 4 * g + i;
+            const float v = fmaf(accl[q][i], 1.0f / 2048.0f, acc[q][i]) * sv;
+            if (rr < p.rows && n < N) {
+                if constexpr (ABSORB) {
+                    p.query_absorbed[(rr * p.heads + h) * p.latent + n] = v;
+                    report_range(p, outside_f16(v));
+                } else {
+                    p.context[(rr * p.heads + h) * p.vdim + n] = v;
+                }
+            }
+        }
+    }
+}
+
+// The f16 head GEMM for K = KS * 32 (absorb: nope, value: latent); false
+// when no instantiation covers K.
+template <bool ABSORB, int FMT>
+bool launch_head_gemm_f16(const MlaParams &p, dim3 grid, hipStream_t stream) {
+    const int K = ABSORB ? p.nope : p.latent;
+    if (K % 32) return false;
+#define MLH_HG(KS)                                                                                 \
+    case KS:                                                                                       \
+        hipLaunchKernelGGL((mla_head_gemm_f16_kernel<ABSORB, FMT, KS>), grid, dim3(256), 0,        \
+                           stream, p);                                                             \
+        return true;
+    if constexpr (ABSORB) {  // nope <= 256
+        switch (K / 32) {
+            MLH_HG(1) MLH_HG(2) MLH_HG(4) MLH_HG(8)
+        default: return false;
+        }
+    } else {  // latent: a multiple of 64, <= 512
+        switch (K / 32) {
+            MLH_HG(2) MLH_HG(4) MLH_HG(8) MLH_HG(16)
+        default: return false;
+        }
+    }
+#undef MLH_HG
+}
+
 // Prefill attention (rows > 1, causal; moonlight_kernels.metal:247-343 with
 // key_count = position + row + 1), flash form: a workgroup takes RB query
 // rows and every head, and streams key tiles of kPfKeys cache rows
@@ -1185,14 +1370,19 @@ int mla_attention_core(const MlaParams &p, hipStream_t stream) {
         const unsigned mt = (unsigned)((p.rows + 63) / 64);
         hipLaunchKernelGGL(mla_prep_kernel<kF32>, dim3(p.rows, 1 + p.heads), dim3(256), 0, stream,
                            p, 0);
-        hipLaunchKernelGGL(mla_head_gemm_kernel<true>,
-                           dim3(mt, (unsigned)((p.latent + 63) / 64), (unsigned)p.heads), dim3(256),
-                           0, stream, p);
+        // the head GEMMs on the f16 matrix cores for integer kv_b (K a
+        // multiple of 32 with an instantiation), else on fp32 MFMA
+        const dim3 ga(mt, (unsigned)((p.latent + 63) / 64), (unsigned)p.heads);
+        const dim3 gv(mt, (unsigned)((p.vdim + 63) / 64), (unsigned)p.heads);
+        const bool q8 = p.kv_b.fmt == kQ8, q4 = p.kv_b.fmt == kQ4;
+        const bool fa = (q8 && launch_head_gemm_f16<true, kQ8>(p, ga, stream)) ||
+                        (q4 && launch_head_gemm_f16<true, kQ4>(p, ga, stream));
+        if (!fa) hipLaunchKernelGGL(mla_head_gemm_kernel<true>, ga, dim3(256), 0, stream, p);
         hipLaunchKernelGGL((mla_prefill_attend_kernel<RB, NW>), dim3((p.rows + RB - 1) / RB),
                            dim3(64 * NW), (pf_lds_bytes<RB, NW>()), stream, p);
-        hipLaunchKernelGGL(mla_head_gemm_kernel<false>,
-                           dim3(mt, (unsigned)((p.vdim + 63) / 64), (unsigned)p.heads), dim3(256),
-                           0, stream, p);
+        const bool fv = (q8 && launch_head_gemm_f16<false, kQ8>(p, gv, stream)) ||
+                        (q4 && launch_head_gemm_f16<false, kQ4>(p, gv, stream));
+        if (!fv) hipLaunchKernelGGL(mla_head_gemm_kernel<false>, gv, dim3(256), 0, stream, p);
         return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
     }
     // decode: groups of at most kMlaDecodeRows rows (the partial buffers'
