@@ -53,6 +53,11 @@ struct MlaParams {
     float *part_sum = nullptr;          // [rows, kMlaMaxHeads, max_splits]
     float *part_lc = nullptr;           // [rows, kMlaMaxHeads, latent / kMlaValueDims, max_splits, kMlaValueDims]
     float *latent_context = nullptr;    // scratch [rows, heads, latent] merged lc
+    // prefill of at least kMlaExpandMinRows rows with position + rows <=
+    // expand_keys: every key's per-head k_nope and value (kv_b . latent) as
+    // f16 halves, laid out for mla_flash_kernel (mla_expand_kv_bytes per key)
+    uint16_t *kv_expanded = nullptr;
+    long expand_keys = 0;               // key capacity of kv_expanded (a multiple of 64)
     float *context = nullptr;           // out [rows, heads, vdim]
     // decode path (at most kMlaDecodeRows rows per launch group):
     float *value_part = nullptr;   // [rows][heads][latent / kMlaValueDims][vdim] value partials
@@ -64,8 +69,20 @@ struct MlaParams {
     int range_code = 0;
 };
 
-// Prefill: cache append + query RoPE, absorb GEMM, flash attention, value
-// GEMM.  Decode: cache append + query RoPE + absorb, split-K
+// Prefill rows from which the attention runs on per-head keys and values
+// (kv_b applied to every cached latent row once) instead of in the absorbed
+// form, and the bytes of their expanded copy per key (0: the shape has no
+// expanded form).
+constexpr int kMlaExpandMinRows = 64;
+// Keys an expanded copy holds at most (a session's allocation: at Moonlight's
+// shape 21,760 bytes a key, 713 MB at this limit).
+constexpr long kMlaExpandMaxKeys = 32768;
+size_t mla_expand_kv_bytes(int heads, int nope, int rope, int vdim);
+
+// Prefill: cache append + query RoPE, then either the per-head expansion
+// and a flash attention over it (kMlaExpandMinRows rows or more, keys
+// within expand_keys), or the absorb GEMM, flash attention on the latent
+// rows and the value GEMM.  Decode: cache append + query RoPE + absorb, split-K
 // attention, merge + value projection (three launches per group of
 // kMlaDecodeRows rows).  o_proj is a plain GEMV on `context`.
 int mla_attention_core(const MlaParams &p, hipStream_t stream);

@@ -44,6 +44,8 @@ __device__ __forceinline__ int mla_position(const MlaParams &p) {
 // outside the range through p.range_error instead of letting the products
 // turn it into inf / NaN.  NaN and inf inputs propagate as in fp32.
 constexpr float kSplitF16Max = 65504.0f;
+// halves per row of an expanded value block (32 keys + 4 pad)
+constexpr int kFlashVRow = 36;
 __device__ __forceinline__ bool outside_f16(float v) {
     const float a = fabsf(v);
     return a >= kSplitF16Max && a < INFINITY;
@@ -691,6 +693,102 @@ __global__ __launch_bounds__(256) void mla_head_gemm_kernel(MlaParams p) {
     }
 }
 
+// ---- expanded per-head keys and values (prefill of many rows)
+// For every cached key and head, kv_b applied to the latent row once:
+// k_nope (nope dims) and the value (vdim dims), as the f16 halves of
+// mla_flash_kernel's split-f16 operands, in the layout its LDS tiles take
+// by straight copies.  Per head h, from kv_expanded:
+//   keys:   [h][key][KROW]  hi of dims 0 .. QKP - 1, then lo, then 8 pad
+//           (dims: k_nope, the key's rope, zeros up to QKP = nope + rope
+//           rounded up to 32)
+//   values: after every head's keys, [h][key / 32][hi, lo][vdim][VROW],
+//           the 32 keys of a block consecutive for each value dim, 4 pad
+// The pads put consecutive rows of a tile on different LDS banks.
+struct ExpandLayout {
+    int qkp, krow, vdim;
+    long keys;  // capacity (a multiple of 64)
+    __host__ __device__ ExpandLayout(const MlaParams &p)
+        : qkp((p.nope + p.rope + 31) / 32 * 32), krow(2 * qkp + 8), vdim(p.vdim),
+          keys(p.expand_keys) {}
+    __host__ __device__ long key_row(int h, long key) const { return ((long)h * keys + key) * krow; }
+    // value block (hi, lo halves) of keys 32 b .. 32 b + 31
+    __host__ __device__ long value_block(int heads, int h, long b) const {
+        return (long)heads * keys * krow + (((long)h * (keys / 32) + b) * 2) * vdim * kFlashVRow;
+    }
+};
+
+// The split halves of four consecutive values as two 8-byte stores.
+__device__ __forceinline__ void store_split4(uint16_t *hi, uint16_t *lo, const float (&v)[4]) {
+    ushort4 h4, l4;
+    split_f16_bits(v[0], h4.x, l4.x);
+    split_f16_bits(v[1], h4.y, l4.y);
+    split_f16_bits(v[2], h4.z, l4.z);
+    split_f16_bits(v[3], h4.w, l4.w);
+    *reinterpret_cast<ushort4 *>(hi) = h4;
+    *reinterpret_cast<ushort4 *>(lo) = l4;
+}
+
+// The expansion's results (the head GEMM tiles of rows rbase .. rbase + 15
+// of the wave, outputs n0 .. n0 + 63) into the expanded layout; keys from
+// nrows on (up to the 64-row block's end) get zeros.
+__device__ __forceinline__ void expand_epilogue(const MlaParams &p, const f32x4v (&acc)[4],
+                                                const f32x4v (&accl)[4], long wrow0, long rbase,
+                                                int n0, int g, int m16, long nrows, bool &bad) {
+    const ExpandLayout L(p);
+    const int h = blockIdx.z, N = p.nope + p.vdim;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const int nq = n0 + 16 * q;
+        if (nq >= N) continue;
+        float v[4];
+        if (nq < p.nope) {  // D[n][key]: dims nq + 4 g .. + 3 of key rbase + m16
+            const long key = rbase + m16;
+            const f32x4 sc = load_f4(p.kv_b.s + wrow0 + nq + 4 * g);
+            const float s4[4] = {sc.x, sc.y, sc.z, sc.w};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                v[i] = key < nrows ? fmaf(accl[q][i], 1.0f / 2048.0f, acc[q][i]) * s4[i] : 0.0f;
+                bad |= outside_f16(v[i]);
+            }
+            uint16_t *row = p.kv_expanded + L.key_row(h, key) + nq + 4 * g;
+            store_split4(row, row + L.qkp, v);
+        } else {  // D[key][n]: keys rbase + 4 g .. + 3 of value dim nq + m16 - nope
+            const int dv = nq + m16 - p.nope;
+            const float sv = p.kv_b.s[wrow0 + nq + m16];
+            const long key = rbase + 4 * g;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                v[i] = key + i < nrows ? fmaf(accl[q][i], 1.0f / 2048.0f, acc[q][i]) * sv : 0.0f;
+                bad |= outside_f16(v[i]);
+            }
+            uint16_t *blk = p.kv_expanded + L.value_block(p.heads, h, key / 32);
+            uint16_t *hi = blk + (long)dv * kFlashVRow + key % 32;
+            store_split4(hi, hi + (long)p.vdim * kFlashVRow, v);
+        }
+    }
+}
+
+// The rope and padding dims (nope .. QKP - 1) of the key rows m0 .. m0 + 63
+// for head blockIdx.z: the key's rope values, zeros past rope or nrows.
+__device__ __forceinline__ void expand_rope(const MlaParams &p, long m0, long nrows, int t,
+                                            bool &bad) {
+    const ExpandLayout L(p);
+    const int h = blockIdx.z, w4 = (L.qkp - p.nope) / 4;  // 4-dim groups a row
+    for (int i = t; i < 64 * w4; i += 256) {
+        const long key = m0 + i / w4;
+        const int d = 4 * (i % w4);  // rope dim of the group
+        float v[4] = {0.f, 0.f, 0.f, 0.f};
+        if (key < nrows && d < p.rope) {
+            const f32x4 x = load_f4(p.rope_cache + key * p.rope + d);
+            v[0] = x.x, v[1] = x.y, v[2] = x.z, v[3] = x.w;
+        }
+        uint16_t *row = p.kv_expanded + L.key_row(h, key) + p.nope + d;
+        store_split4(row, row + L.qkp, v);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) bad |= outside_f16(v[j]);
+    }
+}
+
 // The same products on the f16 matrix cores for q8 / q4 kv_b.  The stored
 // integers are exact in f16, so an fp32 activation x costs two products
 // instead of one fp32 MFMA at a sixteenth of the rate: hi = x with its low
@@ -702,37 +800,55 @@ __global__ __launch_bounds__(256) void mla_head_gemm_kernel(MlaParams p) {
 // so that the activation stays near the magnitude of q (that scale multiplies
 // the result), and onto the sum in the value projection (its rows are the
 // outputs):
-//   ABSORB: qa[r][h][n] = smax sum_k (q_nope[r][h][k] s[h (nope + v) + k] / smax) w[h (nope + v) + k][n]
+//   absorb: qa[r][h][n] = smax sum_k (q_nope[r][h][k] s[h (nope + v) + k] / smax) w[h (nope + v) + k][n]
 //   value:  ctx[r][h][n] = s[h (nope + v) + nope + n] sum_k lc[r][h][k] w[h (nope + v) + nope + n][k]
+//   expand: kv[key][h][n] = s[h (nope + v) + n] sum_k lat[key][k] w[h (nope + v) + n][k]
+//           (n < nope: k_nope, else the value; every cached key)
 // Workgroup: 64 token rows x 64 outputs of one head (grid z); wave w: rows
 // 16 w .. + 15 against four 16-output tiles, KS steps of 32 k on
 // v_mfma_f32_16x16x32_f16 (lane (m16, g) supplies A[m16][8 g .. + 7] and
-// B[8 g .. + 7][m16]; D[4 g + i][m16] in register i).  A wave reads its own
-// activation rows from global memory; the value weights too (a lane's 8 k of
-// one output row are consecutive bytes).  The loops are unrolled with D
-// steps' loads in flight: the absorb (K = nope, a few steps) issues every
-// step at once and its weights (8 k of one output column lie in 8 rows) go
-// through LDS transposed, one barrier; the value projection (K = latent)
-// keeps D = 4 steps in flight.
-template <bool ABSORB, int FMT, int KS>
+// B[8 g .. + 7][m16]; D[4 g + i][m16] in register i).  The workgroup's
+// weights go into LDS once, [output][k]: the value projection's rows as
+// int8, as they are stored (8 k of one output are one 8-byte read,
+// converted at each use); the absorb's [k][output] block transposed through
+// registers, 8 values of a row a thread, and stored as f16 (its few steps
+// are read by four waves, so the conversion is done once).  A wave reads
+// its own activation rows from global memory, D steps ahead (the absorb:
+// all at once).  Measured on MI355X (2048-token prefill, kernel trace):
+// value 53.5 -> 40.0 us with the int8 LDS rows instead of every wave
+// loading its weights; the absorb's block transposed by v_perm_b32 in 4 x 4
+// byte blocks took 50.5 us as int8 rows and 48.9 as f16 rows, against 46.3
+// for the 8-value rows kept here.  The expansion writes
+// its results as the f16 halves of mla_flash_kernel's operands: k_nope
+// tiles with the operands swapped (D[n][key], four dims of one key per
+// lane), value tiles as they come (four keys of one value dim per lane),
+// and the key rows' rope and padding dims from the workgroups of the first
+// output block.
+enum HeadGemmMode { kHgAbsorb, kHgValue, kHgExpand };
+template <int MODE, int FMT, int KS>
 __global__ __launch_bounds__(256) void mla_head_gemm_f16_kernel(MlaParams p) {
+    constexpr bool ABSORB = MODE == kHgAbsorb, EXPAND = MODE == kHgExpand;
     constexpr int BK = 32, K = KS * BK;
     constexpr int D = ABSORB ? KS : (KS < 4 ? KS : 4);  // steps in flight
-    constexpr int WS = K + 8;                            // halves per transposed row
-    __shared__ __attribute__((aligned(16))) _Float16 wt[ABSORB ? 64 : 1][ABSORB ? WS : 8];
+    // LDS weights [output][k]: the absorb's as f16 (K + 8 halves a row), the
+    // value's as int8 (K + 16 bytes a row; converted at each use)
+    constexpr int WB = ABSORB ? 2 * (K + 8) : K + 16;
+    __shared__ __attribute__((aligned(16))) int8_t wt[64][WB];
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const int g = lane >> 4, m16 = lane & 15;
     const int m0 = blockIdx.x * 64, n0 = blockIdx.y * 64, h = blockIdx.z;
-    const int N = ABSORB ? p.latent : p.vdim;
-    const long wrow0 = (long)h * (p.nope + p.vdim) + (ABSORB ? 0 : p.nope);
+    const int N = ABSORB ? p.latent : EXPAND ? p.nope + p.vdim : p.vdim;
+    const long wrow0 = (long)h * (p.nope + p.vdim) + (MODE == kHgValue ? p.nope : 0);
     const long rbytes = FMT == kQ8 ? p.latent : p.latent / 2;  // bytes per kv_b row
+    // the expansion's rows are the cached keys 0 .. position + rows - 1
+    const long nrows = EXPAND ? (long)mla_position(p) + p.rows : p.rows;
     // this lane's activation row (rows past the end load the last, unused)
-    const long r = m0 + 16 * wave + m16 < p.rows ? m0 + 16 * wave + m16 : p.rows - 1;
-    const float *xrow = ABSORB ? p.query + r * p.query_stride + (long)h * (p.nope + p.rope)
-                               : p.latent_context + (r * p.heads + h) * p.latent;
+    const long r = m0 + 16 * wave + m16 < nrows ? m0 + 16 * wave + m16 : nrows - 1;
+    const float *xrow = ABSORB   ? p.query + r * p.query_stride + (long)h * (p.nope + p.rope)
+                        : EXPAND ? p.latent_cache + r * p.latent
+                                 : p.latent_context + (r * p.heads + h) * p.latent;
     struct Step {
         f32x4 x0, x1, s0, s1;
-        uint2 w[4];  // value: tile q's 8 k (q8: 8 bytes; q4: 4 bytes in .x)
     };
     Step st[KS];
     auto load = [&](int j) {
@@ -742,36 +858,26 @@ __global__ __launch_bounds__(256) void mla_head_gemm_f16_kernel(MlaParams p) {
         if constexpr (ABSORB) {
             st[j].s0 = load_f4(p.kv_b.s + wrow0 + k0);
             st[j].s1 = load_f4(p.kv_b.s + wrow0 + k0 + 4);
-        } else {
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const int n = n0 + 16 * q + m16 < N ? n0 + 16 * q + m16 : N - 1;
-                const uint8_t *src = p.kv_b.w + (wrow0 + n) * rbytes;
-                if constexpr (FMT == kQ8)
-                    st[j].w[q] = *reinterpret_cast<const uint2 *>(src + k0);
-                else
-                    st[j].w[q] = uint2{*reinterpret_cast<const unsigned *>(src + k0 / 2), 0u};
-            }
         }
     };
-    // the 8 stored integers of a uint2 / 4-byte nibble run as f16
-    auto to_half8 = [](uint2 v) {
-        half8 o;
+    // four stored integers (q8 bytes, or q4 nibbles of 2 bytes) as int8 bytes
+    auto int8x4 = [](const uint8_t *src) -> unsigned {
+        if constexpr (FMT == kQ8) {
+            return *reinterpret_cast<const unsigned *>(src);
+        } else {
+            const unsigned v = *reinterpret_cast<const unsigned short *>(src);
+            unsigned o = 0;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            if constexpr (FMT == kQ8)
-                o[i] = (_Float16)(int8_t)(((i < 4 ? v.x : v.y) >> (8 * (i & 3))) & 0xFF);
-            else
-                o[i] = (_Float16)((int)((v.x >> (4 * i)) & 15) - 8);
+            for (int i = 0; i < 4; ++i) o |= (unsigned)(((int)((v >> (4 * i)) & 15) - 8) & 0xFF) << (8 * i);
+            return o;
         }
-        return o;
     };
 #pragma unroll
     for (int j = 0; j < D; ++j) load(j);
-    // absorb: the weight block [K k][64 n] into LDS transposed; thread t
-    // takes rows k = t / 8 + 32 u, columns n0 + 8 (t % 8) .. + 7
-    float smax = 1.0f, sinv = 1.0f;
+    // ---- the weights into LDS, [output][k]
     if constexpr (ABSORB) {
+        // thread t: rows k = t / 8 + 32 u of the [K][64] block, columns
+        // n0 + 8 (t % 8) .. + 7, stored transposed as f16
         const int sk = t >> 3, sn = 8 * (t & 7);
         uint2 wv[KS];
 #pragma unroll
@@ -782,20 +888,35 @@ __global__ __launch_bounds__(256) void mla_head_gemm_f16_kernel(MlaParams p) {
             else
                 wv[u] = uint2{*reinterpret_cast<const unsigned *>(src + (n0 + sn) / 2), 0u};
         }
-        // the head's largest absorb-row scale (every wave)
+#pragma unroll
+        for (int u = 0; u < KS; ++u) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const int v = FMT == kQ8 ? (int)(int8_t)(((i < 4 ? wv[u].x : wv[u].y) >> (8 * (i & 3))) & 0xFF)
+                                         : (int)((wv[u].x >> (4 * i)) & 15) - 8;
+                reinterpret_cast<_Float16 *>(&wt[sn + i][0])[sk + 32 * u] = (_Float16)v;
+            }
+        }
+    } else {
+        // 64 output rows of K bytes (q4: unpacked), 4 bytes per thread and pass
+        constexpr int NW4 = 64 * K / 4;
+#pragma unroll
+        for (int i = t; i < NW4; i += 256) {
+            const int row = i / (K / 4), c = 4 * (i % (K / 4));
+            const int n = n0 + row < N ? n0 + row : N - 1;
+            const uint8_t *src = p.kv_b.w + (wrow0 + n) * rbytes;
+            *reinterpret_cast<unsigned *>(&wt[row][c]) = int8x4(src + (FMT == kQ8 ? c : c / 2));
+        }
+    }
+    float smax = 1.0f, sinv = 1.0f;
+    if constexpr (ABSORB) {  // the head's largest absorb-row scale (every wave)
         float m = 0.0f;
         for (int k = lane; k < K; k += 64) m = fmaxf(m, fabsf(p.kv_b.s[wrow0 + k]));
         m = wave_max(m);
         smax = m;
         sinv = m > 0.0f ? 1.0f / m : 0.0f;
-#pragma unroll
-        for (int u = 0; u < KS; ++u) {
-            const half8 v = to_half8(wv[u]);
-#pragma unroll
-            for (int i = 0; i < 8; ++i) wt[sn + i][sk + 32 * u] = v[i];
-        }
-        __syncthreads();
     }
+    __syncthreads();
     f32x4v acc[4], accl[4];
 #pragma unroll
     for (int q = 0; q < 4; ++q) acc[q] = accl[q] = f32x4v{0.f, 0.f, 0.f, 0.f};
@@ -822,13 +943,28 @@ __global__ __launch_bounds__(256) void mla_head_gemm_f16_kernel(MlaParams p) {
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
             half8 b;
-            if constexpr (ABSORB)
-                b = *reinterpret_cast<const half8 *>(&wt[16 * q + m16][j * BK + 8 * g]);
-            else
-                b = to_half8(st[j].w[q]);
-            acc[q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, b, acc[q], 0, 0, 0);
-            accl[q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, b, accl[q], 0, 0, 0);
+            if constexpr (ABSORB) {
+                b = *reinterpret_cast<const half8 *>(&wt[16 * q + m16][2 * (j * BK + 8 * g)]);
+            } else {
+                const uint2 wb = *reinterpret_cast<const uint2 *>(&wt[16 * q + m16][j * BK + 8 * g]);
+#pragma unroll
+                for (int i = 0; i < 8; ++i)
+                    b[i] = (_Float16)(int8_t)(((i < 4 ? wb.x : wb.y) >> (8 * (i & 3))) & 0xFF);
+            }
+            if (EXPAND && n0 + 16 * q < p.nope) {  // k_nope tile: D[n][key]
+                acc[q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(b, ah, acc[q], 0, 0, 0);
+                accl[q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(b, al, accl[q], 0, 0, 0);
+            } else {
+                acc[q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, b, acc[q], 0, 0, 0);
+                accl[q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, b, accl[q], 0, 0, 0);
+            }
         }
+    }
+    if constexpr (EXPAND) {
+        expand_epilogue(p, acc, accl, wrow0, m0 + 16 * wave, n0, g, m16, nrows, bad);
+        if (blockIdx.y == 0) expand_rope(p, m0, nrows, t, bad);
+        report_range(p, bad);
+        return;
     }
     report_range(p, bad);
 #pragma unroll
@@ -851,18 +987,18 @@ __global__ __launch_bounds__(256) void mla_head_gemm_f16_kernel(MlaParams p) {
     }
 }
 
-// The f16 head GEMM for K = KS * 32 (absorb: nope, value: latent); false
-// when no instantiation covers K.
-template <bool ABSORB, int FMT>
+// The f16 head GEMM for K = KS * 32 (absorb: nope, value and expansion:
+// latent); false when no instantiation covers K.
+template <int MODE, int FMT>
 bool launch_head_gemm_f16(const MlaParams &p, dim3 grid, hipStream_t stream) {
-    const int K = ABSORB ? p.nope : p.latent;
+    const int K = MODE == kHgAbsorb ? p.nope : p.latent;
     if (K % 32) return false;
 #define MLH_HG(KS)                                                                                 \
     case KS:                                                                                       \
-        hipLaunchKernelGGL((mla_head_gemm_f16_kernel<ABSORB, FMT, KS>), grid, dim3(256), 0,        \
+        hipLaunchKernelGGL((mla_head_gemm_f16_kernel<MODE, FMT, KS>), grid, dim3(256), 0,          \
                            stream, p);                                                             \
         return true;
-    if constexpr (ABSORB) {  // nope <= 256
+    if constexpr (MODE == kHgAbsorb) {  // nope <= 256
         switch (K / 32) {
             MLH_HG(1) MLH_HG(2) MLH_HG(4) MLH_HG(8)
         default: return false;
@@ -1137,6 +1273,178 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void mla_prefill_attend_kernel(Mla
     }
 }
 
+// Prefill attention on the expanded keys and values (moonlight_kernels.metal
+// :247-343 with key_count = position + row + 1, its latent form multiplied
+// out: q_absorbed . lat = q_nope . (W_UK lat) and W_UV (sum_k p_k lat_k) =
+// sum_k p_k (W_UV lat_k)), one head per workgroup, causal flash form.
+// Workgroup (head, 64 query rows), wave w: rows 16 w .. + 15; every wave
+// holds its rows' queries (QKP dims) as f16 halves and its rows' value
+// context transposed, O^T[dv][row], in registers.  Per tile of 32 keys,
+// copied with its values into LDS by DMA (double buffered, one barrier):
+//   scores S^T[key][row] = K . Q^T, v_mfma_f32_16x16x32_f16 with the key
+//     rows as A (16 keys a product) and the query as B, split-f16 triples:
+//     a lane ends with four keys of one row;
+//   softmax: per row a running max (lazy, kPfLazyMax) and sum, the row's
+//     four lanes meeting by shuffles;
+//   context O^T += V^T . P^T with the lane's probabilities as B directly
+//     (its 8 k slots: keys 4 g .. + 3 and 16 + 4 g .. + 3) and the value
+//     block rows as A; a rescale touches the lane's own row only.
+// NKS: 32-dim score steps (QKP / 32); NV: 16-dim value tiles (vdim / 16).
+template <int NKS, int NV>
+constexpr size_t flash_lds_bytes() {
+    return 2 * sizeof(uint16_t) * (32 * (2 * 32 * NKS + 8) + 2 * 16 * NV * kFlashVRow);
+}
+
+template <int NKS, int NV>
+__global__ __launch_bounds__(256, 1) void mla_flash_kernel(MlaParams p) {
+    constexpr int QKP = 32 * NKS, KROW = 2 * QKP + 8, VD = 16 * NV;
+    constexpr int KHALVES = 32 * KROW, VHALVES = 2 * VD * kFlashVRow;
+    constexpr int BUF = KHALVES + VHALVES;  // halves per LDS buffer
+    extern __shared__ __attribute__((aligned(16))) uint16_t fl_lds[];
+    const ExpandLayout L(p);
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int g = lane >> 4, m16 = lane & 15;
+    const int h = blockIdx.x;
+    const int nrb = (p.rows + 63) / 64;
+    const int r0 = (nrb - 1 - (int)blockIdx.y) * 64;  // the longest rows first
+    const int pos0 = mla_position(p);
+    const int rl = r0 + 16 * wave + m16;               // this lane's query row
+    const int rc = rl < p.rows ? rl : p.rows - 1;      // (absent rows repeat the last)
+    const int rpos = pos0 + rc;                         // keys 0 .. rpos are visible
+    const int wlast = pos0 + min(r0 + 16 * wave + 15, p.rows - 1);  // the wave's last key
+    const int nk = pos0 + min(r0 + 64, p.rows);         // keys of the workgroup
+    const int ntiles = (nk + 31) / 32;
+    // ---- the query row as f16 halves: dims 32 j + 8 g .. + 7 (k_nope dims,
+    // then the rope, zeros past nope + rope)
+    half8 qh[NKS], ql[NKS];
+    bool bad = false;
+    {
+        const float *qn = p.query + (long)rc * p.query_stride + (long)h * (p.nope + p.rope);
+        const float *qr = p.query_rope + ((long)rc * p.heads + h) * p.rope;
+#pragma unroll
+        for (int j = 0; j < NKS; ++j) {
+            const int d = 32 * j + 8 * g;
+            float x[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+            if (d < p.nope + p.rope) {
+                const float *src = d < p.nope ? qn + d : qr + (d - p.nope);
+                const f32x4 v0 = load_f4(src), v1 = load_f4(src + 4);
+                x[0] = v0.x, x[1] = v0.y, x[2] = v0.z, x[3] = v0.w;
+                x[4] = v1.x, x[5] = v1.y, x[6] = v1.z, x[7] = v1.w;
+            }
+#pragma unroll
+            for (int i = 0; i < 8; ++i) bad |= outside_f16(x[i]);
+            split_f16<8>(x, qh[j], ql[j]);
+        }
+    }
+    report_range(p, bad);
+    // ---- DMA of key tile kt (its key rows, then its value block) into
+    // buffer b: 1 KB per wave instruction, 16 bytes a lane
+    auto issue = [&](int kt, int b) {
+        uint16_t *dst = fl_lds + b * BUF;
+        const uint16_t *ks = p.kv_expanded + L.key_row(h, 32L * kt);
+        const uint16_t *vs = p.kv_expanded + L.value_block(p.heads, h, kt);
+        constexpr int KC = KHALVES / 8, VC = VHALVES / 8;  // 16-byte chunks
+        for (int c0 = 64 * wave; c0 < KC; c0 += 256)
+            if (c0 + lane < KC)
+                __builtin_amdgcn_global_load_lds(
+                    (const __attribute__((address_space(1))) void *)(ks + 8L * (c0 + lane)),
+                    (__attribute__((address_space(3))) void *)(dst + 8 * c0), 16, 0, 0);
+        for (int c0 = 64 * wave; c0 < VC; c0 += 256)
+            if (c0 + lane < VC)
+                __builtin_amdgcn_global_load_lds(
+                    (const __attribute__((address_space(1))) void *)(vs + 8L * (c0 + lane)),
+                    (__attribute__((address_space(3))) void *)(dst + KHALVES + 8 * c0), 16, 0, 0);
+    };
+    f32x4v acc[NV];
+#pragma unroll
+    for (int q = 0; q < NV; ++q) acc[q] = f32x4v{0.f, 0.f, 0.f, 0.f};
+    float m = -INFINITY, l = 0.0f;
+    issue(0, 0);
+    for (int kt = 0; kt < ntiles; ++kt) {
+        __builtin_amdgcn_s_waitcnt(0);  // this wave's part of tile kt has landed
+        __syncthreads();                // every part visible; the other buffer free
+        if (kt + 1 < ntiles) issue(kt + 1, (kt + 1) & 1);
+        if (32 * kt > wlast) continue;  // every key of the tile is after the wave's rows
+        const uint16_t *kb = fl_lds + (kt & 1) * BUF;
+        const uint16_t *vb = kb + KHALVES;
+        // ---- scores: keys 16 s + m16 as A rows, this wave's rows as B columns
+        f32x4v sa[2][2];
+#pragma unroll
+        for (int s2 = 0; s2 < 2; ++s2) sa[s2][0] = sa[s2][1] = f32x4v{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int j = 0; j < NKS; ++j) {
+#pragma unroll
+            for (int s2 = 0; s2 < 2; ++s2) {
+                const uint16_t *kr = kb + (16 * s2 + m16) * KROW + 32 * j + 8 * g;
+                const half8 kh = *reinterpret_cast<const half8 *>(kr);
+                const half8 kl = *reinterpret_cast<const half8 *>(kr + QKP);
+                sa[s2][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, qh[j], sa[s2][0], 0, 0, 0);
+                sa[s2][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, ql[j], sa[s2][1], 0, 0, 0);
+                sa[s2][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kl, qh[j], sa[s2][0], 0, 0, 0);
+            }
+        }
+        // ---- causal mask, online softmax of the lane's row
+        float sv[8];
+        bool valid[8];
+        float mt = -INFINITY;
+#pragma unroll
+        for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int key = 32 * kt + 16 * s2 + 4 * g + i;
+                valid[4 * s2 + i] = key <= rpos;
+                sv[4 * s2 + i] = (sa[s2][0][i] + sa[s2][1][i]) * p.scale;
+                if (valid[4 * s2 + i]) mt = fmaxf(mt, sv[4 * s2 + i]);
+            }
+        mt = fmaxf(mt, __shfl_xor(mt, 16));
+        mt = fmaxf(mt, __shfl_xor(mt, 32));
+        const float mn = mt > m + kPfLazyMax ? mt : m;  // -inf m: the tile max
+        float e[8], es = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            e[i] = valid[i] ? __expf(sv[i] - mn) : 0.0f;
+            es += e[i];
+        }
+        es += __shfl_xor(es, 16);
+        es += __shfl_xor(es, 32);
+        const float sc = mn == m ? 1.0f : __expf(m - mn);  // 0 while m is -inf
+        l = l * sc + es;
+        m = mn;
+        if (__ballot(sc != 1.0f)) {  // rare: a row's max moved
+#pragma unroll
+            for (int q = 0; q < NV; ++q)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) acc[q][i] *= sc;
+        }
+        half8 ph, pl;
+        split_f16<8>(e, ph, pl);
+        // ---- context: value dims 16 q + m16 as A rows (keys 4 g .. + 3 and
+        // 16 + 4 g .. + 3 of the block), the probabilities as B
+#pragma unroll
+        for (int q = 0; q < NV; ++q) {
+            const uint16_t *vr = vb + (16 * q + m16) * kFlashVRow + 4 * g;
+            const half4 h0 = *reinterpret_cast<const half4 *>(vr);
+            const half4 h1 = *reinterpret_cast<const half4 *>(vr + 16);
+            const half4 l0 = *reinterpret_cast<const half4 *>(vr + VD * kFlashVRow);
+            const half4 l1 = *reinterpret_cast<const half4 *>(vr + VD * kFlashVRow + 16);
+            const half8 vh = {h0[0], h0[1], h0[2], h0[3], h1[0], h1[1], h1[2], h1[3]};
+            const half8 vl = {l0[0], l0[1], l0[2], l0[3], l1[0], l1[1], l1[2], l1[3]};
+            acc[q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vh, ph, acc[q], 0, 0, 0);
+            acc[q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vh, pl, acc[q], 0, 0, 0);
+            acc[q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vl, ph, acc[q], 0, 0, 0);
+        }
+    }
+    // ---- the row's context: O^T[16 q + 4 g + i][row] / l
+    if (rl < p.rows) {
+        const float inv = 1.0f / l;
+        float *out = p.context + ((long)rl * p.heads + h) * p.vdim + 4 * g;
+#pragma unroll
+        for (int q = 0; q < NV; ++q)
+            *reinterpret_cast<f32x4 *>(out + 16 * q) =
+                f32x4{acc[q][0] * inv, acc[q][1] * inv, acc[q][2] * inv, acc[q][3] * inv};
+    }
+}
+
 // Merge of the key splits and the value projection, one launch.  Workgroup
 // (row, head h, chunk c of kMlaValueDims latent dims), 8 waves:
 //   merge  lc_h[d] = sum_s e^{m_s - M} lc_s[d] / sum_s e^{m_s - M} l_s for
@@ -1349,6 +1657,58 @@ int mla_split_cache(const float *latent, uint16_t *split, long rows, int width,
     return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
 }
 
+// The flash kernel's instantiations: (QKP / 32, vdim / 16) of Moonlight
+// (nope 128 + rope 64, value 128) and of the small test models (32 + 16, 32).
+static bool flash_shape(int nope, int rope, int vdim, int *nks, int *nv) {
+    if (nope <= 0 || rope <= 0 || vdim <= 0 || nope % 16 || rope % 8 || vdim % 16) return false;
+    *nks = (nope + rope + 31) / 32;
+    *nv = vdim / 16;
+    return (*nks == 6 && *nv == 8) || (*nks == 2 && *nv == 2);
+}
+
+size_t mla_expand_kv_bytes(int heads, int nope, int rope, int vdim) {
+    int nks, nv;
+    if (heads <= 0 || !flash_shape(nope, rope, vdim, &nks, &nv)) return 0;
+    const size_t krow = 2 * 32 * (size_t)nks + 8;
+    return (size_t)heads * (krow + 2 * (size_t)vdim * kFlashVRow / 32) * sizeof(uint16_t);
+}
+
+template <int NKS, int NV>
+static void launch_flash(const MlaParams &p, hipStream_t stream) {
+    static const bool attr = hipFuncSetAttribute(
+        reinterpret_cast<const void *>(&mla_flash_kernel<NKS, NV>),
+        hipFuncAttributeMaxDynamicSharedMemorySize, (int)(flash_lds_bytes<NKS, NV>())) == hipSuccess;
+    (void)attr;
+    constexpr size_t lds = flash_lds_bytes<NKS, NV>();
+    hipLaunchKernelGGL((mla_flash_kernel<NKS, NV>), dim3(p.heads, (p.rows + 63) / 64), dim3(256),
+                       lds, stream, p);
+}
+
+// Prefill on the expanded keys and values: the expansion of every key
+// 0 .. position + rows - 1 (a head GEMM over the latent cache), then the
+// flash kernel.  False (nothing launched) when the shape or format has no
+// instantiation or the keys exceed the expanded buffer.
+static bool mla_prefill_expanded(const MlaParams &p, hipStream_t stream) {
+    int nks, nv;
+    const long nk = (long)p.position + p.rows;
+    if (!p.kv_expanded || p.rows < kMlaExpandMinRows || nk > p.expand_keys ||
+        !flash_shape(p.nope, p.rope, p.vdim, &nks, &nv) || p.latent % 32 ||
+        !(p.latent / 32 == 2 || p.latent / 32 == 4 || p.latent / 32 == 8 || p.latent / 32 == 16) ||
+        (p.kv_b.fmt != kQ8 && p.kv_b.fmt != kQ4))
+        return false;
+    const dim3 ge((unsigned)((nk + 63) / 64), (unsigned)((p.nope + p.vdim + 63) / 64),
+                  (unsigned)p.heads);
+    if (p.kv_b.fmt == kQ8)
+        launch_head_gemm_f16<kHgExpand, kQ8>(p, ge, stream);
+    else
+        launch_head_gemm_f16<kHgExpand, kQ4>(p, ge, stream);
+    if (nks == 6)
+        launch_flash<6, 8>(p, stream);
+    else
+        launch_flash<2, 2>(p, stream);
+    return true;
+}
+
 int mla_attention_core(const MlaParams &p, hipStream_t stream) {
     if (p.heads <= 0 || p.heads > kMlaMaxHeads || p.latent <= 0 || p.latent % 64 ||
         p.latent > kMlaMaxLatent || p.rope <= 0 || p.rope > 64 || (p.rope & 1) ||
@@ -1370,18 +1730,20 @@ int mla_attention_core(const MlaParams &p, hipStream_t stream) {
         const unsigned mt = (unsigned)((p.rows + 63) / 64);
         hipLaunchKernelGGL(mla_prep_kernel<kF32>, dim3(p.rows, 1 + p.heads), dim3(256), 0, stream,
                            p, 0);
+        if (mla_prefill_expanded(p, stream))
+            return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
         // the head GEMMs on the f16 matrix cores for integer kv_b (K a
         // multiple of 32 with an instantiation), else on fp32 MFMA
         const dim3 ga(mt, (unsigned)((p.latent + 63) / 64), (unsigned)p.heads);
         const dim3 gv(mt, (unsigned)((p.vdim + 63) / 64), (unsigned)p.heads);
         const bool q8 = p.kv_b.fmt == kQ8, q4 = p.kv_b.fmt == kQ4;
-        const bool fa = (q8 && launch_head_gemm_f16<true, kQ8>(p, ga, stream)) ||
-                        (q4 && launch_head_gemm_f16<true, kQ4>(p, ga, stream));
+        const bool fa = (q8 && launch_head_gemm_f16<kHgAbsorb, kQ8>(p, ga, stream)) ||
+                        (q4 && launch_head_gemm_f16<kHgAbsorb, kQ4>(p, ga, stream));
         if (!fa) hipLaunchKernelGGL(mla_head_gemm_kernel<true>, ga, dim3(256), 0, stream, p);
         hipLaunchKernelGGL((mla_prefill_attend_kernel<RB, NW>), dim3((p.rows + RB - 1) / RB),
                            dim3(64 * NW), (pf_lds_bytes<RB, NW>()), stream, p);
-        const bool fv = (q8 && launch_head_gemm_f16<false, kQ8>(p, gv, stream)) ||
-                        (q4 && launch_head_gemm_f16<false, kQ4>(p, gv, stream));
+        const bool fv = (q8 && launch_head_gemm_f16<kHgValue, kQ8>(p, gv, stream)) ||
+                        (q4 && launch_head_gemm_f16<kHgValue, kQ4>(p, gv, stream));
         if (!fv) hipLaunchKernelGGL(mla_head_gemm_kernel<false>, gv, dim3(256), 0, stream, p);
         return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
     }

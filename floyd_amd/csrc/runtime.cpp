@@ -118,6 +118,11 @@ struct MoonlightSession {
     float *latent_kv = nullptr, *rope_kv = nullptr, *logits = nullptr;
     // the latent cache's f16 halves (hi, lo) per value: [L][ctx][2][latent]
     uint16_t *latent_split = nullptr;
+    // per-head keys and values of one layer for prefills of many rows
+    // (MlaParams::kv_expanded), expand_keys keys; none when max_batch is
+    // below the expanded path's row threshold or the shape has no such form
+    uint16_t *kv_expanded = nullptr;
+    long expand_keys = 0;
     float *router_logits = nullptr, *route_weights = nullptr;
     // router logit partials of one token row written by o_proj for the MoE
     // layer after it ([experts + 1][hidden / 8], GemvParams router_parts)
@@ -1066,6 +1071,8 @@ int attention(MoonlightSession *s, int layer, const float *x, int rows, int posi
     p.part_sum = s->part_sum;
     p.part_lc = s->part_lc;
     p.latent_context = s->latent_ctx;
+    p.kv_expanded = s->kv_expanded;
+    p.expand_keys = s->expand_keys;
     p.context = s->context;
     p.value_part = s->value_part;
     p.merge_count = s->merge_count;
@@ -1575,6 +1582,11 @@ extern "C" int moonlight_session_create(MoonlightSession **out, MoonlightModel *
     // the split-attention (decode) path runs at most kMlaDecodeRows rows per launch group
     const size_t dr = mb < (size_t)kMlaDecodeRows ? mb : (size_t)kMlaDecodeRows;
     const size_t sw = (size_t)c.moe_intermediate_size * c.shared_expert_count;
+    // the expanded prefill keys: the whole context up to kMlaExpandMaxKeys
+    const size_t expand_bytes =
+        mla_expand_kv_bytes(c.head_count, c.qk_nope_dim, c.qk_rope_dim, c.value_dim);
+    if (expand_bytes && mb >= (size_t)kMlaExpandMinRows)
+        s->expand_keys = (long)std::min<size_t>((ctx + 63) / 64 * 64, (size_t)kMlaExpandMaxKeys);
     size_t lat_elems, rope_elems, lc_elems, logit_elems;
     if (!mul_ok(L * ctx, (size_t)c.kv_lora_rank, &lat_elems) ||
         !mul_ok(L * ctx, (size_t)c.qk_rope_dim, &rope_elems) ||
@@ -1610,6 +1622,9 @@ extern "C" int moonlight_session_create(MoonlightSession **out, MoonlightModel *
         session_alloc(s, &s->merge_count, dr * heads * kMlaCountStride, error, error_size) &&
         hipMemset(s->merge_count, 0, dr * heads * kMlaCountStride * sizeof(int)) == hipSuccess &&
         session_alloc(s, &s->latent_ctx, mb * heads * c.kv_lora_rank, error, error_size) &&
+        (s->expand_keys == 0 ||
+         session_alloc(s, &s->kv_expanded, (size_t)s->expand_keys * expand_bytes / sizeof(uint16_t),
+                       error, error_size)) &&
         session_alloc(s, &s->router_logits, mb * E, error, error_size) &&
         session_alloc(s, &s->router_parts, (size_t)(E + 1) * (c.hidden_size / 8 + 1), error,
                       error_size) &&

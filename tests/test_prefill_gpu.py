@@ -9,6 +9,9 @@ when rows * top_k > 1024.
                              semantics)
   test_tiny_prefill_gemm     a 40-token prefill through every GEMM path (q/kv_a,
                              o_proj, dense SwiGLU + down, experts) vs orc_forward
+  test_tiny_prefill_expanded the attention on expanded per-head keys and
+                             values (100 + 70 rows) vs orc_attention and
+                             orc_forward
   test_moonlight_moe_fixed   the Moonlight MoE layer (config 3 shape) with Zipf
                              routes fixed per token (moe_route_fixed), q8 and q4,
                              T = 64 (32-row tiles), 512 and the full T = 2048
@@ -120,6 +123,48 @@ def test_tiny_prefill_gemm(tiny):
     assert O.lib().orc_forward(orc.handle, O.iptr(np.array([greedy], np.int32)), 1, 40, None,
                                None, O.fptr(e_dec))
     assert rel_l2(dec, e_dec) < 1e-4 and np.max(np.abs(dec - e_dec)) < 3e-4
+    sess.close()
+    orc.close()
+
+
+def test_tiny_prefill_expanded(tiny):
+    """Prefill MLA on the expanded per-head keys and values (64 rows or more):
+    a 100-row prefill and a 70-row append at position 100 (keys from both
+    calls), the attention alone against orc_attention, then the whole
+    forward against orc_forward with the reference's logits gate
+    (tests/test_moonlight_metal_runtime.c:216).  The 40-row prefill above
+    covers the absorbed form at the same shape."""
+    cfg, tensors, model = tiny
+    hidden = cfg["hidden_size"]
+    print("[gpu] tiny expanded prefill: attention 100 + 70 rows, forward", flush=True)
+    orc = CU.oracle_model(cfg, tensors, 256)
+    sess = S.Session(model, 256, 128)
+    rng = np.random.default_rng(31)
+    pos = 0
+    for rows in (100, 70):
+        x = rng.standard_normal((rows, hidden)).astype(np.float32)
+        got = sess.test_attention(1, x, pos)
+        assert got is not None
+        expect = np.empty_like(x)
+        assert O.lib().orc_attention(orc.handle, 1, O.fptr(x), rows, pos, O.fptr(expect))
+        err = rel_l2(got, expect)
+        print(f"[gpu] attention rows {rows} at {pos}: rel-L2 {err:.2e}", flush=True)
+        assert err < 1e-4
+        pos += rows
+    sess.close()
+    orc.close()
+    ids = rng.integers(0, cfg["vocab_size"], 170).astype(np.int32)
+    orc = CU.oracle_model(cfg, tensors, 256)
+    sess = S.Session(model, 256, 128)
+    for lo, hi in ((0, 100), (100, 170)):
+        e_logits = np.empty(cfg["vocab_size"], np.float32)
+        assert O.lib().orc_forward(orc.handle, O.iptr(ids[lo:hi]), hi - lo, lo, None, None,
+                                   O.fptr(e_logits))
+        logits = sess.prefill(ids[lo:hi]) if lo == 0 else sess.append(ids[lo:hi])
+        err = np.max(np.abs(logits - e_logits))
+        print(f"[gpu] forward rows {lo}..{hi}: logits max-abs {err:.2e}", flush=True)
+        assert err < 3e-4 and rel_l2(logits, e_logits) < 1e-4
+        assert int(np.argmax(logits)) == int(np.argmax(e_logits))
     sess.close()
     orc.close()
 
