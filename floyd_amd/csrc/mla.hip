@@ -728,52 +728,12 @@ __device__ __forceinline__ void store_split4(uint16_t *hi, uint16_t *lo, const f
     *reinterpret_cast<ushort4 *>(lo) = l4;
 }
 
-// The expansion's results (the head GEMM tiles of rows rbase .. rbase + 15
-// of the wave, outputs n0 .. n0 + 63) into the expanded layout; keys from
-// nrows on (up to the 64-row block's end) get zeros.
-__device__ __forceinline__ void expand_epilogue(const MlaParams &p, const f32x4v (&acc)[4],
-                                                const f32x4v (&accl)[4], long wrow0, long rbase,
-                                                int n0, int g, int m16, long nrows, bool &bad) {
-    const ExpandLayout L(p);
-    const int h = blockIdx.z, N = p.nope + p.vdim;
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-        const int nq = n0 + 16 * q;
-        if (nq >= N) continue;
-        float v[4];
-        if (nq < p.nope) {  // D[n][key]: dims nq + 4 g .. + 3 of key rbase + m16
-            const long key = rbase + m16;
-            const f32x4 sc = load_f4(p.kv_b.s + wrow0 + nq + 4 * g);
-            const float s4[4] = {sc.x, sc.y, sc.z, sc.w};
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                v[i] = key < nrows ? fmaf(accl[q][i], 1.0f / 2048.0f, acc[q][i]) * s4[i] : 0.0f;
-                bad |= outside_f16(v[i]);
-            }
-            uint16_t *row = p.kv_expanded + L.key_row(h, key) + nq + 4 * g;
-            store_split4(row, row + L.qkp, v);
-        } else {  // D[key][n]: keys rbase + 4 g .. + 3 of value dim nq + m16 - nope
-            const int dv = nq + m16 - p.nope;
-            const float sv = p.kv_b.s[wrow0 + nq + m16];
-            const long key = rbase + 4 * g;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                v[i] = key + i < nrows ? fmaf(accl[q][i], 1.0f / 2048.0f, acc[q][i]) * sv : 0.0f;
-                bad |= outside_f16(v[i]);
-            }
-            uint16_t *blk = p.kv_expanded + L.value_block(p.heads, h, key / 32);
-            uint16_t *hi = blk + (long)dv * kFlashVRow + key % 32;
-            store_split4(hi, hi + (long)p.vdim * kFlashVRow, v);
-        }
-    }
-}
-
 // The rope and padding dims (nope .. QKP - 1) of the key rows m0 .. m0 + 63
-// for head blockIdx.z: the key's rope values, zeros past rope or nrows.
-__device__ __forceinline__ void expand_rope(const MlaParams &p, long m0, long nrows, int t,
-                                            bool &bad) {
+// for head h: the key's rope values, zeros past rope or nrows.
+__device__ __forceinline__ void expand_rope(const MlaParams &p, int h, long m0, long nrows,
+                                            int t, bool &bad) {
     const ExpandLayout L(p);
-    const int h = blockIdx.z, w4 = (L.qkp - p.nope) / 4;  // 4-dim groups a row
+    const int w4 = (L.qkp - p.nope) / 4;  // 4-dim groups a row
     for (int i = t; i < 64 * w4; i += 256) {
         const long key = m0 + i / w4;
         const int d = 4 * (i % w4);  // rope dim of the group
@@ -802,8 +762,6 @@ __device__ __forceinline__ void expand_rope(const MlaParams &p, long m0, long nr
 // outputs):
 //   absorb: qa[r][h][n] = smax sum_k (q_nope[r][h][k] s[h (nope + v) + k] / smax) w[h (nope + v) + k][n]
 //   value:  ctx[r][h][n] = s[h (nope + v) + nope + n] sum_k lc[r][h][k] w[h (nope + v) + nope + n][k]
-//   expand: kv[key][h][n] = s[h (nope + v) + n] sum_k lat[key][k] w[h (nope + v) + n][k]
-//           (n < nope: k_nope, else the value; every cached key)
 // Workgroup: 64 token rows x 64 outputs of one head (grid z); wave w: rows
 // 16 w .. + 15 against four 16-output tiles, KS steps of 32 k on
 // v_mfma_f32_16x16x32_f16 (lane (m16, g) supplies A[m16][8 g .. + 7] and
@@ -818,16 +776,11 @@ __device__ __forceinline__ void expand_rope(const MlaParams &p, long m0, long nr
 // value 53.5 -> 40.0 us with the int8 LDS rows instead of every wave
 // loading its weights; the absorb's block transposed by v_perm_b32 in 4 x 4
 // byte blocks took 50.5 us as int8 rows and 48.9 as f16 rows, against 46.3
-// for the 8-value rows kept here.  The expansion writes
-// its results as the f16 halves of mla_flash_kernel's operands: k_nope
-// tiles with the operands swapped (D[n][key], four dims of one key per
-// lane), value tiles as they come (four keys of one value dim per lane),
-// and the key rows' rope and padding dims from the workgroups of the first
-// output block.
-enum HeadGemmMode { kHgAbsorb, kHgValue, kHgExpand };
+// for the 8-value rows kept here.
+enum HeadGemmMode { kHgAbsorb, kHgValue };
 template <int MODE, int FMT, int KS>
 __global__ __launch_bounds__(256) void mla_head_gemm_f16_kernel(MlaParams p) {
-    constexpr bool ABSORB = MODE == kHgAbsorb, EXPAND = MODE == kHgExpand;
+    constexpr bool ABSORB = MODE == kHgAbsorb;
     constexpr int BK = 32, K = KS * BK;
     constexpr int D = ABSORB ? KS : (KS < 4 ? KS : 4);  // steps in flight
     // LDS weights [output][k]: the absorb's as f16 (K + 8 halves a row), the
@@ -837,16 +790,13 @@ __global__ __launch_bounds__(256) void mla_head_gemm_f16_kernel(MlaParams p) {
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const int g = lane >> 4, m16 = lane & 15;
     const int m0 = blockIdx.x * 64, n0 = blockIdx.y * 64, h = blockIdx.z;
-    const int N = ABSORB ? p.latent : EXPAND ? p.nope + p.vdim : p.vdim;
+    const int N = ABSORB ? p.latent : p.vdim;
     const long wrow0 = (long)h * (p.nope + p.vdim) + (MODE == kHgValue ? p.nope : 0);
     const long rbytes = FMT == kQ8 ? p.latent : p.latent / 2;  // bytes per kv_b row
-    // the expansion's rows are the cached keys 0 .. position + rows - 1
-    const long nrows = EXPAND ? (long)mla_position(p) + p.rows : p.rows;
     // this lane's activation row (rows past the end load the last, unused)
-    const long r = m0 + 16 * wave + m16 < nrows ? m0 + 16 * wave + m16 : nrows - 1;
-    const float *xrow = ABSORB   ? p.query + r * p.query_stride + (long)h * (p.nope + p.rope)
-                        : EXPAND ? p.latent_cache + r * p.latent
-                                 : p.latent_context + (r * p.heads + h) * p.latent;
+    const long r = m0 + 16 * wave + m16 < p.rows ? m0 + 16 * wave + m16 : p.rows - 1;
+    const float *xrow = ABSORB ? p.query + r * p.query_stride + (long)h * (p.nope + p.rope)
+                               : p.latent_context + (r * p.heads + h) * p.latent;
     struct Step {
         f32x4 x0, x1, s0, s1;
     };
@@ -951,20 +901,9 @@ __global__ __launch_bounds__(256) void mla_head_gemm_f16_kernel(MlaParams p) {
                 for (int i = 0; i < 8; ++i)
                     b[i] = (_Float16)(int8_t)(((i < 4 ? wb.x : wb.y) >> (8 * (i & 3))) & 0xFF);
             }
-            if (EXPAND && n0 + 16 * q < p.nope) {  // k_nope tile: D[n][key]
-                acc[q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(b, ah, acc[q], 0, 0, 0);
-                accl[q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(b, al, accl[q], 0, 0, 0);
-            } else {
-                acc[q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, b, acc[q], 0, 0, 0);
-                accl[q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, b, accl[q], 0, 0, 0);
-            }
+            acc[q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, b, acc[q], 0, 0, 0);
+            accl[q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, b, accl[q], 0, 0, 0);
         }
-    }
-    if constexpr (EXPAND) {
-        expand_epilogue(p, acc, accl, wrow0, m0 + 16 * wave, n0, g, m16, nrows, bad);
-        if (blockIdx.y == 0) expand_rope(p, m0, nrows, t, bad);
-        report_range(p, bad);
-        return;
     }
     report_range(p, bad);
 #pragma unroll
@@ -987,8 +926,8 @@ __global__ __launch_bounds__(256) void mla_head_gemm_f16_kernel(MlaParams p) {
     }
 }
 
-// The f16 head GEMM for K = KS * 32 (absorb: nope, value and expansion:
-// latent); false when no instantiation covers K.
+// The f16 head GEMM for K = KS * 32 (absorb: nope, value: latent); false
+// when no instantiation covers K.
 template <int MODE, int FMT>
 bool launch_head_gemm_f16(const MlaParams &p, dim3 grid, hipStream_t stream) {
     const int K = MODE == kHgAbsorb ? p.nope : p.latent;
@@ -1010,6 +949,180 @@ bool launch_head_gemm_f16(const MlaParams &p, dim3 grid, hipStream_t stream) {
         }
     }
 #undef MLH_HG
+}
+
+// Expansion of the cached latent rows into the per-head keys and values of
+// mla_flash_kernel (ExpandLayout), for every key 0 .. position + rows - 1:
+//   kv[key][h][n] = s[h (nope + v) + n] sum_k lat[key][k] w[h (nope + v) + n][k]
+// (n < nope: k_nope, else the value), on the f16 matrix cores as the head
+// GEMMs do it (the integers exact in f16; the activation as hi and lo' =
+// (x - hi) 2^11 in two accumulators).  Workgroup: 64 keys x every output of
+// one head (nope + vdim <= 256 in tiles of 16; wave w takes tiles w, w + 4,
+// ..), so each latent row is read and split once per head and the head's
+// kv_b rows once per 64 keys.  Per chunk of 64 k the split keys and the
+// weights converted to f16 go into LDS, the next chunk's loads in flight in
+// registers meanwhile.  k_nope tiles take the weights as A (D[n][key]: four
+// dims of one key a lane, one 8-byte store a half), value tiles the keys as
+// A (D[key][n]: four keys of one value dim a lane, as the value blocks hold
+// them); the workgroup also writes its keys' rope and padding dims.
+constexpr int kExKC = 64;               // k per chunk
+constexpr int kExARow = 2 * kExKC + 8;  // halves per key row in LDS (hi, lo', pad)
+constexpr int kExBRow = kExKC + 8;      // halves per weight row in LDS
+template <int FMT>
+__global__ __launch_bounds__(256, 2) void mla_expand_kernel(MlaParams p) {
+    __shared__ __attribute__((aligned(16))) _Float16 as[64 * kExARow];
+    __shared__ __attribute__((aligned(16))) _Float16 bs[256 * kExBRow];
+    const ExpandLayout L(p);
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int g = lane >> 4, m16 = lane & 15;
+    const long m0 = (long)blockIdx.x * 64;
+    const int h = blockIdx.y;
+    const long nk = (long)mla_position(p) + p.rows;
+    const int N = p.nope + p.vdim, NT = N / 16;
+    const long wrow0 = (long)h * N;
+    const long rbytes = FMT == kQ8 ? p.latent : p.latent / 2;  // bytes per kv_b row
+    constexpr int NB = FMT == kQ8 ? 4 : 2;  // 16-byte weight pieces a thread and chunk
+    f32x4 ra[4];
+    uint4 rb[NB];
+    // chunk c: latent float4 (t + 256 u) = key / 16, k 4 (% 16); weight
+    // piece (t + 256 u) = row / (4 or 2), 16 bytes (% 4 or 2)
+    auto load = [&](int c) {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int idx = t + 256 * u;
+            const long key = m0 + idx / 16 < nk ? m0 + idx / 16 : nk - 1;
+            ra[u] = load_f4(p.latent_cache + key * p.latent + kExKC * c + 4 * (idx % 16));
+        }
+#pragma unroll
+        for (int u = 0; u < NB; ++u) {
+            const int idx = t + 256 * u, row = idx / NB;
+            const int n = row < N ? row : N - 1;
+            rb[u] = *reinterpret_cast<const uint4 *>(p.kv_b.w + (wrow0 + n) * rbytes +
+                                                     (FMT == kQ8 ? kExKC : kExKC / 2) * c +
+                                                     16 * (idx % NB));
+        }
+    };
+    bool bad = false;
+    auto store = [&]() {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int idx = t + 256 * u;
+            const float x[4] = {ra[u].x, ra[u].y, ra[u].z, ra[u].w};
+            half4 hv, lv;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                bad |= outside_f16(2.0f * x[i]);  // lo' is at most 2 |x|
+                const float hx = __uint_as_float(__float_as_uint(x[i]) & 0xFFFFE000u);
+                hv[i] = (_Float16)hx;
+                lv[i] = (_Float16)((x[i] - hx) * 2048.0f);
+            }
+            _Float16 *dst = as + (idx / 16) * kExARow + 4 * (idx % 16);
+            *reinterpret_cast<half4 *>(dst) = hv;
+            *reinterpret_cast<half4 *>(dst + kExKC) = lv;
+        }
+#pragma unroll
+        for (int u = 0; u < NB; ++u) {
+            const int idx = t + 256 * u, row = idx / NB;
+            if (row >= N) continue;
+            const unsigned wv[4] = {rb[u].x, rb[u].y, rb[u].z, rb[u].w};
+            _Float16 *dst = bs + row * kExBRow + (FMT == kQ8 ? 16 : 32) * (idx % NB);
+#pragma unroll
+            for (int v = 0; v < (FMT == kQ8 ? 2 : 4); ++v) {
+                half8 o;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    if constexpr (FMT == kQ8)
+                        o[i] = (_Float16)(int8_t)((wv[2 * v + i / 4] >> (8 * (i & 3))) & 0xFF);
+                    else
+                        o[i] = (_Float16)((int)((wv[v] >> (4 * i)) & 15) - 8);
+                }
+                *reinterpret_cast<half8 *>(dst + 8 * v) = o;
+            }
+        }
+    };
+    f32x4v acc[4][4], accl[4][4];
+#pragma unroll
+    for (int qq = 0; qq < 4; ++qq)
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) acc[qq][mt] = accl[qq][mt] = f32x4v{0.f, 0.f, 0.f, 0.f};
+    const int nch = p.latent / kExKC;
+    load(0);
+    for (int c = 0; c < nch; ++c) {
+        if (c) __syncthreads();  // the previous chunk's LDS reads are done
+        store();
+        __syncthreads();
+        if (c + 1 < nch) load(c + 1);
+#pragma unroll
+        for (int s2 = 0; s2 < kExKC / 32; ++s2) {
+            half8 ah[4], al[4];
+#pragma unroll
+            for (int mt = 0; mt < 4; ++mt) {
+                const _Float16 *src = as + (16 * mt + m16) * kExARow + 32 * s2 + 8 * g;
+                ah[mt] = *reinterpret_cast<const half8 *>(src);
+                al[mt] = *reinterpret_cast<const half8 *>(src + kExKC);
+            }
+#pragma unroll
+            for (int qq = 0; qq < 4; ++qq) {
+                const int q = wave + 4 * qq;
+                if (q >= NT) continue;
+                const half8 b =
+                    *reinterpret_cast<const half8 *>(bs + (16 * q + m16) * kExBRow + 32 * s2 + 8 * g);
+                if (16 * q < p.nope) {
+#pragma unroll
+                    for (int mt = 0; mt < 4; ++mt) {
+                        acc[qq][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(b, ah[mt], acc[qq][mt], 0, 0, 0);
+                        accl[qq][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(b, al[mt], accl[qq][mt], 0, 0, 0);
+                    }
+                } else {
+#pragma unroll
+                    for (int mt = 0; mt < 4; ++mt) {
+                        acc[qq][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[mt], b, acc[qq][mt], 0, 0, 0);
+                        accl[qq][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[mt], b, accl[qq][mt], 0, 0, 0);
+                    }
+                }
+            }
+        }
+    }
+    // ---- results into the expanded layout (keys from nk on: zeros)
+#pragma unroll
+    for (int qq = 0; qq < 4; ++qq) {
+        const int q = wave + 4 * qq, nq = 16 * q;
+        if (q >= NT) continue;
+        if (nq < p.nope) {  // D[n][key]: dims nq + 4 g .. + 3 of key m0 + 16 mt + m16
+            const f32x4 sc = load_f4(p.kv_b.s + wrow0 + nq + 4 * g);
+            const float s4[4] = {sc.x, sc.y, sc.z, sc.w};
+#pragma unroll
+            for (int mt = 0; mt < 4; ++mt) {
+                const long key = m0 + 16 * mt + m16;
+                float v[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    v[i] = key < nk ? fmaf(accl[qq][mt][i], 1.0f / 2048.0f, acc[qq][mt][i]) * s4[i] : 0.0f;
+                    bad |= outside_f16(v[i]);
+                }
+                uint16_t *row = p.kv_expanded + L.key_row(h, key) + nq + 4 * g;
+                store_split4(row, row + L.qkp, v);
+            }
+        } else {  // D[key][n]: keys m0 + 16 mt + 4 g .. + 3 of value dim nq + m16 - nope
+            const int dv = nq + m16 - p.nope;
+            const float sv = p.kv_b.s[wrow0 + nq + m16];
+#pragma unroll
+            for (int mt = 0; mt < 4; ++mt) {
+                const long key = m0 + 16 * mt + 4 * g;
+                float v[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    v[i] = key + i < nk ? fmaf(accl[qq][mt][i], 1.0f / 2048.0f, acc[qq][mt][i]) * sv : 0.0f;
+                    bad |= outside_f16(v[i]);
+                }
+                uint16_t *hi = p.kv_expanded + L.value_block(p.heads, h, key / 32) +
+                               (long)dv * kFlashVRow + key % 32;
+                store_split4(hi, hi + (long)p.vdim * kFlashVRow, v);
+            }
+        }
+    }
+    expand_rope(p, h, m0, nk, t, bad);
+    report_range(p, bad);
 }
 
 // Prefill attention (rows > 1, causal; moonlight_kernels.metal:247-343 with
@@ -1692,16 +1805,14 @@ static bool mla_prefill_expanded(const MlaParams &p, hipStream_t stream) {
     int nks, nv;
     const long nk = (long)p.position + p.rows;
     if (!p.kv_expanded || p.rows < kMlaExpandMinRows || nk > p.expand_keys ||
-        !flash_shape(p.nope, p.rope, p.vdim, &nks, &nv) || p.latent % 32 ||
-        !(p.latent / 32 == 2 || p.latent / 32 == 4 || p.latent / 32 == 8 || p.latent / 32 == 16) ||
-        (p.kv_b.fmt != kQ8 && p.kv_b.fmt != kQ4))
+        !flash_shape(p.nope, p.rope, p.vdim, &nks, &nv) || p.latent % kExKC ||
+        p.nope + p.vdim > 256 || (p.kv_b.fmt != kQ8 && p.kv_b.fmt != kQ4))
         return false;
-    const dim3 ge((unsigned)((nk + 63) / 64), (unsigned)((p.nope + p.vdim + 63) / 64),
-                  (unsigned)p.heads);
+    const dim3 ge((unsigned)((nk + 63) / 64), (unsigned)p.heads);
     if (p.kv_b.fmt == kQ8)
-        launch_head_gemm_f16<kHgExpand, kQ8>(p, ge, stream);
+        hipLaunchKernelGGL(mla_expand_kernel<kQ8>, ge, dim3(256), 0, stream, p);
     else
-        launch_head_gemm_f16<kHgExpand, kQ4>(p, ge, stream);
+        hipLaunchKernelGGL(mla_expand_kernel<kQ4>, ge, dim3(256), 0, stream, p);
     if (nks == 6)
         launch_flash<6, 8>(p, stream);
     else
