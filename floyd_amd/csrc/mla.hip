@@ -1393,26 +1393,46 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void mla_prefill_attend_kernel(Mla
 // Workgroup (head, 64 query rows), wave w: rows 16 w .. + 15; every wave
 // holds its rows' queries (QKP dims) as f16 halves and its rows' value
 // context transposed, O^T[dv][row], in registers.  Per tile of 32 keys,
-// copied with its values into LDS by DMA (double buffered, one barrier):
+// copied with its values into LDS by DMA (one buffer, 43.5 KB at Moonlight's
+// shape, so three workgroups share a CU and hide each other's copies;
+// measured on MI355X against two buffers and one workgroup a CU: 165.7
+// against 180.1 us per layer, 2048-token prefill; workgroups ordered so that
+// the XCD of workgroup i (i % 8) takes one head after another measured
+// 181.9 against 162.3 us with the same L2 hit rate, 89 %):
 //   scores S^T[key][row] = K . Q^T, v_mfma_f32_16x16x32_f16 with the key
 //     rows as A (16 keys a product) and the query as B, split-f16 triples:
 //     a lane ends with four keys of one row;
 //   softmax: per row a running max (lazy, kPfLazyMax) and sum, the row's
-//     four lanes meeting by shuffles;
+//     four lanes meeting by row swaps (quad_rows_max / quad_rows_sum);
 //   context O^T += V^T . P^T with the lane's probabilities as B directly
 //     (its 8 k slots: keys 4 g .. + 3 and 16 + 4 g .. + 3) and the value
 //     block rows as A; a rescale touches the lane's own row only.
 // NKS: 32-dim score steps (QKP / 32); NV: 16-dim value tiles (vdim / 16).
+// Max / sum over the four 16-lane rows of a wave for each lane position
+// (lanes l, l ^ 16, l ^ 32, l ^ 48), by the gfx950 row swaps: the same
+// order of terms in every lane, so the four copies agree bit for bit.
+__device__ __forceinline__ float quad_rows_max(float v) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    const float m = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(m), __float_as_uint(m), false, false);
+    return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+__device__ __forceinline__ float quad_rows_sum(float v) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    const float m = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(m), __float_as_uint(m), false, false);
+    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
 template <int NKS, int NV>
 constexpr size_t flash_lds_bytes() {
-    return 2 * sizeof(uint16_t) * (32 * (2 * 32 * NKS + 8) + 2 * 16 * NV * kFlashVRow);
+    return sizeof(uint16_t) * (32 * (2 * 32 * NKS + 8) + 2 * 16 * NV * kFlashVRow);
 }
 
 template <int NKS, int NV>
 __global__ __launch_bounds__(256, 1) void mla_flash_kernel(MlaParams p) {
     constexpr int QKP = 32 * NKS, KROW = 2 * QKP + 8, VD = 16 * NV;
     constexpr int KHALVES = 32 * KROW, VHALVES = 2 * VD * kFlashVRow;
-    constexpr int BUF = KHALVES + VHALVES;  // halves per LDS buffer
     extern __shared__ __attribute__((aligned(16))) uint16_t fl_lds[];
     const ExpandLayout L(p);
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
@@ -1450,10 +1470,10 @@ __global__ __launch_bounds__(256, 1) void mla_flash_kernel(MlaParams p) {
         }
     }
     report_range(p, bad);
-    // ---- DMA of key tile kt (its key rows, then its value block) into
-    // buffer b: 1 KB per wave instruction, 16 bytes a lane
-    auto issue = [&](int kt, int b) {
-        uint16_t *dst = fl_lds + b * BUF;
+    // ---- DMA of key tile kt (its key rows, then its value block) into LDS:
+    // 1 KB per wave instruction, 16 bytes a lane
+    auto issue = [&](int kt) {
+        uint16_t *dst = fl_lds;
         const uint16_t *ks = p.kv_expanded + L.key_row(h, 32L * kt);
         const uint16_t *vs = p.kv_expanded + L.value_block(p.heads, h, kt);
         constexpr int KC = KHALVES / 8, VC = VHALVES / 8;  // 16-byte chunks
@@ -1472,13 +1492,16 @@ __global__ __launch_bounds__(256, 1) void mla_flash_kernel(MlaParams p) {
 #pragma unroll
     for (int q = 0; q < NV; ++q) acc[q] = f32x4v{0.f, 0.f, 0.f, 0.f};
     float m = -INFINITY, l = 0.0f;
-    issue(0, 0);
+    issue(0);
     for (int kt = 0; kt < ntiles; ++kt) {
         __builtin_amdgcn_s_waitcnt(0);  // this wave's part of tile kt has landed
-        __syncthreads();                // every part visible; the other buffer free
-        if (kt + 1 < ntiles) issue(kt + 1, (kt + 1) & 1);
-        if (32 * kt > wlast) continue;  // every key of the tile is after the wave's rows
-        const uint16_t *kb = fl_lds + (kt & 1) * BUF;
+        __syncthreads();                // every part visible
+        if (32 * kt > wlast) {  // every key of the tile is after the wave's rows
+            __syncthreads();
+            if (kt + 1 < ntiles) issue(kt + 1);
+            continue;
+        }
+        const uint16_t *kb = fl_lds;
         const uint16_t *vb = kb + KHALVES;
         // ---- scores: keys 16 s + m16 as A rows, this wave's rows as B columns
         f32x4v sa[2][2];
@@ -1509,8 +1532,7 @@ __global__ __launch_bounds__(256, 1) void mla_flash_kernel(MlaParams p) {
                 sv[4 * s2 + i] = (sa[s2][0][i] + sa[s2][1][i]) * p.scale;
                 if (valid[4 * s2 + i]) mt = fmaxf(mt, sv[4 * s2 + i]);
             }
-        mt = fmaxf(mt, __shfl_xor(mt, 16));
-        mt = fmaxf(mt, __shfl_xor(mt, 32));
+        mt = quad_rows_max(mt);
         const float mn = mt > m + kPfLazyMax ? mt : m;  // -inf m: the tile max
         float e[8], es = 0.0f;
 #pragma unroll
@@ -1518,8 +1540,7 @@ __global__ __launch_bounds__(256, 1) void mla_flash_kernel(MlaParams p) {
             e[i] = valid[i] ? __expf(sv[i] - mn) : 0.0f;
             es += e[i];
         }
-        es += __shfl_xor(es, 16);
-        es += __shfl_xor(es, 32);
+        es = quad_rows_sum(es);
         const float sc = mn == m ? 1.0f : __expf(m - mn);  // 0 while m is -inf
         l = l * sc + es;
         m = mn;
@@ -1546,6 +1567,8 @@ __global__ __launch_bounds__(256, 1) void mla_flash_kernel(MlaParams p) {
             acc[q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vh, pl, acc[q], 0, 0, 0);
             acc[q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vl, ph, acc[q], 0, 0, 0);
         }
+        __syncthreads();  // every wave is done with the tile
+        if (kt + 1 < ntiles) issue(kt + 1);
     }
     // ---- the row's context: O^T[16 q + 4 g + i][row] / l
     if (rl < p.rows) {
