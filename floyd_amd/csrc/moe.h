@@ -15,6 +15,10 @@ int route_topk(const RouteParams &p, hipStream_t stream);
 // non-null: logits [rows, experts].
 int router_logits(const float *x, const float *norm_w, float eps, const float *w, int rows,
                   int experts, int width, float *logits, hipStream_t stream);
+// The same for fewer rows (one workgroup per expert and 16 rows; width a
+// multiple of 8).
+int router_logits_small(const float *x, const float *norm_w, float eps, const float *w, int rows,
+                        int experts, int width, float *logits, hipStream_t stream);
 
 struct CombineParams {
     int rows = 0, hidden = 0, top_k = 0;

@@ -235,6 +235,80 @@ int router_logits(const float *x, const float *norm_w, float eps, const float *w
     return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
 }
 
+// Router logits for batches of fewer rows than router_logits_kernel needs
+// for its parallelism (decode batches, short prefill chunks): workgroup
+// (expert e, group of up to kRsRows token rows), thread t taking 8
+// consecutive k of every 2048 (one load of the expert's weights and the norm
+// weight), the same sums as router_logits_kernel (sum_k (x n)[k] w[e][k] and
+// sum_k x[k]^2 per row, the norm's 1 / rms applied at the end).  The 256
+// threads' sums meet in LDS: thread (row, segment) adds 16 of them in
+// order, then the row's 16 segments by a butterfly, so the result does not
+// depend on timing.  One round of loads instead of the GEMV's passes.
+constexpr int kRsRows = 16;
+__global__ __launch_bounds__(256) void router_small_kernel(const float *x, const float *norm_w,
+                                                           float eps, const float *w, int rows,
+                                                           int experts, int width,
+                                                           float *logits) {
+    __shared__ float part[2][kRsRows][257];  // [dot, sum of squares][row][thread]
+    const int t = threadIdx.x, e = blockIdx.x, r0 = blockIdx.y * kRsRows;
+    const int nr = rows - r0 < kRsRows ? rows - r0 : kRsRows;
+    const float *we = w + (long)e * width;
+    float dot[kRsRows], ss[kRsRows];
+#pragma unroll
+    for (int r = 0; r < kRsRows; ++r) dot[r] = ss[r] = 0.0f;
+    for (int k = 8 * t; k < width; k += 8 * 256) {
+        const f32x4 w0 = load_f4(we + k), w1 = load_f4(we + k + 4);
+        f32x4 n0 = {1.f, 1.f, 1.f, 1.f}, n1 = {1.f, 1.f, 1.f, 1.f};
+        if (norm_w) {
+            n0 = load_f4(norm_w + k);
+            n1 = load_f4(norm_w + k + 4);
+        }
+        const float wv[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+        const float nv[8] = {n0.x, n0.y, n0.z, n0.w, n1.x, n1.y, n1.z, n1.w};
+#pragma unroll
+        for (int r = 0; r < kRsRows; ++r) {
+            if (r < nr) {
+                const float *xr = x + (long)(r0 + r) * width + k;
+                const f32x4 a = load_f4(xr), b = load_f4(xr + 4);
+                const float xv[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    ss[r] += xv[j] * xv[j];
+                    dot[r] += (xv[j] * nv[j]) * wv[j];
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < kRsRows; ++r) {
+        part[0][r][t] = dot[r];
+        part[1][r][t] = ss[r];
+    }
+    __syncthreads();
+    const int row = t >> 4, seg = t & 15;
+    float d = 0.0f, q = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+        d += part[0][row][16 * seg + j];
+        q += part[1][row][16 * seg + j];
+    }
+    d = group_sum<16>(d);
+    q = group_sum<16>(q);
+    if (seg == 0 && row < nr) {
+        const float inv = norm_w ? 1.0f / sqrtf(q / (float)width + eps) : 1.0f;
+        logits[(long)(r0 + row) * experts + e] = d * inv;
+    }
+}
+
+int router_logits_small(const float *x, const float *norm_w, float eps, const float *w, int rows,
+                        int experts, int width, float *logits, hipStream_t stream) {
+    if (!x || !w || !logits || rows <= 0 || experts <= 0 || width <= 0 || width % 8)
+        return kErrArgs;
+    hipLaunchKernelGGL(router_small_kernel, dim3(experts, (rows + kRsRows - 1) / kRsRows),
+                       dim3(256), 0, stream, x, norm_w, eps, w, rows, experts, width, logits);
+    return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
+}
+
 int route_topk(const RouteParams &p, hipStream_t stream) {
     if (!p.logits || !p.bias || !p.ids || !p.weights || p.rows <= 0 || p.experts <= 0 ||
         p.experts > kMaxExperts || p.top_k <= 0 || p.top_k > kMaxTopK ||

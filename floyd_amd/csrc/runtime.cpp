@@ -1089,7 +1089,8 @@ int attention(MoonlightSession *s, int layer, const float *x, int rows, int posi
 constexpr int kPresplitMinRows = 2;
 
 // The MFMA router (32 x 32 tiles, one workgroup per tile) has the
-// parallelism for prefill batches; fewer rows take the GEMV.
+// parallelism for prefill batches; fewer rows take router_logits_small (one
+// workgroup per expert and 16 rows).
 constexpr int kRouterMfmaMinRows = 256;
 
 // fixed: the MoE test / timing hooks take the caller's expert ids when set
@@ -1154,6 +1155,10 @@ int route(MoonlightSession *s, int layer, const float *x, int rows, const float 
     } else if (rows >= kRouterMfmaMinRows && f32_router && c.hidden_size % 16 == 0) {
         if (router_logits(x, norm_w, c.rms_norm_epsilon, router_w, rows, c.expert_count,
                           c.hidden_size, s->router_logits, stream_of(s)))
+            return kErrLaunch;
+    } else if (f32_router && c.hidden_size % 8 == 0) {
+        if (router_logits_small(x, norm_w, c.rms_norm_epsilon, router_w, rows, c.expert_count,
+                                c.hidden_size, s->router_logits, stream_of(s)))
             return kErrLaunch;
     } else if (gemv_rows(s, lp.router, x, rows, c.hidden_size, c.expert_count,
                          s->router_logits, norm_w)) {
