@@ -109,11 +109,12 @@ __device__ __forceinline__ void kvb_decode8(const Kvb8<FMT> &r, float (&out)[8])
     }
 }
 
-// grid (rows, 1 + heads * chunks), chunks = ceil(latent / 128) (or 0: grid
-// (rows, 1 + heads), the query rope only): role 0 appends the cache rows; role
-// 1 + h * chunks + c ropes head h's query (c == 0) and absorbs it into the
-// latent columns 128 c .. 128 c + 127: qa_h[l] = sum_i q_nope[i] kv_b[h
-// (nope + v) + i][l].  A wave instruction covers 4 nope rows x 128 columns
+// grid (rows, 1 + heads * chunks), chunks = ceil(latent / 128): role 0
+// appends the cache rows and ropes every head's query; role 1 + h * chunks
+// + c absorbs head h's query into the latent columns 128 c .. 128 c + 127:
+// qa_h[l] = sum_i q_nope[i] kv_b[h (nope + v) + i][l].  chunks = -1 (prefill,
+// which absorbs by GEMM or not at all): grid (rows, 1), role 0 alone.
+// (chunks = 0, grid (rows, 1 + heads): role 1 + h ropes head h's query.)  A wave instruction covers 4 nope rows x 128 columns
 // (16 lanes per row, 8 columns per lane: contiguous row runs), wave w rows
 // 4 (w + 4 j) .. + 3 for j = 0, 1, ...; a lane issues the loads of 8 rows
 // before decoding any; the 4 lanes of a column set and the 4 waves meet by
@@ -1477,16 +1478,25 @@ __global__ __launch_bounds__(256, 1) void mla_flash_kernel(MlaParams p) {
         const uint16_t *ks = p.kv_expanded + L.key_row(h, 32L * kt);
         const uint16_t *vs = p.kv_expanded + L.value_block(p.heads, h, kt);
         constexpr int KC = KHALVES / 8, VC = VHALVES / 8;  // 16-byte chunks
-        for (int c0 = 64 * wave; c0 < KC; c0 += 256)
-            if (c0 + lane < KC)
+        // unrolled over compile-time trip counts (the lane test matters for
+        // the last, partial instruction only): 153.8 against 160.9 us per
+        // layer for the runtime loops
+#pragma unroll
+        for (int i = 0; i < (KC + 255) / 256; ++i) {
+            const int c0 = 64 * wave + 256 * i;
+            if (c0 < KC && (KC % 64 == 0 || c0 + lane < KC))
                 __builtin_amdgcn_global_load_lds(
                     (const __attribute__((address_space(1))) void *)(ks + 8L * (c0 + lane)),
                     (__attribute__((address_space(3))) void *)(dst + 8 * c0), 16, 0, 0);
-        for (int c0 = 64 * wave; c0 < VC; c0 += 256)
-            if (c0 + lane < VC)
+        }
+#pragma unroll
+        for (int i = 0; i < (VC + 255) / 256; ++i) {
+            const int c0 = 64 * wave + 256 * i;
+            if (c0 < VC && (VC % 64 == 0 || c0 + lane < VC))
                 __builtin_amdgcn_global_load_lds(
                     (const __attribute__((address_space(1))) void *)(vs + 8L * (c0 + lane)),
                     (__attribute__((address_space(3))) void *)(dst + KHALVES + 8 * c0), 16, 0, 0);
+        }
     };
     f32x4v acc[NV];
 #pragma unroll
@@ -1862,8 +1872,10 @@ int mla_attention_core(const MlaParams &p, hipStream_t stream) {
             hipFuncAttributeMaxDynamicSharedMemorySize, (int)pf_lds_bytes<RB, NW>()) == hipSuccess;
         (void)attr;
         const unsigned mt = (unsigned)((p.rows + 63) / 64);
-        hipLaunchKernelGGL(mla_prep_kernel<kF32>, dim3(p.rows, 1 + p.heads), dim3(256), 0, stream,
-                           p, 0);
+        // the cache rows and every head's query rope, one workgroup a row
+        // (measured on MI355X, 2048-token prefill: 12.5 us per layer against
+        // 28.2 with a workgroup per (row, head) for the rope)
+        hipLaunchKernelGGL(mla_prep_kernel<kF32>, dim3(p.rows, 1), dim3(256), 0, stream, p, -1);
         if (mla_prefill_expanded(p, stream))
             return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
         // the head GEMMs on the f16 matrix cores for integer kv_b (K a
