@@ -1449,7 +1449,10 @@ __global__ __launch_bounds__(256, 1) void mla_flash_kernel(MlaParams p) {
     const int nk = pos0 + min(r0 + 64, p.rows);         // keys of the workgroup
     const int ntiles = (nk + 31) / 32;
     // ---- the query row as f16 halves: dims 32 j + 8 g .. + 7 (k_nope dims,
-    // then the rope, zeros past nope + rope)
+    // then the rope, zeros past nope + rope), scaled by the softmax scale and
+    // log2(e), so that the scores come out in base-2 exponent units
+    constexpr float kLog2e = 1.4426950408889634f;
+    const float qscale = p.scale * kLog2e;
     half8 qh[NKS], ql[NKS];
     bool bad = false;
     {
@@ -1466,7 +1469,10 @@ __global__ __launch_bounds__(256, 1) void mla_flash_kernel(MlaParams p) {
                 x[4] = v1.x, x[5] = v1.y, x[6] = v1.z, x[7] = v1.w;
             }
 #pragma unroll
-            for (int i = 0; i < 8; ++i) bad |= outside_f16(x[i]);
+            for (int i = 0; i < 8; ++i) {
+                bad |= outside_f16(x[i]);
+                x[i] *= qscale;
+            }
             split_f16<8>(x, qh[j], ql[j]);
         }
     }
@@ -1529,29 +1535,41 @@ __global__ __launch_bounds__(256, 1) void mla_flash_kernel(MlaParams p) {
                 sa[s2][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kl, qh[j], sa[s2][0], 0, 0, 0);
             }
         }
-        // ---- causal mask, online softmax of the lane's row
-        float sv[8];
-        bool valid[8];
-        float mt = -INFINITY;
+        // ---- causal mask (tiles the diagonal crosses only), online softmax
+        // of the lane's row in base 2 (v_exp_f32)
+        float sv[8], e[8];
 #pragma unroll
         for (int s2 = 0; s2 < 2; ++s2)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int key = 32 * kt + 16 * s2 + 4 * g + i;
-                valid[4 * s2 + i] = key <= rpos;
-                sv[4 * s2 + i] = (sa[s2][0][i] + sa[s2][1][i]) * p.scale;
-                if (valid[4 * s2 + i]) mt = fmaxf(mt, sv[4 * s2 + i]);
-            }
-        mt = quad_rows_max(mt);
-        const float mn = mt > m + kPfLazyMax ? mt : m;  // -inf m: the tile max
-        float e[8], es = 0.0f;
+            for (int i = 0; i < 4; ++i) sv[4 * s2 + i] = sa[s2][0][i] + sa[s2][1][i];
+        const bool whole = 32 * kt + 31 <= pos0 + r0 + 16 * wave;  // every key visible (wave)
+        float mt = -INFINITY;
+        if (whole) {
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            e[i] = valid[i] ? __expf(sv[i] - mn) : 0.0f;
-            es += e[i];
+            for (int i = 0; i < 8; ++i) mt = fmaxf(mt, sv[i]);
+        } else {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const int key = 32 * kt + 16 * (i >> 2) + 4 * g + (i & 3);
+                if (key > rpos) sv[i] = -INFINITY;
+                mt = fmaxf(mt, sv[i]);
+            }
+        }
+        mt = quad_rows_max(mt);
+        const float mn = mt > m + kPfLazyMax * kLog2e ? mt : m;  // -inf m: the tile max
+        float es = 0.0f;
+        if (mn == -INFINITY) {  // no visible key yet for the row
+#pragma unroll
+            for (int i = 0; i < 8; ++i) e[i] = 0.0f;
+        } else {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                e[i] = __builtin_amdgcn_exp2f(sv[i] - mn);  // masked keys: 2^-inf = 0
+                es += e[i];
+            }
         }
         es = quad_rows_sum(es);
-        const float sc = mn == m ? 1.0f : __expf(m - mn);  // 0 while m is -inf
+        const float sc = mn == m ? 1.0f : __builtin_amdgcn_exp2f(m - mn);  // 0 while m is -inf
         l = l * sc + es;
         m = mn;
         if (__ballot(sc != 1.0f)) {  // rare: a row's max moved
