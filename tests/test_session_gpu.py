@@ -525,15 +525,17 @@ def test_batch_beyond_one_routing_call(tmp_path, device):
     model.close()
 
 
+@pytest.mark.parametrize("rows", [6, 80])
 @pytest.mark.parametrize("factor", [2 ** 10, 2 ** 20])
-def test_attention_operand_range(tmp_path, device, factor):
+def test_attention_operand_range(tmp_path, device, factor, rows):
     """The attention products take split-f16 operands (|v| < 65504).  With
     q_proj and the rope rows of kv_a scaled by 2^10 (row scales times an
     exact power of two) the queries, absorbed queries and rope keys reach the
     hundreds to thousands and attention still matches the oracle; at 2^20
     they leave the f16 range, and the attention hook and a prefill report
-    it instead of returning inf / NaN."""
-    print(f"[gpu] attention operands scaled by {factor}", flush=True)
+    it instead of returning inf / NaN.  6 rows take the absorbed form, 80
+    the expanded heads (64 rows or more)."""
+    print(f"[gpu] attention operands scaled by {factor}, {rows} rows", flush=True)
     cfg = dict(CU.TINY)
     tensors = CU.build_tensors(cfg, ebits=8, dbits=8, seed=31337)
     lora = cfg["kv_lora_rank"]
@@ -545,13 +547,13 @@ def test_attention_operand_range(tmp_path, device, factor):
         tensors[p + "kv_a_proj_with_mqa.weight.qs"] = kv
     model = S.Model.open(CU.write_container(str(tmp_path / f"range{factor}"), cfg, tensors))
     rng = np.random.default_rng(8)
-    x = rng.normal(0, 1, (6, 256)).astype(np.float32)
-    sess = S.Session(model, 32, 8)
+    x = rng.normal(0, 1, (rows, 256)).astype(np.float32)
+    sess = S.Session(model, 128, 96)
     got = sess.test_attention(0, x, 0)
     if factor == 2 ** 10:
-        orc = CU.oracle_model(cfg, tensors, 32)
+        orc = CU.oracle_model(cfg, tensors, 128)
         expect = np.empty_like(x)
-        assert O.lib().orc_attention(orc.handle, 0, O.fptr(x), 6, 0, O.fptr(expect))
+        assert O.lib().orc_attention(orc.handle, 0, O.fptr(x), rows, 0, O.fptr(expect))
         assert got is not None and np.isfinite(got).all()
         err = rel_l2(got, expect)
         print(f"[gpu] scaled attention rel-L2 {err:.2e}", flush=True)
@@ -560,7 +562,8 @@ def test_attention_operand_range(tmp_path, device, factor):
     else:
         assert got is None
         sess.reset()
+        ids = [1, 2, 3] if rows < 64 else (np.arange(rows) % cfg["vocab_size"]).tolist()
         with pytest.raises(S.SessionError, match="outside the f16 range"):
-            sess.prefill([1, 2, 3])
+            sess.prefill(ids)
     sess.close()
     model.close()
