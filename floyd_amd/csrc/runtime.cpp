@@ -1089,9 +1089,12 @@ int attention(MoonlightSession *s, int layer, const float *x, int rows, int posi
 constexpr int kPresplitMinRows = 2;
 
 // The MFMA router (32 x 32 tiles, one workgroup per tile) has the
-// parallelism for prefill batches; fewer rows take router_logits_small (one
-// workgroup per expert and 16 rows).
+// parallelism for prefill batches.  Up to 16 rows take router_logits_small
+// (one workgroup per expert; measured on MI355X, MoE layer at T = 8: 7.5
+// against 8.4 us for the GEMV; at T = 64, four row groups, 12.0 against
+// 11.2 us), the rows between the GEMV.
 constexpr int kRouterMfmaMinRows = 256;
+constexpr int kRouterSmallMaxRows = 16;
 
 // fixed: the MoE test / timing hooks take the caller's expert ids when set
 // (moonlight_session_fix_routes); forward passes always route by top-k.
@@ -1156,7 +1159,7 @@ int route(MoonlightSession *s, int layer, const float *x, int rows, const float 
         if (router_logits(x, norm_w, c.rms_norm_epsilon, router_w, rows, c.expert_count,
                           c.hidden_size, s->router_logits, stream_of(s)))
             return kErrLaunch;
-    } else if (f32_router && c.hidden_size % 8 == 0) {
+    } else if (f32_router && rows <= kRouterSmallMaxRows && c.hidden_size % 8 == 0) {
         if (router_logits_small(x, norm_w, c.rms_norm_epsilon, router_w, rows, c.expert_count,
                                 c.hidden_size, s->router_logits, stream_of(s)))
             return kErrLaunch;
