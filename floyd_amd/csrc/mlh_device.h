@@ -46,6 +46,35 @@ __device__ __forceinline__ float wave_sum(float v) {
     return v;
 }
 
+// Wave reductions on DPP only (no LDS instruction: with an LDS DMA in flight
+// the compiler would wait for it before any LDS instruction, ds_bpermute
+// included).  Lane 63 ends with the total; every lane gets it by readlane.
+#define MLH_DPP(v, ctrl, rmask) \
+    __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), ctrl, rmask, 0xF, false))
+__device__ __forceinline__ float dpp_wave_sum(float v) {
+    v += MLH_DPP(v, 0xB1, 0xF);   // quad_perm [1,0,3,2]
+    v += MLH_DPP(v, 0x4E, 0xF);   // quad_perm [2,3,0,1]
+    v += MLH_DPP(v, 0x141, 0xF);  // row_half_mirror
+    v += MLH_DPP(v, 0x140, 0xF);  // row_mirror
+    // row_bcast15 / row_bcast31 write only the masked rows: the others add
+    // their own value, so they are not read below
+    const float b15 = MLH_DPP(v, 0x142, 0xA);
+    v = (threadIdx.x & 16) ? v + b15 : v;
+    const float b31 = MLH_DPP(v, 0x143, 0xC);
+    v = (threadIdx.x & 32) ? v + b31 : v;
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+__device__ __forceinline__ float dpp_wave_max(float v) {
+    v = fmaxf(v, MLH_DPP(v, 0xB1, 0xF));
+    v = fmaxf(v, MLH_DPP(v, 0x4E, 0xF));
+    v = fmaxf(v, MLH_DPP(v, 0x141, 0xF));
+    v = fmaxf(v, MLH_DPP(v, 0x140, 0xF));
+    v = fmaxf(v, MLH_DPP(v, 0x142, 0xA));
+    v = fmaxf(v, MLH_DPP(v, 0x143, 0xC));
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+#undef MLH_DPP
+
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));

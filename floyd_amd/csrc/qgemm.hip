@@ -99,7 +99,7 @@ __device__ __forceinline__ void quantize_row(const QuantSeg &s, int row) {
             const f32x4 t = value(c);
             ss += t.x * t.x + t.y * t.y + t.z * t.z + t.w * t.w;
         }
-        ss = wave_sum(ss);
+        ss = dpp_wave_sum(ss);
         inv_rms = 1.0f / sqrtf(ss / (float)width + eps);
     }
     auto normed = [&](int c) -> f32x4 {
@@ -119,7 +119,7 @@ __device__ __forceinline__ void quantize_row(const QuantSeg &s, int row) {
         const f32x4 t = normed(c);
         amax = fmaxf(amax, fmaxf(fmaxf(fabsf(t.x), fabsf(t.y)), fmaxf(fabsf(t.z), fabsf(t.w))));
     }
-    amax = wave_max(amax);
+    amax = dpp_wave_max(amax);
     const float inv = amax > 0.0f ? kQuantMax / amax : 0.0f;
     if (lane == 0) scale[row] = amax / kQuantMax;
     int8_t *hr = hi + (long)row * width;
