@@ -23,8 +23,11 @@
 //               its share of ctx_h = W_UV_h lc_h, and the sum of the shares
 //               by the head's last workgroup.
 // Prefill (more than one row, outside a captured graph) runs mla_prep for
-// the cache and the query rope, the absorb and value as per-head MFMA GEMMs
-// and a flash-attention kernel (mla_prefill_attend).
+// the cache and the query rope, then, for 64 rows or more, kv_b applied to
+// every cached key (mla_expand) and a flash-attention kernel per head on the
+// expanded keys and values (mla_flash); for fewer rows the absorb and value
+// as per-head MFMA GEMMs around a flash-attention kernel in the absorbed
+// form (mla_prefill_attend).
 #include "mla.h"
 
 #include "mlh_device.h"
