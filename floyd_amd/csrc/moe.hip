@@ -119,27 +119,33 @@ __global__ __launch_bounds__(1024) void route_lists_kernel(RouteParams p) {
         for (int u = n_unique + tid; u < p.task_slots; u += blockDim.x)
             store_task(p.tasks + u, ExpertWeights{}, 0, 0);
     if (rank < 0) return;  // the whole workgroup: no list entries
-    // list entries of e in position order, blockDim.x positions per round
-    int base = offset;
-    for (int q0 = 0; q0 < n_pos; q0 += blockDim.x) {
-        const int q = q0 + tid;
-        const bool mine = q < n_pos && ids16[q] == e;
+    // list entries of e in position order: wave w takes the contiguous
+    // positions [w * seg, (w + 1) * seg), counts its entries (ballots), the
+    // waves' counts meet in one exclusive scan, then each wave writes its
+    // entries from its start (two barriers whatever the batch)
+    const int nw = (int)(blockDim.x >> 6);
+    const int seg = (n_pos + nw - 1) / nw;
+    const int q_lo = wave * seg, q_hi = min(n_pos, q_lo + seg);
+    int mine_count = 0;
+    for (int q0 = q_lo; q0 < q_hi; q0 += 64) {
+        const int q = q0 + lane;
+        mine_count += __popcll(__ballot(q < q_hi && ids16[q] == e));
+    }
+    if (lane == 0) wave_count[wave] = mine_count;
+    __syncthreads();
+    int j0 = offset;
+    for (int w = 0; w < wave; ++w) j0 += wave_count[w];
+    for (int q0 = q_lo; q0 < q_hi; q0 += 64) {
+        const int q = q0 + lane;
+        const bool mine = q < q_hi && ids16[q] == e;
         const unsigned long long m = __ballot(mine);
-        if (lane == 0) wave_count[wave] = __popcll(m);
-        __syncthreads();
-        int before = base, total = 0;
-        for (int w = 0; w < (int)(blockDim.x >> 6); ++w) {
-            if (w < wave) before += wave_count[w];
-            total += wave_count[w];
-        }
         if (mine) {
-            const int j = before + __popcll(m & ((1ull << lane) - 1ull));
+            const int j = j0 + __popcll(m & ((1ull << lane) - 1ull));
             p.list_rows[j] = q / K;
             p.list_slots[j] = q % K;
             p.list_pos[q] = j;
         }
-        base += total;
-        __syncthreads();  // wave_count is rewritten next round
+        j0 += __popcll(m);
     }
 }
 
