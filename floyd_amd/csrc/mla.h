@@ -71,13 +71,13 @@ struct MlaParams {
 
 // Prefill rows from which the attention runs on per-head keys and values
 // (kv_b applied to every cached latent row once) instead of in the absorbed
-// form, and the bytes of their expanded copy per key (0: the shape has no
-// expanded form).
+// form, and the bytes of their expanded copy per key (0: the shape or the
+// kv_b format (q8 / q4 only) has no expanded form).
 constexpr int kMlaExpandMinRows = 64;
 // Keys an expanded copy holds at most (a session's allocation: at Moonlight's
 // shape 21,760 bytes a key, 713 MB at this limit).
 constexpr long kMlaExpandMaxKeys = 32768;
-size_t mla_expand_kv_bytes(int heads, int nope, int rope, int vdim);
+size_t mla_expand_kv_bytes(int heads, int nope, int rope, int vdim, int latent, int kv_b_fmt);
 
 // Prefill: cache append + query RoPE, then either the per-head expansion
 // and a flash attention over it (kMlaExpandMinRows rows or more, keys

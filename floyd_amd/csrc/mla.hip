@@ -1833,9 +1833,11 @@ static bool flash_shape(int nope, int rope, int vdim, int *nks, int *nv) {
     return (*nks == 6 && *nv == 8) || (*nks == 2 && *nv == 2);
 }
 
-size_t mla_expand_kv_bytes(int heads, int nope, int rope, int vdim) {
+size_t mla_expand_kv_bytes(int heads, int nope, int rope, int vdim, int latent, int kv_b_fmt) {
     int nks, nv;
-    if (heads <= 0 || !flash_shape(nope, rope, vdim, &nks, &nv)) return 0;
+    if (heads <= 0 || !flash_shape(nope, rope, vdim, &nks, &nv) || latent <= 0 ||
+        latent % kExKC || nope + vdim > 256 || (kv_b_fmt != kQ8 && kv_b_fmt != kQ4))
+        return 0;
     const size_t krow = 2 * 32 * (size_t)nks + 8;
     return (size_t)heads * (krow + 2 * (size_t)vdim * kFlashVRow / 32) * sizeof(uint16_t);
 }
@@ -1859,8 +1861,8 @@ static bool mla_prefill_expanded(const MlaParams &p, hipStream_t stream) {
     int nks, nv;
     const long nk = (long)p.position + p.rows;
     if (!p.kv_expanded || p.rows < kMlaExpandMinRows || nk > p.expand_keys ||
-        !flash_shape(p.nope, p.rope, p.vdim, &nks, &nv) || p.latent % kExKC ||
-        p.nope + p.vdim > 256 || (p.kv_b.fmt != kQ8 && p.kv_b.fmt != kQ4))
+        !mla_expand_kv_bytes(p.heads, p.nope, p.rope, p.vdim, p.latent, p.kv_b.fmt) ||
+        !flash_shape(p.nope, p.rope, p.vdim, &nks, &nv))
         return false;
     const dim3 ge((unsigned)((nk + 63) / 64), (unsigned)p.heads);
     if (p.kv_b.fmt == kQ8)

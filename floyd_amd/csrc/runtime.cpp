@@ -1590,9 +1590,19 @@ extern "C" int moonlight_session_create(MoonlightSession **out, MoonlightModel *
     // the split-attention (decode) path runs at most kMlaDecodeRows rows per launch group
     const size_t dr = mb < (size_t)kMlaDecodeRows ? mb : (size_t)kMlaDecodeRows;
     const size_t sw = (size_t)c.moe_intermediate_size * c.shared_expert_count;
-    // the expanded prefill keys: the whole context up to kMlaExpandMaxKeys
-    const size_t expand_bytes =
-        mla_expand_kv_bytes(c.head_count, c.qk_nope_dim, c.qk_rope_dim, c.value_dim);
+    // the expanded prefill keys: the whole context up to kMlaExpandMaxKeys,
+    // when every layer's kv_b has the expanded form
+    size_t expand_bytes = 0;
+    for (int l = 0; l < c.layer_count; ++l) {
+        const size_t b = mla_expand_kv_bytes(c.head_count, c.qk_nope_dim, c.qk_rope_dim,
+                                             c.value_dim, c.kv_lora_rank,
+                                             s->model->layers[l].kv_b.fmt);
+        if (!b) {
+            expand_bytes = 0;
+            break;
+        }
+        expand_bytes = b;
+    }
     if (expand_bytes && mb >= (size_t)kMlaExpandMinRows)
         s->expand_keys = (long)std::min<size_t>((ctx + 63) / 64 * 64, (size_t)kMlaExpandMaxKeys);
     size_t lat_elems, rope_elems, lc_elems, logit_elems;
