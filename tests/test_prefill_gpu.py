@@ -22,6 +22,9 @@ when rows * top_k > 1024.
                              few dims at 100-300x the row rms)
   test_moonlight_prefill_attention  prefill MLA at 16 heads / latent 512 over
                              511 and 512 rows (odd and even row pairs)
+  test_moonlight_prefill_attention_chunks  the same in chunks of 200 + 80 + 2
+                             rows (expanded heads at positions 0 and 200,
+                             the absorbed form at 280)
   test_moonlight_dense_mlp   the 11264-wide dense SwiGLU block at T = 512
 
 Tolerance: rel-L2 <= 1e-3 against the fp32 oracle
@@ -307,6 +310,33 @@ def test_moonlight_prefill_attention(moon, rows):
     assert np.max(np.abs(last[0] - got[rows - 1])) < 3e-4
     assert rel_l2(last[0], expect[rows - 1]) < 1e-4
     split.close()
+    sess.close()
+    orc.close()
+
+
+def test_moonlight_prefill_attention_chunks(moon):
+    """Prefill MLA in chunks at 16 heads / latent 512 / rope 64: 200 rows at
+    position 0 and 80 rows at position 200 (both on the expanded heads, the
+    second expanding the first chunk's keys too), then 2 rows at 280 (the
+    absorbed form), each against orc_attention continuing the same cache
+    (moonlight_kernels.metal:218-375 with key_count = pos + r + 1)."""
+    layer = 1
+    print("[gpu] Moonlight prefill attention in chunks 200 + 80 + 2", flush=True)
+    x = O.fill_normal(282 * 2048, 909).reshape(282, 2048)
+    sess = S.Session(moon, 512, 256)
+    orc = oracle_with(moon, attention_names(layer), 512)
+    pos = 0
+    for rows in (200, 80, 2):
+        xs = np.ascontiguousarray(x[pos:pos + rows])
+        got = sess.test_attention(layer, xs, pos)
+        assert got is not None
+        expect = np.empty_like(xs)
+        assert O.lib().orc_attention(orc.handle, layer, O.fptr(xs), rows, pos, O.fptr(expect))
+        err = rel_l2(got, expect)
+        print(f"[gpu] {rows} rows at {pos}: rel-L2 {err:.2e} "
+              f"max-abs {np.max(np.abs(got - expect)):.2e}", flush=True)
+        assert err < 1e-4
+        pos += rows
     sess.close()
     orc.close()
 
