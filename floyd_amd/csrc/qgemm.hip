@@ -366,7 +366,18 @@ __global__ __launch_bounds__((QgShape<FMT, BM>::kThreads),
     const int tid = threadIdx.x;
     const int lane = tid & (kWave - 1);
     const int wave = tid >> 6;
-    const int wm = wave % Sh::kWM, wn = wave / Sh::kWM;
+    // 128-row tiles: the two waves that share a SIMD (waves w and w + 4)
+    // take 32-row blocks from different halves of the tile (wm and wm + 2)
+    // and the same weight rows, so that in a tile of at most 64 token rows
+    // every SIMD still has one wave with products to run.
+    const int wm = Sh::kWM == 4 ? (wave & 1) | ((wave >> 2) << 1) : wave % Sh::kWM;
+    const int wn = Sh::kWM == 4 ? (wave >> 1) & 1 : wave / Sh::kWM;
+    static_assert(Sh::kWM == 1 || (Sh::kWM == 4 && Sh::kWN == 2), "wave grid");
+    // a wave whose 32 rows all lie past the task's end skips its products
+    // (wave-uniform; it still issues its share of the copies and barriers)
+    // (32-row tiles have one wave row: always live, no branch)
+    const bool live =
+        Sh::kWM == 1 || __builtin_amdgcn_readfirstlane(m0 + wm * (Sh::kMI * 32)) < tk.rows;
 
     if (tid < BM) {
         const int m = m0 + tid;
@@ -588,8 +599,10 @@ __global__ __launch_bounds__((QgShape<FMT, BM>::kThreads),
             // and loads of the fence it implies
             __builtin_amdgcn_s_barrier();
             if (ks + kStages - 1 < nk) issue_dma((ks + kStages - 1) * kRB, (ks + kStages - 1) % kStages);
+            if (live) {
 #pragma unroll
-            for (int kp = 0; kp < kRB / 32; kp += 2) compute_pair(ks % kStages, kp);
+                for (int kp = 0; kp < kRB / 32; kp += 2) compute_pair(ks % kStages, kp);
+            }
         }
     } else {
         // two buffers: slice ks + 2 is in registers while slice ks is multiplied
@@ -599,7 +612,7 @@ __global__ __launch_bounds__((QgShape<FMT, BM>::kThreads),
         if (nk > 1) fetch(kRB);
         __syncthreads();
         for (int ks = 0; ks < nk; ++ks) {
-            compute_pair(ks & 1, 0);
+            if (live) compute_pair(ks & 1, 0);
             if (ks + 1 < nk) {
                 stash((ks + 1) & 1);
                 if (ks + 2 < nk) fetch((ks + 2) * kRB);
